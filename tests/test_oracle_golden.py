@@ -1,0 +1,244 @@
+"""The CPU oracle against vectors written by the reference itself.
+
+The fixtures come from ``tests/golden/make_golden.py`` (run in the build
+container against the reference checkout).  These tests pin the oracle; the
+GPU tests then compare the HIP library against the oracle.
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops
+from oracle.model import OracleModel, Shapes, greedy_decode
+from tests.golden.make_golden import TINY
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def cfg_shapes(name, **kw):
+    with open(os.path.join(GOLD, "configs.json")) as f:
+        return Shapes.from_dict(json.load(f)[name], **kw)
+
+
+def _ops():
+    return np.load(os.path.join(GOLD, "ops.npz"))
+
+
+def T(a):
+    return torch.from_numpy(np.asarray(a))
+
+
+def close(a, b, rtol=1e-5, atol=1e-6):
+    a = a.detach().float() if torch.is_tensor(a) else T(a).float()
+    b = b.detach().float() if torch.is_tensor(b) else T(b).float()
+    assert a.shape == b.shape, (a.shape, b.shape)
+    torch.testing.assert_close(a, b, rtol=rtol, atol=atol)
+
+
+def _sha(t):
+    return hashlib.sha256(t.detach().contiguous().numpy().tobytes()).hexdigest()
+
+
+def tiny_shapes(**kw):
+    return Shapes.from_dict(TINY, **kw)
+
+
+# ---------------------------------------------------------------- weight init
+
+@pytest.mark.parametrize("name,cfg,seed", [
+    ("tiny_seed0", None, 0),
+    ("nano_seed0", "nano", 0),
+    ("nano_chk_seed2", "nano_chk", 2),
+])
+def test_init_stream_matches_reference(name, cfg, seed):
+    with open(os.path.join(GOLD, "init_sha256.json")) as f:
+        want = json.load(f)[name]
+    S = tiny_shapes() if cfg is None else cfg_shapes(cfg)
+    torch.manual_seed(seed)
+    sd = OracleModel(S).state_dict()
+    assert set(sd) == set(want)
+    bad = [k for k, v in sd.items() if _sha(v) != want[k]["sha256"]]
+    assert not bad, f"init differs for {bad[:5]}"
+
+
+# ---------------------------------------------------------------- model step
+
+def _tiny_model(z, carry_token_id=None):
+    S = tiny_shapes(carry_token_id=carry_token_id)
+    m = OracleModel(S).eval()
+    sd = {k[3:]: torch.from_numpy(z[k]) for k in z.files if k.startswith("w::")}
+    m.load_state_dict(sd, strict=True)
+    return m
+
+
+@pytest.mark.parametrize("carry", [False, True])
+def test_tiny_decode_matches_reference(carry):
+    z = np.load(os.path.join(GOLD, "tiny_decode.npz"))
+    suffix = "_carry" if carry else ""
+    m = _tiny_model(z, 5 if carry else None)
+    prompt = T(z["prompt" + suffix])
+    ids, logits = greedy_decode(m, prompt, 12)
+    close(logits, z["logits" + suffix], rtol=1e-4, atol=1e-5)
+    assert torch.equal(ids, T(z["greedy" + suffix]))
+
+
+def test_nano_cpu_reference_greedy_ids():
+    path = os.path.join(GOLD, "nano_cpu_ref.npz")
+    if not os.path.exists(path):
+        pytest.skip("nano_cpu_ref.npz not generated")
+    z = np.load(path)
+    S = cfg_shapes("nano")
+    torch.manual_seed(0)
+    m = OracleModel(S).eval()
+    prompt = T(z["prompt"])
+    ids, logits = greedy_decode(m, prompt, 64)
+    assert torch.equal(ids, T(z["greedy"]))
+    top = torch.topk(logits, 5, dim=-1)
+    close(top.values, z["top5_values"], rtol=1e-4, atol=1e-4)
+
+
+# ---------------------------------------------------------------- per-op
+
+def test_imag_indices():
+    z = _ops()
+    S = tiny_shapes()
+    got = ops.w1_imag_live_flat_indices(S.N, S.QH, S.HD, S.H, "head")
+    assert torch.equal(got, T(z["imag_idx_head"]))
+    got = ops.w1_imag_live_flat_indices(S.N, S.QH, S.HD, S.H, "open")
+    assert torch.equal(got, T(z["imag_idx_open"]))
+
+
+def test_paraplex_ffn_forward():
+    z = _ops()
+    S = tiny_shapes()
+    w = {k.split("::")[1]: T(z[k]) for k in z.files if k.startswith("ffn.w::")}
+    g = {k: T(z[f"ffn.{k}"]) for k in ("u", "q", "kctx", "c", "d", "trace", "p_in", "reset")}
+    beta = ops.beta_space_dense(g["u"], g["q"], g["kctx"], g["c"], g["d"], w["w1_imag"], S.QH, S.HD)
+    close(beta, z["ffn.beta_dense"], rtol=1e-5, atol=1e-5)
+    beta_g = ops.beta_space_grouped(g["u"], g["q"], g["kctx"], g["c"], g["d"], w["w1_imag"], S.QH, S.HD)
+    close(beta_g, z["ffn.beta_dense"], rtol=1e-4, atol=1e-4)
+    for variant in ("full", "plain"):
+        wx = torch.nn.functional.linear(g["u"], w["w1_real.weight"])
+        if variant == "full":
+            alpha = 0.25 * torch.tanh(w["identity_gate.raw_alpha"])
+            R = wx * (1.0 + alpha * g["p_in"]) + w["w1_real.bias"]
+            act, s, nt = ops.paraplex_pointwise(R, R, beta, w["w1_imag_bias"], g["trace"],
+                                                w["w1_imag_trace"], g["reset"], 3.0)
+        else:
+            R = wx + w["w1_real.bias"]
+            act, s, nt = ops.paraplex_pointwise(R, R, beta, w["w1_imag_bias"], None,
+                                                w["w1_imag_trace"], None, 3.0)
+        out = torch.nn.functional.linear(act, w["w2.weight"], w["w2.bias"])
+        close(R, z[f"ffn.R_{variant}"])
+        close(s, z[f"ffn.I_{variant}"], rtol=1e-5, atol=1e-5)
+        close(act, z[f"ffn.O_{variant}"], rtol=1e-5, atol=1e-5)
+        close(nt, z[f"ffn.trace_{variant}"], rtol=1e-5, atol=1e-5)
+        close(out, z[f"ffn.out_{variant}"], rtol=1e-5, atol=1e-5)
+
+
+def test_phase_and_pvpowlu():
+    z = _ops()
+    close(ops.phase_sin(T(z["phase.beta"])), z["phase.out"])
+    close(ops.pvpowlu(T(z["pvpowlu.x1"]), T(z["pvpowlu.x2"]), 3.0), z["pvpowlu.out"])
+
+
+def test_depth_attn():
+    z = _ops()
+    w = {k.split("::")[1]: T(z[k]) for k in z.files if k.startswith("da.w::")}
+    hk, hv = T(z["da.hist_k"]), T(z["da.hist_v"])
+    B, Tt, S, QH, HD = hk.shape
+    d = ops.depth_attn_online(w["q_params"][3], hk, hv)
+    close(d, z["da.d_tensor"])
+    close(torch.nn.functional.linear(d.reshape(B, Tt, -1), w["w_o.weight"]), z["da.skip_tensor"])
+    d2, _, _ = ops.depth_attn_softmax(w["q_params"][4], hk, hv)
+    close(d2, z["da.d_list"])
+    kv = torch.nn.functional.linear(T(z["da.h_in"]), w["kv_weight"])
+    N = QH * HD
+    close(kv[..., :N].reshape(B, Tt, QH, HD), z["da.proj_k"])
+    close(kv[..., N:].reshape(B, Tt, QH, HD), z["da.proj_v"])
+
+
+@pytest.mark.parametrize("axis", [0, 1, 2])
+def test_tria_family(axis):
+    z = _ops()
+    r, i, o = T(z["tria.r"]), T(z["tria.i"]), T(z["tria.o"])
+    prev, seed, valid, w = T(z["tria.prev"]), T(z["tria.seed"]), T(z["tria.valid"]), T(z["tria.w"])
+    a = 0.0375
+    close(ops.build_tria(r, i, o, a, axis), z[f"tria.build_{axis}"])
+    close(ops.tria_init(r, i, o, a, axis), z[f"tria.init_{axis}"])
+    close(ops.tria_step(r, i, o, prev, a, axis), z[f"tria.step_{axis}"])
+    close(ops.tria_init_seed(r, i, o, seed, valid, a, axis), z[f"tria.seed_{axis}"])
+    for nm, (c, p) in (("init_gate", ops.tria_init_and_gate(r, i, o, w, a, axis)),
+                       ("step_gate", ops.tria_step_and_gate(r, i, o, prev, w, a, axis)),
+                       ("seed_gate", ops.tria_init_seed_and_gate(r, i, o, seed, valid, w, a, axis))):
+        close(c, z[f"tria.{nm}_{axis}.carry"])
+        close(p, z[f"tria.{nm}_{axis}.p"])
+
+
+def test_temporal_carry_and_polarm():
+    z = _ops()
+    d, rs, ini, valid = T(z["tc.depth"]), T(z["tc.reset"]), T(z["tc.init"]), T(z["tria.valid"])
+    close(ops.temporal_carry(d, rs), z["tc.full_ref"])
+    close(ops.temporal_carry(d, rs), z["tc.full_scan"], rtol=1e-4, atol=1e-5)
+    close(ops.temporal_carry_endpoint(d, rs), z["tc.end_noinit"])
+    close(ops.temporal_carry_endpoint(d, rs, ini), z["tc.end_init"])
+    close(ops.temporal_carry_endpoint(d, rs, ini, valid), z["tc.end_init_valid"])
+    close(ops.polarm(T(z["polarm.in"]), 0.1), z["polarm.out"])
+    close(ops.polarm(T(z["polarm.in"]), 0.3), z["polarm.out_b03"])
+
+
+def test_readout_and_final_ca():
+    z = _ops()
+    w = {k.split("::")[1]: T(z[k]) for k in z.files if k.startswith("agg.w::")}
+    sw = ops.make_score_w(w["reader.key_proj.weight"], w["pool.query"],
+                          torch.nn.functional.softplus(w["pool.logit_scale_raw"]))
+    close(sw, z["agg.score_w"])
+    pooled, _ = ops.slot_attention_pool(T(z["agg.carry"]), sw)
+    z32 = torch.nn.functional.linear(pooled, w["reader.proj.weight"], w["reader.proj.bias"])
+    close(torch.nn.functional.linear(z32, w["up.weight"], w["up.bias"]), z["agg.out"])
+    N = z["fca.q"].shape[-1]
+    close(ops.final_ca_sparse(T(z["fca.q"]), T(z["fca.k"]), T(z["fca.v"]), T(z["fca.allowed"]), N ** -0.5),
+          z["fca.out"])
+
+
+def test_final_ca_step_sequence():
+    z = _ops()
+    S = tiny_shapes(seq_len=16)
+    torch.manual_seed(0)
+    m = OracleModel(S)
+    w = {k.split("::")[1]: T(z[k]) for k in z.files if k.startswith("fcastep.w::")}
+    m.tria_final_ca.load_state_dict(w)
+    from oracle.model import CACache
+    cache = CACache()
+    a, b, fire = T(z["fcastep.a"]), T(z["fcastep.b"]), T(z["fcastep.fire"])
+    outs = [m.final_ca_step(a[t], b[t], cache, fire[t]) for t in range(a.shape[0])]
+    close(torch.stack(outs), z["fcastep.out"])
+
+
+def test_rope_and_attention_step():
+    z = _ops()
+    S = tiny_shapes()   # the rope fixture is built under the tiny config (YaRN ramp active)
+    inv, att = ops.yarn_inv_freq(S.HD, S.rope_theta, S.rope_factor, S.rope_original,
+                                 S.rope_beta_fast, S.rope_beta_slow)
+    cos, sin = ops.yarn_cos_sin(inv, att, S.seq_len)
+    close(cos, z["rope.cos"])
+    close(sin, z["rope.sin"])
+    St = tiny_shapes()
+    torch.manual_seed(0)
+    m = OracleModel(St)
+    w = {k.split("::")[1]: T(z[k]) for k in z.files if k.startswith("attn.w::")}
+    m.blocks[0].attn.load_state_dict(w)
+    from oracle.model import LayerCache
+    cache = LayerCache()
+    zs = T(z["attn.z"])
+    for pos in range(zs.shape[0]):
+        out, q, kctx, c = m.attn_step(m.blocks[0], zs[pos], pos, cache)
+        cache.cache_len += 1
+        close(out, z["attn.out"][pos])
+        close(q, z["attn.q"][pos])
+        close(kctx, z["attn.kctx"][pos])
+        close(c, z["attn.c"][pos])
