@@ -1,0 +1,318 @@
+#!/usr/bin/env python3
+"""Benchmark of the LoomFormer fused-kernel inference path on one MI355X.
+
+Headline (``value``): end-to-end greedy decode tokens/s of the 113M-shape
+LoomFormer (cfg/nano_chk.yaml shape, seq_len raised to 4096, random-init
+weights from seed 2, bf16) at batch 32: a 2048-token prompt of uniform ids is
+prefilled token by token (the reference's ``infer``), then ``--steps`` greedy
+decode steps are timed (one step = one token for all 32 sequences).  The last
+``--warmup`` prompt positions are the untimed warm-up steps.
+
+Microbenchmarks, each timed live with HIP events on
+the stream the kernels run on:
+  PX  Paraplex FFN, 8192 tokens as [8, 1024], N=768, H=3072, bf16
+  DA  DepthAttn, 16384 tokens, 24 earlier-depth states, 8x96, bf16
+  TR  Tria depth op (gated step), B=8 x T=4096 x H=3072, fp32
+``roofline`` reports the fused Paraplex pointwise kernel (the path's fused
+HBM-bound kernel): algorithmic bytes (R, beta in; I, O out = 8 B/elem in
+bf16) per launch over its mean launch time, against 8 TB/s.
+
+``cpu_baseline`` is the CPU oracle (fp32 PyTorch restatement of the
+reference's unfused path) decoding on the host cores on a bounded sample.
+
+Prints ONE JSON line.  One GPU only: --gpus above 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "loomformer-paraplex_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "decode tokens/s (113M shape, bs32) + fused-kernel HBM GB/s as % of peak"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def timed(fn, iters: int, warmup: int = 3) -> float:
+    """Mean milliseconds per call of fn over `iters` calls (HIP events on the current stream)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters
+
+
+# ----------------------------------------------------------------------------- e2e
+
+def bench_decode(args):
+    import torch
+    from loom_amd.config import NANO_CHK, ModelConfig
+    from loom_amd.engine import LoomDecoder
+    from loom_amd.weights import init_state_dict
+
+    cfg = ModelConfig.from_dict(NANO_CHK).with_seq_len(4096)
+    B, P, K, W = args.batch, args.prompt, args.steps, args.warmup
+    if W > P:
+        raise SystemExit("--warmup cannot exceed --prompt")
+    state = init_state_dict(cfg, 2)
+    eng = LoomDecoder(cfg, state, batch=B, dtype=torch.bfloat16, max_len=P + K + 1)
+    g = torch.Generator().manual_seed(2)
+    prompt = torch.randint(0, cfg.V, (B, P), generator=g).to("cuda")
+    log(f"prefill {P} tokens x B={B} token by token")
+    t0 = time.time()
+    logits = None
+    for pos in range(P - W):
+        logits = eng.step(prompt[:, pos], pos)
+    torch.cuda.synchronize()
+    t_prefill = time.time() - t0
+    for pos in range(P - W, P):                       # warm-up steps
+        logits = eng.step(prompt[:, pos], pos)
+    torch.cuda.synchronize()
+    log(f"prefill done in {t_prefill:.1f}s; timing {K} greedy steps")
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = torch.empty(B, K, dtype=torch.long, device="cuda")
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    s.record()
+    for i in range(K):
+        nxt = torch.argmax(logits, dim=-1)
+        out[:, i] = nxt
+        logits = eng.step(nxt, P + i)
+    e.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = s.elapsed_time(e)
+    return dict(ms_total=ms, ms_per_step=ms / K, tokens_per_s=B * K / (ms / 1e3),
+                wall_s=wall, prefill_s=t_prefill, prefill_tokens_per_s=B * (P - W) / t_prefill,
+                ids_head=out[0, :8].tolist())
+
+
+# ----------------------------------------------------------------------------- micro
+
+def bench_px(iters):
+    import torch
+    from loom_amd import ops
+
+    dev, bf = "cuda", torch.bfloat16
+    B, T, N, QH, HD, H = 8, 1024, 768, 8, 96, 3072
+    M, K_imag = B * T, N + 4 * HD
+    torch.manual_seed(1)
+    mk = lambda o, i: torch.nn.Linear(i, o, bias=True)  # Kaiming-uniform (nn.Linear default), seed 1
+    w_real = mk(H, N).weight.data.to(dev, bf)
+    w_imag = torch.nn.init.kaiming_uniform_(torch.empty(H, K_imag), a=math.sqrt(5)).to(dev, bf)
+    w2 = mk(N, H).weight.data.to(dev, bf)
+    g = torch.Generator(device=dev).manual_seed(1)
+    rn = lambda *s: torch.randn(*s, generator=g, device=dev).to(bf)
+    u = rn(B, T, N)
+    q, kc, c, d = (rn(B, T, QH, HD) for _ in range(4))
+    b_real = torch.zeros(H, device=dev)
+    b2 = torch.zeros(N, device=dev)
+    imag_bias = torch.zeros(H, device=dev)
+    trace_w = (torch.rand(H, generator=g, device=dev) - 0.5)
+    trace = torch.zeros(B, H, device=dev, dtype=bf)
+    anchor = torch.ones((), device=dev)
+    empty_reset = torch.empty(0, dtype=torch.bool, device=dev)
+    R = ops.linear(u, w_real, b_real)
+    beta = ops.beta_forward_cuda(u, q, kc, c, d, w_imag, H // QH, HD, QH, False)[0]
+    act = ops.paraplex_forward(R, R, beta, imag_bias, trace, trace_w, empty_reset, anchor, 1, False,
+                               0.99, 3.0)[0]
+    res = {}
+    res["w_real_ms"] = timed(lambda: ops.linear(u, w_real, b_real, out=R), iters)
+    res["w_imag_ms"] = timed(lambda: ops.beta_forward_cuda(u, q, kc, c, d, w_imag, H // QH, HD, QH, False), iters)
+    res["pointwise_ms"] = timed(lambda: ops.paraplex_forward(R, R, beta, imag_bias, trace, trace_w,
+                                                              empty_reset, anchor, 1, False, 0.99, 3.0), iters)
+    out = torch.empty(B, T, N, device=dev, dtype=bf)
+    res["w2_ms"] = timed(lambda: ops.linear(act, w2, b2, out=out), iters)
+
+    def ffn():
+        R_ = ops.linear(u, w_real, b_real)
+        be = ops.beta_forward_cuda(u, q, kc, c, d, w_imag, H // QH, HD, QH, False)[0]
+        a_ = ops.paraplex_forward(R_, R_, be, imag_bias, trace, trace_w, empty_reset, anchor, 1,
+                                  False, 0.99, 3.0)[0]
+        return ops.linear(a_, w2, b2)
+    res["ffn_ms"] = timed(ffn, iters)
+    elems = M * H
+    res["pointwise_bytes"] = elems * 8            # R, beta in; I, O out (bf16)
+    res["pointwise_GBs"] = res["pointwise_bytes"] / (res["pointwise_ms"] * 1e-3) / 1e9
+    fl = {"w_real": 2 * M * N * H, "w_imag": 2 * M * K_imag * H, "w2": 2 * M * H * N}
+    for k, v in fl.items():
+        res[f"{k}_TFLOPs"] = v / (res[f"{k}_ms"] * 1e-3) / 1e12
+    res["gemm_gflop"] = sum(fl.values()) / 1e9
+    return res
+
+
+def bench_da(iters):
+    import torch
+    from loom_amd import ops
+
+    dev, bf = "cuda", torch.bfloat16
+    BT, S, QH, HD = 16384, 24, 8, 96
+    g = torch.Generator(device=dev).manual_seed(3)
+    K = torch.randn(1, BT, S, QH, HD, generator=g, device=dev).to(bf)
+    V = torch.randn(1, BT, S, QH, HD, generator=g, device=dev).to(bf)
+    q = (torch.randn(QH, HD, generator=g, device=dev) * 0.02).to(bf)
+    ms = timed(lambda: ops.depth_attn_stacked_forward(q, K, V), iters)
+    nbytes = 2 * K.numel() * 2 + BT * QH * HD * 2 + BT * QH * 4
+    return dict(ms=ms, bytes=nbytes, GBs=nbytes / (ms * 1e-3) / 1e9)
+
+
+def bench_tr(iters):
+    import torch
+    from loom_amd import ops
+
+    dev = "cuda"
+    B, T, H = 8, 4096, 3072
+    g = torch.Generator(device=dev).manual_seed(4)
+    r, i, o = (torch.randn(B, T, H, generator=g, device=dev) for _ in range(3))
+    prev = torch.randn(B, T, H, 3, 3, generator=g, device=dev)
+    prev /= prev.square().mean(dim=(-1, -2), keepdim=True).add(1e-6).sqrt()
+    w = torch.full((9,), 1.0 / 9.0, device=dev)
+    ms = timed(lambda: ops.tria_step_gate_forward(r, i, o, prev, w, 0.025, 1), iters)
+    n = B * T * H
+    nbytes = n * (12 + 36 + 36 + 4 + 4)          # r,i,o; C_prev; C; p; scale (fp32)
+    del prev
+    depth = torch.randn(B, 64, H, 3, 3, generator=g, device=dev)
+    reset = torch.zeros(B, 64, dtype=torch.bool, device=dev)
+    empty = torch.empty(0, device=dev)
+    ms_end = timed(lambda: ops.temporal_carry_endpoint_forward(depth, reset, empty,
+                                                               torch.empty(0, dtype=torch.bool, device=dev)), iters)
+    end_bytes = depth.numel() * 4 + B * H * 9 * 8
+    return dict(step_gate_ms=ms, step_gate_bytes=nbytes, step_gate_GBs=nbytes / (ms * 1e-3) / 1e9,
+                endpoint_w64_ms=ms_end, endpoint_w64_GBs=end_bytes / (ms_end * 1e-3) / 1e9)
+
+
+def copy_bandwidth():
+    import torch
+    x = torch.empty(1 << 28, dtype=torch.float32, device="cuda")   # 1 GiB
+    y = torch.empty_like(x)
+    ms = timed(lambda: y.copy_(x), 10)
+    return 2 * x.numel() * 4 / (ms * 1e-3) / 1e9
+
+
+# ----------------------------------------------------------------------------- cpu
+
+def cpu_baseline(args):
+    import torch
+    from oracle.model import OracleModel, Shapes, greedy_decode  # the checker, timed as baseline
+    from loom_amd.config import NANO_CHK
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    S = Shapes.from_dict(dict(NANO_CHK, seq_len=4096))
+    torch.manual_seed(2)
+    model = OracleModel(S).eval()
+    B, P, K = args.batch, args.cpu_prompt, args.cpu_steps
+    g = torch.Generator().manual_seed(2)
+    prompt = torch.randint(0, S.V, (B, P), generator=g)
+    state = None
+    logits = None
+    with torch.no_grad():
+        for pos in range(P):
+            logits, state = model.step(prompt[:, pos], pos, state)
+        t0 = time.perf_counter()
+        for i in range(K):
+            nxt = torch.argmax(logits, dim=-1)
+            logits, state = model.step(nxt, P + i, state)
+        dt = time.perf_counter() - t0
+    return dict(value=B * K / dt, unit="tokens/s", cores=cores, kind="port",
+                sample=f"fp32 oracle Model.step, nano_chk shape seed 2, B={B}, prompt {P} tokens "
+                       f"(untimed), {K} timed greedy steps (context {P}-{P + K}, vs 2048-2304 on GPU)")
+
+
+# ----------------------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--prompt", type=int, default=2048)
+    ap.add_argument("--micro-iters", type=int, default=20)
+    ap.add_argument("--no-micro", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-prompt", type=int, default=32)
+    ap.add_argument("--cpu-steps", type=int, default=8)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(run with --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a HIP device")
+    from loom_amd import _lib
+    _lib.load()
+
+    res = {}
+    dec = bench_decode(args)
+    log(f"decode: {dec['tokens_per_s']:.0f} tok/s, {dec['ms_per_step']:.3f} ms/step")
+    kernels = {}
+    roofline = None
+    if not args.no_micro:
+        px = bench_px(args.micro_iters)
+        log(f"PX: {json.dumps({k: round(v, 3) for k, v in px.items()})}")
+        da = bench_da(args.micro_iters)
+        log(f"DA: {json.dumps({k: round(v, 3) for k, v in da.items()})}")
+        tr = bench_tr(max(3, args.micro_iters // 4))
+        log(f"TR: {json.dumps({k: round(v, 3) for k, v in tr.items()})}")
+        copy_gbs = copy_bandwidth()
+        kernels = {
+            "paraplex_pointwise": {"ms": px["pointwise_ms"], "GB/s": px["pointwise_GBs"],
+                                   "frac": px["pointwise_GBs"] / HBM_PEAK_GBS},
+            "depth_attn": {"ms": da["ms"], "GB/s": da["GBs"], "frac": da["GBs"] / HBM_PEAK_GBS},
+            "tria_step_gate": {"ms": tr["step_gate_ms"], "GB/s": tr["step_gate_GBs"],
+                               "frac": tr["step_gate_GBs"] / HBM_PEAK_GBS},
+            "temporal_endpoint_w64": {"ms": tr["endpoint_w64_ms"], "GB/s": tr["endpoint_w64_GBs"]},
+            "w_real_gemm": {"ms": px["w_real_ms"], "TFLOP/s": px["w_real_TFLOPs"],
+                            "frac": px["w_real_TFLOPs"] / BF16_PEAK_TFLOPS},
+            "w_imag_gemm": {"ms": px["w_imag_ms"], "TFLOP/s": px["w_imag_TFLOPs"],
+                            "frac": px["w_imag_TFLOPs"] / BF16_PEAK_TFLOPS},
+            "w2_gemm": {"ms": px["w2_ms"], "TFLOP/s": px["w2_TFLOPs"],
+                        "frac": px["w2_TFLOPs"] / BF16_PEAK_TFLOPS},
+            "paraplex_ffn_total_ms": px["ffn_ms"],
+            "device_copy_GB/s": copy_gbs,
+        }
+        roofline = {"bound": "hbm", "kernel": "paraplex_forward_kernel (PX: 8x1024x3072 bf16)",
+                    "achieved": px["pointwise_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": px["pointwise_GBs"] / HBM_PEAK_GBS, "traffic": None}
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle on host cores)")
+        cpu = cpu_baseline(args)
+        log(f"CPU: {cpu['value']:.2f} tok/s on {cpu['cores']} cores")
+    line = {
+        "metric": METRIC, "value": dec["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": dec["ms_per_step"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (uniform prompt ids, random-init weights from seed 2)",
+        "config": {"workload": f"e2e greedy decode, nano_chk shape (seq_len 4096), batch {args.batch}, "
+                               f"{args.prompt}-token prompt prefilled by step, {args.steps} timed greedy steps",
+                   "batch": args.batch, "prompt": args.prompt, "decode_steps": args.steps},
+        "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels,
+        "prefill_tokens_per_s": dec["prefill_tokens_per_s"],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,253 @@
+/*
+ * loom_hip.h -- C ABI of libloom_hip.so, the gfx950 (MI355X) implementation of
+ * LoomFormer's fused-kernel inference path.
+ *
+ * Every entry point replaces one function of the reference's CUDA extensions
+ * (srose69/Loomformer-Paraplex, kernels/ *_launcher.cu and
+ * kernels/tria/bindings.cpp); the reference citation is given per function.
+ *
+ * Conventions (shared by all entry points):
+ *   - Plain pointers to device memory, element counts as int64_t; no tensor
+ *     types.  Tensors are dense row-major unless a stride argument says
+ *     otherwise.  The caller allocates every output (the reference launchers
+ *     allocate with torch::empty; the Python mirror does that instead).
+ *   - `dtype` is a loom_dtype and applies to the "activation" tensors named in
+ *     each comment; parameters documented as float are always fp32.
+ *   - bool tensors are 1 byte per element (uint8_t, 0 or 1).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).  No
+ *     entry point synchronises the host or allocates device memory.
+ *   - Return value: LOOM_OK, or a negative error code with a message readable
+ *     through loom_last_error() (thread-local).  The Python mirror raises
+ *     RuntimeError(message), like the reference's TORCH_CHECK.
+ */
+#ifndef LOOM_HIP_H
+#define LOOM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum loom_dtype { LOOM_F32 = 0, LOOM_BF16 = 1, LOOM_F16 = 2 };
+
+enum loom_status {
+    LOOM_OK = 0,
+    LOOM_ERR_INVALID = -1,     /* bad argument / unsupported shape or dtype */
+    LOOM_ERR_LAUNCH = -2,      /* HIP reported an error for a launch */
+};
+
+/* Last error message of the calling thread ("" if none). */
+const char* loom_last_error(void);
+/* ABI version (bumped on any signature change). */
+int loom_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Paraplex FFN
+ * ------------------------------------------------------------------------ */
+
+/* Fused Paraplex pointwise chain.  Replaces paraplex_forward_cuda
+ * (kernels/paraplex/paraplex_launcher.cu:49) in eval mode.
+ *   p_real, gate_src, beta_linear: [B,T,H] dtype (gate_src may equal p_real)
+ *   bias, trace_w: [H] float;  trace: [B,H] dtype;  reset: [B,T] bool or NULL
+ *   anchor: [1] float, copied to anchor_snapshot (eval: no EMA update)
+ *   outputs act (=O), s (=I): [B,T,H] dtype; next_trace: [B,H] dtype (I_base
+ *   at t = T-1).  m = powlu_m.
+ */
+int loom_paraplex_forward(int dtype, const void* p_real, const void* gate_src,
+                          const void* beta_linear, const float* bias, const void* trace,
+                          const float* trace_w, const uint8_t* reset, const float* anchor,
+                          void* act, void* s, void* next_trace, float* anchor_snapshot,
+                          int64_t B, int64_t T, int64_t H, float m, void* stream);
+
+/* sin(pi/2 * beta / sqrt(1 + beta^2)), elementwise.  Replaces
+ * phase_sin_forward_cuda (kernels/phase_sin/phase_sin_launcher.cu:11). */
+int loom_phase_sin_forward(int dtype, const void* beta, void* out, int64_t n, void* stream);
+
+/* x1 * max(x2,1e-12)^(m/(sqrt(x2)+1)) * sigmoid(x2), elementwise.  Replaces
+ * pvpowlu_forward_cuda (kernels/pvpowlu/pvpowlu_launcher.cu:11). */
+int loom_pvpowlu_forward(int dtype, const void* x1, const void* x2, void* out, int64_t n,
+                         float m, void* stream);
+
+/* Sector-gathered grouped W_imag product (no packed copy is materialised).
+ * Replaces beta_forward_cuda (kernels/beta_space/beta_space_launcher.cu:225,
+ * pack kernel beta_space_kernel.cuh:87 + cuBLAS strided-batched GEMM :57).
+ *   u: [M,N]; q_h, k_ctx_h, c_h, d_h: [M, n_q_heads*head_dim] (= [M,N]);
+ *   w_compact: [H, imag_in] with imag_in = N + 4*head_dim (head sectors) or
+ *   4*N + head_dim (open sectors);  out: [M,H].  All dtype; fp32 accumulate.
+ *   Group g (hidden rows [g*Hq,(g+1)*Hq), Hq = hidden_per_q_head) reads the
+ *   activation row [Q_g | Kctx_g | C_g | U | D_g] (head) or
+ *   [Q_g | Kctx | C | U | D] (open).
+ *   If r_pack is not NULL the packed activations [n_q_heads, M, imag_in] are
+ *   also written (the reference's second output). */
+int loom_beta_forward(int dtype, const void* u, const void* q_h, const void* k_ctx_h,
+                      const void* c_h, const void* d_h, const void* w_compact, void* out,
+                      void* r_pack, int64_t M, int64_t N, int64_t H, int64_t imag_in,
+                      int64_t hidden_per_q_head, int64_t head_dim, int64_t n_q_heads,
+                      int open_sectors, void* stream);
+
+/* Dense projection out[M,Nout] = epilogue(A[M,K] @ W[Nout,K]^T), fp32
+ * accumulate (bf16 operands on MFMA).  Replaces the F.linear calls of the
+ * path: ParaplexFFN w1_real (loomformer.py:2839) with the IdentityAnchoredGate
+ * epilogue (tria.py:1287-1299), w2 (loomformer.py:2854), DepthAttn.project
+ * (loomformer.py:3397), attention qkv/o (loomformer.py:3262, 3332), the Tria
+ * readout and final cross-attention projections and the LM head.
+ *   lda/ldw/ldc: row strides in elements.  bias: [Nout] float or NULL.
+ *   gate_p: [M,Nout] dtype (row stride ldc) or NULL; when given the epilogue is
+ *   acc * (1 + gate_alpha * gate_p) + bias, otherwise acc + bias.
+ *   residual: [M,Nout] dtype (row stride ldc) or NULL; added last. */
+int loom_linear(int dtype, const void* A, int64_t lda, const void* W, int64_t ldw,
+                const float* bias, const void* gate_p, float gate_alpha, const void* residual,
+                void* out, int64_t ldc, int64_t M, int64_t Nout, int64_t K, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Depth attention
+ * ------------------------------------------------------------------------ */
+
+/* Softmax read over the depth axis with one learned query per q-head.
+ * Replaces depth_attn_forward_cuda (kernels/depth_attn/depth_attn_launcher.cu:63,
+ * outputs d and weights) and depth_attn_stacked_forward_cuda (:143, outputs d
+ * and lse).
+ *   q: [QH,HD] dtype.  hist_k/hist_v: element (bt, s, qh, d) at
+ *   bt*stride_bt + s*stride_s + qh*HD + d, dtype (a strided history view
+ *   such as hist[:, :, :S] of a [B,T,S_max,QH,HD] buffer needs no copy).
+ *   d_out: [BT,QH,HD] dtype.  w_out: [BT,QH,S] dtype or NULL.
+ *   lse_out: [BT,QH] float or NULL.  Scores are fp32, scale 1/sqrt(HD). */
+int loom_depth_attn_forward(int dtype, const void* q, const void* hist_k, const void* hist_v,
+                            int64_t stride_bt, int64_t stride_s, void* d_out, void* w_out,
+                            float* lse_out, int64_t BT, int64_t S, int64_t QH, int64_t HD,
+                            void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Tria (all math fp32; carry tensors [n,3,3] row-major per element)
+ * ------------------------------------------------------------------------ */
+
+/* Depth step family.  Per element e=(b,t,h) of n = B*T*H:
+ *   M = T(r,i,o; alpha, axis)                          (carrier.cuh:33)
+ *   pre = M @ seed[b,h]  if seed && t == 0 && seed_valid[b]
+ *         M @ carry_prev[e] if carry_prev
+ *         M             otherwise
+ *   carry_out[e] = pre / rms(pre);  scale_out[e] = rms(pre);
+ *   p_out[e] = sum_k w[k] * carry_out[e][k]           (gate variants)
+ * Replaces tria_init_forward, tria_init_gate_forward, tria_init_seed_forward,
+ * tria_init_seed_gate_forward, tria_step_forward, tria_step_gate_forward
+ * (kernels/tria/bindings.cpp:84-93).
+ *   r,i,o: [B,T,H] dtype; carry_prev: [B,T,H,3,3] dtype or NULL;
+ *   seed: [B,H,3,3] dtype or NULL; seed_valid: [B] bool (needed with seed);
+ *   w: [9] dtype or NULL; carry_out: dtype or NULL; p_out: [B,T,H] dtype (needed
+ *   with w); scale_out: [B,T,H] float or NULL.  seed and carry_prev are
+ *   mutually exclusive. */
+int loom_tria_depth_forward(int dtype, const void* r, const void* i, const void* o,
+                            const void* carry_prev, const void* seed, const uint8_t* seed_valid,
+                            const void* w, void* carry_out, void* p_out, float* scale_out,
+                            int64_t B, int64_t T, int64_t H, float alpha, int axis, void* stream);
+
+/* p[e] = sum_k w[k] * carry[e][k].  Replaces gate_slot_mix_forward
+ * (kernels/tria/bindings.cpp:97). carry: [n,9] dtype, w: [9] dtype, p: [n] dtype. */
+int loom_gate_slot_mix_forward(int dtype, const void* carry, const void* w, void* p, int64_t n,
+                               void* stream);
+
+/* Softmax over H of <score_w, vec C_h> per row, pooled 9-slot mean and lse.
+ * Replaces slot_attention_pool_forward (bindings.cpp:99).
+ *   carry: [rows,H,9] dtype; score_w: [9] dtype; pooled: [rows,9] dtype;
+ *   lse: [rows] dtype (may be NULL). */
+int loom_slot_attention_pool_forward(int dtype, const void* carry, const void* score_w,
+                                     void* pooled, void* lse, int64_t rows, int64_t H,
+                                     void* stream);
+
+/* Temporal carry over T per (b,h) stream: acc_t = N(D_t @ acc_{t-1}), restart
+ * acc = N(D_t) on reset[b,t] or when no valid state is held.
+ * Full form replaces temporal_carry_forward (bindings.cpp:101): doc [B,T,H,9]
+ * float and scale [B,T,H] float (either may be NULL).
+ * Endpoint form replaces temporal_carry_endpoint_forward (bindings.cpp:103):
+ * initial [B,H,9] dtype or NULL, initial_valid [B] bool or NULL (all valid),
+ * endpoint [B,H,9] dtype, endpoint_f32 [B,H,9] float (either may be NULL).
+ *   depth: [B,T,H,9] dtype; reset: [B,T] bool. */
+int loom_temporal_carry_forward(int dtype, const void* depth, const uint8_t* reset,
+                                float* doc, float* scale, int64_t B, int64_t T, int64_t H,
+                                void* stream);
+int loom_temporal_carry_endpoint_forward(int dtype, const void* depth, const uint8_t* reset,
+                                         const void* initial, const uint8_t* initial_valid,
+                                         void* endpoint, float* endpoint_f32, int64_t B,
+                                         int64_t T, int64_t H, void* stream);
+
+/* PolARM on [n,3,3] matrices, applied where mask[n / per_mask] is set (mask
+ * NULL = everywhere): G = M^T M, s = max(mean(diag G), eps),
+ * M <- M (I - beta/2 (G/s - I)).  In place allowed (in == out).
+ * Replaces tria.polarm (tria.py:128-166), which has no kernel in the reference. */
+int loom_polarm_forward(int dtype, const void* in, void* out, const uint8_t* mask,
+                        int64_t n, int64_t per_mask, float beta, float eps, void* stream);
+
+/* Sparse final cross-attention: per row (b,t) a masked softmax over K keys
+ * (scale * q.k), out = sum_j w_j v_j, an all-masked row gives exact zeros and
+ * lse = -inf.  Replaces final_ca_sparse_forward (bindings.cpp:107).
+ *   q: [B,T,D]; k,v: [B,K,D]; allowed: [B,T,K] bool; out: [B,T,D] (dtype);
+ *   lse: [B,T] float or NULL.  K <= 1024. */
+int loom_final_ca_sparse_forward(int dtype, const void* q, const void* k, const void* v,
+                                 const uint8_t* allowed, void* out, float* lse, int64_t B,
+                                 int64_t T, int64_t K, int64_t D, float scale, void* stream);
+
+/* final_ca_sparse_forward with explicit layout, for decode caches: k/v row j
+ * of batch b at b*kv_stride_b + j*D, allowed row r (= b*T + t) at
+ * r*allowed_stride; with residual != NULL, out = residual + gamma * attention
+ * (TriaFinalCrossAttention.step, tria.py:1560-1595, h + gamma*out). */
+int loom_final_ca_sparse_strided(int dtype, const void* q, const void* k, const void* v,
+                                 int64_t kv_stride_b, const uint8_t* allowed,
+                                 int64_t allowed_stride, const void* residual, float gamma,
+                                 void* out, float* lse, int64_t B, int64_t T, int64_t K, int64_t D,
+                                 float scale, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Decode step (Model.step, loomformer.py:3951-4091)
+ * ------------------------------------------------------------------------ */
+
+/* RoPE of the new token and KV-cache append.  Replaces the q/k rotation and
+ * cache write of GroupedQueryCausalSelfAttention.step (loomformer.py:3304-3315,
+ * YaRNRotaryEmbedding.forward :2983-2985).
+ *   qkv: [B, (QH + 2*KVH)*HD] dtype (output of the qkv projection);
+ *   q_out: [B,QH,HD] dtype (rotated q); cache element (b, t, kvh, d) at
+ *   b*cache_stride_b + t*cache_stride_t + kvh*HD + d; position `pos` is written.
+ *   cos_table/sin_table: [>pos, HD] float, already multiplied by the YaRN
+ *   attention factor (the reference's cos_cached/sin_cached). */
+int loom_rope_append(int dtype, const void* qkv, void* q_out, void* k_cache, void* v_cache,
+                     const float* cos_table, const float* sin_table, int64_t B, int64_t pos,
+                     int64_t QH, int64_t KVH, int64_t HD, int64_t cache_stride_b,
+                     int64_t cache_stride_t, void* stream);
+
+/* Bytes of float workspace loom_gqa_decode_attention needs for len <= max_len. */
+int64_t loom_gqa_workspace_bytes(int64_t B, int64_t max_len, int64_t QH, int64_t KVH, int64_t HD);
+
+/* Causal GQA attention of one query position over cache positions [0, len):
+ * A = softmax(q k^T / sqrt(HD)) in fp32, c_out = A V, kctx_out = A K (the
+ * roped keys).  Replaces the score/softmax/context part of
+ * GroupedQueryCausalSelfAttention.step (loomformer.py:3316-3329) without
+ * materialising the GQA repeat: q-head h reads kv head h / (QH/KVH).
+ *   q: [B,QH,HD]; caches as in loom_rope_append; c_out, kctx_out: [B,QH,HD]
+ *   (dtype); workspace: at least loom_gqa_workspace_bytes(B, len, ...) bytes. */
+int loom_gqa_decode_attention(int dtype, const void* q, const void* k_cache, const void* v_cache,
+                              int64_t cache_stride_b, int64_t cache_stride_t, void* c_out,
+                              void* kctx_out, float* workspace, int64_t workspace_bytes,
+                              int64_t B, int64_t len, int64_t QH, int64_t KVH, int64_t HD,
+                              void* stream);
+
+/* out = LayerNorm(a + b) (b may be NULL) over rows of N <= 2048, fp32 gamma and
+ * beta, biased variance.  Replaces ln_attn/ln_ffn(skip + branch)
+ * (loomformer.py:4000, :4045). */
+int loom_add_layernorm(int dtype, const void* a, const void* b, const float* gamma,
+                       const float* beta, void* out, int64_t rows, int64_t N, float eps,
+                       void* stream);
+
+/* Decode-time temporal Tria update of one token (loomformer.py:4056-4085):
+ *   out[b] = depth[b]                      if prev == NULL or reset_now[b]
+ *            N(depth[b] @ prev[b])          otherwise
+ *   then, where fire[b] (fire may be NULL), PolARM(out[b], polarm_beta, eps).
+ *   depth, prev, out: [B,H,3,3] dtype; reset_now, fire: [B] bool. */
+int loom_tria_decode_temporal(int dtype, const void* depth, const void* prev,
+                              const uint8_t* reset_now, const uint8_t* fire, void* out,
+                              int64_t B, int64_t H, float polarm_beta, float eps, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOOM_HIP_H */

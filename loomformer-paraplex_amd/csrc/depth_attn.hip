@@ -1,0 +1,249 @@
+// Depth attention for gfx950: softmax over the depth axis of S history keys
+// with one learned query per q-head.
+//
+// Layout: element (bt, s, qh, d) of K/V lives at bt*stride_bt + s*stride_s +
+// qh*HD + d, so a [B,T,S,QH,HD] stack and a strided decode view
+// hist[:, :, :S] of a [B,T,S_max,QH,HD] buffer are both read in place.
+//
+// Mapping: one (bt, qh) row per aligned group of 16 lanes; lane j owns the
+// EPL = HD/16 contiguous elements [j*EPL, (j+1)*EPL).  A wavefront therefore
+// covers 4 heads = 4*HD contiguous elements of one (bt, s) slice.  Scores for
+// 8 depth slots are formed before any value is read (8 independent K loads in
+// flight per lane), then folded into an fp32 online softmax.
+#include <cmath>
+
+#include "loom_common.h"
+
+namespace loom {
+
+template <typename T, int EPL>
+struct RowIO {
+    __device__ __forceinline__ static void load(const T* p, float v[EPL]) {
+        if constexpr (sizeof(T) == 2 && EPL % 2 == 0) {
+#pragma unroll
+            for (int k = 0; k < EPL / 2; ++k) {
+                const uint32_t w = reinterpret_cast<const uint32_t*>(p)[k];
+                T lo{(uint16_t)(w & 0xffffu)}, hi{(uint16_t)(w >> 16)};
+                v[2 * k] = ld(&lo);
+                v[2 * k + 1] = ld(&hi);
+            }
+        } else if constexpr (sizeof(T) == 4 && EPL % 2 == 0) {
+#pragma unroll
+            for (int k = 0; k < EPL / 2; ++k) {
+                const float2 w = reinterpret_cast<const float2*>(p)[k];
+                v[2 * k] = w.x;
+                v[2 * k + 1] = w.y;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) v[k] = ld(p + k);
+        }
+    }
+    __device__ __forceinline__ static void store(T* p, const float v[EPL]) {
+        if constexpr (sizeof(T) == 2 && EPL % 2 == 0) {
+#pragma unroll
+            for (int k = 0; k < EPL / 2; ++k) {
+                T lo, hi;
+                st(&lo, v[2 * k]);
+                st(&hi, v[2 * k + 1]);
+                reinterpret_cast<uint32_t*>(p)[k] = (uint32_t)lo.x | ((uint32_t)hi.x << 16);
+            }
+        } else if constexpr (sizeof(T) == 4 && EPL % 2 == 0) {
+#pragma unroll
+            for (int k = 0; k < EPL / 2; ++k)
+                reinterpret_cast<float2*>(p)[k] = make_float2(v[2 * k], v[2 * k + 1]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) st(p + k, v[k]);
+        }
+    }
+};
+
+constexpr int kDepthChunk = 8;
+
+template <typename T, int EPL>
+__global__ void __launch_bounds__(256)
+depth_attn_kernel(const T* __restrict__ q, const T* __restrict__ hk, const T* __restrict__ hv,
+                  int64_t sbt, int64_t ss, T* __restrict__ d_out, T* __restrict__ w_out,
+                  float* __restrict__ lse_out, int64_t rows, int S, int QH, float scale) {
+    constexpr int HD = EPL * 16;
+    const int j = threadIdx.x & 15;
+    const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+    if (row >= rows) return;  // all 16 lanes of a group leave together
+    const int qh = (int)(row % QH);
+    const int64_t bt = row / QH;
+    const int d0 = j * EPL;
+
+    float qv[EPL];
+    RowIO<T, EPL>::load(q + qh * HD + d0, qv);
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) qv[k] *= scale;
+
+    const T* kp = hk + bt * sbt + qh * HD + d0;
+    const T* vp = hv + bt * sbt + qh * HD + d0;
+    float m = -INFINITY, l = 0.0f, acc[EPL];
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) acc[k] = 0.0f;
+
+    for (int s0 = 0; s0 < S; s0 += kDepthChunk) {
+        float sc[kDepthChunk];
+#pragma unroll
+        for (int c = 0; c < kDepthChunk; ++c) {
+            if (s0 + c < S) {
+                float kv[EPL];
+                RowIO<T, EPL>::load(kp + (int64_t)(s0 + c) * ss, kv);
+                float dot = 0.0f;
+#pragma unroll
+                for (int k = 0; k < EPL; ++k) dot = fmaf(qv[k], kv[k], dot);
+                sc[c] = dot;
+            } else {
+                sc[c] = 0.0f;
+            }
+        }
+        float cmax = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < kDepthChunk; ++c) {
+            sc[c] = group_sum<16>(sc[c]);
+            if (s0 + c < S) cmax = fmaxf(cmax, sc[c]);
+        }
+        const float m_new = fmaxf(m, cmax);
+        const float corr = fexp(m - m_new);  // exp(-inf) = 0 on the first chunk
+        l *= corr;
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) acc[k] *= corr;
+#pragma unroll
+        for (int c = 0; c < kDepthChunk; ++c) {
+            if (s0 + c < S) {
+                const float p = fexp(sc[c] - m_new);
+                float vv[EPL];
+                RowIO<T, EPL>::load(vp + (int64_t)(s0 + c) * ss, vv);
+                l += p;
+#pragma unroll
+                for (int k = 0; k < EPL; ++k) acc[k] = fmaf(p, vv[k], acc[k]);
+            }
+        }
+        m = m_new;
+    }
+    const float inv_l = 1.0f / l;
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) acc[k] *= inv_l;
+    RowIO<T, EPL>::store(d_out + row * HD + d0, acc);
+    if (lse_out != nullptr && j == 0) lse_out[row] = m + logf(l);
+    if (w_out != nullptr) {
+        // weights: recompute each score (one more K read) and normalise
+        for (int s = 0; s < S; ++s) {
+            float kv[EPL];
+            RowIO<T, EPL>::load(kp + (int64_t)s * ss, kv);
+            float dot = 0.0f;
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) dot = fmaf(qv[k], kv[k], dot);
+            dot = group_sum<16>(dot);
+            if (j == 0) st(w_out + row * S + s, fexp(dot - m) * inv_l);
+        }
+    }
+}
+
+// Any HD: one thread per (bt, qh) row, online softmax, scalar loads.
+template <typename T>
+__global__ void __launch_bounds__(256)
+depth_attn_generic_kernel(const T* __restrict__ q, const T* __restrict__ hk,
+                          const T* __restrict__ hv, int64_t sbt, int64_t ss,
+                          T* __restrict__ d_out, T* __restrict__ w_out, float* __restrict__ lse_out,
+                          int64_t rows, int S, int QH, int HD, float scale) {
+    const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const int qh = (int)(row % QH);
+    const int64_t bt = row / QH;
+    const T* kp = hk + bt * sbt + qh * HD;
+    const T* vp = hv + bt * sbt + qh * HD;
+    float m = -INFINITY, l = 0.0f;
+    for (int s = 0; s < S; ++s) {
+        float dot = 0.0f;
+        for (int d = 0; d < HD; ++d) dot = fmaf(ld(q + qh * HD + d), ld(kp + s * ss + d), dot);
+        m = fmaxf(m, dot * scale);
+    }
+    for (int s = 0; s < S; ++s) {
+        float dot = 0.0f;
+        for (int d = 0; d < HD; ++d) dot = fmaf(ld(q + qh * HD + d), ld(kp + s * ss + d), dot);
+        const float p = fexp(dot * scale - m);
+        l += p;
+        if (w_out != nullptr) st(w_out + row * S + s, p);
+    }
+    const float inv_l = 1.0f / l;
+    for (int d = 0; d < HD; ++d) {
+        float a = 0.0f;
+        for (int s = 0; s < S; ++s) {
+            float dot = 0.0f;
+            for (int e = 0; e < HD; ++e) dot = fmaf(ld(q + qh * HD + e), ld(kp + s * ss + e), dot);
+            a = fmaf(fexp(dot * scale - m), ld(vp + s * ss + d), a);
+        }
+        st(d_out + row * HD + d, a * inv_l);
+    }
+    if (w_out != nullptr)
+        for (int s = 0; s < S; ++s) st(w_out + row * S + s, ld(w_out + row * S + s) * inv_l);
+    if (lse_out != nullptr) lse_out[row] = m + logf(l);
+}
+
+template <typename T>
+static int dispatch_depth(const void* q, const void* hk, const void* hv, int64_t sbt, int64_t ss,
+                          void* d_out, void* w_out, float* lse_out, int64_t BT, int64_t S,
+                          int64_t QH, int64_t HD, hipStream_t stream) {
+    const int64_t rows = BT * QH;
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int threads = 256;
+    const bool aligned = ((sbt * (int64_t)sizeof(T)) % 4 == 0) && ((ss * (int64_t)sizeof(T)) % 4 == 0) &&
+                         (((uintptr_t)hk | (uintptr_t)hv | (uintptr_t)q | (uintptr_t)d_out) % 8 == 0);
+    const int epl = (HD % 16 == 0) ? (int)(HD / 16) : 0;
+#define LOOM_DA_CASE(E)                                                                          \
+    case E:                                                                                      \
+        hipLaunchKernelGGL((depth_attn_kernel<T, E>), dim3((unsigned)ceil_div(rows * 16, threads)), \
+                           dim3(threads), 0, stream, (const T*)q, (const T*)hk, (const T*)hv, sbt, \
+                           ss, (T*)d_out, (T*)w_out, lse_out, rows, (int)S, (int)QH, scale);       \
+        return launch_status("loom_depth_attn_forward");
+    if (aligned) {
+        switch (epl) {
+            LOOM_DA_CASE(2)
+            LOOM_DA_CASE(4)
+            LOOM_DA_CASE(6)
+            LOOM_DA_CASE(8)
+            default: break;
+        }
+    }
+#undef LOOM_DA_CASE
+    hipLaunchKernelGGL((depth_attn_generic_kernel<T>), dim3((unsigned)ceil_div(rows, threads)),
+                       dim3(threads), 0, stream, (const T*)q, (const T*)hk, (const T*)hv, sbt, ss,
+                       (T*)d_out, (T*)w_out, lse_out, rows, (int)S, (int)QH, (int)HD, scale);
+    return launch_status("loom_depth_attn_forward");
+}
+
+}  // namespace loom
+
+using namespace loom;
+
+extern "C" int loom_depth_attn_forward(int dtype, const void* q, const void* hist_k,
+                                       const void* hist_v, int64_t stride_bt, int64_t stride_s,
+                                       void* d_out, void* w_out, float* lse_out, int64_t BT,
+                                       int64_t S, int64_t QH, int64_t HD, void* stream) {
+    clear_error();
+    LOOM_CHECK(q && hist_k && hist_v && d_out, "depth_attn: null tensor argument");
+    LOOM_CHECK(BT >= 0 && S >= 1 && QH >= 1 && HD >= 1, "depth_attn: bad shape BT=%lld S=%lld",
+               (long long)BT, (long long)S);
+    LOOM_CHECK(stride_s >= QH * HD && stride_bt >= S * stride_s,
+               "depth_attn: strides (bt=%lld, s=%lld) overlap the [S,QH,HD] block",
+               (long long)stride_bt, (long long)stride_s);
+    if (BT == 0) return LOOM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    switch (dtype) {
+        case LOOM_F32:
+            return dispatch_depth<float>(q, hist_k, hist_v, stride_bt, stride_s, d_out, w_out,
+                                         lse_out, BT, S, QH, HD, st);
+        case LOOM_BF16:
+            return dispatch_depth<bf16_t>(q, hist_k, hist_v, stride_bt, stride_s, d_out, w_out,
+                                          lse_out, BT, S, QH, HD, st);
+        case LOOM_F16:
+            return dispatch_depth<f16_t>(q, hist_k, hist_v, stride_bt, stride_s, d_out, w_out,
+                                         lse_out, BT, S, QH, HD, st);
+    }
+    set_error("depth_attn: unsupported dtype %d", dtype);
+    return LOOM_ERR_INVALID;
+}

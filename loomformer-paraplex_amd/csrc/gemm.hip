@@ -1,0 +1,383 @@
+// Dense projections for gfx950: out[M,N] = epilogue(X[M,K] @ W[N,K]^T).
+//
+// bf16: MFMA v_mfma_f32_16x16x32_bf16, fp32 accumulation.  Block tile
+// 128 (n) x 128 (m) x 64 (k), four waves each owning a 64x64 sub-tile as 4x4
+// MFMA tiles.  The MFMA A operand is the weight tile (rows n), the B operand
+// the activation tile (columns m), so each lane's four accumulator values are
+// four consecutive n of one output row m (one 8-byte store).  Both tiles are
+// K-contiguous in LDS with rows padded to 144 B, so the 16-byte fragment reads
+// of 16 consecutive rows fall in distinct banks.
+//
+// fp32/fp16: SIMT tile 64x64x16, 4x4 outputs per thread, fp32 FMA.
+//
+// "Gather" mode is the grouped W_imag product of ParaplexFFN: the activation
+// row of hidden group g is the concatenation of sector slices
+// [Q_g | Kctx_g | C_g | U | D_g] (head sectors) or [Q_g | Kctx | C | U | D]
+// (open sectors); the loader reads each 8-element piece from its sector, so
+// the packed matrix is never written to HBM.
+#include <cmath>
+
+#include "loom_common.h"
+
+namespace loom {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct GemmArgs {
+    const void* X;
+    int64_t ldx;
+    const void* W;
+    int64_t ldw;
+    const float* bias;
+    const void* gate_p;
+    float gate_alpha;
+    const void* residual;
+    void* out;
+    int64_t ldc;
+    int64_t M, N, K;
+    // gather mode (beta space)
+    const void* src[5];  // Q, Kctx, C, U, D  (each [M, Nm] row-major)
+    int64_t Nm, HD, Hq;
+    int open;
+};
+
+// Element offset of packed column kk of group g, and which source it is in.
+__device__ __forceinline__ const void* gather_ptr(const GemmArgs& a, int64_t m, int64_t kk,
+                                                  int64_t g, int elem_size) {
+    int s;
+    int64_t col;
+    const int64_t HD = a.HD, Nm = a.Nm;
+    if (!a.open) {
+        if (kk < HD) { s = 0; col = g * HD + kk; }
+        else if (kk < 2 * HD) { s = 1; col = g * HD + kk - HD; }
+        else if (kk < 3 * HD) { s = 2; col = g * HD + kk - 2 * HD; }
+        else if (kk < 3 * HD + Nm) { s = 3; col = kk - 3 * HD; }
+        else { s = 4; col = g * HD + kk - 3 * HD - Nm; }
+    } else {
+        if (kk < HD) { s = 0; col = g * HD + kk; }
+        else if (kk < HD + Nm) { s = 1; col = kk - HD; }
+        else if (kk < HD + 2 * Nm) { s = 2; col = kk - HD - Nm; }
+        else if (kk < HD + 3 * Nm) { s = 3; col = kk - HD - 2 * Nm; }
+        else { s = 4; col = kk - HD - 3 * Nm; }
+    }
+    return (const char*)a.src[s] + (m * Nm + col) * elem_size;
+}
+
+template <typename T>
+__device__ __forceinline__ float epilogue(const GemmArgs& a, int64_t m, int64_t n, float v) {
+    if (a.gate_p != nullptr) v *= 1.0f + a.gate_alpha * ld((const T*)a.gate_p + m * a.ldc + n);
+    if (a.bias != nullptr) v += a.bias[n];
+    if (a.residual != nullptr) v += ld((const T*)a.residual + m * a.ldc + n);
+    return v;
+}
+
+// ------------------------------------------------------------------ MFMA bf16
+
+constexpr int MB_M = 128, MB_N = 128, MB_K = 64, MB_PAD = 8, MB_LD = MB_K + MB_PAD;
+
+template <bool GATHER>
+__global__ void __launch_bounds__(256)
+gemm_bf16_mfma_kernel(GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t Ws[MB_N * MB_LD];
+    __shared__ __attribute__((aligned(16))) uint16_t Xs[MB_M * MB_LD];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wn = wave & 1, wm = wave >> 1;
+    const int64_t n0 = (int64_t)blockIdx.x * MB_N;
+    const int64_t m0 = (int64_t)blockIdx.y * MB_M;
+    const int64_t g = GATHER ? n0 / a.Hq : 0;
+    const uint16_t* W = (const uint16_t*)a.W;
+    const uint16_t* X = (const uint16_t*)a.X;
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    uint4 wreg[4], xreg[4];
+    auto load_tiles = [&](int64_t k0) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int chunk = tid + c * 256;
+            const int row = chunk >> 3;
+            const int64_t k = k0 + (chunk & 7) * 8;
+            const int64_t n = n0 + row;
+            const int64_t m = m0 + row;
+            uint4 wv = make_uint4(0, 0, 0, 0), xv = make_uint4(0, 0, 0, 0);
+            if (n < a.N && k < a.K) wv = *reinterpret_cast<const uint4*>(W + n * a.ldw + k);
+            if (m < a.M && k < a.K) {
+                if constexpr (GATHER)
+                    xv = *reinterpret_cast<const uint4*>(gather_ptr(a, m, k, g, 2));
+                else
+                    xv = *reinterpret_cast<const uint4*>(X + m * a.ldx + k);
+            }
+            wreg[c] = wv;
+            xreg[c] = xv;
+        }
+    };
+    auto store_tiles = [&]() {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int chunk = tid + c * 256;
+            const int row = chunk >> 3;
+            const int kc = (chunk & 7) * 8;
+            *reinterpret_cast<uint4*>(&Ws[row * MB_LD + kc]) = wreg[c];
+            *reinterpret_cast<uint4*>(&Xs[row * MB_LD + kc]) = xreg[c];
+        }
+    };
+
+    const int64_t nk = ceil_div(a.K, MB_K);
+    load_tiles(0);
+    store_tiles();
+    __syncthreads();
+    const int fr = lane & 15;          // fragment row
+    const int fk = (lane >> 4) * 8;    // fragment k offset
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        if (kt + 1 < nk) load_tiles((kt + 1) * MB_K);
+#pragma unroll
+        for (int kk = 0; kk < MB_K; kk += 32) {
+            bf16x8 af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                af[i] = *reinterpret_cast<const bf16x8*>(&Ws[(wn * 64 + i * 16 + fr) * MB_LD + kk + fk]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                bf[j] = *reinterpret_cast<const bf16x8*>(&Xs[(wm * 64 + j * 16 + fr) * MB_LD + kk + fk]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+        if (kt + 1 < nk) {
+            store_tiles();
+            __syncthreads();
+        }
+    }
+
+    uint16_t* out = (uint16_t*)a.out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t nb = n0 + wn * 64 + i * 16 + (lane >> 4) * 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t m = m0 + wm * 64 + j * 16 + (lane & 15);
+            if (m >= a.M) continue;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                v[r] = (nb + r < a.N) ? epilogue<bf16_t>(a, m, nb + r, acc[i][j][r]) : 0.0f;
+            uint16_t* op = out + m * a.ldc + nb;
+            if (nb + 3 < a.N && ((uintptr_t)op & 7) == 0) {
+                const uint32_t lo = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+                const uint32_t hi = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+                *reinterpret_cast<uint2*>(op) = make_uint2(lo, hi);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (nb + r < a.N) op[r] = f32_to_bf16(v[r]);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ SIMT
+
+constexpr int SB_M = 64, SB_N = 64, SB_K = 16;
+
+template <typename T, bool GATHER>
+__global__ void __launch_bounds__(256)
+gemm_simt_kernel(GemmArgs a) {
+    __shared__ float As[SB_K][SB_M + 4];
+    __shared__ float Bs[SB_K][SB_N + 4];
+    const int tid = threadIdx.x;
+    const int tx = tid & 15, ty = tid >> 4;
+    const int64_t n0 = (int64_t)blockIdx.x * SB_N;
+    const int64_t m0 = (int64_t)blockIdx.y * SB_M;
+    const int64_t g = GATHER ? n0 / a.Hq : 0;
+    const T* X = (const T*)a.X;
+    const T* W = (const T*)a.W;
+    float acc[4][4] = {};
+    const int lrow = tid >> 2, lk = (tid & 3) * 4;
+    for (int64_t k0 = 0; k0 < a.K; k0 += SB_K) {
+        const int64_t m = m0 + lrow, n = n0 + lrow;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t k = k0 + lk + e;
+            float xv = 0.0f, wv = 0.0f;
+            if (m < a.M && k < a.K) {
+                if constexpr (GATHER)
+                    xv = ld((const T*)gather_ptr(a, m, k, g, (int)sizeof(T)));
+                else
+                    xv = ld(X + m * a.ldx + k);
+            }
+            if (n < a.N && k < a.K) wv = ld(W + n * a.ldw + k);
+            As[lk + e][lrow] = xv;
+            Bs[lk + e][lrow] = wv;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < SB_K; ++k) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) av[i] = As[k][ty * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bv[j] = Bs[k][tx * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+    T* out = (T*)a.out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t m = m0 + ty * 4 + i;
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t n = n0 + tx * 4 + j;
+            if (n < a.N) st(out + m * a.ldc + n, epilogue<T>(a, m, n, acc[i][j]));
+        }
+    }
+}
+
+// One thread per output; any shape / group width.
+template <typename T, bool GATHER>
+__global__ void __launch_bounds__(256)
+gemm_naive_kernel(GemmArgs a) {
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= a.M * a.N) return;
+    const int64_t n = id % a.N, m = id / a.N;
+    const int64_t g = GATHER ? n / a.Hq : 0;
+    float acc = 0.0f;
+    for (int64_t k = 0; k < a.K; ++k) {
+        float xv;
+        if constexpr (GATHER)
+            xv = ld((const T*)gather_ptr(a, m, k, g, (int)sizeof(T)));
+        else
+            xv = ld((const T*)a.X + m * a.ldx + k);
+        acc = fmaf(xv, ld((const T*)a.W + n * a.ldw + k), acc);
+    }
+    st((T*)a.out + m * a.ldc + n, epilogue<T>(a, m, n, acc));
+}
+
+template <typename T, bool GATHER>
+static int run_gemm(const GemmArgs& a, hipStream_t st, const char* what) {
+    if (a.M == 0 || a.N == 0) return LOOM_OK;
+    if constexpr (sizeof(T) == 2 && std::is_same<T, bf16_t>::value) {
+        bool ok = a.K % 8 == 0;
+        if (GATHER) ok = ok && a.Hq % MB_N == 0 && a.HD % 8 == 0 && a.Nm % 8 == 0;
+        else ok = ok && a.ldx % 8 == 0 && ((uintptr_t)a.X & 15) == 0;
+        ok = ok && a.ldw % 8 == 0 && ((uintptr_t)a.W & 15) == 0;
+        if (GATHER)
+            for (int s = 0; s < 5; ++s) ok = ok && ((uintptr_t)a.src[s] & 15) == 0;
+        if (ok) {
+            dim3 grid((unsigned)ceil_div(a.N, MB_N), (unsigned)ceil_div(a.M, MB_M));
+            hipLaunchKernelGGL((gemm_bf16_mfma_kernel<GATHER>), grid, dim3(256), 0, st, a);
+            return launch_status(what);
+        }
+    }
+    if (!GATHER || a.Hq % SB_N == 0) {
+        dim3 grid((unsigned)ceil_div(a.N, SB_N), (unsigned)ceil_div(a.M, SB_M));
+        hipLaunchKernelGGL((gemm_simt_kernel<T, GATHER>), grid, dim3(256), 0, st, a);
+        return launch_status(what);
+    }
+    hipLaunchKernelGGL((gemm_naive_kernel<T, GATHER>), dim3((unsigned)ceil_div(a.M * a.N, 256)),
+                       dim3(256), 0, st, a);
+    return launch_status(what);
+}
+
+template <typename T>
+static int linear_dispatch(const GemmArgs& a, hipStream_t st) {
+    return run_gemm<T, false>(a, st, "loom_linear");
+}
+
+template <typename T>
+static int beta_dispatch(const GemmArgs& a, void* r_pack, int64_t QH, hipStream_t st);
+
+// Optional packed copy [QH, M, imag_in] (the reference's second output).
+template <typename T>
+__global__ void pack_kernel(GemmArgs a, T* __restrict__ pack, int64_t QH) {
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = QH * a.M * a.K;
+    if (id >= total) return;
+    const int64_t kk = id % a.K;
+    const int64_t m = (id / a.K) % a.M;
+    const int64_t g = id / (a.K * a.M);
+    pack[id] = *(const T*)gather_ptr(a, m, kk, g, (int)sizeof(T));
+}
+
+template <typename T>
+static int beta_dispatch(const GemmArgs& a, void* r_pack, int64_t QH, hipStream_t st) {
+    if (r_pack != nullptr) {
+        const int64_t total = QH * a.M * a.K;
+        hipLaunchKernelGGL((pack_kernel<T>), dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
+                           a, (T*)r_pack, QH);
+        int rc = launch_status("loom_beta_forward(pack)");
+        if (rc != LOOM_OK) return rc;
+    }
+    return run_gemm<T, true>(a, st, "loom_beta_forward");
+}
+
+}  // namespace loom
+
+using namespace loom;
+
+extern "C" int loom_linear(int dtype, const void* A, int64_t lda, const void* W, int64_t ldw,
+                           const float* bias, const void* gate_p, float gate_alpha,
+                           const void* residual, void* out, int64_t ldc, int64_t M, int64_t Nout,
+                           int64_t K, void* stream) {
+    clear_error();
+    LOOM_CHECK(A && W && out, "linear: null tensor argument");
+    LOOM_CHECK(M >= 0 && Nout >= 0 && K >= 1, "linear: bad shape M=%lld N=%lld K=%lld",
+               (long long)M, (long long)Nout, (long long)K);
+    LOOM_CHECK(lda >= K && ldw >= K && ldc >= Nout, "linear: row strides smaller than the rows");
+    GemmArgs a{};
+    a.X = A; a.ldx = lda; a.W = W; a.ldw = ldw; a.bias = bias; a.gate_p = gate_p;
+    a.gate_alpha = gate_alpha; a.residual = residual; a.out = out; a.ldc = ldc;
+    a.M = M; a.N = Nout; a.K = K;
+    switch (dtype) {
+        case LOOM_F32: return linear_dispatch<float>(a, (hipStream_t)stream);
+        case LOOM_BF16: return linear_dispatch<bf16_t>(a, (hipStream_t)stream);
+        case LOOM_F16: return linear_dispatch<f16_t>(a, (hipStream_t)stream);
+    }
+    set_error("linear: unsupported dtype %d", dtype);
+    return LOOM_ERR_INVALID;
+}
+
+extern "C" int loom_beta_forward(int dtype, const void* u, const void* q_h, const void* k_ctx_h,
+                                 const void* c_h, const void* d_h, const void* w_compact,
+                                 void* out, void* r_pack, int64_t M, int64_t N, int64_t H,
+                                 int64_t imag_in, int64_t hidden_per_q_head, int64_t head_dim,
+                                 int64_t n_q_heads, int open_sectors, void* stream) {
+    clear_error();
+    LOOM_CHECK(u && q_h && k_ctx_h && c_h && d_h && w_compact && out,
+               "beta_space: null tensor argument");
+    LOOM_CHECK(M >= 0 && N > 0 && H > 0 && head_dim > 0 && n_q_heads > 0, "beta_space: bad shape");
+    LOOM_CHECK(n_q_heads * head_dim == N, "beta_space: n_q_heads*head_dim (%lld) != N (%lld)",
+               (long long)(n_q_heads * head_dim), (long long)N);
+    LOOM_CHECK(hidden_per_q_head * n_q_heads == H, "beta_space: hidden_per_q_head*n_q_heads != H");
+    const int64_t want = open_sectors ? 4 * N + head_dim : N + 4 * head_dim;
+    LOOM_CHECK(imag_in == want, "beta_space: imag_in=%lld, expected %lld", (long long)imag_in,
+               (long long)want);
+    LOOM_CHECK((N % 4) == 0 && (head_dim % 4) == 0 && (imag_in % 4) == 0,
+               "maskpack path requires N, head_dim, IMAG_IN divisible by 4");
+    GemmArgs a{};
+    a.W = w_compact; a.ldw = imag_in; a.out = out; a.ldc = H; a.M = M; a.N = H; a.K = imag_in;
+    a.src[0] = q_h; a.src[1] = k_ctx_h; a.src[2] = c_h; a.src[3] = u; a.src[4] = d_h;
+    a.Nm = N; a.HD = head_dim; a.Hq = hidden_per_q_head; a.open = open_sectors ? 1 : 0;
+    a.X = u; a.ldx = N;
+    switch (dtype) {
+        case LOOM_F32: return beta_dispatch<float>(a, r_pack, n_q_heads, (hipStream_t)stream);
+        case LOOM_BF16: return beta_dispatch<bf16_t>(a, r_pack, n_q_heads, (hipStream_t)stream);
+        case LOOM_F16: return beta_dispatch<f16_t>(a, r_pack, n_q_heads, (hipStream_t)stream);
+    }
+    set_error("beta_space: unsupported dtype %d", dtype);
+    return LOOM_ERR_INVALID;
+}

@@ -1,0 +1,160 @@
+// Shared device/host helpers for the LoomFormer gfx950 library.
+//
+// All arithmetic is fp32 in registers; tensors are fp32, bf16 or fp16 in HBM.
+// Conversions to bf16 round to nearest-even (the same rounding torch uses for
+// .to(torch.bfloat16)).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/loom_hip.h"
+
+namespace loom {
+
+// ------------------------------------------------------------------ errors
+void set_error(const char* fmt, ...);
+void clear_error();
+int launch_status(const char* what);
+
+#define LOOM_CHECK(cond, ...)            \
+    do {                                 \
+        if (!(cond)) {                   \
+            ::loom::set_error(__VA_ARGS__); \
+            return LOOM_ERR_INVALID;     \
+        }                                \
+    } while (0)
+
+// ------------------------------------------------------------------ dtypes
+struct bf16_t { uint16_t x; };
+struct f16_t { uint16_t x; };
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float(((uint32_t)h) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);  // quiet NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+template <typename T> struct Cvt;
+template <> struct Cvt<float> {
+    __device__ __forceinline__ static float load(const float* p) { return *p; }
+    __device__ __forceinline__ static void store(float* p, float v) { *p = v; }
+};
+template <> struct Cvt<bf16_t> {
+    __device__ __forceinline__ static float load(const bf16_t* p) { return bf16_to_f32(p->x); }
+    __device__ __forceinline__ static void store(bf16_t* p, float v) { p->x = f32_to_bf16(v); }
+};
+template <> struct Cvt<f16_t> {
+    __device__ __forceinline__ static float load(const f16_t* p) {
+        return __half2float(__ushort_as_half(p->x));
+    }
+    __device__ __forceinline__ static void store(f16_t* p, float v) {
+        p->x = __half_as_ushort(__float2half_rn(v));
+    }
+};
+
+template <typename T> __device__ __forceinline__ float ld(const T* p) { return Cvt<T>::load(p); }
+template <typename T> __device__ __forceinline__ void st(T* p, float v) { Cvt<T>::store(p, v); }
+
+// Vector of 8 elements (16 B for 16-bit types, 32 B for fp32) loaded/stored
+// as whole 16-byte transactions.
+template <typename T> struct Vec8;
+template <> struct Vec8<float> {
+    __device__ __forceinline__ static void load(const float* p, float v[8]) {
+        const float4 a = *reinterpret_cast<const float4*>(p);
+        const float4 b = *reinterpret_cast<const float4*>(p + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    __device__ __forceinline__ static void store(float* p, const float v[8]) {
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+};
+template <typename T16> struct Vec8_16 {
+    __device__ __forceinline__ static void load(const T16* p, float v[8]) {
+        const uint4 a = *reinterpret_cast<const uint4*>(p);
+        const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            T16 lo{(uint16_t)(w[k] & 0xffffu)}, hi{(uint16_t)(w[k] >> 16)};
+            v[2 * k] = Cvt<T16>::load(&lo);
+            v[2 * k + 1] = Cvt<T16>::load(&hi);
+        }
+    }
+    __device__ __forceinline__ static void store(T16* p, const float v[8]) {
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            T16 lo, hi;
+            Cvt<T16>::store(&lo, v[2 * k]);
+            Cvt<T16>::store(&hi, v[2 * k + 1]);
+            w[k] = (uint32_t)lo.x | ((uint32_t)hi.x << 16);
+        }
+        *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+};
+template <> struct Vec8<bf16_t> : Vec8_16<bf16_t> {};
+template <> struct Vec8<f16_t> : Vec8_16<f16_t> {};
+
+// ------------------------------------------------------------------ fast math
+// Built directly on the gfx950 transcendental instructions (v_exp_f32 = 2^x,
+// v_log_f32 = log2 x, v_sin_f32 = sin(2*pi*x), v_rsq_f32, v_rcp_f32,
+// v_sqrt_f32); each is accurate to about one ulp over the ranges used here.
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+__device__ __forceinline__ float flog2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float frsq(float x) { return __builtin_amdgcn_rsqf(x); }
+__device__ __forceinline__ float fsqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
+// sin(2*pi*r) for |r| <= 0.25 (one quarter turn)
+__device__ __forceinline__ float fsin_turns(float r) { return __builtin_amdgcn_sinf(r); }
+
+// log1p(t) for t in [0, 1]: log(u) corrected by the rounding of u = 1 + t
+// (the classic Goldberg correction), so small t keep full relative accuracy.
+__device__ __forceinline__ float flog1p_unit(float t) {
+    const float u = 1.0f + t;
+    const float du = u - 1.0f;
+    const float l = flog2(u) * kLn2;
+    // when u rounds to 1, du == 0 and log1p(t) ~= t
+    return du == 0.0f ? t : l * (t / du);
+}
+
+// softplus with torch's threshold (x > 20 -> x); log1p(exp(x)) otherwise,
+// evaluated as max(x,0) + log1p(exp(-|x|)) to keep it accurate for x < 0.
+__device__ __forceinline__ float fsoftplus(float x) {
+    if (x > 20.0f) return x;
+    const float t = fexp(-fabsf(x));
+    return fmaxf(x, 0.0f) + flog1p_unit(t);
+}
+
+// ------------------------------------------------------------------ wave ops
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+// sum over aligned groups of G lanes (G a power of two <= 64)
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace loom

@@ -1,0 +1,270 @@
+// Fused Paraplex pointwise chain, phase_sin and PvPowLU for gfx950.
+//
+// paraplex_forward: one thread owns VEC consecutive hidden units h of one
+// batch row and walks a chunk of TC consecutive tokens.  The previous-token
+// phase I_base[t-1] is carried in registers from the previous iteration, so
+// the only extra HBM read is one beta row per chunk (1/TC overhead).  Loads
+// and stores are whole 16-byte vectors, so a wavefront touches 64*16 = 1 KiB
+// of contiguous memory per tensor and per token.
+#include "loom_common.h"
+
+namespace loom {
+
+// I_base = sin(pi/2 * beta / sqrt(1 + beta^2)) = sin(2*pi * beta/(4 sqrt(1+beta^2)))
+__device__ __forceinline__ float phase_of(float beta) {
+    return fsin_turns(0.25f * beta * frsq(1.0f + beta * beta));
+}
+
+// G(A) = max(A,1e-12)^(m/(sqrt(A)+1)) * sigmoid(A), with one reciprocal for
+// both divisions: r = 1/((sqrt A + 1)(1 + e^-A)).
+__device__ __forceinline__ float powlu_gate(float amp, float m) {
+    const float safe = fmaxf(amp, 1.0e-12f);
+    const float d1 = fsqrt(safe) + 1.0f;
+    const float d2 = 1.0f + fexp(-amp);
+    const float r = frcp(d1 * d2);
+    const float expo = m * d2 * r;      // m / (sqrt(A) + 1)
+    const float sig = d1 * r;           // 1 / (1 + e^-A)
+    return __builtin_amdgcn_exp2f(expo * flog2(safe)) * sig;
+}
+
+template <typename T, int VEC>
+struct VecIO {
+    __device__ __forceinline__ static void load(const T* p, float v[VEC]) {
+        if constexpr (VEC == 8) {
+            Vec8<T>::load(p, v);
+        } else {
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) v[k] = ld(p + k);
+        }
+    }
+    __device__ __forceinline__ static void store(T* p, const float v[VEC]) {
+        if constexpr (VEC == 8) {
+            Vec8<T>::store(p, v);
+        } else {
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) st(p + k, v[k]);
+        }
+    }
+};
+
+template <typename T, int VEC, bool SAME_GATE>
+__global__ void __launch_bounds__(256)
+paraplex_forward_kernel(const T* __restrict__ p_real, const T* __restrict__ gate_src,
+                        const T* __restrict__ beta_lin, const float* __restrict__ bias,
+                        const T* __restrict__ trace, const float* __restrict__ trace_w,
+                        const uint8_t* __restrict__ reset, const float* __restrict__ anchor,
+                        T* __restrict__ act, T* __restrict__ s_out, T* __restrict__ next_trace,
+                        float* __restrict__ anchor_snap, int64_t B, int64_t T_, int64_t H,
+                        int64_t nchunks, int TC, float m) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid == 0 && anchor_snap != nullptr) anchor_snap[0] = anchor[0];
+    const int64_t HV = H / VEC;
+    if (gid >= B * nchunks * HV) return;
+    const int64_t hv = gid % HV;
+    const int64_t rest = gid / HV;
+    const int64_t chunk = rest % nchunks;
+    const int64_t b = rest / nchunks;
+    const int64_t h0 = hv * VEC;
+    const int64_t t0 = chunk * TC;
+    const int64_t t1 = t0 + TC < T_ ? t0 + TC : T_;
+
+    float bv[VEC], tw[VEC], prev[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        bv[k] = bias[h0 + k];
+        tw[k] = trace_w[h0 + k];
+    }
+    if (t0 == 0) {
+        VecIO<T, VEC>::load(trace + b * H + h0, prev);
+    } else {
+        float bl[VEC];
+        VecIO<T, VEC>::load(beta_lin + ((b * T_ + t0 - 1) * H + h0), bl);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) prev[k] = phase_of(bl[k] + bv[k]);
+    }
+    for (int64_t t = t0; t < t1; ++t) {
+        const int64_t base = (b * T_ + t) * H + h0;
+        float r[VEC], g[VEC], bl[VEC], so[VEC], ao[VEC];
+        VecIO<T, VEC>::load(p_real + base, r);
+        VecIO<T, VEC>::load(beta_lin + base, bl);
+        if constexpr (!SAME_GATE) VecIO<T, VEC>::load(gate_src + base, g);
+        const bool rs = reset != nullptr && reset[b * T_ + t] != 0;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            const float s0 = phase_of(bl[k] + bv[k]);
+            const float pv = rs ? 0.0f : prev[k];
+            const float raw = s0 + pv * tw[k];
+            const float s = raw * frsq(1.0f + raw * raw);
+            const float amp = fsoftplus(SAME_GATE ? r[k] : g[k]);
+            const float p = r[k] + amp * s;
+            so[k] = s;
+            ao[k] = p * powlu_gate(amp, m);
+            prev[k] = s0;
+        }
+        VecIO<T, VEC>::store(s_out + base, so);
+        VecIO<T, VEC>::store(act + base, ao);
+    }
+    if (t1 == T_) VecIO<T, VEC>::store(next_trace + b * H + h0, prev);
+}
+
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256)
+phase_sin_kernel(const T* __restrict__ beta, T* __restrict__ out, int64_t nvec) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nvec;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        float v[VEC];
+        VecIO<T, VEC>::load(beta + i * VEC, v);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) v[k] = phase_of(v[k]);
+        VecIO<T, VEC>::store(out + i * VEC, v);
+    }
+}
+
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256)
+pvpowlu_kernel(const T* __restrict__ x1, const T* __restrict__ x2, T* __restrict__ out,
+               int64_t nvec, float m) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nvec;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        float a[VEC], g[VEC];
+        VecIO<T, VEC>::load(x1 + i * VEC, a);
+        VecIO<T, VEC>::load(x2 + i * VEC, g);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) a[k] *= powlu_gate(g[k], m);
+        VecIO<T, VEC>::store(out + i * VEC, a);
+    }
+}
+
+static bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
+
+template <typename T, int VEC>
+static int launch_paraplex(const void* p_real, const void* gate_src, const void* beta_lin,
+                           const float* bias, const void* trace, const float* trace_w,
+                           const uint8_t* reset, const float* anchor, void* act, void* s,
+                           void* next_trace, float* anchor_snap, int64_t B, int64_t T_,
+                           int64_t H, float m, hipStream_t stream) {
+    // Tokens per thread: enough threads to fill 256 CUs, and long runs of t
+    // so the carried phase saves most re-reads.
+    const int64_t HV = H / VEC;
+    int TC = 16;
+    while (TC > 1 && B * ceil_div(T_, TC) * HV < 256 * 256 * 4) TC >>= 1;
+    const int64_t nchunks = ceil_div(T_, TC);
+    const int64_t total = B * nchunks * HV;
+    const int threads = 256;
+    const int64_t blocks = ceil_div(total, threads);
+    const bool same = gate_src == p_real;
+    auto kern = same ? paraplex_forward_kernel<T, VEC, true> : paraplex_forward_kernel<T, VEC, false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(threads), 0, stream,
+                       (const T*)p_real, (const T*)gate_src, (const T*)beta_lin, bias,
+                       (const T*)trace, trace_w, reset, anchor, (T*)act, (T*)s, (T*)next_trace,
+                       anchor_snap, B, T_, H, nchunks, TC, m);
+    return launch_status("loom_paraplex_forward");
+}
+
+template <typename T>
+static int dispatch_paraplex(const void* p_real, const void* gate_src, const void* beta_lin,
+                             const float* bias, const void* trace, const float* trace_w,
+                             const uint8_t* reset, const float* anchor, void* act, void* s,
+                             void* next_trace, float* anchor_snap, int64_t B, int64_t T_,
+                             int64_t H, float m, hipStream_t stream) {
+    const bool vec = (H % 8 == 0) && aligned16(p_real) && aligned16(gate_src) &&
+                     aligned16(beta_lin) && aligned16(trace) && aligned16(act) &&
+                     aligned16(s) && aligned16(next_trace);
+    if (vec)
+        return launch_paraplex<T, 8>(p_real, gate_src, beta_lin, bias, trace, trace_w, reset,
+                                     anchor, act, s, next_trace, anchor_snap, B, T_, H, m, stream);
+    return launch_paraplex<T, 1>(p_real, gate_src, beta_lin, bias, trace, trace_w, reset, anchor,
+                                 act, s, next_trace, anchor_snap, B, T_, H, m, stream);
+}
+
+template <typename T>
+static int dispatch_elementwise(int which, const void* a, const void* b, void* out, int64_t n,
+                                float m, hipStream_t stream) {
+    const bool vec = (n % 8 == 0) && aligned16(a) && aligned16(b) && aligned16(out);
+    const int threads = 256;
+    const int64_t nvec = vec ? n / 8 : n;
+    int64_t blocks = ceil_div(nvec, threads);
+    if (blocks > 256 * 64) blocks = 256 * 64;
+    if (which == 0) {
+        if (vec)
+            hipLaunchKernelGGL((phase_sin_kernel<T, 8>), dim3(blocks), dim3(threads), 0, stream,
+                               (const T*)a, (T*)out, nvec);
+        else
+            hipLaunchKernelGGL((phase_sin_kernel<T, 1>), dim3(blocks), dim3(threads), 0, stream,
+                               (const T*)a, (T*)out, nvec);
+        return launch_status("loom_phase_sin_forward");
+    }
+    if (vec)
+        hipLaunchKernelGGL((pvpowlu_kernel<T, 8>), dim3(blocks), dim3(threads), 0, stream,
+                           (const T*)a, (const T*)b, (T*)out, nvec, m);
+    else
+        hipLaunchKernelGGL((pvpowlu_kernel<T, 1>), dim3(blocks), dim3(threads), 0, stream,
+                           (const T*)a, (const T*)b, (T*)out, nvec, m);
+    return launch_status("loom_pvpowlu_forward");
+}
+
+}  // namespace loom
+
+using namespace loom;
+
+extern "C" int loom_paraplex_forward(int dtype, const void* p_real, const void* gate_src,
+                                     const void* beta_linear, const float* bias,
+                                     const void* trace, const float* trace_w,
+                                     const uint8_t* reset, const float* anchor, void* act,
+                                     void* s, void* next_trace, float* anchor_snapshot,
+                                     int64_t B, int64_t T, int64_t H, float m, void* stream) {
+    clear_error();
+    LOOM_CHECK(B > 0 && T > 0 && H > 0, "paraplex: empty tensors are unsupported");
+    LOOM_CHECK(p_real && gate_src && beta_linear && bias && trace && trace_w && act && s &&
+                   next_trace,
+               "paraplex: null tensor argument");
+    LOOM_CHECK((anchor == nullptr) == (anchor_snapshot == nullptr),
+               "paraplex: anchor and anchor_snapshot must be given together");
+    hipStream_t st = (hipStream_t)stream;
+    switch (dtype) {
+        case LOOM_F32:
+            return dispatch_paraplex<float>(p_real, gate_src, beta_linear, bias, trace, trace_w,
+                                            reset, anchor, act, s, next_trace, anchor_snapshot, B,
+                                            T, H, m, st);
+        case LOOM_BF16:
+            return dispatch_paraplex<bf16_t>(p_real, gate_src, beta_linear, bias, trace, trace_w,
+                                             reset, anchor, act, s, next_trace, anchor_snapshot,
+                                             B, T, H, m, st);
+        case LOOM_F16:
+            return dispatch_paraplex<f16_t>(p_real, gate_src, beta_linear, bias, trace, trace_w,
+                                            reset, anchor, act, s, next_trace, anchor_snapshot, B,
+                                            T, H, m, st);
+    }
+    set_error("paraplex: unsupported dtype %d", dtype);
+    return LOOM_ERR_INVALID;
+}
+
+extern "C" int loom_phase_sin_forward(int dtype, const void* beta, void* out, int64_t n,
+                                      void* stream) {
+    clear_error();
+    LOOM_CHECK(n >= 0 && beta && out, "phase_sin: bad arguments");
+    if (n == 0) return LOOM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    switch (dtype) {
+        case LOOM_F32: return dispatch_elementwise<float>(0, beta, beta, out, n, 0.f, st);
+        case LOOM_BF16: return dispatch_elementwise<bf16_t>(0, beta, beta, out, n, 0.f, st);
+        case LOOM_F16: return dispatch_elementwise<f16_t>(0, beta, beta, out, n, 0.f, st);
+    }
+    set_error("phase_sin: unsupported dtype %d", dtype);
+    return LOOM_ERR_INVALID;
+}
+
+extern "C" int loom_pvpowlu_forward(int dtype, const void* x1, const void* x2, void* out,
+                                    int64_t n, float m, void* stream) {
+    clear_error();
+    LOOM_CHECK(n >= 0 && x1 && x2 && out, "pvpowlu: bad arguments");
+    if (n == 0) return LOOM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    switch (dtype) {
+        case LOOM_F32: return dispatch_elementwise<float>(1, x1, x2, out, n, m, st);
+        case LOOM_BF16: return dispatch_elementwise<bf16_t>(1, x1, x2, out, n, m, st);
+        case LOOM_F16: return dispatch_elementwise<f16_t>(1, x1, x2, out, n, m, st);
+    }
+    set_error("pvpowlu: unsupported dtype %d", dtype);
+    return LOOM_ERR_INVALID;
+}

@@ -1,0 +1,589 @@
+// Tria carriers for gfx950: local 3x3 operator construction, depth
+// composition, gate slot mix, slot attention pool, temporal carry, PolARM and
+// the sparse final cross-attention.  All math is fp32 in registers.
+//
+// 3x3 matrices are stored row-major, 9 values per element ([..., 3, 3]).
+// Streaming kernels stage each block's slice of 3x3 matrices through LDS so
+// global traffic is whole coalesced rows; per-thread LDS reads have stride 9
+// words (odd), which spreads consecutive lanes over distinct banks.
+#include <cmath>
+
+#include "loom_common.h"
+
+namespace loom {
+
+constexpr int kTriaThreads = 256;
+
+// Local carrier T(r,i,o) = (I + K(a,b,c)) @ R_axis,
+// (a,b,c) = alpha * tanh(x / sqrt(mean(x^2) + eps)), x = (ri, ro, io).
+// The axis is a compile-time parameter: the kernels are instantiated per axis.
+template <int AXIS>
+__device__ __forceinline__ void carrier9(float r, float i, float o, float alpha, float mt[9]) {
+    const float x0 = r * i, x1 = r * o, x2 = i * o;
+    const float inv = 1.0f / sqrtf((x0 * x0 + x1 * x1 + x2 * x2) * (1.0f / 3.0f) + 1e-6f);
+    const float a = alpha * tanhf(x0 * inv);
+    const float b = alpha * tanhf(x1 * inv);
+    const float c = alpha * tanhf(x2 * inv);
+    if constexpr (AXIS == 0) {          // about z
+        mt[0] = -c;   mt[1] = -1.0f; mt[2] = b;
+        mt[3] = 1.0f; mt[4] = -c;    mt[5] = -a;
+        mt[6] = a;    mt[7] = b;     mt[8] = 1.0f;
+    } else if constexpr (AXIS == 1) {   // about x
+        mt[0] = 1.0f; mt[1] = b;     mt[2] = c;
+        mt[3] = c;    mt[4] = -a;    mt[5] = -1.0f;
+        mt[6] = -b;   mt[7] = 1.0f;  mt[8] = -a;
+    } else {                  // about y
+        mt[0] = -b;   mt[1] = -c;    mt[2] = 1.0f;
+        mt[3] = a;    mt[4] = 1.0f;  mt[5] = c;
+        mt[6] = -1.0f; mt[7] = a;    mt[8] = -b;
+    }
+}
+
+// out = A @ B for row-major 3x3
+__device__ __forceinline__ void mm3(const float A[9], const float B[9], float out[9]) {
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+#pragma unroll
+        for (int c = 0; c < 3; ++c)
+            out[3 * r + c] = fmaf(A[3 * r + 2], B[6 + c], fmaf(A[3 * r + 1], B[3 + c], A[3 * r] * B[c]));
+}
+
+// rms over 9 entries with eps inside the root; returns the rms
+__device__ __forceinline__ float rms9(const float v[9]) {
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) s = fmaf(v[k], v[k], s);
+    return sqrtf(s * (1.0f / 9.0f) + 1e-6f);
+}
+
+// Copy n9 = rows*9 contiguous values between global memory and LDS with
+// coalesced word accesses.
+template <typename T>
+__device__ __forceinline__ void stage_in(float* lds, const T* src, int n9) {
+    for (int k = threadIdx.x; k < n9; k += blockDim.x) lds[k] = ld(src + k);
+}
+template <typename T>
+__device__ __forceinline__ void stage_out(T* dst, const float* lds, int n9) {
+    for (int k = threadIdx.x; k < n9; k += blockDim.x) st(dst + k, lds[k]);
+}
+
+// MODE 0: init (pre = M); 1: step (pre = M @ carry_prev[e]);
+// 2: seeded init (pre = M @ seed[b,h] where t == 0 and valid[b], else M)
+template <typename T, int MODE, bool GATE, int AXIS>
+__global__ void __launch_bounds__(kTriaThreads)
+tria_depth_kernel(const T* __restrict__ r, const T* __restrict__ i_, const T* __restrict__ o,
+                  const T* __restrict__ prev, const T* __restrict__ seed,
+                  const uint8_t* __restrict__ valid, const T* __restrict__ w,
+                  T* __restrict__ carry_out, T* __restrict__ p_out, float* __restrict__ scale_out,
+                  int64_t n, int64_t T_, int64_t H, float alpha) {
+    __shared__ float tile[kTriaThreads * 9];
+    const int64_t e0 = (int64_t)blockIdx.x * kTriaThreads;
+    const int cnt = (int)((n - e0) < kTriaThreads ? (n - e0) : kTriaThreads);
+    const int64_t e = e0 + threadIdx.x;
+    const bool live = threadIdx.x < cnt;
+    if constexpr (MODE == 1) {
+        stage_in(tile, prev + e0 * 9, cnt * 9);
+        __syncthreads();
+    }
+    float pre[9];
+    if (live) {
+        float mt[9];
+        carrier9<AXIS>(ld(r + e), ld(i_ + e), ld(o + e), alpha, mt);
+        if constexpr (MODE == 1) {
+            float cp[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) cp[k] = tile[threadIdx.x * 9 + k];
+            mm3(mt, cp, pre);
+        } else if constexpr (MODE == 2) {
+            const int64_t h = e % H;
+            const int64_t bt = e / H;
+            const int64_t t = bt % T_;
+            const int64_t b = bt / T_;
+            if (t == 0 && valid[b] != 0) {
+                float sd[9];
+#pragma unroll
+                for (int k = 0; k < 9; ++k) sd[k] = ld(seed + (b * H + h) * 9 + k);
+                mm3(mt, sd, pre);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 9; ++k) pre[k] = mt[k];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 9; ++k) pre[k] = mt[k];
+        }
+        const float sc = rms9(pre);
+        const float inv = 1.0f / sc;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) pre[k] *= inv;
+        if (scale_out != nullptr) scale_out[e] = sc;
+        if constexpr (GATE) {
+            float p = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) p = fmaf(pre[k], ld(w + k), p);
+            st(p_out + e, p);
+        }
+    }
+    if (carry_out != nullptr) {
+        if constexpr (MODE == 1) __syncthreads();  // everyone has read tile
+        if (live) {
+#pragma unroll
+            for (int k = 0; k < 9; ++k) tile[threadIdx.x * 9 + k] = pre[k];
+        }
+        __syncthreads();
+        stage_out(carry_out + e0 * 9, tile, cnt * 9);
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kTriaThreads)
+gate_slot_mix_kernel(const T* __restrict__ carry, const T* __restrict__ w, T* __restrict__ p,
+                     int64_t n) {
+    __shared__ float tile[kTriaThreads * 9];
+    const int64_t e0 = (int64_t)blockIdx.x * kTriaThreads;
+    const int cnt = (int)((n - e0) < kTriaThreads ? (n - e0) : kTriaThreads);
+    stage_in(tile, carry + e0 * 9, cnt * 9);
+    __syncthreads();
+    if (threadIdx.x < cnt) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) acc = fmaf(tile[threadIdx.x * 9 + k], ld(w + k), acc);
+        st(p + e0 + threadIdx.x, acc);
+    }
+}
+
+// One block per row: softmax over H of <score_w, vec C_h>; each thread keeps
+// an online (max, sum, 9-slot) state over its h's, then the block merges.
+template <typename T>
+__global__ void __launch_bounds__(kTriaThreads)
+slot_pool_kernel(const T* __restrict__ carry, const T* __restrict__ score_w,
+                 T* __restrict__ pooled, T* __restrict__ lse, int64_t H) {
+    __shared__ float red[kTriaThreads / 64][11];
+    const int64_t row = blockIdx.x;
+    const T* base = carry + row * H * 9;
+    float sw[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) sw[k] = ld(score_w + k);
+    float m = -INFINITY, l = 0.0f, acc[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) acc[k] = 0.0f;
+    for (int64_t h = threadIdx.x; h < H; h += blockDim.x) {
+        float c[9];
+        float sc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            c[k] = ld(base + h * 9 + k);
+            sc = fmaf(c[k], sw[k], sc);
+        }
+        const float mn = fmaxf(m, sc);
+        const float corr = expf(m - mn);
+        const float pe = expf(sc - mn);
+        l = l * corr + pe;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) acc[k] = fmaf(pe, c[k], acc[k] * corr);
+        m = mn;
+    }
+    // merge across the wave
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float mo = __shfl_xor(m, off, 64);
+        const float lo = __shfl_xor(l, off, 64);
+        const float mn = fmaxf(m, mo);
+        const float ca = (m == -INFINITY) ? 0.0f : expf(m - mn);
+        const float cb = (mo == -INFINITY) ? 0.0f : expf(mo - mn);
+        l = l * ca + lo * cb;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            const float ao = __shfl_xor(acc[k], off, 64);
+            acc[k] = acc[k] * ca + ao * cb;
+        }
+        m = mn;
+    }
+    const int wid = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        red[wid][0] = m;
+        red[wid][1] = l;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) red[wid][2 + k] = acc[k];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int nw = blockDim.x >> 6;
+        float M = -INFINITY;
+        for (int q = 0; q < nw; ++q) M = fmaxf(M, red[q][0]);
+        float L = 0.0f, A[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+        for (int q = 0; q < nw; ++q) {
+            if (red[q][0] == -INFINITY) continue;
+            const float c = expf(red[q][0] - M);
+            L = fmaf(red[q][1], c, L);
+            for (int k = 0; k < 9; ++k) A[k] = fmaf(red[q][2 + k], c, A[k]);
+        }
+        const float inv = 1.0f / L;
+        for (int k = 0; k < 9; ++k) st(pooled + row * 9 + k, A[k] * inv);
+        if (lse != nullptr) st(lse + row, logf(L) + M);
+    }
+}
+
+// One thread per (b,h) stream, sequential over T.  The loads of the next
+// kPrefetch local matrices are issued before the current one is consumed.
+constexpr int kPrefetch = 4;
+
+template <typename T, bool FULL>
+__global__ void __launch_bounds__(kTriaThreads)
+temporal_carry_kernel(const T* __restrict__ depth, const uint8_t* __restrict__ reset,
+                      const T* __restrict__ initial, const uint8_t* __restrict__ init_valid,
+                      T* __restrict__ endpoint, float* __restrict__ end_f32,
+                      float* __restrict__ doc, float* __restrict__ scale_out, int64_t B, int64_t T_,
+                      int64_t H) {
+    const int64_t sid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (sid >= B * H) return;
+    const int64_t b = sid / H;
+    const int64_t h = sid - b * H;
+    float acc[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    bool have = false;
+    if (initial != nullptr) {
+        have = init_valid == nullptr || init_valid[b] != 0;
+        if (have) {
+#pragma unroll
+            for (int k = 0; k < 9; ++k) acc[k] = ld(initial + sid * 9 + k);
+        }
+    }
+    const int64_t step = H * 9;
+    const T* p = depth + (b * T_ * H + h) * 9;
+    float buf[kPrefetch][9];
+#pragma unroll
+    for (int u = 0; u < kPrefetch; ++u)
+        if (u < T_) {
+#pragma unroll
+            for (int k = 0; k < 9; ++k) buf[u][k] = ld(p + u * step + k);
+        }
+    for (int64_t t0 = 0; t0 < T_; t0 += kPrefetch) {
+#pragma unroll
+        for (int u = 0; u < kPrefetch; ++u) {
+            const int64_t t = t0 + u;
+            if (t < T_) {
+                float loc[9], pre[9];
+#pragma unroll
+                for (int k = 0; k < 9; ++k) loc[k] = buf[u][k];
+                const int64_t tn = t + kPrefetch;
+                if (tn < T_) {
+#pragma unroll
+                    for (int k = 0; k < 9; ++k) buf[u][k] = ld(p + tn * step + k);
+                }
+                const bool restart = !have || reset[b * T_ + t] != 0;
+                if (restart) {
+#pragma unroll
+                    for (int k = 0; k < 9; ++k) pre[k] = loc[k];
+                } else {
+                    mm3(loc, acc, pre);
+                }
+                const float sc = rms9(pre);
+                const float inv = 1.0f / sc;
+#pragma unroll
+                for (int k = 0; k < 9; ++k) acc[k] = pre[k] * inv;
+                have = true;
+                if constexpr (FULL) {
+                    const int64_t e = (b * T_ + t) * H + h;
+                    if (doc != nullptr) {
+#pragma unroll
+                        for (int k = 0; k < 9; ++k) doc[e * 9 + k] = acc[k];
+                    }
+                    if (scale_out != nullptr) scale_out[e] = sc;
+                }
+            }
+        }
+    }
+    if constexpr (!FULL) {
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            if (endpoint != nullptr) st(endpoint + sid * 9 + k, acc[k]);
+            if (end_f32 != nullptr) end_f32[sid * 9 + k] = acc[k];
+        }
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kTriaThreads)
+polarm_kernel(const T* __restrict__ in, T* __restrict__ out, const uint8_t* __restrict__ mask,
+              int64_t n, int64_t per_mask, float beta, float eps) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    float M[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) M[k] = ld(in + e * 9 + k);
+    if (mask == nullptr || mask[e / per_mask] != 0) {
+        float G[9];  // G = M^T M
+#pragma unroll
+        for (int r = 0; r < 3; ++r)
+#pragma unroll
+            for (int c = 0; c < 3; ++c)
+                G[3 * r + c] = fmaf(M[6 + r], M[6 + c], fmaf(M[3 + r], M[3 + c], M[r] * M[c]));
+        const float s = fmaxf((G[0] + G[4] + G[8]) * (1.0f / 3.0f), eps);
+        float C[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            const float id = (k == 0 || k == 4 || k == 8) ? 1.0f : 0.0f;
+            C[k] = id - 0.5f * beta * (G[k] / s - id);
+        }
+        float R[9];
+        mm3(M, C, R);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) M[k] = R[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 9; ++k) st(out + e * 9 + k, M[k]);
+}
+
+// One block per query row: scores over the K keys (one wave per key at a
+// time, lanes over D), masked softmax in LDS, then out = sum_j w_j v_j.
+constexpr int kCaMaxK = 1024;
+
+// k/v row j of batch b at b*kv_stride_b + j*D; allowed row r at r*allowed_stride.
+// With a residual, out = residual + gamma * attention (TriaFinalCrossAttention
+// adds gamma*out to its input, tria.py:1556-1557, :1593-1595).
+template <typename T>
+__global__ void __launch_bounds__(256)
+final_ca_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+                int64_t kv_stride_b, const uint8_t* __restrict__ allowed, int64_t allowed_stride,
+                const T* __restrict__ residual, float gamma, T* __restrict__ out,
+                float* __restrict__ lse, int64_t T_, int64_t K, int64_t D, float scale) {
+    __shared__ float wts[kCaMaxK];
+    __shared__ float red[2];
+    const int64_t row = blockIdx.x;
+    const int64_t b = row / T_;
+    const int lane = threadIdx.x & 63;
+    const int wid = threadIdx.x >> 6;
+    const int nw = blockDim.x >> 6;
+    const T* qr = q + row * D;
+    for (int64_t j = wid; j < K; j += nw) {
+        float s = -INFINITY;
+        if (allowed[row * allowed_stride + j]) {
+            const T* kr = k + b * kv_stride_b + j * D;
+            float dot = 0.0f;
+            for (int64_t d = lane; d < D; d += 64) dot = fmaf(ld(qr + d), ld(kr + d), dot);
+            s = wave_sum(dot) * scale;
+        }
+        if (lane == 0) wts[j] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float mx = -INFINITY;
+        for (int64_t j = 0; j < K; ++j) mx = fmaxf(mx, wts[j]);
+        float sum = 0.0f;
+        if (mx == -INFINITY) {
+            for (int64_t j = 0; j < K; ++j) wts[j] = 0.0f;
+        } else {
+            for (int64_t j = 0; j < K; ++j) {
+                const float e = (wts[j] == -INFINITY) ? 0.0f : expf(wts[j] - mx);
+                wts[j] = e;
+                sum += e;
+            }
+            const float inv = 1.0f / sum;
+            for (int64_t j = 0; j < K; ++j) wts[j] *= inv;
+        }
+        red[0] = mx;
+        red[1] = sum;
+    }
+    __syncthreads();
+    for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
+        float a = 0.0f;
+        for (int64_t j = 0; j < K; ++j) a = fmaf(wts[j], ld(v + b * kv_stride_b + j * D + d), a);
+        if (residual != nullptr) a = ld(residual + row * D + d) + gamma * a;
+        st(out + row * D + d, a);
+    }
+    if (lse != nullptr && threadIdx.x == 0)
+        lse[row] = red[0] == -INFINITY ? -INFINITY : red[0] + logf(red[1]);
+}
+
+// ---------------------------------------------------------------- dispatch
+
+template <typename T>
+static int tria_depth_dispatch(const void* r, const void* i, const void* o, const void* prev,
+                               const void* seed, const uint8_t* valid, const void* w,
+                               void* carry_out, void* p_out, float* scale_out, int64_t B,
+                               int64_t T_, int64_t H, float alpha, int axis, hipStream_t st) {
+    const int64_t n = B * T_ * H;
+    const dim3 grid((unsigned)ceil_div(n, kTriaThreads)), blk(kTriaThreads);
+    const int mode = prev ? 1 : (seed ? 2 : 0);
+    const bool gate = w != nullptr;
+#define LOOM_TD(M, G, A)                                                                       \
+    hipLaunchKernelGGL((tria_depth_kernel<T, M, G, A>), grid, blk, 0, st, (const T*)r,        \
+                       (const T*)i, (const T*)o, (const T*)prev, (const T*)seed, valid,       \
+                       (const T*)w, (T*)carry_out, (T*)p_out, scale_out, n, T_, H, alpha)
+#define LOOM_TD_AXIS(M, G)                        \
+    switch (axis) {                               \
+        case 0: LOOM_TD(M, G, 0); break;          \
+        case 1: LOOM_TD(M, G, 1); break;          \
+        default: LOOM_TD(M, G, 2); break;         \
+    }
+    if (mode == 0) { if (gate) { LOOM_TD_AXIS(0, true) } else { LOOM_TD_AXIS(0, false) } }
+    else if (mode == 1) { if (gate) { LOOM_TD_AXIS(1, true) } else { LOOM_TD_AXIS(1, false) } }
+    else { if (gate) { LOOM_TD_AXIS(2, true) } else { LOOM_TD_AXIS(2, false) } }
+#undef LOOM_TD_AXIS
+#undef LOOM_TD
+    return launch_status("loom_tria_depth_forward");
+}
+
+#define LOOM_DTYPE_SWITCH(dtype, FN, ...)                            \
+    switch (dtype) {                                                 \
+        case LOOM_F32: return FN<float>(__VA_ARGS__);                \
+        case LOOM_BF16: return FN<bf16_t>(__VA_ARGS__);              \
+        case LOOM_F16: return FN<f16_t>(__VA_ARGS__);                \
+    }                                                                \
+    set_error("unsupported dtype %d", dtype);                        \
+    return LOOM_ERR_INVALID;
+
+template <typename T>
+static int gate_mix_dispatch(const void* carry, const void* w, void* p, int64_t n, hipStream_t st) {
+    hipLaunchKernelGGL((gate_slot_mix_kernel<T>), dim3((unsigned)ceil_div(n, kTriaThreads)),
+                       dim3(kTriaThreads), 0, st, (const T*)carry, (const T*)w, (T*)p, n);
+    return launch_status("loom_gate_slot_mix_forward");
+}
+
+template <typename T>
+static int slot_pool_dispatch(const void* carry, const void* sw, void* pooled, void* lse,
+                              int64_t rows, int64_t H, hipStream_t st) {
+    hipLaunchKernelGGL((slot_pool_kernel<T>), dim3((unsigned)rows), dim3(kTriaThreads), 0, st,
+                       (const T*)carry, (const T*)sw, (T*)pooled, (T*)lse, H);
+    return launch_status("loom_slot_attention_pool_forward");
+}
+
+template <typename T>
+static int temporal_dispatch(bool full, const void* depth, const uint8_t* reset, const void* initial,
+                             const uint8_t* valid, void* endpoint, float* end32, float* doc,
+                             float* scale, int64_t B, int64_t T_, int64_t H, hipStream_t st) {
+    const dim3 grid((unsigned)ceil_div(B * H, kTriaThreads)), blk(kTriaThreads);
+    if (full)
+        hipLaunchKernelGGL((temporal_carry_kernel<T, true>), grid, blk, 0, st, (const T*)depth,
+                           reset, (const T*)nullptr, nullptr, (T*)nullptr, nullptr, doc, scale,
+                           B, T_, H);
+    else
+        hipLaunchKernelGGL((temporal_carry_kernel<T, false>), grid, blk, 0, st, (const T*)depth,
+                           reset, (const T*)initial, valid, (T*)endpoint, end32, nullptr, nullptr,
+                           B, T_, H);
+    return launch_status(full ? "loom_temporal_carry_forward" : "loom_temporal_carry_endpoint_forward");
+}
+
+template <typename T>
+static int polarm_dispatch(const void* in, void* out, const uint8_t* mask, int64_t n,
+                           int64_t per_mask, float beta, float eps, hipStream_t st) {
+    hipLaunchKernelGGL((polarm_kernel<T>), dim3((unsigned)ceil_div(n, kTriaThreads)),
+                       dim3(kTriaThreads), 0, st, (const T*)in, (T*)out, mask, n, per_mask, beta,
+                       eps);
+    return launch_status("loom_polarm_forward");
+}
+
+template <typename T>
+static int final_ca_dispatch(const void* q, const void* k, const void* v, int64_t kv_stride_b,
+                             const uint8_t* allowed, int64_t allowed_stride, const void* residual,
+                             float gamma, void* out, float* lse, int64_t B, int64_t T_, int64_t K,
+                             int64_t D, float scale, hipStream_t st) {
+    hipLaunchKernelGGL((final_ca_kernel<T>), dim3((unsigned)(B * T_)), dim3(256), 0, st,
+                       (const T*)q, (const T*)k, (const T*)v, kv_stride_b, allowed, allowed_stride,
+                       (const T*)residual, gamma, (T*)out, lse, T_, K, D, scale);
+    return launch_status("loom_final_ca_sparse_forward");
+}
+
+}  // namespace loom
+
+using namespace loom;
+
+extern "C" int loom_tria_depth_forward(int dtype, const void* r, const void* i, const void* o,
+                                       const void* carry_prev, const void* seed,
+                                       const uint8_t* seed_valid, const void* w, void* carry_out,
+                                       void* p_out, float* scale_out, int64_t B, int64_t T,
+                                       int64_t H, float alpha, int axis, void* stream) {
+    clear_error();
+    LOOM_CHECK(r && i && o, "tria: r, i, o are required");
+    LOOM_CHECK(axis >= 0 && axis <= 2, "tria: axis must be 0(z), 1(x), or 2(y), got %d", axis);
+    LOOM_CHECK(!(carry_prev && seed), "tria: carry_prev and seed are mutually exclusive");
+    LOOM_CHECK(!seed || seed_valid, "tria: seed needs seed_valid");
+    LOOM_CHECK(!w || p_out, "tria: gate weights need p_out");
+    LOOM_CHECK(B >= 0 && T >= 0 && H >= 0, "tria: bad shape");
+    if (B * T * H == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, tria_depth_dispatch, r, i, o, carry_prev, seed, seed_valid, w,
+                      carry_out, p_out, scale_out, B, T, H, alpha, axis, (hipStream_t)stream)
+}
+
+extern "C" int loom_gate_slot_mix_forward(int dtype, const void* carry, const void* w, void* p,
+                                          int64_t n, void* stream) {
+    clear_error();
+    LOOM_CHECK(carry && w && p && n >= 0, "gate_slot_mix: bad arguments");
+    if (n == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, gate_mix_dispatch, carry, w, p, n, (hipStream_t)stream)
+}
+
+extern "C" int loom_slot_attention_pool_forward(int dtype, const void* carry, const void* score_w,
+                                                void* pooled, void* lse, int64_t rows, int64_t H,
+                                                void* stream) {
+    clear_error();
+    LOOM_CHECK(carry && score_w && pooled && rows >= 0 && H >= 1,
+               "slot_attention_pool: bad arguments");
+    if (rows == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, slot_pool_dispatch, carry, score_w, pooled, lse, rows, H,
+                      (hipStream_t)stream)
+}
+
+extern "C" int loom_temporal_carry_forward(int dtype, const void* depth, const uint8_t* reset,
+                                           float* doc, float* scale, int64_t B, int64_t T,
+                                           int64_t H, void* stream) {
+    clear_error();
+    LOOM_CHECK(depth && reset && B >= 0 && T >= 1 && H >= 0, "temporal_carry: bad arguments");
+    if (B * H == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, temporal_dispatch, true, depth, reset, nullptr, nullptr, nullptr,
+                      nullptr, doc, scale, B, T, H, (hipStream_t)stream)
+}
+
+extern "C" int loom_temporal_carry_endpoint_forward(int dtype, const void* depth,
+                                                    const uint8_t* reset, const void* initial,
+                                                    const uint8_t* initial_valid, void* endpoint,
+                                                    float* endpoint_f32, int64_t B, int64_t T,
+                                                    int64_t H, void* stream) {
+    clear_error();
+    LOOM_CHECK(depth && reset && B >= 0 && H >= 0, "temporal_carry_endpoint: bad arguments");
+    LOOM_CHECK(T >= 1, "temporal carry needs at least one token");
+    if (B * H == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, temporal_dispatch, false, depth, reset, initial, initial_valid,
+                      endpoint, endpoint_f32, nullptr, nullptr, B, T, H, (hipStream_t)stream)
+}
+
+extern "C" int loom_polarm_forward(int dtype, const void* in, void* out, const uint8_t* mask,
+                                   int64_t n, int64_t per_mask, float beta, float eps,
+                                   void* stream) {
+    clear_error();
+    LOOM_CHECK(in && out && n >= 0 && per_mask >= 1, "polarm: bad arguments");
+    LOOM_CHECK(beta >= 0.0f && beta < 1.0f, "PolARM beta must be finite and in [0, 1), got %g",
+               (double)beta);
+    if (n == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, polarm_dispatch, in, out, mask, n, per_mask, beta, eps,
+                      (hipStream_t)stream)
+}
+
+extern "C" int loom_final_ca_sparse_forward(int dtype, const void* q, const void* k, const void* v,
+                                            const uint8_t* allowed, void* out, float* lse,
+                                            int64_t B, int64_t T, int64_t K, int64_t D,
+                                            float scale, void* stream) {
+    clear_error();
+    LOOM_CHECK(q && k && v && allowed && out, "final_ca_sparse: null tensor argument");
+    LOOM_CHECK(K >= 1 && K <= kCaMaxK, "final_ca_sparse: K=%lld outside [1, %d]", (long long)K,
+               kCaMaxK);
+    if (B * T == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, final_ca_dispatch, q, k, v, K * D, allowed, K, nullptr, 0.0f, out, lse,
+                      B, T, K, D, scale, (hipStream_t)stream)
+}
+
+extern "C" int loom_final_ca_sparse_strided(int dtype, const void* q, const void* k, const void* v,
+                                            int64_t kv_stride_b, const uint8_t* allowed,
+                                            int64_t allowed_stride, const void* residual,
+                                            float gamma, void* out, float* lse, int64_t B,
+                                            int64_t T, int64_t K, int64_t D, float scale,
+                                            void* stream) {
+    clear_error();
+    LOOM_CHECK(q && k && v && allowed && out, "final_ca_sparse: null tensor argument");
+    LOOM_CHECK(K >= 1 && K <= kCaMaxK, "final_ca_sparse: K=%lld outside [1, %d]", (long long)K,
+               kCaMaxK);
+    LOOM_CHECK(kv_stride_b >= K * D && allowed_stride >= K, "final_ca_sparse: strides too small");
+    if (B * T == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, final_ca_dispatch, q, k, v, kv_stride_b, allowed, allowed_stride,
+                      residual, gamma, out, lse, B, T, K, D, scale, (hipStream_t)stream)
+}

@@ -1,0 +1,107 @@
+"""ctypes binding of libloom_hip.so (declared in include/loom_hip.h).
+
+The library is built in-tree by ``build_lib.py``; there is no fallback: if it
+is missing or fails to load, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from ctypes import c_float, c_int, c_int64, c_void_p
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libloom_hip.so")
+
+_P = c_void_p
+# name -> argument types (all return c_int status)
+SIGNATURES = {
+    "loom_paraplex_forward": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                              c_int64, c_int64, c_int64, c_float, _P],
+    "loom_phase_sin_forward": [c_int, _P, _P, c_int64, _P],
+    "loom_pvpowlu_forward": [c_int, _P, _P, _P, c_int64, c_float, _P],
+    "loom_beta_forward": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64,
+                          c_int64, c_int64, c_int64, c_int64, c_int, _P],
+    "loom_linear": [c_int, _P, c_int64, _P, c_int64, _P, _P, c_float, _P, _P, c_int64,
+                    c_int64, c_int64, c_int64, _P],
+    "loom_depth_attn_forward": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64,
+                                c_int64, c_int64, c_int64, _P],
+    "loom_tria_depth_forward": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64,
+                                c_int64, c_int64, c_float, c_int, _P],
+    "loom_gate_slot_mix_forward": [c_int, _P, _P, _P, c_int64, _P],
+    "loom_slot_attention_pool_forward": [c_int, _P, _P, _P, _P, c_int64, c_int64, _P],
+    "loom_temporal_carry_forward": [c_int, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P],
+    "loom_temporal_carry_endpoint_forward": [c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64,
+                                             c_int64, _P],
+    "loom_polarm_forward": [c_int, _P, _P, _P, c_int64, c_int64, c_float, c_float, _P],
+    "loom_final_ca_sparse_forward": [c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64,
+                                     c_int64, c_float, _P],
+    "loom_final_ca_sparse_strided": [c_int, _P, _P, _P, c_int64, _P, c_int64, _P, c_float, _P,
+                                     _P, c_int64, c_int64, c_int64, c_int64, c_float, _P],
+    "loom_rope_append": [c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64,
+                         c_int64, c_int64, c_int64, _P],
+    "loom_gqa_decode_attention": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64,
+                                  c_int64, c_int64, c_int64, c_int64, c_int64, _P],
+    "loom_add_layernorm": [c_int, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, _P],
+    "loom_tria_decode_temporal": [c_int, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_float,
+                                  _P],
+}
+# entry points that return a value instead of a status
+QUERIES = {"loom_gqa_workspace_bytes": ([c_int64] * 5, c_int64)}
+
+_lib = None
+_lock = threading.Lock()
+
+DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the library once and set every declared signature."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"libloom_hip.so not found at {path}; build it with "
+                "`python loomformer-paraplex_amd/build_lib.py` (or __graft_entry__.build())")
+        lib = ctypes.CDLL(path)
+        lib.loom_last_error.restype = ctypes.c_char_p
+        lib.loom_last_error.argtypes = []
+        lib.loom_abi_version.restype = c_int
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = c_int
+        for name, (argtypes, restype) in QUERIES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        _lib = lib
+        return lib
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point; raise RuntimeError(loom_last_error()) on failure."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.loom_last_error().decode("utf-8", "replace")
+        raise RuntimeError(msg or f"{name} failed with status {rc}")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise RuntimeError(f"unsupported dtype {t.dtype}; expected float32, bfloat16 or float16")
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return c_void_p(torch.cuda.current_stream(t.device).cuda_stream)

@@ -1,0 +1,318 @@
+"""Batched greedy decode of LoomFormer on the gfx950 kernels.
+
+``LoomDecoder.step`` is ``Model.step`` (loomformer.py:3951-4091) for a batch
+of sequences that share one position counter, and ``generate`` is ``infer``
+(loomformer.py:5290-5311): token-by-token prefill through ``step``, then
+greedy argmax.  Every matrix product, attention, LayerNorm, the fused Paraplex
+chain, depth attention and all Tria ops run in libloom_hip.so on persistent
+buffers; torch provides the device memory, the embedding row gather and the
+argmax.  Activations and weight matrices are in ``dtype`` (bf16 or fp32);
+biases, LayerNorm parameters and the rotary tables stay fp32.
+
+Layouts (all device-resident, allocated once):
+  k_cache/v_cache [L, B, max_len, KVH, HD]    KV cache (preallocated, no wrap)
+  hist            [B, 2L, 2N]                 depth history, row s = [k_s | v_s]
+  trace           [L, B, H]                   previous-token phase per layer
+  doc             [2, B, H, 3, 3]             temporal carry (ping-pong)
+  ca_k/ca_v       [B, max_keys, N], ca_valid [B, max_keys]   final-CA keys
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, Optional
+
+import torch
+
+from . import _lib
+from .config import ModelConfig
+from .weights import rope_tables
+
+_P = _lib.ptr
+
+
+class LoomDecoder:
+    def __init__(self, cfg: ModelConfig, state: Dict[str, torch.Tensor], batch: int,
+                 dtype: torch.dtype = torch.bfloat16, device="cuda", max_len: Optional[int] = None,
+                 carry_token_id: Optional[int] = None):
+        if dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError(f"dtype must be float32 or bfloat16, got {dtype}")
+        self.cfg = cfg
+        self.B = int(batch)
+        self.dtype = dtype
+        self.dev = torch.device(device)
+        self.code = _lib.DTYPE_CODE[dtype]
+        self.max_len = int(max_len or cfg.seq_len)
+        if self.max_len > cfg.seq_len:
+            raise ValueError(f"max_len {self.max_len} exceeds seq_len {cfg.seq_len}")
+        self.carry_token_id = carry_token_id
+        self.lib = _lib.load()
+        c = cfg
+        dev, dt = self.dev, dtype
+
+        def mat(k):
+            return state[k].detach().to(dev, dt).contiguous()
+
+        def f32(k):
+            return state[k].detach().to(dev, torch.float32).contiguous()
+
+        self.emb = mat("emb.weight")
+        self.head = mat("head.weight")
+        self.blocks = []
+        for bi in range(c.L):
+            p = f"blocks.{bi}."
+            raw_alpha = float(state[p + "ffn.identity_gate.raw_alpha"])
+            logits = state[p + "ffn.gate_selector.logits"].detach().float()
+            self.blocks.append(dict(
+                ln1_w=f32(p + "ln_attn.weight"), ln1_b=f32(p + "ln_attn.bias"),
+                qkv=mat(p + "attn.qkv_weight"), o=mat(p + "attn.o.weight"),
+                ln2_w=f32(p + "ln_ffn.weight"), ln2_b=f32(p + "ln_ffn.bias"),
+                w1r=mat(p + "ffn.w1_real.weight"), b1r=f32(p + "ffn.w1_real.bias"),
+                w1i=mat(p + "ffn.w1_imag"), ib=f32(p + "ffn.w1_imag_bias"),
+                tw=f32(p + "ffn.w1_imag_trace"),
+                w2=mat(p + "ffn.w2.weight"), b2=f32(p + "ffn.w2.bias"),
+                gate_w=torch.softmax(logits, 0).to(dev, dt),           # GateSelector weights
+                alpha=0.25 * math.tanh(raw_alpha),                      # IdentityAnchoredGate
+                anchor=torch.ones((), device=dev),
+            ))
+        self.kvw = mat("depth_attn.kv_weight")
+        self.wo = mat("depth_attn.w_o.weight")
+        self.qp = mat("depth_attn.q_params")
+        key_w = state["tria_agg.reader.key_proj.weight"].detach().float()
+        query = state["tria_agg.pool.query"].detach().float()
+        lsr = state["tria_agg.pool.logit_scale_raw"].detach().float()
+        raw = torch.mv(key_w.t(), query)                                 # tria.py:1346-1349
+        score_w = torch.nn.functional.normalize(raw, dim=0, eps=1e-6) * torch.nn.functional.softplus(lsr)
+        self.score_w = score_w.to(dev, dt)
+        self.proj_w, self.proj_b = mat("tria_agg.reader.proj.weight"), f32("tria_agg.reader.proj.bias")
+        self.up_w, self.up_b = mat("tria_agg.up.weight"), f32("tria_agg.up.bias")
+        self.wqk, self.wv = mat("tria_final_ca.w_qk.weight"), mat("tria_final_ca.w_v.weight")
+        self.gamma = c.gamma_max * math.tanh(float(state["tria_final_ca.raw_gamma"]))
+        cos, sin = rope_tables(c, self.max_len)
+        self.cos, self.sin = cos.to(dev), sin.to(dev)
+
+        B, N, H, L = self.B, c.N, c.H, c.L
+        z = lambda *s, dtype=dt: torch.zeros(*s, dtype=dtype, device=dev)
+        self.k_cache = z(L, B, self.max_len, c.KVH, c.HD)
+        self.v_cache = z(L, B, self.max_len, c.KVH, c.HD)
+        self.hist = z(B, 2 * L, 2 * N)
+        self.trace = z(L, B, H)
+        self.doc = z(2, B, H, 3, 3)
+        self.max_keys = max(1, self.max_len // max(1, c.window) + 1)
+        self.ca_k = z(B, self.max_keys, N)
+        self.ca_v = z(B, self.max_keys, N)
+        self.ca_valid = z(B, self.max_keys, dtype=torch.uint8)
+        self.pending = z(B, dtype=torch.uint8)
+        self.reset_now = z(B, dtype=torch.uint8)
+        self.fire = z(B, dtype=torch.uint8)
+        ws = self.lib.loom_gqa_workspace_bytes(B, self.max_len, c.QH, c.KVH, c.HD)
+        self.ws = torch.empty((ws + 3) // 4, dtype=torch.float32, device=dev)
+        self.ws_bytes = ws
+        # activations
+        self.h = z(B, N)
+        self.h2 = z(B, N)
+        self.qkv = z(B, N + 2 * c.KV)
+        self.q = z(B, c.QH, c.HD)
+        self.c = z(B, c.QH, c.HD)
+        self.kctx = z(B, c.QH, c.HD)
+        self.d = z(B, c.QH, c.HD)
+        self.dh = z(B, c.QH, c.HD)
+        self.attn_out = z(B, N)
+        self.skip = z(B, N)
+        self.R = z(B, H)
+        self.beta = z(B, H)
+        self.act = z(B, H)
+        self.s = z(B, H)
+        self.ffn_out = z(B, N)
+        self.carry = z(2, B, H, 3, 3)
+        self.p = z(2, B, H)
+        self.pooled = z(B, 9)
+        self.z32 = z(B, 32)
+        self.a_t = z(B, N)
+        self.q_ca = z(B, N)
+        self.logits = z(B, c.V)
+        self.snap = torch.empty((), dtype=torch.float32, device=dev)
+        self.pos = 0
+        self.has_doc = False
+        self.doc_cur = 0
+        self.ca_len = 0
+
+    # ------------------------------------------------------------------ helpers
+
+    def _call(self, name, *args):
+        rc = getattr(self.lib, name)(*args)
+        if rc != 0:
+            raise RuntimeError(self.lib.loom_last_error().decode())
+
+    def _stream(self):
+        return _lib.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+
+    def _linear(self, x, w, out, M, Nout, K, bias=None, ldx=None, ldc=None, gate_p=None,
+                gate_alpha=0.0, residual=None):
+        self._call("loom_linear", self.code, _P(x), ldx or K, _P(w), K, _P(bias), _P(gate_p),
+                   float(gate_alpha), _P(residual), _P(out), ldc or Nout, M, Nout, K, self._stream())
+
+    def reset(self) -> None:
+        self.pos = 0
+        self.has_doc = False
+        self.ca_len = 0
+        self.trace.zero_()
+        self.pending.zero_()
+        self.ca_valid.zero_()
+
+    # ------------------------------------------------------------------ step
+
+    @torch.no_grad()
+    def step(self, ids: torch.Tensor, pos: int) -> torch.Tensor:
+        """Advance every sequence by one token at position ``pos``; returns logits [B, V]."""
+        c, B, N, H, L = self.cfg, self.B, self.cfg.N, self.cfg.H, self.cfg.L
+        st = self._stream()
+        if pos == 0:
+            self.reset()
+        if pos != self.pos:
+            raise ValueError(f"step expects position {self.pos}, got {pos}")
+        if pos >= self.max_len:
+            raise ValueError(f"generation exceeded seq_len={self.max_len}; no wraparound support")
+        torch.index_select(self.emb, 0, ids.to(self.dev).view(-1), out=self.h)
+        S2 = 2 * L
+        hist_ld = S2 * 2 * N
+        # depth history slot 0: DepthAttn.project(h) (loomformer.py:3973)
+        self._linear(self.h, self.kvw, self.hist[:, 0], B, 2 * N, N, ldc=hist_ld)
+        sub = 0
+        cache_sb = self.max_len * c.KVH * c.HD
+        cache_st = c.KVH * c.HD
+        carry_i = None          # index of the current depth carry in self.carry
+        p_i = None              # index of the gate output p feeding the next block
+        seed = self.has_doc
+        for bi, blk in enumerate(self.blocks):
+            last = bi == L - 1
+            kc, vc = self.k_cache[bi], self.v_cache[bi]
+            # ---- attention step (loomformer.py:3300-3332)
+            self._linear(self.h, blk["qkv"], self.qkv, B, N + 2 * c.KV, N)
+            self._call("loom_rope_append", self.code, _P(self.qkv), _P(self.q), _P(kc), _P(vc),
+                       _P(self.cos), _P(self.sin), B, pos, c.QH, c.KVH, c.HD, cache_sb, cache_st, st)
+            self._call("loom_gqa_decode_attention", self.code, _P(self.q), _P(kc), _P(vc), cache_sb,
+                       cache_st, _P(self.c), _P(self.kctx), _P(self.ws), self.ws_bytes, B, pos + 1,
+                       c.QH, c.KVH, c.HD, st)
+            self._linear(self.c, blk["o"], self.attn_out, B, N, N)
+            # ---- depth read 2*bi, LayerNorm, history slot (loomformer.py:3999-4004)
+            self._depth(sub, self.d)
+            self._linear(self.d, self.wo, self.skip, B, N, N)
+            self._call("loom_add_layernorm", self.code, _P(self.skip), _P(self.attn_out),
+                       _P(blk["ln1_w"]), _P(blk["ln1_b"]), _P(self.h), B, N, 1e-5, st)
+            sub += 1
+            self._linear(self.h, self.kvw, self.hist[:, sub], B, 2 * N, N, ldc=hist_ld)
+            self._depth(sub, self.dh)
+            self._linear(self.dh, self.wo, self.skip, B, N, N)
+            # ---- Paraplex FFN (loomformer.py:2818-2893, fused path :2533-2560)
+            if p_i is None:
+                self._linear(self.h, blk["w1r"], self.R, B, H, N, bias=blk["b1r"])
+            else:
+                self._linear(self.h, blk["w1r"], self.R, B, H, N, bias=blk["b1r"],
+                             gate_p=self.p[p_i], gate_alpha=blk["alpha"])
+            self._call("loom_beta_forward", self.code, _P(self.h), _P(self.q), _P(self.kctx),
+                       _P(self.c), _P(self.dh), _P(blk["w1i"]), _P(self.beta), None, B, N, H,
+                       c.imag_in, c.Hq, c.HD, c.QH, 1 if c.sectors == "open" else 0, st)
+            tr = self.trace[bi]
+            self._call("loom_paraplex_forward", self.code, _P(self.R), _P(self.R), _P(self.beta),
+                       _P(blk["ib"]), _P(tr), _P(blk["tw"]), None, _P(blk["anchor"]), _P(self.act),
+                       _P(self.s), _P(tr), _P(self.snap), B, 1, H, float(c.powlu_m), st)
+            self._linear(self.act, blk["w2"], self.ffn_out, B, N, H, bias=blk["b2"])
+            # ---- Tria depth op (loomformer.py:4012-4040); axis = bi % 3
+            out_i = 0 if carry_i != 0 else 1
+            gate = not last
+            new_p = (0 if p_i != 0 else 1) if gate else None
+            prev = None if carry_i is None else self.carry[carry_i]
+            use_seed = bi == 0 and seed
+            self._call("loom_tria_depth_forward", self.code, _P(self.R), _P(self.s), _P(self.act),
+                       _P(prev) if not use_seed else None,
+                       _P(self.doc[self.doc_cur]) if use_seed else None,
+                       _P(self.pending) if use_seed else None,
+                       _P(blk["gate_w"]) if gate else None, _P(self.carry[out_i]),
+                       _P(self.p[new_p]) if gate else None, None, B, 1, H, float(c.tria_alpha),
+                       bi % 3, st)
+            carry_i, p_i = out_i, new_p
+            # ---- LayerNorm and next history slot (loomformer.py:4045-4050)
+            self._call("loom_add_layernorm", self.code, _P(self.skip), _P(self.ffn_out),
+                       _P(blk["ln2_w"]), _P(blk["ln2_b"]), _P(self.h), B, N, 1e-5, st)
+            if not last:
+                sub += 1
+                self._linear(self.h, self.kvw, self.hist[:, sub], B, 2 * N, N, ldc=hist_ld)
+        # ---- temporal carry, fire, PolARM (loomformer.py:4053-4085)
+        hard_fire = (pos + 1 < c.seq_len) and ((pos + 1) % c.window == 0)
+        if self.carry_token_id is not None:
+            explicit = ids.to(self.dev).view(-1).eq(int(self.carry_token_id))
+            fire_t = explicit | hard_fire
+            any_fire = bool(fire_t.any())          # host sync, as tria.py:1576
+            self.fire.copy_(fire_t)
+        else:
+            any_fire = hard_fire
+            self.fire.fill_(1 if hard_fire else 0)
+        if pos == 0:
+            self.reset_now.fill_(1)
+        else:
+            self.reset_now.copy_(self.pending)
+        nxt = 1 - self.doc_cur
+        self._call("loom_tria_decode_temporal", self.code, _P(self.carry[carry_i]),
+                   _P(self.doc[self.doc_cur]) if self.has_doc else None,
+                   _P(self.reset_now) if self.has_doc else None,
+                   _P(self.fire) if any_fire else None, _P(self.doc[nxt]), B, H,
+                   float(c.polarm_beta), 1e-6, st)
+        self.doc_cur = nxt
+        self.has_doc = True
+        # ---- readout TriaAggregator (tria.py:1436-1441)
+        self._call("loom_slot_attention_pool_forward", self.code, _P(self.doc[nxt]), _P(self.score_w),
+                   _P(self.pooled), None, B, H, st)
+        self._linear(self.pooled, self.proj_w, self.z32, B, 32, 9, bias=self.proj_b)
+        self._linear(self.z32, self.up_w, self.a_t, B, N, 32, bias=self.up_b)
+        # ---- final cross-attention step (tria.py:1560-1595)
+        if any_fire:
+            if self.ca_len >= self.max_keys:
+                raise ValueError("final-CA key cache is full")
+            self._linear(self.a_t, self.wqk, self.ca_k[:, self.ca_len], B, N, N, ldc=self.max_keys * N)
+            self._linear(self.a_t, self.wv, self.ca_v[:, self.ca_len], B, N, N, ldc=self.max_keys * N)
+            self.ca_valid[:, self.ca_len].copy_(self.fire)
+            self.ca_len += 1
+        h_out = self.h
+        if self.ca_len > 0:
+            self._linear(self.h, self.wqk, self.q_ca, B, N, N)
+            self._call("loom_final_ca_sparse_strided", self.code, _P(self.q_ca), _P(self.ca_k),
+                       _P(self.ca_v), self.max_keys * N, _P(self.ca_valid), self.max_keys,
+                       _P(self.h), float(self.gamma), _P(self.h2), None, B, 1, self.ca_len, N,
+                       float(N ** -0.5), st)
+            h_out = self.h2
+        self._linear(h_out, self.head, self.logits, B, c.V, N)
+        self.pending.copy_(self.fire)
+        self.pos = pos + 1
+        return self.logits
+
+    def _depth(self, sub: int, out: torch.Tensor) -> None:
+        """DepthAttn read over history slots [0, sub] (loomformer.py:3404-3429, tensor branch)."""
+        c, N, L = self.cfg, self.cfg.N, self.cfg.L
+        hist_bt = 2 * L * 2 * N
+        self._call("loom_depth_attn_forward", self.code, _P(self.qp[sub]), _P(self.hist),
+                   _P(self.hist[:, :, N:]), hist_bt, 2 * N, _P(out), None, None, self.B, sub + 1,
+                   c.QH, c.HD, self._stream())
+
+    @torch.no_grad()
+    def generate(self, prompt: torch.Tensor, n_new: int, return_logits: bool = False):
+        """Token-by-token prefill of ``prompt`` [B, P] then ``n_new`` greedy tokens."""
+        B, P = prompt.shape
+        if B != self.B:
+            raise ValueError(f"prompt batch {B} != engine batch {self.B}")
+        prompt = prompt.to(self.dev)
+        logits_all = [] if return_logits else None
+        logits = None
+        for pos in range(P):
+            logits = self.step(prompt[:, pos], pos)
+            if return_logits:
+                logits_all.append(logits.float().clone())
+        out = torch.empty(B, n_new, dtype=torch.long, device=self.dev)
+        for i in range(n_new):
+            nxt = torch.argmax(logits, dim=-1)
+            out[:, i] = nxt
+            logits = self.step(nxt, P + i)
+            if return_logits:
+                logits_all.append(logits.float().clone())
+        if return_logits:
+            return out, torch.stack(logits_all, 1)
+        return out

@@ -1,0 +1,67 @@
+"""CPU checks of the C-ABI boundary: the library loads, exports every symbol the
+header declares, and the Python mirror/drop-in reject bad input like the
+reference does (no GPU compute here)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "loom_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(loom_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from loom_amd import _lib
+    lib = _lib.load()
+    syms = declared_symbols()
+    assert "loom_paraplex_forward" in syms and len(syms) >= 15
+    missing = [s for s in syms if not hasattr(lib, s)]
+    assert not missing, missing
+    assert lib.loom_abi_version() == 1
+    # every declared compute entry point has a ctypes signature
+    compute = [s for s in syms if s not in ("loom_last_error", "loom_abi_version")]
+    bound = set(_lib.SIGNATURES) | set(_lib.QUERIES)
+    assert set(compute) == bound, set(compute) ^ bound
+    assert lib.loom_gqa_workspace_bytes(2, 300, 8, 2, 96) == 2 * 2 * 2 * (8 + 2 * 4 * 96) * 4
+
+
+def test_error_channel_reports_argument_errors():
+    from loom_amd import _lib
+    with pytest.raises(RuntimeError, match="axis must be 0"):
+        # argument validation happens before any device work
+        _lib.call("loom_tria_depth_forward", 0, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                  ctypes.c_void_p(16), None, None, None, None, None, None, None, 1, 1, 1,
+                  0.05, 7, None)
+    with pytest.raises(RuntimeError, match="K=0"):
+        _lib.call("loom_final_ca_sparse_forward", 0, *([ctypes.c_void_p(16)] * 5), None,
+                  1, 1, 0, 8, 1.0, None)
+
+
+def test_drop_in_modules_expose_reference_names():
+    from kernels.build import EXPORTS, build_or_load
+    for ext, names in EXPORTS.items():
+        mod = build_or_load(ext, ["ignored.cu"], ptx_kernels={"x": "y"})
+        for n in names:
+            assert callable(getattr(mod, n)), (ext, n)
+    with pytest.raises(RuntimeError, match="unknown extension"):
+        build_or_load("loomformer_chunk_attn", [])
+
+
+def test_mirror_rejects_cpu_tensors_like_the_reference():
+    from loom_amd import ops
+    x = torch.zeros(2, 3, 8)
+    with pytest.raises(RuntimeError, match="CUDA tensors required"):
+        ops.paraplex_forward(x, x, x, torch.zeros(8), torch.zeros(2, 8), torch.zeros(8),
+                             torch.empty(0, dtype=torch.bool), torch.ones(()), 0, False, 0.99, 3.0)
+    with pytest.raises(RuntimeError, match="must be CUDA"):
+        ops.tria_step_forward(x, x, x, torch.zeros(2, 3, 8, 3, 3), 0.05, 0)
+    with pytest.raises(RuntimeError, match="training-only"):
+        ops.paraplex_backward()

@@ -1,0 +1,368 @@
+"""GPU parity of every gfx950 op against the CPU oracle (and, where the
+fixtures hold them, against the reference's own output vectors).
+
+Tolerances (stated by the north star): fp32 rtol 1e-3, bf16 rtol 2e-2.  The
+oracle always runs in fp32 on the CPU, on exactly the inputs the GPU saw
+(bf16 inputs are rounded first and upcast), so the bf16 error is the kernel's
+output rounding plus fp32-vs-fp32 ordering differences.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops as ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.bfloat16: dict(rtol=2e-2, atol=1e-2)}
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    from loom_amd import _lib
+    _lib.load()
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rnd(g, *shape, scale=1.0):
+    return torch.randn(*shape, generator=g) * scale
+
+
+def dev(t, dtype):
+    return t.to(DEV, dtype)
+
+
+def host(t):
+    return t.detach().float().cpu()
+
+
+def check(got, want, dtype, rtol=None, atol=None):
+    tol = dict(TOL[dtype])
+    if rtol is not None:
+        tol["rtol"] = rtol
+    if atol is not None:
+        tol["atol"] = atol
+    torch.testing.assert_close(host(got), want.float(), **tol)
+
+
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+# ----------------------------------------------------------------- paraplex
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,T,H,same_gate,with_reset", [
+    (2, 5, 24, True, False), (2, 7, 20, False, True), (3, 37, 3072, True, True),
+    (1, 1, 3072, True, False), (32, 1, 3072, True, False), (2, 300, 256, False, False),
+])
+def test_paraplex_forward(dtype, B, T, H, same_gate, with_reset):
+    from loom_amd import ops
+    g = gen(B * 1000 + T * 10 + H)
+    r = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    gs = r if same_gate else dev(rnd(g, B, T, H, scale=3.0), dtype)
+    beta = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    bias = dev(rnd(g, H, scale=0.5), torch.float32)
+    trace = dev(rnd(g, B, H, scale=0.5), dtype)
+    tw = dev(torch.rand(H, generator=g) - 0.5, torch.float32)
+    reset = torch.zeros(B, T, dtype=torch.bool)
+    if with_reset:
+        reset[0, min(2, T - 1)] = True
+        reset[-1, 0] = True
+    anchor = torch.ones((), device=DEV)
+    act, s, nt, snap = ops.paraplex_forward(r, gs, beta, bias, trace, tw,
+                                            dev(reset, torch.bool) if with_reset else torch.empty(0, dtype=torch.bool, device=DEV),
+                                            anchor, 1, False, 0.99, 3.0)
+    w_act, w_s, w_nt = ref.paraplex_pointwise(host(r), host(gs), host(beta), host(bias), host(trace),
+                                              host(tw), reset if with_reset else None, 3.0)
+    check(s, w_s, dtype)
+    check(act, w_act, dtype)
+    check(nt, w_nt, dtype)
+    assert float(snap) == 1.0
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_phase_sin_and_pvpowlu(dtype):
+    from loom_amd import ops
+    g = gen(5)
+    beta = torch.cat([rnd(g, 1000, scale=3.0), torch.tensor([0.0, 1e-4, -1e-4, 80.0, -80.0, 3e4, -3e4, 7.0])])
+    b = dev(beta, dtype)
+    check(ops.phase_sin_forward_cuda(b), ref.phase_sin(host(b)), dtype)
+    x1 = dev(rnd(g, 1003), dtype)
+    x2 = dev(torch.nn.functional.softplus(rnd(g, 1003, scale=4.0)), dtype)
+    check(ops.pvpowlu_forward_cuda(x1, x2, 3.0), ref.pvpowlu(host(x1), host(x2), 3.0), dtype)
+    check(ops.pvpowlu_forward_cuda(x1, x2, 0.0), host(x1) * torch.sigmoid(host(x2)), dtype)
+
+
+def test_golden_phase_and_pvpowlu_vs_reference():
+    from loom_amd import ops
+    z = np.load(os.path.join(GOLD, "ops.npz"))
+    b = torch.from_numpy(z["phase.beta"]).to(DEV)
+    check(ops.phase_sin_forward_cuda(b), torch.from_numpy(z["phase.out"]), torch.float32)
+    x1, x2 = torch.from_numpy(z["pvpowlu.x1"]).to(DEV), torch.from_numpy(z["pvpowlu.x2"]).to(DEV)
+    check(ops.pvpowlu_forward_cuda(x1, x2, 3.0), torch.from_numpy(z["pvpowlu.out"]), torch.float32)
+
+
+# ----------------------------------------------------------------- projections
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("M,N,K", [(1, 16, 8), (37, 100, 72), (32, 3072, 768), (130, 768, 3072),
+                                   (256, 256, 1152), (5, 4096, 768)])
+def test_linear(dtype, M, N, K):
+    from loom_amd import ops
+    g = gen(M * 7 + N + K)
+    x = dev(rnd(g, M, K), dtype)
+    w = dev(rnd(g, N, K, scale=K ** -0.5), dtype)
+    bias = dev(rnd(g, N), torch.float32)
+    want = host(x) @ host(w).t()
+    check(ops.linear(x, w), want, dtype)
+    check(ops.linear(x, w, bias), want + host(bias), dtype)
+    p = dev(rnd(g, M, N), dtype)
+    res = dev(rnd(g, M, N), dtype)
+    check(ops.linear(x, w, bias, gate_p=p, gate_alpha=0.2, residual=res),
+          want * (1.0 + 0.2 * host(p)) + host(bias) + host(res), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("QH,HD,Hq,M,sectors", [(4, 8, 32, 10, "head"), (8, 96, 384, 40, "head"),
+                                                 (8, 96, 384, 300, "head"), (4, 8, 32, 6, "open"),
+                                                 (8, 96, 384, 20, "open")])
+def test_beta_forward(dtype, QH, HD, Hq, M, sectors):
+    from loom_amd import ops
+    N, H = QH * HD, QH * Hq
+    K = ref.imag_in(N, HD, sectors)
+    g = gen(QH + HD + M)
+    B, T = 1, M
+    u = dev(rnd(g, B, T, N), dtype)
+    q, kc, c, d = (dev(rnd(g, B, T, QH, HD), dtype) for _ in range(4))
+    w = dev(rnd(g, H, K, scale=K ** -0.5), dtype)
+    out, pack, wc = ops.beta_forward_cuda(u, q, kc, c, d, w, Hq, HD, QH, sectors == "open")
+    want = ref.beta_space_dense(host(u), host(q), host(kc), host(c), host(d), host(w), QH, HD, sectors)
+    check(out, want, dtype)
+    assert pack.numel() == 0 and wc.shape == w.shape
+
+
+# ----------------------------------------------------------------- depth attention
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("HD", [96, 8, 64])
+def test_depth_attn_decode_strided_view(dtype, HD):
+    from loom_amd import ops
+    g = gen(HD)
+    B, S_max, QH = 3, 20, 8
+    hk = dev(rnd(g, B, 1, S_max, QH, HD), dtype)
+    hv = dev(rnd(g, B, 1, S_max, QH, HD), dtype)
+    q = dev(rnd(g, QH, HD, scale=HD ** -0.25), dtype)
+    for s in (1, 2, 9, 20):
+        d, w = ops.depth_attn_forward(q, hk[:, :, :s], hv[:, :, :s])
+        want_d, want_w, _ = ref.depth_attn_softmax(host(q), host(hk)[:, :, :s], host(hv)[:, :, :s])
+        check(d, want_d, dtype)
+        check(w, want_w, dtype)
+    # S=1 returns v_0 exactly (up to the output rounding)
+    d, _ = ops.depth_attn_forward(q, hk[:, :, :1], hv[:, :, :1])
+    check(d, host(hv)[:, :, 0], dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("BT,S", [(50, 24), (7, 33), (1, 1), (4096, 24)])
+def test_depth_attn_stacked(dtype, BT, S):
+    from loom_amd import ops
+    g = gen(BT + S)
+    QH, HD = 8, 96
+    hk = dev(rnd(g, 1, BT, S, QH, HD), dtype)
+    hv = dev(rnd(g, 1, BT, S, QH, HD), dtype)
+    q = dev(rnd(g, QH, HD, scale=0.02), dtype)
+    d, lse = ops.depth_attn_stacked_forward(q, hk, hv)
+    want_d, _, want_lse = ref.depth_attn_softmax(host(q), host(hk), host(hv))
+    check(d, want_d, dtype)
+    check(lse, want_lse, torch.float32, rtol=1e-4, atol=1e-4)
+    # equal keys -> mean of V
+    hk_eq = hk[:, :, :1].expand(-1, -1, S, -1, -1).contiguous()
+    d, _ = ops.depth_attn_stacked_forward(q, hk_eq, hv)
+    check(d, host(hv).mean(2), dtype)
+
+
+def test_golden_depth_attn_vs_reference():
+    from loom_amd import ops
+    z = np.load(os.path.join(GOLD, "ops.npz"))
+    hk, hv = torch.from_numpy(z["da.hist_k"]).to(DEV), torch.from_numpy(z["da.hist_v"]).to(DEV)
+    q = torch.from_numpy(z["da.w::q_params"]).to(DEV)
+    d, _ = ops.depth_attn_forward(q[3], hk, hv)
+    check(d, torch.from_numpy(z["da.d_tensor"]), torch.float32)
+    S = hk.shape[2]
+    d, _ = ops.depth_attn_list_forward(q[4], [hk[:, :, j] for j in range(S)], [hv[:, :, j] for j in range(S)])
+    check(d, torch.from_numpy(z["da.d_list"]), torch.float32)
+
+
+# ----------------------------------------------------------------- tria
+
+def _tria_inputs(g, B, T, H, dtype):
+    r = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    i = dev(rnd(g, B, T, H), dtype)
+    o = dev(rnd(g, B, T, H, scale=0.5), dtype)
+    prev = dev(ref.local_normalize(rnd(g, B, T, H, 3, 3)), dtype)
+    seed = dev(ref.local_normalize(rnd(g, B, H, 3, 3)), dtype)
+    valid = torch.rand(B, generator=g) > 0.4
+    valid[0] = True
+    w = dev(torch.softmax(rnd(g, 9), 0), dtype)
+    return r, i, o, prev, seed, dev(valid, torch.bool), w
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("axis", [0, 1, 2])
+@pytest.mark.parametrize("B,T,H", [(3, 4, 6), (2, 3, 1000), (8, 1, 3072)])
+def test_tria_depth_family(dtype, axis, B, T, H):
+    from loom_amd import ops
+    g = gen(B + T + H + axis)
+    r, i, o, prev, seed, valid, w = _tria_inputs(g, B, T, H, dtype)
+    a = 0.0375
+    R, I, O, P, SD, W = host(r), host(i), host(o), host(prev), host(seed), host(w)
+    c, s = ops.tria_init_forward(r, i, o, a, axis)
+    check(c, ref.tria_init(R, I, O, a, axis), dtype)
+    want_scale = ref.build_tria(R, I, O, a, axis).square().mean(dim=(-1, -2)).add(1e-6).sqrt()
+    check(s, want_scale.reshape(-1), torch.float32, rtol=1e-4)
+    c, p, _ = ops.tria_init_gate_forward(r, i, o, w, a, axis)
+    wc, wp = ref.tria_init_and_gate(R, I, O, W, a, axis)
+    check(c, wc, dtype)
+    check(p, wp, dtype)
+    c, _ = ops.tria_step_forward(r, i, o, prev, a, axis)
+    check(c, ref.tria_step(R, I, O, P, a, axis), dtype)
+    c, p, _ = ops.tria_step_gate_forward(r, i, o, prev, w, a, axis)
+    wc, wp = ref.tria_step_and_gate(R, I, O, P, W, a, axis)
+    check(c, wc, dtype)
+    check(p, wp, dtype)
+    c, _ = ops.tria_init_seed_forward(r, i, o, seed, valid, a, axis)
+    check(c, ref.tria_init_seed(R, I, O, SD, valid.cpu(), a, axis), dtype)
+    c, p = ops.tria_init_seed_gate_forward(r, i, o, seed, valid, w, a, axis)
+    wc, wp = ref.tria_init_seed_and_gate(R, I, O, SD, valid.cpu(), W, a, axis)
+    check(c, wc, dtype)
+    check(p, wp, dtype)
+    # invariant: every carrier has RMS 1 (to eps)
+    rms = host(c).square().mean(dim=(-1, -2)).sqrt()
+    torch.testing.assert_close(rms, torch.ones_like(rms), rtol=2e-2 if dtype == torch.bfloat16 else 1e-5, atol=0)
+
+
+def test_golden_tria_vs_reference():
+    from loom_amd import ops
+    z = np.load(os.path.join(GOLD, "ops.npz"))
+    t = {k: torch.from_numpy(z[f"tria.{k}"]).to(DEV) for k in ("r", "i", "o", "prev", "seed", "valid", "w")}
+    a = 0.0375
+    f32 = torch.float32
+    for axis in range(3):
+        G = lambda nm: torch.from_numpy(z[f"tria.{nm}"])
+        check(ops.tria_init_forward(t["r"], t["i"], t["o"], a, axis)[0], G(f"init_{axis}"), f32)
+        check(ops.tria_step_forward(t["r"], t["i"], t["o"], t["prev"], a, axis)[0], G(f"step_{axis}"), f32)
+        check(ops.tria_init_seed_forward(t["r"], t["i"], t["o"], t["seed"], t["valid"], a, axis)[0],
+              G(f"seed_{axis}"), f32)
+        c, p, _ = ops.tria_step_gate_forward(t["r"], t["i"], t["o"], t["prev"], t["w"], a, axis)
+        check(c, G(f"step_gate_{axis}.carry"), f32)
+        check(p, G(f"step_gate_{axis}.p"), f32)
+        c, p = ops.tria_init_seed_gate_forward(t["r"], t["i"], t["o"], t["seed"], t["valid"], t["w"], a, axis)
+        check(c, G(f"seed_gate_{axis}.carry"), f32)
+        check(p, G(f"seed_gate_{axis}.p"), f32)
+    depth, rs, ini = (torch.from_numpy(z[k]).to(DEV) for k in ("tc.depth", "tc.reset", "tc.init"))
+    doc, _ = ops.temporal_carry_forward(depth, rs)
+    check(doc, torch.from_numpy(z["tc.full_ref"]), f32)
+    e, e32 = ops.temporal_carry_endpoint_forward(depth, rs, torch.empty(0, device=DEV),
+                                                 torch.empty(0, dtype=torch.bool, device=DEV))
+    check(e, torch.from_numpy(z["tc.end_noinit"]), f32)
+    e, _ = ops.temporal_carry_endpoint_forward(depth, rs, ini, t["valid"])
+    check(e, torch.from_numpy(z["tc.end_init_valid"]), f32)
+    e, _ = ops.temporal_carry_endpoint_forward(depth, rs, ini, torch.ones(3, dtype=torch.bool, device=DEV))
+    check(e, torch.from_numpy(z["tc.end_init"]), f32)
+    check(ops.polarm(torch.from_numpy(z["polarm.in"]).to(DEV), 0.1), torch.from_numpy(z["polarm.out"]), f32)
+    q, k, v, al = (torch.from_numpy(z[f"fca.{n}"]).to(DEV) for n in ("q", "k", "v", "allowed"))
+    out, _ = ops.final_ca_sparse_forward(q, k, v, al, q.shape[-1] ** -0.5)
+    check(out, torch.from_numpy(z["fca.out"]), f32)
+    sw = torch.from_numpy(z["agg.score_w"]).to(DEV)
+    carry = torch.from_numpy(z["agg.carry"]).to(DEV)
+    pooled, lse = ops.slot_attention_pool_forward(carry, sw)
+    want, want_lse = ref.slot_attention_pool(carry.cpu(), sw.cpu())
+    check(pooled, want, f32)
+    check(lse, want_lse, f32)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_gate_mix_and_slot_pool(dtype):
+    from loom_amd import ops
+    g = gen(9)
+    carry = dev(ref.local_normalize(rnd(g, 2, 3, 3072, 3, 3)), dtype)
+    w = dev(torch.softmax(rnd(g, 9), 0), dtype)
+    check(ops.gate_slot_mix_forward(carry, w), ref.gate_slot_mix(host(carry), host(w)), dtype)
+    sw = dev(rnd(g, 9, scale=3.0), dtype)
+    pooled, lse = ops.slot_attention_pool_forward(carry, sw)
+    wp, wl = ref.slot_attention_pool(host(carry), host(sw))
+    check(pooled, wp, dtype)
+    check(lse, wl, dtype)
+    # H = 1 -> pooled is the single carrier
+    pooled, _ = ops.slot_attention_pool_forward(carry[:, :, :1].contiguous(), sw)
+    check(pooled, host(carry)[:, :, 0].reshape(2, 3, 9), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,T,H", [(3, 9, 6), (2, 64, 1000), (1, 1, 5)])
+def test_temporal_carry(dtype, B, T, H):
+    from loom_amd import ops
+    g = gen(B * T + H)
+    depth = dev(ref.local_normalize(rnd(g, B, T, H, 3, 3)), dtype)
+    reset = torch.rand(B, T, generator=g) > 0.85
+    rs = dev(reset, torch.bool)
+    ini = dev(ref.local_normalize(rnd(g, B, H, 3, 3)), dtype)
+    valid = torch.rand(B, generator=g) > 0.5
+    D = host(depth)
+    doc, scale = ops.temporal_carry_forward(depth, rs)
+    full = ref.temporal_carry(D, reset)
+    check(doc, full, torch.float32 if dtype == torch.float32 else dtype)
+    e, e32 = ops.temporal_carry_endpoint_forward(depth, rs, torch.empty(0, device=DEV, dtype=dtype),
+                                                 torch.empty(0, dtype=torch.bool, device=DEV))
+    check(e32, full[:, -1], dtype)           # endpoint == last row of the full recurrence
+    e, e32 = ops.temporal_carry_endpoint_forward(depth, rs, ini, dev(valid, torch.bool))
+    check(e32, ref.temporal_carry_endpoint(D, reset, host(ini), valid), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_polarm_and_final_ca(dtype):
+    from loom_amd import ops
+    g = gen(77)
+    M = dev(rnd(g, 4, 50, 3, 3), dtype)
+    mask = torch.tensor([True, False, True, False])
+    got = ops.polarm(M, 0.1, mask=dev(mask, torch.bool))
+    want = torch.where(mask[:, None, None, None], ref.polarm(host(M), 0.1), host(M))
+    check(got, want, dtype)
+    # fixed point: an orthogonal matrix is unchanged
+    Q, _ = torch.linalg.qr(rnd(g, 6, 3, 3))
+    check(ops.polarm(dev(Q, torch.float32), 0.3), Q, torch.float32, atol=1e-5)
+    B, T, K, D = 3, 5, 40, 768
+    q, k, v = dev(rnd(g, B, T, D), dtype), dev(rnd(g, B, K, D), dtype), dev(rnd(g, B, K, D), dtype)
+    allowed = torch.rand(B, T, K, generator=g) > 0.6
+    allowed[1, 3] = False                     # a row with no key -> exact zeros
+    out, lse = ops.final_ca_sparse_forward(q, k, v, dev(allowed, torch.bool), D ** -0.5)
+    check(out, ref.final_ca_sparse(host(q), host(k), host(v), allowed, D ** -0.5), dtype)
+    assert torch.all(host(out)[1, 3] == 0) and float(lse[1, 3]) == -math.inf
+    wl = ref.final_ca_sparse_lse(host(q), host(k), host(v), allowed, D ** -0.5)
+    ok = allowed.any(-1)
+    check(lse[ok.to(DEV)], wl[ok], torch.float32, rtol=1e-3, atol=1e-3)
+
+
+# ----------------------------------------------------------------- drop-in
+
+def test_drop_in_build_or_load_runs_on_gpu():
+    from kernels.build import build_or_load
+    mod = build_or_load("loomformer_tria_carry", ["tria/bindings.cpp"], extra_cuda_cflags=["--use_fast_math"])
+    g = gen(3)
+    r, i, o, prev, seed, valid, w = _tria_inputs(g, 2, 3, 16, torch.float32)
+    c, p, s = mod.tria_step_gate_forward(r, i, o, prev, w, 0.05, 1)
+    wc, wp = ref.tria_step_and_gate(host(r), host(i), host(o), host(prev), host(w), 0.05, 1)
+    check(c, wc, torch.float32)
+    check(p, wp, torch.float32)
+    with pytest.raises(RuntimeError, match="axis"):
+        mod.tria_step_forward(r, i, o, prev, 0.05, 3)

@@ -242,3 +242,28 @@ def test_rope_and_attention_step():
         close(q, z["attn.q"][pos])
         close(kctx, z["attn.kctx"][pos])
         close(c, z["attn.c"][pos])
+
+
+# ---------------------------------------------------------------- product-side init
+
+@pytest.mark.parametrize("name,cfg,seed", [("nano_chk_seed2", "nano_chk", 2), ("tiny_seed0", "tiny", 0)])
+def test_engine_init_stream_matches_reference(name, cfg, seed):
+    """loom_amd.weights (the engine's seeded init) against the reference's sha256."""
+    from loom_amd.config import ModelConfig
+    from loom_amd.weights import init_state_dict
+    with open(os.path.join(GOLD, "init_sha256.json")) as f:
+        want = json.load(f)[name]
+    with open(os.path.join(GOLD, "configs.json")) as f:
+        d = json.load(f)[cfg]
+    sd = init_state_dict(ModelConfig.from_dict(d), seed)
+    assert set(sd) == set(want)
+    bad = [k for k, v in sd.items() if _sha(v) != want[k]["sha256"]]
+    assert not bad, f"init differs for {bad[:5]}"
+
+
+def test_engine_config_presets_match_fixture_configs():
+    from loom_amd.config import NANO, NANO_CHK, ModelConfig
+    with open(os.path.join(GOLD, "configs.json")) as f:
+        d = json.load(f)
+    assert ModelConfig.from_dict(NANO) == ModelConfig.from_dict(d["nano"])
+    assert ModelConfig.from_dict(NANO_CHK) == ModelConfig.from_dict(d["nano_chk"])
