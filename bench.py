@@ -77,30 +77,24 @@ def bench_decode(args):
     eng = LoomDecoder(cfg, state, batch=B, dtype=torch.bfloat16, max_len=P + K + 1)
     g = torch.Generator().manual_seed(2)
     prompt = torch.randint(0, cfg.V, (B, P), generator=g).to("cuda")
-    log(f"prefill {P} tokens x B={B} token by token")
+    log(f"prefill {P} tokens x B={B} token by token (one captured HIP graph per step)")
     t0 = time.time()
-    logits = None
-    for pos in range(P - W):
-        logits = eng.step(prompt[:, pos], pos)
+    eng.start(prompt)                                  # position 0 (eager)
+    eng.replay_steps(P - 1 - W)                        # positions 1 .. P-W-1
     torch.cuda.synchronize()
     t_prefill = time.time() - t0
-    for pos in range(P - W, P):                       # warm-up steps
-        logits = eng.step(prompt[:, pos], pos)
+    eng.replay_steps(W)                                # warm-up steps (last W prompt positions)
     torch.cuda.synchronize()
     log(f"prefill done in {t_prefill:.1f}s; timing {K} greedy steps")
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    out = torch.empty(B, K, dtype=torch.long, device="cuda")
-    torch.cuda.synchronize()
     wall0 = time.perf_counter()
     s.record()
-    for i in range(K):
-        nxt = torch.argmax(logits, dim=-1)
-        out[:, i] = nxt
-        logits = eng.step(nxt, P + i)
+    eng.replay_steps(K)                                # K greedy decode steps
     e.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms = s.elapsed_time(e)
+    out = eng.generated()
     return dict(ms_total=ms, ms_per_step=ms / K, tokens_per_s=B * K / (ms / 1e3),
                 wall_s=wall, prefill_s=t_prefill, prefill_tokens_per_s=B * (P - W) / t_prefill,
                 ids_head=out[0, :8].tolist())
@@ -249,6 +243,8 @@ def main():
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--micro-iters", type=int, default=20)
     ap.add_argument("--no-micro", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="microbenchmarks only (for counter passes); value is then null")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-prompt", type=int, default=32)
     ap.add_argument("--cpu-steps", type=int, default=8)
@@ -263,9 +259,11 @@ def main():
     from loom_amd import _lib
     _lib.load()
 
-    res = {}
-    dec = bench_decode(args)
-    log(f"decode: {dec['tokens_per_s']:.0f} tok/s, {dec['ms_per_step']:.3f} ms/step")
+    if args.no_e2e:
+        dec = dict(tokens_per_s=None, ms_per_step=None, prefill_tokens_per_s=None)
+    else:
+        dec = bench_decode(args)
+        log(f"decode: {dec['tokens_per_s']:.0f} tok/s, {dec['ms_per_step']:.3f} ms/step")
     kernels = {}
     roofline = None
     if not args.no_micro:

@@ -190,12 +190,14 @@ int loom_final_ca_sparse_forward(int dtype, const void* q, const void* k, const 
 /* final_ca_sparse_forward with explicit layout, for decode caches: k/v row j
  * of batch b at b*kv_stride_b + j*D, allowed row r (= b*T + t) at
  * r*allowed_stride; with residual != NULL, out = residual + gamma * attention
- * (TriaFinalCrossAttention.step, tria.py:1560-1595, h + gamma*out). */
+ * (TriaFinalCrossAttention.step, tria.py:1560-1595, h + gamma*out).  With
+ * k_dev != NULL the key count is min(*k_dev, K), read on the device (K is then
+ * the capacity and may be 0 keys at run time: out = residual). */
 int loom_final_ca_sparse_strided(int dtype, const void* q, const void* k, const void* v,
                                  int64_t kv_stride_b, const uint8_t* allowed,
                                  int64_t allowed_stride, const void* residual, float gamma,
-                                 void* out, float* lse, int64_t B, int64_t T, int64_t K, int64_t D,
-                                 float scale, void* stream);
+                                 void* out, float* lse, int64_t B, int64_t T, int64_t K,
+                                 const int64_t* k_dev, int64_t D, float scale, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Decode step (Model.step, loomformer.py:3951-4091)
@@ -206,13 +208,14 @@ int loom_final_ca_sparse_strided(int dtype, const void* q, const void* k, const 
  * YaRNRotaryEmbedding.forward :2983-2985).
  *   qkv: [B, (QH + 2*KVH)*HD] dtype (output of the qkv projection);
  *   q_out: [B,QH,HD] dtype (rotated q); cache element (b, t, kvh, d) at
- *   b*cache_stride_b + t*cache_stride_t + kvh*HD + d; position `pos` is written.
+ *   b*cache_stride_b + t*cache_stride_t + kvh*HD + d; position `pos` is written
+ *   (or *pos_dev, read on the device, when pos_dev != NULL).
  *   cos_table/sin_table: [>pos, HD] float, already multiplied by the YaRN
  *   attention factor (the reference's cos_cached/sin_cached). */
 int loom_rope_append(int dtype, const void* qkv, void* q_out, void* k_cache, void* v_cache,
                      const float* cos_table, const float* sin_table, int64_t B, int64_t pos,
-                     int64_t QH, int64_t KVH, int64_t HD, int64_t cache_stride_b,
-                     int64_t cache_stride_t, void* stream);
+                     const int64_t* pos_dev, int64_t QH, int64_t KVH, int64_t HD,
+                     int64_t cache_stride_b, int64_t cache_stride_t, void* stream);
 
 /* Bytes of float workspace loom_gqa_decode_attention needs for len <= max_len. */
 int64_t loom_gqa_workspace_bytes(int64_t B, int64_t max_len, int64_t QH, int64_t KVH, int64_t HD);
@@ -223,12 +226,14 @@ int64_t loom_gqa_workspace_bytes(int64_t B, int64_t max_len, int64_t QH, int64_t
  * GroupedQueryCausalSelfAttention.step (loomformer.py:3316-3329) without
  * materialising the GQA repeat: q-head h reads kv head h / (QH/KVH).
  *   q: [B,QH,HD]; caches as in loom_rope_append; c_out, kctx_out: [B,QH,HD]
- *   (dtype); workspace: at least loom_gqa_workspace_bytes(B, len, ...) bytes. */
+ *   (dtype); workspace: at least loom_gqa_workspace_bytes(B, len, ...) bytes.
+ *   With pos_dev != NULL the length is *pos_dev + 1 (read on the device) and
+ *   `len` is the capacity the launch covers. */
 int loom_gqa_decode_attention(int dtype, const void* q, const void* k_cache, const void* v_cache,
                               int64_t cache_stride_b, int64_t cache_stride_t, void* c_out,
                               void* kctx_out, float* workspace, int64_t workspace_bytes,
-                              int64_t B, int64_t len, int64_t QH, int64_t KVH, int64_t HD,
-                              void* stream);
+                              int64_t B, int64_t len, const int64_t* pos_dev, int64_t QH,
+                              int64_t KVH, int64_t HD, void* stream);
 
 /* out = LayerNorm(a + b) (b may be NULL) over rows of N <= 2048, fp32 gamma and
  * beta, biased variance.  Replaces ln_attn/ln_ffn(skip + branch)
@@ -245,6 +250,37 @@ int loom_add_layernorm(int dtype, const void* a, const void* b, const float* gam
 int loom_tria_decode_temporal(int dtype, const void* depth, const void* prev,
                               const uint8_t* reset_now, const uint8_t* fire, void* out,
                               int64_t B, int64_t H, float polarm_beta, float eps, void* stream);
+
+/* Start of a decode step with device-resident state (pos = *pos_dev), so a
+ * whole step is a fixed launch sequence that a HIP graph can replay.  Token
+ * ids: ids[b] = prompt[b, pos] (row stride prompt_ld) while pos < prompt_len
+ * (prompt may be NULL), otherwise ids is left as written by the caller (the
+ * previous argmax); tokens[b, pos] = ids[b] when tokens != NULL (row stride
+ * tokens_ld).
+ * fire[b] = hard fire for the next token ((pos+1) % window == 0 and
+ * pos+1 < seq_len, loomformer.py:4069-4073) or ids[b] == carry_id (carry_id < 0
+ * disables); reset_now[b] = pending[b] (loomformer.py:3985-3990, 4058). */
+int loom_decode_prologue(int64_t* ids, const int64_t* prompt, int64_t prompt_len,
+                         int64_t prompt_ld, int64_t* tokens, int64_t tokens_ld,
+                         const int64_t* pos_dev, const uint8_t* pending, uint8_t* fire,
+                         uint8_t* reset_now, int64_t carry_id, int64_t window, int64_t seq_len,
+                         int64_t B, void* stream);
+
+/* Greedy pick ids[r] = argmax_v logits[r, v] (first index on ties, as
+ * torch.argmax), the `argmax(logits)` of infer (loomformer.py:5306).
+ * logits: [rows, V] dtype; ids: [rows] int64. */
+int loom_argmax_rows(int dtype, const void* logits, int64_t rows, int64_t V, int64_t* ids,
+                     void* stream);
+
+/* End of a decode step: if any fire[b], the staged final-CA key/value rows
+ * stage_k/stage_v [B,N] (w_qk(a_t), w_v(a_t)) are stored at slot *ca_len of
+ * ca_k/ca_v [B,max_keys,N], ca_valid[b, slot] = fire[b], *ca_len += 1
+ * (TriaFinalCrossAttention.step, tria.py:1576-1582); then pending = fire and
+ * *pos_dev += 1. */
+int loom_decode_epilogue(int dtype, const void* stage_k, const void* stage_v, void* ca_k,
+                         void* ca_v, uint8_t* ca_valid, int64_t* ca_len, const uint8_t* fire,
+                         uint8_t* pending, int64_t* pos_dev, int64_t B, int64_t N,
+                         int64_t max_keys, void* stream);
 
 #ifdef __cplusplus
 }

@@ -15,8 +15,9 @@ template <typename T>
 __global__ void __launch_bounds__(256)
 rope_append_kernel(const T* __restrict__ qkv, T* __restrict__ q_out, T* __restrict__ kc,
                    T* __restrict__ vc, const float* __restrict__ cosv, const float* __restrict__ sinv,
-                   int64_t B, int64_t pos, int QH, int KVH, int HD, int64_t cstride_b,
-                   int64_t cstride_t) {
+                   int64_t B, int64_t pos, const int64_t* __restrict__ pos_dev, int QH, int KVH,
+                   int HD, int64_t cstride_b, int64_t cstride_t) {
+    if (pos_dev != nullptr) pos = *pos_dev;
     const int heads = QH + 2 * KVH;
     const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= B * heads * HD) return;
@@ -42,30 +43,42 @@ rope_append_kernel(const T* __restrict__ qkv, T* __restrict__ q_out, T* __restri
 }
 
 // ------------------------------------------------------------------ GQA attention
-// Split over the sequence (flash-decoding): block (chunk, kvh, b) handles
+// Split over the sequence (flash-decoding): block (chunk, kvh, b) covers
 // kAttnChunk positions for the G query heads that share kv head kvh and writes
-// an unnormalised partial (m, l, sum p*v, sum p*k) per head; the combine
-// kernel merges the chunks.  Lanes are grouped 16 per cache row, EPL = HD/16
-// contiguous elements per lane.
+// an unnormalised partial (m, l, sum p*v, sum p*k) per head; the combine kernel
+// merges the chunks.  One pass over K and V: each cache row is read once and
+// feeds both the scores and the A.K readout.
+//
+// Mapping: LPR lanes per cache row (EPL = HD/LPR contiguous elements each);
+// the block's NG = 256/LPR row groups take positions t0 + grp + NG*i.  A group
+// scores kAttnBatch positions for all G heads at once, then folds them into an
+// online softmax with one rescale per batch.  Scores are kept in log2 units
+// (q is pre-scaled by log2(e)/sqrt(HD)) so every exponential is one v_exp_f32.
 constexpr int kAttnChunk = 256;
 constexpr int kAttnMaxG = 8;
+constexpr int kAttnBatch = 4;
 
 template <typename T, int EPL, int G, int LPR>
 __global__ void __launch_bounds__(256)
 gqa_partial_kernel(const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
                    int64_t cstride_b, int64_t cstride_t, float* __restrict__ ws, int64_t len,
-                   int QH, int KVH, float scale) {
+                   const int64_t* __restrict__ pos_dev, int QH, int KVH, float qscale) {
     constexpr int HD = EPL * LPR;
-    constexpr int RG = 256 / LPR;          // rows handled concurrently by the block
-    constexpr int RPW = 64 / LPR;          // row groups per wave
-    __shared__ float sc[G][kAttnChunk];
-    __shared__ float red[4][2 * G * HD];
-    __shared__ float stat[G][2];
+    constexpr int NG = 256 / LPR;          // row groups per block
+    constexpr int REC = 2 * G + 2 * G * HD;
+    __shared__ float wred[4][2 * G + 2 * G * HD];
     const int chunk = blockIdx.x, kvh = blockIdx.y;
     const int64_t b = blockIdx.z;
     const int nchunks = gridDim.x;
     const int tid = threadIdx.x, j = tid % LPR, grp = tid / LPR;
+    const int wave = tid >> 6, lane = tid & 63;
     const int64_t t0 = (int64_t)chunk * kAttnChunk;
+    if (pos_dev != nullptr) len = *pos_dev + 1;   // graph replay: length from the device
+    float* rec = ws + (((int64_t)b * KVH + kvh) * nchunks + chunk) * REC;
+    if (t0 >= len) {                              // chunk past the end: empty partial
+        for (int k = tid; k < REC; k += blockDim.x) rec[k] = k < G ? -INFINITY : 0.0f;
+        return;
+    }
     const int64_t t1 = t0 + kAttnChunk < len ? t0 + kAttnChunk : len;
     const int d0 = j * EPL;
 
@@ -73,107 +86,122 @@ gqa_partial_kernel(const T* __restrict__ q, const T* __restrict__ kc, const T* _
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) qv[g][e] = ld(q + (b * QH + kvh * G + g) * HD + d0 + e) * scale;
+        for (int e = 0; e < EPL; ++e)
+            qv[g][e] = ld(q + (b * QH + kvh * G + g) * HD + d0 + e) * qscale;
 
     const T* kbase = kc + b * cstride_b + kvh * HD + d0;
     const T* vbase = vc + b * cstride_b + kvh * HD + d0;
-    // scores
-    for (int64_t t = t0 + grp; t < t0 + kAttnChunk; t += RG) {
-        float dot[G];
+    float m[G], l[G], ac[G][EPL], ak[G][EPL];
 #pragma unroll
-        for (int g = 0; g < G; ++g) dot[g] = 0.0f;
-        if (t < t1) {
-            float kv[EPL];
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) kv[e] = ld(kbase + t * cstride_t + e);
+        for (int e = 0; e < EPL; ++e) ac[g][e] = ak[g][e] = 0.0f;
+    }
+    for (int64_t base = t0 + grp; base < t1; base += NG * kAttnBatch) {
+        float kv[kAttnBatch][EPL], vv[kAttnBatch][EPL];
+        bool ok[kAttnBatch];
 #pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) dot[g] = fmaf(qv[g][e], kv[e], dot[g]);
+        for (int u = 0; u < kAttnBatch; ++u) {
+            const int64_t t = base + (int64_t)NG * u;
+            ok[u] = t < t1;
+            const int64_t tc = ok[u] ? t : t1 - 1;   // in-range row; its score is masked
+            RowIO<T, EPL>::load(kbase + tc * cstride_t, kv[u]);
+            RowIO<T, EPL>::load(vbase + tc * cstride_t, vv[u]);
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float s = group_sum<LPR>(dot[g]);
-            if (j == 0) sc[g][t - t0] = t < t1 ? s : -INFINITY;
-        }
-    }
-    __syncthreads();
-    // per-head max / exp / sum (wave w handles heads w, w+4, ...)
-    const int wave = tid >> 6, lane = tid & 63;
-    for (int g = wave; g < G; g += 4) {
-        float m = -INFINITY;
-        for (int k = lane; k < kAttnChunk; k += 64) m = fmaxf(m, sc[g][k]);
-        m = wave_max(m);
-        float l = 0.0f;
-        for (int k = lane; k < kAttnChunk; k += 64) {
-            const float p = sc[g][k] == -INFINITY ? 0.0f : fexp(sc[g][k] - m);
-            sc[g][k] = p;
-            l += p;
-        }
-        l = wave_sum(l);
-        if (lane == 0) {
-            stat[g][0] = m;
-            stat[g][1] = l;
-        }
-    }
-    __syncthreads();
-    // weighted sums of V and K
-    float cacc[G][EPL], kacc[G][EPL];
+            float s[kAttnBatch];
+            float mx = m[g];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+            for (int u = 0; u < kAttnBatch; ++u) {
+                float dot = 0.0f;
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) cacc[g][e] = kacc[g][e] = 0.0f;
-    for (int64_t t = t0 + grp; t < t1; t += RG) {
-        float kv[EPL], vv[EPL];
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            kv[e] = ld(kbase + t * cstride_t + e);
-            vv[e] = ld(vbase + t * cstride_t + e);
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float p = sc[g][t - t0];
+                for (int e = 0; e < EPL; ++e) dot = fmaf(qv[g][e], kv[u][e], dot);
+                dot = group_sum<LPR>(dot);
+                s[u] = ok[u] ? dot : -INFINITY;
+                mx = fmaxf(mx, s[u]);
+            }
+            if (mx == -INFINITY) continue;        // whole batch past the end for this group
+            const float corr = __builtin_amdgcn_exp2f(m[g] - mx);   // 0 when m was -inf
+            float lsum = l[g] * corr;
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
-                cacc[g][e] = fmaf(p, vv[e], cacc[g][e]);
-                kacc[g][e] = fmaf(p, kv[e], kacc[g][e]);
+                ac[g][e] *= corr;
+                ak[g][e] *= corr;
             }
+#pragma unroll
+            for (int u = 0; u < kAttnBatch; ++u) {
+                const float p = ok[u] ? __builtin_amdgcn_exp2f(s[u] - mx) : 0.0f;
+                lsum += p;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    ac[g][e] = fmaf(p, vv[u][e], ac[g][e]);
+                    ak[g][e] = fmaf(p, kv[u][e], ak[g][e]);
+                }
+            }
+            l[g] = lsum;
+            m[g] = mx;
         }
     }
-    // reduce the RPW row groups of each wave (lanes j, j+LPR, ...)
+    // merge the row groups of each wave (lanes j, j+LPR, ...), head by head
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g) {
+        float M = m[g];
+#pragma unroll
+        for (int off = LPR; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        const float f = (M == -INFINITY || m[g] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m[g] - M);
+        float L = l[g] * f;
+#pragma unroll
+        for (int off = LPR; off < 64; off <<= 1) L += __shfl_xor(L, off, 64);
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
-            float c = cacc[g][e], k = kacc[g][e];
+            float c = ac[g][e] * f, k = ak[g][e] * f;
 #pragma unroll
             for (int off = LPR; off < 64; off <<= 1) {
                 c += __shfl_xor(c, off, 64);
                 k += __shfl_xor(k, off, 64);
             }
-            cacc[g][e] = c;
-            kacc[g][e] = k;
+            ac[g][e] = c;
+            ak[g][e] = k;
         }
+        m[g] = M;
+        l[g] = L;
+    }
     if (lane < LPR) {
 #pragma unroll
-        for (int g = 0; g < G; ++g)
+        for (int g = 0; g < G; ++g) {
+            if (lane == 0) {
+                wred[wave][g] = m[g];
+                wred[wave][G + g] = l[g];
+            }
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
-                red[wave][g * HD + d0 + e] = cacc[g][e];
-                red[wave][G * HD + g * HD + d0 + e] = kacc[g][e];
+                wred[wave][2 * G + g * HD + d0 + e] = ac[g][e];
+                wred[wave][2 * G + G * HD + g * HD + d0 + e] = ak[g][e];
             }
+        }
     }
     __syncthreads();
-    // partial record: [m(G) | l(G) | c(G*HD) | kctx(G*HD)]
-    const int rec = 2 * G + 2 * G * HD;
-    float* out = ws + (((int64_t)b * KVH + kvh) * nchunks + chunk) * rec;
-    for (int k = tid; k < 2 * G * HD; k += blockDim.x)
-        out[2 * G + k] = red[0][k] + red[1][k] + red[2][k] + red[3][k];
-    if (tid < G) {
-        out[tid] = stat[tid][0];
-        out[G + tid] = stat[tid][1];
+    // merge the four waves into the chunk record
+    for (int k = tid; k < REC; k += blockDim.x) {
+        int g;
+        if (k < 2 * G) g = k % G;
+        else g = ((k - 2 * G) % (G * HD)) / HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, wred[w][g]);
+        if (k < G) {
+            rec[k] = M;
+            continue;
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            if (wred[w][g] != -INFINITY) acc = fmaf(wred[w][k], __builtin_amdgcn_exp2f(wred[w][g] - M), acc);
+        rec[k] = acc;
     }
-    (void)RPW;
 }
 
 template <typename T, int G>
@@ -186,13 +214,13 @@ gqa_combine_kernel(const float* __restrict__ ws, T* __restrict__ c_out, T* __res
     const float* base = ws + ((int64_t)b * KVH + kvh) * nchunks * rec;
     for (int k = threadIdx.x; k < G * HD; k += blockDim.x) {
         const int g = k / HD, d = k % HD;
-        float M = -INFINITY;
+        float M = -INFINITY;   // chunk 0 always holds position 0, so M is finite
         for (int c = 0; c < nchunks; ++c) M = fmaxf(M, base[c * rec + g]);
         float L = 0.0f, C = 0.0f, K = 0.0f;
         for (int c = 0; c < nchunks; ++c) {
             const float* r = base + c * rec;
             if (r[g] == -INFINITY) continue;
-            const float w = fexp(r[g] - M);
+            const float w = __builtin_amdgcn_exp2f(r[g] - M);   // log2-domain maxima
             L = fmaf(r[G + g], w, L);
             C = fmaf(r[2 * G + g * HD + d], w, C);
             K = fmaf(r[2 * G + G * HD + g * HD + d], w, K);
@@ -242,6 +270,59 @@ add_layernorm_kernel(const T* __restrict__ a, const T* __restrict__ bsrc,
     for (int k = 0; k < kMax; ++k) {
         const int c = lane + 64 * k;
         if (c < N) st(out + row * N + c, (x[k] - mean) * rstd * gamma[c] + beta[c]);
+    }
+}
+
+// Vector form for N % 8 == 0 (N <= 64*8*4): lane owns 8-element vectors
+// lane, lane+64, ...; two wave reductions (mean, variance).
+template <typename T, int NV>
+__global__ void __launch_bounds__(256)
+add_layernorm_vec_kernel(const T* __restrict__ a, const T* __restrict__ bsrc,
+                         const float* __restrict__ gamma, const float* __restrict__ beta,
+                         T* __restrict__ out, int64_t rows, int N, float eps) {
+    const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int nvec = N >> 3;
+    float x[NV][8];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int v = lane + 64 * k;
+        if (v < nvec) {
+            Vec8<T>::load(a + row * N + v * 8, x[k]);
+            if (bsrc != nullptr) {
+                float y[8];
+                Vec8<T>::load(bsrc + row * N + v * 8, y);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[k][e] += y[e];
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s += x[k][e];
+        }
+    }
+    const float mean = wave_sum(s) / N;
+    float var = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+        if (lane + 64 * k < nvec) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = x[k][e] - mean;
+                var = fmaf(d, d, var);
+            }
+        }
+    const float rstd = 1.0f / sqrtf(wave_sum(var) / N + eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int v = lane + 64 * k;
+        if (v < nvec) {
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                o[e] = (x[k][e] - mean) * rstd * gamma[v * 8 + e] + beta[v * 8 + e];
+            Vec8<T>::store(out + row * N + v * 8, o);
+        }
     }
 }
 
@@ -303,28 +384,30 @@ decode_temporal_kernel(const T* __restrict__ depth, const T* __restrict__ prev,
 
 template <typename T>
 static int rope_dispatch(const void* qkv, void* q_out, void* kc, void* vc, const float* cosv,
-                         const float* sinv, int64_t B, int64_t pos, int64_t QH, int64_t KVH,
-                         int64_t HD, int64_t sb, int64_t stt, hipStream_t st) {
+                         const float* sinv, int64_t B, int64_t pos, const int64_t* pos_dev,
+                         int64_t QH, int64_t KVH, int64_t HD, int64_t sb, int64_t stt,
+                         hipStream_t st) {
     const int64_t total = B * (QH + 2 * KVH) * HD;
     hipLaunchKernelGGL((rope_append_kernel<T>), dim3((unsigned)ceil_div(total, 256)), dim3(256), 0,
-                       st, (const T*)qkv, (T*)q_out, (T*)kc, (T*)vc, cosv, sinv, B, pos, (int)QH,
-                       (int)KVH, (int)HD, sb, stt);
+                       st, (const T*)qkv, (T*)q_out, (T*)kc, (T*)vc, cosv, sinv, B, pos, pos_dev,
+                       (int)QH, (int)KVH, (int)HD, sb, stt);
     return launch_status("loom_rope_append");
 }
 
 template <typename T>
 static int gqa_dispatch(const void* q, const void* kc, const void* vc, int64_t sb, int64_t stt,
-                        void* c_out, void* k_out, float* ws, int64_t B, int64_t len, int64_t QH,
-                        int64_t KVH, int64_t HD, hipStream_t st) {
+                        void* c_out, void* k_out, float* ws, int64_t B, int64_t len,
+                        const int64_t* pos_dev, int64_t QH, int64_t KVH, int64_t HD,
+                        hipStream_t st) {
     const int G = (int)(QH / KVH);
     const int nchunks = (int)ceil_div(len, kAttnChunk);
-    const float scale = 1.0f / sqrtf((float)HD);
+    const float scale = kLog2e / sqrtf((float)HD);   // scores in log2 units
     dim3 grid(nchunks, (unsigned)KVH, (unsigned)B);
 #define LOOM_GQA(E, GG, LPR)                                                                     \
     if (HD == E * LPR && G == GG) {                                                              \
         hipLaunchKernelGGL((gqa_partial_kernel<T, E, GG, LPR>), grid, dim3(256), 0, st, (const T*)q, \
-                           (const T*)kc, (const T*)vc, sb, stt, ws, len, (int)QH, (int)KVH,       \
-                           scale);                                                               \
+                           (const T*)kc, (const T*)vc, sb, stt, ws, len, pos_dev, (int)QH,        \
+                           (int)KVH, scale);                                                     \
         int rc = launch_status("loom_gqa_decode_attention");                                    \
         if (rc != LOOM_OK) return rc;                                                            \
         hipLaunchKernelGGL((gqa_combine_kernel<T, GG>), dim3((unsigned)KVH, (unsigned)B),        \
@@ -352,6 +435,19 @@ static int gqa_dispatch(const void* q, const void* kc, const void* vc, int64_t s
 template <typename T>
 static int ln_dispatch(const void* a, const void* b, const float* g, const float* be, void* out,
                        int64_t rows, int64_t N, float eps, hipStream_t st) {
+    const bool vec = N % 8 == 0 && N <= 64 * 8 * 4 &&
+                     (((uintptr_t)a | (uintptr_t)b | (uintptr_t)out) & 15) == 0;
+    if (vec) {
+        const dim3 grid((unsigned)ceil_div(rows * 64, 256));
+        const int nv = (int)ceil_div(N / 8, 64);
+        if (nv <= 2)
+            hipLaunchKernelGGL((add_layernorm_vec_kernel<T, 2>), grid, dim3(256), 0, st,
+                               (const T*)a, (const T*)b, g, be, (T*)out, rows, (int)N, eps);
+        else
+            hipLaunchKernelGGL((add_layernorm_vec_kernel<T, 4>), grid, dim3(256), 0, st,
+                               (const T*)a, (const T*)b, g, be, (T*)out, rows, (int)N, eps);
+        return launch_status("loom_add_layernorm");
+    }
     hipLaunchKernelGGL((add_layernorm_kernel<T>), dim3((unsigned)ceil_div(rows * 64, 256)),
                        dim3(256), 0, st, (const T*)a, (const T*)b, g, be, (T*)out, rows, (int)N,
                        eps);
@@ -390,8 +486,9 @@ extern "C" int64_t loom_gqa_workspace_bytes(int64_t B, int64_t max_len, int64_t 
 
 extern "C" int loom_rope_append(int dtype, const void* qkv, void* q_out, void* k_cache,
                                 void* v_cache, const float* cos_table, const float* sin_table,
-                                int64_t B, int64_t pos, int64_t QH, int64_t KVH, int64_t HD,
-                                int64_t cache_stride_b, int64_t cache_stride_t, void* stream) {
+                                int64_t B, int64_t pos, const int64_t* pos_dev, int64_t QH,
+                                int64_t KVH, int64_t HD, int64_t cache_stride_b,
+                                int64_t cache_stride_t, void* stream) {
     clear_error();
     LOOM_CHECK(qkv && q_out && k_cache && v_cache && cos_table && sin_table,
                "rope_append: null argument");
@@ -399,15 +496,16 @@ extern "C" int loom_rope_append(int dtype, const void* qkv, void* q_out, void* k
     LOOM_CHECK(cache_stride_t >= KVH * HD, "rope_append: cache row stride too small");
     if (B == 0) return LOOM_OK;
     LOOM_DTYPE_SWITCH(dtype, rope_dispatch, qkv, q_out, k_cache, v_cache, cos_table, sin_table, B,
-                      pos, QH, KVH, HD, cache_stride_b, cache_stride_t, (hipStream_t)stream)
+                      pos, pos_dev, QH, KVH, HD, cache_stride_b, cache_stride_t,
+                      (hipStream_t)stream)
 }
 
 extern "C" int loom_gqa_decode_attention(int dtype, const void* q, const void* k_cache,
                                          const void* v_cache, int64_t cache_stride_b,
                                          int64_t cache_stride_t, void* c_out, void* kctx_out,
                                          float* workspace, int64_t workspace_bytes, int64_t B,
-                                         int64_t len, int64_t QH, int64_t KVH, int64_t HD,
-                                         void* stream) {
+                                         int64_t len, const int64_t* pos_dev, int64_t QH,
+                                         int64_t KVH, int64_t HD, void* stream) {
     clear_error();
     LOOM_CHECK(q && k_cache && v_cache && c_out && kctx_out && workspace,
                "gqa_decode_attention: null argument");
@@ -416,9 +514,162 @@ extern "C" int loom_gqa_decode_attention(int dtype, const void* q, const void* k
                (long long)QH, (long long)KVH);
     LOOM_CHECK(workspace_bytes >= loom_gqa_workspace_bytes(B, len, QH, KVH, HD),
                "gqa_decode_attention: workspace too small (%lld bytes)", (long long)workspace_bytes);
+    // cache rows are read as 4-/8-byte words when each lane owns an even count
+    LOOM_CHECK(HD % 32 != 0 || ((((uintptr_t)k_cache | (uintptr_t)v_cache) & 7) == 0 &&
+                                cache_stride_b % 2 == 0 && cache_stride_t % 2 == 0),
+               "gqa_decode_attention: caches must be 8-byte aligned with even strides");
     if (B == 0) return LOOM_OK;
     LOOM_DTYPE_SWITCH(dtype, gqa_dispatch, q, k_cache, v_cache, cache_stride_b, cache_stride_t,
-                      c_out, kctx_out, workspace, B, len, QH, KVH, HD, (hipStream_t)stream)
+                      c_out, kctx_out, workspace, B, len, pos_dev, QH, KVH, HD,
+                      (hipStream_t)stream)
+}
+
+// ---------------------------------------------------------------- step control
+// Device-resident step state so a whole decode step is a fixed launch sequence
+// (capturable in a HIP graph): pos_dev[0] = position of this step.
+
+__global__ void decode_prologue_kernel(int64_t* __restrict__ ids, const int64_t* __restrict__ prompt,
+                                       int64_t prompt_len, int64_t prompt_ld,
+                                       int64_t* __restrict__ tokens, int64_t tokens_ld,
+                                       const int64_t* __restrict__ pos_dev,
+                                       const uint8_t* __restrict__ pending, uint8_t* __restrict__ fire,
+                                       uint8_t* __restrict__ reset_now, int64_t carry_id,
+                                       int64_t window, int64_t seq_len, int64_t B) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    const int64_t pos = *pos_dev;
+    int64_t id = ids[b];
+    if (prompt != nullptr && pos < prompt_len) {
+        id = prompt[b * prompt_ld + pos];
+        ids[b] = id;
+    }
+    if (tokens != nullptr) tokens[b * tokens_ld + pos] = id;
+    // hard fire for the next token (loomformer.py:4069-4073) or an explicit <CARRY> id
+    const bool hard = (pos + 1 < seq_len) && ((pos + 1) % window == 0);
+    fire[b] = (hard || (carry_id >= 0 && id == carry_id)) ? 1 : 0;
+    reset_now[b] = pending[b];
+}
+
+// Final-CA key append (tria.py:1576-1582) and end-of-step bookkeeping: if any
+// row fires, the staged keys/values of every row are stored at slot ca_len and
+// marked valid where that row fired; then pending = fire and pos += 1.
+template <typename T>
+__global__ void __launch_bounds__(256)
+decode_epilogue_kernel(const T* __restrict__ stage_k, const T* __restrict__ stage_v,
+                       T* __restrict__ ca_k, T* __restrict__ ca_v, uint8_t* __restrict__ ca_valid,
+                       int64_t* __restrict__ ca_len, const uint8_t* __restrict__ fire,
+                       uint8_t* __restrict__ pending, int64_t* __restrict__ pos_dev, int64_t B,
+                       int64_t N, int64_t max_keys) {
+    __shared__ int any;
+    __shared__ int64_t slot;
+    if (threadIdx.x == 0) {
+        int a = 0;
+        for (int64_t b = 0; b < B; ++b) a |= fire[b];
+        any = a;
+        slot = *ca_len;
+    }
+    __syncthreads();
+    if (any && slot < max_keys) {
+        for (int64_t e = threadIdx.x; e < B * N; e += blockDim.x) {
+            const int64_t b = e / N, d = e - b * N;
+            ca_k[(b * max_keys + slot) * N + d] = stage_k[e];
+            ca_v[(b * max_keys + slot) * N + d] = stage_v[e];
+        }
+        for (int64_t b = threadIdx.x; b < B; b += blockDim.x)
+            ca_valid[b * max_keys + slot] = fire[b];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (any && slot < max_keys) *ca_len = slot + 1;
+        *pos_dev += 1;
+    }
+    for (int64_t b = threadIdx.x; b < B; b += blockDim.x) pending[b] = fire[b];
+}
+
+// Greedy pick: ids[r] = argmax_v logits[r, v], the first index on ties
+// (torch.argmax semantics); one block per row.
+template <typename T>
+__global__ void __launch_bounds__(256)
+argmax_rows_kernel(const T* __restrict__ logits, int64_t V, int64_t* __restrict__ ids) {
+    __shared__ float bv[4];
+    __shared__ int64_t bi[4];
+    const int64_t row = blockIdx.x;
+    const T* x = logits + row * V;
+    float best = -INFINITY;
+    int64_t idx = V;                       // NaN-free rows always replace this
+    for (int64_t v = threadIdx.x; v < V; v += blockDim.x) {
+        const float f = ld(x + v);
+        if (f > best || (f == best && v < idx)) { best = f; idx = v; }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ob = __shfl_xor(best, off, 64);
+        const int64_t oi = __shfl_xor(idx, off, 64);
+        if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { bv[w] = best; bi[w] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < (int)(blockDim.x >> 6); ++k)
+            if (bv[k] > best || (bv[k] == best && bi[k] < idx)) { best = bv[k]; idx = bi[k]; }
+        ids[row] = idx < V ? idx : 0;
+    }
+}
+
+template <typename T>
+static int argmax_dispatch(const void* logits, int64_t rows, int64_t V, int64_t* ids,
+                           hipStream_t st) {
+    hipLaunchKernelGGL((argmax_rows_kernel<T>), dim3((unsigned)rows), dim3(256), 0, st,
+                       (const T*)logits, V, ids);
+    return launch_status("loom_argmax_rows");
+}
+
+template <typename T>
+static int epilogue_dispatch(const void* sk, const void* sv, void* ck, void* cv, uint8_t* valid,
+                             int64_t* ca_len, const uint8_t* fire, uint8_t* pending,
+                             int64_t* pos_dev, int64_t B, int64_t N, int64_t max_keys,
+                             hipStream_t st) {
+    hipLaunchKernelGGL((decode_epilogue_kernel<T>), dim3(1), dim3(256), 0, st, (const T*)sk,
+                       (const T*)sv, (T*)ck, (T*)cv, valid, ca_len, fire, pending, pos_dev, B, N,
+                       max_keys);
+    return launch_status("loom_decode_epilogue");
+}
+
+extern "C" int loom_decode_prologue(int64_t* ids, const int64_t* prompt, int64_t prompt_len,
+                                    int64_t prompt_ld, int64_t* tokens, int64_t tokens_ld,
+                                    const int64_t* pos_dev, const uint8_t* pending, uint8_t* fire,
+                                    uint8_t* reset_now, int64_t carry_id, int64_t window,
+                                    int64_t seq_len, int64_t B, void* stream) {
+    clear_error();
+    LOOM_CHECK(ids && pos_dev && pending && fire && reset_now, "decode_prologue: null argument");
+    LOOM_CHECK(window >= 1 && B >= 0, "decode_prologue: bad window/batch");
+    LOOM_CHECK(!prompt || prompt_ld >= prompt_len, "decode_prologue: prompt row stride < length");
+    if (B == 0) return LOOM_OK;
+    hipLaunchKernelGGL(decode_prologue_kernel, dim3((unsigned)ceil_div(B, 256)), dim3(256), 0,
+                       (hipStream_t)stream, ids, prompt, prompt_len, prompt_ld, tokens, tokens_ld,
+                       pos_dev, pending, fire, reset_now, carry_id, window, seq_len, B);
+    return launch_status("loom_decode_prologue");
+}
+
+extern "C" int loom_argmax_rows(int dtype, const void* logits, int64_t rows, int64_t V,
+                                int64_t* ids, void* stream) {
+    clear_error();
+    LOOM_CHECK(logits && ids && V >= 1 && rows >= 0, "argmax_rows: bad arguments");
+    if (rows == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, argmax_dispatch, logits, rows, V, ids, (hipStream_t)stream)
+}
+
+extern "C" int loom_decode_epilogue(int dtype, const void* stage_k, const void* stage_v,
+                                    void* ca_k, void* ca_v, uint8_t* ca_valid, int64_t* ca_len,
+                                    const uint8_t* fire, uint8_t* pending, int64_t* pos_dev,
+                                    int64_t B, int64_t N, int64_t max_keys, void* stream) {
+    clear_error();
+    LOOM_CHECK(stage_k && stage_v && ca_k && ca_v && ca_valid && ca_len && fire && pending &&
+                   pos_dev,
+               "decode_epilogue: null argument");
+    LOOM_DTYPE_SWITCH(dtype, epilogue_dispatch, stage_k, stage_v, ca_k, ca_v, ca_valid, ca_len,
+                      fire, pending, pos_dev, B, N, max_keys, (hipStream_t)stream)
 }
 
 extern "C" int loom_add_layernorm(int dtype, const void* a, const void* b, const float* gamma,

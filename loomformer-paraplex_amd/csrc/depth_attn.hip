@@ -16,49 +16,6 @@
 
 namespace loom {
 
-template <typename T, int EPL>
-struct RowIO {
-    __device__ __forceinline__ static void load(const T* p, float v[EPL]) {
-        if constexpr (sizeof(T) == 2 && EPL % 2 == 0) {
-#pragma unroll
-            for (int k = 0; k < EPL / 2; ++k) {
-                const uint32_t w = reinterpret_cast<const uint32_t*>(p)[k];
-                T lo{(uint16_t)(w & 0xffffu)}, hi{(uint16_t)(w >> 16)};
-                v[2 * k] = ld(&lo);
-                v[2 * k + 1] = ld(&hi);
-            }
-        } else if constexpr (sizeof(T) == 4 && EPL % 2 == 0) {
-#pragma unroll
-            for (int k = 0; k < EPL / 2; ++k) {
-                const float2 w = reinterpret_cast<const float2*>(p)[k];
-                v[2 * k] = w.x;
-                v[2 * k + 1] = w.y;
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < EPL; ++k) v[k] = ld(p + k);
-        }
-    }
-    __device__ __forceinline__ static void store(T* p, const float v[EPL]) {
-        if constexpr (sizeof(T) == 2 && EPL % 2 == 0) {
-#pragma unroll
-            for (int k = 0; k < EPL / 2; ++k) {
-                T lo, hi;
-                st(&lo, v[2 * k]);
-                st(&hi, v[2 * k + 1]);
-                reinterpret_cast<uint32_t*>(p)[k] = (uint32_t)lo.x | ((uint32_t)hi.x << 16);
-            }
-        } else if constexpr (sizeof(T) == 4 && EPL % 2 == 0) {
-#pragma unroll
-            for (int k = 0; k < EPL / 2; ++k)
-                reinterpret_cast<float2*>(p)[k] = make_float2(v[2 * k], v[2 * k + 1]);
-        } else {
-#pragma unroll
-            for (int k = 0; k < EPL; ++k) st(p + k, v[k]);
-        }
-    }
-};
-
 constexpr int kDepthChunk = 8;
 
 template <typename T, int EPL>

@@ -185,6 +185,88 @@ gemm_bf16_mfma_kernel(GemmArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ skinny bf16 (M <= 64)
+// Decode-shaped products: the weight is streamed once and dominates traffic.
+// Block = 16 weight rows (one MFMA n-tile) x all M rows (MT m-tiles of 16);
+// its four waves split K into contiguous quarters.  Fragments are loaded
+// straight from global memory in the MFMA operand layout (lane l: row l%16,
+// 8 consecutive k at 8*(l/16)), kUnroll k-steps at a time so each lane keeps
+// several 16-byte weight loads in flight.  The four partial tiles are summed
+// through LDS and the epilogue is applied by all 256 threads.
+constexpr int SK_WAVES = 4, SK_UNROLL = 4;
+
+template <int MT, bool GATHER>
+__global__ void __launch_bounds__(256)
+gemm_bf16_skinny_kernel(GemmArgs a) {
+    __shared__ float red[SK_WAVES][MT][4][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t n0 = (int64_t)blockIdx.x * 16;
+    const int64_t g = GATHER ? n0 / a.Hq : 0;
+    const int fr = lane & 15, fk = (lane >> 4) * 8;
+    const uint16_t* W = (const uint16_t*)a.W;
+    const uint16_t* X = (const uint16_t*)a.X;
+    // k range of this wave, in whole 32-wide steps
+    const int64_t nsteps = ceil_div(a.K, 32);
+    const int64_t per = ceil_div(nsteps, SK_WAVES);
+    const int64_t s_begin = wave * per;
+    const int64_t s_end = s_begin + per < nsteps ? s_begin + per : nsteps;
+    const int64_t n = n0 + fr;
+    const bool nvalid = n < a.N;
+
+    f32x4 acc[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int64_t s0 = s_begin; s0 < s_end; s0 += SK_UNROLL) {
+        uint4 wv[SK_UNROLL];
+        uint4 xv[SK_UNROLL][MT];
+#pragma unroll
+        for (int u = 0; u < SK_UNROLL; ++u) {
+            const int64_t k = (s0 + u) * 32 + fk;
+            const bool kin = (s0 + u) < s_end && k < a.K;
+            wv[u] = (kin && nvalid) ? *reinterpret_cast<const uint4*>(W + n * a.ldw + k)
+                                    : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+                const int64_t m = j * 16 + fr;
+                uint4 v = make_uint4(0, 0, 0, 0);
+                if (kin && m < a.M) {
+                    if constexpr (GATHER)
+                        v = *reinterpret_cast<const uint4*>(gather_ptr(a, m, k, g, 2));
+                    else
+                        v = *reinterpret_cast<const uint4*>(X + m * a.ldx + k);
+                }
+                xv[u][j] = v;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SK_UNROLL; ++u)
+#pragma unroll
+            for (int j = 0; j < MT; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8, wv[u]), __builtin_bit_cast(bf16x8, xv[u][j]), acc[j],
+                    0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][j][r][lane] = acc[j][r];
+    __syncthreads();
+    // output (m, nn) with nn = n - n0; accumulator element: lane = m%16 + 16*(nn/4), r = nn%4
+    uint16_t* out = (uint16_t*)a.out;
+    for (int o = tid; o < MT * 256; o += 256) {
+        const int nn = o & 15, mi = o >> 4;       // mi in [0, 16*MT)
+        const int j = mi >> 4, ml = mi & 15;
+        const int64_t m = mi, nidx = n0 + nn;
+        if (m >= a.M || nidx >= a.N) continue;
+        const int ln = ml + 16 * (nn >> 2), r = nn & 3;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < SK_WAVES; ++w) v += red[w][j][r][ln];
+        out[m * a.ldc + nidx] = f32_to_bf16(epilogue<bf16_t>(a, m, nidx, v));
+    }
+}
+
 // ------------------------------------------------------------------ SIMT
 
 constexpr int SB_M = 64, SB_N = 64, SB_K = 16;
@@ -271,6 +353,24 @@ template <typename T, bool GATHER>
 static int run_gemm(const GemmArgs& a, hipStream_t st, const char* what) {
     if (a.M == 0 || a.N == 0) return LOOM_OK;
     if constexpr (sizeof(T) == 2 && std::is_same<T, bf16_t>::value) {
+        bool sk = a.M <= 64 && a.K % 8 == 0 && a.ldw % 8 == 0 && ((uintptr_t)a.W & 15) == 0;
+        if (GATHER)
+            sk = sk && a.Hq % 16 == 0 && a.HD % 8 == 0 && a.Nm % 8 == 0 &&
+                 ((uintptr_t)a.src[0] | (uintptr_t)a.src[1] | (uintptr_t)a.src[2] |
+                  (uintptr_t)a.src[3] | (uintptr_t)a.src[4]) % 16 == 0;
+        else
+            sk = sk && a.ldx % 8 == 0 && ((uintptr_t)a.X & 15) == 0;
+        if (sk) {
+            const dim3 grid((unsigned)ceil_div(a.N, 16));
+            const int mt = (int)ceil_div(a.M, 16);
+            switch (mt) {
+                case 1: hipLaunchKernelGGL((gemm_bf16_skinny_kernel<1, GATHER>), grid, dim3(256), 0, st, a); break;
+                case 2: hipLaunchKernelGGL((gemm_bf16_skinny_kernel<2, GATHER>), grid, dim3(256), 0, st, a); break;
+                case 3: hipLaunchKernelGGL((gemm_bf16_skinny_kernel<3, GATHER>), grid, dim3(256), 0, st, a); break;
+                default: hipLaunchKernelGGL((gemm_bf16_skinny_kernel<4, GATHER>), grid, dim3(256), 0, st, a); break;
+            }
+            return launch_status(what);
+        }
         bool ok = a.K % 8 == 0;
         if (GATHER) ok = ok && a.Hq % MB_N == 0 && a.HD % 8 == 0 && a.Nm % 8 == 0;
         else ok = ok && a.ldx % 8 == 0 && ((uintptr_t)a.X & 15) == 0;

@@ -34,11 +34,17 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __uint_as_float(((uint32_t)h) << 16);
 }
 
+// Round to nearest-even with gfx950's v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);  // quiet NaN
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// two floats -> packed bf16 pair (low = a), one conversion instruction
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
 template <typename T> struct Cvt;
@@ -100,8 +106,58 @@ template <typename T16> struct Vec8_16 {
         *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
     }
 };
-template <> struct Vec8<bf16_t> : Vec8_16<bf16_t> {};
+template <> struct Vec8<bf16_t> : Vec8_16<bf16_t> {
+    __device__ __forceinline__ static void store(bf16_t* p, const float v[8]) {
+        *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                  pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+    }
+};
 template <> struct Vec8<f16_t> : Vec8_16<f16_t> {};
+
+// EPL contiguous elements of one row, moved as 4- or 8-byte words (the
+// caller guarantees 4-byte alignment of p for 16-bit types, 8 for fp32).
+template <typename T, int EPL>
+struct RowIO {
+    __device__ __forceinline__ static void load(const T* p, float v[EPL]) {
+        if constexpr (sizeof(T) == 2 && EPL % 2 == 0) {
+#pragma unroll
+            for (int k = 0; k < EPL / 2; ++k) {
+                const uint32_t w = reinterpret_cast<const uint32_t*>(p)[k];
+                T lo{(uint16_t)(w & 0xffffu)}, hi{(uint16_t)(w >> 16)};
+                v[2 * k] = ld(&lo);
+                v[2 * k + 1] = ld(&hi);
+            }
+        } else if constexpr (sizeof(T) == 4 && EPL % 2 == 0) {
+#pragma unroll
+            for (int k = 0; k < EPL / 2; ++k) {
+                const float2 w = reinterpret_cast<const float2*>(p)[k];
+                v[2 * k] = w.x;
+                v[2 * k + 1] = w.y;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) v[k] = ld(p + k);
+        }
+    }
+    __device__ __forceinline__ static void store(T* p, const float v[EPL]) {
+        if constexpr (sizeof(T) == 2 && EPL % 2 == 0) {
+#pragma unroll
+            for (int k = 0; k < EPL / 2; ++k) {
+                T lo, hi;
+                st(&lo, v[2 * k]);
+                st(&hi, v[2 * k + 1]);
+                reinterpret_cast<uint32_t*>(p)[k] = (uint32_t)lo.x | ((uint32_t)hi.x << 16);
+            }
+        } else if constexpr (sizeof(T) == 4 && EPL % 2 == 0) {
+#pragma unroll
+            for (int k = 0; k < EPL / 2; ++k)
+                reinterpret_cast<float2*>(p)[k] = make_float2(v[2 * k], v[2 * k + 1]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) st(p + k, v[k]);
+        }
+    }
+};
 
 // ------------------------------------------------------------------ fast math
 // Built directly on the gfx950 transcendental instructions (v_exp_f32 = 2^x,
@@ -137,22 +193,58 @@ __device__ __forceinline__ float fsoftplus(float x) {
 }
 
 // ------------------------------------------------------------------ wave ops
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+// Lane permutations inside a 16-lane DPP row (VALU only, no LDS traffic):
+// quad_perm [1,0,3,2] and [2,3,0,1] pair lanes at distance 1 and 2, the
+// half-row mirror pairs the two quads of each 8-lane half, the row mirror pairs
+// the two halves.  Each is an involution, so after k steps every lane of an
+// aligned group of 2^k lanes holds the group's reduction.
+constexpr int kDppQuad1032 = 0xB1, kDppQuad2301 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+// (every source lane of these permutations lies in the same row, so none is
+// out of range; the "old" operand is the lane's own value regardless)
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    const int b = __builtin_bit_cast(int, v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, CTRL, 0xF, 0xF, false));
 }
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
+
 // sum over aligned groups of G lanes (G a power of two <= 64)
 template <int G>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if constexpr (G >= 2) v += dpp<kDppQuad1032>(v);
+    if constexpr (G >= 4) v += dpp<kDppQuad2301>(v);
+    if constexpr (G >= 8) v += dpp<kDppHalfMirror>(v);
+    if constexpr (G >= 16) v += dpp<kDppMirror>(v);
+    if constexpr (G >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (G >= 64) v += __shfl_xor(v, 32, 64);
     return v;
+}
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (G >= 2) v = fmaxf(v, dpp<kDppQuad1032>(v));
+    if constexpr (G >= 4) v = fmaxf(v, dpp<kDppQuad2301>(v));
+    if constexpr (G >= 8) v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    if constexpr (G >= 16) v = fmaxf(v, dpp<kDppMirror>(v));
+    if constexpr (G >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+    if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
+// whole-wave reductions: rows by DPP, then the four row results by readlane
+__device__ __forceinline__ float wave_sum(float v) {
+    v = group_sum<16>(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
+           __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16)) +
+           __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32)) +
+           __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = group_max<16>(v);
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

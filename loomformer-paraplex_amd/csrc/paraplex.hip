@@ -27,6 +27,29 @@ __device__ __forceinline__ float powlu_gate(float amp, float m) {
     return __builtin_amdgcn_exp2f(expo * flog2(safe)) * sig;
 }
 
+// A = softplus(x) and G(A) for the fused chain.  With t = e^-|x|:
+//   A = max(x,0) + log1p(t)                 (torch's x > 20 -> x falls out: the
+//                                            log1p term is below half an ulp of x)
+//   e^-A = 1/(1 + e^x), so sigmoid(A) = (1+t)/(1+2t) for x >= 0 and
+//   (1+t)/(2+t) for x < 0 -- no second exponential.
+//   log1p(t) = t - t^2/2 + t^3/3 for t < 1/64 (error < t^4/4), log2(1+t) ln2 above.
+// Then G = A^(m/(sqrt A + 1)) * sigmoid(A) with a single reciprocal for both
+// quotients.
+__device__ __forceinline__ void softplus_gate(float x, float m, float& amp, float& gate) {
+    const float t = fexp(-fabsf(x));
+    const float u = 1.0f + t;
+    const float series = t * (1.0f - t * (0.5f - t * (1.0f / 3.0f)));
+    const float l1p = t < 0.015625f ? series : flog2(u) * kLn2;
+    amp = fmaxf(x, 0.0f) + l1p;
+    const float den = x >= 0.0f ? fmaf(2.0f, t, 1.0f) : 2.0f + t;
+    const float safe = fmaxf(amp, 1.0e-12f);
+    const float d1 = fsqrt(safe) + 1.0f;
+    const float r = frcp(d1 * den);
+    const float expo = m * den * r;     // m / (sqrt(A) + 1)
+    const float sig = u * d1 * r;       // sigmoid(A)
+    gate = __builtin_amdgcn_exp2f(expo * flog2(safe)) * sig;
+}
+
 template <typename T, int VEC>
 struct VecIO {
     __device__ __forceinline__ static void load(const T* p, float v[VEC]) {
@@ -66,7 +89,7 @@ paraplex_forward_kernel(const T* __restrict__ p_real, const T* __restrict__ gate
     const int64_t b = rest / nchunks;
     const int64_t h0 = hv * VEC;
     const int64_t t0 = chunk * TC;
-    const int64_t t1 = t0 + TC < T_ ? t0 + TC : T_;
+    const int n = (int)((t0 + TC < T_ ? t0 + TC : T_) - t0);
 
     float bv[VEC], tw[VEC], prev[VEC];
 #pragma unroll
@@ -74,37 +97,61 @@ paraplex_forward_kernel(const T* __restrict__ p_real, const T* __restrict__ gate
         bv[k] = bias[h0 + k];
         tw[k] = trace_w[h0 + k];
     }
+    const int64_t base0 = (b * T_ + t0) * H + h0;
     if (t0 == 0) {
         VecIO<T, VEC>::load(trace + b * H + h0, prev);
     } else {
         float bl[VEC];
-        VecIO<T, VEC>::load(beta_lin + ((b * T_ + t0 - 1) * H + h0), bl);
+        VecIO<T, VEC>::load(beta_lin + base0 - H, bl);
 #pragma unroll
         for (int k = 0; k < VEC; ++k) prev[k] = phase_of(bl[k] + bv[k]);
     }
-    for (int64_t t = t0; t < t1; ++t) {
-        const int64_t base = (b * T_ + t) * H + h0;
-        float r[VEC], g[VEC], bl[VEC], so[VEC], ao[VEC];
-        VecIO<T, VEC>::load(p_real + base, r);
-        VecIO<T, VEC>::load(beta_lin + base, bl);
-        if constexpr (!SAME_GATE) VecIO<T, VEC>::load(gate_src + base, g);
-        const bool rs = reset != nullptr && reset[b * T_ + t] != 0;
+    const T* pr = p_real + base0;
+    const T* pg = gate_src + base0;
+    const T* pb = beta_lin + base0;
+    T* po = act + base0;
+    T* ps = s_out + base0;
+    const uint8_t* prs = reset == nullptr ? nullptr : reset + b * T_ + t0;
+    float r[VEC], g[VEC], bl[VEC];
+    VecIO<T, VEC>::load(pr, r);
+    VecIO<T, VEC>::load(pb, bl);
+    if constexpr (!SAME_GATE) VecIO<T, VEC>::load(pg, g);
+    for (int it = 0; it < n; ++it) {
+        // issue the next token's loads before this token's math
+        float rn[VEC], gn[VEC], bn[VEC];
+        const bool more = it + 1 < n;
+        if (more) {
+            VecIO<T, VEC>::load(pr + H, rn);
+            VecIO<T, VEC>::load(pb + H, bn);
+            if constexpr (!SAME_GATE) VecIO<T, VEC>::load(pg + H, gn);
+        }
+        const bool rs = prs != nullptr && prs[it] != 0;
+        float so[VEC], ao[VEC];
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
             const float s0 = phase_of(bl[k] + bv[k]);
             const float pv = rs ? 0.0f : prev[k];
-            const float raw = s0 + pv * tw[k];
-            const float s = raw * frsq(1.0f + raw * raw);
-            const float amp = fsoftplus(SAME_GATE ? r[k] : g[k]);
-            const float p = r[k] + amp * s;
+            const float raw = fmaf(pv, tw[k], s0);
+            const float s = raw * frsq(fmaf(raw, raw, 1.0f));
+            float amp, gate;
+            softplus_gate(SAME_GATE ? r[k] : g[k], m, amp, gate);
             so[k] = s;
-            ao[k] = p * powlu_gate(amp, m);
+            ao[k] = fmaf(amp, s, r[k]) * gate;
             prev[k] = s0;
         }
-        VecIO<T, VEC>::store(s_out + base, so);
-        VecIO<T, VEC>::store(act + base, ao);
+        VecIO<T, VEC>::store(ps, so);
+        VecIO<T, VEC>::store(po, ao);
+        if (more) {
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) {
+                r[k] = rn[k];
+                bl[k] = bn[k];
+                if constexpr (!SAME_GATE) g[k] = gn[k];
+            }
+        }
+        pr += H; pb += H; pg += H; po += H; ps += H;
     }
-    if (t1 == T_) VecIO<T, VEC>::store(next_trace + b * H + h0, prev);
+    if (t0 + n == T_) VecIO<T, VEC>::store(next_trace + b * H + h0, prev);
 }
 
 template <typename T, int VEC>

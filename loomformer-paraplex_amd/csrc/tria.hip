@@ -346,9 +346,11 @@ __global__ void __launch_bounds__(256)
 final_ca_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
                 int64_t kv_stride_b, const uint8_t* __restrict__ allowed, int64_t allowed_stride,
                 const T* __restrict__ residual, float gamma, T* __restrict__ out,
-                float* __restrict__ lse, int64_t T_, int64_t K, int64_t D, float scale) {
+                float* __restrict__ lse, int64_t T_, int64_t K, const int64_t* __restrict__ k_dev,
+                int64_t D, float scale) {
     __shared__ float wts[kCaMaxK];
     __shared__ float red[2];
+    if (k_dev != nullptr) K = *k_dev < K ? *k_dev : K;   // graph replay: key count on the device
     const int64_t row = blockIdx.x;
     const int64_t b = row / T_;
     const int lane = threadIdx.x & 63;
@@ -477,10 +479,10 @@ template <typename T>
 static int final_ca_dispatch(const void* q, const void* k, const void* v, int64_t kv_stride_b,
                              const uint8_t* allowed, int64_t allowed_stride, const void* residual,
                              float gamma, void* out, float* lse, int64_t B, int64_t T_, int64_t K,
-                             int64_t D, float scale, hipStream_t st) {
+                             const int64_t* k_dev, int64_t D, float scale, hipStream_t st) {
     hipLaunchKernelGGL((final_ca_kernel<T>), dim3((unsigned)(B * T_)), dim3(256), 0, st,
                        (const T*)q, (const T*)k, (const T*)v, kv_stride_b, allowed, allowed_stride,
-                       (const T*)residual, gamma, (T*)out, lse, T_, K, D, scale);
+                       (const T*)residual, gamma, (T*)out, lse, T_, K, k_dev, D, scale);
     return launch_status("loom_final_ca_sparse_forward");
 }
 
@@ -569,21 +571,21 @@ extern "C" int loom_final_ca_sparse_forward(int dtype, const void* q, const void
                kCaMaxK);
     if (B * T == 0) return LOOM_OK;
     LOOM_DTYPE_SWITCH(dtype, final_ca_dispatch, q, k, v, K * D, allowed, K, nullptr, 0.0f, out, lse,
-                      B, T, K, D, scale, (hipStream_t)stream)
+                      B, T, K, nullptr, D, scale, (hipStream_t)stream)
 }
 
 extern "C" int loom_final_ca_sparse_strided(int dtype, const void* q, const void* k, const void* v,
                                             int64_t kv_stride_b, const uint8_t* allowed,
                                             int64_t allowed_stride, const void* residual,
                                             float gamma, void* out, float* lse, int64_t B,
-                                            int64_t T, int64_t K, int64_t D, float scale,
-                                            void* stream) {
+                                            int64_t T, int64_t K, const int64_t* k_dev, int64_t D,
+                                            float scale, void* stream) {
     clear_error();
     LOOM_CHECK(q && k && v && allowed && out, "final_ca_sparse: null tensor argument");
-    LOOM_CHECK(K >= 1 && K <= kCaMaxK, "final_ca_sparse: K=%lld outside [1, %d]", (long long)K,
-               kCaMaxK);
+    LOOM_CHECK(K >= (k_dev ? 0 : 1) && K <= kCaMaxK, "final_ca_sparse: K=%lld outside [1, %d]",
+               (long long)K, kCaMaxK);
     LOOM_CHECK(kv_stride_b >= K * D && allowed_stride >= K, "final_ca_sparse: strides too small");
     if (B * T == 0) return LOOM_OK;
     LOOM_DTYPE_SWITCH(dtype, final_ca_dispatch, q, k, v, kv_stride_b, allowed, allowed_stride,
-                      residual, gamma, out, lse, B, T, K, D, scale, (hipStream_t)stream)
+                      residual, gamma, out, lse, B, T, K, k_dev, D, scale, (hipStream_t)stream)
 }

@@ -38,11 +38,16 @@ SIGNATURES = {
     "loom_final_ca_sparse_forward": [c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64,
                                      c_int64, c_float, _P],
     "loom_final_ca_sparse_strided": [c_int, _P, _P, _P, c_int64, _P, c_int64, _P, c_float, _P,
-                                     _P, c_int64, c_int64, c_int64, c_int64, c_float, _P],
-    "loom_rope_append": [c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64,
+                                     _P, c_int64, c_int64, c_int64, _P, c_int64, c_float, _P],
+    "loom_rope_append": [c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, _P, c_int64, c_int64,
                          c_int64, c_int64, c_int64, _P],
     "loom_gqa_decode_attention": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64,
-                                  c_int64, c_int64, c_int64, c_int64, c_int64, _P],
+                                  c_int64, c_int64, _P, c_int64, c_int64, c_int64, _P],
+    "loom_decode_prologue": [_P, _P, c_int64, c_int64, _P, c_int64, _P, _P, _P, _P, c_int64,
+                             c_int64, c_int64, c_int64, _P],
+    "loom_decode_epilogue": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64,
+                             _P],
+    "loom_argmax_rows": [c_int, _P, c_int64, c_int64, _P, _P],
     "loom_add_layernorm": [c_int, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, _P],
     "loom_tria_decode_temporal": [c_int, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_float,
                                   _P],

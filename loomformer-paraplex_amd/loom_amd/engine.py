@@ -9,12 +9,20 @@ buffers; torch provides the device memory, the embedding row gather and the
 argmax.  Activations and weight matrices are in ``dtype`` (bf16 or fp32);
 biases, LayerNorm parameters and the rotary tables stay fp32.
 
+The per-step state that changes with the position (position, KV length,
+final-CA key count, fire / reset / pending flags, the token ids) lives on the
+device, so one step is a fixed sequence of launches.  ``generate`` captures
+that sequence once in a HIP graph (``torch.cuda.CUDAGraph``) and replays it
+for every position after the first: the host issues one graph launch per
+token instead of ~300 kernel launches.
+
 Layouts (all device-resident, allocated once):
   k_cache/v_cache [L, B, max_len, KVH, HD]    KV cache (preallocated, no wrap)
   hist            [B, 2L, 2N]                 depth history, row s = [k_s | v_s]
   trace           [L, B, H]                   previous-token phase per layer
-  doc             [2, B, H, 3, 3]             temporal carry (ping-pong)
+  doc             [B, H, 3, 3]                temporal carry (updated in place)
   ca_k/ca_v       [B, max_keys, N], ca_valid [B, max_keys]   final-CA keys
+  tokens          [B, max_len]                token fed at each position
 """
 from __future__ import annotations
 
@@ -96,14 +104,24 @@ class LoomDecoder:
         self.v_cache = z(L, B, self.max_len, c.KVH, c.HD)
         self.hist = z(B, 2 * L, 2 * N)
         self.trace = z(L, B, H)
-        self.doc = z(2, B, H, 3, 3)
-        self.max_keys = max(1, self.max_len // max(1, c.window) + 1)
+        self.doc = z(B, H, 3, 3)
+        # final-CA key slots: one per hard fire (every `window` tokens); with an
+        # explicit <CARRY> id any position may fire
+        if carry_token_id is None:
+            self.max_keys = max(1, self.max_len // max(1, c.window) + 1)
+        else:
+            self.max_keys = min(self.max_len, 1024)
         self.ca_k = z(B, self.max_keys, N)
         self.ca_v = z(B, self.max_keys, N)
         self.ca_valid = z(B, self.max_keys, dtype=torch.uint8)
         self.pending = z(B, dtype=torch.uint8)
         self.reset_now = z(B, dtype=torch.uint8)
         self.fire = z(B, dtype=torch.uint8)
+        self.pos_dev = z(1, dtype=torch.int64)
+        self.ca_len = z(1, dtype=torch.int64)
+        self.ids = z(B, dtype=torch.int64)
+        self.tokens = z(B, self.max_len, dtype=torch.int64)
+        self.prompt_buf = z(B, self.max_len, dtype=torch.int64)
         ws = self.lib.loom_gqa_workspace_bytes(B, self.max_len, c.QH, c.KVH, c.HD)
         self.ws = torch.empty((ws + 3) // 4, dtype=torch.float32, device=dev)
         self.ws_bytes = ws
@@ -128,13 +146,13 @@ class LoomDecoder:
         self.pooled = z(B, 9)
         self.z32 = z(B, 32)
         self.a_t = z(B, N)
+        self.stage_k = z(B, N)
+        self.stage_v = z(B, N)
         self.q_ca = z(B, N)
         self.logits = z(B, c.V)
         self.snap = torch.empty((), dtype=torch.float32, device=dev)
         self.pos = 0
-        self.has_doc = False
-        self.doc_cur = 0
-        self.ca_len = 0
+        self._graphs: Dict[int, torch.cuda.CUDAGraph] = {}
 
     # ------------------------------------------------------------------ helpers
 
@@ -152,29 +170,28 @@ class LoomDecoder:
                    float(gate_alpha), _P(residual), _P(out), ldc or Nout, M, Nout, K, self._stream())
 
     def reset(self) -> None:
+        """Forget all sequence state (Model.step at pos 0 starts afresh)."""
         self.pos = 0
-        self.has_doc = False
-        self.ca_len = 0
         self.trace.zero_()
         self.pending.zero_()
         self.ca_valid.zero_()
+        self.ca_len.zero_()
+        self.pos_dev.zero_()
 
-    # ------------------------------------------------------------------ step
+    # ------------------------------------------------------------------ the step
 
-    @torch.no_grad()
-    def step(self, ids: torch.Tensor, pos: int) -> torch.Tensor:
-        """Advance every sequence by one token at position ``pos``; returns logits [B, V]."""
+    def _launch_step(self, first: bool, prompt_len: int) -> None:
+        """Enqueue one Model.step for position *pos_dev (device-resident).  `first`
+        selects the position-0 variant (no seed, no previous temporal state)."""
         c, B, N, H, L = self.cfg, self.B, self.cfg.N, self.cfg.H, self.cfg.L
         st = self._stream()
-        if pos == 0:
-            self.reset()
-        if pos != self.pos:
-            raise ValueError(f"step expects position {self.pos}, got {pos}")
-        if pos >= self.max_len:
-            raise ValueError(f"generation exceeded seq_len={self.max_len}; no wraparound support")
-        torch.index_select(self.emb, 0, ids.to(self.dev).view(-1), out=self.h)
-        S2 = 2 * L
-        hist_ld = S2 * 2 * N
+        carry_id = -1 if self.carry_token_id is None else int(self.carry_token_id)
+        self._call("loom_decode_prologue", _P(self.ids),
+                   _P(self.prompt_buf) if prompt_len > 0 else None, prompt_len, self.max_len,
+                   _P(self.tokens), self.max_len, _P(self.pos_dev), _P(self.pending), _P(self.fire),
+                   _P(self.reset_now), carry_id, c.window, c.seq_len, B, st)
+        torch.index_select(self.emb, 0, self.ids, out=self.h)
+        hist_ld = 2 * L * 2 * N
         # depth history slot 0: DepthAttn.project(h) (loomformer.py:3973)
         self._linear(self.h, self.kvw, self.hist[:, 0], B, 2 * N, N, ldc=hist_ld)
         sub = 0
@@ -182,17 +199,17 @@ class LoomDecoder:
         cache_st = c.KVH * c.HD
         carry_i = None          # index of the current depth carry in self.carry
         p_i = None              # index of the gate output p feeding the next block
-        seed = self.has_doc
         for bi, blk in enumerate(self.blocks):
             last = bi == L - 1
             kc, vc = self.k_cache[bi], self.v_cache[bi]
             # ---- attention step (loomformer.py:3300-3332)
             self._linear(self.h, blk["qkv"], self.qkv, B, N + 2 * c.KV, N)
             self._call("loom_rope_append", self.code, _P(self.qkv), _P(self.q), _P(kc), _P(vc),
-                       _P(self.cos), _P(self.sin), B, pos, c.QH, c.KVH, c.HD, cache_sb, cache_st, st)
+                       _P(self.cos), _P(self.sin), B, 0, _P(self.pos_dev), c.QH, c.KVH, c.HD,
+                       cache_sb, cache_st, st)
             self._call("loom_gqa_decode_attention", self.code, _P(self.q), _P(kc), _P(vc), cache_sb,
-                       cache_st, _P(self.c), _P(self.kctx), _P(self.ws), self.ws_bytes, B, pos + 1,
-                       c.QH, c.KVH, c.HD, st)
+                       cache_st, _P(self.c), _P(self.kctx), _P(self.ws), self.ws_bytes, B,
+                       self.max_len, _P(self.pos_dev), c.QH, c.KVH, c.HD, st)
             self._linear(self.c, blk["o"], self.attn_out, B, N, N)
             # ---- depth read 2*bi, LayerNorm, history slot (loomformer.py:3999-4004)
             self._depth(sub, self.d)
@@ -222,10 +239,10 @@ class LoomDecoder:
             gate = not last
             new_p = (0 if p_i != 0 else 1) if gate else None
             prev = None if carry_i is None else self.carry[carry_i]
-            use_seed = bi == 0 and seed
+            use_seed = bi == 0 and not first
             self._call("loom_tria_depth_forward", self.code, _P(self.R), _P(self.s), _P(self.act),
                        _P(prev) if not use_seed else None,
-                       _P(self.doc[self.doc_cur]) if use_seed else None,
+                       _P(self.doc) if use_seed else None,
                        _P(self.pending) if use_seed else None,
                        _P(blk["gate_w"]) if gate else None, _P(self.carry[out_i]),
                        _P(self.p[new_p]) if gate else None, None, B, 1, H, float(c.tria_alpha),
@@ -237,53 +254,33 @@ class LoomDecoder:
             if not last:
                 sub += 1
                 self._linear(self.h, self.kvw, self.hist[:, sub], B, 2 * N, N, ldc=hist_ld)
-        # ---- temporal carry, fire, PolARM (loomformer.py:4053-4085)
-        hard_fire = (pos + 1 < c.seq_len) and ((pos + 1) % c.window == 0)
-        if self.carry_token_id is not None:
-            explicit = ids.to(self.dev).view(-1).eq(int(self.carry_token_id))
-            fire_t = explicit | hard_fire
-            any_fire = bool(fire_t.any())          # host sync, as tria.py:1576
-            self.fire.copy_(fire_t)
-        else:
-            any_fire = hard_fire
-            self.fire.fill_(1 if hard_fire else 0)
-        if pos == 0:
-            self.reset_now.fill_(1)
-        else:
-            self.reset_now.copy_(self.pending)
-        nxt = 1 - self.doc_cur
+        # ---- temporal carry + PolARM on fires (loomformer.py:4053-4085), in place
         self._call("loom_tria_decode_temporal", self.code, _P(self.carry[carry_i]),
-                   _P(self.doc[self.doc_cur]) if self.has_doc else None,
-                   _P(self.reset_now) if self.has_doc else None,
-                   _P(self.fire) if any_fire else None, _P(self.doc[nxt]), B, H,
-                   float(c.polarm_beta), 1e-6, st)
-        self.doc_cur = nxt
-        self.has_doc = True
+                   None if first else _P(self.doc), None if first else _P(self.reset_now),
+                   _P(self.fire), _P(self.doc), B, H, float(c.polarm_beta), 1e-6, st)
         # ---- readout TriaAggregator (tria.py:1436-1441)
-        self._call("loom_slot_attention_pool_forward", self.code, _P(self.doc[nxt]), _P(self.score_w),
+        self._call("loom_slot_attention_pool_forward", self.code, _P(self.doc), _P(self.score_w),
                    _P(self.pooled), None, B, H, st)
         self._linear(self.pooled, self.proj_w, self.z32, B, 32, 9, bias=self.proj_b)
         self._linear(self.z32, self.up_w, self.a_t, B, N, 32, bias=self.up_b)
-        # ---- final cross-attention step (tria.py:1560-1595)
-        if any_fire:
-            if self.ca_len >= self.max_keys:
-                raise ValueError("final-CA key cache is full")
-            self._linear(self.a_t, self.wqk, self.ca_k[:, self.ca_len], B, N, N, ldc=self.max_keys * N)
-            self._linear(self.a_t, self.wv, self.ca_v[:, self.ca_len], B, N, N, ldc=self.max_keys * N)
-            self.ca_valid[:, self.ca_len].copy_(self.fire)
-            self.ca_len += 1
-        h_out = self.h
-        if self.ca_len > 0:
-            self._linear(self.h, self.wqk, self.q_ca, B, N, N)
-            self._call("loom_final_ca_sparse_strided", self.code, _P(self.q_ca), _P(self.ca_k),
-                       _P(self.ca_v), self.max_keys * N, _P(self.ca_valid), self.max_keys,
-                       _P(self.h), float(self.gamma), _P(self.h2), None, B, 1, self.ca_len, N,
-                       float(N ** -0.5), st)
-            h_out = self.h2
-        self._linear(h_out, self.head, self.logits, B, c.V, N)
-        self.pending.copy_(self.fire)
-        self.pos = pos + 1
-        return self.logits
+        # ---- final cross-attention step (tria.py:1560-1595): stage k/v, append on
+        # fire (+ end-of-step bookkeeping), then attend over the appended keys
+        self._linear(self.a_t, self.wqk, self.stage_k, B, N, N)
+        self._linear(self.a_t, self.wv, self.stage_v, B, N, N)
+        self._call("loom_decode_epilogue", self.code, _P(self.stage_k), _P(self.stage_v),
+                   _P(self.ca_k), _P(self.ca_v), _P(self.ca_valid), _P(self.ca_len), _P(self.fire),
+                   _P(self.pending), _P(self.pos_dev), B, N, self.max_keys, st)
+        self._linear(self.h, self.wqk, self.q_ca, B, N, N)
+        self._call("loom_final_ca_sparse_strided", self.code, _P(self.q_ca), _P(self.ca_k),
+                   _P(self.ca_v), self.max_keys * N, _P(self.ca_valid), self.max_keys,
+                   _P(self.h), float(self.gamma), _P(self.h2), None, B, 1, self.max_keys,
+                   _P(self.ca_len), N, float(N ** -0.5), st)
+        self._linear(self.h2, self.head, self.logits, B, c.V, N)
+
+    def _argmax(self) -> None:
+        """ids = argmax(logits) per row (infer's greedy pick, loomformer.py:5306)."""
+        self._call("loom_argmax_rows", self.code, _P(self.logits), self.B, self.cfg.V, _P(self.ids),
+                   self._stream())
 
     def _depth(self, sub: int, out: torch.Tensor) -> None:
         """DepthAttn read over history slots [0, sub] (loomformer.py:3404-3429, tensor branch)."""
@@ -293,26 +290,99 @@ class LoomDecoder:
                    _P(self.hist[:, :, N:]), hist_bt, 2 * N, _P(out), None, None, self.B, sub + 1,
                    c.QH, c.HD, self._stream())
 
+    def _check_capacity(self, pos: int) -> None:
+        if pos >= self.max_len:
+            raise ValueError(f"generation exceeded seq_len={self.max_len}; no wraparound support")
+        # hard fires up to and including `pos`: multiples of W in [1, min(pos+1, seq_len-1)]
+        fires = min(pos + 1, self.cfg.seq_len - 1) // self.cfg.window
+        if self.carry_token_id is None and fires > self.max_keys:
+            raise ValueError("final-CA key cache is full")
+
     @torch.no_grad()
-    def generate(self, prompt: torch.Tensor, n_new: int, return_logits: bool = False):
-        """Token-by-token prefill of ``prompt`` [B, P] then ``n_new`` greedy tokens."""
+    def step(self, ids: torch.Tensor, pos: int) -> torch.Tensor:
+        """Advance every sequence by one token at position ``pos`` (eager launches);
+        returns logits [B, V]."""
+        if pos == 0:
+            self.reset()
+        if pos != self.pos:
+            raise ValueError(f"step expects position {self.pos}, got {pos}")
+        self._check_capacity(pos)
+        self.ids.copy_(ids.to(self.dev).view(-1))
+        self._launch_step(first=pos == 0, prompt_len=0)
+        self.pos = pos + 1
+        return self.logits
+
+    # ------------------------------------------------------------------ generation
+
+    def _graph_for(self, prompt_len: int) -> torch.cuda.CUDAGraph:
+        """Capture argmax -> ids, then one step for a position >= 1, reading the
+        prompt while pos < prompt_len."""
+        g = self._graphs.get(prompt_len)
+        if g is None:
+            torch.cuda.synchronize(self.dev)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._argmax()
+                self._launch_step(first=False, prompt_len=prompt_len)
+            self._graphs[prompt_len] = g
+        return g
+
+    @torch.no_grad()
+    def generate(self, prompt: torch.Tensor, n_new: int, return_logits: bool = False,
+                 use_graph: bool = True):
+        """Token-by-token prefill of ``prompt`` [B, P], then ``n_new`` greedy tokens
+        (the reference's infer loop).  Returns the new ids [B, n_new] (and the logits
+        after every step [B, P + n_new, V] with return_logits)."""
         B, P = prompt.shape
         if B != self.B:
             raise ValueError(f"prompt batch {B} != engine batch {self.B}")
-        prompt = prompt.to(self.dev)
+        if P < 1:
+            raise ValueError("prompt must hold at least one token")
+        total = P + n_new
+        self._check_capacity(total - 1)
+        self.reset()
+        self.prompt_buf[:, :P].copy_(prompt.to(self.dev))
         logits_all = [] if return_logits else None
-        logits = None
-        for pos in range(P):
-            logits = self.step(prompt[:, pos], pos)
+        self._launch_step(first=True, prompt_len=P)
+        if return_logits:
+            logits_all.append(self.logits.float().clone())
+        graph = self._graph_for(P) if use_graph else None
+        for _ in range(1, total):
+            if graph is not None:
+                graph.replay()
+            else:
+                self._argmax()
+                self._launch_step(first=False, prompt_len=P)
             if return_logits:
-                logits_all.append(logits.float().clone())
-        out = torch.empty(B, n_new, dtype=torch.long, device=self.dev)
-        for i in range(n_new):
-            nxt = torch.argmax(logits, dim=-1)
-            out[:, i] = nxt
-            logits = self.step(nxt, P + i)
-            if return_logits:
-                logits_all.append(logits.float().clone())
+                logits_all.append(self.logits.float().clone())
+        self.pos = total
+        out = self.tokens[:, P:total].clone()
         if return_logits:
             return out, torch.stack(logits_all, 1)
         return out
+
+    @torch.no_grad()
+    def start(self, prompt: torch.Tensor) -> None:
+        """Reset, load ``prompt`` [B, P] and run position 0 (eager)."""
+        B, P = prompt.shape
+        if B != self.B or P < 1:
+            raise ValueError("prompt must be [batch, >=1]")
+        self.reset()
+        self.prompt_buf[:, :P].copy_(prompt.to(self.dev))
+        self._prompt_len = P
+        self._launch_step(first=True, prompt_len=P)
+        self.pos = 1
+
+    @torch.no_grad()
+    def replay_steps(self, n: int) -> None:
+        """Advance ``n`` positions with the captured step (prompt tokens while
+        pos < P, greedy argmax after)."""
+        self._check_capacity(self.pos + n - 1)
+        g = self._graph_for(self._prompt_len)
+        for _ in range(n):
+            g.replay()
+        self.pos += n
+
+    def generated(self) -> torch.Tensor:
+        """Greedy tokens produced so far (positions >= P)."""
+        return self.tokens[:, self._prompt_len:self.pos]

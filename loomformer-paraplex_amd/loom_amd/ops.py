@@ -79,8 +79,10 @@ def paraplex_forward(p_real, gate_src, beta_linear, bias, trace, trace_w, reset,
     nxt = torch.empty(B, H, dtype=pc.dtype, device=dev)
     snap = torch.empty(anchor.shape, dtype=torch.float32, device=dev)
     rc = reset.contiguous() if reset.numel() else None
-    call("loom_paraplex_forward", dtype_code(pc), ptr(pc), ptr(gc), ptr(bc), ptr(bias.contiguous()),
-         ptr(trace.contiguous()), ptr(trace_w.contiguous()), ptr(rc), ptr(anchor.contiguous()),
+    # contiguous copies are bound to names so they outlive the asynchronous launch
+    bias_c, trace_c, tw_c, anchor_c = (t.contiguous() for t in (bias, trace, trace_w, anchor))
+    call("loom_paraplex_forward", dtype_code(pc), ptr(pc), ptr(gc), ptr(bc), ptr(bias_c),
+         ptr(trace_c), ptr(tw_c), ptr(rc), ptr(anchor_c),
          ptr(act), ptr(s), ptr(nxt), ptr(snap), B, T, H, float(m), stream_of(pc))
     return [act, s, nxt, snap]
 
@@ -245,8 +247,9 @@ def _tria_call(r, i, o, prev, seed, valid, w, want_scale, alpha, axis, want_carr
     carry = torch.empty(B, T, H, 3, 3, dtype=r.dtype, device=r.device) if want_carry else None
     p = torch.empty_like(rc) if w is not None else None
     scale = torch.empty(n, dtype=torch.float32, device=r.device) if want_scale else None
-    call("loom_tria_depth_forward", dtype_code(rc), ptr(rc), ptr(ic), ptr(oc), ptr(_c(prev)),
-         ptr(_c(seed)), ptr(_c(valid)), ptr(_c(w)), ptr(carry), ptr(p), ptr(scale), B, T, H,
+    prev_c, seed_c, valid_c, w_c = _c(prev), _c(seed), _c(valid), _c(w)
+    call("loom_tria_depth_forward", dtype_code(rc), ptr(rc), ptr(ic), ptr(oc), ptr(prev_c),
+         ptr(seed_c), ptr(valid_c), ptr(w_c), ptr(carry), ptr(p), ptr(scale), B, T, H,
          float(alpha), int(axis), stream_of(rc))
     return carry, p, scale
 
@@ -325,7 +328,8 @@ def gate_slot_mix_forward(carry, w):
     _check(w.numel() == 9, f"{name}: w must have exactly 9 elements")
     cc = carry.contiguous()
     p = torch.empty(cc.shape[:-2], dtype=cc.dtype, device=cc.device)
-    call("loom_gate_slot_mix_forward", dtype_code(cc), ptr(cc), ptr(w.contiguous()), ptr(p),
+    wc = w.contiguous()
+    call("loom_gate_slot_mix_forward", dtype_code(cc), ptr(cc), ptr(wc), ptr(p),
          cc.numel() // 9, stream_of(cc))
     return p
 
@@ -341,7 +345,8 @@ def slot_attention_pool_forward(carry, score_w):
     cc = carry.contiguous()
     pooled = torch.empty(B, T, 9, dtype=cc.dtype, device=cc.device)
     lse = torch.empty(B, T, dtype=cc.dtype, device=cc.device)
-    call("loom_slot_attention_pool_forward", dtype_code(cc), ptr(cc), ptr(score_w.contiguous()),
+    sw = score_w.contiguous()
+    call("loom_slot_attention_pool_forward", dtype_code(cc), ptr(cc), ptr(sw),
          ptr(pooled), ptr(lse), B * T, H, stream_of(cc))
     return [pooled, lse]
 
@@ -358,7 +363,8 @@ def temporal_carry_forward(depth_carry, reset_mask):
     dc = depth_carry.contiguous()
     doc = torch.empty(dc.shape, dtype=torch.float32, device=dc.device)
     scale = torch.empty(B, T, H, dtype=torch.float32, device=dc.device)
-    call("loom_temporal_carry_forward", dtype_code(dc), ptr(dc), ptr(reset_mask.contiguous()),
+    rm = reset_mask.contiguous()
+    call("loom_temporal_carry_forward", dtype_code(dc), ptr(dc), ptr(rm),
          ptr(doc), ptr(scale), B, T, H, stream_of(dc))
     return [doc, scale]
 
@@ -385,7 +391,8 @@ def temporal_carry_endpoint_forward(depth, reset, initial, initial_valid):
     dc = depth.contiguous()
     ep = torch.empty(B, H, 3, 3, dtype=dc.dtype, device=dc.device)
     ep32 = torch.empty(B, H, 3, 3, dtype=torch.float32, device=dc.device)
-    call("loom_temporal_carry_endpoint_forward", dtype_code(dc), ptr(dc), ptr(reset.contiguous()),
+    rs = reset.contiguous()
+    call("loom_temporal_carry_endpoint_forward", dtype_code(dc), ptr(dc), ptr(rs),
          ptr(init_c), ptr(valid_c), ptr(ep), ptr(ep32), B, T, H, stream_of(dc))
     return [ep, ep32]
 
@@ -403,11 +410,11 @@ def final_ca_sparse_forward(q, k, v, allowed, scale: float):
     B, T, D = q.shape
     K = k.shape[1]
     _check(0 < K <= 256, "final CA: expected 1..256 sparse keys")
-    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    qc, kc, vc, ac = q.contiguous(), k.contiguous(), v.contiguous(), allowed.contiguous()
     out = torch.empty_like(qc)
     lse = torch.empty(B, T, dtype=torch.float32, device=q.device)
     call("loom_final_ca_sparse_forward", dtype_code(qc), ptr(qc), ptr(kc), ptr(vc),
-         ptr(allowed.contiguous()), ptr(out), ptr(lse), B, T, K, D, float(scale), stream_of(qc))
+         ptr(ac), ptr(out), ptr(lse), B, T, K, D, float(scale), stream_of(qc))
     return [out, lse]
 
 
@@ -420,7 +427,8 @@ def polarm(matrix: torch.Tensor, beta: float = 0.1, eps: float = 1e-6,
     out = torch.empty_like(mc)
     n = mc.numel() // 9
     per = n // mc.shape[0] if mask is not None else 1
-    call("loom_polarm_forward", dtype_code(mc), ptr(mc), ptr(out), ptr(_c(mask)), n, per,
+    mk = _c(mask)
+    call("loom_polarm_forward", dtype_code(mc), ptr(mc), ptr(out), ptr(mk), n, per,
          float(beta), float(eps), stream_of(mc))
     return out
 

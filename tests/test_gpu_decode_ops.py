@@ -1,0 +1,182 @@
+"""GPU parity of the decode-step kernels against fp32 references (oracle ops
+or plain torch on the CPU)."""
+import math
+
+import pytest
+import torch
+
+from oracle import ops as ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TOL = {torch.float32: dict(rtol=1e-3, atol=1e-4), torch.bfloat16: dict(rtol=2e-2, atol=1e-2)}
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+
+
+def L():
+    from loom_amd import _lib
+    return _lib
+
+
+def P(t):
+    return L().ptr(t)
+
+
+def S(t):
+    return L().stream_of(t)
+
+
+def code(t):
+    return L().dtype_code(t)
+
+
+def host(t):
+    return t.detach().float().cpu()
+
+
+def check(got, want, dtype):
+    torch.testing.assert_close(host(got), want.float(), **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,N", [(32, 768), (3, 32), (5, 20), (1, 2048)])
+def test_add_layernorm(dtype, rows, N):
+    g = torch.Generator().manual_seed(rows + N)
+    a = torch.randn(rows, N, generator=g).to(DEV, dtype)
+    b = torch.randn(rows, N, generator=g).to(DEV, dtype)
+    w = torch.randn(N, generator=g).to(DEV)
+    bb = torch.randn(N, generator=g).to(DEV)
+    out = torch.empty_like(a)
+    L().call("loom_add_layernorm", code(a), P(a), P(b), P(w), P(bb), P(out), rows, N, 1e-5, S(a))
+    want = torch.nn.functional.layer_norm(host(a) + host(b), (N,), host(w), host(bb), 1e-5)
+    check(out, want, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_rope_append(dtype):
+    B, QH, KVH, HD, max_len, pos = 3, 8, 2, 96, 40, 17
+    g = torch.Generator().manual_seed(1)
+    qkv = torch.randn(B, (QH + 2 * KVH) * HD, generator=g).to(DEV, dtype)
+    inv, att = ref.yarn_inv_freq(HD, 10000.0, 4.0, 16, 32.0, 1.0)
+    cos, sin = ref.yarn_cos_sin(inv, att, max_len)
+    kc = torch.zeros(B, max_len, KVH, HD, device=DEV, dtype=dtype)
+    vc = torch.zeros_like(kc)
+    q = torch.empty(B, QH, HD, device=DEV, dtype=dtype)
+    cos_d, sin_d = cos.to(DEV), sin.to(DEV)       # keep the device copies alive across the call
+    L().call("loom_rope_append", code(qkv), P(qkv), P(q), P(kc), P(vc), P(cos_d), P(sin_d),
+             B, pos, None, QH, KVH, HD, max_len * KVH * HD, KVH * HD, S(qkv))
+    x = host(qkv)
+    c, s = cos[pos].view(1, 1, HD), sin[pos].view(1, 1, HD)
+    check(q, ref.apply_rope(x[:, :QH * HD].view(B, QH, HD), c, s), dtype)
+    check(kc[:, pos], ref.apply_rope(x[:, QH * HD:(QH + KVH) * HD].view(B, KVH, HD), c, s), dtype)
+    check(vc[:, pos], x[:, (QH + KVH) * HD:].view(B, KVH, HD), dtype)
+    assert float(host(kc[:, pos + 1]).abs().max()) == 0.0
+    # the position can come from device memory instead (graph replay)
+    pos_d = torch.tensor([pos + 1], dtype=torch.int64, device=DEV)
+    L().call("loom_rope_append", code(qkv), P(qkv), P(q), P(kc), P(vc), P(cos_d), P(sin_d),
+             B, 0, P(pos_d), QH, KVH, HD, max_len * KVH * HD, KVH * HD, S(qkv))
+    c1, s1 = cos[pos + 1].view(1, 1, HD), sin[pos + 1].view(1, 1, HD)
+    check(kc[:, pos + 1], ref.apply_rope(x[:, QH * HD:(QH + KVH) * HD].view(B, KVH, HD), c1, s1), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,QH,KVH,HD,length", [(4, 8, 2, 96, 1), (2, 8, 2, 96, 255), (2, 8, 2, 96, 256),
+                                                 (2, 8, 2, 96, 257), (3, 8, 2, 96, 1000),
+                                                 (3, 4, 2, 8, 37), (2, 4, 1, 64, 300)])
+def test_gqa_decode_attention(dtype, B, QH, KVH, HD, length):
+    from loom_amd import _lib
+    max_len = length + 5
+    g = torch.Generator().manual_seed(length + HD)
+    q = torch.randn(B, QH, HD, generator=g).to(DEV, dtype)
+    kc = torch.randn(B, max_len, KVH, HD, generator=g).to(DEV, dtype)
+    vc = torch.randn(B, max_len, KVH, HD, generator=g).to(DEV, dtype)
+    c = torch.empty(B, QH, HD, device=DEV, dtype=dtype)
+    kx = torch.empty_like(c)
+    nb = _lib.load().loom_gqa_workspace_bytes(B, max_len, QH, KVH, HD)
+    ws = torch.empty(nb // 4 + 1, device=DEV)
+    _lib.call("loom_gqa_decode_attention", code(q), P(q), P(kc), P(vc), max_len * KVH * HD, KVH * HD,
+              P(c), P(kx), P(ws), nb, B, length, None, QH, KVH, HD, S(q))
+    G = QH // KVH
+    K = host(kc)[:, :length].repeat_interleave(G, dim=2).transpose(1, 2)   # [B,QH,len,HD]
+    V = host(vc)[:, :length].repeat_interleave(G, dim=2).transpose(1, 2)
+    a = torch.softmax((host(q).unsqueeze(2) @ K.transpose(-1, -2)) / math.sqrt(HD), dim=-1)
+    check(c, (a @ V).squeeze(2), dtype)
+    check(kx, (a @ K).squeeze(2), dtype)
+    # device-resident length (pos + 1) with the launch covering the whole capacity
+    c.zero_()
+    kx.zero_()
+    pos_d = torch.tensor([length - 1], dtype=torch.int64, device=DEV)
+    _lib.call("loom_gqa_decode_attention", code(q), P(q), P(kc), P(vc), max_len * KVH * HD, KVH * HD,
+              P(c), P(kx), P(ws), nb, B, max_len, P(pos_d), QH, KVH, HD, S(q))
+    check(c, (a @ V).squeeze(2), dtype)
+    check(kx, (a @ K).squeeze(2), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_decode_temporal(dtype):
+    B, H = 4, 300
+    g = torch.Generator().manual_seed(3)
+    depth = ref.local_normalize(torch.randn(B, H, 3, 3, generator=g)).to(DEV, dtype)
+    prev = ref.local_normalize(torch.randn(B, H, 3, 3, generator=g)).to(DEV, dtype)
+    reset = torch.tensor([1, 0, 0, 1], dtype=torch.uint8)
+    fire = torch.tensor([0, 1, 0, 1], dtype=torch.uint8)
+    out = torch.empty_like(depth)
+    reset_d, fire_d = reset.to(DEV), fire.to(DEV)
+    L().call("loom_tria_decode_temporal", code(depth), P(depth), P(prev), P(reset_d),
+             P(fire_d), P(out), B, H, 0.1, 1e-6, S(depth))
+    D, Pv = host(depth), host(prev)
+    doc = torch.where(reset.bool()[:, None, None, None], D, ref.local_normalize(D @ Pv))
+    doc = torch.where(fire.bool()[:, None, None, None], ref.polarm(doc, 0.1), doc)
+    check(out, doc, dtype)
+    # first token: no previous state, no fire -> the depth carry itself
+    L().call("loom_tria_decode_temporal", code(depth), P(depth), None, None, None, P(out), B, H,
+             0.1, 1e-6, S(depth))
+    check(out, D, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_final_ca_strided_with_residual(dtype):
+    B, Kmax, K, D = 3, 9, 4, 96
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(B, 1, D, generator=g).to(DEV, dtype)
+    kb = torch.randn(B, Kmax, D, generator=g).to(DEV, dtype)
+    vb = torch.randn(B, Kmax, D, generator=g).to(DEV, dtype)
+    valid = torch.zeros(B, Kmax, dtype=torch.uint8)
+    valid[0, :3] = 1
+    valid[2, 1] = 1                           # row 1: no key -> output == residual
+    res = torch.randn(B, 1, D, generator=g).to(DEV, dtype)
+    out = torch.empty_like(res)
+    valid_d = valid.to(DEV)
+    L().call("loom_final_ca_sparse_strided", code(q), P(q), P(kb), P(vb), Kmax * D, P(valid_d),
+             Kmax, P(res), 0.7, P(out), None, B, 1, K, None, D, D ** -0.5, S(q))
+    att = ref.final_ca_sparse(host(q), host(kb)[:, :K], host(vb)[:, :K], valid[:, None, :K].bool(), D ** -0.5)
+    check(out, host(res) + 0.7 * att, dtype)
+    # key count from the device: K keys, and 0 keys (exact identity)
+    for kd in (K, 0):
+        k_d = torch.tensor([kd], dtype=torch.int64, device=DEV)
+        L().call("loom_final_ca_sparse_strided", code(q), P(q), P(kb), P(vb), Kmax * D, P(valid_d),
+                 Kmax, P(res), 0.7, P(out), None, B, 1, Kmax, P(k_d), D, D ** -0.5, S(q))
+        if kd == 0:
+            assert torch.equal(out.cpu(), res.cpu())
+        else:
+            check(out, host(res) + 0.7 * att, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_argmax_rows_first_index_on_ties(dtype):
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(33, 4096, generator=g)
+    x[3, 100] = x[3, 4000] = 50.0           # tie: first index wins
+    x[7, :] = 1.0                           # all equal -> 0
+    xd = x.to(DEV, dtype)
+    ids = torch.empty(33, dtype=torch.int64, device=DEV)
+    L().call("loom_argmax_rows", code(xd), P(xd), 33, 4096, P(ids), S(xd))
+    assert torch.equal(ids.cpu(), torch.argmax(host(xd), dim=-1))
+    assert int(ids[3]) == 100 and int(ids[7]) == 0

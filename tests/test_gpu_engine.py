@@ -48,6 +48,22 @@ def test_tiny_engine_matches_reference(carry):
     assert torch.equal(ids.cpu(), torch.from_numpy(z["greedy" + sfx]))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_graph_replay_equals_eager_launches(dtype):
+    """The captured HIP-graph step and the eager launch sequence give identical
+    logits and tokens (fires at W=8 and per-row <CARRY> ids included)."""
+    from loom_amd.engine import LoomDecoder
+    z = np.load(os.path.join(GOLD, "tiny_decode.npz"))
+    state = {k[3:]: torch.from_numpy(z[k]) for k in z.files if k.startswith("w::")}
+    prompt = torch.from_numpy(z["prompt_carry"])
+    runs = []
+    for use_graph in (False, True):
+        eng = LoomDecoder(_cfg("tiny"), state, batch=3, dtype=dtype, carry_token_id=5)
+        runs.append(eng.generate(prompt, 20, return_logits=True, use_graph=use_graph))
+    assert torch.equal(runs[0][0], runs[1][0])
+    assert torch.equal(runs[0][1], runs[1][1])
+
+
 def test_nano_cpu_reference_greedy_ids_bit_exact_fp32():
     from loom_amd.engine import LoomDecoder
     from loom_amd.weights import init_state_dict
