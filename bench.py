@@ -47,18 +47,32 @@ def log(msg: str) -> None:
 
 
 def timed(fn, iters: int, warmup: int = 3) -> float:
-    """Mean milliseconds per call of fn over `iters` calls (HIP events on the current stream)."""
+    """Mean milliseconds per call of fn over `iters` calls.
+
+    The calls are captured into one HIP graph and the graph replay is bracketed
+    by HIP events on the stream it runs on, so host-side op overhead (output
+    allocation, the ctypes call) cannot starve the GPU between launches and
+    the figure is device time (plus the graph's own node-to-node gaps).
+    """
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(iters):
+            fn()
+    g.replay()                      # first replay uploads the graph
+    torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
-    for _ in range(iters):
-        fn()
+    g.replay()
     e.record()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) / iters
+    ms = s.elapsed_time(e) / iters
+    del g
+    torch.cuda.empty_cache()
+    return ms
 
 
 # ----------------------------------------------------------------------------- e2e

@@ -11,6 +11,7 @@
 // 8 depth slots are formed before any value is read (8 independent K loads in
 // flight per lane), then folded into an fp32 online softmax.
 #include <cmath>
+#include <type_traits>
 
 #include "loom_common.h"
 
@@ -18,74 +19,106 @@ namespace loom {
 
 constexpr int kDepthChunk = 8;
 
+// EPL elements of one row as raw 32-bit words (16-bit types stay packed);
+// EPL is even on every path that uses it.
+template <typename T, int EPL>
+struct RawRow {
+    static constexpr int NW = (int)(sizeof(T) * EPL / 4);
+    uint32_t w[NW];
+    __device__ __forceinline__ void load(const T* p) {
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+        for (int k = 0; k < NW; ++k) w[k] = q[k];
+    }
+    __device__ __forceinline__ void to_float(float v[EPL]) const {
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            if constexpr (sizeof(T) == 4) {
+                v[k] = __uint_as_float(w[k]);
+            } else if constexpr (std::is_same<T, bf16_t>::value) {
+                v[2 * k] = __uint_as_float(w[k] << 16);
+                v[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+            } else {
+                T lo{(uint16_t)(w[k] & 0xffffu)}, hi{(uint16_t)(w[k] >> 16)};
+                v[2 * k] = ld(&lo);
+                v[2 * k + 1] = ld(&hi);
+            }
+        }
+    }
+};
+
 template <typename T, int EPL>
 __global__ void __launch_bounds__(256)
 depth_attn_kernel(const T* __restrict__ q, const T* __restrict__ hk, const T* __restrict__ hv,
                   int64_t sbt, int64_t ss, T* __restrict__ d_out, T* __restrict__ w_out,
-                  float* __restrict__ lse_out, int64_t rows, int S, int QH, float scale) {
+                  float* __restrict__ lse_out, int rows, int S, int QH, float scale) {
     constexpr int HD = EPL * 16;
+    constexpr int C = kDepthChunk;
     const int j = threadIdx.x & 15;
-    const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;
+    const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 4);
     if (row >= rows) return;  // all 16 lanes of a group leave together
-    const int qh = (int)(row % QH);
-    const int64_t bt = row / QH;
+    const int qh = row % QH;
+    const int bt = row / QH;
     const int d0 = j * EPL;
 
     float qv[EPL];
     RowIO<T, EPL>::load(q + qh * HD + d0, qv);
 #pragma unroll
-    for (int k = 0; k < EPL; ++k) qv[k] *= scale;
+    for (int k = 0; k < EPL; ++k) qv[k] *= scale * kLog2e;   // scores in log2 units
 
-    const T* kp = hk + bt * sbt + qh * HD + d0;
-    const T* vp = hv + bt * sbt + qh * HD + d0;
+    const T* kp = hk + (int64_t)bt * sbt + qh * HD + d0;
+    const T* vp = hv + (int64_t)bt * sbt + qh * HD + d0;
     float m = -INFINITY, l = 0.0f, acc[EPL];
 #pragma unroll
     for (int k = 0; k < EPL; ++k) acc[k] = 0.0f;
 
-    for (int s0 = 0; s0 < S; s0 += kDepthChunk) {
-        float sc[kDepthChunk];
+    // the K and V rows of C depth slots are requested together (2C loads in
+    // flight per lane), then scored and folded into the online softmax
+    for (int s0 = 0; s0 < S; s0 += C) {
+        RawRow<T, EPL> kr[C], vr[C];
 #pragma unroll
-        for (int c = 0; c < kDepthChunk; ++c) {
-            if (s0 + c < S) {
-                float kv[EPL];
-                RowIO<T, EPL>::load(kp + (int64_t)(s0 + c) * ss, kv);
-                float dot = 0.0f;
+        for (int c = 0; c < C; ++c) {
+            const int sc_ = s0 + c < S ? s0 + c : S - 1;   // in range; masked below
+            kr[c].load(kp + (int64_t)sc_ * ss);
+            vr[c].load(vp + (int64_t)sc_ * ss);
+        }
+        float sc[C];
 #pragma unroll
-                for (int k = 0; k < EPL; ++k) dot = fmaf(qv[k], kv[k], dot);
-                sc[c] = dot;
-            } else {
-                sc[c] = 0.0f;
-            }
+        for (int c = 0; c < C; ++c) {
+            float kv[EPL];
+            kr[c].to_float(kv);
+            float dot = 0.0f;
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) dot = fmaf(qv[k], kv[k], dot);
+            sc[c] = dot;
         }
         float cmax = -INFINITY;
 #pragma unroll
-        for (int c = 0; c < kDepthChunk; ++c) {
+        for (int c = 0; c < C; ++c) {
             sc[c] = group_sum<16>(sc[c]);
             if (s0 + c < S) cmax = fmaxf(cmax, sc[c]);
         }
         const float m_new = fmaxf(m, cmax);
-        const float corr = fexp(m - m_new);  // exp(-inf) = 0 on the first chunk
+        const float corr = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first chunk
         l *= corr;
 #pragma unroll
         for (int k = 0; k < EPL; ++k) acc[k] *= corr;
 #pragma unroll
-        for (int c = 0; c < kDepthChunk; ++c) {
-            if (s0 + c < S) {
-                const float p = fexp(sc[c] - m_new);
-                float vv[EPL];
-                RowIO<T, EPL>::load(vp + (int64_t)(s0 + c) * ss, vv);
-                l += p;
+        for (int c = 0; c < C; ++c) {
+            float vv[EPL];
+            vr[c].to_float(vv);
+            const float p = s0 + c < S ? __builtin_amdgcn_exp2f(sc[c] - m_new) : 0.0f;
+            l += p;
 #pragma unroll
-                for (int k = 0; k < EPL; ++k) acc[k] = fmaf(p, vv[k], acc[k]);
-            }
+            for (int k = 0; k < EPL; ++k) acc[k] = fmaf(p, vv[k], acc[k]);
         }
         m = m_new;
     }
     const float inv_l = 1.0f / l;
 #pragma unroll
     for (int k = 0; k < EPL; ++k) acc[k] *= inv_l;
-    RowIO<T, EPL>::store(d_out + row * HD + d0, acc);
-    if (lse_out != nullptr && j == 0) lse_out[row] = m + logf(l);
+    RowIO<T, EPL>::store(d_out + (int64_t)row * HD + d0, acc);
+    if (lse_out != nullptr && j == 0) lse_out[row] = (m + flog2(l)) * kLn2;
     if (w_out != nullptr) {
         // weights: recompute each score (one more K read) and normalise
         for (int s = 0; s < S; ++s) {
@@ -95,7 +128,7 @@ depth_attn_kernel(const T* __restrict__ q, const T* __restrict__ hk, const T* __
 #pragma unroll
             for (int k = 0; k < EPL; ++k) dot = fmaf(qv[k], kv[k], dot);
             dot = group_sum<16>(dot);
-            if (j == 0) st(w_out + row * S + s, fexp(dot - m) * inv_l);
+            if (j == 0) st(w_out + (int64_t)row * S + s, __builtin_amdgcn_exp2f(dot - m) * inv_l);
         }
     }
 }
@@ -148,14 +181,17 @@ static int dispatch_depth(const void* q, const void* hk, const void* hv, int64_t
     const int64_t rows = BT * QH;
     const float scale = 1.0f / sqrtf((float)HD);
     const int threads = 256;
-    const bool aligned = ((sbt * (int64_t)sizeof(T)) % 4 == 0) && ((ss * (int64_t)sizeof(T)) % 4 == 0) &&
-                         (((uintptr_t)hk | (uintptr_t)hv | (uintptr_t)q | (uintptr_t)d_out) % 8 == 0);
+    // the vector path moves pairs of elements (4 B for 16-bit types, 8 B for
+    // fp32) and indexes rows with 32-bit integers
+    const bool aligned = sbt % 2 == 0 && ss % 2 == 0 &&
+                         (((uintptr_t)hk | (uintptr_t)hv | (uintptr_t)q | (uintptr_t)d_out) % 8 == 0) &&
+                         rows * 16 < ((int64_t)1 << 31) && BT * sbt < ((int64_t)1 << 62);
     const int epl = (HD % 16 == 0) ? (int)(HD / 16) : 0;
 #define LOOM_DA_CASE(E)                                                                          \
     case E:                                                                                      \
         hipLaunchKernelGGL((depth_attn_kernel<T, E>), dim3((unsigned)ceil_div(rows * 16, threads)), \
                            dim3(threads), 0, stream, (const T*)q, (const T*)hk, (const T*)hv, sbt, \
-                           ss, (T*)d_out, (T*)w_out, lse_out, rows, (int)S, (int)QH, scale);       \
+                           ss, (T*)d_out, (T*)w_out, lse_out, (int)rows, (int)S, (int)QH, scale); \
         return launch_status("loom_depth_attn_forward");
     if (aligned) {
         switch (epl) {

@@ -17,6 +17,9 @@ namespace loom {
 void set_error(const char* fmt, ...);
 void clear_error();
 int launch_status(const char* what);
+// compute units of the current device; threads of `kernel` it keeps resident
+int device_cus();
+int64_t resident_threads(const void* kernel, int block);
 
 #define LOOM_CHECK(cond, ...)            \
     do {                                 \

@@ -6,6 +6,8 @@
 // the only extra HBM read is one beta row per chunk (1/TC overhead).  Loads
 // and stores are whole 16-byte vectors, so a wavefront touches 64*16 = 1 KiB
 // of contiguous memory per tensor and per token.
+#include <type_traits>
+
 #include "loom_common.h"
 
 namespace loom {
@@ -27,28 +29,75 @@ __device__ __forceinline__ float powlu_gate(float amp, float m) {
     return __builtin_amdgcn_exp2f(expo * flog2(safe)) * sig;
 }
 
-// A = softplus(x) and G(A) for the fused chain.  With t = e^-|x|:
-//   A = max(x,0) + log1p(t)                 (torch's x > 20 -> x falls out: the
-//                                            log1p term is below half an ulp of x)
-//   e^-A = 1/(1 + e^x), so sigmoid(A) = (1+t)/(1+2t) for x >= 0 and
-//   (1+t)/(2+t) for x < 0 -- no second exponential.
-//   log1p(t) = t - t^2/2 + t^3/3 for t < 1/64 (error < t^4/4), log2(1+t) ln2 above.
-// Then G = A^(m/(sqrt A + 1)) * sigmoid(A) with a single reciprocal for both
-// quotients.
+// A = softplus(x) and G(A) for the fused chain, from one exponential
+// E = e^min(x, 20):
+//   A = log(1 + E), with the rounding of u = 1 + E put back
+//       (log(u) + (E - (u - 1)) is log1p(E) to a few ulp for every E);
+//       x > 20 -> A = x (torch's softplus threshold): log1p(E) > x for
+//       every x <= 20 and E is capped at e^20, so A = max(x, log1p(E));
+//   e^-A = 1/(1 + e^x), so sigmoid(A) = (1 + E)/(2 + E) = u/(1 + u)
+//       (for x > 20 this is 1 - 5e-10, i.e. 1 in fp32, as torch gives);
+//   G = A^(m/(sqrt A + 1)) * sigmoid(A), with one reciprocal for both
+//       quotients: r = 1/((sqrt A + 1)(1 + u)).
+// No branch and no select on the sign of x.
 __device__ __forceinline__ void softplus_gate(float x, float m, float& amp, float& gate) {
-    const float t = fexp(-fabsf(x));
-    const float u = 1.0f + t;
-    const float series = t * (1.0f - t * (0.5f - t * (1.0f / 3.0f)));
-    const float l1p = t < 0.015625f ? series : flog2(u) * kLn2;
-    amp = fmaxf(x, 0.0f) + l1p;
-    const float den = x >= 0.0f ? fmaf(2.0f, t, 1.0f) : 2.0f + t;
-    const float safe = fmaxf(amp, 1.0e-12f);
+    const float e = x * kLog2e;
+    const float E = __builtin_amdgcn_exp2f(fminf(e, 20.0f * kLog2e));
+    const float u = 1.0f + E;
+    const float a0 = fmaf(flog2(u), kLn2, E - (u - 1.0f));
+    amp = __builtin_amdgcn_fmed3f(x, a0, 3.0e38f);   // max(x, a0) without a NaN-quieting pass
+    const float safe = __builtin_amdgcn_fmed3f(amp, 1.0e-12f, 3.0e38f);
     const float d1 = fsqrt(safe) + 1.0f;
+    const float den = 1.0f + u;
     const float r = frcp(d1 * den);
     const float expo = m * den * r;     // m / (sqrt(A) + 1)
     const float sig = u * d1 * r;       // sigmoid(A)
     gate = __builtin_amdgcn_exp2f(expo * flog2(safe)) * sig;
 }
+
+// VEC elements held as the raw words loaded from memory (16-bit types stay
+// packed, so a prefetched row costs VEC/2 registers instead of VEC).
+template <typename T, int VEC>
+struct RawVec {
+    static constexpr int NW = (int)((sizeof(T) * VEC + 3) / 4);
+    uint32_t w[NW];
+    __device__ __forceinline__ void load(const T* p) {
+        if constexpr (sizeof(T) * VEC % 16 == 0) {
+#pragma unroll
+            for (int k = 0; k < NW / 4; ++k) {
+                const uint4 v = reinterpret_cast<const uint4*>(p)[k];
+                w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
+            }
+        } else if constexpr (sizeof(T) == 4) {
+#pragma unroll
+            for (int k = 0; k < NW; ++k) w[k] = __float_as_uint(p[k]);
+        } else if constexpr (VEC == 1) {
+            w[0] = p->x;                       // one 16-bit element
+        } else {
+            static_assert(sizeof(T) * VEC % 16 == 0, "RawVec: unsupported width");
+        }
+    }
+    __device__ __forceinline__ void to_float(float v[VEC]) const {
+        if constexpr (sizeof(T) == 2 && VEC == 1) {
+            const T one{(uint16_t)w[0]};
+            v[0] = ld(&one);
+            return;
+        }
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            if constexpr (sizeof(T) == 4) {
+                v[k] = __uint_as_float(w[k]);
+            } else if constexpr (std::is_same<T, bf16_t>::value) {
+                v[2 * k] = __uint_as_float(w[k] << 16);
+                v[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+            } else {
+                T lo{(uint16_t)(w[k] & 0xffffu)}, hi{(uint16_t)(w[k] >> 16)};
+                v[2 * k] = ld(&lo);
+                v[2 * k + 1] = ld(&hi);
+            }
+        }
+    }
+};
 
 template <typename T, int VEC>
 struct VecIO {
@@ -70,26 +119,31 @@ struct VecIO {
     }
 };
 
-template <typename T, int VEC, bool SAME_GATE>
+constexpr int kPxPrefetch = 2;   // tokens of R / beta (/ gate_src) in flight per thread
+
+template <typename T, int VEC, bool SAME_GATE, bool HAS_RESET>
 __global__ void __launch_bounds__(256)
 paraplex_forward_kernel(const T* __restrict__ p_real, const T* __restrict__ gate_src,
                         const T* __restrict__ beta_lin, const float* __restrict__ bias,
                         const T* __restrict__ trace, const float* __restrict__ trace_w,
                         const uint8_t* __restrict__ reset, const float* __restrict__ anchor,
                         T* __restrict__ act, T* __restrict__ s_out, T* __restrict__ next_trace,
-                        float* __restrict__ anchor_snap, int64_t B, int64_t T_, int64_t H,
-                        int64_t nchunks, int TC, float m) {
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+                        float* __restrict__ anchor_snap, int B, int T_, int H, int nchunks, int TC,
+                        float m) {
+    constexpr int PF = kPxPrefetch;
+    // 32-bit index math: the host guarantees B*nchunks*(H/VEC) < 2^31
+    const unsigned gid = blockIdx.x * blockDim.x + threadIdx.x;
     if (gid == 0 && anchor_snap != nullptr) anchor_snap[0] = anchor[0];
-    const int64_t HV = H / VEC;
-    if (gid >= B * nchunks * HV) return;
-    const int64_t hv = gid % HV;
-    const int64_t rest = gid / HV;
-    const int64_t chunk = rest % nchunks;
-    const int64_t b = rest / nchunks;
-    const int64_t h0 = hv * VEC;
-    const int64_t t0 = chunk * TC;
-    const int n = (int)((t0 + TC < T_ ? t0 + TC : T_) - t0);
+    const unsigned HV = (unsigned)H / VEC;
+    if (gid >= (unsigned)B * (unsigned)nchunks * HV) return;
+    const unsigned hv = gid % HV;
+    const unsigned rest = gid / HV;
+    const unsigned chunk = rest % (unsigned)nchunks;
+    const unsigned b = rest / (unsigned)nchunks;
+    const int h0 = (int)hv * VEC;
+    const int t0 = (int)chunk * TC;
+    if (t0 >= T_) return;
+    const int n = (t0 + TC < T_ ? t0 + TC : T_) - t0;
 
     float bv[VEC], tw[VEC], prev[VEC];
 #pragma unroll
@@ -97,9 +151,9 @@ paraplex_forward_kernel(const T* __restrict__ p_real, const T* __restrict__ gate
         bv[k] = bias[h0 + k];
         tw[k] = trace_w[h0 + k];
     }
-    const int64_t base0 = (b * T_ + t0) * H + h0;
+    const int64_t base0 = ((int64_t)b * T_ + t0) * H + h0;
     if (t0 == 0) {
-        VecIO<T, VEC>::load(trace + b * H + h0, prev);
+        VecIO<T, VEC>::load(trace + (int64_t)b * H + h0, prev);
     } else {
         float bl[VEC];
         VecIO<T, VEC>::load(beta_lin + base0 - H, bl);
@@ -111,47 +165,54 @@ paraplex_forward_kernel(const T* __restrict__ p_real, const T* __restrict__ gate
     const T* pb = beta_lin + base0;
     T* po = act + base0;
     T* ps = s_out + base0;
-    const uint8_t* prs = reset == nullptr ? nullptr : reset + b * T_ + t0;
-    float r[VEC], g[VEC], bl[VEC];
-    VecIO<T, VEC>::load(pr, r);
-    VecIO<T, VEC>::load(pb, bl);
-    if constexpr (!SAME_GATE) VecIO<T, VEC>::load(pg, g);
-    for (int it = 0; it < n; ++it) {
-        // issue the next token's loads before this token's math
-        float rn[VEC], gn[VEC], bn[VEC];
-        const bool more = it + 1 < n;
-        if (more) {
-            VecIO<T, VEC>::load(pr + H, rn);
-            VecIO<T, VEC>::load(pb + H, bn);
-            if constexpr (!SAME_GATE) VecIO<T, VEC>::load(pg + H, gn);
-        }
-        const bool rs = prs != nullptr && prs[it] != 0;
-        float so[VEC], ao[VEC];
+    const uint8_t* prs = HAS_RESET ? reset + (int64_t)b * T_ + t0 : nullptr;
+    // ring of PF prefetched tokens; slot p holds token it0 + p
+    RawVec<T, VEC> rr[PF], rb[PF], rg[PF];
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) {
-            const float s0 = phase_of(bl[k] + bv[k]);
-            const float pv = rs ? 0.0f : prev[k];
-            const float raw = fmaf(pv, tw[k], s0);
-            const float s = raw * frsq(fmaf(raw, raw, 1.0f));
-            float amp, gate;
-            softplus_gate(SAME_GATE ? r[k] : g[k], m, amp, gate);
-            so[k] = s;
-            ao[k] = fmaf(amp, s, r[k]) * gate;
-            prev[k] = s0;
+    for (int p = 0; p < PF; ++p) {
+        if (p < n) {
+            rr[p].load(pr + (int64_t)p * H);
+            rb[p].load(pb + (int64_t)p * H);
+            if constexpr (!SAME_GATE) rg[p].load(pg + (int64_t)p * H);
         }
-        VecIO<T, VEC>::store(ps, so);
-        VecIO<T, VEC>::store(po, ao);
-        if (more) {
+    }
+    for (int it0 = 0; it0 < n; it0 += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int it = it0 + p;
+            if (it >= n) break;
+            float r[VEC], bl[VEC], g[VEC];
+            rr[p].to_float(r);
+            rb[p].to_float(bl);
+            if constexpr (!SAME_GATE) rg[p].to_float(g);
+            if (it + PF < n) {
+                // issue token it+PF's loads ahead of this token's math, at raised
+                // wave priority so the loads of all waves go out early
+                __builtin_amdgcn_s_setprio(3);
+                rr[p].load(pr + (int64_t)PF * H);
+                rb[p].load(pb + (int64_t)PF * H);
+                if constexpr (!SAME_GATE) rg[p].load(pg + (int64_t)PF * H);
+                __builtin_amdgcn_s_setprio(0);
+            }
+            const bool rs = HAS_RESET && prs[it] != 0;
+            float so[VEC], ao[VEC];
 #pragma unroll
             for (int k = 0; k < VEC; ++k) {
-                r[k] = rn[k];
-                bl[k] = bn[k];
-                if constexpr (!SAME_GATE) g[k] = gn[k];
+                const float s0 = phase_of(bl[k] + bv[k]);
+                const float raw = rs ? s0 : fmaf(prev[k], tw[k], s0);
+                const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
+                float amp, gate;
+                softplus_gate(SAME_GATE ? r[k] : g[k], m, amp, gate);
+                so[k] = sv;
+                ao[k] = fmaf(amp, sv, r[k]) * gate;
+                prev[k] = s0;
             }
+            VecIO<T, VEC>::store(ps, so);
+            VecIO<T, VEC>::store(po, ao);
+            pr += H; pb += H; pg += H; po += H; ps += H;
         }
-        pr += H; pb += H; pg += H; po += H; ps += H;
     }
-    if (t0 + n == T_) VecIO<T, VEC>::store(next_trace + b * H + h0, prev);
+    if (t0 + n == T_) VecIO<T, VEC>::store(next_trace + (int64_t)b * H + h0, prev);
 }
 
 template <typename T, int VEC>
@@ -190,21 +251,29 @@ static int launch_paraplex(const void* p_real, const void* gate_src, const void*
                            const uint8_t* reset, const float* anchor, void* act, void* s,
                            void* next_trace, float* anchor_snap, int64_t B, int64_t T_,
                            int64_t H, float m, hipStream_t stream) {
-    // Tokens per thread: enough threads to fill 256 CUs, and long runs of t
-    // so the carried phase saves most re-reads.
+    // Tokens per thread: the longest run of t that still gives every SIMD at
+    // least 3 waves (enough to hide memory latency behind the math).  Longer
+    // runs mean fewer per-chunk restarts (each recomputes one carried phase).
     const int64_t HV = H / VEC;
-    int TC = 16;
-    while (TC > 1 && B * ceil_div(T_, TC) * HV < 256 * 256 * 4) TC >>= 1;
+    const bool same = gate_src == p_real;
+    auto kern = same ? (reset ? paraplex_forward_kernel<T, VEC, true, true>
+                              : paraplex_forward_kernel<T, VEC, true, false>)
+                     : (reset ? paraplex_forward_kernel<T, VEC, false, true>
+                              : paraplex_forward_kernel<T, VEC, false, false>);
+    const int64_t simds = 4 * (int64_t)device_cus();
+    int TC = 64;
+    while (TC > 1 && B * ceil_div(T_, TC) * HV < 3 * 64 * simds) --TC;
     const int64_t nchunks = ceil_div(T_, TC);
     const int64_t total = B * nchunks * HV;
+    LOOM_CHECK(total < ((int64_t)1 << 31) && T_ < ((int64_t)1 << 31) && H < ((int64_t)1 << 31),
+               "paraplex: %lld x %lld x %lld exceeds the 32-bit thread index", (long long)B,
+               (long long)T_, (long long)H);
     const int threads = 256;
     const int64_t blocks = ceil_div(total, threads);
-    const bool same = gate_src == p_real;
-    auto kern = same ? paraplex_forward_kernel<T, VEC, true> : paraplex_forward_kernel<T, VEC, false>;
     hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(threads), 0, stream,
                        (const T*)p_real, (const T*)gate_src, (const T*)beta_lin, bias,
                        (const T*)trace, trace_w, reset, anchor, (T*)act, (T*)s, (T*)next_trace,
-                       anchor_snap, B, T_, H, nchunks, TC, m);
+                       anchor_snap, (int)B, (int)T_, (int)H, (int)nchunks, TC, m);
     return launch_status("loom_paraplex_forward");
 }
 
