@@ -216,6 +216,17 @@ def copy_bandwidth():
     return 2 * x.numel() * 4 / (ms * 1e-3) / 1e9
 
 
+def measured_traffic():
+    """HBM bytes per launch of the fused kernels, from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes summarised in profiles/ (FETCH scaled by the copy-kernel
+    factor, see the profile texts); empty if the file is absent."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return {k: v["hbm_bytes_per_launch"] for k, v in json.load(f).items()}
+
+
 # ----------------------------------------------------------------------------- cpu
 
 def cpu_baseline(args):
@@ -304,9 +315,16 @@ def main():
             "paraplex_ffn_total_ms": px["ffn_ms"],
             "device_copy_GB/s": copy_gbs,
         }
+        traffic = measured_traffic()
+        for key, name in (("paraplex_forward_kernel_px", "paraplex_pointwise"),
+                          ("depth_attn_kernel_da", "depth_attn"),
+                          ("tria_depth_kernel_step_gate_tr", "tria_step_gate")):
+            kernels[name]["hbm_traffic_bytes"] = traffic.get(key)
         roofline = {"bound": "hbm", "kernel": "paraplex_forward_kernel (PX: 8x1024x3072 bf16)",
                     "achieved": px["pointwise_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": px["pointwise_GBs"] / HBM_PEAK_GBS, "traffic": None}
+                    "frac": px["pointwise_GBs"] / HBM_PEAK_GBS,
+                    "traffic": traffic.get("paraplex_forward_kernel_px"),
+                    "algorithmic_bytes": px["pointwise_bytes"]}
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (oracle on host cores)")
