@@ -217,7 +217,11 @@ int loom_rope_append(int dtype, const void* qkv, void* q_out, void* k_cache, voi
                      const int64_t* pos_dev, int64_t QH, int64_t KVH, int64_t HD,
                      int64_t cache_stride_b, int64_t cache_stride_t, void* stream);
 
-/* Bytes of float workspace loom_gqa_decode_attention needs for len <= max_len. */
+/* Bytes of workspace loom_gqa_decode_attention / loom_gqa_decode_step need for
+ * len <= max_len: a 256-byte-rounded block of B*KVH int32 arrival counters,
+ * then the per-chunk partial records.  The counter block must be zero before
+ * the first call (allocate the workspace zero-filled, 256-byte aligned); every
+ * call leaves it zero again.  Zero it again if B or KVH changes. */
 int64_t loom_gqa_workspace_bytes(int64_t B, int64_t max_len, int64_t QH, int64_t KVH, int64_t HD);
 
 /* Causal GQA attention of one query position over cache positions [0, len):
@@ -226,14 +230,31 @@ int64_t loom_gqa_workspace_bytes(int64_t B, int64_t max_len, int64_t QH, int64_t
  * GroupedQueryCausalSelfAttention.step (loomformer.py:3316-3329) without
  * materialising the GQA repeat: q-head h reads kv head h / (QH/KVH).
  *   q: [B,QH,HD]; caches as in loom_rope_append; c_out, kctx_out: [B,QH,HD]
- *   (dtype); workspace: at least loom_gqa_workspace_bytes(B, len, ...) bytes.
- *   With pos_dev != NULL the length is *pos_dev + 1 (read on the device) and
- *   `len` is the capacity the launch covers. */
+ *   (dtype); workspace: see loom_gqa_workspace_bytes.  With pos_dev != NULL
+ *   the length is *pos_dev + 1 (read on the device) and `len` is the capacity
+ *   the launch covers.  Calls that share a workspace must not overlap. */
 int loom_gqa_decode_attention(int dtype, const void* q, const void* k_cache, const void* v_cache,
                               int64_t cache_stride_b, int64_t cache_stride_t, void* c_out,
                               void* kctx_out, float* workspace, int64_t workspace_bytes,
                               int64_t B, int64_t len, const int64_t* pos_dev, int64_t QH,
                               int64_t KVH, int64_t HD, void* stream);
+
+/* The whole attention part of GroupedQueryCausalSelfAttention.step
+ * (loomformer.py:3300-3329) in one launch, for position pos = len - 1 (or
+ * *pos_dev): rope q and this token's k from the projection row qkv
+ * [B, (QH + 2 KVH) HD] (= [q | k | v], YaRN tables as in loom_rope_append),
+ * append (k_roped, v) at row pos of the caches, and attend over positions
+ * 0..pos as loom_gqa_decode_attention does.  q_out (optional, [B,QH,HD])
+ * receives the roped q, which the Paraplex FFN reads.  c_out / kctx_out rows are
+ * out_stride_b elements apart (>= QH*HD), so they can land inside a wider
+ * row.  Equivalent to loom_rope_append followed by loom_gqa_decode_attention. */
+int loom_gqa_decode_step(int dtype, const void* qkv, void* k_cache, void* v_cache,
+                         int64_t cache_stride_b, int64_t cache_stride_t, const float* cos_table,
+                         const float* sin_table, void* q_out, void* c_out, void* kctx_out,
+                         int64_t out_stride_b,
+                         float* workspace, int64_t workspace_bytes, int64_t B, int64_t len,
+                         const int64_t* pos_dev, int64_t QH, int64_t KVH, int64_t HD,
+                         void* stream);
 
 /* out = LayerNorm(a + b) (b may be NULL) over rows of N <= 2048, fp32 gamma and
  * beta, biased variance.  Replaces ln_attn/ln_ffn(skip + branch)

@@ -44,10 +44,17 @@ rope_append_kernel(const T* __restrict__ qkv, T* __restrict__ q_out, T* __restri
 
 // ------------------------------------------------------------------ GQA attention
 // Split over the sequence (flash-decoding): block (chunk, kvh, b) covers
-// kAttnChunk positions for the G query heads that share kv head kvh and writes
-// an unnormalised partial (m, l, sum p*v, sum p*k) per head; the combine kernel
-// merges the chunks.  One pass over K and V: each cache row is read once and
-// feeds both the scores and the A.K readout.
+// kAttnChunk positions for the G query heads that share kv head kvh and
+// publishes an unnormalised partial record (m, l, sum p*v, sum p*k) per head.
+// One pass over K and V: each cache row is read once and feeds both the
+// scores and the A.K readout.  The last block of each (b, kvh) to finish
+// (a per-(b, kvh) arrival counter in the workspace) merges the records and
+// writes C = A.V and Kctx = A.K_roped; it leaves the counter at zero again.
+//
+// FROM_QKV: q comes unroped from the step's qkv row; the block roped q
+// itself, and the block that holds position pos also ropes this token's k,
+// attends to it from registers and appends (k_roped, v) to the caches
+// (RoPE + cache append + attention + combine in one launch).
 //
 // Mapping: LPR lanes per cache row (EPL = HD/LPR contiguous elements each);
 // the block's NG = 256/LPR row groups take positions t0 + grp + NG*i.  A group
@@ -57,40 +64,92 @@ rope_append_kernel(const T* __restrict__ qkv, T* __restrict__ q_out, T* __restri
 constexpr int kAttnChunk = 256;
 constexpr int kAttnMaxG = 8;
 constexpr int kAttnBatch = 4;
+constexpr int kAttnMerge = 8;     // records loaded together by the merging block
 
-template <typename T, int EPL, int G, int LPR>
+// bytes of the arrival counters at the head of the workspace
+__host__ __device__ inline int64_t gqa_counter_bytes(int64_t B, int64_t KVH) {
+    return (B * KVH * 4 + 255) / 256 * 256;
+}
+
+template <typename T>
+struct GqaArgs {
+    const T* q;            // roped q [B, QH, HD], or the qkv rows [B, (QH + 2 KVH) HD]
+    T* kc;
+    T* vc;
+    int64_t csb, cst;      // cache strides (elements) of b and t
+    const float* cosv;     // FROM_QKV: RoPE tables [*, HD] (attention factor folded in)
+    const float* sinv;
+    T* q_out;              // FROM_QKV, optional: the roped q [B, QH, HD]
+    int* counters;         // [B * KVH], zero between calls
+    float* rec;            // [B, KVH, nchunks, REC]
+    T* c_out;              // [B, QH, HD] with row stride out_sb
+    T* k_out;
+    int64_t out_sb;
+    int64_t len;           // attended positions (ignored when pos_dev is set)
+    const int64_t* pos_dev;
+    int QH, KVH;
+    float qscale;
+};
+
+// element d of head h of a qkv row, roped for position pos (x*cos + rot(x)*sin)
+template <typename T>
+__device__ __forceinline__ float rope_elem(const T* head, const float* cr, const float* sr, int d,
+                                           int HD) {
+    const int half = HD / 2;
+    const float rot = d < half ? -ld(head + d + half) : ld(head + d - half);
+    return ld(head + d) * cr[d] + rot * sr[d];
+}
+
+template <typename T, int EPL, int G, int LPR, bool FROM_QKV>
 __global__ void __launch_bounds__(256)
-gqa_partial_kernel(const T* __restrict__ q, const T* __restrict__ kc, const T* __restrict__ vc,
-                   int64_t cstride_b, int64_t cstride_t, float* __restrict__ ws, int64_t len,
-                   const int64_t* __restrict__ pos_dev, int QH, int KVH, float qscale) {
+gqa_decode_kernel(GqaArgs<T> a) {
     constexpr int HD = EPL * LPR;
     constexpr int NG = 256 / LPR;          // row groups per block
     constexpr int REC = 2 * G + 2 * G * HD;
-    __shared__ float wred[4][2 * G + 2 * G * HD];
+    __shared__ float wred[4][REC];
+    __shared__ int s_last;
     const int chunk = blockIdx.x, kvh = blockIdx.y;
     const int64_t b = blockIdx.z;
     const int nchunks = gridDim.x;
     const int tid = threadIdx.x, j = tid % LPR, grp = tid / LPR;
     const int wave = tid >> 6, lane = tid & 63;
+    const int64_t len = a.pos_dev != nullptr ? *a.pos_dev + 1 : a.len;
+    const int64_t pos = len - 1;
+    const int nact = (int)((len + kAttnChunk - 1) / kAttnChunk);
+    if (chunk >= nact) return;                    // past the end: no record, not counted
     const int64_t t0 = (int64_t)chunk * kAttnChunk;
-    if (pos_dev != nullptr) len = *pos_dev + 1;   // graph replay: length from the device
-    float* rec = ws + (((int64_t)b * KVH + kvh) * nchunks + chunk) * REC;
-    if (t0 >= len) {                              // chunk past the end: empty partial
-        for (int k = tid; k < REC; k += blockDim.x) rec[k] = k < G ? -INFINITY : 0.0f;
-        return;
-    }
     const int64_t t1 = t0 + kAttnChunk < len ? t0 + kAttnChunk : len;
+    // FROM_QKV: the cache holds positions < pos; position pos comes from qkv
+    // and is folded in by the one chunk that contains it
+    const bool holds_pos = FROM_QKV && t1 == len;
+    const int64_t tc = holds_pos ? pos : t1;
     const int d0 = j * EPL;
+    const int QKV = (a.QH + 2 * a.KVH) * HD;
 
     float qv[G][EPL];
+    if constexpr (FROM_QKV) {
+        const T* qrow = a.q + b * QKV;
+        const float* cr = a.cosv + pos * HD;
+        const float* sr = a.sinv + pos * HD;
+        const bool write_q = a.q_out != nullptr && chunk == 0 && grp == 0;
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e)
-            qv[g][e] = ld(q + (b * QH + kvh * G + g) * HD + d0 + e) * qscale;
+            for (int e = 0; e < EPL; ++e) {
+                const float x = rope_elem(qrow + (kvh * G + g) * HD, cr, sr, d0 + e, HD);
+                if (write_q) st(a.q_out + (b * a.QH + kvh * G + g) * HD + d0 + e, x);
+                qv[g][e] = x * a.qscale;
+            }
+    } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < EPL; ++e)
+                qv[g][e] = ld(a.q + (b * a.QH + kvh * G + g) * HD + d0 + e) * a.qscale;
+    }
 
-    const T* kbase = kc + b * cstride_b + kvh * HD + d0;
-    const T* vbase = vc + b * cstride_b + kvh * HD + d0;
+    const T* kbase = a.kc + b * a.csb + kvh * HD + d0;
+    const T* vbase = a.vc + b * a.csb + kvh * HD + d0;
     float m[G], l[G], ac[G][EPL], ak[G][EPL];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -99,50 +158,88 @@ gqa_partial_kernel(const T* __restrict__ q, const T* __restrict__ kc, const T* _
 #pragma unroll
         for (int e = 0; e < EPL; ++e) ac[g][e] = ak[g][e] = 0.0f;
     }
-    for (int64_t base = t0 + grp; base < t1; base += NG * kAttnBatch) {
+    // fold kAttnBatch positions (scores s[u], rows kv[u], vv[u]) into head g's state
+    auto fold = [&](int g, const float* s, const bool* ok, float (*kv)[EPL], float (*vv)[EPL],
+                    int nb) {
+        float mx = m[g];
+        for (int u = 0; u < nb; ++u) mx = fmaxf(mx, ok[u] ? s[u] : -INFINITY);
+        if (mx == -INFINITY) return;
+        const float corr = __builtin_amdgcn_exp2f(m[g] - mx);   // 0 when m was -inf
+        float lsum = l[g] * corr;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            ac[g][e] *= corr;
+            ak[g][e] *= corr;
+        }
+        for (int u = 0; u < nb; ++u) {
+            const float p = ok[u] ? __builtin_amdgcn_exp2f(s[u] - mx) : 0.0f;
+            lsum += p;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                ac[g][e] = fmaf(p, vv[u][e], ac[g][e]);
+                ak[g][e] = fmaf(p, kv[u][e], ak[g][e]);
+            }
+        }
+        l[g] = lsum;
+        m[g] = mx;
+    };
+    for (int64_t base = t0 + grp; base < tc; base += NG * kAttnBatch) {
         float kv[kAttnBatch][EPL], vv[kAttnBatch][EPL];
         bool ok[kAttnBatch];
 #pragma unroll
         for (int u = 0; u < kAttnBatch; ++u) {
             const int64_t t = base + (int64_t)NG * u;
-            ok[u] = t < t1;
-            const int64_t tc = ok[u] ? t : t1 - 1;   // in-range row; its score is masked
-            RowIO<T, EPL>::load(kbase + tc * cstride_t, kv[u]);
-            RowIO<T, EPL>::load(vbase + tc * cstride_t, vv[u]);
+            ok[u] = t < tc;
+            const int64_t tr = ok[u] ? t : tc - 1;   // in-range row; its score is masked
+            RowIO<T, EPL>::load(kbase + tr * a.cst, kv[u]);
+            RowIO<T, EPL>::load(vbase + tr * a.cst, vv[u]);
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float s[kAttnBatch];
-            float mx = m[g];
 #pragma unroll
             for (int u = 0; u < kAttnBatch; ++u) {
                 float dot = 0.0f;
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) dot = fmaf(qv[g][e], kv[u][e], dot);
-                dot = group_sum<LPR>(dot);
-                s[u] = ok[u] ? dot : -INFINITY;
-                mx = fmaxf(mx, s[u]);
+                s[u] = group_sum<LPR>(dot);
             }
-            if (mx == -INFINITY) continue;        // whole batch past the end for this group
-            const float corr = __builtin_amdgcn_exp2f(m[g] - mx);   // 0 when m was -inf
-            float lsum = l[g] * corr;
+            fold(g, s, ok, kv, vv, kAttnBatch);
+        }
+    }
+    if constexpr (FROM_QKV) {
+        if (holds_pos && grp == 0) {
+            // this token: rope k, attend to it from registers, append (k, v)
+            const T* krow = a.q + b * QKV + (a.QH + kvh) * HD;
+            const T* vrow = a.q + b * QKV + (a.QH + a.KVH + kvh) * HD;
+            const float* cr = a.cosv + pos * HD;
+            const float* sr = a.sinv + pos * HD;
+            float kn[1][EPL], vn[1][EPL];
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
-                ac[g][e] *= corr;
-                ak[g][e] *= corr;
+                kn[0][e] = rope_elem(krow, cr, sr, d0 + e, HD);
+                vn[0][e] = ld(vrow + d0 + e);
             }
+            // attend with k, v as stored (rounded to T), like every cached row
 #pragma unroll
-            for (int u = 0; u < kAttnBatch; ++u) {
-                const float p = ok[u] ? __builtin_amdgcn_exp2f(s[u] - mx) : 0.0f;
-                lsum += p;
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) {
-                    ac[g][e] = fmaf(p, vv[u][e], ac[g][e]);
-                    ak[g][e] = fmaf(p, kv[u][e], ak[g][e]);
-                }
+            for (int e = 0; e < EPL; ++e) {
+                T kt, vt;
+                st(&kt, kn[0][e]);
+                st(&vt, vn[0][e]);
+                kn[0][e] = ld(&kt);
+                vn[0][e] = ld(&vt);
             }
-            l[g] = lsum;
-            m[g] = mx;
+            RowIO<T, EPL>::store(a.kc + b * a.csb + pos * a.cst + kvh * HD + d0, kn[0]);
+            RowIO<T, EPL>::store(a.vc + b * a.csb + pos * a.cst + kvh * HD + d0, vn[0]);
+            const bool one = true;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float dot = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) dot = fmaf(qv[g][e], kn[0][e], dot);
+                const float s1 = group_sum<LPR>(dot);
+                fold(g, &s1, &one, kn, vn, 1);
+            }
         }
     }
     // merge the row groups of each wave (lanes j, j+LPR, ...), head by head
@@ -184,52 +281,67 @@ gqa_partial_kernel(const T* __restrict__ q, const T* __restrict__ kc, const T* _
         }
     }
     __syncthreads();
-    // merge the four waves into the chunk record
+    // merge the four waves into this chunk's record
+    float* recs = a.rec + ((int64_t)b * a.KVH + kvh) * nchunks * REC;
+    float* rec = recs + (int64_t)chunk * REC;
     for (int k = tid; k < REC; k += blockDim.x) {
-        int g;
-        if (k < 2 * G) g = k % G;
-        else g = ((k - 2 * G) % (G * HD)) / HD;
+        const int g = k < 2 * G ? k % G : ((k - 2 * G) % (G * HD)) / HD;
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < 4; ++w) M = fmaxf(M, wred[w][g]);
-        if (k < G) {
-            rec[k] = M;
-            continue;
-        }
-        float acc = 0.0f;
+        float acc = M;
+        if (k >= G) {
+            acc = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w)
-            if (wred[w][g] != -INFINITY) acc = fmaf(wred[w][k], __builtin_amdgcn_exp2f(wred[w][g] - M), acc);
-        rec[k] = acc;
+            for (int w = 0; w < 4; ++w)
+                if (wred[w][g] != -INFINITY) acc = fmaf(wred[w][k], __builtin_amdgcn_exp2f(wred[w][g] - M), acc);
+        }
+        st_coherent(rec + k, acc);
     }
-}
-
-template <typename T, int G>
-__global__ void __launch_bounds__(256)
-gqa_combine_kernel(const float* __restrict__ ws, T* __restrict__ c_out, T* __restrict__ k_out,
-                   int nchunks, int QH, int KVH, int HD) {
-    const int kvh = blockIdx.x;
-    const int64_t b = blockIdx.y;
-    const int rec = 2 * G + 2 * G * HD;
-    const float* base = ws + ((int64_t)b * KVH + kvh) * nchunks * rec;
-    for (int k = threadIdx.x; k < G * HD; k += blockDim.x) {
+    // publish the record; the block that arrives last merges all of them
+    __syncthreads();
+    int* counter = a.counters + b * a.KVH + kvh;
+    if (tid == 0) s_last = arrive(counter) == nact - 1;
+    __syncthreads();
+    if (!s_last) return;
+    for (int k = tid; k < G * HD; k += blockDim.x) {
         const int g = k / HD, d = k % HD;
-        float M = -INFINITY;   // chunk 0 always holds position 0, so M is finite
-        for (int c = 0; c < nchunks; ++c) M = fmaxf(M, base[c * rec + g]);
+        float M = -INFINITY;
+        for (int c0 = 0; c0 < nact; c0 += kAttnMerge) {
+            float mv[kAttnMerge];
+#pragma unroll
+            for (int u = 0; u < kAttnMerge; ++u)
+                mv[u] = c0 + u < nact ? ld_coherent(recs + (int64_t)(c0 + u) * REC + g) : -INFINITY;
+#pragma unroll
+            for (int u = 0; u < kAttnMerge; ++u) M = fmaxf(M, mv[u]);
+        }
         float L = 0.0f, C = 0.0f, K = 0.0f;
-        for (int c = 0; c < nchunks; ++c) {
-            const float* r = base + c * rec;
-            if (r[g] == -INFINITY) continue;
-            const float w = __builtin_amdgcn_exp2f(r[g] - M);   // log2-domain maxima
-            L = fmaf(r[G + g], w, L);
-            C = fmaf(r[2 * G + g * HD + d], w, C);
-            K = fmaf(r[2 * G + G * HD + g * HD + d], w, K);
+        for (int c0 = 0; c0 < nact; c0 += kAttnMerge) {
+            float mv[kAttnMerge], lv[kAttnMerge], cv[kAttnMerge], kv[kAttnMerge];
+#pragma unroll
+            for (int u = 0; u < kAttnMerge; ++u) {
+                const bool ok = c0 + u < nact;
+                const float* r = recs + (int64_t)(ok ? c0 + u : 0) * REC;
+                mv[u] = ok ? ld_coherent(r + g) : -INFINITY;
+                lv[u] = ld_coherent(r + G + g);
+                cv[u] = ld_coherent(r + 2 * G + g * HD + d);
+                kv[u] = ld_coherent(r + 2 * G + G * HD + g * HD + d);
+            }
+#pragma unroll
+            for (int u = 0; u < kAttnMerge; ++u) {
+                if (mv[u] == -INFINITY) continue;
+                const float w = __builtin_amdgcn_exp2f(mv[u] - M);
+                L = fmaf(lv[u], w, L);
+                C = fmaf(cv[u], w, C);
+                K = fmaf(kv[u], w, K);
+            }
         }
         const float inv = 1.0f / L;
-        const int64_t o = (b * QH + kvh * G + g) * HD + d;
-        st(c_out + o, C * inv);
-        st(k_out + o, K * inv);
+        const int64_t o = b * a.out_sb + (kvh * G + g) * HD + d;
+        st(a.c_out + o, C * inv);
+        st(a.k_out + o, K * inv);
     }
+    if (tid == 0) reset_counter(counter);
 }
 
 // ------------------------------------------------------------------ add + LayerNorm
@@ -395,38 +507,47 @@ static int rope_dispatch(const void* qkv, void* q_out, void* kc, void* vc, const
 }
 
 template <typename T>
-static int gqa_dispatch(const void* q, const void* kc, const void* vc, int64_t sb, int64_t stt,
-                        void* c_out, void* k_out, float* ws, int64_t B, int64_t len,
-                        const int64_t* pos_dev, int64_t QH, int64_t KVH, int64_t HD,
-                        hipStream_t st) {
+static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void* vc, int64_t sb,
+                        int64_t stt, const float* cosv, const float* sinv, void* q_out,
+                        void* c_out, void* k_out,
+                        int64_t out_sb, float* ws, int64_t B, int64_t len, const int64_t* pos_dev,
+                        int64_t QH, int64_t KVH, int64_t HD, hipStream_t st) {
     const int G = (int)(QH / KVH);
     const int nchunks = (int)ceil_div(len, kAttnChunk);
-    const float scale = kLog2e / sqrtf((float)HD);   // scores in log2 units
+    GqaArgs<T> a;
+    a.q = (const T*)q;
+    a.kc = (T*)kc;
+    a.vc = (T*)vc;
+    a.csb = sb;
+    a.cst = stt;
+    a.cosv = cosv;
+    a.sinv = sinv;
+    a.q_out = (T*)q_out;
+    a.counters = (int*)ws;
+    a.rec = (float*)((char*)ws + gqa_counter_bytes(B, KVH));
+    a.c_out = (T*)c_out;
+    a.k_out = (T*)k_out;
+    a.out_sb = out_sb;
+    a.len = len;
+    a.pos_dev = pos_dev;
+    a.QH = (int)QH;
+    a.KVH = (int)KVH;
+    a.qscale = kLog2e / sqrtf((float)HD);   // scores in log2 units
     dim3 grid(nchunks, (unsigned)KVH, (unsigned)B);
-#define LOOM_GQA(E, GG, LPR)                                                                     \
-    if (HD == E * LPR && G == GG) {                                                              \
-        hipLaunchKernelGGL((gqa_partial_kernel<T, E, GG, LPR>), grid, dim3(256), 0, st, (const T*)q, \
-                           (const T*)kc, (const T*)vc, sb, stt, ws, len, pos_dev, (int)QH,        \
-                           (int)KVH, scale);                                                     \
-        int rc = launch_status("loom_gqa_decode_attention");                                    \
-        if (rc != LOOM_OK) return rc;                                                            \
-        hipLaunchKernelGGL((gqa_combine_kernel<T, GG>), dim3((unsigned)KVH, (unsigned)B),        \
-                           dim3(256), 0, st, ws, (T*)c_out, (T*)k_out, nchunks, (int)QH,         \
-                           (int)KVH, (int)HD);                                                   \
-        return launch_status("loom_gqa_decode_attention(combine)");                              \
+#define LOOM_GQA(E, GG, LPR)                                                                    \
+    if (HD == E * LPR && G == GG) {                                                             \
+        if (from_qkv)                                                                           \
+            hipLaunchKernelGGL((gqa_decode_kernel<T, E, GG, LPR, true>), grid, dim3(256), 0, st, a); \
+        else                                                                                    \
+            hipLaunchKernelGGL((gqa_decode_kernel<T, E, GG, LPR, false>), grid, dim3(256), 0, st, a); \
+        return launch_status(from_qkv ? "loom_gqa_decode_step" : "loom_gqa_decode_attention");  \
     }
-    LOOM_GQA(6, 4, 16)
-    LOOM_GQA(6, 1, 16)
-    LOOM_GQA(6, 2, 16)
-    LOOM_GQA(6, 8, 16)
-    LOOM_GQA(4, 4, 16)
-    LOOM_GQA(8, 4, 16)
-    LOOM_GQA(2, 4, 16)
-    LOOM_GQA(4, 2, 16)
-    LOOM_GQA(8, 2, 16)
-    LOOM_GQA(1, 1, 8)
-    LOOM_GQA(1, 2, 8)
-    LOOM_GQA(1, 4, 8)
+    // head_dim 32/64/96/128 (16 lanes per row) and 8 (8 lanes), groups 1/2/4/8
+    LOOM_GQA(6, 4, 16) LOOM_GQA(6, 1, 16) LOOM_GQA(6, 2, 16) LOOM_GQA(6, 8, 16)
+    LOOM_GQA(4, 4, 16) LOOM_GQA(4, 1, 16) LOOM_GQA(4, 2, 16) LOOM_GQA(4, 8, 16)
+    LOOM_GQA(8, 4, 16) LOOM_GQA(8, 1, 16) LOOM_GQA(8, 2, 16) LOOM_GQA(8, 8, 16)
+    LOOM_GQA(2, 4, 16) LOOM_GQA(2, 1, 16) LOOM_GQA(2, 2, 16) LOOM_GQA(2, 8, 16)
+    LOOM_GQA(1, 1, 8) LOOM_GQA(1, 2, 8) LOOM_GQA(1, 4, 8) LOOM_GQA(1, 8, 8)
 #undef LOOM_GQA
     set_error("gqa_decode_attention: unsupported head_dim %lld / group %d", (long long)HD, G);
     return LOOM_ERR_INVALID;
@@ -481,7 +602,7 @@ extern "C" int64_t loom_gqa_workspace_bytes(int64_t B, int64_t max_len, int64_t 
                                             int64_t HD) {
     const int64_t G = QH / KVH;
     const int64_t nchunks = ceil_div(max_len, kAttnChunk);
-    return B * KVH * nchunks * (2 * G + 2 * G * HD) * (int64_t)sizeof(float);
+    return gqa_counter_bytes(B, KVH) + B * KVH * nchunks * (2 * G + 2 * G * HD) * (int64_t)sizeof(float);
 }
 
 extern "C" int loom_rope_append(int dtype, const void* qkv, void* q_out, void* k_cache,
@@ -500,6 +621,24 @@ extern "C" int loom_rope_append(int dtype, const void* qkv, void* q_out, void* k
                       (hipStream_t)stream)
 }
 
+static int gqa_checks(const char* who, const void* k_cache, const void* v_cache,
+                      int64_t cache_stride_b, int64_t cache_stride_t, const void* workspace,
+                      int64_t workspace_bytes, int64_t B, int64_t len, int64_t QH, int64_t KVH,
+                      int64_t HD) {
+    LOOM_CHECK(len >= 1 && KVH >= 1 && QH % KVH == 0 && QH / KVH <= kAttnMaxG,
+               "%s: bad shape len=%lld QH=%lld KVH=%lld", who, (long long)len, (long long)QH,
+               (long long)KVH);
+    LOOM_CHECK(workspace_bytes >= loom_gqa_workspace_bytes(B, len, QH, KVH, HD),
+               "%s: workspace too small (%lld bytes)", who, (long long)workspace_bytes);
+    LOOM_CHECK(((uintptr_t)workspace & 255) == 0, "%s: workspace must be 256-byte aligned", who);
+    // cache rows are read as 4-/8-byte words when each lane owns an even count
+    LOOM_CHECK(HD % 32 != 0 || ((((uintptr_t)k_cache | (uintptr_t)v_cache) & 7) == 0 &&
+                                cache_stride_b % 2 == 0 && cache_stride_t % 2 == 0),
+               "%s: caches must be 8-byte aligned with even strides", who);
+    LOOM_CHECK(cache_stride_t >= KVH * HD, "%s: cache row stride too small", who);
+    return LOOM_OK;
+}
+
 extern "C" int loom_gqa_decode_attention(int dtype, const void* q, const void* k_cache,
                                          const void* v_cache, int64_t cache_stride_b,
                                          int64_t cache_stride_t, void* c_out, void* kctx_out,
@@ -509,19 +648,34 @@ extern "C" int loom_gqa_decode_attention(int dtype, const void* q, const void* k
     clear_error();
     LOOM_CHECK(q && k_cache && v_cache && c_out && kctx_out && workspace,
                "gqa_decode_attention: null argument");
-    LOOM_CHECK(len >= 1 && KVH >= 1 && QH % KVH == 0 && QH / KVH <= kAttnMaxG,
-               "gqa_decode_attention: bad shape len=%lld QH=%lld KVH=%lld", (long long)len,
-               (long long)QH, (long long)KVH);
-    LOOM_CHECK(workspace_bytes >= loom_gqa_workspace_bytes(B, len, QH, KVH, HD),
-               "gqa_decode_attention: workspace too small (%lld bytes)", (long long)workspace_bytes);
-    // cache rows are read as 4-/8-byte words when each lane owns an even count
-    LOOM_CHECK(HD % 32 != 0 || ((((uintptr_t)k_cache | (uintptr_t)v_cache) & 7) == 0 &&
-                                cache_stride_b % 2 == 0 && cache_stride_t % 2 == 0),
-               "gqa_decode_attention: caches must be 8-byte aligned with even strides");
+    const int rc = gqa_checks("gqa_decode_attention", k_cache, v_cache, cache_stride_b,
+                              cache_stride_t, workspace, workspace_bytes, B, len, QH, KVH, HD);
+    if (rc != LOOM_OK) return rc;
     if (B == 0) return LOOM_OK;
-    LOOM_DTYPE_SWITCH(dtype, gqa_dispatch, q, k_cache, v_cache, cache_stride_b, cache_stride_t,
-                      c_out, kctx_out, workspace, B, len, pos_dev, QH, KVH, HD,
-                      (hipStream_t)stream)
+    LOOM_DTYPE_SWITCH(dtype, gqa_dispatch, false, q, k_cache, v_cache, cache_stride_b,
+                      cache_stride_t, nullptr, nullptr, nullptr, c_out, kctx_out, QH * HD, workspace, B,
+                      len, pos_dev, QH, KVH, HD, (hipStream_t)stream)
+}
+
+extern "C" int loom_gqa_decode_step(int dtype, const void* qkv, void* k_cache, void* v_cache,
+                                    int64_t cache_stride_b, int64_t cache_stride_t,
+                                    const float* cos_table, const float* sin_table, void* q_out,
+                                    void* c_out, void* kctx_out, int64_t out_stride_b, float* workspace,
+                                    int64_t workspace_bytes, int64_t B, int64_t len,
+                                    const int64_t* pos_dev, int64_t QH, int64_t KVH, int64_t HD,
+                                    void* stream) {
+    clear_error();
+    LOOM_CHECK(qkv && k_cache && v_cache && cos_table && sin_table && c_out && kctx_out &&
+                   workspace,
+               "gqa_decode_step: null argument");
+    LOOM_CHECK(HD % 2 == 0 && out_stride_b >= QH * HD, "gqa_decode_step: bad head_dim / out stride");
+    const int rc = gqa_checks("gqa_decode_step", k_cache, v_cache, cache_stride_b, cache_stride_t,
+                              workspace, workspace_bytes, B, len, QH, KVH, HD);
+    if (rc != LOOM_OK) return rc;
+    if (B == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, gqa_dispatch, true, qkv, k_cache, v_cache, cache_stride_b,
+                      cache_stride_t, cos_table, sin_table, q_out, c_out, kctx_out, out_stride_b,
+                      workspace, B, len, pos_dev, QH, KVH, HD, (hipStream_t)stream)
 }
 
 // ---------------------------------------------------------------- step control

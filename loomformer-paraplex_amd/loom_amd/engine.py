@@ -123,7 +123,7 @@ class LoomDecoder:
         self.tokens = z(B, self.max_len, dtype=torch.int64)
         self.prompt_buf = z(B, self.max_len, dtype=torch.int64)
         ws = self.lib.loom_gqa_workspace_bytes(B, self.max_len, c.QH, c.KVH, c.HD)
-        self.ws = torch.empty((ws + 3) // 4, dtype=torch.float32, device=dev)
+        self.ws = torch.zeros((ws + 3) // 4, dtype=torch.float32, device=dev)   # counters start at 0
         self.ws_bytes = ws
         # activations
         self.h = z(B, N)
@@ -204,12 +204,11 @@ class LoomDecoder:
             kc, vc = self.k_cache[bi], self.v_cache[bi]
             # ---- attention step (loomformer.py:3300-3332)
             self._linear(self.h, blk["qkv"], self.qkv, B, N + 2 * c.KV, N)
-            self._call("loom_rope_append", self.code, _P(self.qkv), _P(self.q), _P(kc), _P(vc),
-                       _P(self.cos), _P(self.sin), B, 0, _P(self.pos_dev), c.QH, c.KVH, c.HD,
-                       cache_sb, cache_st, st)
-            self._call("loom_gqa_decode_attention", self.code, _P(self.q), _P(kc), _P(vc), cache_sb,
-                       cache_st, _P(self.c), _P(self.kctx), _P(self.ws), self.ws_bytes, B,
-                       self.max_len, _P(self.pos_dev), c.QH, c.KVH, c.HD, st)
+            # RoPE + cache append + attention + chunk merge, one launch
+            self._call("loom_gqa_decode_step", self.code, _P(self.qkv), _P(kc), _P(vc), cache_sb,
+                       cache_st, _P(self.cos), _P(self.sin), _P(self.q), _P(self.c), _P(self.kctx), N,
+                       _P(self.ws), self.ws_bytes, B, self.max_len, _P(self.pos_dev), c.QH, c.KVH,
+                       c.HD, st)
             self._linear(self.c, blk["o"], self.attn_out, B, N, N)
             # ---- depth read 2*bi, LayerNorm, history slot (loomformer.py:3999-4004)
             self._depth(sub, self.d)

@@ -100,7 +100,7 @@ def test_gqa_decode_attention(dtype, B, QH, KVH, HD, length):
     c = torch.empty(B, QH, HD, device=DEV, dtype=dtype)
     kx = torch.empty_like(c)
     nb = _lib.load().loom_gqa_workspace_bytes(B, max_len, QH, KVH, HD)
-    ws = torch.empty(nb // 4 + 1, device=DEV)
+    ws = torch.zeros(nb // 4 + 1, device=DEV)      # arrival counters start at zero
     _lib.call("loom_gqa_decode_attention", code(q), P(q), P(kc), P(vc), max_len * KVH * HD, KVH * HD,
               P(c), P(kx), P(ws), nb, B, length, None, QH, KVH, HD, S(q))
     G = QH // KVH
@@ -117,6 +117,71 @@ def test_gqa_decode_attention(dtype, B, QH, KVH, HD, length):
               P(c), P(kx), P(ws), nb, B, max_len, P(pos_d), QH, KVH, HD, S(q))
     check(c, (a @ V).squeeze(2), dtype)
     check(kx, (a @ K).squeeze(2), dtype)
+    # every call leaves the arrival counters at zero
+    ncnt = B * KVH
+    assert int(ws[:ncnt].view(torch.int32).abs().sum().item()) == 0
+
+
+def _rope_tables(HD, n):
+    inv, af = ref.yarn_inv_freq(HD, 10000.0, 4.0, 256, 32.0, 1.0)
+    return ref.yarn_cos_sin(inv, af, n)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,QH,KVH,HD,length", [
+    (2, 8, 2, 96, 1), (3, 8, 2, 96, 255), (2, 8, 2, 96, 257), (32, 8, 2, 96, 700),
+    (2, 4, 4, 64, 300), (2, 8, 1, 64, 513), (1, 4, 2, 8, 90), (2, 8, 2, 32, 256)])
+def test_gqa_decode_step(dtype, B, QH, KVH, HD, length):
+    """RoPE + cache append + attention + merge in one launch, against the
+    oracle's RoPE and a plain softmax over the appended cache."""
+    from loom_amd import _lib
+    max_len = length + 7
+    pos = length - 1
+    g = torch.Generator().manual_seed(length * 7 + HD + QH)
+    qkv = torch.randn(B, (QH + 2 * KVH) * HD, generator=g).to(DEV, dtype)
+    kc = torch.randn(B, max_len, KVH, HD, generator=g).to(DEV, dtype)
+    vc = torch.randn(B, max_len, KVH, HD, generator=g).to(DEV, dtype)
+    kc0, vc0 = host(kc), host(vc)
+    cos, sin = _rope_tables(HD, max_len)
+    cos_d, sin_d = cos.to(DEV), sin.to(DEV)
+    out_sb = 2 * QH * HD                            # outputs written with a row stride
+    cbuf = torch.zeros(B, out_sb, device=DEV, dtype=dtype)
+    kbuf = torch.zeros(B, out_sb, device=DEV, dtype=dtype)
+    nb = _lib.load().loom_gqa_workspace_bytes(B, max_len, QH, KVH, HD)
+    ws = torch.zeros(nb // 4 + 1, device=DEV)
+    pos_d = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    qout = torch.zeros(B, QH, HD, device=DEV, dtype=dtype)
+    # oracle: rope q and this token's k, append, attend over positions 0..pos
+    x = host(qkv)
+    qr = ref.apply_rope(x[:, :QH * HD].view(B, QH, HD), cos[pos], sin[pos])
+    kr = ref.apply_rope(x[:, QH * HD:(QH + KVH) * HD].view(B, KVH, HD), cos[pos], sin[pos])
+    vn = x[:, (QH + KVH) * HD:].view(B, KVH, HD)
+    kr = kr.to(dtype).float()                       # the cache stores T
+    Kc, Vc = kc0.clone(), vc0.clone()
+    Kc[:, pos], Vc[:, pos] = kr, vn
+    G = QH // KVH
+    K = Kc[:, :length].repeat_interleave(G, dim=2).transpose(1, 2)
+    V = Vc[:, :length].repeat_interleave(G, dim=2).transpose(1, 2)
+    a = torch.softmax((qr.unsqueeze(2) @ K.transpose(-1, -2)) / math.sqrt(HD), dim=-1)
+    for call in range(2):                           # host length, then device position
+        cbuf.zero_()
+        kbuf.zero_()
+        kc.copy_(kc0.to(dtype))
+        vc.copy_(vc0.to(dtype))
+        _lib.call("loom_gqa_decode_step", code(qkv), P(qkv), P(kc), P(vc), max_len * KVH * HD,
+                  KVH * HD, P(cos_d), P(sin_d), P(qout), P(cbuf), P(kbuf), out_sb, P(ws), nb, B,
+                  length if call == 0 else max_len, None if call == 0 else P(pos_d), QH, KVH, HD,
+                  S(qkv))
+        check(cbuf[:, :QH * HD].view(B, QH, HD), (a @ V).squeeze(2), dtype)
+        check(kbuf[:, :QH * HD].view(B, QH, HD), (a @ K).squeeze(2), dtype)
+        check(qout, qr, dtype)
+        assert bool((cbuf[:, QH * HD:] == 0).all()) and bool((kbuf[:, QH * HD:] == 0).all())
+        torch.testing.assert_close(host(kc)[:, pos], kr, **TOL[dtype])
+        torch.testing.assert_close(host(vc)[:, pos], vn.to(dtype).float(), rtol=0, atol=0)
+        rest = [t for t in range(max_len) if t != pos]
+        assert torch.equal(host(kc)[:, rest], kc0[:, rest])
+        assert torch.equal(host(vc)[:, rest], vc0[:, rest])
+        assert int(ws[:B * KVH].view(torch.int32).abs().sum().item()) == 0
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
