@@ -100,6 +100,47 @@ int loom_linear(int dtype, const void* A, int64_t lda, const void* W, int64_t ld
                 const float* bias, const void* gate_p, float gate_alpha, const void* residual,
                 void* out, int64_t ldc, int64_t M, int64_t Nout, int64_t K, void* stream);
 
+/* One output segment of loom_linear_multi: n columns with their own weight
+ * rows, output, bias and identity-anchored gate. */
+typedef struct {
+    const void* w;        /* [n, k] rows multiplying x (row stride ldw) */
+    int64_t ldw;
+    const void* w2;       /* [n, k2] rows multiplying x2; NULL when k2 == 0 */
+    int64_t ldw2;
+    void* out;            /* [m, n] output (row stride ldc) */
+    int64_t ldc;
+    const float* bias;    /* [n] fp32 or NULL */
+    const void* gate_p;   /* [m, n] dtype (row stride gate_ld) or NULL; single-input only */
+    int64_t gate_ld;
+    float gate_alpha;
+    int64_t n;
+} loom_linear_segment;
+
+typedef struct {
+    const void* x;        /* [m, k] activations (row stride ldx) */
+    int64_t ldx;
+    int64_t k;
+    const void* x2;       /* [m, k2] second activations or NULL (k2 = 0) */
+    int64_t ldx2;
+    int64_t k2;
+    int64_t m;
+    int32_t nseg;         /* 1..4 */
+    loom_linear_segment seg[4];
+} loom_linear_multi_desc;
+
+/* Several decode projections in one launch (no counterpart in the reference;
+ * the engine's restatement of Model.step, loomformer.py:3951-4091, uses it to
+ * merge adjacent nn.Linear calls):
+ *   seg s: out_s = (x w_s^T + x2 w2_s^T) [* (1 + gate_alpha * gate_p)] + bias
+ * Concatenation along k sums two products in one accumulator (o-projection
+ * plus depth read-out before LayerNorm); segments share x (e.g. the depth
+ * history projection and W_real of the same hidden state).  bf16 with m <= 64
+ * runs as one fused MFMA launch; other dtypes run one product per piece. */
+int loom_linear_multi(int dtype, const loom_linear_multi_desc* desc, void* stream);
+
+/* sizeof(loom_linear_multi_desc), so an FFI binding can check its layout. */
+int64_t loom_linear_multi_desc_bytes(void);
+
 /* ---------------------------------------------------------------------------
  * Depth attention
  * ------------------------------------------------------------------------ */

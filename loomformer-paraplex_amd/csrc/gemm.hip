@@ -16,6 +16,7 @@
 // (open sectors); the loader reads each 8-element piece from its sector, so
 // the packed matrix is never written to HBM.
 #include <cmath>
+#include <type_traits>
 
 #include "loom_common.h"
 
@@ -267,6 +268,115 @@ gemm_bf16_skinny_kernel(GemmArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ fused decode projections
+// Several decode projections in one launch (M <= 64, bf16):
+//   * concat-K: out = X W^T + X2 W2^T (two activations, two weights, one
+//     accumulator), e.g. attn_out + depth skip before LayerNorm;
+//   * output segments: the N columns are split into up to 4 segments that
+//     share the activations but have their own weight rows, output (and row
+//     stride), bias and identity-anchored gate, e.g. [history kv | W_real].
+// Same block shape as the skinny kernel: 16 output columns x all M rows per
+// block, the four waves split the combined k-steps of X and X2.
+struct LinSeg {
+    const uint16_t* W;
+    int64_t ldw;
+    const uint16_t* W2;
+    int64_t ldw2;
+    void* out;
+    int64_t ldc;
+    const float* bias;
+    const void* gate_p;
+    int64_t gate_ld;
+    float gate_alpha;
+    int64_t n;
+};
+
+constexpr int kMaxSeg = 4;
+
+struct LinArgs {
+    const uint16_t* X;
+    int64_t ldx, K;
+    const uint16_t* X2;
+    int64_t ldx2, K2;
+    int64_t M;
+    int nseg;
+    int64_t nstart[kMaxSeg + 1];   // first global column of each segment
+    LinSeg seg[kMaxSeg];
+};
+
+template <int MT>
+__global__ void __launch_bounds__(256)
+gemm_bf16_skinny_multi_kernel(LinArgs a) {
+    __shared__ float red[SK_WAVES][MT][4][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t ng = (int64_t)blockIdx.x * 16;
+    int s = 0;
+#pragma unroll
+    for (int q = 1; q < kMaxSeg; ++q) s += (q < a.nseg && ng >= a.nstart[q]) ? 1 : 0;
+    const LinSeg sg = a.seg[s];
+    const int64_t n0 = ng - a.nstart[s];
+    const int fr = lane & 15, fk = (lane >> 4) * 8;
+    const int64_t n = n0 + fr;
+    const bool nvalid = n < sg.n;
+    const int64_t S1 = ceil_div(a.K, 32), S2 = ceil_div(a.K2, 32), S = S1 + S2;
+    const int64_t per = ceil_div(S, SK_WAVES);
+    const int64_t s_begin = wave * per;
+    const int64_t s_end = s_begin + per < S ? s_begin + per : S;
+
+    f32x4 acc[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int64_t s0 = s_begin; s0 < s_end; s0 += SK_UNROLL) {
+        uint4 wv[SK_UNROLL];
+        uint4 xv[SK_UNROLL][MT];
+#pragma unroll
+        for (int u = 0; u < SK_UNROLL; ++u) {
+            const int64_t step = s0 + u;
+            const bool first = step < S1;
+            const int64_t k = (first ? step : step - S1) * 32 + fk;
+            const bool kin = step < s_end && k < (first ? a.K : a.K2);
+            const uint16_t* wrow = first ? sg.W + n * sg.ldw : sg.W2 + n * sg.ldw2;
+            const uint16_t* xb = first ? a.X : a.X2;
+            const int64_t ldx = first ? a.ldx : a.ldx2;
+            wv[u] = (kin && nvalid) ? *reinterpret_cast<const uint4*>(wrow + k) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+                const int64_t m = j * 16 + fr;
+                xv[u][j] = (kin && m < a.M) ? *reinterpret_cast<const uint4*>(xb + m * ldx + k)
+                                            : make_uint4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SK_UNROLL; ++u)
+#pragma unroll
+            for (int j = 0; j < MT; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8, wv[u]), __builtin_bit_cast(bf16x8, xv[u][j]), acc[j],
+                    0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][j][r][lane] = acc[j][r];
+    __syncthreads();
+    uint16_t* out = (uint16_t*)sg.out;
+    for (int o = tid; o < MT * 256; o += 256) {
+        const int nn = o & 15, mi = o >> 4;
+        const int j = mi >> 4, ml = mi & 15;
+        const int64_t m = mi, nidx = n0 + nn;
+        if (m >= a.M || nidx >= sg.n) continue;
+        const int ln = ml + 16 * (nn >> 2), r = nn & 3;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < SK_WAVES; ++w) v += red[w][j][r][ln];
+        if (sg.gate_p != nullptr)
+            v *= 1.0f + sg.gate_alpha * ld((const bf16_t*)sg.gate_p + m * sg.gate_ld + nidx);
+        if (sg.bias != nullptr) v += sg.bias[nidx];
+        out[m * sg.ldc + nidx] = f32_to_bf16(v);
+    }
+}
+
 // ------------------------------------------------------------------ SIMT
 
 constexpr int SB_M = 64, SB_N = 64, SB_K = 16;
@@ -448,6 +558,94 @@ extern "C" int loom_linear(int dtype, const void* A, int64_t lda, const void* W,
         case LOOM_F16: return linear_dispatch<f16_t>(a, (hipStream_t)stream);
     }
     set_error("linear: unsupported dtype %d", dtype);
+    return LOOM_ERR_INVALID;
+}
+
+// Host side of loom_linear_multi: one fused launch for bf16 when every piece
+// is 16-byte aligned, otherwise (and for fp32 / fp16) one product per segment
+// and input, the second input accumulated through the residual epilogue.
+template <typename T>
+static int linear_multi_dispatch(const loom_linear_multi_desc& d, hipStream_t st) {
+    bool fused = std::is_same<T, bf16_t>::value && d.m <= 64 && d.k % 8 == 0 && d.ldx % 8 == 0 &&
+                 ((uintptr_t)d.x & 15) == 0;
+    if (d.k2 > 0) fused = fused && d.k2 % 8 == 0 && d.ldx2 % 8 == 0 && ((uintptr_t)d.x2 & 15) == 0;
+    for (int s = 0; s < d.nseg; ++s) {
+        const loom_linear_segment& g = d.seg[s];
+        fused = fused && g.ldw % 8 == 0 && ((uintptr_t)g.w & 15) == 0 && (s == d.nseg - 1 || g.n % 16 == 0);
+        if (d.k2 > 0) fused = fused && g.ldw2 % 8 == 0 && ((uintptr_t)g.w2 & 15) == 0;
+    }
+    if (fused) {
+        LinArgs a{};
+        a.X = (const uint16_t*)d.x; a.ldx = d.ldx; a.K = d.k;
+        a.X2 = (const uint16_t*)d.x2; a.ldx2 = d.ldx2; a.K2 = d.k2;
+        a.M = d.m; a.nseg = d.nseg;
+        int64_t ncols = 0;
+        for (int s = 0; s < d.nseg; ++s) {
+            const loom_linear_segment& g = d.seg[s];
+            a.nstart[s] = ncols;
+            a.seg[s] = LinSeg{(const uint16_t*)g.w, g.ldw, (const uint16_t*)g.w2, g.ldw2, g.out, g.ldc,
+                              g.bias, g.gate_p, g.gate_ld, g.gate_alpha, g.n};
+            ncols += ceil_div(g.n, 16) * 16;
+        }
+        for (int s = d.nseg; s <= kMaxSeg; ++s) a.nstart[s] = ncols;
+        const dim3 grid((unsigned)(ncols / 16));
+        switch (ceil_div(d.m, 16)) {
+            case 1: hipLaunchKernelGGL((gemm_bf16_skinny_multi_kernel<1>), grid, dim3(256), 0, st, a); break;
+            case 2: hipLaunchKernelGGL((gemm_bf16_skinny_multi_kernel<2>), grid, dim3(256), 0, st, a); break;
+            case 3: hipLaunchKernelGGL((gemm_bf16_skinny_multi_kernel<3>), grid, dim3(256), 0, st, a); break;
+            default: hipLaunchKernelGGL((gemm_bf16_skinny_multi_kernel<4>), grid, dim3(256), 0, st, a); break;
+        }
+        return launch_status("loom_linear_multi");
+    }
+    for (int s = 0; s < d.nseg; ++s) {
+        const loom_linear_segment& g = d.seg[s];
+        GemmArgs a{};
+        a.X = d.x; a.ldx = d.ldx; a.W = g.w; a.ldw = g.ldw; a.out = g.out; a.ldc = g.ldc;
+        a.M = d.m; a.N = g.n; a.K = d.k;
+        if (d.k2 == 0) {
+            a.bias = g.bias; a.gate_p = g.gate_p; a.gate_alpha = g.gate_alpha;
+            int rc = run_gemm<T, false>(a, st, "loom_linear_multi");
+            if (rc != LOOM_OK) return rc;
+            continue;
+        }
+        int rc = run_gemm<T, false>(a, st, "loom_linear_multi");
+        if (rc != LOOM_OK) return rc;
+        GemmArgs b = a;
+        b.X = d.x2; b.ldx = d.ldx2; b.W = g.w2; b.ldw = g.ldw2; b.K = d.k2;
+        b.bias = g.bias; b.residual = g.out;
+        rc = run_gemm<T, false>(b, st, "loom_linear_multi");
+        if (rc != LOOM_OK) return rc;
+    }
+    return LOOM_OK;
+}
+
+extern "C" int64_t loom_linear_multi_desc_bytes(void) { return (int64_t)sizeof(loom_linear_multi_desc); }
+
+extern "C" int loom_linear_multi(int dtype, const loom_linear_multi_desc* d, void* stream) {
+    clear_error();
+    LOOM_CHECK(d != nullptr && d->x != nullptr, "linear_multi: null descriptor or input");
+    LOOM_CHECK(d->nseg >= 1 && d->nseg <= kMaxSeg, "linear_multi: nseg=%d outside [1, %d]",
+               (int)d->nseg, kMaxSeg);
+    LOOM_CHECK(d->m >= 0 && d->k >= 1 && d->ldx >= d->k && d->k2 >= 0,
+               "linear_multi: bad input shape");
+    LOOM_CHECK(d->k2 == 0 || (d->x2 != nullptr && d->ldx2 >= d->k2),
+               "linear_multi: second input missing or its stride is too small");
+    for (int s = 0; s < d->nseg; ++s) {
+        const loom_linear_segment& g = d->seg[s];
+        LOOM_CHECK(g.w && g.out && g.n >= 1 && g.ldw >= d->k && g.ldc >= g.n,
+                   "linear_multi: bad segment %d", s);
+        LOOM_CHECK(d->k2 == 0 || (g.w2 && g.ldw2 >= d->k2), "linear_multi: segment %d lacks w2", s);
+        LOOM_CHECK(d->k2 == 0 || g.gate_p == nullptr,
+                   "linear_multi: the gate applies to single-input segments only");
+        LOOM_CHECK(g.gate_p == nullptr || g.gate_ld >= g.n, "linear_multi: gate row stride too small");
+    }
+    if (d->m == 0) return LOOM_OK;
+    switch (dtype) {
+        case LOOM_F32: return linear_multi_dispatch<float>(*d, (hipStream_t)stream);
+        case LOOM_BF16: return linear_multi_dispatch<bf16_t>(*d, (hipStream_t)stream);
+        case LOOM_F16: return linear_multi_dispatch<f16_t>(*d, (hipStream_t)stream);
+    }
+    set_error("linear_multi: unsupported dtype %d", dtype);
     return LOOM_ERR_INVALID;
 }
 

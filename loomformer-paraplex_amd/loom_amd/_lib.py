@@ -15,6 +15,21 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libloom_hip.so")
 
 _P = c_void_p
+
+
+class LinearSegment(ctypes.Structure):
+    """loom_linear_segment (include/loom_hip.h)."""
+    _fields_ = [("w", c_void_p), ("ldw", c_int64), ("w2", c_void_p), ("ldw2", c_int64),
+                ("out", c_void_p), ("ldc", c_int64), ("bias", c_void_p), ("gate_p", c_void_p),
+                ("gate_ld", c_int64), ("gate_alpha", c_float), ("n", c_int64)]
+
+
+class LinearMultiDesc(ctypes.Structure):
+    """loom_linear_multi_desc (include/loom_hip.h)."""
+    _fields_ = [("x", c_void_p), ("ldx", c_int64), ("k", c_int64), ("x2", c_void_p),
+                ("ldx2", c_int64), ("k2", c_int64), ("m", c_int64), ("nseg", ctypes.c_int32),
+                ("seg", LinearSegment * 4)]
+
 # name -> argument types (all return c_int status)
 SIGNATURES = {
     "loom_paraplex_forward": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
@@ -23,6 +38,7 @@ SIGNATURES = {
     "loom_pvpowlu_forward": [c_int, _P, _P, _P, c_int64, c_float, _P],
     "loom_beta_forward": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64,
                           c_int64, c_int64, c_int64, c_int64, c_int, _P],
+    "loom_linear_multi": [c_int, _P, _P],
     "loom_linear": [c_int, _P, c_int64, _P, c_int64, _P, _P, c_float, _P, _P, c_int64,
                     c_int64, c_int64, c_int64, _P],
     "loom_depth_attn_forward": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64,
@@ -55,7 +71,8 @@ SIGNATURES = {
                                   _P],
 }
 # entry points that return a value instead of a status
-QUERIES = {"loom_gqa_workspace_bytes": ([c_int64] * 5, c_int64)}
+QUERIES = {"loom_gqa_workspace_bytes": ([c_int64] * 5, c_int64),
+           "loom_linear_multi_desc_bytes": ([], c_int64)}
 
 _lib = None
 _lock = threading.Lock()
@@ -103,6 +120,32 @@ def dtype_code(t: torch.Tensor) -> int:
         return DTYPE_CODE[t.dtype]
     except KeyError:
         raise RuntimeError(f"unsupported dtype {t.dtype}; expected float32, bfloat16 or float16")
+
+
+def linear_multi_desc(x, segments, x2=None, m=None):
+    """Build a LinearMultiDesc.  x, x2: [m, k] tensors (row-strided views are
+    fine); segments: dicts with w, out and optional w2, bias, gate_p,
+    gate_alpha (tensors keep their own row strides)."""
+    d = LinearMultiDesc()
+    d.x, d.ldx, d.k = x.data_ptr(), x.stride(0), x.shape[1]
+    if x2 is not None:
+        d.x2, d.ldx2, d.k2 = x2.data_ptr(), x2.stride(0), x2.shape[1]
+    d.m = x.shape[0] if m is None else m
+    if not 1 <= len(segments) <= 4:
+        raise ValueError("linear_multi takes 1 to 4 segments")
+    d.nseg = len(segments)
+    for i, sg in enumerate(segments):
+        e = d.seg[i]
+        w, out = sg["w"], sg["out"]
+        e.w, e.ldw, e.out, e.ldc, e.n = w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0), w.shape[0]
+        if sg.get("w2") is not None:
+            e.w2, e.ldw2 = sg["w2"].data_ptr(), sg["w2"].stride(0)
+        if sg.get("bias") is not None:
+            e.bias = sg["bias"].data_ptr()
+        if sg.get("gate_p") is not None:
+            e.gate_p, e.gate_ld = sg["gate_p"].data_ptr(), sg["gate_p"].stride(0)
+            e.gate_alpha = float(sg.get("gate_alpha", 0.0))
+    return d
 
 
 def ptr(t):

@@ -141,6 +141,7 @@ class LoomDecoder:
         self.act = z(B, H)
         self.s = z(B, H)
         self.ffn_out = z(B, N)
+        self.y = z(B, N)                # pre-LayerNorm sum of a sublayer
         self.carry = z(2, B, H, 3, 3)
         self.p = z(2, B, H)
         self.pooled = z(B, 9)
@@ -153,6 +154,7 @@ class LoomDecoder:
         self.snap = torch.empty((), dtype=torch.float32, device=dev)
         self.pos = 0
         self._graphs: Dict[int, torch.cuda.CUDAGraph] = {}
+        self._descs: Dict[object, object] = {}
 
     # ------------------------------------------------------------------ helpers
 
@@ -168,6 +170,15 @@ class LoomDecoder:
                 gate_alpha=0.0, residual=None):
         self._call("loom_linear", self.code, _P(x), ldx or K, _P(w), K, _P(bias), _P(gate_p),
                    float(gate_alpha), _P(residual), _P(out), ldc or Nout, M, Nout, K, self._stream())
+
+    def _multi(self, key, x, segments, x2=None) -> None:
+        """loom_linear_multi with a descriptor built once per call site (every
+        pointer in it is a persistent engine buffer or weight)."""
+        d = self._descs.get(key)
+        if d is None:
+            d = _lib.linear_multi_desc(x, segments, x2=x2)
+            self._descs[key] = d
+        self._call("loom_linear_multi", self.code, _lib.ctypes.byref(d), self._stream())
 
     def reset(self) -> None:
         """Forget all sequence state (Model.step at pos 0 starts afresh)."""
@@ -191,9 +202,11 @@ class LoomDecoder:
                    _P(self.tokens), self.max_len, _P(self.pos_dev), _P(self.pending), _P(self.fire),
                    _P(self.reset_now), carry_id, c.window, c.seq_len, B, st)
         torch.index_select(self.emb, 0, self.ids, out=self.h)
-        hist_ld = 2 * L * 2 * N
-        # depth history slot 0: DepthAttn.project(h) (loomformer.py:3973)
-        self._linear(self.h, self.kvw, self.hist[:, 0], B, 2 * N, N, ldc=hist_ld)
+        hist = self.hist
+        # depth history slot 0 = DepthAttn.project(h) (loomformer.py:3973), with
+        # layer 0's qkv projection of the same h in the same launch
+        self._multi("first", self.h, [dict(w=self.kvw, out=hist[:, 0]),
+                                      dict(w=self.blocks[0]["qkv"], out=self.qkv)])
         sub = 0
         cache_sb = self.max_len * c.KVH * c.HD
         cache_st = c.KVH * c.HD
@@ -202,29 +215,28 @@ class LoomDecoder:
         for bi, blk in enumerate(self.blocks):
             last = bi == L - 1
             kc, vc = self.k_cache[bi], self.v_cache[bi]
-            # ---- attention step (loomformer.py:3300-3332)
-            self._linear(self.h, blk["qkv"], self.qkv, B, N + 2 * c.KV, N)
-            # RoPE + cache append + attention + chunk merge, one launch
+            # ---- attention step (loomformer.py:3300-3332): RoPE + cache append +
+            # attention + chunk merge, one launch
             self._call("loom_gqa_decode_step", self.code, _P(self.qkv), _P(kc), _P(vc), cache_sb,
                        cache_st, _P(self.cos), _P(self.sin), _P(self.q), _P(self.c), _P(self.kctx), N,
                        _P(self.ws), self.ws_bytes, B, self.max_len, _P(self.pos_dev), c.QH, c.KVH,
                        c.HD, st)
-            self._linear(self.c, blk["o"], self.attn_out, B, N, N)
-            # ---- depth read 2*bi, LayerNorm, history slot (loomformer.py:3999-4004)
+            # ---- depth read 2*bi, then LN(o(c) + w_o(d)) (loomformer.py:3999-4000):
+            # both products accumulate in one launch
             self._depth(sub, self.d)
-            self._linear(self.d, self.wo, self.skip, B, N, N)
-            self._call("loom_add_layernorm", self.code, _P(self.skip), _P(self.attn_out),
+            self._multi(("attn", bi), self.c.view(B, N),
+                        [dict(w=blk["o"], w2=self.wo, out=self.y)], x2=self.d.view(B, N))
+            self._call("loom_add_layernorm", self.code, _P(self.y), None,
                        _P(blk["ln1_w"]), _P(blk["ln1_b"]), _P(self.h), B, N, 1e-5, st)
+            # ---- history slot 2*bi+1 (loomformer.py:4004) and W_real of the same h
+            # (+ IdentityAnchoredGate with the previous block's p, loomformer.py:2839)
             sub += 1
-            self._linear(self.h, self.kvw, self.hist[:, sub], B, 2 * N, N, ldc=hist_ld)
+            real = dict(w=blk["w1r"], out=self.R, bias=blk["b1r"])
+            if p_i is not None:
+                real.update(gate_p=self.p[p_i], gate_alpha=blk["alpha"])
+            self._multi(("kvr", bi), self.h, [dict(w=self.kvw, out=hist[:, sub]), real])
             self._depth(sub, self.dh)
-            self._linear(self.dh, self.wo, self.skip, B, N, N)
             # ---- Paraplex FFN (loomformer.py:2818-2893, fused path :2533-2560)
-            if p_i is None:
-                self._linear(self.h, blk["w1r"], self.R, B, H, N, bias=blk["b1r"])
-            else:
-                self._linear(self.h, blk["w1r"], self.R, B, H, N, bias=blk["b1r"],
-                             gate_p=self.p[p_i], gate_alpha=blk["alpha"])
             self._call("loom_beta_forward", self.code, _P(self.h), _P(self.q), _P(self.kctx),
                        _P(self.c), _P(self.dh), _P(blk["w1i"]), _P(self.beta), None, B, N, H,
                        c.imag_in, c.Hq, c.HD, c.QH, 1 if c.sectors == "open" else 0, st)
@@ -232,7 +244,6 @@ class LoomDecoder:
             self._call("loom_paraplex_forward", self.code, _P(self.R), _P(self.R), _P(self.beta),
                        _P(blk["ib"]), _P(tr), _P(blk["tw"]), None, _P(blk["anchor"]), _P(self.act),
                        _P(self.s), _P(tr), _P(self.snap), B, 1, H, float(c.powlu_m), st)
-            self._linear(self.act, blk["w2"], self.ffn_out, B, N, H, bias=blk["b2"])
             # ---- Tria depth op (loomformer.py:4012-4040); axis = bi % 3
             out_i = 0 if carry_i != 0 else 1
             gate = not last
@@ -247,12 +258,19 @@ class LoomDecoder:
                        _P(self.p[new_p]) if gate else None, None, B, 1, H, float(c.tria_alpha),
                        bi % 3, st)
             carry_i, p_i = out_i, new_p
-            # ---- LayerNorm and next history slot (loomformer.py:4045-4050)
-            self._call("loom_add_layernorm", self.code, _P(self.skip), _P(self.ffn_out),
+            # ---- LN(w_o(d_h) + W2(act) + b2) (loomformer.py:4045): one launch + LN
+            self._multi(("ffn", bi), self.dh.view(B, N),
+                        [dict(w=self.wo, w2=blk["w2"], out=self.y, bias=blk["b2"])], x2=self.act)
+            self._call("loom_add_layernorm", self.code, _P(self.y), None,
                        _P(blk["ln2_w"]), _P(blk["ln2_b"]), _P(self.h), B, N, 1e-5, st)
             if not last:
+                # next history slot (loomformer.py:4050) and the next block's qkv
                 sub += 1
-                self._linear(self.h, self.kvw, self.hist[:, sub], B, 2 * N, N, ldc=hist_ld)
+                self._multi(("next", bi), self.h, [dict(w=self.kvw, out=hist[:, sub]),
+                                                   dict(w=self.blocks[bi + 1]["qkv"], out=self.qkv)])
+            else:
+                # the final-CA query of the last hidden state (tria.py:1580)
+                self._multi(("next", bi), self.h, [dict(w=self.wqk, out=self.q_ca)])
         # ---- temporal carry + PolARM on fires (loomformer.py:4053-4085), in place
         self._call("loom_tria_decode_temporal", self.code, _P(self.carry[carry_i]),
                    None if first else _P(self.doc), None if first else _P(self.reset_now),
@@ -264,12 +282,11 @@ class LoomDecoder:
         self._linear(self.z32, self.up_w, self.a_t, B, N, 32, bias=self.up_b)
         # ---- final cross-attention step (tria.py:1560-1595): stage k/v, append on
         # fire (+ end-of-step bookkeeping), then attend over the appended keys
-        self._linear(self.a_t, self.wqk, self.stage_k, B, N, N)
-        self._linear(self.a_t, self.wv, self.stage_v, B, N, N)
+        self._multi("stage", self.a_t, [dict(w=self.wqk, out=self.stage_k),
+                                        dict(w=self.wv, out=self.stage_v)])
         self._call("loom_decode_epilogue", self.code, _P(self.stage_k), _P(self.stage_v),
                    _P(self.ca_k), _P(self.ca_v), _P(self.ca_valid), _P(self.ca_len), _P(self.fire),
                    _P(self.pending), _P(self.pos_dev), B, N, self.max_keys, st)
-        self._linear(self.h, self.wqk, self.q_ca, B, N, N)
         self._call("loom_final_ca_sparse_strided", self.code, _P(self.q_ca), _P(self.ca_k),
                    _P(self.ca_v), self.max_keys * N, _P(self.ca_valid), self.max_keys,
                    _P(self.h), float(self.gamma), _P(self.h2), None, B, 1, self.max_keys,

@@ -1,5 +1,6 @@
 """GPU parity of the decode-step kernels against fp32 references (oracle ops
 or plain torch on the CPU)."""
+import ctypes
 import math
 
 import pytest
@@ -245,3 +246,41 @@ def test_argmax_rows_first_index_on_ties(dtype):
     L().call("loom_argmax_rows", code(xd), P(xd), 33, 4096, P(ids), S(xd))
     assert torch.equal(ids.cpu(), torch.argmax(host(xd), dim=-1))
     assert int(ids[3]) == 100 and int(ids[7]) == 0
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("M", [1, 3, 32, 64])
+def test_linear_multi(dtype, M):
+    """Fused decode projections: output segments sharing x (own weights,
+    strided outputs, bias, gate) and concatenation along k, against fp32
+    products of the same (dtype-rounded) operands."""
+    from loom_amd import _lib
+    g = torch.Generator().manual_seed(M)
+    K, K2 = 768, 256
+    r = lambda *s: (torch.randn(*s, generator=g) * 0.5).to(DEV, dtype)
+    xw = r(M, K + 8)
+    x = xw[:, :K]                                   # row stride K + 8
+    w0, w1, w2 = r(64, K), r(96, K), r(40, K)
+    b1 = torch.randn(96, generator=g).to(DEV)
+    gate = r(M, 96)
+    wide = torch.zeros(M, 200, device=DEV, dtype=dtype)
+    out0 = wide[:, 16:80]                           # strided output view
+    out1 = torch.zeros(M, 96, device=DEV, dtype=dtype)
+    out2 = torch.zeros(M, 40, device=DEV, dtype=dtype)
+    d = _lib.linear_multi_desc(x, [dict(w=w0, out=out0),
+                                   dict(w=w1, out=out1, bias=b1, gate_p=gate, gate_alpha=0.3),
+                                   dict(w=w2, out=out2)])
+    _lib.call("loom_linear_multi", code(x), ctypes.byref(d), S(x))
+    X = host(x)
+    check(out0, X @ host(w0).T, dtype)
+    check(out1, (X @ host(w1).T) * (1 + 0.3 * host(gate)) + host(b1), dtype)
+    check(out2, X @ host(w2).T, dtype)
+    assert bool((wide[:, :16] == 0).all()) and bool((wide[:, 80:] == 0).all())
+    # concatenation along k: out = x w^T + x2 w2^T + b
+    x2 = r(M, K2)
+    wa, wb = r(768, K), r(768, K2)
+    bb = torch.randn(768, generator=g).to(DEV)
+    out = torch.zeros(M, 768, device=DEV, dtype=dtype)
+    d = _lib.linear_multi_desc(x, [dict(w=wa, w2=wb, out=out, bias=bb)], x2=x2)
+    _lib.call("loom_linear_multi", code(x), ctypes.byref(d), S(x))
+    check(out, X @ host(wa).T + host(x2) @ host(wb).T + host(bb), dtype)
