@@ -141,6 +141,51 @@ int loom_linear_multi(int dtype, const loom_linear_multi_desc* desc, void* strea
 /* sizeof(loom_linear_multi_desc), so an FFI binding can check its layout. */
 int64_t loom_linear_multi_desc_bytes(void);
 
+/* One decode token (T = 1) of the Paraplex FFN core and the Tria depth op. */
+typedef struct {
+    /* beta space, as loom_beta_forward */
+    const void* u;
+    const void* q_h;
+    const void* k_ctx_h;
+    const void* c_h;
+    const void* d_h;
+    const void* w_compact;
+    int64_t M, N, H, imag_in, hidden_per_q_head, head_dim, n_q_heads;
+    int32_t open_sectors;
+    /* Paraplex pointwise, as loom_paraplex_forward with T = 1 and gate_src = p_real */
+    const void* p_real;        /* R [M, H] */
+    const float* imag_bias;    /* [H] */
+    void* trace;               /* [M, H]: previous phase in, this token's phase out */
+    const float* trace_w;      /* [H] */
+    float powlu_m;
+    void* act;                 /* [M, H] out */
+    void* s;                   /* [M, H] out; optional on the fused path */
+    void* beta;                /* [M, H] scratch; optional on the fused path */
+    /* Tria depth op on (p_real, s, act), as loom_tria_depth_forward with T = 1 */
+    const void* carry_prev;
+    const void* seed;
+    const uint8_t* seed_valid;
+    const void* gate_w;
+    void* carry_out;
+    void* p_out;
+    float alpha;
+    int32_t axis;
+} loom_ffn_decode_desc;
+
+/* beta = beta_space(u, q, kctx, c, d); (act, s, trace) = paraplex(R, beta);
+ * (carry_out, p_out) = tria_depth(R, s, act) for one decode token: the
+ * sequence loom_beta_forward -> loom_paraplex_forward -> loom_tria_depth_forward
+ * of Model.step's FFN and depth step (loomformer.py:2818-2893, :4012-4040).
+ * No counterpart in the reference as one call.  bf16 with M <= 64 runs as one
+ * launch whose epilogue evaluates the pointwise chain and the Tria op on the
+ * product in registers (beta and s stay on chip; R, s, act enter the Tria op
+ * rounded to bf16 as the unfused sequence stores them); other cases run the
+ * three entry points in turn and need the beta and s buffers. */
+int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* desc, void* stream);
+
+/* sizeof(loom_ffn_decode_desc), so an FFI binding can check its layout. */
+int64_t loom_ffn_decode_desc_bytes(void);
+
 /* ---------------------------------------------------------------------------
  * Depth attention
  * ------------------------------------------------------------------------ */

@@ -19,34 +19,6 @@ namespace loom {
 
 constexpr int kDepthChunk = 8;
 
-// EPL elements of one row as raw 32-bit words (16-bit types stay packed);
-// EPL is even on every path that uses it.
-template <typename T, int EPL>
-struct RawRow {
-    static constexpr int NW = (int)(sizeof(T) * EPL / 4);
-    uint32_t w[NW];
-    __device__ __forceinline__ void load(const T* p) {
-        const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-#pragma unroll
-        for (int k = 0; k < NW; ++k) w[k] = q[k];
-    }
-    __device__ __forceinline__ void to_float(float v[EPL]) const {
-#pragma unroll
-        for (int k = 0; k < NW; ++k) {
-            if constexpr (sizeof(T) == 4) {
-                v[k] = __uint_as_float(w[k]);
-            } else if constexpr (std::is_same<T, bf16_t>::value) {
-                v[2 * k] = __uint_as_float(w[k] << 16);
-                v[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
-            } else {
-                T lo{(uint16_t)(w[k] & 0xffffu)}, hi{(uint16_t)(w[k] >> 16)};
-                v[2 * k] = ld(&lo);
-                v[2 * k + 1] = ld(&hi);
-            }
-        }
-    }
-};
-
 template <typename T, int EPL>
 __global__ void __launch_bounds__(256)
 depth_attn_kernel(const T* __restrict__ q, const T* __restrict__ hk, const T* __restrict__ hv,

@@ -19,6 +19,8 @@
 #include <type_traits>
 
 #include "loom_common.h"
+#include "paraplex_math.h"
+#include "tria_math.h"
 
 namespace loom {
 
@@ -194,21 +196,20 @@ gemm_bf16_mfma_kernel(GemmArgs a) {
 // 8 consecutive k at 8*(l/16)), kUnroll k-steps at a time so each lane keeps
 // several 16-byte weight loads in flight.  The four partial tiles are summed
 // through LDS and the epilogue is applied by all 256 threads.
-constexpr int SK_WAVES = 4, SK_UNROLL = 4;
-
-template <int MT, bool GATHER>
-__global__ void __launch_bounds__(256)
-gemm_bf16_skinny_kernel(GemmArgs a) {
-    __shared__ float red[SK_WAVES][MT][4][64];
+// Main loop of the skinny product for the 16 columns starting at n0: every
+// wave accumulates its k-range, the partial tiles land in red[] (summed by the
+// caller's epilogue after the barrier).
+template <int MT, bool GATHER, int NW, int UN>
+__device__ __forceinline__ void skinny_mainloop(const GemmArgs& a, int64_t n0,
+                                                float (&red)[NW][MT][4][64]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t n0 = (int64_t)blockIdx.x * 16;
     const int64_t g = GATHER ? n0 / a.Hq : 0;
     const int fr = lane & 15, fk = (lane >> 4) * 8;
     const uint16_t* W = (const uint16_t*)a.W;
     const uint16_t* X = (const uint16_t*)a.X;
     // k range of this wave, in whole 32-wide steps
     const int64_t nsteps = ceil_div(a.K, 32);
-    const int64_t per = ceil_div(nsteps, SK_WAVES);
+    const int64_t per = ceil_div(nsteps, NW);
     const int64_t s_begin = wave * per;
     const int64_t s_end = s_begin + per < nsteps ? s_begin + per : nsteps;
     const int64_t n = n0 + fr;
@@ -218,11 +219,11 @@ gemm_bf16_skinny_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < MT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int64_t s0 = s_begin; s0 < s_end; s0 += SK_UNROLL) {
-        uint4 wv[SK_UNROLL];
-        uint4 xv[SK_UNROLL][MT];
+    for (int64_t s0 = s_begin; s0 < s_end; s0 += UN) {
+        uint4 wv[UN];
+        uint4 xv[UN][MT];
 #pragma unroll
-        for (int u = 0; u < SK_UNROLL; ++u) {
+        for (int u = 0; u < UN; ++u) {
             const int64_t k = (s0 + u) * 32 + fk;
             const bool kin = (s0 + u) < s_end && k < a.K;
             wv[u] = (kin && nvalid) ? *reinterpret_cast<const uint4*>(W + n * a.ldw + k)
@@ -241,7 +242,7 @@ gemm_bf16_skinny_kernel(GemmArgs a) {
             }
         }
 #pragma unroll
-        for (int u = 0; u < SK_UNROLL; ++u)
+        for (int u = 0; u < UN; ++u)
 #pragma unroll
             for (int j = 0; j < MT; ++j)
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -253,18 +254,124 @@ gemm_bf16_skinny_kernel(GemmArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) red[wave][j][r][lane] = acc[j][r];
     __syncthreads();
-    // output (m, nn) with nn = n - n0; accumulator element: lane = m%16 + 16*(nn/4), r = nn%4
+}
+
+// Sum of the NW partial tiles for output (row mi, column nn) of the block:
+// accumulator element of (m, nn) sits in lane m%16 + 16*(nn/4), register nn%4.
+template <int MT, int NW>
+__device__ __forceinline__ float skinny_sum(const float (&red)[NW][MT][4][64], int mi, int nn) {
+    const int j = mi >> 4, ml = mi & 15;
+    const int ln = ml + 16 * (nn >> 2), r = nn & 3;
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) v += red[w][j][r][ln];
+    return v;
+}
+
+template <int MT, bool GATHER, int NW, int UN>
+__global__ void __launch_bounds__(NW * 64)
+gemm_bf16_skinny_kernel(GemmArgs a) {
+    __shared__ float red[NW][MT][4][64];
+    const int64_t n0 = (int64_t)blockIdx.x * 16;
+    skinny_mainloop<MT, GATHER, NW, UN>(a, n0, red);
     uint16_t* out = (uint16_t*)a.out;
-    for (int o = tid; o < MT * 256; o += 256) {
+    for (int o = threadIdx.x; o < MT * 256; o += NW * 64) {
         const int nn = o & 15, mi = o >> 4;       // mi in [0, 16*MT)
-        const int j = mi >> 4, ml = mi & 15;
         const int64_t m = mi, nidx = n0 + nn;
         if (m >= a.M || nidx >= a.N) continue;
-        const int ln = ml + 16 * (nn >> 2), r = nn & 3;
-        float v = 0.0f;
-#pragma unroll
-        for (int w = 0; w < SK_WAVES; ++w) v += red[w][j][r][ln];
+        const float v = skinny_sum<MT, NW>(red, mi, nn);
         out[m * a.ldc + nidx] = f32_to_bf16(epilogue<bf16_t>(a, m, nidx, v));
+    }
+}
+
+// ------------------------------------------------------------------ fused decode FFN core
+// One decode token of the Paraplex FFN and the Tria depth op in one launch
+// (bf16): the beta-space gather product, then per output (b, h) in the
+// epilogue the fused pointwise chain (phase, trace combine with the carried
+// phase, softplus, PvPowLU; loomformer.py:2533-2560) and the Tria carrier
+// composed onto the previous depth carry with its gate mix (tria.py:890-978).
+// beta and I never leave registers.
+struct FfnArgs {
+    GemmArgs g;                 // beta space: out unused
+    const uint16_t* R;          // p_real [M, H]
+    const float* ib;            // w1_imag_bias [H]
+    uint16_t* trace;            // [M, H]: previous phase in, this token's phase out
+    const float* tw;            // [H]
+    float m;
+    uint16_t* act;              // [M, H]
+    uint16_t* s;                // [M, H] or null
+    const uint16_t* prev;       // [M, H, 9] (mode 1)
+    const uint16_t* seed;       // [M, H, 9] (mode 2)
+    const uint8_t* valid;       // [M] (mode 2)
+    const uint16_t* gate_w;     // [9] or null
+    uint16_t* carry;            // [M, H, 9]
+    uint16_t* p;                // [M, H] (with gate_w)
+    float alpha;
+    int mode, axis;
+};
+
+__device__ __forceinline__ float bf(uint16_t x) { return bf16_to_f32(x); }
+__device__ __forceinline__ float round_bf(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+template <int AXIS>
+__device__ __forceinline__ void ffn_tria(const FfnArgs& f, int64_t e, int64_t m, float r, float i,
+                                         float o) {
+    float mt[9], pre[9];
+    carrier9<AXIS>(r, i, o, f.alpha, mt);
+    if (f.mode == 1 || (f.mode == 2 && f.valid[m] != 0)) {
+        const uint16_t* src = (f.mode == 1 ? f.prev : f.seed) + e * 9;
+        float cp[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) cp[k] = bf(src[k]);
+        mm3(mt, cp, pre);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 9; ++k) pre[k] = mt[k];
+    }
+    const float inv = 1.0f / rms9(pre);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) pre[k] *= inv;
+    if (f.gate_w != nullptr) {
+        float pv = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) pv = fmaf(pre[k], bf(f.gate_w[k]), pv);
+        f.p[e] = f32_to_bf16(pv);
+    }
+#pragma unroll
+    for (int k = 0; k < 9; ++k) f.carry[e * 9 + k] = f32_to_bf16(pre[k]);
+}
+
+template <int MT, int NW, int UN>
+__global__ void __launch_bounds__(NW * 64)
+ffn_decode_kernel(FfnArgs f) {
+    __shared__ float red[NW][MT][4][64];
+    const int64_t n0 = (int64_t)blockIdx.x * 16;
+    skinny_mainloop<MT, true, NW, UN>(f.g, n0, red);
+    const int64_t H = f.g.N;
+    for (int o = threadIdx.x; o < MT * 256; o += NW * 64) {
+        const int nn = o & 15, mi = o >> 4;
+        const int64_t m = mi, h = n0 + nn;
+        if (m >= f.g.M || h >= H) continue;
+        const int64_t e = m * H + h;
+        const float beta = skinny_sum<MT, NW>(red, mi, nn);
+        // Paraplex pointwise, one token: prev phase = the carried trace
+        const float s0 = phase_of(beta + f.ib[h]);
+        const float raw = fmaf(bf(f.trace[e]), f.tw[h], s0);
+        const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
+        const float x = bf(f.R[e]);
+        float amp, gate;
+        softplus_gate(x, f.m, amp, gate);
+        const float act = fmaf(amp, sv, x) * gate;
+        f.trace[e] = f32_to_bf16(s0);
+        f.act[e] = f32_to_bf16(act);
+        if (f.s != nullptr) f.s[e] = f32_to_bf16(sv);
+        // Tria depth op on (r, i, o) = (R, I, O) as stored
+        const float i_ = round_bf(sv), o_ = round_bf(act);
+        switch (f.axis) {
+            case 0: ffn_tria<0>(f, e, m, x, i_, o_); break;
+            case 1: ffn_tria<1>(f, e, m, x, i_, o_); break;
+            default: ffn_tria<2>(f, e, m, x, i_, o_); break;
+        }
     }
 }
 
@@ -304,10 +411,10 @@ struct LinArgs {
     LinSeg seg[kMaxSeg];
 };
 
-template <int MT>
-__global__ void __launch_bounds__(256)
+template <int MT, int NW, int UN>
+__global__ void __launch_bounds__(NW * 64)
 gemm_bf16_skinny_multi_kernel(LinArgs a) {
-    __shared__ float red[SK_WAVES][MT][4][64];
+    __shared__ float red[NW][MT][4][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t ng = (int64_t)blockIdx.x * 16;
     int s = 0;
@@ -319,7 +426,7 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
     const int64_t n = n0 + fr;
     const bool nvalid = n < sg.n;
     const int64_t S1 = ceil_div(a.K, 32), S2 = ceil_div(a.K2, 32), S = S1 + S2;
-    const int64_t per = ceil_div(S, SK_WAVES);
+    const int64_t per = ceil_div(S, NW);
     const int64_t s_begin = wave * per;
     const int64_t s_end = s_begin + per < S ? s_begin + per : S;
 
@@ -327,11 +434,11 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
 #pragma unroll
     for (int j = 0; j < MT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int64_t s0 = s_begin; s0 < s_end; s0 += SK_UNROLL) {
-        uint4 wv[SK_UNROLL];
-        uint4 xv[SK_UNROLL][MT];
+    for (int64_t s0 = s_begin; s0 < s_end; s0 += UN) {
+        uint4 wv[UN];
+        uint4 xv[UN][MT];
 #pragma unroll
-        for (int u = 0; u < SK_UNROLL; ++u) {
+        for (int u = 0; u < UN; ++u) {
             const int64_t step = s0 + u;
             const bool first = step < S1;
             const int64_t k = (first ? step : step - S1) * 32 + fk;
@@ -348,7 +455,7 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
             }
         }
 #pragma unroll
-        for (int u = 0; u < SK_UNROLL; ++u)
+        for (int u = 0; u < UN; ++u)
 #pragma unroll
             for (int j = 0; j < MT; ++j)
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -361,7 +468,7 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
         for (int r = 0; r < 4; ++r) red[wave][j][r][lane] = acc[j][r];
     __syncthreads();
     uint16_t* out = (uint16_t*)sg.out;
-    for (int o = tid; o < MT * 256; o += 256) {
+    for (int o = tid; o < MT * 256; o += NW * 64) {
         const int nn = o & 15, mi = o >> 4;
         const int j = mi >> 4, ml = mi & 15;
         const int64_t m = mi, nidx = n0 + nn;
@@ -369,7 +476,7 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
         const int ln = ml + 16 * (nn >> 2), r = nn & 3;
         float v = 0.0f;
 #pragma unroll
-        for (int w = 0; w < SK_WAVES; ++w) v += red[w][j][r][ln];
+        for (int w = 0; w < NW; ++w) v += red[w][j][r][ln];
         if (sg.gate_p != nullptr)
             v *= 1.0f + sg.gate_alpha * ld((const bf16_t*)sg.gate_p + m * sg.gate_ld + nidx);
         if (sg.bias != nullptr) v += sg.bias[nidx];
@@ -459,6 +566,35 @@ gemm_naive_kernel(GemmArgs a) {
     st((T*)a.out + m * a.ldc + n, epilogue<T>(a, m, n, acc));
 }
 
+// Waves per block and k-steps in flight per wave for a skinny product of
+// `steps` 32-wide k-steps and MT 16-row m-tiles: enough waves that each makes
+// one pass (a single round of weight loads) where the registers allow it:
+// 8 steps in flight only for one m-tile, 16 waves only up to 3 m-tiles.
+static void skinny_shape(int64_t steps, int mt, int& nw, int& un) {
+    un = 4;
+    if (steps <= 16) nw = 4;
+    else if (steps <= 32 || mt >= 4) nw = 8;
+    else nw = 16;
+    if (nw == 16 && mt == 1 && steps > 64) un = 8;
+}
+
+template <int MT, bool GATHER>
+static void launch_skinny(const GemmArgs& a, dim3 grid, hipStream_t st) {
+    int nw, un;
+    skinny_shape(ceil_div(a.K, 32), MT, nw, un);
+    if (nw == 4) {
+        hipLaunchKernelGGL((gemm_bf16_skinny_kernel<MT, GATHER, 4, 4>), grid, dim3(256), 0, st, a);
+    } else if (nw == 8) {
+        hipLaunchKernelGGL((gemm_bf16_skinny_kernel<MT, GATHER, 8, 4>), grid, dim3(512), 0, st, a);
+    } else if constexpr (MT <= 3) {
+        if (un == 4 || MT > 1)
+            hipLaunchKernelGGL((gemm_bf16_skinny_kernel<MT, GATHER, 16, 4>), grid, dim3(1024), 0, st, a);
+        else
+            hipLaunchKernelGGL((gemm_bf16_skinny_kernel<MT, GATHER, 16, (MT == 1 ? 8 : 4)>), grid,
+                               dim3(1024), 0, st, a);
+    }
+}
+
 template <typename T, bool GATHER>
 static int run_gemm(const GemmArgs& a, hipStream_t st, const char* what) {
     if (a.M == 0 || a.N == 0) return LOOM_OK;
@@ -472,12 +608,11 @@ static int run_gemm(const GemmArgs& a, hipStream_t st, const char* what) {
             sk = sk && a.ldx % 8 == 0 && ((uintptr_t)a.X & 15) == 0;
         if (sk) {
             const dim3 grid((unsigned)ceil_div(a.N, 16));
-            const int mt = (int)ceil_div(a.M, 16);
-            switch (mt) {
-                case 1: hipLaunchKernelGGL((gemm_bf16_skinny_kernel<1, GATHER>), grid, dim3(256), 0, st, a); break;
-                case 2: hipLaunchKernelGGL((gemm_bf16_skinny_kernel<2, GATHER>), grid, dim3(256), 0, st, a); break;
-                case 3: hipLaunchKernelGGL((gemm_bf16_skinny_kernel<3, GATHER>), grid, dim3(256), 0, st, a); break;
-                default: hipLaunchKernelGGL((gemm_bf16_skinny_kernel<4, GATHER>), grid, dim3(256), 0, st, a); break;
+            switch ((int)ceil_div(a.M, 16)) {
+                case 1: launch_skinny<1, GATHER>(a, grid, st); break;
+                case 2: launch_skinny<2, GATHER>(a, grid, st); break;
+                case 3: launch_skinny<3, GATHER>(a, grid, st); break;
+                default: launch_skinny<4, GATHER>(a, grid, st); break;
             }
             return launch_status(what);
         }
@@ -561,6 +696,32 @@ extern "C" int loom_linear(int dtype, const void* A, int64_t lda, const void* W,
     return LOOM_ERR_INVALID;
 }
 
+template <int MT>
+static void launch_skinny_multi_mt(const LinArgs& a, dim3 grid, int64_t steps, hipStream_t st) {
+    int nw, un;
+    skinny_shape(steps, MT, nw, un);
+    if (nw == 4) {
+        hipLaunchKernelGGL((gemm_bf16_skinny_multi_kernel<MT, 4, 4>), grid, dim3(256), 0, st, a);
+    } else if (nw == 8) {
+        hipLaunchKernelGGL((gemm_bf16_skinny_multi_kernel<MT, 8, 4>), grid, dim3(512), 0, st, a);
+    } else if constexpr (MT <= 3) {
+        if (un == 4 || MT > 1)
+            hipLaunchKernelGGL((gemm_bf16_skinny_multi_kernel<MT, 16, 4>), grid, dim3(1024), 0, st, a);
+        else
+            hipLaunchKernelGGL((gemm_bf16_skinny_multi_kernel<MT, 16, (MT == 1 ? 8 : 4)>), grid,
+                               dim3(1024), 0, st, a);
+    }
+}
+
+static void launch_skinny_multi(const LinArgs& a, dim3 grid, int mt, int64_t steps, hipStream_t st) {
+    switch (mt) {
+        case 1: launch_skinny_multi_mt<1>(a, grid, steps, st); break;
+        case 2: launch_skinny_multi_mt<2>(a, grid, steps, st); break;
+        case 3: launch_skinny_multi_mt<3>(a, grid, steps, st); break;
+        default: launch_skinny_multi_mt<4>(a, grid, steps, st); break;
+    }
+}
+
 // Host side of loom_linear_multi: one fused launch for bf16 when every piece
 // is 16-byte aligned, otherwise (and for fp32 / fp16) one product per segment
 // and input, the second input accumulated through the residual epilogue.
@@ -589,12 +750,8 @@ static int linear_multi_dispatch(const loom_linear_multi_desc& d, hipStream_t st
         }
         for (int s = d.nseg; s <= kMaxSeg; ++s) a.nstart[s] = ncols;
         const dim3 grid((unsigned)(ncols / 16));
-        switch (ceil_div(d.m, 16)) {
-            case 1: hipLaunchKernelGGL((gemm_bf16_skinny_multi_kernel<1>), grid, dim3(256), 0, st, a); break;
-            case 2: hipLaunchKernelGGL((gemm_bf16_skinny_multi_kernel<2>), grid, dim3(256), 0, st, a); break;
-            case 3: hipLaunchKernelGGL((gemm_bf16_skinny_multi_kernel<3>), grid, dim3(256), 0, st, a); break;
-            default: hipLaunchKernelGGL((gemm_bf16_skinny_multi_kernel<4>), grid, dim3(256), 0, st, a); break;
-        }
+        const int64_t steps = ceil_div(d.k, 32) + ceil_div(d.k2, 32);
+        launch_skinny_multi(a, grid, (int)ceil_div(d.m, 16), steps, st);
         return launch_status("loom_linear_multi");
     }
     for (int s = 0; s < d.nseg; ++s) {
@@ -647,6 +804,78 @@ extern "C" int loom_linear_multi(int dtype, const loom_linear_multi_desc* d, voi
     }
     set_error("linear_multi: unsupported dtype %d", dtype);
     return LOOM_ERR_INVALID;
+}
+
+extern "C" int64_t loom_ffn_decode_desc_bytes(void) { return (int64_t)sizeof(loom_ffn_decode_desc); }
+
+template <int MT>
+static void launch_ffn_mt(const FfnArgs& f, dim3 grid, hipStream_t st) {
+    int nw, un;
+    skinny_shape(ceil_div(f.g.K, 32), MT, nw, un);
+    if (nw == 4) hipLaunchKernelGGL((ffn_decode_kernel<MT, 4, 4>), grid, dim3(256), 0, st, f);
+    else if (nw == 8) hipLaunchKernelGGL((ffn_decode_kernel<MT, 8, 4>), grid, dim3(512), 0, st, f);
+    else if constexpr (MT <= 3) hipLaunchKernelGGL((ffn_decode_kernel<MT, 16, 4>), grid, dim3(1024), 0, st, f);
+}
+
+extern "C" int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* d, void* stream) {
+    clear_error();
+    LOOM_CHECK(d != nullptr, "ffn_decode: null descriptor");
+    LOOM_CHECK(d->u && d->q_h && d->k_ctx_h && d->c_h && d->d_h && d->w_compact && d->p_real &&
+                   d->imag_bias && d->trace && d->trace_w && d->act && d->carry_out,
+               "ffn_decode: null tensor argument");
+    LOOM_CHECK(d->axis >= 0 && d->axis <= 2, "ffn_decode: axis must be 0(z), 1(x), or 2(y), got %d",
+               (int)d->axis);
+    LOOM_CHECK(!(d->carry_prev && d->seed), "ffn_decode: carry_prev and seed are mutually exclusive");
+    LOOM_CHECK(!d->seed || d->seed_valid, "ffn_decode: seed needs seed_valid");
+    LOOM_CHECK(!d->gate_w || d->p_out, "ffn_decode: gate weights need p_out");
+    LOOM_CHECK(d->M >= 0 && d->N > 0 && d->H > 0 && d->head_dim > 0 && d->n_q_heads > 0 &&
+                   d->n_q_heads * d->head_dim == d->N && d->hidden_per_q_head * d->n_q_heads == d->H,
+               "ffn_decode: bad shape");
+    const int64_t want = d->open_sectors ? 4 * d->N + d->head_dim : d->N + 4 * d->head_dim;
+    LOOM_CHECK(d->imag_in == want, "ffn_decode: imag_in=%lld, expected %lld", (long long)d->imag_in,
+               (long long)want);
+    if (d->M == 0) return LOOM_OK;
+    const uintptr_t al = (uintptr_t)d->u | (uintptr_t)d->q_h | (uintptr_t)d->k_ctx_h |
+                         (uintptr_t)d->c_h | (uintptr_t)d->d_h | (uintptr_t)d->w_compact;
+    const bool fused = dtype == LOOM_BF16 && d->M <= 64 && d->imag_in % 8 == 0 &&
+                       d->hidden_per_q_head % 16 == 0 && d->head_dim % 8 == 0 && d->N % 8 == 0 &&
+                       (al & 15) == 0;
+    if (fused) {
+        FfnArgs f{};
+        GemmArgs& a = f.g;
+        a.W = d->w_compact; a.ldw = d->imag_in; a.M = d->M; a.N = d->H; a.K = d->imag_in;
+        a.src[0] = d->q_h; a.src[1] = d->k_ctx_h; a.src[2] = d->c_h; a.src[3] = d->u; a.src[4] = d->d_h;
+        a.Nm = d->N; a.HD = d->head_dim; a.Hq = d->hidden_per_q_head; a.open = d->open_sectors ? 1 : 0;
+        a.X = d->u; a.ldx = d->N;
+        f.R = (const uint16_t*)d->p_real; f.ib = d->imag_bias; f.trace = (uint16_t*)d->trace;
+        f.tw = d->trace_w; f.m = d->powlu_m; f.act = (uint16_t*)d->act; f.s = (uint16_t*)d->s;
+        f.prev = (const uint16_t*)d->carry_prev; f.seed = (const uint16_t*)d->seed;
+        f.valid = d->seed_valid; f.gate_w = (const uint16_t*)d->gate_w;
+        f.carry = (uint16_t*)d->carry_out; f.p = (uint16_t*)d->p_out; f.alpha = d->alpha;
+        f.mode = d->carry_prev ? 1 : (d->seed ? 2 : 0);
+        f.axis = d->axis;
+        const dim3 grid((unsigned)ceil_div(d->H, 16));
+        hipStream_t st = (hipStream_t)stream;
+        switch ((int)ceil_div(d->M, 16)) {
+            case 1: launch_ffn_mt<1>(f, grid, st); break;
+            case 2: launch_ffn_mt<2>(f, grid, st); break;
+            case 3: launch_ffn_mt<3>(f, grid, st); break;
+            default: launch_ffn_mt<4>(f, grid, st); break;
+        }
+        return launch_status("loom_ffn_decode");
+    }
+    LOOM_CHECK(d->beta && d->s, "ffn_decode: the unfused path needs the beta and s buffers");
+    int rc = loom_beta_forward(dtype, d->u, d->q_h, d->k_ctx_h, d->c_h, d->d_h, d->w_compact,
+                               d->beta, nullptr, d->M, d->N, d->H, d->imag_in, d->hidden_per_q_head,
+                               d->head_dim, d->n_q_heads, d->open_sectors, stream);
+    if (rc != LOOM_OK) return rc;
+    rc = loom_paraplex_forward(dtype, d->p_real, d->p_real, d->beta, d->imag_bias, d->trace,
+                               d->trace_w, nullptr, nullptr, d->act, d->s, d->trace, nullptr, d->M,
+                               1, d->H, d->powlu_m, stream);
+    if (rc != LOOM_OK) return rc;
+    return loom_tria_depth_forward(dtype, d->p_real, d->s, d->act, d->carry_prev, d->seed,
+                                   d->seed_valid, d->gate_w, d->carry_out, d->p_out, nullptr, d->M,
+                                   1, d->H, d->alpha, d->axis, stream);
 }
 
 extern "C" int loom_beta_forward(int dtype, const void* u, const void* q_h, const void* k_ctx_h,

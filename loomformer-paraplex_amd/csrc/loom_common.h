@@ -9,6 +9,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/loom_hip.h"
 
 namespace loom {
@@ -158,6 +160,52 @@ struct RowIO {
         } else {
 #pragma unroll
             for (int k = 0; k < EPL; ++k) st(p + k, v[k]);
+        }
+    }
+};
+
+// EPL elements of one row held as the raw words loaded from memory (16-bit
+// types stay packed two to a register until to_float); p must be 4-byte
+// aligned when EPL is even.
+template <typename T, int EPL>
+struct RawRow {
+    static constexpr bool kPairs = sizeof(T) == 4 || EPL % 2 == 0;
+    static constexpr int NW = sizeof(T) == 4 ? EPL : (kPairs ? EPL / 2 : EPL);
+    uint32_t w[NW];
+    __device__ __forceinline__ void load(const T* p) {
+        if constexpr (kPairs) {
+            const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+            for (int k = 0; k < NW; ++k) w[k] = q[k];
+        } else {
+            const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
+#pragma unroll
+            for (int k = 0; k < NW; ++k) w[k] = q[k];
+        }
+    }
+    // Hide the words' values from the compiler (no instruction is emitted), so a
+    // later to_float recomputes the unpacking instead of keeping an earlier
+    // unpacked copy alive in registers.
+    __device__ __forceinline__ void opaque() {
+#pragma unroll
+        for (int k = 0; k < NW; ++k) asm volatile("" : "+v"(w[k]));
+    }
+    __device__ __forceinline__ void to_float(float v[EPL]) const {
+#pragma unroll
+        for (int k = 0; k < NW; ++k) {
+            if constexpr (sizeof(T) == 4) {
+                v[k] = __uint_as_float(w[k]);
+            } else if constexpr (!kPairs) {
+                const T one{(uint16_t)w[k]};
+                v[k] = ld(&one);
+            } else if constexpr (std::is_same<T, bf16_t>::value) {
+                v[2 * k] = __uint_as_float(w[k] << 16);
+                v[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+            } else {
+                T lo{(uint16_t)(w[k] & 0xffffu)}, hi{(uint16_t)(w[k] >> 16)};
+                v[2 * k] = ld(&lo);
+                v[2 * k + 1] = ld(&hi);
+            }
         }
     }
 };

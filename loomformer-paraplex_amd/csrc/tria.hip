@@ -9,52 +9,11 @@
 #include <cmath>
 
 #include "loom_common.h"
+#include "tria_math.h"
 
 namespace loom {
 
 constexpr int kTriaThreads = 256;
-
-// Local carrier T(r,i,o) = (I + K(a,b,c)) @ R_axis,
-// (a,b,c) = alpha * tanh(x / sqrt(mean(x^2) + eps)), x = (ri, ro, io).
-// The axis is a compile-time parameter: the kernels are instantiated per axis.
-template <int AXIS>
-__device__ __forceinline__ void carrier9(float r, float i, float o, float alpha, float mt[9]) {
-    const float x0 = r * i, x1 = r * o, x2 = i * o;
-    const float inv = 1.0f / sqrtf((x0 * x0 + x1 * x1 + x2 * x2) * (1.0f / 3.0f) + 1e-6f);
-    const float a = alpha * tanhf(x0 * inv);
-    const float b = alpha * tanhf(x1 * inv);
-    const float c = alpha * tanhf(x2 * inv);
-    if constexpr (AXIS == 0) {          // about z
-        mt[0] = -c;   mt[1] = -1.0f; mt[2] = b;
-        mt[3] = 1.0f; mt[4] = -c;    mt[5] = -a;
-        mt[6] = a;    mt[7] = b;     mt[8] = 1.0f;
-    } else if constexpr (AXIS == 1) {   // about x
-        mt[0] = 1.0f; mt[1] = b;     mt[2] = c;
-        mt[3] = c;    mt[4] = -a;    mt[5] = -1.0f;
-        mt[6] = -b;   mt[7] = 1.0f;  mt[8] = -a;
-    } else {                  // about y
-        mt[0] = -b;   mt[1] = -c;    mt[2] = 1.0f;
-        mt[3] = a;    mt[4] = 1.0f;  mt[5] = c;
-        mt[6] = -1.0f; mt[7] = a;    mt[8] = -b;
-    }
-}
-
-// out = A @ B for row-major 3x3
-__device__ __forceinline__ void mm3(const float A[9], const float B[9], float out[9]) {
-#pragma unroll
-    for (int r = 0; r < 3; ++r)
-#pragma unroll
-        for (int c = 0; c < 3; ++c)
-            out[3 * r + c] = fmaf(A[3 * r + 2], B[6 + c], fmaf(A[3 * r + 1], B[3 + c], A[3 * r] * B[c]));
-}
-
-// rms over 9 entries with eps inside the root; returns the rms
-__device__ __forceinline__ float rms9(const float v[9]) {
-    float s = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 9; ++k) s = fmaf(v[k], v[k], s);
-    return sqrtf(s * (1.0f / 9.0f) + 1e-6f);
-}
 
 // Copy n9 = rows*9 contiguous values between global memory and LDS with
 // coalesced word accesses.
@@ -397,6 +356,111 @@ final_ca_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __res
         lse[row] = red[0] == -INFINITY ? -INFINITY : red[0] + logf(red[1]);
 }
 
+// Vector form for D % 8 == 0, D <= 1536 and 16-byte aligned rows: q is held as
+// 8-element chunks (lane l: chunks l, l+64, l+128), keys are scored by the
+// waves two at a time with 16-byte loads, wave 0 forms the softmax with its
+// lanes over the keys, and P.V runs one 8-element chunk per thread with the
+// key loop unrolled so several value rows are in flight.
+constexpr int kCaChunks = 3;   // 8-element chunks of q per lane (D <= 3*64*8)
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+final_ca_vec_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+                    int64_t kv_stride_b, const uint8_t* __restrict__ allowed,
+                    int64_t allowed_stride, const T* __restrict__ residual, float gamma,
+                    T* __restrict__ out, float* __restrict__ lse, int64_t T_, int64_t K,
+                    const int64_t* __restrict__ k_dev, int D, float scale) {
+    __shared__ float wts[kCaMaxK];
+    __shared__ float red[2];
+    if (k_dev != nullptr) K = *k_dev < K ? *k_dev : K;   // graph replay: key count on the device
+    const int64_t row = blockIdx.x;
+    const int64_t b = row / T_;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int nch = D / 8;
+    float qf[kCaChunks][8];
+#pragma unroll
+    for (int c = 0; c < kCaChunks; ++c) {
+        const int ch = lane + 64 * c;
+        if (ch < nch) Vec8<T>::load(q + row * D + ch * 8, qf[c]);
+        else
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[c][e] = 0.0f;
+    }
+    const T* kb = k + b * kv_stride_b;
+    for (int64_t j0 = wid; j0 < K; j0 += 8) {            // keys j0 and j0 + 4 per wave
+        float dot[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t j = j0 + 4 * u;
+            if (j >= K) continue;
+#pragma unroll
+            for (int c = 0; c < kCaChunks; ++c) {
+                const int ch = lane + 64 * c;
+                if (ch >= nch) continue;
+                float kv[8];
+                Vec8<T>::load(kb + j * D + ch * 8, kv);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) dot[u] = fmaf(qf[c][e], kv[e], dot[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int64_t j = j0 + 4 * u;
+            const float s = wave_sum(dot[u]) * scale;
+            if (lane == 0 && j < K) wts[j] = allowed[row * allowed_stride + j] ? s : -INFINITY;
+        }
+    }
+    __syncthreads();
+    if (wid == 0) {
+        float mx = -INFINITY;
+        for (int64_t j = lane; j < K; j += 64) mx = fmaxf(mx, wts[j]);
+        mx = wave_max(mx);
+        float sum = 0.0f;
+        for (int64_t j = lane; j < K; j += 64) {
+            const float e = (mx == -INFINITY || wts[j] == -INFINITY) ? 0.0f : fexp(wts[j] - mx);
+            wts[j] = e;
+            sum += e;
+        }
+        sum = wave_sum(sum);
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        for (int64_t j = lane; j < K; j += 64) wts[j] *= inv;
+        if (lane == 0) {
+            red[0] = mx;
+            red[1] = sum;
+        }
+    }
+    __syncthreads();
+    const T* vb = v + b * kv_stride_b;
+    for (int ch = threadIdx.x; ch < nch; ch += blockDim.x) {
+        float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        int64_t j = 0;
+        for (; j + 4 <= K; j += 4) {
+            float vv[4][8];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) Vec8<T>::load(vb + (j + u) * D + ch * 8, vv[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) a[e] = fmaf(wts[j + u], vv[u][e], a[e]);
+        }
+        for (; j < K; ++j) {
+            float vv[8];
+            Vec8<T>::load(vb + j * D + ch * 8, vv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = fmaf(wts[j], vv[e], a[e]);
+        }
+        if (residual != nullptr) {
+            float rr[8];
+            Vec8<T>::load(residual + row * D + ch * 8, rr);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = rr[e] + gamma * a[e];
+        }
+        Vec8<T>::store(out + row * D + ch * 8, a);
+    }
+    if (lse != nullptr && threadIdx.x == 0)
+        lse[row] = red[0] == -INFINITY ? -INFINITY : red[0] + logf(red[1]);
+}
+
 // ---------------------------------------------------------------- dispatch
 
 template <typename T>
@@ -480,9 +544,18 @@ static int final_ca_dispatch(const void* q, const void* k, const void* v, int64_
                              const uint8_t* allowed, int64_t allowed_stride, const void* residual,
                              float gamma, void* out, float* lse, int64_t B, int64_t T_, int64_t K,
                              const int64_t* k_dev, int64_t D, float scale, hipStream_t st) {
-    hipLaunchKernelGGL((final_ca_kernel<T>), dim3((unsigned)(B * T_)), dim3(256), 0, st,
-                       (const T*)q, (const T*)k, (const T*)v, kv_stride_b, allowed, allowed_stride,
-                       (const T*)residual, gamma, (T*)out, lse, T_, K, k_dev, D, scale);
+    const bool vec = D % 8 == 0 && D <= kCaChunks * 64 * 8 && kv_stride_b % 8 == 0 &&
+                     (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out |
+                       (uintptr_t)residual) & 15) == 0;
+    if (vec)
+        hipLaunchKernelGGL((final_ca_vec_kernel<T>), dim3((unsigned)(B * T_)), dim3(256), 0, st,
+                           (const T*)q, (const T*)k, (const T*)v, kv_stride_b, allowed,
+                           allowed_stride, (const T*)residual, gamma, (T*)out, lse, T_, K, k_dev,
+                           (int)D, scale);
+    else
+        hipLaunchKernelGGL((final_ca_kernel<T>), dim3((unsigned)(B * T_)), dim3(256), 0, st,
+                           (const T*)q, (const T*)k, (const T*)v, kv_stride_b, allowed, allowed_stride,
+                           (const T*)residual, gamma, (T*)out, lse, T_, K, k_dev, D, scale);
     return launch_status("loom_final_ca_sparse_forward");
 }
 

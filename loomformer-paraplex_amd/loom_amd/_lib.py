@@ -39,6 +39,7 @@ SIGNATURES = {
     "loom_beta_forward": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64,
                           c_int64, c_int64, c_int64, c_int64, c_int, _P],
     "loom_linear_multi": [c_int, _P, _P],
+    "loom_ffn_decode": [c_int, _P, _P],
     "loom_linear": [c_int, _P, c_int64, _P, c_int64, _P, _P, c_float, _P, _P, c_int64,
                     c_int64, c_int64, c_int64, _P],
     "loom_depth_attn_forward": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64,
@@ -72,7 +73,8 @@ SIGNATURES = {
 }
 # entry points that return a value instead of a status
 QUERIES = {"loom_gqa_workspace_bytes": ([c_int64] * 5, c_int64),
-           "loom_linear_multi_desc_bytes": ([], c_int64)}
+           "loom_linear_multi_desc_bytes": ([], c_int64),
+           "loom_ffn_decode_desc_bytes": ([], c_int64)}
 
 _lib = None
 _lock = threading.Lock()
@@ -122,6 +124,21 @@ def dtype_code(t: torch.Tensor) -> int:
         raise RuntimeError(f"unsupported dtype {t.dtype}; expected float32, bfloat16 or float16")
 
 
+class FfnDecodeDesc(ctypes.Structure):
+    """loom_ffn_decode_desc (include/loom_hip.h)."""
+    _fields_ = [("u", c_void_p), ("q_h", c_void_p), ("k_ctx_h", c_void_p), ("c_h", c_void_p),
+                ("d_h", c_void_p), ("w_compact", c_void_p),
+                ("M", c_int64), ("N", c_int64), ("H", c_int64), ("imag_in", c_int64),
+                ("hidden_per_q_head", c_int64), ("head_dim", c_int64), ("n_q_heads", c_int64),
+                ("open_sectors", ctypes.c_int32),
+                ("p_real", c_void_p), ("imag_bias", c_void_p), ("trace", c_void_p),
+                ("trace_w", c_void_p), ("powlu_m", c_float),
+                ("act", c_void_p), ("s", c_void_p), ("beta", c_void_p),
+                ("carry_prev", c_void_p), ("seed", c_void_p), ("seed_valid", c_void_p),
+                ("gate_w", c_void_p), ("carry_out", c_void_p), ("p_out", c_void_p),
+                ("alpha", c_float), ("axis", ctypes.c_int32)]
+
+
 def linear_multi_desc(x, segments, x2=None, m=None):
     """Build a LinearMultiDesc.  x, x2: [m, k] tensors (row-strided views are
     fine); segments: dicts with w, out and optional w2, bias, gate_p,
@@ -145,6 +162,17 @@ def linear_multi_desc(x, segments, x2=None, m=None):
         if sg.get("gate_p") is not None:
             e.gate_p, e.gate_ld = sg["gate_p"].data_ptr(), sg["gate_p"].stride(0)
             e.gate_alpha = float(sg.get("gate_alpha", 0.0))
+    return d
+
+
+def ffn_decode_desc(**kw):
+    """Build an FfnDecodeDesc from keyword fields; tensors give their device
+    pointers, None gives NULL."""
+    d = FfnDecodeDesc()
+    for k, v in kw.items():
+        if isinstance(v, torch.Tensor):
+            v = v.data_ptr()
+        setattr(d, k, v)
     return d
 
 

@@ -236,27 +236,29 @@ class LoomDecoder:
                 real.update(gate_p=self.p[p_i], gate_alpha=blk["alpha"])
             self._multi(("kvr", bi), self.h, [dict(w=self.kvw, out=hist[:, sub]), real])
             self._depth(sub, self.dh)
-            # ---- Paraplex FFN (loomformer.py:2818-2893, fused path :2533-2560)
-            self._call("loom_beta_forward", self.code, _P(self.h), _P(self.q), _P(self.kctx),
-                       _P(self.c), _P(self.dh), _P(blk["w1i"]), _P(self.beta), None, B, N, H,
-                       c.imag_in, c.Hq, c.HD, c.QH, 1 if c.sectors == "open" else 0, st)
-            tr = self.trace[bi]
-            self._call("loom_paraplex_forward", self.code, _P(self.R), _P(self.R), _P(self.beta),
-                       _P(blk["ib"]), _P(tr), _P(blk["tw"]), None, _P(blk["anchor"]), _P(self.act),
-                       _P(self.s), _P(tr), _P(self.snap), B, 1, H, float(c.powlu_m), st)
-            # ---- Tria depth op (loomformer.py:4012-4040); axis = bi % 3
+            # ---- Paraplex FFN core (beta space, fused pointwise chain; loomformer.py:
+            # 2818-2893, :2533-2560) and the Tria depth op (loomformer.py:4012-4040,
+            # axis = bi % 3) of this token, one launch in bf16
             out_i = 0 if carry_i != 0 else 1
             gate = not last
             new_p = (0 if p_i != 0 else 1) if gate else None
-            prev = None if carry_i is None else self.carry[carry_i]
             use_seed = bi == 0 and not first
-            self._call("loom_tria_depth_forward", self.code, _P(self.R), _P(self.s), _P(self.act),
-                       _P(prev) if not use_seed else None,
-                       _P(self.doc) if use_seed else None,
-                       _P(self.pending) if use_seed else None,
-                       _P(blk["gate_w"]) if gate else None, _P(self.carry[out_i]),
-                       _P(self.p[new_p]) if gate else None, None, B, 1, H, float(c.tria_alpha),
-                       bi % 3, st)
+            key = ("ffn_core", bi, use_seed)
+            d = self._descs.get(key)
+            if d is None:
+                d = _lib.ffn_decode_desc(
+                    u=self.h, q_h=self.q, k_ctx_h=self.kctx, c_h=self.c, d_h=self.dh,
+                    w_compact=blk["w1i"], M=B, N=N, H=H, imag_in=c.imag_in, hidden_per_q_head=c.Hq,
+                    head_dim=c.HD, n_q_heads=c.QH, open_sectors=1 if c.sectors == "open" else 0,
+                    p_real=self.R, imag_bias=blk["ib"], trace=self.trace[bi], trace_w=blk["tw"],
+                    powlu_m=float(c.powlu_m), act=self.act, s=self.s, beta=self.beta,
+                    carry_prev=None if (carry_i is None or use_seed) else self.carry[carry_i],
+                    seed=self.doc if use_seed else None,
+                    seed_valid=self.pending if use_seed else None,
+                    gate_w=blk["gate_w"] if gate else None, carry_out=self.carry[out_i],
+                    p_out=self.p[new_p] if gate else None, alpha=float(c.tria_alpha), axis=bi % 3)
+                self._descs[key] = d
+            self._call("loom_ffn_decode", self.code, _lib.ctypes.byref(d), st)
             carry_i, p_i = out_i, new_p
             # ---- LN(w_o(d_h) + W2(act) + b2) (loomformer.py:4045): one launch + LN
             self._multi(("ffn", bi), self.dh.view(B, N),

@@ -34,6 +34,7 @@ def test_library_exports_every_declared_symbol():
     assert lib.loom_gqa_workspace_bytes(2, 300, 8, 2, 96) == 256 + 2 * 2 * 2 * (8 + 2 * 4 * 96) * 4
     # the ctypes mirror of the descriptor struct has the C layout
     assert lib.loom_linear_multi_desc_bytes() == ctypes.sizeof(_lib.LinearMultiDesc)
+    assert lib.loom_ffn_decode_desc_bytes() == ctypes.sizeof(_lib.FfnDecodeDesc)
 
 
 def test_error_channel_reports_argument_errors():

@@ -284,3 +284,65 @@ def test_linear_multi(dtype, M):
     d = _lib.linear_multi_desc(x, [dict(w=wa, w2=wb, out=out, bias=bb)], x2=x2)
     _lib.call("loom_linear_multi", code(x), ctypes.byref(d), S(x))
     check(out, X @ host(wa).T + host(x2) @ host(wb).T + host(bb), dtype)
+    # a long second input (120 k-steps: the widest block shape)
+    x3 = r(M, 3072)
+    wc = r(768, 3072) * 0.25
+    d = _lib.linear_multi_desc(x, [dict(w=wa, w2=wc, out=out, bias=bb)], x2=x3)
+    _lib.call("loom_linear_multi", code(x), ctypes.byref(d), S(x))
+    check(out, X @ host(wa).T + host(x3) @ host(wc).T + host(bb), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("mode,gate,axis", [(1, True, 0), (1, True, 1), (1, False, 2),
+                                            (0, True, 2), (2, True, 1), (2, False, 0)])
+def test_ffn_decode(dtype, mode, gate, axis):
+    """One decode token of beta space -> Paraplex chain -> Tria depth op (one
+    launch in bf16) against the oracle: beta_space_grouped, paraplex_pointwise
+    and tria_*_and_gate on the same (dtype-rounded) inputs."""
+    from loom_amd import _lib
+    g = torch.Generator().manual_seed(10 * mode + axis + (5 if gate else 0))
+    M, QH, HD, H = 32, 8, 96, 3072
+    N = QH * HD
+    K = N + 4 * HD
+    r = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(DEV, dtype)
+    u = r(M, N)
+    q, kc, c, d = (r(M, QH, HD) for _ in range(4))
+    w = r(H, K, sc=K ** -0.5)
+    R = r(M, H, sc=2.0)
+    ib = (torch.randn(H, generator=g) * 0.3).to(DEV)
+    tw = (torch.rand(H, generator=g) - 0.5).to(DEV)
+    trace0 = r(M, H, sc=0.5)
+    trace = trace0.clone()
+    prev = ref.local_normalize(torch.randn(M, H, 3, 3, generator=g)).to(DEV, dtype)
+    valid = (torch.arange(M) % 3 != 1).to(torch.uint8).to(DEV)
+    gw = torch.softmax(torch.randn(9, generator=g), 0).to(DEV, dtype)
+    act, s, beta = (torch.empty(M, H, device=DEV, dtype=dtype) for _ in range(3))
+    carry = torch.empty(M, H, 3, 3, device=DEV, dtype=dtype)
+    p = torch.empty(M, H, device=DEV, dtype=dtype)
+    desc = _lib.ffn_decode_desc(
+        u=u, q_h=q, k_ctx_h=kc, c_h=c, d_h=d, w_compact=w, M=M, N=N, H=H, imag_in=K,
+        hidden_per_q_head=H // QH, head_dim=HD, n_q_heads=QH, open_sectors=0,
+        p_real=R, imag_bias=ib, trace=trace, trace_w=tw, powlu_m=3.0, act=act, s=s, beta=beta,
+        carry_prev=prev if mode == 1 else None, seed=prev if mode == 2 else None,
+        seed_valid=valid if mode == 2 else None, gate_w=gw if gate else None, carry_out=carry,
+        p_out=p if gate else None, alpha=0.0375, axis=axis)
+    _lib.call("loom_ffn_decode", code(u), ctypes.byref(desc), S(u))
+    # oracle, fp32 on the host
+    be = ref.beta_space_grouped(host(u)[:, None], host(q)[:, None], host(kc)[:, None],
+                                host(c)[:, None], host(d)[:, None], host(w), QH, HD, "head")
+    wa, ws_, wt = ref.paraplex_pointwise(host(R)[:, None], host(R)[:, None], be, host(ib),
+                                         host(trace0), host(tw), None, 3.0)
+    check(act, wa[:, 0], dtype)
+    check(s, ws_[:, 0], dtype)
+    check(trace, wt, dtype)
+    ri = [host(R)[:, None], ws_.to(dtype).float(), wa.to(dtype).float()]   # Tria sees stored R, I, O
+    wgt = host(gw) if gate else torch.zeros(9)
+    if mode == 1:
+        wc, wp = ref.tria_step_and_gate(*ri, host(prev)[:, None], wgt, 0.0375, axis)
+    elif mode == 2:
+        wc, wp = ref.tria_init_seed_and_gate(*ri, host(prev), host(valid).bool(), wgt, 0.0375, axis)
+    else:
+        wc, wp = ref.tria_init_and_gate(*ri, wgt, 0.0375, axis)
+    check(carry, wc[:, 0], dtype)
+    if gate:
+        check(p, wp[:, 0], dtype)
