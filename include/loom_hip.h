@@ -141,6 +141,20 @@ int loom_linear_multi(int dtype, const loom_linear_multi_desc* desc, void* strea
 /* sizeof(loom_linear_multi_desc), so an FFI binding can check its layout. */
 int64_t loom_linear_multi_desc_bytes(void);
 
+/* out = LayerNorm(x w^T + x2 w2^T + bias) * gamma + beta for a one-segment
+ * descriptor (no gate; N <= 2048): the sublayer tails
+ * ln_attn(skip + attn_out) and ln_ffn(skip + ffn_out) of Model.step
+ * (loomformer.py:4000, :4045) with both products in one accumulator.  No
+ * counterpart in the reference as one call.  bf16 with m <= 64 splits K over
+ * blocks, writing fp32 partial sums to the workspace (at least
+ * loom_linear_ln_workspace_bytes(m, n), 16-byte aligned), and the LayerNorm
+ * kernel adds them up; other cases write x w^T + x2 w2^T + bias to seg[0].out
+ * (dense [m, n]) and normalise that. */
+int loom_linear_ln(int dtype, const loom_linear_multi_desc* desc, const float* gamma,
+                   const float* beta, float eps, void* out, int64_t ldo, float* workspace,
+                   int64_t workspace_bytes, void* stream);
+int64_t loom_linear_ln_workspace_bytes(int64_t M, int64_t N);
+
 /* One decode token (T = 1) of the Paraplex FFN core and the Tria depth op. */
 typedef struct {
     /* beta space, as loom_beta_forward */

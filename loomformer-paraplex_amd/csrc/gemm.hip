@@ -409,6 +409,11 @@ struct LinArgs {
     int nseg;
     int64_t nstart[kMaxSeg + 1];   // first global column of each segment
     LinSeg seg[kMaxSeg];
+    // split-K (one segment): blockIdx.y takes k-steps [y*S/nsplit, (y+1)*S/nsplit)
+    // and writes raw fp32 sums to partial[(y*M + m)*ldp + n]; no epilogue
+    float* partial;
+    int64_t ldp;
+    int nsplit;
 };
 
 template <int MT, int NW, int UN>
@@ -426,9 +431,10 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
     const int64_t n = n0 + fr;
     const bool nvalid = n < sg.n;
     const int64_t S1 = ceil_div(a.K, 32), S2 = ceil_div(a.K2, 32), S = S1 + S2;
-    const int64_t per = ceil_div(S, NW);
-    const int64_t s_begin = wave * per;
-    const int64_t s_end = s_begin + per < S ? s_begin + per : S;
+    const int64_t sb = S * blockIdx.y / a.nsplit, se = S * (blockIdx.y + 1) / a.nsplit;
+    const int64_t per = ceil_div(se - sb, NW);
+    const int64_t s_begin = sb + wave * per;
+    const int64_t s_end = s_begin + per < se ? s_begin + per : se;
 
     f32x4 acc[MT];
 #pragma unroll
@@ -477,6 +483,10 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) v += red[w][j][r][ln];
+        if (a.partial != nullptr) {
+            a.partial[((int64_t)blockIdx.y * a.M + m) * a.ldp + nidx] = v;
+            continue;
+        }
         if (sg.gate_p != nullptr)
             v *= 1.0f + sg.gate_alpha * ld((const bf16_t*)sg.gate_p + m * sg.gate_ld + nidx);
         if (sg.bias != nullptr) v += sg.bias[nidx];
@@ -739,7 +749,7 @@ static int linear_multi_dispatch(const loom_linear_multi_desc& d, hipStream_t st
         LinArgs a{};
         a.X = (const uint16_t*)d.x; a.ldx = d.ldx; a.K = d.k;
         a.X2 = (const uint16_t*)d.x2; a.ldx2 = d.ldx2; a.K2 = d.k2;
-        a.M = d.m; a.nseg = d.nseg;
+        a.M = d.m; a.nseg = d.nseg; a.nsplit = 1;
         int64_t ncols = 0;
         for (int s = 0; s < d.nseg; ++s) {
             const loom_linear_segment& g = d.seg[s];
@@ -804,6 +814,129 @@ extern "C" int loom_linear_multi(int dtype, const loom_linear_multi_desc* d, voi
     }
     set_error("linear_multi: unsupported dtype %d", dtype);
     return LOOM_ERR_INVALID;
+}
+
+// ------------------------------------------------------------------ split-K + LayerNorm
+constexpr int kMaxSplit = 8;
+
+// out[m] = LN(sum_s partial[s, m] + bias) * gamma + beta; one wave per row,
+// N <= 64 * 4 * kLnVec.
+constexpr int kLnVec = 8;
+template <typename T, int NS>
+__global__ void __launch_bounds__(256)
+splitk_ln_kernel(const float* __restrict__ partial, int64_t ldp,
+                 const float* __restrict__ bias, const float* __restrict__ gamma,
+                 const float* __restrict__ beta, T* __restrict__ out, int64_t ldo, int64_t rows,
+                 int N, float eps) {
+    const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;                       // whole waves leave together
+    float x[kLnVec][4];
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kLnVec; ++k) {
+        const int c = (lane + 64 * k) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[k][e] = 0.0f;
+        if (c < N) {
+            float4 v[NS];                          // all splits of the chunk in flight
+#pragma unroll
+            for (int sp = 0; sp < NS; ++sp)
+                v[sp] = *reinterpret_cast<const float4*>(partial + (sp * rows + row) * ldp + c);
+#pragma unroll
+            for (int sp = 0; sp < NS; ++sp) {
+                x[k][0] += v[sp].x; x[k][1] += v[sp].y; x[k][2] += v[sp].z; x[k][3] += v[sp].w;
+            }
+            if (bias != nullptr)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[k][e] += bias[c + e];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s += x[k][e];
+        }
+    }
+    const float mean = wave_sum(s) / N;
+    float var = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kLnVec; ++k)
+        if ((lane + 64 * k) * 4 < N)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float dlt = x[k][e] - mean;
+                var = fmaf(dlt, dlt, var);
+            }
+    const float rstd = frsq(wave_sum(var) / N + eps);
+#pragma unroll
+    for (int k = 0; k < kLnVec; ++k) {
+        const int c = (lane + 64 * k) * 4;
+        if (c >= N) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            st(out + row * ldo + c + e, fmaf((x[k][e] - mean) * rstd, gamma[c + e], beta[c + e]));
+    }
+}
+
+extern "C" int64_t loom_linear_ln_workspace_bytes(int64_t M, int64_t N) {
+    return kMaxSplit * M * N * (int64_t)sizeof(float);
+}
+
+extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const float* gamma,
+                              const float* beta, float eps, void* out, int64_t ldo, float* workspace,
+                              int64_t workspace_bytes, void* stream) {
+    clear_error();
+    LOOM_CHECK(d != nullptr && d->nseg == 1, "linear_ln: one output segment expected");
+    LOOM_CHECK(gamma && beta && out, "linear_ln: null LayerNorm argument");
+    const loom_linear_segment& g = d->seg[0];
+    LOOM_CHECK(g.gate_p == nullptr, "linear_ln: no gate on a LayerNorm input");
+    LOOM_CHECK(g.n >= 1 && g.n <= 64 * 4 * kLnVec && ldo >= g.n,
+               "linear_ln: N=%lld outside [1, %d]", (long long)g.n, 64 * 4 * kLnVec);
+    hipStream_t st = (hipStream_t)stream;
+    bool fused = dtype == LOOM_BF16 && d->m >= 1 && d->m <= 64 && d->k % 8 == 0 && d->ldx % 8 == 0 &&
+                 ((uintptr_t)d->x & 15) == 0 && g.ldw % 8 == 0 && ((uintptr_t)g.w & 15) == 0 &&
+                 g.n % 4 == 0 && workspace != nullptr && ((uintptr_t)workspace & 15) == 0 &&
+                 workspace_bytes >= loom_linear_ln_workspace_bytes(d->m, g.n);
+    if (d->k2 > 0)
+        fused = fused && d->k2 % 8 == 0 && d->ldx2 % 8 == 0 && ((uintptr_t)d->x2 & 15) == 0 &&
+                g.ldw2 % 8 == 0 && ((uintptr_t)g.w2 & 15) == 0;
+    if (!fused) {
+        // y = product (+ bias) into seg.out, then LayerNorm of y
+        int rc = loom_linear_multi(dtype, d, stream);
+        if (rc != LOOM_OK) return rc;
+        LOOM_CHECK(g.ldc == g.n && ldo == g.n, "linear_ln: the unfused path needs dense rows");
+        return loom_add_layernorm(dtype, g.out, nullptr, gamma, beta, out, d->m, g.n, eps, stream);
+    }
+    if (d->m == 0) return LOOM_OK;
+    LinArgs a{};
+    a.X = (const uint16_t*)d->x; a.ldx = d->ldx; a.K = d->k;
+    a.X2 = (const uint16_t*)d->x2; a.ldx2 = d->ldx2; a.K2 = d->k2;
+    a.M = d->m; a.nseg = 1;
+    a.seg[0] = LinSeg{(const uint16_t*)g.w, g.ldw, (const uint16_t*)g.w2, g.ldw2, g.out, g.ldc,
+                      nullptr, nullptr, 0, 0.0f, g.n};
+    const int64_t ntiles = ceil_div(g.n, 16);
+    for (int s2 = 0; s2 <= kMaxSeg; ++s2) a.nstart[s2] = s2 == 0 ? 0 : ntiles * 16;
+    const int64_t steps = ceil_div(d->k, 32) + ceil_div(d->k2, 32);
+    // enough k-splits to give every CU a block, at least 4 k-steps per split
+    int64_t ns = ceil_div(4 * (int64_t)device_cus() / 4, ntiles);
+    if (ns > kMaxSplit) ns = kMaxSplit;
+    if (ns > steps / 4) ns = steps / 4 > 0 ? steps / 4 : 1;
+    a.nsplit = (int)ns;
+    a.partial = workspace;
+    a.ldp = g.n;
+    const dim3 grid((unsigned)ntiles, (unsigned)ns);
+    launch_skinny_multi(a, grid, (int)ceil_div(d->m, 16), ceil_div(steps, ns), st);
+    int rc = launch_status("loom_linear_ln");
+    if (rc != LOOM_OK) return rc;
+    const dim3 lgrid((unsigned)ceil_div(d->m * 64, 256));
+#define LOOM_SLN(NS)                                                                          \
+    case NS:                                                                                  \
+        hipLaunchKernelGGL((splitk_ln_kernel<bf16_t, NS>), lgrid, dim3(256), 0, st, workspace,  \
+                           g.n, g.bias, gamma, beta, (bf16_t*)out, ldo, d->m, (int)g.n, eps); \
+        break;
+    switch (ns) {
+        LOOM_SLN(1) LOOM_SLN(2) LOOM_SLN(3) LOOM_SLN(4) LOOM_SLN(5) LOOM_SLN(6) LOOM_SLN(7)
+        LOOM_SLN(8)
+    }
+#undef LOOM_SLN
+    return launch_status("loom_linear_ln(layernorm)");
 }
 
 extern "C" int64_t loom_ffn_decode_desc_bytes(void) { return (int64_t)sizeof(loom_ffn_decode_desc); }

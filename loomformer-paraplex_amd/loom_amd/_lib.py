@@ -40,6 +40,7 @@ SIGNATURES = {
                           c_int64, c_int64, c_int64, c_int64, c_int, _P],
     "loom_linear_multi": [c_int, _P, _P],
     "loom_ffn_decode": [c_int, _P, _P],
+    "loom_linear_ln": [c_int, _P, _P, _P, c_float, _P, c_int64, _P, c_int64, _P],
     "loom_linear": [c_int, _P, c_int64, _P, c_int64, _P, _P, c_float, _P, _P, c_int64,
                     c_int64, c_int64, c_int64, _P],
     "loom_depth_attn_forward": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64,
@@ -74,7 +75,8 @@ SIGNATURES = {
 # entry points that return a value instead of a status
 QUERIES = {"loom_gqa_workspace_bytes": ([c_int64] * 5, c_int64),
            "loom_linear_multi_desc_bytes": ([], c_int64),
-           "loom_ffn_decode_desc_bytes": ([], c_int64)}
+           "loom_ffn_decode_desc_bytes": ([], c_int64),
+           "loom_linear_ln_workspace_bytes": ([c_int64, c_int64], c_int64)}
 
 _lib = None
 _lock = threading.Lock()

@@ -141,7 +141,9 @@ class LoomDecoder:
         self.act = z(B, H)
         self.s = z(B, H)
         self.ffn_out = z(B, N)
-        self.y = z(B, N)                # pre-LayerNorm sum of a sublayer
+        self.y = z(B, N)                # pre-LayerNorm sum of a sublayer (unfused path)
+        ln_ws = self.lib.loom_linear_ln_workspace_bytes(B, N)
+        self.ln_ws = torch.empty((ln_ws + 3) // 4, dtype=torch.float32, device=dev)
         self.carry = z(2, B, H, 3, 3)
         self.p = z(2, B, H)
         self.pooled = z(B, 9)
@@ -179,6 +181,15 @@ class LoomDecoder:
             d = _lib.linear_multi_desc(x, segments, x2=x2)
             self._descs[key] = d
         self._call("loom_linear_multi", self.code, _lib.ctypes.byref(d), self._stream())
+
+    def _linear_ln(self, key, x, segment, x2, gamma, beta) -> None:
+        """h = LayerNorm(x w^T + x2 w2^T + bias) through loom_linear_ln."""
+        d = self._descs.get(key)
+        if d is None:
+            d = _lib.linear_multi_desc(x, [segment], x2=x2)
+            self._descs[key] = d
+        self._call("loom_linear_ln", self.code, _lib.ctypes.byref(d), _P(gamma), _P(beta), 1e-5,
+                   _P(self.h), self.cfg.N, _P(self.ln_ws), self.ln_ws.numel() * 4, self._stream())
 
     def reset(self) -> None:
         """Forget all sequence state (Model.step at pos 0 starts afresh)."""
@@ -224,10 +235,9 @@ class LoomDecoder:
             # ---- depth read 2*bi, then LN(o(c) + w_o(d)) (loomformer.py:3999-4000):
             # both products accumulate in one launch
             self._depth(sub, self.d)
-            self._multi(("attn", bi), self.c.view(B, N),
-                        [dict(w=blk["o"], w2=self.wo, out=self.y)], x2=self.d.view(B, N))
-            self._call("loom_add_layernorm", self.code, _P(self.y), None,
-                       _P(blk["ln1_w"]), _P(blk["ln1_b"]), _P(self.h), B, N, 1e-5, st)
+            self._linear_ln(("attn", bi), self.c.view(B, N),
+                            dict(w=blk["o"], w2=self.wo, out=self.y), self.d.view(B, N),
+                            blk["ln1_w"], blk["ln1_b"])
             # ---- history slot 2*bi+1 (loomformer.py:4004) and W_real of the same h
             # (+ IdentityAnchoredGate with the previous block's p, loomformer.py:2839)
             sub += 1
@@ -261,10 +271,9 @@ class LoomDecoder:
             self._call("loom_ffn_decode", self.code, _lib.ctypes.byref(d), st)
             carry_i, p_i = out_i, new_p
             # ---- LN(w_o(d_h) + W2(act) + b2) (loomformer.py:4045): one launch + LN
-            self._multi(("ffn", bi), self.dh.view(B, N),
-                        [dict(w=self.wo, w2=blk["w2"], out=self.y, bias=blk["b2"])], x2=self.act)
-            self._call("loom_add_layernorm", self.code, _P(self.y), None,
-                       _P(blk["ln2_w"]), _P(blk["ln2_b"]), _P(self.h), B, N, 1e-5, st)
+            self._linear_ln(("ffn", bi), self.dh.view(B, N),
+                            dict(w=self.wo, w2=blk["w2"], out=self.y, bias=blk["b2"]), self.act,
+                            blk["ln2_w"], blk["ln2_b"])
             if not last:
                 # next history slot (loomformer.py:4050) and the next block's qkv
                 sub += 1

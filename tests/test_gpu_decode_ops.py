@@ -346,3 +346,33 @@ def test_ffn_decode(dtype, mode, gate, axis):
     check(carry, wc[:, 0], dtype)
     if gate:
         check(p, wp[:, 0], dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("M,K2", [(1, 768), (32, 768), (32, 3072), (64, 3072), (7, 0)])
+def test_linear_ln(dtype, M, K2):
+    """LayerNorm(x w^T + x2 w2^T + b): split-K partial sums reduced inside the
+    LayerNorm kernel (bf16) or product + LayerNorm (fp32), against torch."""
+    from loom_amd import _lib
+    g = torch.Generator().manual_seed(M + K2)
+    N, K = 768, 768
+    r = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(DEV, dtype)
+    x = r(M, K)
+    w = r(N, K, sc=K ** -0.5)
+    x2 = r(M, K2) if K2 else None
+    w2 = r(N, K2, sc=K2 ** -0.5) if K2 else None
+    b = torch.randn(N, generator=g).to(DEV)
+    gam = (torch.rand(N, generator=g) + 0.5).to(DEV)
+    bet = torch.randn(N, generator=g).to(DEV)
+    y = torch.zeros(M, N, device=DEV, dtype=dtype)
+    out = torch.zeros(M, N, device=DEV, dtype=dtype)
+    nb = _lib.load().loom_linear_ln_workspace_bytes(M, N)
+    ws = torch.empty(nb // 4, device=DEV)
+    d = _lib.linear_multi_desc(x, [dict(w=w, w2=w2, out=y, bias=b)], x2=x2)
+    _lib.call("loom_linear_ln", code(x), ctypes.byref(d), P(gam), P(bet), 1e-5, P(out), N, P(ws),
+              nb, S(x))
+    pre = host(x) @ host(w).T + host(b)
+    if K2:
+        pre = pre + host(x2) @ host(w2).T
+    want = torch.nn.functional.layer_norm(pre, (N,), host(gam), host(bet), 1e-5)
+    check(out, want, dtype)
