@@ -2,6 +2,7 @@
 // attention with the dual readout (A.V and A.K_roped), fused residual add +
 // LayerNorm, and the decode-time temporal Tria update (+ PolARM on fires).
 #include <cmath>
+#include <type_traits>
 
 #include "loom_common.h"
 
@@ -98,6 +99,106 @@ __device__ __forceinline__ float rope_elem(const T* head, const float* cr, const
     const int half = HD / 2;
     const float rot = d < half ? -ld(head + d + half) : ld(head + d - half);
     return ld(head + d) * cr[d] + rot * sr[d];
+}
+
+// End of a GQA chunk block: merge the four waves' partials wred[w] = [m(G) |
+// l(G) | c(G*HD) | k(G*HD)] into the chunk record, publish it, and, in the
+// block that arrives last for (b, kvh), merge every chunk record into C and
+// Kctx and reset the arrival counter.  The merging block stages the records
+// in LDS (`stage`, `stage_floats` floats, reusing the block's scratch) with
+// every device-coherent load of a batch in flight at once.
+constexpr int kMergeLoads = 32;   // record words each thread has in flight while staging
+
+template <typename T, int G, int HD>
+__device__ __forceinline__ void gqa_finish(const GqaArgs<T>& a, float (*wred)[2 * G + 2 * G * HD],
+                                           int& s_last, int64_t b, int kvh, int chunk, int nchunks,
+                                           int nact, float* stage, int stage_floats) {
+    constexpr int REC = 2 * G + 2 * G * HD;
+    constexpr int kOut = (G * HD + 255) / 256;
+    const int tid = threadIdx.x;
+    float* recs = a.rec + ((int64_t)b * a.KVH + kvh) * nchunks * REC;
+    float* rec = recs + (int64_t)chunk * REC;
+    for (int k = tid; k < REC; k += blockDim.x) {
+        const int g = k < 2 * G ? k % G : ((k - 2 * G) % (G * HD)) / HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, wred[w][g]);
+        float acc = M;
+        if (k >= G) {
+            acc = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                if (wred[w][g] != -INFINITY) acc = fmaf(wred[w][k], __builtin_amdgcn_exp2f(wred[w][g] - M), acc);
+        }
+        st_coherent(rec + k, acc);
+    }
+    // publish the record; the block that arrives last merges all of them
+    __syncthreads();
+    int* counter = a.counters + b * a.KVH + kvh;
+    if (tid == 0) s_last = arrive(counter) == nact - 1;
+    __syncthreads();
+    if (!s_last) return;
+    float M[kOut], L[kOut], C[kOut], K[kOut];
+#pragma unroll
+    for (int i = 0; i < kOut; ++i) {
+        M[i] = -INFINITY;
+        L[i] = C[i] = K[i] = 0.0f;
+    }
+    const int per_batch = stage_floats / REC > 0 ? stage_floats / REC : 1;
+    for (int c0 = 0; c0 < nact; c0 += per_batch) {
+        const int nc = nact - c0 < per_batch ? nact - c0 : per_batch;
+        const int nval = nc * REC;
+        const float* src = recs + (int64_t)c0 * REC;
+        __syncthreads();                   // the scratch is free (previous batch / partials read)
+        for (int k0 = tid; k0 < nval; k0 += kMergeLoads * 256) {
+            float v[kMergeLoads];
+#pragma unroll
+            for (int u = 0; u < kMergeLoads; ++u) {
+                const int k = k0 + 256 * u;
+                v[u] = k < nval ? ld_coherent(src + k) : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < kMergeLoads; ++u) {
+                const int k = k0 + 256 * u;
+                if (k < nval) stage[k] = v[u];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kOut; ++i) {
+            const int k = tid + 256 * i;
+            if (k >= G * HD) continue;
+            const int g = k / HD, d = k % HD;
+            float Mb = M[i];
+            for (int c = 0; c < nc; ++c) Mb = fmaxf(Mb, stage[c * REC + g]);
+            if (Mb == -INFINITY) continue;
+            const float r = __builtin_amdgcn_exp2f(M[i] - Mb);   // 0 while M is -inf
+            float l = L[i] * r, cc = C[i] * r, kk = K[i] * r;
+            for (int c = 0; c < nc; ++c) {
+                const float* rc = stage + c * REC;
+                if (rc[g] == -INFINITY) continue;
+                const float w = __builtin_amdgcn_exp2f(rc[g] - Mb);
+                l = fmaf(rc[G + g], w, l);
+                cc = fmaf(rc[2 * G + g * HD + d], w, cc);
+                kk = fmaf(rc[2 * G + G * HD + g * HD + d], w, kk);
+            }
+            M[i] = Mb;
+            L[i] = l;
+            C[i] = cc;
+            K[i] = kk;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kOut; ++i) {
+        const int k = tid + 256 * i;
+        if (k >= G * HD) continue;
+        const int g = k / HD, d = k % HD;
+        const float inv = 1.0f / L[i];
+        const int64_t o = b * a.out_sb + (kvh * G + g) * HD + d;
+        st(a.c_out + o, C[i] * inv);
+        st(a.k_out + o, K[i] * inv);
+    }
+    if (tid == 0) reset_counter(counter);
 }
 
 template <typename T, int EPL, int G, int LPR, bool FROM_QKV>
@@ -281,67 +382,212 @@ gqa_decode_kernel(GqaArgs<T> a) {
         }
     }
     __syncthreads();
-    // merge the four waves into this chunk's record
-    float* recs = a.rec + ((int64_t)b * a.KVH + kvh) * nchunks * REC;
-    float* rec = recs + (int64_t)chunk * REC;
-    for (int k = tid; k < REC; k += blockDim.x) {
-        const int g = k < 2 * G ? k % G : ((k - 2 * G) % (G * HD)) / HD;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, wred[w][g]);
-        float acc = M;
-        if (k >= G) {
-            acc = 0.0f;
-#pragma unroll
-            for (int w = 0; w < 4; ++w)
-                if (wred[w][g] != -INFINITY) acc = fmaf(wred[w][k], __builtin_amdgcn_exp2f(wred[w][g] - M), acc);
+    gqa_finish<T, G, HD>(a, wred, s_last, b, kvh, chunk, nchunks, nact, &wred[0][0], 4 * REC);
+}
+
+// ------------------------------------------------------------------ GQA attention on MFMA (bf16)
+// Same contract, chunking and merge as gqa_decode_kernel, with the three
+// products on v_mfma_f32_16x16x32_bf16 (A: 16 rows x 32 k, B: 32 k x 16
+// columns; lane l holds row/column l%16, k = 8*(l/16)..+7; result element
+// [4*(l/16)+r][l%16] in register r):
+//   S^T = K Q^T    A = 16 cached K rows (16-byte loads straight from the cache),
+//                  B = the G query heads (columns >= G are zero);
+//   C   = P V      A = P (rows = heads, k = 32 positions, bf16 like the
+//   Kctx= P K      reference's softmax output), B = V / K transposed through LDS.
+// Each wave takes 32 positions at a time; the online softmax runs in the
+// lanes holding S (lane l: head l%16), P and the rescale factors go to the
+// accumulator lanes through LDS.  Scores are in log2 units.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMfTile = 32;   // positions per wave step
+
+__device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+template <int HD, int G, bool FROM_QKV>
+__global__ void __launch_bounds__(256)
+gqa_mfma_kernel(GqaArgs<bf16_t> a) {
+    constexpr int KK = HD / 32;            // 32-wide k-steps of a head
+    constexpr int DT = HD / 16;            // 16-wide output tiles of a head
+    constexpr int REC = 2 * G + 2 * G * HD;
+    struct Tiles {
+        uint16_t kt[HD][kMfTile];          // K tile transposed: [dim][position]
+        uint16_t vt[HD][kMfTile];
+        uint16_t pt[16][kMfTile];          // P: [head][position]
+        float cr[16];                      // per-head rescale of this step
+    };
+    constexpr int kTileBytes = 4 * (int)sizeof(Tiles);
+    constexpr int kRedBytes = 4 * REC * (int)sizeof(float);
+    __shared__ __align__(16) unsigned char lds[kTileBytes > kRedBytes ? kTileBytes : kRedBytes];
+    __shared__ int s_last;
+    const int chunk = blockIdx.x, kvh = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    const int nchunks = gridDim.x;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 15, lq = lane >> 4;
+    const int64_t len = a.pos_dev != nullptr ? *a.pos_dev + 1 : a.len;
+    const int64_t pos = len - 1;
+    const int nact = (int)((len + kAttnChunk - 1) / kAttnChunk);
+    if (chunk >= nact) return;
+    const int64_t t0 = (int64_t)chunk * kAttnChunk;
+    const int64_t t1 = t0 + kAttnChunk < len ? t0 + kAttnChunk : len;
+    const int QKV = (a.QH + 2 * a.KVH) * HD;
+    Tiles& tl = reinterpret_cast<Tiles*>(lds)[wave];
+
+    // FROM_QKV: the block holding pos appends this token's (k_roped, v) first,
+    // then reads it back like every cached row
+    if constexpr (FROM_QKV) {
+        if (t1 == len && tid < HD) {
+            const bf16_t* krow = a.q + b * QKV + (a.QH + kvh) * HD;
+            const bf16_t* vrow = krow + a.KVH * HD;
+            const float* cr = a.cosv + pos * HD;
+            const float* sr = a.sinv + pos * HD;
+            st(a.kc + b * a.csb + pos * a.cst + kvh * HD + tid, rope_elem(krow, cr, sr, tid, HD));
+            a.vc[b * a.csb + pos * a.cst + kvh * HD + tid] = vrow[tid];
         }
-        st_coherent(rec + k, acc);
+        __syncthreads();                   // stores complete (vmcnt) before any wave reads row pos
     }
-    // publish the record; the block that arrives last merges all of them
-    __syncthreads();
-    int* counter = a.counters + b * a.KVH + kvh;
-    if (tid == 0) s_last = arrive(counter) == nact - 1;
-    __syncthreads();
-    if (!s_last) return;
-    for (int k = tid; k < G * HD; k += blockDim.x) {
-        const int g = k / HD, d = k % HD;
-        float M = -INFINITY;
-        for (int c0 = 0; c0 < nact; c0 += kAttnMerge) {
-            float mv[kAttnMerge];
+    // B operand of S^T: q of head lr, dims 32*kk + 8*lq .. +7, rounded to bf16
+    uint4 qf[KK];
 #pragma unroll
-            for (int u = 0; u < kAttnMerge; ++u)
-                mv[u] = c0 + u < nact ? ld_coherent(recs + (int64_t)(c0 + u) * REC + g) : -INFINITY;
+    for (int kk = 0; kk < KK; ++kk) {
+        float x[8];
 #pragma unroll
-            for (int u = 0; u < kAttnMerge; ++u) M = fmaxf(M, mv[u]);
-        }
-        float L = 0.0f, C = 0.0f, K = 0.0f;
-        for (int c0 = 0; c0 < nact; c0 += kAttnMerge) {
-            float mv[kAttnMerge], lv[kAttnMerge], cv[kAttnMerge], kv[kAttnMerge];
+        for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+        if (lr < G) {
+            const int d0 = 32 * kk + 8 * lq;
+            if constexpr (FROM_QKV) {
+                const bf16_t* qh = a.q + b * QKV + (kvh * G + lr) * HD;
+                const float* cr = a.cosv + pos * HD;
+                const float* sr = a.sinv + pos * HD;
 #pragma unroll
-            for (int u = 0; u < kAttnMerge; ++u) {
-                const bool ok = c0 + u < nact;
-                const float* r = recs + (int64_t)(ok ? c0 + u : 0) * REC;
-                mv[u] = ok ? ld_coherent(r + g) : -INFINITY;
-                lv[u] = ld_coherent(r + G + g);
-                cv[u] = ld_coherent(r + 2 * G + g * HD + d);
-                kv[u] = ld_coherent(r + 2 * G + G * HD + g * HD + d);
-            }
-#pragma unroll
-            for (int u = 0; u < kAttnMerge; ++u) {
-                if (mv[u] == -INFINITY) continue;
-                const float w = __builtin_amdgcn_exp2f(mv[u] - M);
-                L = fmaf(lv[u], w, L);
-                C = fmaf(cv[u], w, C);
-                K = fmaf(kv[u], w, K);
+                for (int e = 0; e < 8; ++e) x[e] = rope_elem(qh, cr, sr, d0 + e, HD);
+                if (a.q_out != nullptr && chunk == 0 && wave == 0)
+                    Vec8<bf16_t>::store(a.q_out + (b * a.QH + kvh * G + lr) * HD + d0, x);
+            } else {
+                Vec8<bf16_t>::load(a.q + (b * a.QH + kvh * G + lr) * HD + d0, x);
             }
         }
-        const float inv = 1.0f / L;
-        const int64_t o = b * a.out_sb + (kvh * G + g) * HD + d;
-        st(a.c_out + o, C * inv);
-        st(a.k_out + o, K * inv);
+        qf[kk] = make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]),
+                            pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
     }
-    if (tid == 0) reset_counter(counter);
+    const bf16_t* kb = a.kc + b * a.csb + kvh * HD;
+    const bf16_t* vb = a.vc + b * a.csb + kvh * HD;
+    float mh = -INFINITY, lh = 0.0f;       // running max / sum of head lr (lanes l%16 == head)
+    f32x4_t accC[DT], accK[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) accC[dt] = accK[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // every wave runs the same number of steps (the loop holds barriers); a
+    // step past t1 is fully masked
+    const int nstep = (int)((t1 - t0 + 4 * kMfTile - 1) / (4 * kMfTile));
+    for (int it = 0; it < nstep; ++it) {
+        const int64_t ts = t0 + wave * kMfTile + (int64_t)it * 4 * kMfTile;
+        // K and V rows ts + 16*hf + lr, dims 32*kk + 8*lq (row clamped in range; masked below)
+        uint4 kr[2][KK], vr[2][KK];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            int64_t t = ts + 16 * hf + lr;
+            t = t < t1 ? t : t1 - 1;
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                kr[hf][kk] = *reinterpret_cast<const uint4*>(kb + t * a.cst + 32 * kk + 8 * lq);
+                vr[hf][kk] = *reinterpret_cast<const uint4*>(vb + t * a.cst + 32 * kk + 8 * lq);
+            }
+        }
+        // S^T[position 16*hf + 4*lq + r][head lr]
+        f32x4_t sc[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            sc[hf] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) sc[hf] = mfma16(kr[hf][kk], qf[kk], sc[hf]);
+        }
+        float mx = -INFINITY;
+        float sv[2][4];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool ok = ts + 16 * hf + 4 * lq + r < t1;
+                sv[hf][r] = ok ? sc[hf][r] * a.qscale : -INFINITY;
+                mx = fmaxf(mx, sv[hf][r]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(mh, mx);
+        // nothing seen yet (mnew = -inf): keep the zero state; otherwise 0 on the first step
+        const float corr = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(mh - mnew);
+        float ls = 0.0f;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float pv = sv[hf][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[hf][r] - mnew);
+                ls += pv;
+                tl.pt[lr][16 * hf + 4 * lq + r] = f32_to_bf16(pv);
+            }
+        ls += __shfl_xor(ls, 16, 64);
+        ls += __shfl_xor(ls, 32, 64);
+        lh = fmaf(lh, corr, ls);
+        mh = mnew;
+        if (lq == 0) tl.cr[lr] = corr;
+        // K, V transposed into LDS: [dim 32*kk + 8*lq + e][position 16*hf + lr]
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                const uint32_t kw[4] = {kr[hf][kk].x, kr[hf][kk].y, kr[hf][kk].z, kr[hf][kk].w};
+                const uint32_t vw[4] = {vr[hf][kk].x, vr[hf][kk].y, vr[hf][kk].z, vr[hf][kk].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int d = 32 * kk + 8 * lq + e;
+                    tl.kt[d][16 * hf + lr] = (uint16_t)(kw[e >> 1] >> (16 * (e & 1)));
+                    tl.vt[d][16 * hf + lr] = (uint16_t)(vw[e >> 1] >> (16 * (e & 1)));
+                }
+            }
+        __syncthreads();
+        // rescale the accumulators (rows = heads 4*lq + r) and add P V, P K
+        float cf[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cf[r] = tl.cr[4 * lq + r];
+        const uint4 pa = *reinterpret_cast<const uint4*>(&tl.pt[lr][8 * lq]);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                accC[dt][r] *= cf[r];
+                accK[dt][r] *= cf[r];
+            }
+            const uint4 vbf = *reinterpret_cast<const uint4*>(&tl.vt[16 * dt + lr][8 * lq]);
+            const uint4 kbf = *reinterpret_cast<const uint4*>(&tl.kt[16 * dt + lr][8 * lq]);
+            accC[dt] = mfma16(pa, vbf, accC[dt]);
+            accK[dt] = mfma16(pa, kbf, accK[dt]);
+        }
+        __syncthreads();                   // tiles are rewritten next step
+    }
+    // this wave's partials -> wred[wave] = [m | l | c | k] (unnormalised)
+    float (*wred)[REC] = reinterpret_cast<float (*)[REC]>(lds);
+    if (lq == 0 && lr < G) {
+        wred[wave][lr] = mh;
+        wred[wave][G + lr] = lh;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int g = 4 * lq + r;
+            if (g < G) {
+                wred[wave][2 * G + g * HD + 16 * dt + lr] = accC[dt][r];
+                wred[wave][2 * G + G * HD + g * HD + 16 * dt + lr] = accK[dt][r];
+            }
+        }
+    __syncthreads();
+    gqa_finish<bf16_t, G, HD>(a, wred, s_last, b, kvh, chunk, nchunks, nact,
+                              reinterpret_cast<float*>(lds), (int)(sizeof(lds) / sizeof(float)));
 }
 
 // ------------------------------------------------------------------ add + LayerNorm
@@ -534,6 +780,22 @@ static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void
     a.KVH = (int)KVH;
     a.qscale = kLog2e / sqrtf((float)HD);   // scores in log2 units
     dim3 grid(nchunks, (unsigned)KVH, (unsigned)B);
+    if constexpr (std::is_same<T, bf16_t>::value) {
+        // bf16: the MFMA form for head_dim 32/64/96/128 and groups 1/2/4/8
+#define LOOM_GQA_MF(HDV, GG)                                                                      \
+        if (HD == HDV && G == GG) {                                                              \
+            if (from_qkv)                                                                         \
+                hipLaunchKernelGGL((gqa_mfma_kernel<HDV, GG, true>), grid, dim3(256), 0, st, a);  \
+            else                                                                                  \
+                hipLaunchKernelGGL((gqa_mfma_kernel<HDV, GG, false>), grid, dim3(256), 0, st, a); \
+            return launch_status(from_qkv ? "loom_gqa_decode_step" : "loom_gqa_decode_attention"); \
+        }
+        LOOM_GQA_MF(96, 4) LOOM_GQA_MF(96, 1) LOOM_GQA_MF(96, 2) LOOM_GQA_MF(96, 8)
+        LOOM_GQA_MF(64, 4) LOOM_GQA_MF(64, 1) LOOM_GQA_MF(64, 2) LOOM_GQA_MF(64, 8)
+        LOOM_GQA_MF(128, 4) LOOM_GQA_MF(128, 1) LOOM_GQA_MF(128, 2) LOOM_GQA_MF(128, 8)
+        LOOM_GQA_MF(32, 4) LOOM_GQA_MF(32, 1) LOOM_GQA_MF(32, 2) LOOM_GQA_MF(32, 8)
+#undef LOOM_GQA_MF
+    }
 #define LOOM_GQA(E, GG, LPR)                                                                    \
     if (HD == E * LPR && G == GG) {                                                             \
         if (from_qkv)                                                                           \
