@@ -407,8 +407,33 @@ __device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
+// Barrier for LDS traffic only: waits for this wave's LDS operations, not
+// for its outstanding global loads (which __syncthreads would also drain).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Eight consecutive elements d0..d0+7 of a head, roped for one position
+// (d0 a multiple of 8 and HD/2 a multiple of 8: the group never straddles
+// the rotate-half boundary): 16-byte loads of x and its partner half.
+__device__ __forceinline__ void rope8(const bf16_t* head, const float* cr, const float* sr, int d0,
+                                      int HD, float out[8]) {
+    const int half = HD / 2;
+    float x[8], y[8], c[8], sn[8];
+    Vec8<bf16_t>::load(head + d0, x);
+    Vec8<bf16_t>::load(head + (d0 < half ? d0 + half : d0 - half), y);
+    Vec8<float>::load(cr + d0, c);
+    Vec8<float>::load(sr + d0, sn);
+    const float sg = d0 < half ? -1.0f : 1.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = fmaf(x[e], c[e], sg * y[e] * sn[e]);
+}
+
+// 3 waves per SIMD (<= 168 VGPRs): all chunk blocks of a decode step resident in one round
 template <int HD, int G, bool FROM_QKV>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3)))
 gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     constexpr int KK = HD / 32;            // 32-wide k-steps of a head
     constexpr int DT = HD / 16;            // 16-wide output tiles of a head
@@ -437,19 +462,53 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     const int QKV = (a.QH + 2 * a.KVH) * HD;
     Tiles& tl = reinterpret_cast<Tiles*>(lds)[wave];
 
-    // FROM_QKV: the block holding pos appends this token's (k_roped, v) first,
-    // then reads it back like every cached row
+    // FROM_QKV: the block holding pos appends this token's (k_roped, v) to the
+    // caches; its own attention takes that row from the qkv registers below,
+    // so nothing in this launch reads the appended row back
+    const bf16_t* krow_new = a.q + b * QKV + (a.QH + kvh) * HD;
+    const bf16_t* vrow_new = krow_new + a.KVH * HD;
+    __shared__ uint4 knew[HD / 8], vnew[HD / 8];   // this token's (k_roped, v) as bf16
     if constexpr (FROM_QKV) {
-        if (t1 == len && tid < HD) {
-            const bf16_t* krow = a.q + b * QKV + (a.QH + kvh) * HD;
-            const bf16_t* vrow = krow + a.KVH * HD;
-            const float* cr = a.cosv + pos * HD;
-            const float* sr = a.sinv + pos * HD;
-            st(a.kc + b * a.csb + pos * a.cst + kvh * HD + tid, rope_elem(krow, cr, sr, tid, HD));
-            a.vc[b * a.csb + pos * a.cst + kvh * HD + tid] = vrow[tid];
+        if (t1 == len && tid < HD / 8) {
+            float x[8];
+            rope8(krow_new, a.cosv + pos * HD, a.sinv + pos * HD, 8 * tid, HD, x);
+            const uint4 kw = make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]),
+                                        pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
+            const uint4 vw = *reinterpret_cast<const uint4*>(vrow_new + 8 * tid);
+            *reinterpret_cast<uint4*>(a.kc + b * a.csb + pos * a.cst + kvh * HD + 8 * tid) = kw;
+            *reinterpret_cast<uint4*>(a.vc + b * a.csb + pos * a.cst + kvh * HD + 8 * tid) = vw;
+            knew[tid] = kw;
+            vnew[tid] = vw;
         }
-        __syncthreads();                   // stores complete (vmcnt) before any wave reads row pos
+        lds_barrier();
     }
+    const bf16_t* kb = a.kc + b * a.csb + kvh * HD;
+    const bf16_t* vb = a.vc + b * a.csb + kvh * HD;
+    const int nstep = (int)((t1 - t0 + 4 * kMfTile - 1) / (4 * kMfTile));
+    // K and V rows ts + 16*hf + lr, dims 32*kk + 8*lq (row clamped in range; masked
+    // below); the next step's rows are requested as soon as this step's are in LDS
+    uint4 kr[2][KK], vr[2][KK];
+    auto load_kv = [&](int64_t ts) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            int64_t t = ts + 16 * hf + lr;
+            t = t < t1 ? t : t1 - 1;
+            if (FROM_QKV && t == pos) {            // this token: the row staged in LDS
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) {
+                    kr[hf][kk] = knew[4 * kk + lq];
+                    vr[hf][kk] = vnew[4 * kk + lq];
+                }
+                continue;
+            }
+#pragma unroll
+            for (int kk = 0; kk < KK; ++kk) {
+                kr[hf][kk] = *reinterpret_cast<const uint4*>(kb + t * a.cst + 32 * kk + 8 * lq);
+                vr[hf][kk] = *reinterpret_cast<const uint4*>(vb + t * a.cst + 32 * kk + 8 * lq);
+            }
+        }
+    };
+    load_kv(t0 + wave * kMfTile);
     // B operand of S^T: q of head lr, dims 32*kk + 8*lq .. +7, rounded to bf16
     uint4 qf[KK];
 #pragma unroll
@@ -460,11 +519,8 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
         if (lr < G) {
             const int d0 = 32 * kk + 8 * lq;
             if constexpr (FROM_QKV) {
-                const bf16_t* qh = a.q + b * QKV + (kvh * G + lr) * HD;
-                const float* cr = a.cosv + pos * HD;
-                const float* sr = a.sinv + pos * HD;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] = rope_elem(qh, cr, sr, d0 + e, HD);
+                rope8(a.q + b * QKV + (kvh * G + lr) * HD, a.cosv + pos * HD, a.sinv + pos * HD, d0,
+                      HD, x);
                 if (a.q_out != nullptr && chunk == 0 && wave == 0)
                     Vec8<bf16_t>::store(a.q_out + (b * a.QH + kvh * G + lr) * HD + d0, x);
             } else {
@@ -474,8 +530,6 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
         qf[kk] = make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]),
                             pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
     }
-    const bf16_t* kb = a.kc + b * a.csb + kvh * HD;
-    const bf16_t* vb = a.vc + b * a.csb + kvh * HD;
     float mh = -INFINITY, lh = 0.0f;       // running max / sum of head lr (lanes l%16 == head)
     f32x4_t accC[DT], accK[DT];
 #pragma unroll
@@ -483,21 +537,8 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
 
     // every wave runs the same number of steps (the loop holds barriers); a
     // step past t1 is fully masked
-    const int nstep = (int)((t1 - t0 + 4 * kMfTile - 1) / (4 * kMfTile));
     for (int it = 0; it < nstep; ++it) {
         const int64_t ts = t0 + wave * kMfTile + (int64_t)it * 4 * kMfTile;
-        // K and V rows ts + 16*hf + lr, dims 32*kk + 8*lq (row clamped in range; masked below)
-        uint4 kr[2][KK], vr[2][KK];
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            int64_t t = ts + 16 * hf + lr;
-            t = t < t1 ? t : t1 - 1;
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-                kr[hf][kk] = *reinterpret_cast<const uint4*>(kb + t * a.cst + 32 * kk + 8 * lq);
-                vr[hf][kk] = *reinterpret_cast<const uint4*>(vb + t * a.cst + 32 * kk + 8 * lq);
-            }
-        }
         // S^T[position 16*hf + 4*lq + r][head lr]
         f32x4_t sc[2];
 #pragma unroll
@@ -549,7 +590,8 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
                     tl.vt[d][16 * hf + lr] = (uint16_t)(vw[e >> 1] >> (16 * (e & 1)));
                 }
             }
-        __syncthreads();
+        if (it + 1 < nstep) load_kv(ts + 4 * kMfTile);
+        lds_barrier();
         // rescale the accumulators (rows = heads 4*lq + r) and add P V, P K
         float cf[4];
 #pragma unroll
@@ -567,7 +609,7 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
             accC[dt] = mfma16(pa, vbf, accC[dt]);
             accK[dt] = mfma16(pa, kbf, accK[dt]);
         }
-        __syncthreads();                   // tiles are rewritten next step
+        lds_barrier();                     // tiles are rewritten next step
     }
     // this wave's partials -> wred[wave] = [m | l | c | k] (unnormalised)
     float (*wred)[REC] = reinterpret_cast<float (*)[REC]>(lds);
