@@ -308,14 +308,17 @@ int loom_final_ca_sparse_strided(int dtype, const void* q, const void* k, const 
  * YaRNRotaryEmbedding.forward :2983-2985).
  *   qkv: [B, (QH + 2*KVH)*HD] dtype (output of the qkv projection);
  *   q_out: [B,QH,HD] dtype (rotated q); cache element (b, t, kvh, d) at
- *   b*cache_stride_b + t*cache_stride_t + kvh*HD + d; position `pos` is written
+ *   b*cache_stride_b + t*cache_stride_t + kvh*cache_stride_h + d (a
+ *   [B,T,KVH,HD] cache has cache_stride_h = HD, a head-major [B,KVH,T,HD] one
+ *   cache_stride_t = HD); position `pos` is written
  *   (or *pos_dev, read on the device, when pos_dev != NULL).
  *   cos_table/sin_table: [>pos, HD] float, already multiplied by the YaRN
  *   attention factor (the reference's cos_cached/sin_cached). */
 int loom_rope_append(int dtype, const void* qkv, void* q_out, void* k_cache, void* v_cache,
                      const float* cos_table, const float* sin_table, int64_t B, int64_t pos,
                      const int64_t* pos_dev, int64_t QH, int64_t KVH, int64_t HD,
-                     int64_t cache_stride_b, int64_t cache_stride_t, void* stream);
+                     int64_t cache_stride_b, int64_t cache_stride_t, int64_t cache_stride_h,
+                     void* stream);
 
 /* Bytes of workspace loom_gqa_decode_attention / loom_gqa_decode_step need for
  * len <= max_len: a 256-byte-rounded block of B*KVH int32 arrival counters,
@@ -334,8 +337,8 @@ int64_t loom_gqa_workspace_bytes(int64_t B, int64_t max_len, int64_t QH, int64_t
  *   the length is *pos_dev + 1 (read on the device) and `len` is the capacity
  *   the launch covers.  Calls that share a workspace must not overlap. */
 int loom_gqa_decode_attention(int dtype, const void* q, const void* k_cache, const void* v_cache,
-                              int64_t cache_stride_b, int64_t cache_stride_t, void* c_out,
-                              void* kctx_out, float* workspace, int64_t workspace_bytes,
+                              int64_t cache_stride_b, int64_t cache_stride_t,
+                              int64_t cache_stride_h, void* c_out, void* kctx_out, float* workspace, int64_t workspace_bytes,
                               int64_t B, int64_t len, const int64_t* pos_dev, int64_t QH,
                               int64_t KVH, int64_t HD, void* stream);
 
@@ -349,8 +352,9 @@ int loom_gqa_decode_attention(int dtype, const void* q, const void* k_cache, con
  * out_stride_b elements apart (>= QH*HD), so they can land inside a wider
  * row.  Equivalent to loom_rope_append followed by loom_gqa_decode_attention. */
 int loom_gqa_decode_step(int dtype, const void* qkv, void* k_cache, void* v_cache,
-                         int64_t cache_stride_b, int64_t cache_stride_t, const float* cos_table,
-                         const float* sin_table, void* q_out, void* c_out, void* kctx_out,
+                         int64_t cache_stride_b, int64_t cache_stride_t, int64_t cache_stride_h,
+                         const float* cos_table, const float* sin_table, void* q_out, void* c_out,
+                         void* kctx_out,
                          int64_t out_stride_b,
                          float* workspace, int64_t workspace_bytes, int64_t B, int64_t len,
                          const int64_t* pos_dev, int64_t QH, int64_t KVH, int64_t HD,

@@ -17,7 +17,7 @@ __global__ void __launch_bounds__(256)
 rope_append_kernel(const T* __restrict__ qkv, T* __restrict__ q_out, T* __restrict__ kc,
                    T* __restrict__ vc, const float* __restrict__ cosv, const float* __restrict__ sinv,
                    int64_t B, int64_t pos, const int64_t* __restrict__ pos_dev, int QH, int KVH,
-                   int HD, int64_t cstride_b, int64_t cstride_t) {
+                   int HD, int64_t cstride_b, int64_t cstride_t, int64_t cstride_h) {
     if (pos_dev != nullptr) pos = *pos_dev;
     const int heads = QH + 2 * KVH;
     const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -36,10 +36,10 @@ rope_append_kernel(const T* __restrict__ qkv, T* __restrict__ q_out, T* __restri
         if (hs < QH)
             st(q_out + (b * QH + hs) * HD + d, v);
         else
-            st(kc + b * cstride_b + pos * cstride_t + (hs - QH) * HD + d, v);
+            st(kc + b * cstride_b + pos * cstride_t + (hs - QH) * cstride_h + d, v);
     } else {
         const int kvh = hs - QH - KVH;
-        st(vc + b * cstride_b + pos * cstride_t + kvh * HD + d, ld(row + hs * HD + d));
+        st(vc + b * cstride_b + pos * cstride_t + kvh * cstride_h + d, ld(row + hs * HD + d));
     }
 }
 
@@ -77,7 +77,7 @@ struct GqaArgs {
     const T* q;            // roped q [B, QH, HD], or the qkv rows [B, (QH + 2 KVH) HD]
     T* kc;
     T* vc;
-    int64_t csb, cst;      // cache strides (elements) of b and t
+    int64_t csb, cst, csh; // cache strides (elements) of b, t and kv head
     const float* cosv;     // FROM_QKV: RoPE tables [*, HD] (attention factor folded in)
     const float* sinv;
     T* q_out;              // FROM_QKV, optional: the roped q [B, QH, HD]
@@ -249,8 +249,8 @@ gqa_decode_kernel(GqaArgs<T> a) {
                 qv[g][e] = ld(a.q + (b * a.QH + kvh * G + g) * HD + d0 + e) * a.qscale;
     }
 
-    const T* kbase = a.kc + b * a.csb + kvh * HD + d0;
-    const T* vbase = a.vc + b * a.csb + kvh * HD + d0;
+    const T* kbase = a.kc + b * a.csb + kvh * a.csh + d0;
+    const T* vbase = a.vc + b * a.csb + kvh * a.csh + d0;
     float m[G], l[G], ac[G][EPL], ak[G][EPL];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -330,8 +330,8 @@ gqa_decode_kernel(GqaArgs<T> a) {
                 kn[0][e] = ld(&kt);
                 vn[0][e] = ld(&vt);
             }
-            RowIO<T, EPL>::store(a.kc + b * a.csb + pos * a.cst + kvh * HD + d0, kn[0]);
-            RowIO<T, EPL>::store(a.vc + b * a.csb + pos * a.cst + kvh * HD + d0, vn[0]);
+            RowIO<T, EPL>::store(a.kc + b * a.csb + pos * a.cst + kvh * a.csh + d0, kn[0]);
+            RowIO<T, EPL>::store(a.vc + b * a.csb + pos * a.cst + kvh * a.csh + d0, vn[0]);
             const bool one = true;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
@@ -475,15 +475,15 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
             const uint4 kw = make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]),
                                         pack_bf16x2(x[4], x[5]), pack_bf16x2(x[6], x[7]));
             const uint4 vw = *reinterpret_cast<const uint4*>(vrow_new + 8 * tid);
-            *reinterpret_cast<uint4*>(a.kc + b * a.csb + pos * a.cst + kvh * HD + 8 * tid) = kw;
-            *reinterpret_cast<uint4*>(a.vc + b * a.csb + pos * a.cst + kvh * HD + 8 * tid) = vw;
+            *reinterpret_cast<uint4*>(a.kc + b * a.csb + pos * a.cst + kvh * a.csh + 8 * tid) = kw;
+            *reinterpret_cast<uint4*>(a.vc + b * a.csb + pos * a.cst + kvh * a.csh + 8 * tid) = vw;
             knew[tid] = kw;
             vnew[tid] = vw;
         }
         lds_barrier();
     }
-    const bf16_t* kb = a.kc + b * a.csb + kvh * HD;
-    const bf16_t* vb = a.vc + b * a.csb + kvh * HD;
+    const bf16_t* kb = a.kc + b * a.csb + kvh * a.csh;
+    const bf16_t* vb = a.vc + b * a.csb + kvh * a.csh;
     const int nstep = (int)((t1 - t0 + 4 * kMfTile - 1) / (4 * kMfTile));
     // K and V rows ts + 16*hf + lr, dims 32*kk + 8*lq (row clamped in range; masked
     // below); the next step's rows are requested as soon as this step's are in LDS
@@ -786,17 +786,17 @@ template <typename T>
 static int rope_dispatch(const void* qkv, void* q_out, void* kc, void* vc, const float* cosv,
                          const float* sinv, int64_t B, int64_t pos, const int64_t* pos_dev,
                          int64_t QH, int64_t KVH, int64_t HD, int64_t sb, int64_t stt,
-                         hipStream_t st) {
+                         int64_t sh, hipStream_t st) {
     const int64_t total = B * (QH + 2 * KVH) * HD;
     hipLaunchKernelGGL((rope_append_kernel<T>), dim3((unsigned)ceil_div(total, 256)), dim3(256), 0,
                        st, (const T*)qkv, (T*)q_out, (T*)kc, (T*)vc, cosv, sinv, B, pos, pos_dev,
-                       (int)QH, (int)KVH, (int)HD, sb, stt);
+                       (int)QH, (int)KVH, (int)HD, sb, stt, sh);
     return launch_status("loom_rope_append");
 }
 
 template <typename T>
 static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void* vc, int64_t sb,
-                        int64_t stt, const float* cosv, const float* sinv, void* q_out,
+                        int64_t stt, int64_t sh, const float* cosv, const float* sinv, void* q_out,
                         void* c_out, void* k_out,
                         int64_t out_sb, float* ws, int64_t B, int64_t len, const int64_t* pos_dev,
                         int64_t QH, int64_t KVH, int64_t HD, hipStream_t st) {
@@ -808,6 +808,7 @@ static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void
     a.vc = (T*)vc;
     a.csb = sb;
     a.cst = stt;
+    a.csh = sh;
     a.cosv = cosv;
     a.sinv = sinv;
     a.q_out = (T*)q_out;
@@ -913,20 +914,22 @@ extern "C" int loom_rope_append(int dtype, const void* qkv, void* q_out, void* k
                                 void* v_cache, const float* cos_table, const float* sin_table,
                                 int64_t B, int64_t pos, const int64_t* pos_dev, int64_t QH,
                                 int64_t KVH, int64_t HD, int64_t cache_stride_b,
-                                int64_t cache_stride_t, void* stream) {
+                                int64_t cache_stride_t, int64_t cache_stride_h, void* stream) {
     clear_error();
     LOOM_CHECK(qkv && q_out && k_cache && v_cache && cos_table && sin_table,
                "rope_append: null argument");
     LOOM_CHECK(HD % 2 == 0 && QH > 0 && KVH > 0 && pos >= 0, "rope_append: bad shape");
-    LOOM_CHECK(cache_stride_t >= KVH * HD, "rope_append: cache row stride too small");
+    LOOM_CHECK(cache_stride_t >= HD && cache_stride_h >= HD,
+               "rope_append: cache strides smaller than a head row");
     if (B == 0) return LOOM_OK;
     LOOM_DTYPE_SWITCH(dtype, rope_dispatch, qkv, q_out, k_cache, v_cache, cos_table, sin_table, B,
-                      pos, pos_dev, QH, KVH, HD, cache_stride_b, cache_stride_t,
+                      pos, pos_dev, QH, KVH, HD, cache_stride_b, cache_stride_t, cache_stride_h,
                       (hipStream_t)stream)
 }
 
 static int gqa_checks(const char* who, const void* k_cache, const void* v_cache,
-                      int64_t cache_stride_b, int64_t cache_stride_t, const void* workspace,
+                      int64_t cache_stride_b, int64_t cache_stride_t, int64_t cache_stride_h,
+                      const void* workspace,
                       int64_t workspace_bytes, int64_t B, int64_t len, int64_t QH, int64_t KVH,
                       int64_t HD) {
     LOOM_CHECK(len >= 1 && KVH >= 1 && QH % KVH == 0 && QH / KVH <= kAttnMaxG,
@@ -936,16 +939,20 @@ static int gqa_checks(const char* who, const void* k_cache, const void* v_cache,
                "%s: workspace too small (%lld bytes)", who, (long long)workspace_bytes);
     LOOM_CHECK(((uintptr_t)workspace & 255) == 0, "%s: workspace must be 256-byte aligned", who);
     // cache rows are read as 4-/8-byte words when each lane owns an even count
-    LOOM_CHECK(HD % 32 != 0 || ((((uintptr_t)k_cache | (uintptr_t)v_cache) & 7) == 0 &&
-                                cache_stride_b % 2 == 0 && cache_stride_t % 2 == 0),
-               "%s: caches must be 8-byte aligned with even strides", who);
-    LOOM_CHECK(cache_stride_t >= KVH * HD, "%s: cache row stride too small", who);
+    // (the bf16 MFMA form reads 16-byte pieces: 16-byte aligned, strides multiples of 8)
+    LOOM_CHECK(HD % 32 != 0 || ((((uintptr_t)k_cache | (uintptr_t)v_cache) & 15) == 0 &&
+                                cache_stride_b % 8 == 0 && cache_stride_t % 8 == 0 &&
+                                cache_stride_h % 8 == 0),
+               "%s: caches must be 16-byte aligned with strides divisible by 8", who);
+    LOOM_CHECK(cache_stride_t >= HD && cache_stride_h >= HD,
+               "%s: cache strides smaller than a head row", who);
     return LOOM_OK;
 }
 
 extern "C" int loom_gqa_decode_attention(int dtype, const void* q, const void* k_cache,
                                          const void* v_cache, int64_t cache_stride_b,
-                                         int64_t cache_stride_t, void* c_out, void* kctx_out,
+                                         int64_t cache_stride_t, int64_t cache_stride_h,
+                                         void* c_out, void* kctx_out,
                                          float* workspace, int64_t workspace_bytes, int64_t B,
                                          int64_t len, const int64_t* pos_dev, int64_t QH,
                                          int64_t KVH, int64_t HD, void* stream) {
@@ -953,17 +960,20 @@ extern "C" int loom_gqa_decode_attention(int dtype, const void* q, const void* k
     LOOM_CHECK(q && k_cache && v_cache && c_out && kctx_out && workspace,
                "gqa_decode_attention: null argument");
     const int rc = gqa_checks("gqa_decode_attention", k_cache, v_cache, cache_stride_b,
-                              cache_stride_t, workspace, workspace_bytes, B, len, QH, KVH, HD);
+                              cache_stride_t, cache_stride_h, workspace, workspace_bytes, B, len,
+                              QH, KVH, HD);
     if (rc != LOOM_OK) return rc;
     if (B == 0) return LOOM_OK;
     LOOM_DTYPE_SWITCH(dtype, gqa_dispatch, false, q, k_cache, v_cache, cache_stride_b,
-                      cache_stride_t, nullptr, nullptr, nullptr, c_out, kctx_out, QH * HD, workspace, B,
+                      cache_stride_t, cache_stride_h, nullptr, nullptr, nullptr, c_out, kctx_out,
+                      QH * HD, workspace, B,
                       len, pos_dev, QH, KVH, HD, (hipStream_t)stream)
 }
 
 extern "C" int loom_gqa_decode_step(int dtype, const void* qkv, void* k_cache, void* v_cache,
                                     int64_t cache_stride_b, int64_t cache_stride_t,
-                                    const float* cos_table, const float* sin_table, void* q_out,
+                                    int64_t cache_stride_h, const float* cos_table,
+                                    const float* sin_table, void* q_out,
                                     void* c_out, void* kctx_out, int64_t out_stride_b, float* workspace,
                                     int64_t workspace_bytes, int64_t B, int64_t len,
                                     const int64_t* pos_dev, int64_t QH, int64_t KVH, int64_t HD,
@@ -974,11 +984,12 @@ extern "C" int loom_gqa_decode_step(int dtype, const void* qkv, void* k_cache, v
                "gqa_decode_step: null argument");
     LOOM_CHECK(HD % 2 == 0 && out_stride_b >= QH * HD, "gqa_decode_step: bad head_dim / out stride");
     const int rc = gqa_checks("gqa_decode_step", k_cache, v_cache, cache_stride_b, cache_stride_t,
-                              workspace, workspace_bytes, B, len, QH, KVH, HD);
+                              cache_stride_h, workspace, workspace_bytes, B, len, QH, KVH, HD);
     if (rc != LOOM_OK) return rc;
     if (B == 0) return LOOM_OK;
     LOOM_DTYPE_SWITCH(dtype, gqa_dispatch, true, qkv, k_cache, v_cache, cache_stride_b,
-                      cache_stride_t, cos_table, sin_table, q_out, c_out, kctx_out, out_stride_b,
+                      cache_stride_t, cache_stride_h, cos_table, sin_table, q_out, c_out, kctx_out,
+                      out_stride_b,
                       workspace, B, len, pos_dev, QH, KVH, HD, (hipStream_t)stream)
 }
 

@@ -58,11 +58,12 @@ SIGNATURES = {
     "loom_final_ca_sparse_strided": [c_int, _P, _P, _P, c_int64, _P, c_int64, _P, c_float, _P,
                                      _P, c_int64, c_int64, c_int64, _P, c_int64, c_float, _P],
     "loom_rope_append": [c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, _P, c_int64, c_int64,
-                         c_int64, c_int64, c_int64, _P],
-    "loom_gqa_decode_attention": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64,
-                                  c_int64, c_int64, _P, c_int64, c_int64, c_int64, _P],
-    "loom_gqa_decode_step": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, _P, _P, c_int64,
-                             _P, c_int64, c_int64, c_int64, _P, c_int64, c_int64, c_int64, _P],
+                         c_int64, c_int64, c_int64, c_int64, _P],
+    "loom_gqa_decode_attention": [c_int, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P,
+                                  c_int64, c_int64, c_int64, _P, c_int64, c_int64, c_int64, _P],
+    "loom_gqa_decode_step": [c_int, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P,
+                             c_int64, _P, c_int64, c_int64, c_int64, _P, c_int64, c_int64, c_int64,
+                             _P],
     "loom_decode_prologue": [_P, _P, c_int64, c_int64, _P, c_int64, _P, _P, _P, _P, c_int64,
                              c_int64, c_int64, c_int64, _P],
     "loom_decode_epilogue": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64,

@@ -100,8 +100,9 @@ class LoomDecoder:
 
         B, N, H, L = self.B, c.N, c.H, c.L
         z = lambda *s, dtype=dt: torch.zeros(*s, dtype=dtype, device=dev)
-        self.k_cache = z(L, B, self.max_len, c.KVH, c.HD)
-        self.v_cache = z(L, B, self.max_len, c.KVH, c.HD)
+        # head-major caches [L, B, KVH, max_len, HD]: one kv head's rows are contiguous
+        self.k_cache = z(L, B, c.KVH, self.max_len, c.HD)
+        self.v_cache = z(L, B, c.KVH, self.max_len, c.HD)
         self.hist = z(B, 2 * L, 2 * N)
         self.trace = z(L, B, H)
         self.doc = z(B, H, 3, 3)
@@ -219,8 +220,9 @@ class LoomDecoder:
         self._multi("first", self.h, [dict(w=self.kvw, out=hist[:, 0]),
                                       dict(w=self.blocks[0]["qkv"], out=self.qkv)])
         sub = 0
-        cache_sb = self.max_len * c.KVH * c.HD
-        cache_st = c.KVH * c.HD
+        cache_sb = c.KVH * self.max_len * c.HD
+        cache_st = c.HD
+        cache_sh = self.max_len * c.HD
         carry_i = None          # index of the current depth carry in self.carry
         p_i = None              # index of the gate output p feeding the next block
         for bi, blk in enumerate(self.blocks):
@@ -229,7 +231,8 @@ class LoomDecoder:
             # ---- attention step (loomformer.py:3300-3332): RoPE + cache append +
             # attention + chunk merge, one launch
             self._call("loom_gqa_decode_step", self.code, _P(self.qkv), _P(kc), _P(vc), cache_sb,
-                       cache_st, _P(self.cos), _P(self.sin), _P(self.q), _P(self.c), _P(self.kctx), N,
+                       cache_st, cache_sh, _P(self.cos), _P(self.sin), _P(self.q), _P(self.c),
+                       _P(self.kctx), N,
                        _P(self.ws), self.ws_bytes, B, self.max_len, _P(self.pos_dev), c.QH, c.KVH,
                        c.HD, st)
             # ---- depth read 2*bi, then LN(o(c) + w_o(d)) (loomformer.py:3999-4000):

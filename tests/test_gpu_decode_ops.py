@@ -72,7 +72,7 @@ def test_rope_append(dtype):
     q = torch.empty(B, QH, HD, device=DEV, dtype=dtype)
     cos_d, sin_d = cos.to(DEV), sin.to(DEV)       # keep the device copies alive across the call
     L().call("loom_rope_append", code(qkv), P(qkv), P(q), P(kc), P(vc), P(cos_d), P(sin_d),
-             B, pos, None, QH, KVH, HD, max_len * KVH * HD, KVH * HD, S(qkv))
+             B, pos, None, QH, KVH, HD, max_len * KVH * HD, KVH * HD, HD, S(qkv))
     x = host(qkv)
     c, s = cos[pos].view(1, 1, HD), sin[pos].view(1, 1, HD)
     check(q, ref.apply_rope(x[:, :QH * HD].view(B, QH, HD), c, s), dtype)
@@ -82,7 +82,7 @@ def test_rope_append(dtype):
     # the position can come from device memory instead (graph replay)
     pos_d = torch.tensor([pos + 1], dtype=torch.int64, device=DEV)
     L().call("loom_rope_append", code(qkv), P(qkv), P(q), P(kc), P(vc), P(cos_d), P(sin_d),
-             B, 0, P(pos_d), QH, KVH, HD, max_len * KVH * HD, KVH * HD, S(qkv))
+             B, 0, P(pos_d), QH, KVH, HD, max_len * KVH * HD, KVH * HD, HD, S(qkv))
     c1, s1 = cos[pos + 1].view(1, 1, HD), sin[pos + 1].view(1, 1, HD)
     check(kc[:, pos + 1], ref.apply_rope(x[:, QH * HD:(QH + KVH) * HD].view(B, KVH, HD), c1, s1), dtype)
 
@@ -103,7 +103,7 @@ def test_gqa_decode_attention(dtype, B, QH, KVH, HD, length):
     nb = _lib.load().loom_gqa_workspace_bytes(B, max_len, QH, KVH, HD)
     ws = torch.zeros(nb // 4 + 1, device=DEV)      # arrival counters start at zero
     _lib.call("loom_gqa_decode_attention", code(q), P(q), P(kc), P(vc), max_len * KVH * HD, KVH * HD,
-              P(c), P(kx), P(ws), nb, B, length, None, QH, KVH, HD, S(q))
+              HD, P(c), P(kx), P(ws), nb, B, length, None, QH, KVH, HD, S(q))
     G = QH // KVH
     K = host(kc)[:, :length].repeat_interleave(G, dim=2).transpose(1, 2)   # [B,QH,len,HD]
     V = host(vc)[:, :length].repeat_interleave(G, dim=2).transpose(1, 2)
@@ -115,7 +115,7 @@ def test_gqa_decode_attention(dtype, B, QH, KVH, HD, length):
     kx.zero_()
     pos_d = torch.tensor([length - 1], dtype=torch.int64, device=DEV)
     _lib.call("loom_gqa_decode_attention", code(q), P(q), P(kc), P(vc), max_len * KVH * HD, KVH * HD,
-              P(c), P(kx), P(ws), nb, B, max_len, P(pos_d), QH, KVH, HD, S(q))
+              HD, P(c), P(kx), P(ws), nb, B, max_len, P(pos_d), QH, KVH, HD, S(q))
     check(c, (a @ V).squeeze(2), dtype)
     check(kx, (a @ K).squeeze(2), dtype)
     # every call leaves the arrival counters at zero
@@ -129,10 +129,11 @@ def _rope_tables(HD, n):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_major", [False, True])
 @pytest.mark.parametrize("B,QH,KVH,HD,length", [
     (2, 8, 2, 96, 1), (3, 8, 2, 96, 255), (2, 8, 2, 96, 257), (32, 8, 2, 96, 700),
     (2, 4, 4, 64, 300), (2, 8, 1, 64, 513), (1, 4, 2, 8, 90), (2, 8, 2, 32, 256)])
-def test_gqa_decode_step(dtype, B, QH, KVH, HD, length):
+def test_gqa_decode_step(dtype, head_major, B, QH, KVH, HD, length):
     """RoPE + cache append + attention + merge in one launch, against the
     oracle's RoPE and a plain softmax over the appended cache."""
     from loom_amd import _lib
@@ -164,24 +165,34 @@ def test_gqa_decode_step(dtype, B, QH, KVH, HD, length):
     K = Kc[:, :length].repeat_interleave(G, dim=2).transpose(1, 2)
     V = Vc[:, :length].repeat_interleave(G, dim=2).transpose(1, 2)
     a = torch.softmax((qr.unsqueeze(2) @ K.transpose(-1, -2)) / math.sqrt(HD), dim=-1)
+    # cache layouts: [B, T, KVH, HD] (stride_h = HD) or head-major [B, KVH, T, HD]
+    if head_major:
+        kc = kc.transpose(1, 2).contiguous()
+        vc = vc.transpose(1, 2).contiguous()
+        strides = (KVH * max_len * HD, HD, max_len * HD)
+        view = lambda t: host(t).transpose(1, 2)   # back to [B, T, KVH, HD]
+    else:
+        strides = (max_len * KVH * HD, KVH * HD, HD)
+        view = host
     for call in range(2):                           # host length, then device position
         cbuf.zero_()
         kbuf.zero_()
-        kc.copy_(kc0.to(dtype))
-        vc.copy_(vc0.to(dtype))
-        _lib.call("loom_gqa_decode_step", code(qkv), P(qkv), P(kc), P(vc), max_len * KVH * HD,
-                  KVH * HD, P(cos_d), P(sin_d), P(qout), P(cbuf), P(kbuf), out_sb, P(ws), nb, B,
+        src_k, src_v = (kc0, vc0) if not head_major else (kc0.transpose(1, 2), vc0.transpose(1, 2))
+        kc.copy_(src_k.to(dtype))
+        vc.copy_(src_v.to(dtype))
+        _lib.call("loom_gqa_decode_step", code(qkv), P(qkv), P(kc), P(vc), *strides,
+                  P(cos_d), P(sin_d), P(qout), P(cbuf), P(kbuf), out_sb, P(ws), nb, B,
                   length if call == 0 else max_len, None if call == 0 else P(pos_d), QH, KVH, HD,
                   S(qkv))
         check(cbuf[:, :QH * HD].view(B, QH, HD), (a @ V).squeeze(2), dtype)
         check(kbuf[:, :QH * HD].view(B, QH, HD), (a @ K).squeeze(2), dtype)
         check(qout, qr, dtype)
         assert bool((cbuf[:, QH * HD:] == 0).all()) and bool((kbuf[:, QH * HD:] == 0).all())
-        torch.testing.assert_close(host(kc)[:, pos], kr, **TOL[dtype])
-        torch.testing.assert_close(host(vc)[:, pos], vn.to(dtype).float(), rtol=0, atol=0)
+        torch.testing.assert_close(view(kc)[:, pos], kr, **TOL[dtype])
+        torch.testing.assert_close(view(vc)[:, pos], vn.to(dtype).float(), rtol=0, atol=0)
         rest = [t for t in range(max_len) if t != pos]
-        assert torch.equal(host(kc)[:, rest], kc0[:, rest])
-        assert torch.equal(host(vc)[:, rest], vc0[:, rest])
+        assert torch.equal(view(kc)[:, rest], kc0[:, rest])
+        assert torch.equal(view(vc)[:, rest], vc0[:, rest])
         assert int(ws[:B * KVH].view(torch.int32).abs().sum().item()) == 0
 
 
