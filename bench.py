@@ -12,7 +12,9 @@ Microbenchmarks, each timed live with HIP events on
 the stream the kernels run on:
   PX  Paraplex FFN, 8192 tokens as [8, 1024], N=768, H=3072, bf16
   DA  DepthAttn, 16384 tokens, 24 earlier-depth states, 8x96, bf16
-  TR  Tria depth op (gated step), B=8 x T=4096 x H=3072, fp32
+  TR  Tria, B=8 x T=4096 x H=3072, 24 layers, fp32: the gated depth step
+      alone, and the whole chunked path (depth composition, temporal carry
+      every 64 tokens with PolARM at fires) plus the readout to d_model=768
 ``roofline`` reports the fused Paraplex pointwise kernel (the path's fused
 HBM-bound kernel): algorithmic bytes (R, beta in; I, O out = 8 B/elem in
 bf16) per launch over its mean launch time, against 8 TB/s.
@@ -208,6 +210,38 @@ def bench_tr(iters):
                 endpoint_w64_ms=ms_end, endpoint_w64_GBs=end_bytes / (ms_end * 1e-3) / 1e9)
 
 
+def bench_tr_pipeline(iters):
+    """The whole TR microbench path: B=8 x T=4096 tokens, 24 layers, H=3072,
+    fp32, fires every 64 tokens (63 boundaries), PolARM beta 0.1, then the
+    readout of the 63 document keys to d_model=768."""
+    import torch
+    from loom_amd import ops
+
+    dev = "cuda"
+    L, B, T, H, W, N = 24, 8, 4096, 3072, 64, 768
+    g = torch.Generator(device=dev).manual_seed(5)
+    r, i, o = (torch.randn(L, B, T, H, generator=g, device=dev) for _ in range(3))
+    key_w = torch.randn(32, 9, generator=g, device=dev) * 1.5
+    query = torch.randn(32, generator=g, device=dev)
+    raw = key_w.t() @ query
+    score_w = raw / raw.norm().clamp_min(1e-6)
+    pw, pb = torch.randn(32, 9, generator=g, device=dev) / 3, torch.zeros(32, device=dev)
+    uw, ub = torch.randn(N, 32, generator=g, device=dev) / 6, torch.zeros(N, device=dev)
+    out = {}
+
+    def chunked():
+        out["keys"] = ops.tria_chunked_forward(r, i, o, 0.025, W, 0.1)[0]
+
+    ms = timed(chunked, iters)
+    keys = out["keys"]
+    ms_read = timed(lambda: ops.tria_readout(keys, score_w, pw, pb, uw, ub), iters)
+    K = keys.shape[1]
+    nbytes = 3 * L * B * T * H * 4 + B * K * H * 36
+    del r, i, o
+    return dict(ms=ms, bytes=nbytes, GBs=nbytes / (ms * 1e-3) / 1e9, readout_ms=ms_read,
+                keys=K)
+
+
 def copy_bandwidth():
     import torch
     x = torch.empty(1 << 28, dtype=torch.float32, device="cuda")   # 1 GiB
@@ -298,6 +332,8 @@ def main():
         log(f"DA: {json.dumps({k: round(v, 3) for k, v in da.items()})}")
         tr = bench_tr(max(3, args.micro_iters // 4))
         log(f"TR: {json.dumps({k: round(v, 3) for k, v in tr.items()})}")
+        trp = bench_tr_pipeline(max(3, args.micro_iters // 4))
+        log(f"TR pipeline: {json.dumps({k: round(v, 3) for k, v in trp.items()})}")
         copy_gbs = copy_bandwidth()
         kernels = {
             "paraplex_pointwise": {"ms": px["pointwise_ms"], "GB/s": px["pointwise_GBs"],
@@ -306,6 +342,8 @@ def main():
             "tria_step_gate": {"ms": tr["step_gate_ms"], "GB/s": tr["step_gate_GBs"],
                                "frac": tr["step_gate_GBs"] / HBM_PEAK_GBS},
             "temporal_endpoint_w64": {"ms": tr["endpoint_w64_ms"], "GB/s": tr["endpoint_w64_GBs"]},
+            "tria_chunked_tr": {"ms": trp["ms"], "GB/s": trp["GBs"], "frac": trp["GBs"] / HBM_PEAK_GBS,
+                                "algorithmic_bytes": trp["bytes"], "readout_ms": trp["readout_ms"]},
             "w_real_gemm": {"ms": px["w_real_ms"], "TFLOP/s": px["w_real_TFLOPs"],
                             "frac": px["w_real_TFLOPs"] / BF16_PEAK_TFLOPS},
             "w_imag_gemm": {"ms": px["w_imag_ms"], "TFLOP/s": px["w_imag_TFLOPs"],

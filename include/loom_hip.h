@@ -278,6 +278,30 @@ int loom_temporal_carry_endpoint_forward(int dtype, const void* depth, const uin
 int loom_polarm_forward(int dtype, const void* in, void* out, const uint8_t* mask,
                         int64_t n, int64_t per_mask, float beta, float eps, void* stream);
 
+/* Tria path of the chunked sequence forward (Model._forward_chunked,
+ * loomformer.py:3788-3883) on the fixed fire grid every W tokens, in two
+ * launches: every token's L-layer depth composition (axis l % 3, C_1 = N(T_1),
+ * C_l = N(T_l C_{l-1})) folded into per-chunk temporal products, then the scan
+ * over chunk boundaries (seeded chunk starts, temporal restarts at document
+ * resets, PolARM at valid fires).  Replaces the per-chunk sequence of
+ * tria_init_seed / tria_step / temporal_carry_endpoint / polarm calls the
+ * reference issues (tria.py:814-910, :1089-1141, :128-166); the gated-slot
+ * outputs p of the middle layers are not produced (they feed the hidden
+ * stream, not the Tria carry).
+ *   r, i, o: L stacked [B,T,H] dtype slices, layer l at offset l*layer_stride;
+ *   reset: [B,T] bool (document starts; NULL = none after t = 0);
+ *   keys: [B, ceil(T/W)-1, H, 3, 3] float, the state after each boundary
+ *   (chunk ends except the last, t = T-1 never fires); may be NULL when T <= W;
+ *   depth_out: [B,T,H,3,3] dtype final-layer carry per token, or NULL;
+ *   ws: loom_tria_chunked_workspace_bytes(B,T,H,W) bytes, no initial contents;
+ *   eps: PolARM's floor for mean(diag M^T M) (1e-6 in the reference). */
+int64_t loom_tria_chunked_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t W);
+int loom_tria_chunked_forward(int dtype, const void* r, const void* i, const void* o,
+                              int64_t layer_stride, int64_t L, const uint8_t* reset,
+                              float* keys, void* depth_out, void* ws, int64_t ws_bytes,
+                              int64_t B, int64_t T, int64_t H, int64_t W, float alpha,
+                              float polarm_beta, float eps, void* stream);
+
 /* Sparse final cross-attention: per row (b,t) a masked softmax over K keys
  * (scale * q.k), out = sum_j w_j v_j, an all-masked row gives exact zeros and
  * lse = -inf.  Replaces final_ca_sparse_forward (bindings.cpp:107).

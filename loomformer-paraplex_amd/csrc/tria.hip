@@ -270,25 +270,7 @@ polarm_kernel(const T* __restrict__ in, T* __restrict__ out, const uint8_t* __re
     float M[9];
 #pragma unroll
     for (int k = 0; k < 9; ++k) M[k] = ld(in + e * 9 + k);
-    if (mask == nullptr || mask[e / per_mask] != 0) {
-        float G[9];  // G = M^T M
-#pragma unroll
-        for (int r = 0; r < 3; ++r)
-#pragma unroll
-            for (int c = 0; c < 3; ++c)
-                G[3 * r + c] = fmaf(M[6 + r], M[6 + c], fmaf(M[3 + r], M[3 + c], M[r] * M[c]));
-        const float s = fmaxf((G[0] + G[4] + G[8]) * (1.0f / 3.0f), eps);
-        float C[9];
-#pragma unroll
-        for (int k = 0; k < 9; ++k) {
-            const float id = (k == 0 || k == 4 || k == 8) ? 1.0f : 0.0f;
-            C[k] = id - 0.5f * beta * (G[k] / s - id);
-        }
-        float R[9];
-        mm3(M, C, R);
-#pragma unroll
-        for (int k = 0; k < 9; ++k) M[k] = R[k];
-    }
+    if (mask == nullptr || mask[e / per_mask] != 0) polarm9(M, beta, eps);
 #pragma unroll
     for (int k = 0; k < 9; ++k) st(out + e * 9 + k, M[k]);
 }

@@ -433,6 +433,48 @@ def polarm(matrix: torch.Tensor, beta: float = 0.1, eps: float = 1e-6,
     return out
 
 
+def tria_chunked_forward(r: torch.Tensor, i: torch.Tensor, o: torch.Tensor, alpha: float,
+                         window: int, polarm_beta: float = 0.1,
+                         reset: Optional[torch.Tensor] = None, want_depth: bool = False,
+                         eps: float = 1e-6):
+    """Tria part of Model._forward_chunked (loomformer.py:3788-3883) on the
+    fixed fire grid: r, i, o are [L,B,T,H] stacks of the per-layer summaries
+    (layer l uses axis l % 3).  Returns (keys [B,K,H,3,3] float32 with
+    K = ceil(T/window) - 1, depth [B,T,H,3,3] or None): the document keys
+    (state after each boundary's PolARM) and optionally each token's
+    final-layer depth carry."""
+    name = "tria_chunked_forward"
+    _cuda(r, i, o, name=name)
+    _same_dtype(r, i, o, name=name)
+    _check(r.dim() == 4 and r.shape == i.shape == o.shape, f"{name}: r, i, o must be [L,B,T,H]")
+    L, B, T, H = r.shape
+    _check(T >= 1 and window >= 1, f"{name}: need T >= 1 and window >= 1")
+    rc, ic, oc = r.contiguous(), i.contiguous(), o.contiguous()
+    rs = None
+    if reset is not None:
+        _check(reset.is_cuda and reset.dtype == torch.bool and reset.shape == (B, T),
+               f"{name}: reset must be a CUDA [B,T] bool tensor")
+        rs = reset.contiguous()
+    K = -(-T // window) - 1
+    keys = torch.empty(B, max(K, 0), H, 3, 3, dtype=torch.float32, device=r.device)
+    depth = torch.empty(B, T, H, 3, 3, dtype=r.dtype, device=r.device) if want_depth else None
+    nbytes = _lib.load().loom_tria_chunked_workspace_bytes(B, T, H, window)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=r.device)
+    call("loom_tria_chunked_forward", dtype_code(rc), ptr(rc), ptr(ic), ptr(oc), B * T * H, L,
+         ptr(rs), ptr(keys) if K > 0 else None, ptr(depth), ptr(ws), nbytes, B, T, H, window,
+         float(alpha), float(polarm_beta), float(eps), stream_of(rc))
+    return keys, depth
+
+
+def tria_readout(carry: torch.Tensor, score_w: torch.Tensor, proj_w: torch.Tensor,
+                 proj_b: torch.Tensor, up_w: torch.Tensor, up_b: torch.Tensor) -> torch.Tensor:
+    """TriaAggregator.forward (tria.py:1436-1441): slot-attention pool over H of
+    carry [B,K,H,3,3] with score_w [9], then proj (9 -> k) and up (k -> d_model)."""
+    pooled, _ = slot_attention_pool_forward(carry, score_w.to(carry.dtype))
+    z = linear(pooled, proj_w.to(carry.dtype), proj_b)
+    return linear(z, up_w.to(carry.dtype), up_b)
+
+
 # ---------------------------------------------------------------- projections
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,

@@ -444,20 +444,8 @@ class OracleModel(nn.Module):
             skip, d_h = self.depth_read(sub, hist_k[:, :, :sub + 1], hist_v[:, :, :sub + 1])
             ffn_out, next_trace, (r, i, o) = self.ffn(blk, h, q_h, kctx_h, c_h, d_h,
                                                       cache.phase_trace, p)
-            axis = bi % 3
             w = torch.softmax(blk.ffn.gate_selector.logits, dim=0)
-            if bi == 0 and seed is not None:
-                if last:
-                    carry, p = ops.tria_init_seed(r, i, o, seed, seed_valid, S.tria_alpha, axis), None
-                else:
-                    carry, p = ops.tria_init_seed_and_gate(r, i, o, seed, seed_valid, w, S.tria_alpha, axis)
-            elif last:
-                carry = (ops.tria_init(r, i, o, S.tria_alpha, axis) if carry is None
-                         else ops.tria_step(r, i, o, carry, S.tria_alpha, axis))
-                p = None
-            else:
-                carry, p = (ops.tria_init_and_gate(r, i, o, w, S.tria_alpha, axis) if carry is None
-                            else ops.tria_step_and_gate(r, i, o, carry, w, S.tria_alpha, axis))
+            carry, p = tria_layer_op(bi, last, r, i, o, carry, seed, seed_valid, w, S.tria_alpha)
             h = F.layer_norm(skip + ffn_out, (S.N,), blk.ln_ffn.weight, blk.ln_ffn.bias, 1e-5)
             if not last:
                 k_i, v_i = self.kv_project(h)
@@ -466,25 +454,52 @@ class OracleModel(nn.Module):
                 hist_v[:, :, sub] = v_i
             cache.phase_trace = next_trace
             cache.cache_len += 1
-        depth_t = carry[:, 0]
-        reset_now = pending | is_bos
-        if ts.carry is None:
-            doc = depth_t
-        else:
-            cont = ops.local_normalize(torch.matmul(depth_t, ts.carry))
-            doc = torch.where(reset_now[:, None, None, None], depth_t, cont)
-        hard_fire = (pos + 1 < S.seq_len) and ((pos + 1) % S.window == 0)
         if S.carry_token_id is not None:
             explicit = idx_t.view(-1).eq(int(S.carry_token_id))
         else:
             explicit = torch.zeros(B, dtype=torch.bool)
-        fire = explicit | hard_fire
-        if hard_fire or bool(explicit.any()):
-            doc = torch.where(fire[:, None, None, None], ops.polarm(doc, S.polarm_beta), doc)
+        doc, fire = tria_temporal_token(carry[:, 0], ts, pending, pos, explicit, S.seq_len,
+                                        S.window, S.polarm_beta)
         a_t = self.tria_agg_fn(doc.unsqueeze(1))
         h = self.final_ca_step(a_t, h, state.ca, fire)
         state.temporal = TemporalState(carry=doc, pending=fire)
         return self.head(h[:, -1, :]), state
+
+
+def tria_layer_op(bi: int, last: bool, r, i, o, carry, seed, seed_valid, w, alpha: float):
+    """The Tria depth op of block bi in Model.step (loomformer.py:4012-4040,
+    same choice as _block_core :3588-3617): axis bi % 3; the first block is
+    seeded when a seed is held, the last block is ungated.  Returns (carry, p)."""
+    axis = bi % 3
+    if bi == 0 and seed is not None:
+        if last:
+            return ops.tria_init_seed(r, i, o, seed, seed_valid, alpha, axis), None
+        return ops.tria_init_seed_and_gate(r, i, o, seed, seed_valid, w, alpha, axis)
+    if last:
+        return (ops.tria_init(r, i, o, alpha, axis) if carry is None
+                else ops.tria_step(r, i, o, carry, alpha, axis)), None
+    return (ops.tria_init_and_gate(r, i, o, w, alpha, axis) if carry is None
+            else ops.tria_step_and_gate(r, i, o, carry, w, alpha, axis))
+
+
+def tria_temporal_token(depth_t, ts: TemporalState, pending, pos: int, explicit,
+                        seq_len: int, window: int, polarm_beta: float):
+    """Temporal recurrence, fire and PolARM of one decode token
+    (loomformer.py:4056-4078): restart from the token's depth carry after a
+    fire or at position 0, else N(D_t @ state); hard fire when
+    (pos + 1) % window == 0 and pos + 1 < seq_len, or on an explicit <CARRY>
+    token; PolARM where fired.  Returns (doc [B,H,3,3], fire [B])."""
+    reset_now = pending | (pos == 0)
+    if ts.carry is None:
+        doc = depth_t
+    else:
+        cont = ops.local_normalize(torch.matmul(depth_t, ts.carry))
+        doc = torch.where(reset_now[:, None, None, None], depth_t, cont)
+    hard_fire = (pos + 1 < seq_len) and ((pos + 1) % window == 0)
+    fire = explicit | hard_fire
+    if hard_fire or bool(explicit.any()):
+        doc = torch.where(fire[:, None, None, None], ops.polarm(doc, polarm_beta), doc)
+    return doc, fire
 
 
 @torch.no_grad()

@@ -354,6 +354,70 @@ def polarm(matrix: torch.Tensor, beta: float = 0.1, eps: float = 1e-6) -> torch.
     return w @ (eye - 0.5 * beta * (gram / s - eye))
 
 
+def tria_chunked(r: torch.Tensor, i: torch.Tensor, o: torch.Tensor, alpha: float, window: int,
+                 polarm_beta: float = 0.1, reset: Optional[torch.Tensor] = None):
+    """Tria part of Model._forward_chunked (loomformer.py:3788-3883) with hard
+    fires on the grid only (no <CARRY> tokens), chunk by chunk as the reference
+    runs it: layer l of the chunk uses axis l % 3 (oracle.model's block loop,
+    loomformer.py:3588-3617); layer 0 of chunk c >= 1 is seeded with the
+    temporal state where seed_valid = fire[s-1] & ~reset[s] (:3826-3828);
+    the endpoint restarts at local resets and at a valid seed (:3834-3850);
+    at a boundary the state becomes polarm(state) where the fire is valid
+    (:3852-3858).  r, i, o: [L,B,T,H]; reset: [B,T] bool document starts
+    (None = position-0 only, :3534-3542).  Returns (keys [B,K,H,3,3],
+    depth [B,T,H,3,3])."""
+    L, B, T, H = r.shape
+    W = int(window)
+    doc_reset = torch.zeros(B, T, dtype=torch.bool) if reset is None else reset.bool().clone()
+    doc_reset[:, 0] = True
+    grid = ((torch.arange(T) + 1) % W) == 0
+    grid[-1] = False
+    next_is_reset = torch.zeros(B, T, dtype=torch.bool)
+    next_is_reset[:, :-1] = doc_reset[:, 1:]
+    fire = grid[None, :] & ~next_is_reset
+    bounds = grid.nonzero().flatten().tolist()
+    bset = set(bounds)
+    stops = bounds + ([T - 1] if not bounds or bounds[-1] != T - 1 else [])
+    state = None
+    keys, depth = [], []
+    s = 0
+    for bp in stops:
+        e = min(bp + 1, T)
+        seed = seed_valid = None
+        if state is not None:
+            seed_valid = fire[:, s - 1] & ~doc_reset[:, s]
+            seed = state
+        carry = None
+        for l in range(L):
+            ax = l % 3
+            rl, il, ol = r[l, :, s:e], i[l, :, s:e], o[l, :, s:e]
+            if l == 0:
+                carry = (tria_init_seed(rl, il, ol, seed, seed_valid, alpha, ax) if seed is not None
+                         else tria_init(rl, il, ol, alpha, ax))
+            else:
+                carry = tria_step(rl, il, ol, carry, alpha, ax)
+        local_reset = doc_reset[:, s:e].clone()
+        if seed_valid is not None:
+            local_reset[:, 0] |= seed_valid
+        if e != T or (e - 1) in bset:
+            state = temporal_carry_endpoint(carry, local_reset, initial_state=state)
+        depth.append(carry)
+        if (e - 1) in bset:
+            valid = fire[:, e - 1]
+            state = torch.where(valid[:, None, None, None], polarm(state, polarm_beta), state)
+            keys.append(state)
+        s = e
+    keys_t = torch.stack(keys, dim=1) if keys else torch.zeros(B, 0, H, 3, 3)
+    return keys_t, torch.cat(depth, dim=1)
+
+
+def tria_readout(carry: torch.Tensor, score_w: torch.Tensor, proj_w: torch.Tensor,
+                 proj_b: torch.Tensor, up_w: torch.Tensor, up_b: torch.Tensor) -> torch.Tensor:
+    """TriaAggregator.forward (tria.py:1436-1441): up(proj(pool(carry)))."""
+    pooled, _ = slot_attention_pool(carry, score_w)
+    return F.linear(F.linear(pooled, _f(proj_w), _f(proj_b)), _f(up_w), _f(up_b))
+
+
 def make_score_w(key_proj_w: torch.Tensor, query: torch.Tensor,
                  logit_scale: torch.Tensor) -> torch.Tensor:
     """score_w = normalize(key_proj^T query) * logit_scale (tria.py:1346-1349)."""

@@ -361,3 +361,97 @@ def test_yarn_reduces_to_rope_and_rotation_preserves_pairs():
     inv4, af4 = ops.yarn_inv_freq(HD, theta, 4.0, 2048, 32.0, 1.0)
     assert abs(af4 - (0.1 * math.log(4.0) + 1.0)) < 1e-7
     assert bool(((inv4 <= want * (1 + 1e-6)) & (inv4 >= want / 4 * (1 - 1e-6))).all())
+
+
+# ------------------------------------------------------------------ chunked Tria path
+
+def _tria_by_token(r, i, o, alpha, window, beta):
+    """Keys of the token-by-token formulation: Model.step's Tria bookkeeping
+    (oracle.model.tria_layer_op / tria_temporal_token, pinned by the decode
+    fixtures the reference wrote) driven by given per-layer summaries."""
+    from oracle.model import TemporalState, tria_layer_op, tria_temporal_token
+    L, B, T, H = r.shape
+    w = torch.full((9,), 1.0 / 9.0)
+    ts = TemporalState()
+    keys = []
+    for t in range(T):
+        pending = torch.zeros(B, dtype=torch.bool) if ts.pending is None else ts.pending
+        seed_valid = pending & (t != 0)
+        carry = None
+        for l in range(L):
+            sl = slice(t, t + 1)
+            carry, _ = tria_layer_op(l, l == L - 1, r[l, :, sl], i[l, :, sl], o[l, :, sl], carry,
+                                     ts.carry, seed_valid, w, alpha)
+        doc, fire = tria_temporal_token(carry[:, 0], ts, pending, t,
+                                        torch.zeros(B, dtype=torch.bool), T, window, beta)
+        if bool(fire.any()):
+            keys.append(doc)
+        ts = TemporalState(carry=doc, pending=fire)
+    return torch.stack(keys, dim=1)
+
+
+@pytest.mark.parametrize("L,T,W", [(4, 23, 5), (3, 20, 4), (1, 9, 2)])
+def test_tria_chunked_matches_token_by_token_step(L, T, W):
+    """The chunked forward and the decode step carry the same Tria state
+    (_forward_chunked vs step, loomformer.py:3788-3883 / :4012-4078): the
+    document keys at every fire agree (up to the eps of the extra N at a
+    restart)."""
+    g = _gen(51)
+    B, H = 2, 6
+    r, i, o = (torch.randn(L, B, T, H, generator=g) for _ in range(3))
+    keys, depth = ops.tria_chunked(r, i, o, 0.3, W, 0.1)
+    assert keys.shape == (B, -(-T // W) - 1, H, 3, 3) and depth.shape == (B, T, H, 3, 3)
+    want = _tria_by_token(r, i, o, 0.3, W, 0.1)
+    torch.testing.assert_close(keys, want, rtol=1e-5, atol=1e-5)
+
+
+def test_tria_chunked_rotation_products_at_alpha_zero():
+    """alpha = 0 makes every local operator the signed permutation R_axis
+    (axis l % 3), whose products are exact: the first key is the normalised
+    product D_{W-1} ... D_0 with D = R_{(L-1)%3} ... R_1 R_0 (layer 0 rightmost),
+    and PolARM leaves a scaled orthogonal matrix unchanged."""
+    Rz = torch.tensor([[0., -1, 0], [1, 0, 0], [0, 0, 1]])
+    Rx = torch.tensor([[1., 0, 0], [0, 0, -1], [0, 1, 0]])
+    Ry = torch.tensor([[0., 0, 1], [0, 1, 0], [-1, 0, 0]])
+    axes = [Rz, Rx, Ry]
+    L, B, T, H, W = 4, 1, 7, 3, 2
+    g = _gen(52)
+    r, i, o = (torch.randn(L, B, T, H, generator=g) for _ in range(3))
+    keys, _ = ops.tria_chunked(r, i, o, 0.0, W, 0.1)
+    assert keys.shape[1] == 3
+    D, D_rev = torch.eye(3), torch.eye(3)
+    for l in range(L):
+        D = axes[l % 3] @ D
+        D_rev = D_rev @ axes[l % 3]
+    P = torch.linalg.matrix_power(D, W)
+    # the layer order and the chunk chaining are visible in these products
+    assert not torch.allclose(P, torch.linalg.matrix_power(D_rev, W))
+    assert not torch.allclose(P @ P, torch.eye(3))
+    for c in range(3):
+        Pc = torch.linalg.matrix_power(P, c + 1)   # chunk c continues from key c-1
+        torch.testing.assert_close(keys[0, c], (Pc / Pc.square().mean().sqrt()).expand(H, 3, 3),
+                                   rtol=0, atol=1e-5)
+
+
+def test_tria_chunked_reset_cuts_history_and_fire():
+    """A document start inside a chunk makes its key independent of every
+    earlier token; a document start at a chunk's first token suppresses the
+    previous boundary's fire (hard_fire & ~next_is_reset, :3808-3810), so that
+    key is the uncorrected state, which PolARM maps to the fired key."""
+    g = _gen(53)
+    L, B, T, H, W = 3, 2, 16, 5, 4
+    r, i, o = (torch.randn(L, B, T, H, generator=g) for _ in range(3))
+    reset = torch.zeros(B, T, dtype=torch.bool)
+    reset[0, 9] = True                # inside chunk 2 of batch 0
+    keys, _ = ops.tria_chunked(r, i, o, 0.3, W, 0.1, reset)
+    r2 = r.clone()
+    r2[:, 0, :9] += 1.0               # tokens before the reset
+    keys2, _ = ops.tria_chunked(r2, i, o, 0.3, W, 0.1, reset)
+    torch.testing.assert_close(keys2[0, 2:], keys[0, 2:], rtol=0, atol=0)
+    assert not torch.allclose(keys2[0, 1], keys[0, 1])
+    reset_b = torch.zeros(B, T, dtype=torch.bool)
+    reset_b[1, 8] = True              # start of chunk 2 of batch 1
+    keys_b, _ = ops.tria_chunked(r, i, o, 0.3, W, 0.1, reset_b)
+    keys_n, _ = ops.tria_chunked(r, i, o, 0.3, W, 0.1)
+    torch.testing.assert_close(ops.polarm(keys_b[1, 1], 0.1), keys_n[1, 1], rtol=1e-6, atol=1e-6)
+    assert not torch.allclose(keys_b[1, 1], keys_n[1, 1], atol=1e-4)
