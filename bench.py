@@ -20,7 +20,9 @@ HBM-bound kernel): algorithmic bytes (R, beta in; I, O out = 8 B/elem in
 bf16) per launch over its mean launch time, against 8 TB/s.
 
 ``cpu_baseline`` is the CPU oracle (fp32 PyTorch restatement of the
-reference's unfused path) decoding on the host cores on a bounded sample.
+reference's unfused path) decoding on the host cores on a bounded sample;
+``cpu_micro`` times the same oracle on PX and DA at full size and on a slice
+of TR scaled to its full size.
 
 Prints ONE JSON line.  One GPU only: --gpus above 1 exits with a message.
 """
@@ -291,6 +293,74 @@ def cpu_baseline(args):
                        f"(untimed), {K} timed greedy steps (context {P}-{P + K}, vs 2048-2304 on GPU)")
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_wall(fn, reps: int = 3) -> float:
+    fn()                                                   # warm-up
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_micro():
+    """The microbenchmark configs on the host cores with the CPU oracle (the
+    reference's unfused fp32 path restated): PX and DA at full size, TR on a
+    slice of the streams (B=1, H=64 of 8 x 3072), scaled to the full size by the
+    stream count (the streams are independent).  1 warm-up, median of 3."""
+    import torch
+    from oracle import ops as ref  # the checker, timed as baseline
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    out = {"cores": cores, "cpu": _cpu_model(), "kind": "port"}
+    with torch.no_grad():
+        B, T, N, QH, HD, H = 8, 1024, 768, 8, 96, 3072
+        g = torch.Generator().manual_seed(1)
+        u = torch.randn(B, T, N, generator=g)
+        q, kc, c, d = (torch.randn(B, T, QH, HD, generator=g) for _ in range(4))
+        w_real = torch.randn(H, N, generator=g) / math.sqrt(N)
+        w_imag = torch.randn(H, N + 4 * HD, generator=g) / math.sqrt(N + 4 * HD)
+        w2 = torch.randn(N, H, generator=g) / math.sqrt(H)
+        trace_w = torch.rand(H, generator=g) - 0.5
+        zH = torch.zeros(H)
+
+        def px():
+            R = torch.nn.functional.linear(u, w_real)
+            beta = ref.beta_space_grouped(u, q, kc, c, d, w_imag, QH, HD)
+            act = ref.paraplex_pointwise(R, R, beta, zH, None, trace_w, None, 3.0)[0]
+            return torch.nn.functional.linear(act, w2)
+        out["px_ms"] = _median_wall(px) * 1e3
+        del u, q, kc, c, d
+        BT, S = 16384, 24
+        g = torch.Generator().manual_seed(3)
+        K = torch.randn(1, BT, S, QH, HD, generator=g).to(torch.bfloat16).float()
+        V = torch.randn(1, BT, S, QH, HD, generator=g).to(torch.bfloat16).float()
+        qd = torch.randn(QH, HD, generator=g) * 0.02
+        out["da_ms"] = _median_wall(lambda: ref.depth_attn_softmax(qd, K, V)) * 1e3
+        del K, V
+        L, Bs, Ts, Hs, W = 24, 1, 4096, 64, 64
+        g = torch.Generator().manual_seed(5)
+        r, i, o = (torch.randn(L, Bs, Ts, Hs, generator=g) for _ in range(3))
+        slice_s = _median_wall(lambda: ref.tria_chunked(r, i, o, 0.025, W, 0.1))
+        scale = (8 * 3072) / (Bs * Hs)
+        out["tr_ms"] = slice_s * 1e3 * scale
+        out["tr_sample"] = (f"chunked Tria path on B=1 x H=64 streams of T=4096, 24 layers, W=64 "
+                            f"({slice_s * 1e3:.0f} ms), scaled x{scale:.0f} to B=8 x H=3072")
+    return out
+
+
 # ----------------------------------------------------------------------------- main
 
 def main():
@@ -364,10 +434,15 @@ def main():
                     "traffic": traffic.get("paraplex_forward_kernel_px"),
                     "algorithmic_bytes": px["pointwise_bytes"]}
     cpu = None
+    cpu_mi = None
     if not args.no_cpu:
         log("CPU baseline (oracle on host cores)")
         cpu = cpu_baseline(args)
         log(f"CPU: {cpu['value']:.2f} tok/s on {cpu['cores']} cores")
+        if not args.no_micro:
+            log("CPU microbenchmarks (oracle on host cores)")
+            cpu_mi = cpu_micro()
+            log(f"CPU micro: {json.dumps(cpu_mi)}")
     line = {
         "metric": METRIC, "value": dec["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": dec["ms_per_step"],
@@ -376,7 +451,7 @@ def main():
         "config": {"workload": f"e2e greedy decode, nano_chk shape (seq_len 4096), batch {args.batch}, "
                                f"{args.prompt}-token prompt prefilled by step, {args.steps} timed greedy steps",
                    "batch": args.batch, "prompt": args.prompt, "decode_steps": args.steps},
-        "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels,
+        "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels, "cpu_micro": cpu_mi,
         "prefill_tokens_per_s": dec["prefill_tokens_per_s"],
     }
     print(json.dumps(line), flush=True)
