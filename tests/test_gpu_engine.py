@@ -98,3 +98,39 @@ def test_bf16_engine_tracks_fp32():
         rel.append(float((l16 - ref).norm() / ref.norm()))
     print("bf16 vs fp32 relative logit error: max %.4f mean %.4f" % (max(rel), sum(rel) / len(rel)))
     assert max(rel) < 0.08, max(rel)
+
+
+def test_aio_package_decodes_like_reference(tmp_path):
+    """A loom.aio v1 package (legacy split QKV / depth K-V keys, the <CARRY>
+    id taken from its tokenizer) decodes to the reference's own ids."""
+    from tokenizers import Tokenizer, models
+    from loom_amd.checkpoint import load_aio
+    z = np.load(os.path.join(GOLD, "tiny_decode.npz"))
+    state = {k[3:]: torch.from_numpy(z[k]) for k in z.files if k.startswith("w::")}
+    with open(os.path.join(GOLD, "configs.json")) as f:
+        raw = json.load(f)["tiny"]
+    legacy = dict(state)
+    N = state["emb.weight"].shape[1]
+    for l in range(raw["layers"]):
+        p = f"blocks.{l}.attn."
+        qkv = legacy.pop(p + "qkv_weight")
+        kv = (qkv.shape[0] - N) // 2
+        legacy[p + "q.weight"], legacy[p + "k.weight"], legacy[p + "v.weight"] = qkv.split([N, kv, kv], 0)
+    words = {f"w{i}": i for i in range(raw["vocab"])}
+    words["<CARRY>"] = 5
+    del words["w5"]
+    tok = Tokenizer(models.WordLevel(vocab=words, unk_token="w0"))
+    tok.add_special_tokens(["<CARRY>"])
+    pkg = {"format": "loom.aio", "version": 1, "manifest": {},
+           "checkpoint": {"model_kind": "loomformer", "ffn_type": "paraplex", "cfg": raw,
+                          "model": legacy},
+           "tokenizer_json": tok.to_str().encode("utf-8"), "chat_template_jinja": b"t"}
+    path = tmp_path / "tiny.aio"
+    torch.save(pkg, path)
+    loaded = load_aio(str(path))
+    assert loaded.carry_token_id == 5
+    prompt = torch.from_numpy(z["prompt_carry"])
+    eng = loaded.decoder(batch=prompt.shape[0], dtype=torch.float32)
+    ids, logits = eng.generate(prompt, 12, return_logits=True)
+    torch.testing.assert_close(logits.cpu(), torch.from_numpy(z["logits_carry"]), rtol=1e-3, atol=1e-4)
+    assert torch.equal(ids.cpu(), torch.from_numpy(z["greedy_carry"]))
