@@ -384,6 +384,24 @@ int loom_gqa_decode_step(int dtype, const void* qkv, void* k_cache, void* v_cach
                          const int64_t* pos_dev, int64_t QH, int64_t KVH, int64_t HD,
                          void* stream);
 
+/* loom_gqa_decode_step plus the decode step's DepthAttn read that follows it
+ * in Model.step (loomformer.py:3999, DepthAttn.forward :3404-3429, decode
+ * T = 1): depth_out [B,QH,HD] = softmax_s(depth_q . hist_k[b,s] / sqrt(HD))
+ * weighted hist_v rows, over S history slots at (hist_stride_bt,
+ * hist_stride_s) as in loom_depth_attn_forward.  The two reads are
+ * independent; the bf16 MFMA form computes the depth rows in extra blocks of
+ * the attention launch, other forms run loom_depth_attn_forward after it.
+ * No counterpart in the reference (one launch for two of its calls). */
+int loom_gqa_decode_step_depth(int dtype, const void* qkv, void* k_cache, void* v_cache,
+                               int64_t cache_stride_b, int64_t cache_stride_t,
+                               int64_t cache_stride_h, const float* cos_table,
+                               const float* sin_table, void* q_out, void* c_out, void* kctx_out,
+                               int64_t out_stride_b, float* workspace, int64_t workspace_bytes,
+                               int64_t B, int64_t len, const int64_t* pos_dev, int64_t QH,
+                               int64_t KVH, int64_t HD, const void* depth_q, const void* hist_k,
+                               const void* hist_v, int64_t hist_stride_bt, int64_t hist_stride_s,
+                               int64_t S, void* depth_out, void* stream);
+
 /* out = LayerNorm(a + b) (b may be NULL) over rows of N <= 2048, fp32 gamma and
  * beta, biased variance.  Replaces ln_attn/ln_ffn(skip + branch)
  * (loomformer.py:4000, :4045). */

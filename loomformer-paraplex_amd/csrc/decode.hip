@@ -5,6 +5,7 @@
 #include <type_traits>
 
 #include "loom_common.h"
+#include "depth_row.h"
 
 namespace loom {
 
@@ -90,6 +91,16 @@ struct GqaArgs {
     const int64_t* pos_dev;
     int QH, KVH;
     float qscale;
+    int nchunks;           // chunk blocks per (b, kv head) in the grid (records per row)
+    // optional depth read folded into the launch (bf16 MFMA form): grid slice
+    // x == nchunks computes DepthAttn rows (b, kvh*G .. kvh*G+G-1)
+    const T* dq;           // [QH, HD] learned queries of the depth slot, or null
+    const T* dk;
+    const T* dv;
+    int64_t dsbt, dss;     // history strides (b, slot)
+    T* dout;               // [B, QH, HD]
+    int dS;
+    float dscale;
 };
 
 // element d of head h of a qkv row, roped for position pos (x*cos + rot(x)*sin)
@@ -211,7 +222,7 @@ gqa_decode_kernel(GqaArgs<T> a) {
     __shared__ int s_last;
     const int chunk = blockIdx.x, kvh = blockIdx.y;
     const int64_t b = blockIdx.z;
-    const int nchunks = gridDim.x;
+    const int nchunks = a.nchunks;
     const int tid = threadIdx.x, j = tid % LPR, grp = tid / LPR;
     const int wave = tid >> 6, lane = tid & 63;
     const int64_t len = a.pos_dev != nullptr ? *a.pos_dev + 1 : a.len;
@@ -450,9 +461,17 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     __shared__ int s_last;
     const int chunk = blockIdx.x, kvh = blockIdx.y;
     const int64_t b = blockIdx.z;
-    const int nchunks = gridDim.x;
+    const int nchunks = a.nchunks;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 15, lq = lane >> 4;
+    if (chunk == nchunks) {
+        // the depth read of this step: rows (b, heads kvh*G ..), 16 lanes each
+        if (tid < 16 * G)
+            depth_row<bf16_t, HD / 16>(a.dq, a.dk, a.dv, a.dsbt, a.dss, a.dout, nullptr, nullptr,
+                                       (int)b * a.QH + kvh * G + (tid >> 4), tid & 15, a.dS, a.QH,
+                                       a.dscale);
+        return;
+    }
     const int64_t len = a.pos_dev != nullptr ? *a.pos_dev + 1 : a.len;
     const int64_t pos = len - 1;
     const int nact = (int)((len + kAttnChunk - 1) / kAttnChunk);
@@ -794,15 +813,42 @@ static int rope_dispatch(const void* qkv, void* q_out, void* kc, void* vc, const
     return launch_status("loom_rope_append");
 }
 
+// A DepthAttn read (loomformer.py:3404-3429) to run with the attention launch.
+struct DepthRead {
+    const void* q;         // [QH, HD]
+    const void* hk;
+    const void* hv;
+    int64_t sbt, ss, S;
+    void* out;             // [B, QH, HD]
+};
+
+template <typename T> constexpr int dtype_code();
+template <> constexpr int dtype_code<float>() { return LOOM_F32; }
+template <> constexpr int dtype_code<bf16_t>() { return LOOM_BF16; }
+template <> constexpr int dtype_code<f16_t>() { return LOOM_F16; }
+
 template <typename T>
 static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void* vc, int64_t sb,
                         int64_t stt, int64_t sh, const float* cosv, const float* sinv, void* q_out,
                         void* c_out, void* k_out,
                         int64_t out_sb, float* ws, int64_t B, int64_t len, const int64_t* pos_dev,
-                        int64_t QH, int64_t KVH, int64_t HD, hipStream_t st) {
+                        int64_t QH, int64_t KVH, int64_t HD, hipStream_t st,
+                        const DepthRead* depth = nullptr) {
     const int G = (int)(QH / KVH);
     const int nchunks = (int)ceil_div(len, kAttnChunk);
-    GqaArgs<T> a;
+    // the depth read rides in the attention grid when the rows can take the
+    // paired 4-byte loads of depth_row (else it is its own launch, after)
+    const bool fuse_depth =
+        depth != nullptr && depth->sbt % 2 == 0 && depth->ss % 2 == 0 &&
+        ((((uintptr_t)depth->q | (uintptr_t)depth->hk | (uintptr_t)depth->hv |
+           (uintptr_t)depth->out) % 8) == 0) && B * QH * 16 < ((int64_t)1 << 31);
+    auto depth_after = [&]() -> int {
+        if (depth == nullptr) return LOOM_OK;
+        return loom_depth_attn_forward(dtype_code<T>(), depth->q, depth->hk, depth->hv, depth->sbt,
+                                       depth->ss, depth->out, nullptr, nullptr, B, depth->S, QH,
+                                       HD, st);
+    };
+    GqaArgs<T> a{};
     a.q = (const T*)q;
     a.kc = (T*)kc;
     a.vc = (T*)vc;
@@ -822,16 +868,30 @@ static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void
     a.QH = (int)QH;
     a.KVH = (int)KVH;
     a.qscale = kLog2e / sqrtf((float)HD);   // scores in log2 units
+    a.nchunks = nchunks;
     dim3 grid(nchunks, (unsigned)KVH, (unsigned)B);
     if constexpr (std::is_same<T, bf16_t>::value) {
         // bf16: the MFMA form for head_dim 32/64/96/128 and groups 1/2/4/8
+        dim3 mgrid = grid;
+        if (fuse_depth) {
+            a.dq = (const T*)depth->q;
+            a.dk = (const T*)depth->hk;
+            a.dv = (const T*)depth->hv;
+            a.dsbt = depth->sbt;
+            a.dss = depth->ss;
+            a.dout = (T*)depth->out;
+            a.dS = (int)depth->S;
+            a.dscale = 1.0f / sqrtf((float)HD);
+            mgrid.x += 1;
+        }
 #define LOOM_GQA_MF(HDV, GG)                                                                      \
         if (HD == HDV && G == GG) {                                                              \
             if (from_qkv)                                                                         \
-                hipLaunchKernelGGL((gqa_mfma_kernel<HDV, GG, true>), grid, dim3(256), 0, st, a);  \
+                hipLaunchKernelGGL((gqa_mfma_kernel<HDV, GG, true>), mgrid, dim3(256), 0, st, a); \
             else                                                                                  \
-                hipLaunchKernelGGL((gqa_mfma_kernel<HDV, GG, false>), grid, dim3(256), 0, st, a); \
-            return launch_status(from_qkv ? "loom_gqa_decode_step" : "loom_gqa_decode_attention"); \
+                hipLaunchKernelGGL((gqa_mfma_kernel<HDV, GG, false>), mgrid, dim3(256), 0, st, a); \
+            const int rc = launch_status(from_qkv ? "loom_gqa_decode_step" : "loom_gqa_decode_attention"); \
+            return (rc != LOOM_OK || fuse_depth) ? rc : depth_after();                            \
         }
         LOOM_GQA_MF(96, 4) LOOM_GQA_MF(96, 1) LOOM_GQA_MF(96, 2) LOOM_GQA_MF(96, 8)
         LOOM_GQA_MF(64, 4) LOOM_GQA_MF(64, 1) LOOM_GQA_MF(64, 2) LOOM_GQA_MF(64, 8)
@@ -845,7 +905,8 @@ static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void
             hipLaunchKernelGGL((gqa_decode_kernel<T, E, GG, LPR, true>), grid, dim3(256), 0, st, a); \
         else                                                                                    \
             hipLaunchKernelGGL((gqa_decode_kernel<T, E, GG, LPR, false>), grid, dim3(256), 0, st, a); \
-        return launch_status(from_qkv ? "loom_gqa_decode_step" : "loom_gqa_decode_attention");  \
+        const int rc = launch_status(from_qkv ? "loom_gqa_decode_step" : "loom_gqa_decode_attention"); \
+        return rc != LOOM_OK ? rc : depth_after();                                              \
     }
     // head_dim 32/64/96/128 (16 lanes per row) and 8 (8 lanes), groups 1/2/4/8
     LOOM_GQA(6, 4, 16) LOOM_GQA(6, 1, 16) LOOM_GQA(6, 2, 16) LOOM_GQA(6, 8, 16)
@@ -991,6 +1052,38 @@ extern "C" int loom_gqa_decode_step(int dtype, const void* qkv, void* k_cache, v
                       cache_stride_t, cache_stride_h, cos_table, sin_table, q_out, c_out, kctx_out,
                       out_stride_b,
                       workspace, B, len, pos_dev, QH, KVH, HD, (hipStream_t)stream)
+}
+
+extern "C" int loom_gqa_decode_step_depth(int dtype, const void* qkv, void* k_cache, void* v_cache,
+                                          int64_t cache_stride_b, int64_t cache_stride_t,
+                                          int64_t cache_stride_h, const float* cos_table,
+                                          const float* sin_table, void* q_out, void* c_out,
+                                          void* kctx_out, int64_t out_stride_b, float* workspace,
+                                          int64_t workspace_bytes, int64_t B, int64_t len,
+                                          const int64_t* pos_dev, int64_t QH, int64_t KVH,
+                                          int64_t HD, const void* depth_q, const void* hist_k,
+                                          const void* hist_v, int64_t hist_stride_bt,
+                                          int64_t hist_stride_s, int64_t S, void* depth_out,
+                                          void* stream) {
+    clear_error();
+    LOOM_CHECK(qkv && k_cache && v_cache && cos_table && sin_table && c_out && kctx_out &&
+                   workspace && depth_q && hist_k && hist_v && depth_out,
+               "gqa_decode_step_depth: null argument");
+    LOOM_CHECK(HD % 2 == 0 && out_stride_b >= QH * HD,
+               "gqa_decode_step_depth: bad head_dim / out stride");
+    LOOM_CHECK(S >= 1 && hist_stride_s >= QH * HD && hist_stride_bt >= S * hist_stride_s,
+               "gqa_decode_step_depth: history strides (bt=%lld, s=%lld) overlap the [S,QH,HD] block",
+               (long long)hist_stride_bt, (long long)hist_stride_s);
+    const int rc = gqa_checks("gqa_decode_step_depth", k_cache, v_cache, cache_stride_b,
+                              cache_stride_t, cache_stride_h, workspace, workspace_bytes, B, len,
+                              QH, KVH, HD);
+    if (rc != LOOM_OK) return rc;
+    if (B == 0) return LOOM_OK;
+    const DepthRead dr{depth_q, hist_k, hist_v, hist_stride_bt, hist_stride_s, S, depth_out};
+    LOOM_DTYPE_SWITCH(dtype, gqa_dispatch, true, qkv, k_cache, v_cache, cache_stride_b,
+                      cache_stride_t, cache_stride_h, cos_table, sin_table, q_out, c_out, kctx_out,
+                      out_stride_b, workspace, B, len, pos_dev, QH, KVH, HD, (hipStream_t)stream,
+                      &dr)
 }
 
 // ---------------------------------------------------------------- step control

@@ -5,104 +5,26 @@
 // qh*HD + d, so a [B,T,S,QH,HD] stack and a strided decode view
 // hist[:, :, :S] of a [B,T,S_max,QH,HD] buffer are both read in place.
 //
-// Mapping: one (bt, qh) row per aligned group of 16 lanes; lane j owns the
-// EPL = HD/16 contiguous elements [j*EPL, (j+1)*EPL).  A wavefront therefore
-// covers 4 heads = 4*HD contiguous elements of one (bt, s) slice.  Scores for
-// 8 depth slots are formed before any value is read (8 independent K loads in
-// flight per lane), then folded into an fp32 online softmax.
+// Mapping: one (bt, qh) row per aligned group of 16 lanes (depth_row.h); a
+// wavefront therefore covers 4 heads = 4*HD contiguous elements of one (bt, s)
+// slice.
 #include <cmath>
 #include <type_traits>
 
 #include "loom_common.h"
+#include "depth_row.h"
 
 namespace loom {
-
-constexpr int kDepthChunk = 8;
 
 template <typename T, int EPL>
 __global__ void __launch_bounds__(256)
 depth_attn_kernel(const T* __restrict__ q, const T* __restrict__ hk, const T* __restrict__ hv,
                   int64_t sbt, int64_t ss, T* __restrict__ d_out, T* __restrict__ w_out,
                   float* __restrict__ lse_out, int rows, int S, int QH, float scale) {
-    constexpr int HD = EPL * 16;
-    constexpr int C = kDepthChunk;
-    const int j = threadIdx.x & 15;
     const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 4);
     if (row >= rows) return;  // all 16 lanes of a group leave together
-    const int qh = row % QH;
-    const int bt = row / QH;
-    const int d0 = j * EPL;
-
-    float qv[EPL];
-    RowIO<T, EPL>::load(q + qh * HD + d0, qv);
-#pragma unroll
-    for (int k = 0; k < EPL; ++k) qv[k] *= scale * kLog2e;   // scores in log2 units
-
-    const T* kp = hk + (int64_t)bt * sbt + qh * HD + d0;
-    const T* vp = hv + (int64_t)bt * sbt + qh * HD + d0;
-    float m = -INFINITY, l = 0.0f, acc[EPL];
-#pragma unroll
-    for (int k = 0; k < EPL; ++k) acc[k] = 0.0f;
-
-    // the K and V rows of C depth slots are requested together (2C loads in
-    // flight per lane), then scored and folded into the online softmax
-    for (int s0 = 0; s0 < S; s0 += C) {
-        RawRow<T, EPL> kr[C], vr[C];
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-            const int sc_ = s0 + c < S ? s0 + c : S - 1;   // in range; masked below
-            kr[c].load(kp + (int64_t)sc_ * ss);
-            vr[c].load(vp + (int64_t)sc_ * ss);
-        }
-        float sc[C];
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-            float kv[EPL];
-            kr[c].to_float(kv);
-            float dot = 0.0f;
-#pragma unroll
-            for (int k = 0; k < EPL; ++k) dot = fmaf(qv[k], kv[k], dot);
-            sc[c] = dot;
-        }
-        float cmax = -INFINITY;
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-            sc[c] = group_sum<16>(sc[c]);
-            if (s0 + c < S) cmax = fmaxf(cmax, sc[c]);
-        }
-        const float m_new = fmaxf(m, cmax);
-        const float corr = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first chunk
-        l *= corr;
-#pragma unroll
-        for (int k = 0; k < EPL; ++k) acc[k] *= corr;
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-            float vv[EPL];
-            vr[c].to_float(vv);
-            const float p = s0 + c < S ? __builtin_amdgcn_exp2f(sc[c] - m_new) : 0.0f;
-            l += p;
-#pragma unroll
-            for (int k = 0; k < EPL; ++k) acc[k] = fmaf(p, vv[k], acc[k]);
-        }
-        m = m_new;
-    }
-    const float inv_l = 1.0f / l;
-#pragma unroll
-    for (int k = 0; k < EPL; ++k) acc[k] *= inv_l;
-    RowIO<T, EPL>::store(d_out + (int64_t)row * HD + d0, acc);
-    if (lse_out != nullptr && j == 0) lse_out[row] = (m + flog2(l)) * kLn2;
-    if (w_out != nullptr) {
-        // weights: recompute each score (one more K read) and normalise
-        for (int s = 0; s < S; ++s) {
-            float kv[EPL];
-            RowIO<T, EPL>::load(kp + (int64_t)s * ss, kv);
-            float dot = 0.0f;
-#pragma unroll
-            for (int k = 0; k < EPL; ++k) dot = fmaf(qv[k], kv[k], dot);
-            dot = group_sum<16>(dot);
-            if (j == 0) st(w_out + (int64_t)row * S + s, __builtin_amdgcn_exp2f(dot - m) * inv_l);
-        }
-    }
+    depth_row<T, EPL>(q, hk, hv, sbt, ss, d_out, w_out, lse_out, row, threadIdx.x & 15, S, QH,
+                      scale);
 }
 
 // Any HD: one thread per (bt, qh) row, online softmax, scalar loads.

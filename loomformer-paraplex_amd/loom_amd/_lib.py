@@ -67,6 +67,10 @@ SIGNATURES = {
     "loom_gqa_decode_step": [c_int, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P,
                              c_int64, _P, c_int64, c_int64, c_int64, _P, c_int64, c_int64, c_int64,
                              _P],
+    "loom_gqa_decode_step_depth": [c_int, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P,
+                                   _P, c_int64, _P, c_int64, c_int64, c_int64, _P, c_int64,
+                                   c_int64, c_int64, _P, _P, _P, c_int64, c_int64, c_int64, _P,
+                                   _P],
     "loom_decode_prologue": [_P, _P, c_int64, c_int64, _P, c_int64, _P, _P, _P, _P, c_int64,
                              c_int64, c_int64, c_int64, _P],
     "loom_decode_epilogue": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64,

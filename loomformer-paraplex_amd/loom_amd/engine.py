@@ -230,14 +230,15 @@ class LoomDecoder:
             kc, vc = self.k_cache[bi], self.v_cache[bi]
             # ---- attention step (loomformer.py:3300-3332): RoPE + cache append +
             # attention + chunk merge, one launch
-            self._call("loom_gqa_decode_step", self.code, _P(self.qkv), _P(kc), _P(vc), cache_sb,
-                       cache_st, cache_sh, _P(self.cos), _P(self.sin), _P(self.q), _P(self.c),
-                       _P(self.kctx), N,
+            # with the depth read 2*bi of this token (loomformer.py:3999) in the same launch
+            self._call("loom_gqa_decode_step_depth", self.code, _P(self.qkv), _P(kc), _P(vc),
+                       cache_sb, cache_st, cache_sh, _P(self.cos), _P(self.sin), _P(self.q),
+                       _P(self.c), _P(self.kctx), N,
                        _P(self.ws), self.ws_bytes, B, self.max_len, _P(self.pos_dev), c.QH, c.KVH,
-                       c.HD, st)
-            # ---- depth read 2*bi, then LN(o(c) + w_o(d)) (loomformer.py:3999-4000):
-            # both products accumulate in one launch
-            self._depth(sub, self.d)
+                       c.HD, _P(self.qp[sub]), _P(self.hist), _P(self.hist[:, :, N:]),
+                       2 * L * 2 * N, 2 * N, sub + 1, _P(self.d), st)
+            # ---- LN(o(c) + w_o(d)) (loomformer.py:3999-4000): both products
+            # accumulate in one launch
             self._linear_ln(("attn", bi), self.c.view(B, N),
                             dict(w=blk["o"], w2=self.wo, out=self.y), self.d.view(B, N),
                             blk["ln1_w"], blk["ln1_b"])

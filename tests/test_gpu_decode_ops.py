@@ -129,6 +129,57 @@ def _rope_tables(HD, n):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,QH,KVH,HD,length,S_,L2", [
+    (32, 8, 2, 96, 700, 3, 20), (2, 8, 2, 96, 1, 1, 20), (3, 4, 2, 64, 300, 7, 8),
+    (2, 8, 1, 128, 260, 12, 12), (2, 4, 2, 8, 40, 2, 4)])
+def test_gqa_decode_step_depth(dtype, B, QH, KVH, HD, length, S_, L2):
+    """The attention step with the depth read in the same launch gives exactly
+    what the two separate entry points give (bf16 with head_dim 32-128 takes the
+    fused grid, the rest runs the depth kernel after), and the depth rows match
+    the oracle's softmax over the history slots."""
+    from loom_amd import _lib
+    max_len = length + 5
+    pos = length - 1
+    g = torch.Generator().manual_seed(length + 31 * S_ + HD)
+    qkv = torch.randn(B, (QH + 2 * KVH) * HD, generator=g).to(DEV, dtype)
+    kc0 = torch.randn(B, KVH, max_len, HD, generator=g).to(DEV, dtype)
+    vc0 = torch.randn(B, KVH, max_len, HD, generator=g).to(DEV, dtype)
+    hist = torch.randn(B, L2, 2 * QH * HD, generator=g).to(DEV, dtype)   # slot s = [k | v]
+    dq = (torch.randn(QH, HD, generator=g) * 0.3).to(DEV, dtype)
+    cos, sin = _rope_tables(HD, max_len)
+    cos_d, sin_d = cos.to(DEV), sin.to(DEV)
+    strides = (KVH * max_len * HD, HD, max_len * HD)
+    nb = _lib.load().loom_gqa_workspace_bytes(B, max_len, QH, KVH, HD)
+    pos_d = torch.tensor([pos], dtype=torch.int64, device=DEV)
+    N = QH * HD
+    outs = []
+    for fused in (False, True):
+        kc, vc = kc0.clone(), vc0.clone()
+        ws = torch.zeros(nb // 4 + 1, device=DEV)
+        c = torch.zeros(B, N, device=DEV, dtype=dtype)
+        kx = torch.zeros_like(c)
+        qo = torch.zeros_like(c)
+        d = torch.zeros_like(c)
+        args = (P(qkv), P(kc), P(vc), *strides, P(cos_d), P(sin_d), P(qo), P(c), P(kx), N, P(ws),
+                nb, B, max_len, P(pos_d), QH, KVH, HD)
+        if fused:
+            _lib.call("loom_gqa_decode_step_depth", code(qkv), *args, P(dq), P(hist),
+                      P(hist[:, :, N:]), L2 * 2 * N, 2 * N, S_, P(d), S(qkv))
+        else:
+            _lib.call("loom_gqa_decode_step", code(qkv), *args, S(qkv))
+            _lib.call("loom_depth_attn_forward", code(qkv), P(dq), P(hist), P(hist[:, :, N:]),
+                      L2 * 2 * N, 2 * N, P(d), None, None, B, S_, QH, HD, S(qkv))
+        outs.append([host(t) for t in (c, kx, qo, d, kc, vc)])
+        assert int(ws[:B * KVH].view(torch.int32).abs().sum().item()) == 0
+    for x, y in zip(*outs):
+        assert torch.equal(x, y)
+    hk = host(hist)[:, :S_, :N].view(B, S_, QH, HD)
+    hv = host(hist)[:, :S_, N:].view(B, S_, QH, HD)
+    w = torch.softmax((hk * host(dq)).sum(-1) / math.sqrt(HD), dim=1)      # [B, S, QH]
+    check(outs[1][3].view(B, QH, HD), (w.unsqueeze(-1) * hv).sum(1), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("head_major", [False, True])
 @pytest.mark.parametrize("B,QH,KVH,HD,length", [
     (2, 8, 2, 96, 1), (3, 8, 2, 96, 255), (2, 8, 2, 96, 257), (32, 8, 2, 96, 700),
