@@ -39,6 +39,10 @@ _P = _lib.ptr
 
 
 class LoomDecoder:
+    """Model.step / infer for a batch of sequences on the gfx950 kernels."""
+
+    STEPS_PER_GRAPH = 8      # decode steps chained in one replayed graph
+
     def __init__(self, cfg: ModelConfig, state: Dict[str, torch.Tensor], batch: int,
                  dtype: torch.dtype = torch.bfloat16, device="cuda", max_len: Optional[int] = None,
                  carry_token_id: Optional[int] = None):
@@ -345,17 +349,21 @@ class LoomDecoder:
 
     # ------------------------------------------------------------------ generation
 
-    def _graph_for(self, prompt_len: int) -> torch.cuda.CUDAGraph:
-        """Capture argmax -> ids, then one step for a position >= 1, reading the
-        prompt while pos < prompt_len."""
-        g = self._graphs.get(prompt_len)
+    def _graph_for(self, prompt_len: int, steps: int = 1) -> torch.cuda.CUDAGraph:
+        """Capture `steps` x (argmax -> ids, then one step for a position >= 1,
+        reading the prompt while pos < prompt_len).  The position advances on the
+        device, so several steps chain inside one graph and the gap between
+        graph launches is paid once per `steps` tokens."""
+        key = (prompt_len, steps)
+        g = self._graphs.get(key)
         if g is None:
             torch.cuda.synchronize(self.dev)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                self._argmax()
-                self._launch_step(first=False, prompt_len=prompt_len)
-            self._graphs[prompt_len] = g
+                for _ in range(steps):
+                    self._argmax()
+                    self._launch_step(first=False, prompt_len=prompt_len)
+            self._graphs[key] = g
         return g
 
     @torch.no_grad()
@@ -409,8 +417,12 @@ class LoomDecoder:
         """Advance ``n`` positions with the captured step (prompt tokens while
         pos < P, greedy argmax after)."""
         self._check_capacity(self.pos + n - 1)
+        if n >= self.STEPS_PER_GRAPH:
+            g = self._graph_for(self._prompt_len, self.STEPS_PER_GRAPH)
+            for _ in range(n // self.STEPS_PER_GRAPH):
+                g.replay()
         g = self._graph_for(self._prompt_len)
-        for _ in range(n):
+        for _ in range(n % self.STEPS_PER_GRAPH):
             g.replay()
         self.pos += n
 

@@ -134,3 +134,19 @@ def test_aio_package_decodes_like_reference(tmp_path):
     ids, logits = eng.generate(prompt, 12, return_logits=True)
     torch.testing.assert_close(logits.cpu(), torch.from_numpy(z["logits_carry"]), rtol=1e-3, atol=1e-4)
     assert torch.equal(ids.cpu(), torch.from_numpy(z["greedy_carry"]))
+
+
+def test_chained_step_graphs_equal_single_steps():
+    """replay_steps chains STEPS_PER_GRAPH steps per graph (plus single-step
+    replays for the rest): the tokens equal generate()'s one-step replays."""
+    from loom_amd.engine import LoomDecoder
+    z = np.load(os.path.join(GOLD, "tiny_decode.npz"))
+    state = {k[3:]: torch.from_numpy(z[k]) for k in z.files if k.startswith("w::")}
+    prompt = torch.from_numpy(z["prompt_carry"])
+    P, n = prompt.shape[1], 21
+    eng = LoomDecoder(_cfg("tiny"), state, batch=3, dtype=torch.bfloat16, carry_token_id=5)
+    want = eng.generate(prompt, n)
+    eng2 = LoomDecoder(_cfg("tiny"), state, batch=3, dtype=torch.bfloat16, carry_token_id=5)
+    eng2.start(prompt)
+    eng2.replay_steps(P - 1 + n)
+    assert torch.equal(eng2.generated().cpu(), want.cpu())
