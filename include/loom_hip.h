@@ -302,6 +302,24 @@ int loom_tria_chunked_forward(int dtype, const void* r, const void* i, const voi
                               int64_t B, int64_t T, int64_t H, int64_t W, float alpha,
                               float polarm_beta, float eps, void* stream);
 
+/* Causal GQA attention of a chunk of T prompt tokens at positions
+ * start .. start+T-1, for prefilling the decode state chunk by chunk (the
+ * reference runs its stack chunk by chunk in Model._forward_chunked,
+ * loomformer.py:3788-3883, with GroupedQueryCausalSelfAttention's readouts
+ * C = A.V and Kctx = A.K_roped, :3215-3332).  Ropes q and k of every token
+ * (tables as in loom_rope_append), writes the roped q to q_out [B,T,QH,HD],
+ * appends (k_roped, v) at rows start.. of the caches (strides as in
+ * loom_gqa_decode_step; cache_len = their capacity in positions), then
+ * attends token t to cache rows 0..start+t.
+ *   qkv: rows (b,t) of [q | k | v] ((QH + 2 KVH) HD) at qkv_ld elements apart;
+ *   c_out, kctx_out: rows (b,t) of QH*HD at out_ld elements apart.
+ * No counterpart in the reference (its chunked forward uses SDPA per chunk). */
+int loom_gqa_prefill(int dtype, const void* qkv, int64_t qkv_ld, void* k_cache, void* v_cache,
+                     int64_t cache_stride_b, int64_t cache_stride_t, int64_t cache_stride_h,
+                     const float* cos_table, const float* sin_table, void* q_out, void* c_out,
+                     void* kctx_out, int64_t out_ld, int64_t B, int64_t T, int64_t start,
+                     int64_t cache_len, int64_t QH, int64_t KVH, int64_t HD, void* stream);
+
 /* Sparse final cross-attention: per row (b,t) a masked softmax over K keys
  * (scale * q.k), out = sum_j w_j v_j, an all-masked row gives exact zeros and
  * lse = -inf.  Replaces final_ca_sparse_forward (bindings.cpp:107).

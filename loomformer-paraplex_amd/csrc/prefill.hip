@@ -1,0 +1,535 @@
+// Causal GQA attention over a chunk of prompt tokens, for prefilling the
+// decode state in chunks (Model._forward_chunked, loomformer.py:3788-3883,
+// runs the stack chunk by chunk; GroupedQueryCausalSelfAttention attends each
+// chunk's queries to the cached keys of earlier chunks plus the chunk's own,
+// :3215-3332).
+//
+// Token t of the chunk sits at position start + t.  One call:
+//   1. ropes q and k of every token (YaRN tables as in the decode step),
+//      writes the roped q [B, T, QH, HD] and appends (k_roped, v) at rows
+//      start .. start+T-1 of the caches;
+//   2. attends every (token, q head) to cache rows 0 .. start + t with an fp32
+//      softmax and writes both readouts, C = A.V and Kctx = A.K_roped.
+// The caches take the decode engine's strides (batch, position, kv head).
+//
+// bf16 with head_dim 32/64/96/128 runs on MFMA: a block holds 4 (query tile
+// of 16 positions, head) pairs of one kv head, streams 32 cached rows per step
+// through LDS once for all four (K as stored for the scores, K and V
+// transposed for the two readouts), and keeps one online softmax per query
+// column.  Other dtypes / head sizes take a 16-lanes-per-row VALU kernel, one
+// block per (token, kv head).
+#include <cmath>
+
+#include "loom_common.h"
+
+namespace loom {
+
+template <typename T>
+struct PrefillArgs {
+    const T* q;            // roped q [B, T, QH, HD]
+    const T* kc;
+    const T* vc;
+    int64_t csb, cst, csh;
+    T* c_out;              // [B, T, QH*HD] rows at out_ld
+    T* k_out;
+    int64_t out_ld;
+    int64_t start;         // position of token 0 of the chunk
+    int Tc, QH, KVH;
+    float qscale;          // log2(e) / sqrt(HD): scores in log2 units
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+prefill_rope_append_kernel(const T* __restrict__ qkv, int64_t qkv_ld, T* __restrict__ q_out,
+                           T* __restrict__ kc, T* __restrict__ vc, const float* __restrict__ cosv,
+                           const float* __restrict__ sinv, int64_t B, int64_t Tc, int64_t start,
+                           int QH, int KVH, int HD, int64_t csb, int64_t cst, int64_t csh) {
+    const int heads = QH + 2 * KVH;
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= B * Tc * heads * HD) return;
+    const int d = (int)(id % HD);
+    const int hs = (int)((id / HD) % heads);
+    const int64_t bt = id / ((int64_t)HD * heads);
+    const int64_t b = bt / Tc, t = bt - b * Tc;
+    const int64_t pos = start + t;
+    const T* row = qkv + bt * qkv_ld;
+    const int half = HD / 2;
+    if (hs < QH + KVH) {
+        const T* x = row + hs * HD;
+        const float rot = d < half ? -ld(x + d + half) : ld(x + d - half);
+        const float v = ld(x + d) * cosv[pos * HD + d] + rot * sinv[pos * HD + d];
+        if (hs < QH)
+            st(q_out + (bt * QH + hs) * HD + d, v);
+        else
+            st(kc + b * csb + pos * cst + (hs - QH) * csh + d, v);
+    } else {
+        const int kvh = hs - QH - KVH;
+        st(vc + b * csb + pos * cst + kvh * csh + d, ld(row + hs * HD + d));
+    }
+}
+
+// ------------------------------------------------------------------ VALU form
+// Block (t, kvh, b): 256 / LPR row groups of LPR lanes (HD = EPL * LPR); group
+// r takes cache rows r, r + NG, ... up to the token's position, in batches of
+// 4 rows per load round, and keeps an online softmax per head of the group;
+// the groups are merged through shuffles and LDS.
+template <typename T, int EPL, int G, int LPR>
+__global__ void __launch_bounds__(256)
+gqa_prefill_kernel(PrefillArgs<T> a) {
+    constexpr int HD = EPL * LPR;
+    constexpr int NG = 256 / LPR;
+    constexpr int NB = 4;
+    constexpr int REC = 2 * G + 2 * G * HD;
+    __shared__ float wred[4][REC];
+    const int t = blockIdx.x, kvh = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    const int tid = threadIdx.x, j = tid % LPR, grp = tid / LPR;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int64_t pos = a.start + t;
+    const int d0 = j * EPL;
+    const int64_t bt = b * a.Tc + t;
+
+    float qv[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        RowIO<T, EPL>::load(a.q + (bt * a.QH + kvh * G + g) * HD + d0, qv[g]);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) qv[g][e] *= a.qscale;
+    }
+    const T* kbase = a.kc + b * a.csb + kvh * a.csh + d0;
+    const T* vbase = a.vc + b * a.csb + kvh * a.csh + d0;
+    float m[G], l[G], ac[G][EPL], ak[G][EPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) ac[g][e] = ak[g][e] = 0.0f;
+    }
+    for (int64_t base = grp; base <= pos; base += (int64_t)NG * NB) {
+        float kv[NB][EPL], vv[NB][EPL];
+        bool ok[NB];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int64_t r = base + (int64_t)NG * u;
+            ok[u] = r <= pos;
+            const int64_t rr = ok[u] ? r : pos;      // in range; masked below
+            RowIO<T, EPL>::load(kbase + rr * a.cst, kv[u]);
+            RowIO<T, EPL>::load(vbase + rr * a.cst, vv[u]);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float s[NB];
+            float mx = m[g];
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                float dot = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) dot = fmaf(qv[g][e], kv[u][e], dot);
+                s[u] = group_sum<LPR>(dot);
+                if (ok[u]) mx = fmaxf(mx, s[u]);
+            }
+            const float corr = __builtin_amdgcn_exp2f(m[g] - mx);   // 0 when m was -inf
+            float ls = l[g] * corr;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                ac[g][e] *= corr;
+                ak[g][e] *= corr;
+            }
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                const float p = ok[u] ? __builtin_amdgcn_exp2f(s[u] - mx) : 0.0f;
+                ls += p;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    ac[g][e] = fmaf(p, vv[u][e], ac[g][e]);
+                    ak[g][e] = fmaf(p, kv[u][e], ak[g][e]);
+                }
+            }
+            l[g] = ls;
+            m[g] = mx;
+        }
+    }
+    // groups of one wave (lanes j, j+LPR, ...), head by head; a group that saw
+    // no row keeps m = -inf and contributes nothing
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float M = m[g];
+#pragma unroll
+        for (int off = LPR; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        const float f = m[g] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[g] - M);
+        float L = l[g] * f;
+#pragma unroll
+        for (int off = LPR; off < 64; off <<= 1) L += __shfl_xor(L, off, 64);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            float c = ac[g][e] * f, k = ak[g][e] * f;
+#pragma unroll
+            for (int off = LPR; off < 64; off <<= 1) {
+                c += __shfl_xor(c, off, 64);
+                k += __shfl_xor(k, off, 64);
+            }
+            ac[g][e] = c;
+            ak[g][e] = k;
+        }
+        m[g] = M;
+        l[g] = L;
+    }
+    if (lane < LPR) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            if (lane == 0) {
+                wred[wave][g] = m[g];
+                wred[wave][G + g] = l[g];
+            }
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                wred[wave][2 * G + g * HD + d0 + e] = ac[g][e];
+                wred[wave][2 * G + G * HD + g * HD + d0 + e] = ak[g][e];
+            }
+        }
+    }
+    __syncthreads();
+    // merge the 4 waves: thread i -> (head, dim) pairs
+    for (int i = tid; i < G * HD; i += 256) {
+        const int g = i / HD, d = i - g * HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, wred[w][g]);
+        float L = 0.0f, c = 0.0f, k = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float mw = wred[w][g];
+            const float f = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            L = fmaf(wred[w][G + g], f, L);
+            c = fmaf(wred[w][2 * G + g * HD + d], f, c);
+            k = fmaf(wred[w][2 * G + G * HD + g * HD + d], f, k);
+        }
+        const float inv = 1.0f / L;
+        const int64_t o = bt * a.out_ld + (int64_t)(kvh * G + g) * HD + d;
+        st(a.c_out + o, c * inv);
+        st(a.k_out + o, k * inv);
+    }
+}
+
+// ------------------------------------------------------------------ MFMA form (bf16)
+// v_mfma_f32_16x16x32_bf16 (A: 16 rows x 32 k, B: 32 k x 16 columns; lane l
+// holds row/column l%16, k = 8*(l/16)..+7; result [4*(l/16)+r][l%16] in r):
+//   S^T = K Q^T   A = 16 cached rows as stored, B = 16 query positions of one head
+//   C   = P V     A = P (rows = query positions, k = 32 cached rows, bf16),
+//   Kctx= P K     B = V / K transposed through LDS.
+// Block (x, y, b): y = kvh * HSPLIT + part; wave w takes head
+// kvh*G + part*GP + w%GP and query tile x*QTB + w/GP (16 positions each).
+typedef __bf16 bf16x8_p __attribute__((ext_vector_type(8)));
+typedef float f32x4_p __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_p mfma16p(uint4 x, uint4 y, f32x4_p c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_p, x),
+                                                   __builtin_bit_cast(bf16x8_p, y), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+constexpr int kPfRows = 32;   // cached rows per step
+
+template <int HD, int GP, int HSPLIT>
+__global__ void __launch_bounds__(256)
+gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
+    constexpr int KK = HD / 32;
+    constexpr int DT = HD / 16;
+    constexpr int QTB = 4 / GP;                 // query tiles per block
+    constexpr int G = GP * HSPLIT;
+    constexpr int PIECES = kPfRows * HD / 8;    // 16-byte pieces of one 32-row tile
+    constexpr int PPT = (2 * PIECES + 255) / 256;
+    __shared__ __align__(16) uint16_t kn[kPfRows][HD];   // K rows as stored
+    __shared__ __align__(16) uint16_t kt[HD][kPfRows];   // K transposed
+    __shared__ __align__(16) uint16_t vt[HD][kPfRows];   // V transposed
+    __shared__ __align__(16) uint16_t pt[4][16][kPfRows];
+    __shared__ float cr[4][16];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 15, lq = lane >> 4;
+    const int kvh = blockIdx.y / HSPLIT, part = blockIdx.y % HSPLIT;
+    const int64_t b = blockIdx.z;
+    const int head = kvh * G + part * GP + wave % GP;
+    const int q0 = (blockIdx.x * QTB + wave / GP) * 16;          // first query of the wave's tile
+    const int qlast_blk = min((int)(blockIdx.x + 1) * QTB * 16, a.Tc) - 1;
+    const int64_t kmax = a.start + qlast_blk;                    // last cached row the block reads
+    const int nsteps = (int)((kmax + kPfRows) / kPfRows);
+    // this lane's query column (lr): its position; a column past the chunk
+    // attends to row 0 only (finite, never stored)
+    const int qcol = q0 + lr;
+    const int64_t qpos = qcol < a.Tc ? a.start + qcol : 0;
+    const int wave_qlast = min(q0 + 15, a.Tc - 1);
+    const int64_t wave_kmax = q0 < a.Tc ? a.start + wave_qlast : -1;
+
+    const bf16_t* kb = a.kc + b * a.csb + kvh * a.csh;
+    const bf16_t* vb = a.vc + b * a.csb + kvh * a.csh;
+    // one 32-row tile: piece p -> (tensor, row, 8-dim chunk), rows clamped to kmax
+    uint4 reg[PPT];
+    auto load_tile = [&](int64_t r0) {
+#pragma unroll
+        for (int u = 0; u < PPT; ++u) {
+            const int p = tid + 256 * u;
+            if (p < 2 * PIECES) {
+                const int tensor = p / PIECES, q = p % PIECES;
+                const int row = q / (HD / 8), ch = q % (HD / 8);
+                int64_t r = r0 + row;
+                r = r <= kmax ? r : kmax;
+                const bf16_t* src = (tensor == 0 ? kb : vb) + r * a.cst + 8 * ch;
+                reg[u] = *reinterpret_cast<const uint4*>(src);
+            }
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int u = 0; u < PPT; ++u) {
+            const int p = tid + 256 * u;
+            if (p < 2 * PIECES) {
+                const int tensor = p / PIECES, q = p % PIECES;
+                const int row = q / (HD / 8), ch = q % (HD / 8);
+                const uint32_t w[4] = {reg[u].x, reg[u].y, reg[u].z, reg[u].w};
+                if (tensor == 0) {
+                    *reinterpret_cast<uint4*>(&kn[row][8 * ch]) = reg[u];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        kt[8 * ch + e][row] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        vt[8 * ch + e][row] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+                }
+            }
+        }
+    };
+    load_tile(0);
+    // B operand of S^T: q of query column lr, dims 32*kk + 8*lq .. +7
+    uint4 qf[KK];
+    {
+        const int qrow = qcol < a.Tc ? qcol : a.Tc - 1;
+        const bf16_t* qp = a.q + ((b * a.Tc + qrow) * a.QH + head) * HD;
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+            qf[kk] = *reinterpret_cast<const uint4*>(qp + 32 * kk + 8 * lq);
+    }
+    store_tile();
+    lds_sync();
+
+    float mh = -INFINITY, lh = 0.0f;      // running max / sum of query column lr
+    f32x4_p accC[DT], accK[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) accC[dt] = accK[dt] = f32x4_p{0.f, 0.f, 0.f, 0.f};
+
+    for (int it = 0; it < nsteps; ++it) {
+        const int64_t r0 = (int64_t)it * kPfRows;
+        if (it + 1 < nsteps) load_tile(r0 + kPfRows);
+        const bool active = r0 <= wave_kmax;                 // wave-uniform
+        if (active) {
+            f32x4_p sc[2];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                sc[hf] = f32x4_p{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk) {
+                    const uint4 ka = *reinterpret_cast<const uint4*>(&kn[16 * hf + lr][32 * kk + 8 * lq]);
+                    sc[hf] = mfma16p(ka, qf[kk], sc[hf]);
+                }
+            }
+            // S^T[row 16*hf + 4*lq + r][query column lr]
+            float sv[2][4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = r0 + 16 * hf + 4 * lq + r;
+                    sv[hf][r] = row <= qpos ? sc[hf][r] * a.qscale : -INFINITY;
+                    mx = fmaxf(mx, sv[hf][r]);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mnew = fmaxf(mh, mx);               // finite: row 0 is seen at step 0
+            const float corr = __builtin_amdgcn_exp2f(mh - mnew);
+            float ls = 0.0f;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float p = sv[hf][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[hf][r] - mnew);
+                    ls += p;
+                    pt[wave][lr][16 * hf + 4 * lq + r] = f32_to_bf16(p);
+                }
+            ls += __shfl_xor(ls, 16, 64);
+            ls += __shfl_xor(ls, 32, 64);
+            lh = fmaf(lh, corr, ls);
+            mh = mnew;
+            if (lq == 0) cr[wave][lr] = corr;
+        }
+        lds_sync();
+        if (active) {
+            float cf[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cf[r] = cr[wave][4 * lq + r];
+            const uint4 pa = *reinterpret_cast<const uint4*>(&pt[wave][lr][8 * lq]);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    accC[dt][r] *= cf[r];
+                    accK[dt][r] *= cf[r];
+                }
+                const uint4 vbf = *reinterpret_cast<const uint4*>(&vt[16 * dt + lr][8 * lq]);
+                const uint4 kbf = *reinterpret_cast<const uint4*>(&kt[16 * dt + lr][8 * lq]);
+                accC[dt] = mfma16p(pa, vbf, accC[dt]);
+                accK[dt] = mfma16p(pa, kbf, accK[dt]);
+            }
+        }
+        lds_sync();                            // every wave is done with this tile
+        if (it + 1 < nsteps) {
+            store_tile();
+            lds_sync();
+        }
+    }
+    // normalise: the sum of query column c lives in lanes with lr == c
+    if (lq == 0) cr[wave][lr] = lh;
+    lds_sync();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int col = 4 * lq + r;
+        const int qi = q0 + col;
+        if (qi >= a.Tc) continue;
+        const float inv = 1.0f / cr[wave][col];
+        const int64_t o = (b * a.Tc + qi) * a.out_ld + (int64_t)head * HD;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            a.c_out[o + 16 * dt + lr].x = f32_to_bf16(accC[dt][r] * inv);
+            a.k_out[o + 16 * dt + lr].x = f32_to_bf16(accK[dt][r] * inv);
+        }
+    }
+}
+
+template <typename T>
+static int prefill_dispatch(const void* qkv, int64_t qkv_ld, void* kc, void* vc, int64_t csb,
+                            int64_t cst, int64_t csh, const float* cosv, const float* sinv,
+                            void* q_out, void* c_out, void* k_out, int64_t out_ld, int64_t B,
+                            int64_t Tc, int64_t start, int64_t QH, int64_t KVH, int64_t HD,
+                            hipStream_t st) {
+    const int64_t total = B * Tc * (QH + 2 * KVH) * HD;
+    hipLaunchKernelGGL((prefill_rope_append_kernel<T>), dim3((unsigned)ceil_div(total, 256)),
+                       dim3(256), 0, st, (const T*)qkv, qkv_ld, (T*)q_out, (T*)kc, (T*)vc, cosv,
+                       sinv, B, Tc, start, (int)QH, (int)KVH, (int)HD, csb, cst, csh);
+    int rc = launch_status("loom_gqa_prefill (rope/append)");
+    if (rc != LOOM_OK) return rc;
+    PrefillArgs<T> a{};
+    a.q = (const T*)q_out;
+    a.kc = (const T*)kc;
+    a.vc = (const T*)vc;
+    a.csb = csb;
+    a.cst = cst;
+    a.csh = csh;
+    a.c_out = (T*)c_out;
+    a.k_out = (T*)k_out;
+    a.out_ld = out_ld;
+    a.start = start;
+    a.Tc = (int)Tc;
+    a.QH = (int)QH;
+    a.KVH = (int)KVH;
+    a.qscale = kLog2e / sqrtf((float)HD);
+    const int G = (int)(QH / KVH);
+    if constexpr (std::is_same<T, bf16_t>::value) {
+        const bool mf_ok = (HD == 32 || HD == 64 || HD == 96 || HD == 128) &&
+                           (G == 1 || G == 2 || G == 4 || G == 8);
+        if (mf_ok) {
+#define LOOM_PF_MF(HDV)                                                                          \
+            if (HD == HDV) {                                                                     \
+                if (G == 4) {                                                                    \
+                    dim3 g((unsigned)ceil_div(Tc, 16), (unsigned)KVH, (unsigned)B);             \
+                    hipLaunchKernelGGL((gqa_prefill_mfma_kernel<HDV, 4, 1>), g, dim3(256), 0, st, a); \
+                } else if (G == 8) {                                                             \
+                    dim3 g((unsigned)ceil_div(Tc, 16), (unsigned)(KVH * 2), (unsigned)B);       \
+                    hipLaunchKernelGGL((gqa_prefill_mfma_kernel<HDV, 4, 2>), g, dim3(256), 0, st, a); \
+                } else if (G == 2) {                                                             \
+                    dim3 g((unsigned)ceil_div(Tc, 32), (unsigned)KVH, (unsigned)B);             \
+                    hipLaunchKernelGGL((gqa_prefill_mfma_kernel<HDV, 2, 1>), g, dim3(256), 0, st, a); \
+                } else {                                                                         \
+                    dim3 g((unsigned)ceil_div(Tc, 64), (unsigned)KVH, (unsigned)B);             \
+                    hipLaunchKernelGGL((gqa_prefill_mfma_kernel<HDV, 1, 1>), g, dim3(256), 0, st, a); \
+                }                                                                                \
+                return launch_status("loom_gqa_prefill");                                       \
+            }
+            LOOM_PF_MF(96) LOOM_PF_MF(64) LOOM_PF_MF(128) LOOM_PF_MF(32)
+#undef LOOM_PF_MF
+        }
+    }
+    dim3 grid((unsigned)Tc, (unsigned)KVH, (unsigned)B);
+#define LOOM_PF(E, GG, LPR)                                                                     \
+    if (HD == E * LPR && G == GG) {                                                             \
+        hipLaunchKernelGGL((gqa_prefill_kernel<T, E, GG, LPR>), grid, dim3(256), 0, st, a);     \
+        return launch_status("loom_gqa_prefill");                                               \
+    }
+    LOOM_PF(6, 4, 16) LOOM_PF(6, 1, 16) LOOM_PF(6, 2, 16) LOOM_PF(6, 8, 16)
+    LOOM_PF(4, 4, 16) LOOM_PF(4, 1, 16) LOOM_PF(4, 2, 16) LOOM_PF(4, 8, 16)
+    LOOM_PF(8, 4, 16) LOOM_PF(8, 1, 16) LOOM_PF(8, 2, 16) LOOM_PF(8, 8, 16)
+    LOOM_PF(2, 4, 16) LOOM_PF(2, 1, 16) LOOM_PF(2, 2, 16) LOOM_PF(2, 8, 16)
+    LOOM_PF(1, 1, 8) LOOM_PF(1, 2, 8) LOOM_PF(1, 4, 8) LOOM_PF(1, 8, 8)
+#undef LOOM_PF
+    set_error("gqa_prefill: unsupported head_dim %lld / group %d", (long long)HD, G);
+    return LOOM_ERR_INVALID;
+}
+
+}  // namespace loom
+
+using namespace loom;
+
+extern "C" int loom_gqa_prefill(int dtype, const void* qkv, int64_t qkv_ld, void* k_cache,
+                                void* v_cache, int64_t cache_stride_b, int64_t cache_stride_t,
+                                int64_t cache_stride_h, const float* cos_table,
+                                const float* sin_table, void* q_out, void* c_out, void* kctx_out,
+                                int64_t out_ld, int64_t B, int64_t T, int64_t start,
+                                int64_t cache_len, int64_t QH, int64_t KVH, int64_t HD,
+                                void* stream) {
+    clear_error();
+    LOOM_CHECK(qkv && k_cache && v_cache && cos_table && sin_table && q_out && c_out && kctx_out,
+               "gqa_prefill: null argument");
+    LOOM_CHECK(B >= 0 && T >= 0 && start >= 0 && KVH >= 1 && QH % KVH == 0 && HD % 2 == 0,
+               "gqa_prefill: bad shape B=%lld T=%lld start=%lld QH=%lld KVH=%lld HD=%lld",
+               (long long)B, (long long)T, (long long)start, (long long)QH, (long long)KVH,
+               (long long)HD);
+    LOOM_CHECK(qkv_ld >= (QH + 2 * KVH) * HD && out_ld >= QH * HD,
+               "gqa_prefill: row strides smaller than the rows");
+    LOOM_CHECK(cache_stride_t >= HD && cache_stride_h >= HD,
+               "gqa_prefill: cache strides smaller than a head row");
+    LOOM_CHECK(T <= (1 << 20), "gqa_prefill: chunk of %lld tokens too long", (long long)T);
+    LOOM_CHECK(start + T <= cache_len,
+               "gqa_prefill: positions %lld..%lld beyond the cache capacity %lld", (long long)start,
+               (long long)(start + T - 1), (long long)cache_len);
+    // the vector forms read 16-byte pieces of rows
+    LOOM_CHECK(HD % 32 != 0 ||
+                   ((((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q_out) & 15) == 0 &&
+                    cache_stride_b % 8 == 0 && cache_stride_t % 8 == 0 && cache_stride_h % 8 == 0),
+               "gqa_prefill: caches must be 16-byte aligned with strides divisible by 8");
+    if (B == 0 || T == 0) return LOOM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    switch (dtype) {
+        case LOOM_F32:
+            return prefill_dispatch<float>(qkv, qkv_ld, k_cache, v_cache, cache_stride_b,
+                                           cache_stride_t, cache_stride_h, cos_table, sin_table,
+                                           q_out, c_out, kctx_out, out_ld, B, T, start, QH, KVH,
+                                           HD, st);
+        case LOOM_BF16:
+            return prefill_dispatch<bf16_t>(qkv, qkv_ld, k_cache, v_cache, cache_stride_b,
+                                            cache_stride_t, cache_stride_h, cos_table, sin_table,
+                                            q_out, c_out, kctx_out, out_ld, B, T, start, QH, KVH,
+                                            HD, st);
+        case LOOM_F16:
+            return prefill_dispatch<f16_t>(qkv, qkv_ld, k_cache, v_cache, cache_stride_b,
+                                           cache_stride_t, cache_stride_h, cos_table, sin_table,
+                                           q_out, c_out, kctx_out, out_ld, B, T, start, QH, KVH,
+                                           HD, st);
+    }
+    set_error("gqa_prefill: unsupported dtype %d", dtype);
+    return LOOM_ERR_INVALID;
+}

@@ -368,10 +368,12 @@ class LoomDecoder:
 
     @torch.no_grad()
     def generate(self, prompt: torch.Tensor, n_new: int, return_logits: bool = False,
-                 use_graph: bool = True):
-        """Token-by-token prefill of ``prompt`` [B, P], then ``n_new`` greedy tokens
-        (the reference's infer loop).  Returns the new ids [B, n_new] (and the logits
-        after every step [B, P + n_new, V] with return_logits)."""
+                 use_graph: bool = True, chunked_prefill: bool = False):
+        """Prefill ``prompt`` [B, P] token by token (the reference's infer loop) or,
+        with ``chunked_prefill``, through the chunked forward; then ``n_new``
+        greedy tokens.  Returns the new ids [B, n_new] (and with return_logits the
+        logits after every step: [B, P + n_new, V] token by token, or
+        [B, 1 + n_new, V] from the last prompt position on when chunked)."""
         B, P = prompt.shape
         if B != self.B:
             raise ValueError(f"prompt batch {B} != engine batch {self.B}")
@@ -379,14 +381,19 @@ class LoomDecoder:
             raise ValueError("prompt must hold at least one token")
         total = P + n_new
         self._check_capacity(total - 1)
-        self.reset()
-        self.prompt_buf[:, :P].copy_(prompt.to(self.dev))
         logits_all = [] if return_logits else None
-        self._launch_step(first=True, prompt_len=P)
+        if chunked_prefill:
+            self.prefill(prompt)
+            first_pos = P
+        else:
+            self.reset()
+            self.prompt_buf[:, :P].copy_(prompt.to(self.dev))
+            self._launch_step(first=True, prompt_len=P)
+            first_pos = 1
         if return_logits:
             logits_all.append(self.logits.float().clone())
         graph = self._graph_for(P) if use_graph else None
-        for _ in range(1, total):
+        for _ in range(first_pos, total):
             if graph is not None:
                 graph.replay()
             else:
@@ -411,6 +418,14 @@ class LoomDecoder:
         self._prompt_len = P
         self._launch_step(first=True, prompt_len=P)
         self.pos = 1
+
+    def prefill(self, prompt: torch.Tensor) -> None:
+        """Chunked prefill of ``prompt`` [B, P] (the reference's chunked forward,
+        loomformer.py:3788-3883): afterwards the engine stands at position P
+        with the last prompt token's logits, as token-by-token steps would leave
+        it; ``replay_steps`` / ``generated`` continue from there."""
+        from .prefill import prefill
+        prefill(self, prompt)
 
     @torch.no_grad()
     def replay_steps(self, n: int) -> None:

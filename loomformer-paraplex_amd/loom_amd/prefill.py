@@ -1,0 +1,223 @@
+"""Chunked prefill of the decode state.
+
+The reference runs a prompt through ``Model._forward_chunked``
+(loomformer.py:3788-3883): the whole block stack for one temporal chunk of
+tokens at a time, the temporal Tria carry from boundary to boundary, PolARM
+and a document key at every fire, and the final cross-attention over the keys
+of earlier fires.  ``prefill`` does the same on the gfx950 kernels and leaves
+the engine exactly where token-by-token ``Model.step`` (:3951-4091) would be
+after the last prompt token: KV caches, per-layer phase traces, the Tria
+document state and pending fire, the final-CA key cache, the position and the
+last token's logits.  Decoding then continues with the captured step.
+
+Chunk boundaries are the step's fire positions: (t + 1) % W == 0 while
+t + 1 < seq_len, plus every position where some row holds the <CARRY> id;
+the fire of row b at a boundary t is hard(t) or prompt[b, t] == <CARRY>
+(loomformer.py:4067-4078).  A chunk's first token is seeded from the state
+after the previous boundary in the rows where that boundary fired
+(tria_init_seed, tria.py:835-844), and the temporal carry restarts there
+(:3834-3850).
+"""
+from __future__ import annotations
+
+from typing import List
+
+import torch
+
+from . import _lib
+
+_P = _lib.ptr
+
+
+def chunk_bounds(prompt_cpu: torch.Tensor, window: int, seq_len: int, carry_id) -> List[int]:
+    """Last position of every chunk of a [B, P] prompt (the final one is P-1)."""
+    B, P = prompt_cpu.shape
+    fires = set(t for t in range(P) if (t + 1) % window == 0 and t + 1 < seq_len)
+    if carry_id is not None:
+        hit = (prompt_cpu == int(carry_id)).any(dim=0)
+        fires |= set(int(t) for t in hit.nonzero().flatten().tolist())
+    ends = sorted(fires)
+    if not ends or ends[-1] != P - 1:
+        ends.append(P - 1)
+    return ends
+
+
+@torch.no_grad()
+def prefill(eng, prompt: torch.Tensor) -> None:
+    """Run ``prompt`` [B, P] through the chunked forward and set ``eng`` up to
+    decode position P (see the module docstring)."""
+    c = eng.cfg
+    B, P = prompt.shape
+    if B != eng.B or P < 1:
+        raise ValueError("prompt must be [batch, >=1]")
+    eng._check_capacity(P - 1)
+    N, H, L, QH, KVH, HD = c.N, c.H, c.L, c.QH, c.KVH, c.HD
+    dev, dt, code = eng.dev, eng.dtype, eng.code
+    st = eng._stream()
+    call = eng._call
+    prompt_d = prompt.to(dev)
+    prompt_cpu = prompt.cpu()
+    ends = chunk_bounds(prompt_cpu, c.window, c.seq_len, eng.carry_token_id)
+    hard = torch.tensor([(t + 1) % c.window == 0 and t + 1 < c.seq_len for t in range(P)])
+    fire_all = hard[None, :].expand(B, P).clone()
+    if eng.carry_token_id is not None:
+        fire_all |= prompt_cpu == int(eng.carry_token_id)
+    fire_all_d = fire_all.to(dev)
+
+    eng.reset()
+    eng.prompt_buf[:, :P].copy_(prompt_d)
+    eng.tokens[:, :P].copy_(prompt_d)
+    Tmax = max(e - s + 1 for s, e in zip([0] + [x + 1 for x in ends[:-1]], ends))
+    z = lambda *s, dtype=dt: torch.zeros(*s, dtype=dtype, device=dev)
+    M = B * Tmax
+    h = z(M, N)
+    y = z(M, N)
+    qkv = z(M, N + 2 * c.KV)
+    q = z(M, QH, HD)
+    cbuf = z(M, N)
+    kctx = z(M, N)
+    d = z(M, N)
+    dh = z(M, N)
+    R = z(M, H)
+    beta = z(M, H)
+    act = z(M, H)
+    sbuf = z(M, H)
+    hist = z(M, 2 * L, 2 * N)
+    carry = z(2, M, H, 3, 3)
+    pbuf = z(2, M, H)
+    traces = z(2, L, B, H)       # phase traces in / out of a chunk (swapped per chunk)
+    state = z(B, H, 3, 3)
+    state32 = torch.empty(B, H, 3, 3, dtype=torch.float32, device=dev)
+    pooled, z32, a_key = z(B, 9), z(B, 32), z(B, N)
+    stage_k, stage_v = z(B, N), z(B, N)
+    snap = torch.empty((), dtype=torch.float32, device=dev)
+    empty_reset = None
+    hist_bt = 2 * L * 2 * N
+    cache_sb = KVH * eng.max_len * HD
+    cache_st = HD
+    cache_sh = eng.max_len * HD
+
+    def lin(x, w, out, rows, nout, k, **kw):
+        eng._linear(x, w, out, rows, nout, k, **kw)
+
+    def depth(sub, out, rows):
+        call("loom_depth_attn_forward", code, _P(eng.qp[sub]), _P(hist), _P(hist[:, :, N:]),
+             hist_bt, 2 * N, _P(out), None, None, rows, sub + 1, QH, HD, st)
+
+    have_state = False
+    tin = 0
+    seed_valid = z(B, dtype=torch.uint8)
+    ca_len = 0
+    s = 0
+    for e in ends:
+        Tc = e - s + 1
+        rows = B * Tc
+        # token rows (b, t) of this chunk, b-major
+        ids = prompt_d[:, s:e + 1].reshape(-1)
+        torch.index_select(eng.emb, 0, ids, out=h[:rows])
+        hv = hist[:rows]
+        lin(h, eng.kvw, hv[:, 0], rows, 2 * N, N, ldc=2 * L * 2 * N)
+        lin(h, eng.blocks[0]["qkv"], qkv, rows, N + 2 * c.KV, N)
+        sub = 0
+        carry_i, p_i = None, None
+        for bi, blk in enumerate(eng.blocks):
+            last = bi == L - 1
+            # ---- attention over the cache (rows < s) and this chunk (loomformer.py:3215-3332)
+            call("loom_gqa_prefill", code, _P(qkv), N + 2 * c.KV, _P(eng.k_cache[bi]),
+                 _P(eng.v_cache[bi]), cache_sb, cache_st, cache_sh, _P(eng.cos), _P(eng.sin),
+                 _P(q), _P(cbuf), _P(kctx), N, B, Tc, s, eng.max_len, QH, KVH, HD, st)
+            # ---- LN(o(C) + w_o(depth read 2*bi)) (loomformer.py:3999-4000)
+            depth(sub, d, rows)
+            lin(cbuf, blk["o"], y, rows, N, N)
+            lin(d, eng.wo, y, rows, N, N, residual=y)
+            call("loom_add_layernorm", code, _P(y), None, _P(blk["ln1_w"]), _P(blk["ln1_b"]),
+                 _P(h), rows, N, 1e-5, st)
+            # ---- history slot 2*bi+1, W_real (+ gate with the previous block's p)
+            sub += 1
+            lin(h, eng.kvw, hv[:, sub], rows, 2 * N, N, ldc=2 * L * 2 * N)
+            if p_i is None:
+                lin(h, blk["w1r"], R, rows, H, N, bias=blk["b1r"])
+            else:
+                lin(h, blk["w1r"], R, rows, H, N, bias=blk["b1r"], gate_p=pbuf[p_i],
+                    gate_alpha=blk["alpha"])
+            depth(sub, dh, rows)
+            # ---- Paraplex FFN (loomformer.py:2818-2893): beta space, fused pointwise
+            # chain with the phase trace carried from the previous chunk
+            call("loom_beta_forward", code, _P(h), _P(q), _P(kctx), _P(cbuf), _P(dh),
+                 _P(blk["w1i"]), _P(beta), None, rows, N, H, c.imag_in, c.Hq, HD, QH,
+                 1 if c.sectors == "open" else 0, st)
+            call("loom_paraplex_forward", code, _P(R), _P(R), _P(beta), _P(blk["ib"]),
+                 _P(traces[tin, bi]), _P(blk["tw"]), empty_reset, _P(blk["anchor"]), _P(act),
+                 _P(sbuf), _P(traces[1 - tin, bi]), _P(snap), B, Tc, H, float(c.powlu_m), st)
+            # ---- Tria depth op of the block (loomformer.py:3588-3617), axis bi % 3
+            out_i = 0 if carry_i != 0 else 1
+            gate = not last
+            new_p = (0 if p_i != 0 else 1) if gate else None
+            seeded = bi == 0 and have_state
+            call("loom_tria_depth_forward", code, _P(R), _P(sbuf), _P(act),
+                 None if (carry_i is None or seeded) else _P(carry[carry_i]),
+                 _P(state) if seeded else None, _P(seed_valid) if seeded else None,
+                 _P(blk["gate_w"]) if gate else None, _P(carry[out_i]),
+                 _P(pbuf[new_p]) if gate else None, None, B, Tc, H, float(c.tria_alpha),
+                 bi % 3, st)
+            carry_i, p_i = out_i, new_p
+            # ---- LN(w_o(d_h) + W2(act) + b2) (loomformer.py:4045)
+            lin(dh, eng.wo, y, rows, N, N)
+            lin(act, blk["w2"], y, rows, N, H, bias=blk["b2"], residual=y)
+            call("loom_add_layernorm", code, _P(y), None, _P(blk["ln2_w"]), _P(blk["ln2_b"]),
+                 _P(h), rows, N, 1e-5, st)
+            if not last:
+                sub += 1
+                lin(h, eng.kvw, hv[:, sub], rows, 2 * N, N, ldc=2 * L * 2 * N)
+                lin(h, eng.blocks[bi + 1]["qkv"], qkv, rows, N + 2 * c.KV, N)
+        # ---- temporal carry over the chunk: restart at position 0 and at a
+        # seeded first token, else continue from the state (loomformer.py:3834-3850)
+        reset = z(B, Tc, dtype=torch.uint8)
+        if s == 0:
+            reset[:, 0] = 1
+        else:
+            reset[:, 0] = seed_valid
+        call("loom_temporal_carry_endpoint_forward", code, _P(carry[carry_i]), _P(reset),
+             _P(state) if have_state else None, None, _P(state), _P(state32), B, Tc, H, st)
+        have_state = True
+        fire_e = fire_all_d[:, e]
+        if bool(fire_all[:, e].any()):
+            # PolARM where the row fired, then the document key of this boundary
+            fmask = fire_e.to(torch.uint8)
+            call("loom_polarm_forward", code, _P(state), _P(state), _P(fmask), B * H, H,
+                 float(c.polarm_beta), 1e-6, st)
+            call("loom_slot_attention_pool_forward", code, _P(state), _P(eng.score_w),
+                 _P(pooled), None, B, H, st)
+            lin(pooled, eng.proj_w, z32, B, 32, 9, bias=eng.proj_b)
+            lin(z32, eng.up_w, a_key, B, N, 32, bias=eng.up_b)
+            lin(a_key, eng.wqk, stage_k, B, N, N)
+            lin(a_key, eng.wv, stage_v, B, N, N)
+            if ca_len >= eng.max_keys:
+                raise ValueError("final-CA key cache is full")
+            eng.ca_k[:, ca_len].copy_(stage_k)
+            eng.ca_v[:, ca_len].copy_(stage_v)
+            eng.ca_valid[:, ca_len].copy_(fmask)
+            ca_len += 1
+            seed_valid.copy_(fmask)
+        else:
+            seed_valid.zero_()
+        tin = 1 - tin
+        s = e + 1
+    # ---- final cross-attention and head of the last prompt token (tria.py:1560-1595)
+    Tc = ends[-1] - (ends[-2] + 1 if len(ends) > 1 else 0) + 1
+    h_last = h[:B * Tc].view(B, Tc, N)[:, Tc - 1].contiguous()
+    eng.h.copy_(h_last)
+    lin(eng.h, eng.wqk, eng.q_ca, B, N, N)
+    eng.ca_len.fill_(ca_len)
+    call("loom_final_ca_sparse_strided", code, _P(eng.q_ca), _P(eng.ca_k), _P(eng.ca_v),
+         eng.max_keys * N, _P(eng.ca_valid), eng.max_keys, _P(eng.h), float(eng.gamma),
+         _P(eng.h2), None, B, 1, eng.max_keys, _P(eng.ca_len), N, float(N ** -0.5), st)
+    lin(eng.h2, eng.head, eng.logits, B, c.V, N)
+    # ---- the engine's decode state after position P-1
+    eng.trace.copy_(traces[tin])
+    eng.doc.copy_(state)
+    eng.pending.copy_(fire_all_d[:, P - 1].to(torch.uint8))
+    eng.pos_dev.fill_(P)
+    eng.ids.copy_(prompt_d[:, P - 1])
+    eng.pos = P
+    eng._prompt_len = P
