@@ -77,13 +77,13 @@ __device__ __forceinline__ float epilogue(const GemmArgs& a, int64_t m, int64_t 
 
 // ------------------------------------------------------------------ MFMA bf16
 
-constexpr int MB_M = 128, MB_N = 128, MB_K = 64, MB_PAD = 8, MB_LD = MB_K + MB_PAD;
+constexpr int MB_M = 128, MB_N = 128, MB_K = 64;
 
 template <bool GATHER>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gemm_bf16_mfma_kernel(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t Ws[MB_N * MB_LD];
-    __shared__ __attribute__((aligned(16))) uint16_t Xs[MB_M * MB_LD];
+    __shared__ __attribute__((aligned(16))) uint16_t Ws[2][MB_N * MB_K];
+    __shared__ __attribute__((aligned(16))) uint16_t Xs[2][MB_M * MB_K];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -100,8 +100,11 @@ gemm_bf16_mfma_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    uint4 wreg[4], xreg[4];
-    auto load_tiles = [&](int64_t k0) {
+    // Tiles are 64 k per row (128 B) with the 16-byte chunk c of row r stored at
+    // chunk c ^ ((r >> 1) & 7): the 16 rows of a fragment read and the two rows
+    // of 8 chunks in a 16-lane store each cover all 64 banks once.
+    auto lds_off = [](int r, int c) { return r * MB_K + ((c ^ ((r >> 1) & 7)) << 3); };
+    auto load_tiles = [&](int64_t k0, uint4 (&wr)[4], uint4 (&xr)[4]) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int chunk = tid + c * 256;
@@ -117,49 +120,60 @@ gemm_bf16_mfma_kernel(GemmArgs a) {
                 else
                     xv = *reinterpret_cast<const uint4*>(X + m * a.ldx + k);
             }
-            wreg[c] = wv;
-            xreg[c] = xv;
+            wr[c] = wv;
+            xr[c] = xv;
         }
     };
-    auto store_tiles = [&]() {
+    auto store_tiles = [&](int buf, const uint4 (&wr)[4], const uint4 (&xr)[4]) {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int chunk = tid + c * 256;
-            const int row = chunk >> 3;
-            const int kc = (chunk & 7) * 8;
-            *reinterpret_cast<uint4*>(&Ws[row * MB_LD + kc]) = wreg[c];
-            *reinterpret_cast<uint4*>(&Xs[row * MB_LD + kc]) = xreg[c];
+            const int off = lds_off(chunk >> 3, chunk & 7);
+            *reinterpret_cast<uint4*>(&Ws[buf][off]) = wr[c];
+            *reinterpret_cast<uint4*>(&Xs[buf][off]) = xr[c];
         }
     };
-
-    const int64_t nk = ceil_div(a.K, MB_K);
-    load_tiles(0);
-    store_tiles();
-    __syncthreads();
     const int fr = lane & 15;          // fragment row
-    const int fk = (lane >> 4) * 8;    // fragment k offset
-    for (int64_t kt = 0; kt < nk; ++kt) {
-        if (kt + 1 < nk) load_tiles((kt + 1) * MB_K);
+    const int fc = lane >> 4;          // fragment 8-element chunk within a 32-wide k-step
+    auto compute = [&](int buf) {
 #pragma unroll
-        for (int kk = 0; kk < MB_K; kk += 32) {
+        for (int kk = 0; kk < MB_K / 32; ++kk) {
             bf16x8 af[4], bf[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                af[i] = *reinterpret_cast<const bf16x8*>(&Ws[(wn * 64 + i * 16 + fr) * MB_LD + kk + fk]);
+                af[i] = *reinterpret_cast<const bf16x8*>(&Ws[buf][lds_off(wn * 64 + i * 16 + fr, 4 * kk + fc)]);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                bf[j] = *reinterpret_cast<const bf16x8*>(&Xs[(wm * 64 + j * 16 + fr) * MB_LD + kk + fk]);
+                bf[j] = *reinterpret_cast<const bf16x8*>(&Xs[buf][lds_off(wm * 64 + j * 16 + fr, 4 * kk + fc)]);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-        __syncthreads();
-        if (kt + 1 < nk) {
-            store_tiles();
-            __syncthreads();
-        }
+    };
+    // Barrier for the LDS tiles only: the global loads of later k-tiles stay in
+    // flight (each is waited for where its registers are stored to LDS).
+    auto lds_sync = []() {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    };
+
+    // k-tile t lives in LDS buffer t & 1; its global loads are issued one
+    // k-step ahead and waited for where they are stored to LDS
+    const int64_t nk = ceil_div(a.K, MB_K);
+    uint4 wr[4], xr[4];
+    load_tiles(0, wr, xr);
+    store_tiles(0, wr, xr);
+    lds_sync();
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        const int cur = (int)(kt & 1);
+        const bool more = kt + 1 < nk;
+        if (more) load_tiles((kt + 1) * MB_K, wr, xr);
+        compute(cur);
+        if (more) store_tiles(cur ^ 1, wr, xr);
+        lds_sync();
     }
 
     uint16_t* out = (uint16_t*)a.out;
