@@ -16,13 +16,40 @@ namespace loom {
 constexpr int kTriaThreads = 256;
 
 // Copy n9 = rows*9 contiguous values between global memory and LDS with
-// coalesced word accesses.
+// coalesced accesses: whole 16-byte pieces (8 values of a 16-bit type, 4 of
+// fp32) when the slice is 16-byte aligned and a whole number of pieces, single
+// values otherwise.
 template <typename T>
 __device__ __forceinline__ void stage_in(float* lds, const T* src, int n9) {
+    constexpr int V = 16 / (int)sizeof(T);
+    if (((uintptr_t)src & 15) == 0 && n9 % V == 0) {
+        for (int c = threadIdx.x; c < n9 / V; c += blockDim.x) {
+            float v[V];
+            if constexpr (V == 8) Vec8<T>::load(src + c * 8, v);
+            else {
+                const float4 x = *reinterpret_cast<const float4*>(src + c * 4);
+                v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+            }
+#pragma unroll
+            for (int e = 0; e < V; ++e) lds[c * V + e] = v[e];
+        }
+        return;
+    }
     for (int k = threadIdx.x; k < n9; k += blockDim.x) lds[k] = ld(src + k);
 }
 template <typename T>
 __device__ __forceinline__ void stage_out(T* dst, const float* lds, int n9) {
+    constexpr int V = 16 / (int)sizeof(T);
+    if (((uintptr_t)dst & 15) == 0 && n9 % V == 0) {
+        for (int c = threadIdx.x; c < n9 / V; c += blockDim.x) {
+            float v[V];
+#pragma unroll
+            for (int e = 0; e < V; ++e) v[e] = lds[c * V + e];
+            if constexpr (V == 8) Vec8<T>::store(dst + c * 8, v);
+            else *reinterpret_cast<float4*>(dst + c * 4) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+        return;
+    }
     for (int k = threadIdx.x; k < n9; k += blockDim.x) st(dst + k, lds[k]);
 }
 
