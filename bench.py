@@ -244,6 +244,36 @@ def bench_tr_pipeline(iters):
                 keys=K)
 
 
+def bench_gqa(iters):
+    """The decode step's attention (its largest kernel): B=32, 8 q heads over 2
+    kv heads of 96, a head-major bf16 cache at 2176 positions (the middle of
+    the timed decode), RoPE + append + attention + merge in one launch."""
+    import torch
+    from loom_amd import _lib
+
+    dev, bf = "cuda", torch.bfloat16
+    B, QH, KVH, HD, L, cap = 32, 8, 2, 96, 2176, 2305
+    g = torch.Generator(device=dev).manual_seed(6)
+    qkv = torch.randn(B, (QH + 2 * KVH) * HD, generator=g, device=dev).to(bf)
+    kc = torch.randn(B, KVH, cap, HD, generator=g, device=dev).to(bf)
+    vc = torch.randn(B, KVH, cap, HD, generator=g, device=dev).to(bf)
+    from loom_amd.weights import rope_tables
+    from loom_amd.config import NANO_CHK, ModelConfig
+    cos, sin = (t.to(dev) for t in rope_tables(ModelConfig.from_dict(NANO_CHK).with_seq_len(4096), cap))
+    out = torch.empty(3, B, QH * HD, device=dev, dtype=bf)
+    nb = _lib.load().loom_gqa_workspace_bytes(B, cap, QH, KVH, HD)
+    ws = torch.zeros(nb // 4 + 1, device=dev)
+    P = _lib.ptr
+
+    def fn():   # on the current stream (the capture stream inside timed())
+        _lib.call("loom_gqa_decode_step", 1, P(qkv), P(kc), P(vc), KVH * cap * HD, HD, cap * HD,
+                  P(cos), P(sin), P(out[0]), P(out[1]), P(out[2]), QH * HD, P(ws), nb, B, L, None,
+                  QH, KVH, HD, _lib.stream_of(qkv))
+    ms = timed(fn, iters)
+    nbytes = 2 * B * KVH * L * HD * 2
+    return dict(ms=ms, bytes=nbytes, GBs=nbytes / (ms * 1e-3) / 1e9)
+
+
 def copy_bandwidth():
     import torch
     x = torch.empty(1 << 28, dtype=torch.float32, device="cuda")   # 1 GiB
@@ -404,6 +434,8 @@ def main():
         log(f"TR: {json.dumps({k: round(v, 3) for k, v in tr.items()})}")
         trp = bench_tr_pipeline(max(3, args.micro_iters // 4))
         log(f"TR pipeline: {json.dumps({k: round(v, 3) for k, v in trp.items()})}")
+        gq = bench_gqa(args.micro_iters)
+        log(f"GQA decode: {json.dumps({k: round(v, 3) for k, v in gq.items()})}")
         copy_gbs = copy_bandwidth()
         kernels = {
             "paraplex_pointwise": {"ms": px["pointwise_ms"], "GB/s": px["pointwise_GBs"],
@@ -420,6 +452,8 @@ def main():
                             "frac": px["w_imag_TFLOPs"] / BF16_PEAK_TFLOPS},
             "w2_gemm": {"ms": px["w2_ms"], "TFLOP/s": px["w2_TFLOPs"],
                         "frac": px["w2_TFLOPs"] / BF16_PEAK_TFLOPS},
+            "gqa_decode_ctx2176": {"ms": gq["ms"], "GB/s": gq["GBs"], "frac": gq["GBs"] / HBM_PEAK_GBS,
+                                   "algorithmic_bytes": gq["bytes"]},
             "paraplex_ffn_total_ms": px["ffn_ms"],
             "device_copy_GB/s": copy_gbs,
         }
