@@ -5,7 +5,8 @@
 // qh*HD + d.  Lane j of the row's 16 owns the EPL = HD/16 contiguous elements
 // [j*EPL, (j+1)*EPL).  Scores for 8 depth slots are formed before any value is
 // read (8 independent K loads in flight per lane), then folded into an fp32
-// online softmax in log2 units.
+// online softmax in log2 units.  The K/V rows are read
+// once, with nontemporal loads.
 #pragma once
 
 #include "loom_common.h"
@@ -44,8 +45,8 @@ __device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __re
 #pragma unroll
         for (int c = 0; c < C; ++c) {
             const int sc_ = s0 + c < S ? s0 + c : S - 1;   // in range; masked below
-            kr[c].load(kp + (int64_t)sc_ * ss);
-            vr[c].load(vp + (int64_t)sc_ * ss);
+            kr[c].load_nt(kp + (int64_t)sc_ * ss);
+            vr[c].load_nt(vp + (int64_t)sc_ * ss);
         }
         float sc[C];
 #pragma unroll

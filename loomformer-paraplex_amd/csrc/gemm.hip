@@ -374,7 +374,7 @@ ffn_decode_kernel(FfnArgs f) {
         const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
         const float x = bf(f.R[e]);
         float amp, gate;
-        softplus_gate(x, f.m, amp, gate);
+        softplus_gate<false>(x, f.m, amp, gate);   // bf16 outputs (see softplus_gate)
         const float act = fmaf(amp, sv, x) * gate;
         f.trace[e] = f32_to_bf16(s0);
         f.act[e] = f32_to_bf16(act);

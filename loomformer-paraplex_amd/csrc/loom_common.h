@@ -116,6 +116,13 @@ template <> struct Vec8<bf16_t> : Vec8_16<bf16_t> {
         *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
                                                   pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
     }
+    // write-once output: one nontemporal 16-byte store
+    __device__ __forceinline__ static void store_nt(bf16_t* p, const float v[8]) {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const u32x4 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                         pack_bf16x2(v[6], v[7])};
+        __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));
+    }
 };
 template <> struct Vec8<f16_t> : Vec8_16<f16_t> {};
 
@@ -181,6 +188,19 @@ struct RawRow {
             const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
 #pragma unroll
             for (int k = 0; k < NW; ++k) w[k] = q[k];
+        }
+    }
+    // Streaming form of load for rows read exactly once: the nontemporal hint
+    // keeps them from displacing reused lines in the caches.
+    __device__ __forceinline__ void load_nt(const T* p) {
+        if constexpr (kPairs) {
+            const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+            for (int k = 0; k < NW; ++k) w[k] = __builtin_nontemporal_load(q + k);
+        } else {
+            const uint16_t* q = reinterpret_cast<const uint16_t*>(p);
+#pragma unroll
+            for (int k = 0; k < NW; ++k) w[k] = __builtin_nontemporal_load(q + k);
         }
     }
     // Hide the words' values from the compiler (no instruction is emitted), so a

@@ -75,6 +75,13 @@ struct VecIO {
             for (int k = 0; k < VEC; ++k) st(p + k, v[k]);
         }
     }
+    // write-once outputs of the chain (nontemporal where the row is one 16-byte vector)
+    __device__ __forceinline__ static void store_nt(T* p, const float v[VEC]) {
+        if constexpr (VEC == 8 && std::is_same<T, bf16_t>::value)
+            Vec8<T>::store_nt(p, v);
+        else
+            store(p, v);
+    }
 };
 
 constexpr int kPxPrefetch = 2;   // tokens of R / beta (/ gate_src) in flight per thread
@@ -160,13 +167,13 @@ paraplex_forward_kernel(const T* __restrict__ p_real, const T* __restrict__ gate
                 const float raw = rs ? s0 : fmaf(prev[k], tw[k], s0);
                 const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
                 float amp, gate;
-                softplus_gate(SAME_GATE ? r[k] : g[k], m, amp, gate);
+                softplus_gate<!std::is_same<T, bf16_t>::value>(SAME_GATE ? r[k] : g[k], m, amp, gate);
                 so[k] = sv;
                 ao[k] = fmaf(amp, sv, r[k]) * gate;
                 prev[k] = s0;
             }
-            VecIO<T, VEC>::store(ps, so);
-            VecIO<T, VEC>::store(po, ao);
+            VecIO<T, VEC>::store_nt(ps, so);
+            VecIO<T, VEC>::store_nt(po, ao);
             pr += H; pb += H; pg += H; po += H; ps += H;
         }
     }

@@ -35,11 +35,16 @@ __device__ __forceinline__ float powlu_gate(float amp, float m) {
 //   G = A^(m/(sqrt A + 1)) * sigmoid(A), with one reciprocal for both
 //       quotients: r = 1/((sqrt A + 1)(1 + u)).
 // No branch and no select on the sign of x.
+// EXACT = false drops the log1p rounding term: then A = log(u) exactly as
+// rounded, off by at most 2^-24 absolute from log1p(E) (relative error below
+// 2^-24 / E, under half a bf16 ulp for every E > 2^-16, and for smaller E both
+// A and G are below the bf16 resolution of the output (A + r) * G).
+template <bool EXACT = true>
 __device__ __forceinline__ void softplus_gate(float x, float m, float& amp, float& gate) {
     const float e = x * kLog2e;
     const float E = __builtin_amdgcn_exp2f(fminf(e, 20.0f * kLog2e));
     const float u = 1.0f + E;
-    const float a0 = fmaf(flog2(u), kLn2, E - (u - 1.0f));
+    const float a0 = EXACT ? fmaf(flog2(u), kLn2, E - (u - 1.0f)) : flog2(u) * kLn2;
     amp = __builtin_amdgcn_fmed3f(x, a0, 3.0e38f);   // max(x, a0) without a NaN-quieting pass
     const float safe = __builtin_amdgcn_fmed3f(amp, 1.0e-12f, 3.0e38f);
     const float d1 = fsqrt(safe) + 1.0f;
