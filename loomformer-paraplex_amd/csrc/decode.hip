@@ -754,21 +754,14 @@ __device__ __forceinline__ void mm3d(const float A[9], const float B[9], float o
             o[3 * r + c] = fmaf(A[3 * r + 2], B[6 + c], fmaf(A[3 * r + 1], B[3 + c], A[3 * r] * B[c]));
 }
 
-template <typename T>
-__global__ void __launch_bounds__(256)
-decode_temporal_kernel(const T* __restrict__ depth, const T* __restrict__ prev,
-                       const uint8_t* __restrict__ reset_now, const uint8_t* __restrict__ fire,
-                       T* __restrict__ out, int64_t B, int64_t H, float beta, float eps) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= B * H) return;
-    const int64_t b = e / H;
-    float M[9];
-#pragma unroll
-    for (int k = 0; k < 9; ++k) M[k] = ld(depth + e * 9 + k);
-    if (prev != nullptr && reset_now[b] == 0) {
-        float P[9], R[9];
-#pragma unroll
-        for (int k = 0; k < 9; ++k) P[k] = ld(prev + e * 9 + k);
+// One (b, h) stream of the decode temporal step (loomformer.py:4053-4085):
+// M = D unless the stream continues, then M = N(D . P) (N: rms normalisation
+// with eps 1e-6 inside the root); on a fire, PolARM: G = M^T M,
+// s = max(tr(G)/3, eps), M <- M (I - beta/2 (G/s - I)) (tria.py:128-139).
+__device__ __forceinline__ void temporal_head(float M[9], const float P[9], bool cont, bool fires,
+                                              float beta, float eps) {
+    if (cont) {
+        float R[9];
         mm3d(M, P, R);
         float s = 0.0f;
 #pragma unroll
@@ -777,7 +770,7 @@ decode_temporal_kernel(const T* __restrict__ depth, const T* __restrict__ prev,
 #pragma unroll
         for (int k = 0; k < 9; ++k) M[k] = R[k] * inv;
     }
-    if (fire != nullptr && fire[b] != 0) {
+    if (fires) {
         float Gm[9];
 #pragma unroll
         for (int r = 0; r < 3; ++r)
@@ -795,8 +788,150 @@ decode_temporal_kernel(const T* __restrict__ depth, const T* __restrict__ prev,
 #pragma unroll
         for (int k = 0; k < 9; ++k) M[k] = R[k];
     }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+decode_temporal_kernel(const T* __restrict__ depth, const T* __restrict__ prev,
+                       const uint8_t* __restrict__ reset_now, const uint8_t* __restrict__ fire,
+                       T* __restrict__ out, int64_t B, int64_t H, float beta, float eps) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= B * H) return;
+    const int64_t b = e / H;
+    float M[9], P[9];
+    const bool cont = prev != nullptr && reset_now[b] == 0;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        M[k] = ld(depth + e * 9 + k);
+        P[k] = cont ? ld(prev + e * 9 + k) : 0.0f;
+    }
+    temporal_head(M, P, cont, fire != nullptr && fire[b] != 0, beta, eps);
 #pragma unroll
     for (int k = 0; k < 9; ++k) st(out + e * 9 + k, M[k]);
+}
+
+// The whole per-token Tria tail of a decode step, one block per batch row b
+// (thread t owns heads h = t + kReadThreads*i, i < IT):
+//   the temporal step and PolARM of every head (temporal_head), stored as
+//   the new document state doc[b] (in place: a thread reads its own heads'
+//   previous state before it writes them);
+//   the slot attention pool of the stored state over h (tria.py:1351-1389):
+//   softmax_h <score_w, vec C_h>, pooled = sum_h softmax * vec C_h (natural
+//   exponentials, online per thread, merged over the block);
+//   proj Linear(9, 32) and up Linear(32, N) of the pooled row (tria.py:
+//   1436-1441).  Every intermediate the unfused ops store (doc, pooled, z) is
+//   rounded to T before it is used, as they would read it back.
+constexpr int kReadThreads = 1024;
+
+template <typename T, int IT>
+__global__ void __launch_bounds__(kReadThreads)
+decode_readout_kernel(const T* __restrict__ depth, const T* prev, const uint8_t* __restrict__ reset_now,
+                      const uint8_t* __restrict__ fire, T* doc, const T* __restrict__ score_w,
+                      const T* __restrict__ proj_w, const float* __restrict__ proj_b,
+                      const T* __restrict__ up_w, const float* __restrict__ up_b,
+                      T* __restrict__ a_out, int H, int N, float beta, float eps) {
+    __shared__ float red[kReadThreads / 64][11];
+    __shared__ float xs[9];
+    __shared__ float zs[32];
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int64_t b = blockIdx.x;
+    const bool cont = prev != nullptr && reset_now[b] == 0;
+    const bool fires = fire != nullptr && fire[b] != 0;
+    const int64_t base = b * H * 9;
+    float M[IT][9], P[IT][9];
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+        const int h = tid + kReadThreads * i;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            M[i][k] = h < H ? ld(depth + base + h * 9 + k) : 0.0f;
+            P[i][k] = (cont && h < H) ? ld(prev + base + h * 9 + k) : 0.0f;
+        }
+    }
+    float sw[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) sw[k] = ld(score_w + k);
+    float m = -INFINITY, l = 0.0f, acc[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) acc[k] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+        const int h = tid + kReadThreads * i;
+        if (h >= H) continue;
+        temporal_head(M[i], P[i], cont, fires, beta, eps);
+        float sc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            T* slot = doc + base + h * 9 + k;
+            st(slot, M[i][k]);
+            T rounded;
+            st(&rounded, M[i][k]);
+            M[i][k] = ld(&rounded);
+            sc = fmaf(M[i][k], sw[k], sc);
+        }
+        const float mn = fmaxf(m, sc);
+        const float corr = expf(m - mn);
+        const float pe = expf(sc - mn);
+        l = l * corr + pe;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) acc[k] = fmaf(pe, M[i][k], acc[k] * corr);
+        m = mn;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float mo = __shfl_xor(m, off, 64);
+        const float lo = __shfl_xor(l, off, 64);
+        const float mn = fmaxf(m, mo);
+        const float ca = (m == -INFINITY) ? 0.0f : expf(m - mn);
+        const float cb = (mo == -INFINITY) ? 0.0f : expf(mo - mn);
+        l = l * ca + lo * cb;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            const float ao = __shfl_xor(acc[k], off, 64);
+            acc[k] = acc[k] * ca + ao * cb;
+        }
+        m = mn;
+    }
+    if (lane == 0) {
+        red[wid][0] = m;
+        red[wid][1] = l;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) red[wid][2 + k] = acc[k];
+    }
+    __syncthreads();
+    if (tid < 9) {
+        float Mx = -INFINITY;
+        for (int q = 0; q < kReadThreads / 64; ++q) Mx = fmaxf(Mx, red[q][0]);
+        float L = 0.0f, A = 0.0f;
+        for (int q = 0; q < kReadThreads / 64; ++q) {
+            if (red[q][0] == -INFINITY) continue;
+            const float c = expf(red[q][0] - Mx);
+            L = fmaf(red[q][1], c, L);
+            A = fmaf(red[q][2 + tid], c, A);
+        }
+        T pooled;
+        st(&pooled, A * (1.0f / L));
+        xs[tid] = ld(&pooled);
+    }
+    __syncthreads();
+    if (tid < 32) {
+        float z = proj_b != nullptr ? proj_b[tid] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) z = fmaf(ld(proj_w + tid * 9 + k), xs[k], z);
+        T zr;
+        st(&zr, z);
+        zs[tid] = ld(&zr);
+    }
+    __syncthreads();
+    for (int n = tid; n < N; n += kReadThreads) {
+        float a = up_b != nullptr ? up_b[n] : 0.0f;
+        float w[32];
+#pragma unroll
+        for (int j = 0; j < 32; j += 8) Vec8<T>::load(up_w + (int64_t)n * 32 + j, w + j);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) a = fmaf(w[j], zs[j], a);
+        st(a_out + b * N + n, a);
+    }
 }
 
 // ------------------------------------------------------------------ dispatch
@@ -949,6 +1084,25 @@ static int temporal_step_dispatch(const void* depth, const void* prev, const uin
                        0, st, (const T*)depth, (const T*)prev, reset_now, fire, (T*)out, B, H,
                        beta, eps);
     return launch_status("loom_tria_decode_temporal");
+}
+
+template <typename T>
+static int readout_dispatch(const void* depth, const void* prev, const uint8_t* reset_now,
+                            const uint8_t* fire, void* doc, const void* score_w, const void* proj_w,
+                            const float* proj_b, const void* up_w, const float* up_b, void* a_out,
+                            int64_t B, int64_t H, int64_t N, float beta, float eps, hipStream_t st) {
+#define LOOM_READOUT(IT)                                                                         \
+    if (H <= (int64_t)(IT) * kReadThreads) {                                                     \
+        hipLaunchKernelGGL((decode_readout_kernel<T, IT>), dim3((unsigned)B), dim3(kReadThreads), \
+                           0, st, (const T*)depth, (const T*)prev, reset_now, fire, (T*)doc,       \
+                           (const T*)score_w, (const T*)proj_w, proj_b, (const T*)up_w, up_b,      \
+                           (T*)a_out, (int)H, (int)N, beta, eps);                                \
+        return launch_status("loom_decode_tria_readout");                                        \
+    }
+    LOOM_READOUT(1) LOOM_READOUT(2) LOOM_READOUT(3) LOOM_READOUT(4)
+#undef LOOM_READOUT
+    set_error("decode_tria_readout: H=%lld above %d", (long long)H, 4 * kReadThreads);
+    return LOOM_ERR_INVALID;
 }
 
 #define LOOM_DTYPE_SWITCH(dtype, FN, ...)               \
@@ -1179,9 +1333,60 @@ argmax_rows_kernel(const T* __restrict__ logits, int64_t V, int64_t* __restrict_
     }
 }
 
+// Same pick for rows of 8-element vectors (V % 8 == 0, 16-byte aligned rows of
+// at most 256*8*VPT values): every thread requests all of its VPT vectors
+// before it compares, so a row costs one memory round trip.
+template <typename T, int VPT>
+__global__ void __launch_bounds__(256)
+argmax_rows_vec_kernel(const T* __restrict__ logits, int64_t V, int64_t* __restrict__ ids) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const T* x = logits + (int64_t)blockIdx.x * V;
+    const int nvec = (int)(V / 8);
+    float vals[VPT][8];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int v = threadIdx.x + 256 * i;
+        if (v < nvec) Vec8<T>::load(x + 8 * v, vals[i]);
+    }
+    float best = -INFINITY;
+    int idx = (int)V;                      // NaN-free rows always replace this
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int v = threadIdx.x + 256 * i;
+        if (v >= nvec) continue;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (vals[i][e] > best) { best = vals[i][e]; idx = 8 * v + e; }   // increasing index
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ob = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { bv[w] = best; bi[w] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; ++k)
+            if (bv[k] > best || (bv[k] == best && bi[k] < idx)) { best = bv[k]; idx = bi[k]; }
+        ids[blockIdx.x] = idx < V ? idx : 0;
+    }
+}
+
 template <typename T>
 static int argmax_dispatch(const void* logits, int64_t rows, int64_t V, int64_t* ids,
                            hipStream_t st) {
+    const bool vec = V % 8 == 0 && V <= 256 * 8 * 8 && ((uintptr_t)logits & 15) == 0;
+#define LOOM_ARGMAX(VPT)                                                                        \
+    if (vec && V <= 256 * 8 * (VPT)) {                                                          \
+        hipLaunchKernelGGL((argmax_rows_vec_kernel<T, VPT>), dim3((unsigned)rows), dim3(256), 0, \
+                           st, (const T*)logits, V, ids);                                       \
+        return launch_status("loom_argmax_rows");                                               \
+    }
+    LOOM_ARGMAX(1) LOOM_ARGMAX(2) LOOM_ARGMAX(4) LOOM_ARGMAX(8)
+#undef LOOM_ARGMAX
     hipLaunchKernelGGL((argmax_rows_kernel<T>), dim3((unsigned)rows), dim3(256), 0, st,
                        (const T*)logits, V, ids);
     return launch_status("loom_argmax_rows");
@@ -1256,4 +1461,25 @@ extern "C" int loom_tria_decode_temporal(int dtype, const void* depth, const voi
     if (B * H == 0) return LOOM_OK;
     LOOM_DTYPE_SWITCH(dtype, temporal_step_dispatch, depth, prev, reset_now, fire, out, B, H,
                       polarm_beta, eps, (hipStream_t)stream)
+}
+
+extern "C" int loom_decode_tria_readout(int dtype, const void* depth, const void* prev,
+                                        const uint8_t* reset_now, const uint8_t* fire, void* doc,
+                                        const void* score_w, const void* proj_w,
+                                        const float* proj_b, const void* up_w, const float* up_b,
+                                        void* a_out, int64_t B, int64_t H, int64_t N,
+                                        float polarm_beta, float eps, void* stream) {
+    clear_error();
+    LOOM_CHECK(depth && doc && score_w && proj_w && up_w && a_out,
+               "decode_tria_readout: null argument");
+    LOOM_CHECK(!prev || reset_now, "decode_tria_readout: prev needs reset_now");
+    LOOM_CHECK(polarm_beta >= 0.0f && polarm_beta < 1.0f,
+               "PolARM beta must be finite and in [0, 1), got %g", (double)polarm_beta);
+    LOOM_CHECK(H >= 1 && N >= 1 && B >= 0 && N < ((int64_t)1 << 31),
+               "decode_tria_readout: bad shape B=%lld H=%lld N=%lld", (long long)B, (long long)H,
+               (long long)N);
+    LOOM_CHECK(((uintptr_t)up_w & 15) == 0, "decode_tria_readout: up weight must be 16-byte aligned");
+    if (B == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, readout_dispatch, depth, prev, reset_now, fire, doc, score_w, proj_w,
+                      proj_b, up_w, up_b, a_out, B, H, N, polarm_beta, eps, (hipStream_t)stream)
 }

@@ -151,8 +151,6 @@ class LoomDecoder:
         self.ln_ws = torch.empty((ln_ws + 3) // 4, dtype=torch.float32, device=dev)
         self.carry = z(2, B, H, 3, 3)
         self.p = z(2, B, H)
-        self.pooled = z(B, 9)
-        self.z32 = z(B, 32)
         self.a_t = z(B, N)
         self.stage_k = z(B, N)
         self.stage_v = z(B, N)
@@ -290,15 +288,13 @@ class LoomDecoder:
             else:
                 # the final-CA query of the last hidden state (tria.py:1580)
                 self._multi(("next", bi), self.h, [dict(w=self.wqk, out=self.q_ca)])
-        # ---- temporal carry + PolARM on fires (loomformer.py:4053-4085), in place
-        self._call("loom_tria_decode_temporal", self.code, _P(self.carry[carry_i]),
+        # ---- temporal carry + PolARM on fires (loomformer.py:4053-4085), in place,
+        # and the TriaAggregator readout of the new state (tria.py:1436-1441): one launch
+        self._call("loom_decode_tria_readout", self.code, _P(self.carry[carry_i]),
                    None if first else _P(self.doc), None if first else _P(self.reset_now),
-                   _P(self.fire), _P(self.doc), B, H, float(c.polarm_beta), 1e-6, st)
-        # ---- readout TriaAggregator (tria.py:1436-1441)
-        self._call("loom_slot_attention_pool_forward", self.code, _P(self.doc), _P(self.score_w),
-                   _P(self.pooled), None, B, H, st)
-        self._linear(self.pooled, self.proj_w, self.z32, B, 32, 9, bias=self.proj_b)
-        self._linear(self.z32, self.up_w, self.a_t, B, N, 32, bias=self.up_b)
+                   _P(self.fire), _P(self.doc), _P(self.score_w), _P(self.proj_w), _P(self.proj_b),
+                   _P(self.up_w), _P(self.up_b), _P(self.a_t), B, H, N, float(c.polarm_beta), 1e-6,
+                   st)
         # ---- final cross-attention step (tria.py:1560-1595): stage k/v, append on
         # fire (+ end-of-step bookkeeping), then attend over the appended keys
         self._multi("stage", self.a_t, [dict(w=self.wqk, out=self.stage_k),

@@ -298,16 +298,63 @@ def test_final_ca_strided_with_residual(dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_argmax_rows_first_index_on_ties(dtype):
+@pytest.mark.parametrize("V", [4096, 1000, 12000, 4097, 20000])
+def test_argmax_rows_first_index_on_ties(dtype, V):
+    # 4096 / 1000 / 12000: vector form (1, 1 and 8 vectors per thread); 4097, 20000: scalar form
     g = torch.Generator().manual_seed(5)
-    x = torch.randn(33, 4096, generator=g)
-    x[3, 100] = x[3, 4000] = 50.0           # tie: first index wins
+    x = torch.randn(33, V, generator=g)
+    x[3, 100] = x[3, V - 96] = 50.0         # tie: first index wins
     x[7, :] = 1.0                           # all equal -> 0
+    x[9, V - 1] = 60.0                      # maximum at the last index
     xd = x.to(DEV, dtype)
     ids = torch.empty(33, dtype=torch.int64, device=DEV)
-    L().call("loom_argmax_rows", code(xd), P(xd), 33, 4096, P(ids), S(xd))
+    L().call("loom_argmax_rows", code(xd), P(xd), 33, V, P(ids), S(xd))
     assert torch.equal(ids.cpu(), torch.argmax(host(xd), dim=-1))
-    assert int(ids[3]) == 100 and int(ids[7]) == 0
+    assert int(ids[3]) == 100 and int(ids[7]) == 0 and int(ids[9]) == V - 1
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("H,N", [(300, 96), (3072, 768), (1100, 40)])
+def test_decode_tria_readout(dtype, H, N):
+    # temporal step + PolARM + slot pool + proj + up in one launch, against the
+    # oracle ops with the intermediates rounded to dtype as the unfused ops store them
+    B = 4
+    g = torch.Generator().manual_seed(H + N)
+    depth = ref.local_normalize(torch.randn(B, H, 3, 3, generator=g)).to(DEV, dtype)
+    prev = ref.local_normalize(torch.randn(B, H, 3, 3, generator=g)).to(DEV, dtype)
+    key_w, query = torch.randn(32, 9, generator=g) * 1.5, torch.randn(32, generator=g)
+    sw = (torch.nn.functional.normalize(key_w.t() @ query, dim=0) * 2.0).to(DEV, dtype)
+    pw = (torch.randn(32, 9, generator=g) / 3).to(DEV, dtype)
+    pb = torch.randn(32, generator=g).to(DEV)
+    uw = (torch.randn(N, 32, generator=g) / 6).to(DEV, dtype)
+    ub = torch.randn(N, generator=g).to(DEV)
+    reset = torch.tensor([1, 0, 0, 1], dtype=torch.uint8)
+    fire = torch.tensor([0, 1, 0, 1], dtype=torch.uint8)
+    reset_d, fire_d = reset.to(DEV), fire.to(DEV)
+    rnd = lambda t: t.to(dtype).float()
+
+    def want(D, Pv):
+        doc = D if Pv is None else torch.where(reset.bool()[:, None, None, None], D,
+                                                ref.local_normalize(D @ Pv))
+        doc = torch.where(fire.bool()[:, None, None, None], ref.polarm(doc, 0.1), doc)
+        doc = rnd(doc)
+        pooled = rnd(ref.slot_attention_pool(doc, host(sw))[0])
+        z = rnd(pooled @ host(pw).t() + host(pb))
+        return doc, z @ host(uw).t() + host(ub)
+
+    doc = prev.clone()                      # in place: prev and doc are one buffer
+    a = torch.empty(B, N, device=DEV, dtype=dtype)
+    wd, wa = want(host(depth), host(prev))
+    L().call("loom_decode_tria_readout", code(depth), P(depth), P(doc), P(reset_d), P(fire_d),
+             P(doc), P(sw), P(pw), P(pb), P(uw), P(ub), P(a), B, H, N, 0.1, 1e-6, S(depth))
+    check(doc, wd, dtype)
+    check(a, wa, dtype)
+    # first token: no previous state (no reset flags needed)
+    wd, wa = want(host(depth), None)
+    L().call("loom_decode_tria_readout", code(depth), P(depth), None, None, P(fire_d), P(doc),
+             P(sw), P(pw), P(pb), P(uw), P(ub), P(a), B, H, N, 0.1, 1e-6, S(depth))
+    check(doc, wd, dtype)
+    check(a, wa, dtype)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
