@@ -468,6 +468,18 @@ int loom_decode_prologue(int64_t* ids, const int64_t* prompt, int64_t prompt_len
                          uint8_t* reset_now, int64_t carry_id, int64_t window, int64_t seq_len,
                          int64_t B, void* stream);
 
+/* loom_decode_prologue followed by the step's embedding lookup,
+ * h[b] = emb[ids[b]] (emb [V,N], h [B,N] dtype, both 16-byte aligned; ids
+ * outside [0, V) read row 0 or V-1: callers validate prompt ids, argmax ids are
+ * in range), one launch (nn.Embedding in Model.step, loomformer.py:3971).  No
+ * reference counterpart of its own. */
+int loom_decode_prologue_embed(int dtype, int64_t* ids, const int64_t* prompt, int64_t prompt_len,
+                               int64_t prompt_ld, int64_t* tokens, int64_t tokens_ld,
+                               const int64_t* pos_dev, const uint8_t* pending, uint8_t* fire,
+                               uint8_t* reset_now, int64_t carry_id, int64_t window,
+                               int64_t seq_len, const void* emb, void* h, int64_t N, int64_t V,
+                               int64_t B, void* stream);
+
 /* Greedy pick ids[r] = argmax_v logits[r, v] (first index on ties, as
  * torch.argmax), the `argmax(logits)` of infer (loomformer.py:5306).
  * logits: [rows, V] dtype; ids: [rows] int64. */

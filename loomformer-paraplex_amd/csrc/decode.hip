@@ -1266,6 +1266,45 @@ __global__ void decode_prologue_kernel(int64_t* __restrict__ ids, const int64_t*
     reset_now[b] = pending[b];
 }
 
+// decode_prologue_kernel for row b (one block per row) followed by the
+// embedding lookup of the step's token: h[b] = emb[ids[b]] (rows of N
+// elements, copied as 16-byte pieces when N * sizeof(T) % 16 == 0).
+template <typename T>
+__global__ void __launch_bounds__(128)
+decode_prologue_embed_kernel(int64_t* __restrict__ ids, const int64_t* __restrict__ prompt,
+                             int64_t prompt_len, int64_t prompt_ld, int64_t* __restrict__ tokens,
+                             int64_t tokens_ld, const int64_t* __restrict__ pos_dev,
+                             const uint8_t* __restrict__ pending, uint8_t* __restrict__ fire,
+                             uint8_t* __restrict__ reset_now, int64_t carry_id, int64_t window,
+                             int64_t seq_len, const T* __restrict__ emb, T* __restrict__ h,
+                             int64_t N, int64_t V) {
+    __shared__ int64_t s_id;
+    const int64_t b = blockIdx.x;
+    if (threadIdx.x == 0) {
+        const int64_t pos = *pos_dev;
+        int64_t id = ids[b];
+        if (prompt != nullptr && pos < prompt_len) {
+            id = prompt[b * prompt_ld + pos];
+            ids[b] = id;
+        }
+        if (tokens != nullptr) tokens[b * tokens_ld + pos] = id;
+        const bool hard = (pos + 1 < seq_len) && ((pos + 1) % window == 0);
+        fire[b] = (hard || (carry_id >= 0 && id == carry_id)) ? 1 : 0;
+        reset_now[b] = pending[b];
+        s_id = id < 0 ? 0 : (id >= V ? V - 1 : id);   // out-of-vocabulary ids read a valid row
+    }
+    __syncthreads();
+    const T* src = emb + s_id * N;
+    T* dst = h + b * N;
+    if ((N * (int64_t)sizeof(T)) % 16 == 0) {
+        const int64_t nv = N * (int64_t)sizeof(T) / 16;
+        for (int64_t i = threadIdx.x; i < nv; i += blockDim.x)
+            reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+    } else {
+        for (int64_t i = threadIdx.x; i < N; i += blockDim.x) dst[i] = src[i];
+    }
+}
+
 // Final-CA key append (tria.py:1576-1582) and end-of-step bookkeeping: if any
 // row fires, the staged keys/values of every row are stored at slot ca_len and
 // marked valid where that row fired; then pending = fire and pos += 1.
@@ -1417,6 +1456,39 @@ extern "C" int loom_decode_prologue(int64_t* ids, const int64_t* prompt, int64_t
                        (hipStream_t)stream, ids, prompt, prompt_len, prompt_ld, tokens, tokens_ld,
                        pos_dev, pending, fire, reset_now, carry_id, window, seq_len, B);
     return launch_status("loom_decode_prologue");
+}
+
+template <typename T>
+static int prologue_embed_dispatch(int64_t* ids, const int64_t* prompt, int64_t prompt_len,
+                                   int64_t prompt_ld, int64_t* tokens, int64_t tokens_ld,
+                                   const int64_t* pos_dev, const uint8_t* pending, uint8_t* fire,
+                                   uint8_t* reset_now, int64_t carry_id, int64_t window,
+                                   int64_t seq_len, const void* emb, void* h, int64_t N, int64_t V,
+                                   int64_t B, hipStream_t st) {
+    hipLaunchKernelGGL((decode_prologue_embed_kernel<T>), dim3((unsigned)B), dim3(128), 0, st, ids,
+                       prompt, prompt_len, prompt_ld, tokens, tokens_ld, pos_dev, pending, fire,
+                       reset_now, carry_id, window, seq_len, (const T*)emb, (T*)h, N, V);
+    return launch_status("loom_decode_prologue_embed");
+}
+
+extern "C" int loom_decode_prologue_embed(int dtype, int64_t* ids, const int64_t* prompt,
+                                          int64_t prompt_len, int64_t prompt_ld, int64_t* tokens,
+                                          int64_t tokens_ld, const int64_t* pos_dev,
+                                          const uint8_t* pending, uint8_t* fire,
+                                          uint8_t* reset_now, int64_t carry_id, int64_t window,
+                                          int64_t seq_len, const void* emb, void* h, int64_t N,
+                                          int64_t V, int64_t B, void* stream) {
+    clear_error();
+    LOOM_CHECK(ids && pos_dev && pending && fire && reset_now && emb && h,
+               "decode_prologue_embed: null argument");
+    LOOM_CHECK(window >= 1 && B >= 0 && N >= 1 && V >= 1, "decode_prologue_embed: bad shape");
+    LOOM_CHECK(!prompt || prompt_ld >= prompt_len, "decode_prologue_embed: prompt row stride < length");
+    LOOM_CHECK((((uintptr_t)emb | (uintptr_t)h) & 15) == 0,
+               "decode_prologue_embed: emb and h must be 16-byte aligned");
+    if (B == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, prologue_embed_dispatch, ids, prompt, prompt_len, prompt_ld, tokens,
+                      tokens_ld, pos_dev, pending, fire, reset_now, carry_id, window, seq_len, emb,
+                      h, N, V, B, (hipStream_t)stream)
 }
 
 extern "C" int loom_argmax_rows(int dtype, const void* logits, int64_t rows, int64_t V,

@@ -48,10 +48,9 @@ __device__ __forceinline__ void softplus_gate(float x, float m, float& amp, floa
     amp = __builtin_amdgcn_fmed3f(x, a0, 3.0e38f);   // max(x, a0) without a NaN-quieting pass
     const float safe = __builtin_amdgcn_fmed3f(amp, 1.0e-12f, 3.0e38f);
     const float d1 = fsqrt(safe) + 1.0f;
-    const float den = 1.0f + u;
-    const float r = frcp(d1 * den);
-    const float expo = m * den * r;     // m / (sqrt(A) + 1)
-    const float sig = u * d1 * r;       // sigmoid(A)
+    const float r = frcp(fmaf(d1, u, d1));   // 1 / ((sqrt A + 1)(1 + u))
+    const float expo = fmaf(m, u, m) * r;     // m (1 + u) r = m / (sqrt(A) + 1)
+    const float sig = u * d1 * r;             // sigmoid(A)
     gate = __builtin_amdgcn_exp2f(expo * flog2(safe)) * sig;
 }
 

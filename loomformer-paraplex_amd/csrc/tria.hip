@@ -470,6 +470,131 @@ final_ca_vec_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
         lse[row] = red[0] == -INFINITY ? -INFINITY : red[0] + logf(red[1]);
 }
 
+// Short key lists (16-bit types, K <= kCaRowKeys, D % 8 == 0, D <= 1024): every load of the
+// row is issued before any arithmetic, so the row costs one memory round trip.
+// 512 threads.  Scores: wave w holds keys w + 8i (lane l: 8-element chunks l
+// and l + 64 of q and of each key).  P.V: thread t takes chunk t % 128 for the
+// keys t/128 + 4i; its value rows are loaded together with the keys, and the
+// four key subsets are summed through LDS.
+constexpr int kCaRowKeys = 64;
+
+// eight 16-bit elements held as one 16-byte word, to fp32
+template <typename T>
+__device__ __forceinline__ void unpack8(const uint4 w, float v[8]) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const T lo{(uint16_t)(u[k] & 0xffffu)}, hi{(uint16_t)(u[k] >> 16)};
+        v[2 * k] = ld(&lo);
+        v[2 * k + 1] = ld(&hi);
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(512)
+final_ca_row_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+                    int64_t kv_stride_b, const uint8_t* __restrict__ allowed,
+                    int64_t allowed_stride, const T* __restrict__ residual, float gamma,
+                    T* __restrict__ out, float* __restrict__ lse, int64_t T_, int64_t K,
+                    const int64_t* __restrict__ k_dev, int D, float scale) {
+    constexpr int KW = kCaRowKeys / 8, KS = kCaRowKeys / 4;
+    __shared__ float wts[kCaRowKeys];
+    __shared__ float part[4][128][9];      // [subset][chunk][8] (+1: bank spread)
+    __shared__ float red[2];
+    if (k_dev != nullptr) K = *k_dev < K ? *k_dev : K;
+    const int64_t row = blockIdx.x;
+    const int64_t b = row / T_;
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int nch = D / 8;
+    const T* kb = k + b * kv_stride_b;
+    const T* vb = v + b * kv_stride_b;
+    // every load first: q and key chunks for the scores, value chunks for P.V
+    float qf[2][8];
+    uint4 kr[KW][2], vr[KS];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int ch = lane + 64 * c;
+        if (ch < nch) {
+            Vec8<T>::load(q + row * D + ch * 8, qf[c]);
+#pragma unroll
+            for (int i = 0; i < KW; ++i) {
+                const int64_t j = wid + 8 * i;
+                if (j < K) kr[i][c] = *reinterpret_cast<const uint4*>(kb + j * D + ch * 8);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) qf[c][e] = 0.0f;
+        }
+    }
+    const int c2 = tid & 127, s2 = tid >> 7;
+    if (c2 < nch) {
+#pragma unroll
+        for (int i = 0; i < KS; ++i) {
+            const int64_t j = s2 + 4 * i;
+            if (j < K) vr[i] = *reinterpret_cast<const uint4*>(vb + j * D + c2 * 8);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < KW; ++i) {
+        const int64_t j = wid + 8 * i;
+        float dot = 0.0f;
+        if (j < K) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                if (lane + 64 * c >= nch) continue;
+                float kv[8];
+                unpack8<T>(kr[i][c], kv);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) dot = fmaf(qf[c][e], kv[e], dot);
+            }
+        }
+        const float sc = wave_sum(dot) * scale;
+        if (lane == 0 && j < K) wts[j] = allowed[row * allowed_stride + j] ? sc : -INFINITY;
+    }
+    __syncthreads();
+    if (wid == 0) {
+        const float sv = lane < K ? wts[lane] : -INFINITY;
+        const float mx = wave_max(sv);
+        const float e = (mx == -INFINITY || sv == -INFINITY) ? 0.0f : fexp(sv - mx);
+        const float sum = wave_sum(e);
+        if (lane < K) wts[lane] = sum > 0.0f ? e / sum : 0.0f;
+        if (lane == 0) {
+            red[0] = mx;
+            red[1] = sum;
+        }
+    }
+    __syncthreads();
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (c2 < nch) {
+#pragma unroll
+        for (int i = 0; i < KS; ++i) {
+            const int64_t j = s2 + 4 * i;
+            if (j >= K) continue;
+            float vv[8];
+            unpack8<T>(vr[i], vv);
+            const float w = wts[j];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = fmaf(w, vv[e], a[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part[s2][c2][e] = a[e];
+    }
+    __syncthreads();
+    if (tid < nch) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = part[0][tid][e] + part[1][tid][e] + part[2][tid][e] + part[3][tid][e];
+        if (residual != nullptr) {
+            float rr[8];
+            Vec8<T>::load(residual + row * D + tid * 8, rr);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = rr[e] + gamma * a[e];
+        }
+        Vec8<T>::store(out + row * D + tid * 8, a);
+    }
+    if (lse != nullptr && tid == 0)
+        lse[row] = red[0] == -INFINITY ? -INFINITY : red[0] + logf(red[1]);
+}
+
 // ---------------------------------------------------------------- dispatch
 
 template <typename T>
@@ -556,6 +681,15 @@ static int final_ca_dispatch(const void* q, const void* k, const void* v, int64_
     const bool vec = D % 8 == 0 && D <= kCaChunks * 64 * 8 && kv_stride_b % 8 == 0 &&
                      (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out |
                        (uintptr_t)residual) & 15) == 0;
+    if constexpr (sizeof(T) == 2) {
+        if (vec && K <= kCaRowKeys && D <= 1024) {
+            hipLaunchKernelGGL((final_ca_row_kernel<T>), dim3((unsigned)(B * T_)), dim3(512), 0, st,
+                               (const T*)q, (const T*)k, (const T*)v, kv_stride_b, allowed,
+                               allowed_stride, (const T*)residual, gamma, (T*)out, lse, T_, K,
+                               k_dev, (int)D, scale);
+            return launch_status("loom_final_ca_sparse_forward");
+        }
+    }
     if (vec)
         hipLaunchKernelGGL((final_ca_vec_kernel<T>), dim3((unsigned)(B * T_)), dim3(256), 0, st,
                            (const T*)q, (const T*)k, (const T*)v, kv_stride_b, allowed,

@@ -76,6 +76,8 @@ SIGNATURES = {
                                    _P],
     "loom_decode_prologue": [_P, _P, c_int64, c_int64, _P, c_int64, _P, _P, _P, _P, c_int64,
                              c_int64, c_int64, c_int64, _P],
+    "loom_decode_prologue_embed": [c_int, _P, _P, c_int64, c_int64, _P, c_int64, _P, _P, _P, _P,
+                                   c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, _P],
     "loom_decode_epilogue": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64,
                              _P],
     "loom_argmax_rows": [c_int, _P, c_int64, c_int64, _P, _P],

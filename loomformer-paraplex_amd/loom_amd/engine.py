@@ -211,11 +211,12 @@ class LoomDecoder:
         c, B, N, H, L = self.cfg, self.B, self.cfg.N, self.cfg.H, self.cfg.L
         st = self._stream()
         carry_id = -1 if self.carry_token_id is None else int(self.carry_token_id)
-        self._call("loom_decode_prologue", _P(self.ids),
+        # token ids, fire / reset flags and the embedding row of this step, one launch
+        self._call("loom_decode_prologue_embed", self.code, _P(self.ids),
                    _P(self.prompt_buf) if prompt_len > 0 else None, prompt_len, self.max_len,
                    _P(self.tokens), self.max_len, _P(self.pos_dev), _P(self.pending), _P(self.fire),
-                   _P(self.reset_now), carry_id, c.window, c.seq_len, B, st)
-        torch.index_select(self.emb, 0, self.ids, out=self.h)
+                   _P(self.reset_now), carry_id, c.window, c.seq_len, _P(self.emb), _P(self.h), N,
+                   c.V, B, st)
         hist = self.hist
         # depth history slot 0 = DepthAttn.project(h) (loomformer.py:3973), with
         # layer 0's qkv projection of the same h in the same launch
@@ -321,6 +322,11 @@ class LoomDecoder:
                    _P(self.hist[:, :, N:]), hist_bt, 2 * N, _P(out), None, None, self.B, sub + 1,
                    c.QH, c.HD, self._stream())
 
+    def _check_ids(self, ids: torch.Tensor) -> None:
+        """Token ids must index the embedding table (nn.Embedding raises otherwise)."""
+        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= self.cfg.V):
+            raise ValueError(f"token ids must lie in [0, {self.cfg.V})")
+
     def _check_capacity(self, pos: int) -> None:
         if pos >= self.max_len:
             raise ValueError(f"generation exceeded seq_len={self.max_len}; no wraparound support")
@@ -338,6 +344,7 @@ class LoomDecoder:
         if pos != self.pos:
             raise ValueError(f"step expects position {self.pos}, got {pos}")
         self._check_capacity(pos)
+        self._check_ids(ids)
         self.ids.copy_(ids.to(self.dev).view(-1))
         self._launch_step(first=pos == 0, prompt_len=0)
         self.pos = pos + 1
@@ -383,6 +390,7 @@ class LoomDecoder:
             first_pos = P
         else:
             self.reset()
+            self._check_ids(prompt)
             self.prompt_buf[:, :P].copy_(prompt.to(self.dev))
             self._launch_step(first=True, prompt_len=P)
             first_pos = 1
@@ -410,6 +418,7 @@ class LoomDecoder:
         if B != self.B or P < 1:
             raise ValueError("prompt must be [batch, >=1]")
         self.reset()
+        self._check_ids(prompt)
         self.prompt_buf[:, :P].copy_(prompt.to(self.dev))
         self._prompt_len = P
         self._launch_step(first=True, prompt_len=P)

@@ -51,6 +51,7 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     if B != eng.B or P < 1:
         raise ValueError("prompt must be [batch, >=1]")
     eng._check_capacity(P - 1)
+    eng._check_ids(prompt)
     N, H, L, QH, KVH, HD = c.N, c.H, c.L, c.QH, c.KVH, c.HD
     dev, dt, code = eng.dev, eng.dtype, eng.code
     st = eng._stream()

@@ -485,3 +485,33 @@ def test_linear_ln(dtype, M, K2):
         pre = pre + host(x2) @ host(w2).T
     want = torch.nn.functional.layer_norm(pre, (N,), host(gam), host(bet), 1e-5)
     check(out, want, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_decode_prologue_embed(dtype):
+    # ids from the prompt while pos < prompt_len, else the caller's ids; fire on a
+    # hard boundary or the carry id; reset_now = pending; h = emb[ids]
+    B, V, N, W = 5, 50, 40, 4
+    g = torch.Generator().manual_seed(9)
+    emb = torch.randn(V, N, generator=g).to(DEV, dtype)
+    prompt = torch.randint(0, V, (B, 6), generator=g)
+    prompt[2, 3] = 7                          # carry id at pos 3 in row 2
+    prompt_d = prompt.to(DEV)
+    pending = torch.tensor([1, 0, 1, 0, 0], dtype=torch.uint8, device=DEV)
+    for pos, from_prompt in ((3, True), (7, False)):
+        ids = torch.randint(0, V, (B,), generator=g).to(DEV)
+        ids0 = ids.clone()
+        tokens = torch.zeros(B, 10, dtype=torch.int64, device=DEV)
+        fire = torch.empty(B, dtype=torch.uint8, device=DEV)
+        reset = torch.empty(B, dtype=torch.uint8, device=DEV)
+        h = torch.empty(B, N, device=DEV, dtype=dtype)
+        pos_d = torch.tensor([pos], dtype=torch.int64, device=DEV)
+        L().call("loom_decode_prologue_embed", code(h), P(ids), P(prompt_d), 6, 6, P(tokens), 10,
+                 P(pos_d), P(pending), P(fire), P(reset), 7, W, 100, P(emb), P(h), N, V, B, S(h))
+        want_ids = prompt[:, pos] if from_prompt else ids0.cpu()
+        assert torch.equal(ids.cpu(), want_ids)
+        assert torch.equal(tokens[:, pos].cpu(), want_ids)
+        hard = (pos + 1) % W == 0
+        assert torch.equal(fire.cpu().bool(), torch.tensor(hard) | (want_ids == 7))
+        assert torch.equal(reset.cpu(), pending.cpu())
+        assert torch.equal(h.cpu(), emb.cpu()[want_ids])
