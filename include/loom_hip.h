@@ -436,22 +436,26 @@ int loom_tria_decode_temporal(int dtype, const void* depth, const void* prev,
                               const uint8_t* reset_now, const uint8_t* fire, void* out,
                               int64_t B, int64_t H, float polarm_beta, float eps, void* stream);
 
-/* The per-token Tria tail of a decode step in one launch (one block per
- * batch row): the loom_tria_decode_temporal update of every head, stored in
- * doc (doc may equal prev: each head's previous state is read before it is
- * written), then the readout of the stored state, TriaAggregator.forward
- * (tria.py:1436-1441): pooled = slot attention pool over H with score_w
- * (tria.py:1351-1389), z = pooled @ proj_w^T + proj_b (proj_w [32,9]),
- * a_out[b] = z @ up_w^T + up_b (up_w [N,32], 16-byte aligned).  pooled and z
- * are rounded to dtype between the steps as the separate ops store them.
- * proj_b, up_b: fp32 or NULL.  H <= 4096.  Replaces loom_tria_decode_temporal +
- * loom_slot_attention_pool_forward + two loom_linear calls in Model.step
- * (loomformer.py:4053-4085); no reference counterpart of its own. */
+/* The per-token Tria tail of a decode step: the loom_tria_decode_temporal
+ * update of every head, stored in doc (doc may equal prev: each head's
+ * previous state is read before it is written), then the readout of the
+ * stored state, TriaAggregator.forward (tria.py:1436-1441): pooled = slot
+ * attention pool over H with score_w (tria.py:1351-1389), z = pooled @
+ * proj_w^T + proj_b (proj_w [32,9]), a_out[b] = z @ up_w^T + up_b (up_w [N,32],
+ * 16-byte aligned).  pooled and z are rounded to dtype between the steps as the
+ * separate ops store them.  proj_b, up_b: fp32 or NULL.  H <= 32768.
+ * workspace: fp32 scratch of loom_decode_tria_readout_workspace_bytes(B, H)
+ * bytes (per-block pool records); two launches on stream.  Replaces
+ * loom_tria_decode_temporal + loom_slot_attention_pool_forward + two
+ * loom_linear calls in Model.step (loomformer.py:4053-4085); no reference
+ * counterpart of its own. */
+int64_t loom_decode_tria_readout_workspace_bytes(int64_t B, int64_t H);
 int loom_decode_tria_readout(int dtype, const void* depth, const void* prev,
                              const uint8_t* reset_now, const uint8_t* fire, void* doc,
                              const void* score_w, const void* proj_w, const float* proj_b,
-                             const void* up_w, const float* up_b, void* a_out, int64_t B,
-                             int64_t H, int64_t N, float polarm_beta, float eps, void* stream);
+                             const void* up_w, const float* up_b, void* a_out, float* workspace,
+                             int64_t workspace_bytes, int64_t B, int64_t H, int64_t N,
+                             float polarm_beta, float eps, void* stream);
 
 /* Start of a decode step with device-resident state (pos = *pos_dev), so a
  * whole step is a fixed launch sequence that a HIP graph can replay.  Token

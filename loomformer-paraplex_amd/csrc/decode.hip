@@ -810,72 +810,59 @@ decode_temporal_kernel(const T* __restrict__ depth, const T* __restrict__ prev,
     for (int k = 0; k < 9; ++k) st(out + e * 9 + k, M[k]);
 }
 
-// The whole per-token Tria tail of a decode step, one block per batch row b
-// (thread t owns heads h = t + kReadThreads*i, i < IT):
-//   the temporal step and PolARM of every head (temporal_head), stored as
-//   the new document state doc[b] (in place: a thread reads its own heads'
-//   previous state before it writes them);
-//   the slot attention pool of the stored state over h (tria.py:1351-1389):
-//   softmax_h <score_w, vec C_h>, pooled = sum_h softmax * vec C_h (natural
-//   exponentials, online per thread, merged over the block);
-//   proj Linear(9, 32) and up Linear(32, N) of the pooled row (tria.py:
-//   1436-1441).  Every intermediate the unfused ops store (doc, pooled, z) is
-//   rounded to T before it is used, as they would read it back.
-constexpr int kReadThreads = 1024;
+// The per-token Tria tail of a decode step, in two launches spread over the
+// chip (one CU streams its share far slower than the whole device, so a
+// launch with one block per batch row would be bound by 32 CUs):
+//   decode_readout_heads_kernel, grid (H / kReadHeads, B), one thread per head:
+//     the temporal step and PolARM (temporal_head), stored as the new document
+//     state doc[b, h] (in place: each thread reads its head's previous state
+//     before it writes it); then this block's part of the slot attention pool
+//     over h (tria.py:1351-1389), an online-softmax record (m, l, sum p vec C)
+//     of <score_w, vec C_h> over the stored (rounded) state, natural exponentials;
+//   decode_readout_rows_kernel, grid (N / kReadCols, B): merges row b's
+//     records into pooled, then proj Linear(9, 32) and kReadCols outputs of up
+//     Linear(32, N) (tria.py:1436-1441).
+// pooled and z are rounded to T before use, as the unfused ops store them.
+constexpr int kReadHeads = 256;
+constexpr int kReadCols = 128;
+constexpr int kReadRec = 11;           // m, l, acc[9]
 
-template <typename T, int IT>
-__global__ void __launch_bounds__(kReadThreads)
-decode_readout_kernel(const T* __restrict__ depth, const T* prev, const uint8_t* __restrict__ reset_now,
-                      const uint8_t* __restrict__ fire, T* doc, const T* __restrict__ score_w,
-                      const T* __restrict__ proj_w, const float* __restrict__ proj_b,
-                      const T* __restrict__ up_w, const float* __restrict__ up_b,
-                      T* __restrict__ a_out, int H, int N, float beta, float eps) {
-    __shared__ float red[kReadThreads / 64][11];
-    __shared__ float xs[9];
-    __shared__ float zs[32];
+template <typename T>
+__global__ void __launch_bounds__(kReadHeads)
+decode_readout_heads_kernel(const T* __restrict__ depth, const T* prev,
+                            const uint8_t* __restrict__ reset_now, const uint8_t* __restrict__ fire,
+                            T* doc, const T* __restrict__ score_w, float* __restrict__ rec, int H,
+                            float beta, float eps) {
+    __shared__ float red[kReadHeads / 64][kReadRec];
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int64_t b = blockIdx.x;
+    const int64_t b = blockIdx.y;
+    const int h = blockIdx.x * kReadHeads + tid;
     const bool cont = prev != nullptr && reset_now[b] == 0;
     const bool fires = fire != nullptr && fire[b] != 0;
-    const int64_t base = b * H * 9;
-    float M[IT][9], P[IT][9];
+    const int64_t e = (b * H + h) * 9;
+    float M[9], P[9], sw[9];
 #pragma unroll
-    for (int i = 0; i < IT; ++i) {
-        const int h = tid + kReadThreads * i;
-#pragma unroll
-        for (int k = 0; k < 9; ++k) {
-            M[i][k] = h < H ? ld(depth + base + h * 9 + k) : 0.0f;
-            P[i][k] = (cont && h < H) ? ld(prev + base + h * 9 + k) : 0.0f;
-        }
+    for (int k = 0; k < 9; ++k) {
+        M[k] = h < H ? ld(depth + e + k) : 0.0f;
+        P[k] = (cont && h < H) ? ld(prev + e + k) : 0.0f;
+        sw[k] = ld(score_w + k);
     }
-    float sw[9];
-#pragma unroll
-    for (int k = 0; k < 9; ++k) sw[k] = ld(score_w + k);
     float m = -INFINITY, l = 0.0f, acc[9];
 #pragma unroll
     for (int k = 0; k < 9; ++k) acc[k] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < IT; ++i) {
-        const int h = tid + kReadThreads * i;
-        if (h >= H) continue;
-        temporal_head(M[i], P[i], cont, fires, beta, eps);
+    if (h < H) {
+        temporal_head(M, P, cont, fires, beta, eps);
         float sc = 0.0f;
 #pragma unroll
         for (int k = 0; k < 9; ++k) {
-            T* slot = doc + base + h * 9 + k;
-            st(slot, M[i][k]);
             T rounded;
-            st(&rounded, M[i][k]);
-            M[i][k] = ld(&rounded);
-            sc = fmaf(M[i][k], sw[k], sc);
+            st(&rounded, M[k]);
+            doc[e + k] = rounded;
+            acc[k] = ld(&rounded);
+            sc = fmaf(acc[k], sw[k], sc);
         }
-        const float mn = fmaxf(m, sc);
-        const float corr = expf(m - mn);
-        const float pe = expf(sc - mn);
-        l = l * corr + pe;
-#pragma unroll
-        for (int k = 0; k < 9; ++k) acc[k] = fmaf(pe, M[i][k], acc[k] * corr);
-        m = mn;
+        m = sc;
+        l = 1.0f;                          // one head: p = e^(sc - m) = 1
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -899,15 +886,59 @@ decode_readout_kernel(const T* __restrict__ depth, const T* prev, const uint8_t*
         for (int k = 0; k < 9; ++k) red[wid][2 + k] = acc[k];
     }
     __syncthreads();
+    if (tid < kReadRec) {
+        float Mx = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < kReadHeads / 64; ++q) Mx = fmaxf(Mx, red[q][0]);
+        float v = 0.0f;
+        if (tid == 0) {
+            v = Mx;
+        } else {
+#pragma unroll
+            for (int q = 0; q < kReadHeads / 64; ++q)
+                if (red[q][0] != -INFINITY) v = fmaf(red[q][tid], expf(red[q][0] - Mx), v);
+        }
+        rec[(b * gridDim.x + blockIdx.x) * kReadRec + tid] = v;
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kReadCols)
+decode_readout_rows_kernel(const float* __restrict__ rec, int nrec, const T* __restrict__ proj_w,
+                           const float* __restrict__ proj_b, const T* __restrict__ up_w,
+                           const float* __restrict__ up_b, T* __restrict__ a_out, int N) {
+    constexpr int kMaxRec = kReadCols;     // records per row (H <= kReadHeads * kReadCols)
+    __shared__ float rs[kMaxRec * kReadRec];
+    __shared__ float xs[9];
+    __shared__ float zs[32];
+    const int tid = threadIdx.x;
+    const int64_t b = blockIdx.y;
+    const int n = blockIdx.x * kReadCols + tid;
+    // every load first: this row's records, the proj row of thread tid < 32 and
+    // the up row of column n
+    const float* rb = rec + b * nrec * kReadRec;
+    for (int i = tid; i < nrec * kReadRec; i += kReadCols) rs[i] = rb[i];
+    float pw[9], uw[32];
+    float pbias = 0.0f, ubias = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) pw[k] = tid < 32 ? ld(proj_w + tid * 9 + k) : 0.0f;
+    if (tid < 32 && proj_b != nullptr) pbias = proj_b[tid];
+    if (n < N) {
+#pragma unroll
+        for (int j = 0; j < 32; j += 8) Vec8<T>::load(up_w + (int64_t)n * 32 + j, uw + j);
+        if (up_b != nullptr) ubias = up_b[n];
+    }
+    __syncthreads();
     if (tid < 9) {
         float Mx = -INFINITY;
-        for (int q = 0; q < kReadThreads / 64; ++q) Mx = fmaxf(Mx, red[q][0]);
+        for (int r = 0; r < nrec; ++r) Mx = fmaxf(Mx, rs[r * kReadRec]);
         float L = 0.0f, A = 0.0f;
-        for (int q = 0; q < kReadThreads / 64; ++q) {
-            if (red[q][0] == -INFINITY) continue;
-            const float c = expf(red[q][0] - Mx);
-            L = fmaf(red[q][1], c, L);
-            A = fmaf(red[q][2 + tid], c, A);
+        for (int r = 0; r < nrec; ++r) {
+            const float* q = rs + r * kReadRec;
+            if (q[0] == -INFINITY) continue;
+            const float c = expf(q[0] - Mx);
+            L = fmaf(q[1], c, L);
+            A = fmaf(q[2 + tid], c, A);
         }
         T pooled;
         st(&pooled, A * (1.0f / L));
@@ -915,21 +946,18 @@ decode_readout_kernel(const T* __restrict__ depth, const T* prev, const uint8_t*
     }
     __syncthreads();
     if (tid < 32) {
-        float z = proj_b != nullptr ? proj_b[tid] : 0.0f;
+        float z = pbias;
 #pragma unroll
-        for (int k = 0; k < 9; ++k) z = fmaf(ld(proj_w + tid * 9 + k), xs[k], z);
+        for (int k = 0; k < 9; ++k) z = fmaf(pw[k], xs[k], z);
         T zr;
         st(&zr, z);
         zs[tid] = ld(&zr);
     }
     __syncthreads();
-    for (int n = tid; n < N; n += kReadThreads) {
-        float a = up_b != nullptr ? up_b[n] : 0.0f;
-        float w[32];
+    if (n < N) {
+        float a = ubias;
 #pragma unroll
-        for (int j = 0; j < 32; j += 8) Vec8<T>::load(up_w + (int64_t)n * 32 + j, w + j);
-#pragma unroll
-        for (int j = 0; j < 32; ++j) a = fmaf(w[j], zs[j], a);
+        for (int j = 0; j < 32; ++j) a = fmaf(uw[j], zs[j], a);
         st(a_out + b * N + n, a);
     }
 }
@@ -1090,19 +1118,18 @@ template <typename T>
 static int readout_dispatch(const void* depth, const void* prev, const uint8_t* reset_now,
                             const uint8_t* fire, void* doc, const void* score_w, const void* proj_w,
                             const float* proj_b, const void* up_w, const float* up_b, void* a_out,
-                            int64_t B, int64_t H, int64_t N, float beta, float eps, hipStream_t st) {
-#define LOOM_READOUT(IT)                                                                         \
-    if (H <= (int64_t)(IT) * kReadThreads) {                                                     \
-        hipLaunchKernelGGL((decode_readout_kernel<T, IT>), dim3((unsigned)B), dim3(kReadThreads), \
-                           0, st, (const T*)depth, (const T*)prev, reset_now, fire, (T*)doc,       \
-                           (const T*)score_w, (const T*)proj_w, proj_b, (const T*)up_w, up_b,      \
-                           (T*)a_out, (int)H, (int)N, beta, eps);                                \
-        return launch_status("loom_decode_tria_readout");                                        \
-    }
-    LOOM_READOUT(1) LOOM_READOUT(2) LOOM_READOUT(3) LOOM_READOUT(4)
-#undef LOOM_READOUT
-    set_error("decode_tria_readout: H=%lld above %d", (long long)H, 4 * kReadThreads);
-    return LOOM_ERR_INVALID;
+                            float* ws, int64_t B, int64_t H, int64_t N, float beta, float eps,
+                            hipStream_t st) {
+    const int nrec = (int)ceil_div(H, kReadHeads);
+    hipLaunchKernelGGL((decode_readout_heads_kernel<T>), dim3((unsigned)nrec, (unsigned)B),
+                       dim3(kReadHeads), 0, st, (const T*)depth, (const T*)prev, reset_now, fire,
+                       (T*)doc, (const T*)score_w, ws, (int)H, beta, eps);
+    int rc = launch_status("loom_decode_tria_readout");
+    if (rc != LOOM_OK) return rc;
+    hipLaunchKernelGGL((decode_readout_rows_kernel<T>), dim3((unsigned)ceil_div(N, kReadCols), (unsigned)B),
+                       dim3(kReadCols), 0, st, ws, nrec, (const T*)proj_w, proj_b, (const T*)up_w,
+                       up_b, (T*)a_out, (int)N);
+    return launch_status("loom_decode_tria_readout");
 }
 
 #define LOOM_DTYPE_SWITCH(dtype, FN, ...)               \
@@ -1535,23 +1562,33 @@ extern "C" int loom_tria_decode_temporal(int dtype, const void* depth, const voi
                       polarm_beta, eps, (hipStream_t)stream)
 }
 
+extern "C" int64_t loom_decode_tria_readout_workspace_bytes(int64_t B, int64_t H) {
+    return B * ceil_div(H, kReadHeads) * kReadRec * (int64_t)sizeof(float);
+}
+
 extern "C" int loom_decode_tria_readout(int dtype, const void* depth, const void* prev,
                                         const uint8_t* reset_now, const uint8_t* fire, void* doc,
                                         const void* score_w, const void* proj_w,
                                         const float* proj_b, const void* up_w, const float* up_b,
-                                        void* a_out, int64_t B, int64_t H, int64_t N,
-                                        float polarm_beta, float eps, void* stream) {
+                                        void* a_out, float* workspace, int64_t workspace_bytes,
+                                        int64_t B, int64_t H, int64_t N, float polarm_beta,
+                                        float eps, void* stream) {
     clear_error();
-    LOOM_CHECK(depth && doc && score_w && proj_w && up_w && a_out,
+    LOOM_CHECK(depth && doc && score_w && proj_w && up_w && a_out && workspace,
                "decode_tria_readout: null argument");
     LOOM_CHECK(!prev || reset_now, "decode_tria_readout: prev needs reset_now");
     LOOM_CHECK(polarm_beta >= 0.0f && polarm_beta < 1.0f,
                "PolARM beta must be finite and in [0, 1), got %g", (double)polarm_beta);
-    LOOM_CHECK(H >= 1 && N >= 1 && B >= 0 && N < ((int64_t)1 << 31),
-               "decode_tria_readout: bad shape B=%lld H=%lld N=%lld", (long long)B, (long long)H,
-               (long long)N);
+    LOOM_CHECK(H >= 1 && H <= (int64_t)kReadHeads * kReadCols && N >= 1 && B >= 0 &&
+                   N < ((int64_t)1 << 31) && B < 65536,
+               "decode_tria_readout: bad shape B=%lld H=%lld N=%lld (H <= %d)", (long long)B,
+               (long long)H, (long long)N, kReadHeads * kReadCols);
     LOOM_CHECK(((uintptr_t)up_w & 15) == 0, "decode_tria_readout: up weight must be 16-byte aligned");
+    LOOM_CHECK(workspace_bytes >= loom_decode_tria_readout_workspace_bytes(B, H),
+               "decode_tria_readout: workspace of %lld bytes, %lld needed", (long long)workspace_bytes,
+               (long long)loom_decode_tria_readout_workspace_bytes(B, H));
     if (B == 0) return LOOM_OK;
     LOOM_DTYPE_SWITCH(dtype, readout_dispatch, depth, prev, reset_now, fire, doc, score_w, proj_w,
-                      proj_b, up_w, up_b, a_out, B, H, N, polarm_beta, eps, (hipStream_t)stream)
+                      proj_b, up_w, up_b, a_out, workspace, B, H, N, polarm_beta, eps,
+                      (hipStream_t)stream)
 }

@@ -16,15 +16,15 @@
 
 namespace loom {
 
-template <typename T, int EPL>
+template <typename T, int EPL, int C>
 __global__ void __launch_bounds__(256)
 depth_attn_kernel(const T* __restrict__ q, const T* __restrict__ hk, const T* __restrict__ hv,
                   int64_t sbt, int64_t ss, T* __restrict__ d_out, T* __restrict__ w_out,
                   float* __restrict__ lse_out, int rows, int S, int QH, float scale) {
     const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 4);
     if (row >= rows) return;  // all 16 lanes of a group leave together
-    depth_row<T, EPL>(q, hk, hv, sbt, ss, d_out, w_out, lse_out, row, threadIdx.x & 15, S, QH,
-                      scale);
+    depth_row<T, EPL, C>(q, hk, hv, sbt, ss, d_out, w_out, lse_out, row, threadIdx.x & 15, S, QH,
+                         scale);
 }
 
 // Any HD: one thread per (bt, qh) row, online softmax, scalar loads.
@@ -74,18 +74,22 @@ static int dispatch_depth(const void* q, const void* hk, const void* hv, int64_t
                           int64_t QH, int64_t HD, hipStream_t stream) {
     const int64_t rows = BT * QH;
     const float scale = 1.0f / sqrtf((float)HD);
-    const int threads = 256;
+    // a small launch (a decode step's rows) takes one wave per block so it
+    // spreads over as many CUs as it has waves
+    const int threads = rows * 16 >= 256 * 256 ? 256 : 64;
     // the vector path moves pairs of elements (4 B for 16-bit types, 8 B for
     // fp32) and indexes rows with 32-bit integers
     const bool aligned = sbt % 2 == 0 && ss % 2 == 0 &&
                          (((uintptr_t)hk | (uintptr_t)hv | (uintptr_t)q | (uintptr_t)d_out) % 8 == 0) &&
                          rows * 16 < ((int64_t)1 << 31) && BT * sbt < ((int64_t)1 << 62);
     const int epl = (HD % 16 == 0) ? (int)(HD / 16) : 0;
+#define LOOM_DA_LAUNCH(E, C)                                                                     \
+        hipLaunchKernelGGL((depth_attn_kernel<T, E, C>), dim3((unsigned)ceil_div(rows * 16, threads)), \
+                           dim3(threads), 0, stream, (const T*)q, (const T*)hk, (const T*)hv, sbt, \
+                           ss, (T*)d_out, (T*)w_out, lse_out, (int)rows, (int)S, (int)QH, scale);
 #define LOOM_DA_CASE(E)                                                                          \
     case E:                                                                                      \
-        hipLaunchKernelGGL((depth_attn_kernel<T, E>), dim3((unsigned)ceil_div(rows * 16, threads)), \
-                           dim3(threads), 0, stream, (const T*)q, (const T*)hk, (const T*)hv, sbt, \
-                           ss, (T*)d_out, (T*)w_out, lse_out, (int)rows, (int)S, (int)QH, scale); \
+        LOOM_DA_LAUNCH(E, kDepthChunk)                                                           \
         return launch_status("loom_depth_attn_forward");
     if (aligned) {
         switch (epl) {
@@ -97,6 +101,7 @@ static int dispatch_depth(const void* q, const void* hk, const void* hv, int64_t
         }
     }
 #undef LOOM_DA_CASE
+#undef LOOM_DA_LAUNCH
     hipLaunchKernelGGL((depth_attn_generic_kernel<T>), dim3((unsigned)ceil_div(rows, threads)),
                        dim3(threads), 0, stream, (const T*)q, (const T*)hk, (const T*)hv, sbt, ss,
                        (T*)d_out, (T*)w_out, lse_out, rows, (int)S, (int)QH, (int)HD, scale);

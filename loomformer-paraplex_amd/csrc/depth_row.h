@@ -15,14 +15,13 @@ namespace loom {
 
 constexpr int kDepthChunk = 8;
 
-template <typename T, int EPL>
+template <typename T, int EPL, int C = kDepthChunk>
 __device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __restrict__ hk,
                                           const T* __restrict__ hv, int64_t sbt, int64_t ss,
                                           T* __restrict__ d_out, T* __restrict__ w_out,
                                           float* __restrict__ lse_out, int row, int j, int S,
                                           int QH, float scale) {
     constexpr int HD = EPL * 16;
-    constexpr int C = kDepthChunk;
     const int qh = row % QH;
     const int bt = row / QH;
     const int d0 = j * EPL;

@@ -835,58 +835,62 @@ constexpr int kMaxSplit = 8;
 
 // out[m] = LN(sum_s partial[s, m] + bias) * gamma + beta; one wave per row,
 // N <= 64 * 4 * kLnVec.
-constexpr int kLnVec = 8;
-template <typename T, int NS>
-__global__ void __launch_bounds__(256)
+constexpr int kLnVec = 8;      // 256-column chunks per row: rows of up to 2048
+// One block per row, one wave per 256-column chunk (KV waves), so a decode
+// step's 32 rows spread over 32 CUs.  Every load of the row (all NS split
+// partials, bias, gamma and beta) is issued before the first add; the row's
+// sum and squared deviation are reduced over the waves through LDS.
+template <typename T, int NS, int KV>
+__global__ void __launch_bounds__(64 * KV)
 splitk_ln_kernel(const float* __restrict__ partial, int64_t ldp,
                  const float* __restrict__ bias, const float* __restrict__ gamma,
                  const float* __restrict__ beta, T* __restrict__ out, int64_t ldo, int64_t rows,
                  int N, float eps) {
-    const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-    const int lane = threadIdx.x & 63;
-    if (row >= rows) return;                       // whole waves leave together
-    float x[kLnVec][4];
-    float s = 0.0f;
+    __shared__ float red[2][KV];
+    const int64_t row = blockIdx.x;
+    const int lane = threadIdx.x & 63, k = threadIdx.x >> 6;
+    const int c = (lane + 64 * k) * 4;
+    const bool in = c < N;
+    float4 v[NS], bv, gv, ev;
 #pragma unroll
-    for (int k = 0; k < kLnVec; ++k) {
-        const int c = (lane + 64 * k) * 4;
+    for (int sp = 0; sp < NS; ++sp)
+        v[sp] = in ? *reinterpret_cast<const float4*>(partial + (sp * rows + row) * ldp + c)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    bv = (in && bias != nullptr) ? *reinterpret_cast<const float4*>(bias + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    gv = in ? *reinterpret_cast<const float4*>(gamma + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    ev = in ? *reinterpret_cast<const float4*>(beta + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    float x[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[k][e] = 0.0f;
-        if (c < N) {
-            float4 v[NS];                          // all splits of the chunk in flight
-#pragma unroll
-            for (int sp = 0; sp < NS; ++sp)
-                v[sp] = *reinterpret_cast<const float4*>(partial + (sp * rows + row) * ldp + c);
-#pragma unroll
-            for (int sp = 0; sp < NS; ++sp) {
-                x[k][0] += v[sp].x; x[k][1] += v[sp].y; x[k][2] += v[sp].z; x[k][3] += v[sp].w;
-            }
-            if (bias != nullptr)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) x[k][e] += bias[c + e];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) s += x[k][e];
-        }
+    for (int sp = 0; sp < NS; ++sp) {
+        x[0] += v[sp].x; x[1] += v[sp].y; x[2] += v[sp].z; x[3] += v[sp].w;
     }
-    const float mean = wave_sum(s) / N;
+    float s = in ? (x[0] + x[1]) + (x[2] + x[3]) : 0.0f;
+    s = wave_sum(s);
+    if (lane == 0) red[0][k] = s;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int q = 0; q < KV; ++q) tot += red[0][q];
+    const float mean = tot / N;
     float var = 0.0f;
+    if (in)
 #pragma unroll
-    for (int k = 0; k < kLnVec; ++k)
-        if ((lane + 64 * k) * 4 < N)
+        for (int e = 0; e < 4; ++e) {
+            const float dlt = x[e] - mean;
+            var = fmaf(dlt, dlt, var);
+        }
+    var = wave_sum(var);
+    if (lane == 0) red[1][k] = var;
+    __syncthreads();
+    float vt = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float dlt = x[k][e] - mean;
-                var = fmaf(dlt, dlt, var);
-            }
-    const float rstd = frsq(wave_sum(var) / N + eps);
+    for (int q = 0; q < KV; ++q) vt += red[1][q];
+    const float rstd = frsq(vt / N + eps);
+    if (!in) return;
+    const float g[4] = {gv.x, gv.y, gv.z, gv.w};
+    const float e4[4] = {ev.x, ev.y, ev.z, ev.w};
 #pragma unroll
-    for (int k = 0; k < kLnVec; ++k) {
-        const int c = (lane + 64 * k) * 4;
-        if (c >= N) continue;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            st(out + row * ldo + c + e, fmaf((x[k][e] - mean) * rstd, gamma[c + e], beta[c + e]));
-    }
+    for (int e = 0; e < 4; ++e) st(out + row * ldo + c + e, fmaf((x[e] - mean) * rstd, g[e], e4[e]));
 }
 
 extern "C" int64_t loom_linear_ln_workspace_bytes(int64_t M, int64_t N) {
@@ -907,6 +911,7 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
     bool fused = dtype == LOOM_BF16 && d->m >= 1 && d->m <= 64 && d->k % 8 == 0 && d->ldx % 8 == 0 &&
                  ((uintptr_t)d->x & 15) == 0 && g.ldw % 8 == 0 && ((uintptr_t)g.w & 15) == 0 &&
                  g.n % 4 == 0 && workspace != nullptr && ((uintptr_t)workspace & 15) == 0 &&
+                 ((((uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)g.bias) & 15) == 0) &&
                  workspace_bytes >= loom_linear_ln_workspace_bytes(d->m, g.n);
     if (d->k2 > 0)
         fused = fused && d->k2 % 8 == 0 && d->ldx2 % 8 == 0 && ((uintptr_t)d->x2 & 15) == 0 &&
@@ -939,16 +944,24 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
     launch_skinny_multi(a, grid, (int)ceil_div(d->m, 16), ceil_div(steps, ns), st);
     int rc = launch_status("loom_linear_ln");
     if (rc != LOOM_OK) return rc;
-    const dim3 lgrid((unsigned)ceil_div(d->m * 64, 256));
+#define LOOM_SLN_KV(NS, KV)                                                                   \
+    hipLaunchKernelGGL((splitk_ln_kernel<bf16_t, NS, KV>), dim3((unsigned)d->m), dim3(64 * (KV)), \
+                       0, st, workspace, g.n, g.bias, gamma, beta, (bf16_t*)out, ldo, d->m,     \
+                       (int)g.n, eps);
 #define LOOM_SLN(NS)                                                                          \
     case NS:                                                                                  \
-        hipLaunchKernelGGL((splitk_ln_kernel<bf16_t, NS>), lgrid, dim3(256), 0, st, workspace,  \
-                           g.n, g.bias, gamma, beta, (bf16_t*)out, ldo, d->m, (int)g.n, eps); \
+        if (kv <= 1) { LOOM_SLN_KV(NS, 1) }                                                   \
+        else if (kv == 2) { LOOM_SLN_KV(NS, 2) }                                              \
+        else if (kv == 3) { LOOM_SLN_KV(NS, 3) }                                              \
+        else if (kv == 4) { LOOM_SLN_KV(NS, 4) }                                              \
+        else { LOOM_SLN_KV(NS, 8) }                                                           \
         break;
+    const int kv = (int)ceil_div(g.n, 256);
     switch (ns) {
         LOOM_SLN(1) LOOM_SLN(2) LOOM_SLN(3) LOOM_SLN(4) LOOM_SLN(5) LOOM_SLN(6) LOOM_SLN(7)
         LOOM_SLN(8)
     }
+#undef LOOM_SLN_KV
 #undef LOOM_SLN
     return launch_status("loom_linear_ln(layernorm)");
 }

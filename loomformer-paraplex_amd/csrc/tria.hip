@@ -534,6 +534,10 @@ final_ca_row_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
             if (j < K) vr[i] = *reinterpret_cast<const uint4*>(vb + j * D + c2 * 8);
         }
     }
+    // the key mask (wave 0, lane = key) and the residual chunk, in the same round
+    const bool ok = wid == 0 && lane < K && allowed[row * allowed_stride + lane] != 0;
+    float rr[8];
+    if (residual != nullptr && tid < nch) Vec8<T>::load(residual + row * D + tid * 8, rr);
 #pragma unroll
     for (int i = 0; i < KW; ++i) {
         const int64_t j = wid + 8 * i;
@@ -549,11 +553,11 @@ final_ca_row_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
             }
         }
         const float sc = wave_sum(dot) * scale;
-        if (lane == 0 && j < K) wts[j] = allowed[row * allowed_stride + j] ? sc : -INFINITY;
+        if (lane == 0 && j < K) wts[j] = sc;
     }
     __syncthreads();
     if (wid == 0) {
-        const float sv = lane < K ? wts[lane] : -INFINITY;
+        const float sv = ok ? wts[lane] : -INFINITY;
         const float mx = wave_max(sv);
         const float e = (mx == -INFINITY || sv == -INFINITY) ? 0.0f : fexp(sv - mx);
         const float sum = wave_sum(e);
@@ -584,8 +588,6 @@ final_ca_row_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[e] = part[0][tid][e] + part[1][tid][e] + part[2][tid][e] + part[3][tid][e];
         if (residual != nullptr) {
-            float rr[8];
-            Vec8<T>::load(residual + row * D + tid * 8, rr);
 #pragma unroll
             for (int e = 0; e < 8; ++e) a[e] = rr[e] + gamma * a[e];
         }

@@ -84,12 +84,13 @@ SIGNATURES = {
     "loom_add_layernorm": [c_int, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, _P],
     "loom_tria_decode_temporal": [c_int, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_float,
                                   _P],
-    "loom_decode_tria_readout": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64,
-                                 c_int64, c_int64, c_float, c_float, _P],
+    "loom_decode_tria_readout": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64,
+                                 c_int64, c_int64, c_int64, c_float, c_float, _P],
 }
 # entry points that return a value instead of a status
 QUERIES = {"loom_gqa_workspace_bytes": ([c_int64] * 5, c_int64),
            "loom_linear_multi_desc_bytes": ([], c_int64),
+           "loom_decode_tria_readout_workspace_bytes": ([c_int64, c_int64], c_int64),
            "loom_ffn_decode_desc_bytes": ([], c_int64),
            "loom_linear_ln_workspace_bytes": ([c_int64, c_int64], c_int64),
            "loom_tria_chunked_workspace_bytes": ([c_int64] * 4, c_int64)}

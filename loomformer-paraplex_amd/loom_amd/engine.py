@@ -130,6 +130,10 @@ class LoomDecoder:
         ws = self.lib.loom_gqa_workspace_bytes(B, self.max_len, c.QH, c.KVH, c.HD)
         self.ws = torch.zeros((ws + 3) // 4, dtype=torch.float32, device=dev)   # counters start at 0
         self.ws_bytes = ws
+        # per-block slot-pool records of the decode Tria readout
+        rb = self.lib.loom_decode_tria_readout_workspace_bytes(B, H)
+        self.rd_ws = torch.empty((rb + 3) // 4, dtype=torch.float32, device=dev)
+        self.rd_ws_bytes = rb
         # activations
         self.h = z(B, N)
         self.h2 = z(B, N)
@@ -294,8 +298,8 @@ class LoomDecoder:
         self._call("loom_decode_tria_readout", self.code, _P(self.carry[carry_i]),
                    None if first else _P(self.doc), None if first else _P(self.reset_now),
                    _P(self.fire), _P(self.doc), _P(self.score_w), _P(self.proj_w), _P(self.proj_b),
-                   _P(self.up_w), _P(self.up_b), _P(self.a_t), B, H, N, float(c.polarm_beta), 1e-6,
-                   st)
+                   _P(self.up_w), _P(self.up_b), _P(self.a_t), _P(self.rd_ws), self.rd_ws_bytes, B, H, N,
+                   float(c.polarm_beta), 1e-6, st)
         # ---- final cross-attention step (tria.py:1560-1595): stage k/v, append on
         # fire (+ end-of-step bookkeeping), then attend over the appended keys
         self._multi("stage", self.a_t, [dict(w=self.wqk, out=self.stage_k),

@@ -314,7 +314,7 @@ def test_argmax_rows_first_index_on_ties(dtype, V):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("H,N", [(300, 96), (3072, 768), (1100, 40)])
+@pytest.mark.parametrize("H,N", [(300, 96), (3072, 768), (1100, 40), (5000, 200)])
 def test_decode_tria_readout(dtype, H, N):
     # temporal step + PolARM + slot pool + proj + up in one launch, against the
     # oracle ops with the intermediates rounded to dtype as the unfused ops store them
@@ -344,15 +344,18 @@ def test_decode_tria_readout(dtype, H, N):
 
     doc = prev.clone()                      # in place: prev and doc are one buffer
     a = torch.empty(B, N, device=DEV, dtype=dtype)
+    nb = L().load().loom_decode_tria_readout_workspace_bytes(B, H)
+    ws = torch.full((nb // 4,), float("nan"), device=DEV)   # scratch: no zeroing needed
     wd, wa = want(host(depth), host(prev))
     L().call("loom_decode_tria_readout", code(depth), P(depth), P(doc), P(reset_d), P(fire_d),
-             P(doc), P(sw), P(pw), P(pb), P(uw), P(ub), P(a), B, H, N, 0.1, 1e-6, S(depth))
+             P(doc), P(sw), P(pw), P(pb), P(uw), P(ub), P(a), P(ws), nb, B, H, N, 0.1, 1e-6,
+             S(depth))
     check(doc, wd, dtype)
     check(a, wa, dtype)
     # first token: no previous state (no reset flags needed)
     wd, wa = want(host(depth), None)
     L().call("loom_decode_tria_readout", code(depth), P(depth), None, None, P(fire_d), P(doc),
-             P(sw), P(pw), P(pb), P(uw), P(ub), P(a), B, H, N, 0.1, 1e-6, S(depth))
+             P(sw), P(pw), P(pb), P(uw), P(ub), P(a), P(ws), nb, B, H, N, 0.1, 1e-6, S(depth))
     check(doc, wd, dtype)
     check(a, wa, dtype)
 
