@@ -363,10 +363,9 @@ int loom_rope_append(int dtype, const void* qkv, void* q_out, void* k_cache, voi
                      void* stream);
 
 /* Bytes of workspace loom_gqa_decode_attention / loom_gqa_decode_step need for
- * len <= max_len: a 256-byte-rounded block of B*KVH int32 arrival counters,
- * then the per-chunk partial records.  The counter block must be zero before
- * the first call (allocate the workspace zero-filled, 256-byte aligned); every
- * call leaves it zero again.  Zero it again if B or KVH changes. */
+ * len <= max_len: the per-chunk partial records [B, KVH, ceil(max_len/256),
+ * 2G + 2G*HD] fp32 (G = QH/KVH) that the attention launch writes and the merge
+ * launch after it reads.  Scratch: no initial contents are needed. */
 int64_t loom_gqa_workspace_bytes(int64_t B, int64_t max_len, int64_t QH, int64_t KVH, int64_t HD);
 
 /* Causal GQA attention of one query position over cache positions [0, len):

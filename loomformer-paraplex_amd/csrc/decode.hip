@@ -49,14 +49,15 @@ rope_append_kernel(const T* __restrict__ qkv, T* __restrict__ q_out, T* __restri
 // kAttnChunk positions for the G query heads that share kv head kvh and
 // publishes an unnormalised partial record (m, l, sum p*v, sum p*k) per head.
 // One pass over K and V: each cache row is read once and feeds both the
-// scores and the A.K readout.  The last block of each (b, kvh) to finish
-// (a per-(b, kvh) arrival counter in the workspace) merges the records and
-// writes C = A.V and Kctx = A.K_roped; it leaves the counter at zero again.
+// scores and the A.K readout.  gqa_merge_kernel, the next launch, merges each
+// row's records and writes C = A.V and Kctx = A.K_roped (a separate launch is
+// cheaper than an in-kernel last-block merge, whose device-coherent record
+// stores, arrival atomic and record loads are three serial memory trips).
 //
 // FROM_QKV: q comes unroped from the step's qkv row; the block roped q
 // itself, and the block that holds position pos also ropes this token's k,
 // attends to it from registers and appends (k_roped, v) to the caches
-// (RoPE + cache append + attention + combine in one launch).
+// (RoPE + cache append + attention in one launch, the combine in the next).
 //
 // Mapping: LPR lanes per cache row (EPL = HD/LPR contiguous elements each);
 // the block's NG = 256/LPR row groups take positions t0 + grp + NG*i.  A group
@@ -66,12 +67,6 @@ rope_append_kernel(const T* __restrict__ qkv, T* __restrict__ q_out, T* __restri
 constexpr int kAttnChunk = 256;
 constexpr int kAttnMaxG = 8;
 constexpr int kAttnBatch = 4;
-constexpr int kAttnMerge = 8;     // records loaded together by the merging block
-
-// bytes of the arrival counters at the head of the workspace
-__host__ __device__ inline int64_t gqa_counter_bytes(int64_t B, int64_t KVH) {
-    return (B * KVH * 4 + 255) / 256 * 256;
-}
 
 template <typename T>
 struct GqaArgs {
@@ -82,7 +77,6 @@ struct GqaArgs {
     const float* cosv;     // FROM_QKV: RoPE tables [*, HD] (attention factor folded in)
     const float* sinv;
     T* q_out;              // FROM_QKV, optional: the roped q [B, QH, HD]
-    int* counters;         // [B * KVH], zero between calls
     float* rec;            // [B, KVH, nchunks, REC]
     T* c_out;              // [B, QH, HD] with row stride out_sb
     T* k_out;
@@ -113,23 +107,15 @@ __device__ __forceinline__ float rope_elem(const T* head, const float* cr, const
 }
 
 // End of a GQA chunk block: merge the four waves' partials wred[w] = [m(G) |
-// l(G) | c(G*HD) | k(G*HD)] into the chunk record, publish it, and, in the
-// block that arrives last for (b, kvh), merge every chunk record into C and
-// Kctx and reset the arrival counter.  The merging block stages the records
-// in LDS (`stage`, `stage_floats` floats, reusing the block's scratch) with
-// every device-coherent load of a batch in flight at once.
-constexpr int kMergeLoads = 32;   // record words each thread has in flight while staging
-
+// l(G) | c(G*HD) | k(G*HD)] into the chunk's record (unnormalised, scores in
+// log2 units).  The records of a row are merged by gqa_merge_kernel, the next
+// launch on the stream.
 template <typename T, int G, int HD>
-__device__ __forceinline__ void gqa_finish(const GqaArgs<T>& a, float (*wred)[2 * G + 2 * G * HD],
-                                           int& s_last, int64_t b, int kvh, int chunk, int nchunks,
-                                           int nact, float* stage, int stage_floats) {
+__device__ __forceinline__ void gqa_record(const GqaArgs<T>& a, float (*wred)[2 * G + 2 * G * HD],
+                                           int64_t b, int kvh, int chunk, int nchunks) {
     constexpr int REC = 2 * G + 2 * G * HD;
-    constexpr int kOut = (G * HD + 255) / 256;
-    const int tid = threadIdx.x;
-    float* recs = a.rec + ((int64_t)b * a.KVH + kvh) * nchunks * REC;
-    float* rec = recs + (int64_t)chunk * REC;
-    for (int k = tid; k < REC; k += blockDim.x) {
+    float* rec = a.rec + (((int64_t)b * a.KVH + kvh) * nchunks + chunk) * REC;
+    for (int k = threadIdx.x; k < REC; k += blockDim.x) {
         const int g = k < 2 * G ? k % G : ((k - 2 * G) % (G * HD)) / HD;
         float M = -INFINITY;
 #pragma unroll
@@ -141,75 +127,65 @@ __device__ __forceinline__ void gqa_finish(const GqaArgs<T>& a, float (*wred)[2 
             for (int w = 0; w < 4; ++w)
                 if (wred[w][g] != -INFINITY) acc = fmaf(wred[w][k], __builtin_amdgcn_exp2f(wred[w][g] - M), acc);
         }
-        st_coherent(rec + k, acc);
+        rec[k] = acc;
     }
-    // publish the record; the block that arrives last merges all of them
-    __syncthreads();
-    int* counter = a.counters + b * a.KVH + kvh;
-    if (tid == 0) s_last = arrive(counter) == nact - 1;
-    __syncthreads();
-    if (!s_last) return;
-    float M[kOut], L[kOut], C[kOut], K[kOut];
+}
+
+// Second pass of the split attention: thread per output element (b, head, d)
+// merges the nact chunk records of its (b, kv head) into C = A.V and
+// Kctx = A.K_roped (flash-decoding's combine), with kMergeBatch chunks' loads
+// in flight at once.
+constexpr int kMergeBatch = 16;
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+gqa_merge_kernel(const float* __restrict__ rec, int nchunks, int64_t len,
+                 const int64_t* __restrict__ pos_dev, T* __restrict__ c_out, T* __restrict__ k_out,
+                 int64_t out_sb, int B, int QH, int KVH, int HD) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (int64_t)B * QH * HD) return;
+    const int d = (int)(e % HD);
+    const int h = (int)((e / HD) % QH);
+    const int64_t b = e / ((int64_t)HD * QH);
+    const int G = QH / KVH, kvh = h / G, g = h % G;
+    const int REC = 2 * G + 2 * G * HD;
+    const int64_t n = pos_dev != nullptr ? *pos_dev + 1 : len;
+    const int nact = (int)((n + kAttnChunk - 1) / kAttnChunk);
+    const float* recs = rec + (b * KVH + kvh) * (int64_t)nchunks * REC;
+    float M = -INFINITY, L = 0.0f, C = 0.0f, K = 0.0f;
+    for (int c0 = 0; c0 < nact; c0 += kMergeBatch) {
+        float m[kMergeBatch], l[kMergeBatch], cv[kMergeBatch], kv[kMergeBatch];
 #pragma unroll
-    for (int i = 0; i < kOut; ++i) {
-        M[i] = -INFINITY;
-        L[i] = C[i] = K[i] = 0.0f;
-    }
-    const int per_batch = stage_floats / REC > 0 ? stage_floats / REC : 1;
-    for (int c0 = 0; c0 < nact; c0 += per_batch) {
-        const int nc = nact - c0 < per_batch ? nact - c0 : per_batch;
-        const int nval = nc * REC;
-        const float* src = recs + (int64_t)c0 * REC;
-        __syncthreads();                   // the scratch is free (previous batch / partials read)
-        for (int k0 = tid; k0 < nval; k0 += kMergeLoads * 256) {
-            float v[kMergeLoads];
-#pragma unroll
-            for (int u = 0; u < kMergeLoads; ++u) {
-                const int k = k0 + 256 * u;
-                v[u] = k < nval ? ld_coherent(src + k) : 0.0f;
-            }
-#pragma unroll
-            for (int u = 0; u < kMergeLoads; ++u) {
-                const int k = k0 + 256 * u;
-                if (k < nval) stage[k] = v[u];
-            }
+        for (int u = 0; u < kMergeBatch; ++u) {
+            const float* r = recs + (int64_t)(c0 + u) * REC;
+            const bool ok = c0 + u < nact;
+            m[u] = ok ? r[g] : -INFINITY;
+            l[u] = ok ? r[G + g] : 0.0f;
+            cv[u] = ok ? r[2 * G + g * HD + d] : 0.0f;
+            kv[u] = ok ? r[2 * G + G * HD + g * HD + d] : 0.0f;
         }
-        __syncthreads();
+        float Mb = M;
 #pragma unroll
-        for (int i = 0; i < kOut; ++i) {
-            const int k = tid + 256 * i;
-            if (k >= G * HD) continue;
-            const int g = k / HD, d = k % HD;
-            float Mb = M[i];
-            for (int c = 0; c < nc; ++c) Mb = fmaxf(Mb, stage[c * REC + g]);
-            if (Mb == -INFINITY) continue;
-            const float r = __builtin_amdgcn_exp2f(M[i] - Mb);   // 0 while M is -inf
-            float l = L[i] * r, cc = C[i] * r, kk = K[i] * r;
-            for (int c = 0; c < nc; ++c) {
-                const float* rc = stage + c * REC;
-                if (rc[g] == -INFINITY) continue;
-                const float w = __builtin_amdgcn_exp2f(rc[g] - Mb);
-                l = fmaf(rc[G + g], w, l);
-                cc = fmaf(rc[2 * G + g * HD + d], w, cc);
-                kk = fmaf(rc[2 * G + G * HD + g * HD + d], w, kk);
-            }
-            M[i] = Mb;
-            L[i] = l;
-            C[i] = cc;
-            K[i] = kk;
+        for (int u = 0; u < kMergeBatch; ++u) Mb = fmaxf(Mb, m[u]);
+        if (Mb == -INFINITY) continue;
+        const float r0 = __builtin_amdgcn_exp2f(M - Mb);   // 0 while M is -inf
+        L *= r0;
+        C *= r0;
+        K *= r0;
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+            if (m[u] == -INFINITY) continue;
+            const float w = __builtin_amdgcn_exp2f(m[u] - Mb);
+            L = fmaf(l[u], w, L);
+            C = fmaf(cv[u], w, C);
+            K = fmaf(kv[u], w, K);
         }
+        M = Mb;
     }
-#pragma unroll
-    for (int i = 0; i < kOut; ++i) {
-        const int k = tid + 256 * i;
-        if (k >= G * HD) continue;
-        const int g = k / HD, d = k % HD;
-        const float inv = 1.0f / L[i];
-        const int64_t o = b * a.out_sb + (kvh * G + g) * HD + d;
-        st(a.c_out + o, C[i] * inv);
-        st(a.k_out + o, K[i] * inv);
-    }
-    if (tid == 0) reset_counter(counter);
+    const float inv = 1.0f / L;
+    const int64_t o = b * out_sb + h * HD + d;
+    st(c_out + o, C * inv);
+    st(k_out + o, K * inv);
 }
 
 template <typename T, int EPL, int G, int LPR, bool FROM_QKV>
@@ -219,7 +195,6 @@ gqa_decode_kernel(GqaArgs<T> a) {
     constexpr int NG = 256 / LPR;          // row groups per block
     constexpr int REC = 2 * G + 2 * G * HD;
     __shared__ float wred[4][REC];
-    __shared__ int s_last;
     const int chunk = blockIdx.x, kvh = blockIdx.y;
     const int64_t b = blockIdx.z;
     const int nchunks = a.nchunks;
@@ -393,7 +368,7 @@ gqa_decode_kernel(GqaArgs<T> a) {
         }
     }
     __syncthreads();
-    gqa_finish<T, G, HD>(a, wred, s_last, b, kvh, chunk, nchunks, nact, &wred[0][0], 4 * REC);
+    gqa_record<T, G, HD>(a, wred, b, kvh, chunk, nchunks);
 }
 
 // ------------------------------------------------------------------ GQA attention on MFMA (bf16)
@@ -458,7 +433,6 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     constexpr int kTileBytes = 4 * (int)sizeof(Tiles);
     constexpr int kRedBytes = 4 * REC * (int)sizeof(float);
     __shared__ __align__(16) unsigned char lds[kTileBytes > kRedBytes ? kTileBytes : kRedBytes];
-    __shared__ int s_last;
     const int chunk = blockIdx.x, kvh = blockIdx.y;
     const int64_t b = blockIdx.z;
     const int nchunks = a.nchunks;
@@ -647,8 +621,7 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
             }
         }
     __syncthreads();
-    gqa_finish<bf16_t, G, HD>(a, wred, s_last, b, kvh, chunk, nchunks, nact,
-                              reinterpret_cast<float*>(lds), (int)(sizeof(lds) / sizeof(float)));
+    gqa_record<bf16_t, G, HD>(a, wred, b, kvh, chunk, nchunks);
 }
 
 // ------------------------------------------------------------------ add + LayerNorm
@@ -1012,6 +985,17 @@ static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void
                                        HD, st);
     };
     GqaArgs<T> a{};
+    // after the chunk launch: the merge of its records, then (unless folded in)
+    // the depth read
+    auto finish = [&](bool depth_done) -> int {
+        int rc = launch_status(from_qkv ? "loom_gqa_decode_step" : "loom_gqa_decode_attention");
+        if (rc != LOOM_OK) return rc;
+        hipLaunchKernelGGL((gqa_merge_kernel<T>), dim3((unsigned)ceil_div(B * QH * HD, 256)), dim3(256),
+                           0, st, a.rec, nchunks, len, pos_dev, (T*)c_out, (T*)k_out, out_sb, (int)B,
+                           (int)QH, (int)KVH, (int)HD);
+        rc = launch_status(from_qkv ? "loom_gqa_decode_step(merge)" : "loom_gqa_decode_attention(merge)");
+        return (rc != LOOM_OK || depth_done) ? rc : depth_after();
+    };
     a.q = (const T*)q;
     a.kc = (T*)kc;
     a.vc = (T*)vc;
@@ -1021,8 +1005,7 @@ static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void
     a.cosv = cosv;
     a.sinv = sinv;
     a.q_out = (T*)q_out;
-    a.counters = (int*)ws;
-    a.rec = (float*)((char*)ws + gqa_counter_bytes(B, KVH));
+    a.rec = ws;
     a.c_out = (T*)c_out;
     a.k_out = (T*)k_out;
     a.out_sb = out_sb;
@@ -1053,8 +1036,7 @@ static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void
                 hipLaunchKernelGGL((gqa_mfma_kernel<HDV, GG, true>), mgrid, dim3(256), 0, st, a); \
             else                                                                                  \
                 hipLaunchKernelGGL((gqa_mfma_kernel<HDV, GG, false>), mgrid, dim3(256), 0, st, a); \
-            const int rc = launch_status(from_qkv ? "loom_gqa_decode_step" : "loom_gqa_decode_attention"); \
-            return (rc != LOOM_OK || fuse_depth) ? rc : depth_after();                            \
+            return finish(fuse_depth);                                                            \
         }
         LOOM_GQA_MF(96, 4) LOOM_GQA_MF(96, 1) LOOM_GQA_MF(96, 2) LOOM_GQA_MF(96, 8)
         LOOM_GQA_MF(64, 4) LOOM_GQA_MF(64, 1) LOOM_GQA_MF(64, 2) LOOM_GQA_MF(64, 8)
@@ -1068,8 +1050,7 @@ static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void
             hipLaunchKernelGGL((gqa_decode_kernel<T, E, GG, LPR, true>), grid, dim3(256), 0, st, a); \
         else                                                                                    \
             hipLaunchKernelGGL((gqa_decode_kernel<T, E, GG, LPR, false>), grid, dim3(256), 0, st, a); \
-        const int rc = launch_status(from_qkv ? "loom_gqa_decode_step" : "loom_gqa_decode_attention"); \
-        return rc != LOOM_OK ? rc : depth_after();                                              \
+        return finish(false);                                                                   \
     }
     // head_dim 32/64/96/128 (16 lanes per row) and 8 (8 lanes), groups 1/2/4/8
     LOOM_GQA(6, 4, 16) LOOM_GQA(6, 1, 16) LOOM_GQA(6, 2, 16) LOOM_GQA(6, 8, 16)
@@ -1149,7 +1130,7 @@ extern "C" int64_t loom_gqa_workspace_bytes(int64_t B, int64_t max_len, int64_t 
                                             int64_t HD) {
     const int64_t G = QH / KVH;
     const int64_t nchunks = ceil_div(max_len, kAttnChunk);
-    return gqa_counter_bytes(B, KVH) + B * KVH * nchunks * (2 * G + 2 * G * HD) * (int64_t)sizeof(float);
+    return B * KVH * nchunks * (2 * G + 2 * G * HD) * (int64_t)sizeof(float);
 }
 
 extern "C" int loom_rope_append(int dtype, const void* qkv, void* q_out, void* k_cache,

@@ -128,7 +128,7 @@ class LoomDecoder:
         self.tokens = z(B, self.max_len, dtype=torch.int64)
         self.prompt_buf = z(B, self.max_len, dtype=torch.int64)
         ws = self.lib.loom_gqa_workspace_bytes(B, self.max_len, c.QH, c.KVH, c.HD)
-        self.ws = torch.zeros((ws + 3) // 4, dtype=torch.float32, device=dev)   # counters start at 0
+        self.ws = torch.zeros((ws + 3) // 4, dtype=torch.float32, device=dev)   # GQA chunk records
         self.ws_bytes = ws
         # per-block slot-pool records of the decode Tria readout
         rb = self.lib.loom_decode_tria_readout_workspace_bytes(B, H)

@@ -101,7 +101,7 @@ def test_gqa_decode_attention(dtype, B, QH, KVH, HD, length):
     c = torch.empty(B, QH, HD, device=DEV, dtype=dtype)
     kx = torch.empty_like(c)
     nb = _lib.load().loom_gqa_workspace_bytes(B, max_len, QH, KVH, HD)
-    ws = torch.zeros(nb // 4 + 1, device=DEV)      # arrival counters start at zero
+    ws = torch.full((nb // 4 + 1,), float("nan"), device=DEV)   # chunk records: scratch, no initial contents
     _lib.call("loom_gqa_decode_attention", code(q), P(q), P(kc), P(vc), max_len * KVH * HD, KVH * HD,
               HD, P(c), P(kx), P(ws), nb, B, length, None, QH, KVH, HD, S(q))
     G = QH // KVH
@@ -118,9 +118,6 @@ def test_gqa_decode_attention(dtype, B, QH, KVH, HD, length):
               HD, P(c), P(kx), P(ws), nb, B, max_len, P(pos_d), QH, KVH, HD, S(q))
     check(c, (a @ V).squeeze(2), dtype)
     check(kx, (a @ K).squeeze(2), dtype)
-    # every call leaves the arrival counters at zero
-    ncnt = B * KVH
-    assert int(ws[:ncnt].view(torch.int32).abs().sum().item()) == 0
 
 
 def _rope_tables(HD, n):
@@ -170,7 +167,6 @@ def test_gqa_decode_step_depth(dtype, B, QH, KVH, HD, length, S_, L2):
             _lib.call("loom_depth_attn_forward", code(qkv), P(dq), P(hist), P(hist[:, :, N:]),
                       L2 * 2 * N, 2 * N, P(d), None, None, B, S_, QH, HD, S(qkv))
         outs.append([host(t) for t in (c, kx, qo, d, kc, vc)])
-        assert int(ws[:B * KVH].view(torch.int32).abs().sum().item()) == 0
     for x, y in zip(*outs):
         assert torch.equal(x, y)
     hk = host(hist)[:, :S_, :N].view(B, S_, QH, HD)
@@ -244,7 +240,6 @@ def test_gqa_decode_step(dtype, head_major, B, QH, KVH, HD, length):
         rest = [t for t in range(max_len) if t != pos]
         assert torch.equal(view(kc)[:, rest], kc0[:, rest])
         assert torch.equal(view(vc)[:, rest], vc0[:, rest])
-        assert int(ws[:B * KVH].view(torch.int32).abs().sum().item()) == 0
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
