@@ -363,9 +363,10 @@ int loom_rope_append(int dtype, const void* qkv, void* q_out, void* k_cache, voi
                      void* stream);
 
 /* Bytes of workspace loom_gqa_decode_attention / loom_gqa_decode_step need for
- * len <= max_len: the per-chunk partial records [B, KVH, ceil(max_len/256),
- * 2G + 2G*HD] fp32 (G = QH/KVH) that the attention launch writes and the merge
- * launch after it reads.  Scratch: no initial contents are needed. */
+ * len <= max_len: the per-chunk partial records [B, KVH, nchunks, 2G + 2G*HD]
+ * fp32 (G = QH/KVH) that the attention launch writes and the merge launch after
+ * it reads; nchunks = min(ceil(1.5 * CUs / (B*KVH)), ceil(max_len/128)) on the
+ * current device.  Scratch: no initial contents are needed. */
 int64_t loom_gqa_workspace_bytes(int64_t B, int64_t max_len, int64_t QH, int64_t KVH, int64_t HD);
 
 /* Causal GQA attention of one query position over cache positions [0, len):

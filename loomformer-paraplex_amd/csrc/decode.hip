@@ -45,8 +45,9 @@ rope_append_kernel(const T* __restrict__ qkv, T* __restrict__ q_out, T* __restri
 }
 
 // ------------------------------------------------------------------ GQA attention
-// Split over the sequence (flash-decoding): block (chunk, kvh, b) covers
-// kAttnChunk positions for the G query heads that share kv head kvh and
+// Split over the sequence (flash-decoding): block (chunk, kvh, b) covers one
+// of the row's nchunks equal slices of the positions (gqa_chunk_len) for the
+// G query heads that share kv head kvh and
 // publishes an unnormalised partial record (m, l, sum p*v, sum p*k) per head.
 // One pass over K and V: each cache row is read once and feeds both the
 // scores and the A.K readout.  gqa_merge_kernel, the next launch, merges each
@@ -64,7 +65,25 @@ rope_append_kernel(const T* __restrict__ qkv, T* __restrict__ q_out, T* __restri
 // scores kAttnBatch positions for all G heads at once, then folds them into an
 // online softmax with one rescale per batch.  Scores are kept in log2 units
 // (q is pre-scaled by log2(e)/sqrt(HD)) so every exponential is one v_exp_f32.
-constexpr int kAttnChunk = 256;
+// Chunk blocks per (b, kv head) row: about 1.5 blocks per CU over the whole
+// grid (fewer, longer chunks measured faster than one chunk per 256 positions:
+// every block pays its record and its ramp-up), and no chunk shorter than
+// kAttnMinChunk positions.  The workspace and the launch use the same count.
+constexpr int kAttnMinChunk = 128;
+static int gqa_nchunks(int64_t B, int64_t KVH, int64_t max_len) {
+    const int64_t rows = B * KVH;
+    int64_t nc = (3 * (int64_t)device_cus() / 2 + rows - 1) / rows;
+    const int64_t cap = (max_len + kAttnMinChunk - 1) / kAttnMinChunk;
+    nc = nc < cap ? nc : cap;
+    return (int)(nc > 1 ? nc : 1);
+}
+
+// Positions per chunk block when a row of len positions is split over nchunks
+// blocks: equal slices, rounded up to a whole 32-position wave step.
+__host__ __device__ __forceinline__ int64_t gqa_chunk_len(int64_t len, int nchunks) {
+    const int64_t c = (len + nchunks - 1) / nchunks;
+    return (c + 31) / 32 * 32;
+}
 constexpr int kAttnMaxG = 8;
 constexpr int kAttnBatch = 4;
 
@@ -150,7 +169,8 @@ gqa_merge_kernel(const float* __restrict__ rec, int nchunks, int64_t len,
     const int G = QH / KVH, kvh = h / G, g = h % G;
     const int REC = 2 * G + 2 * G * HD;
     const int64_t n = pos_dev != nullptr ? *pos_dev + 1 : len;
-    const int nact = (int)((n + kAttnChunk - 1) / kAttnChunk);
+    const int64_t clen = gqa_chunk_len(n, nchunks);
+    const int nact = (int)((n + clen - 1) / clen);
     const float* recs = rec + (b * KVH + kvh) * (int64_t)nchunks * REC;
     float M = -INFINITY, L = 0.0f, C = 0.0f, K = 0.0f;
     for (int c0 = 0; c0 < nact; c0 += kMergeBatch) {
@@ -202,10 +222,11 @@ gqa_decode_kernel(GqaArgs<T> a) {
     const int wave = tid >> 6, lane = tid & 63;
     const int64_t len = a.pos_dev != nullptr ? *a.pos_dev + 1 : a.len;
     const int64_t pos = len - 1;
-    const int nact = (int)((len + kAttnChunk - 1) / kAttnChunk);
-    if (chunk >= nact) return;                    // past the end: no record, not counted
-    const int64_t t0 = (int64_t)chunk * kAttnChunk;
-    const int64_t t1 = t0 + kAttnChunk < len ? t0 + kAttnChunk : len;
+    const int64_t clen = gqa_chunk_len(len, nchunks);
+    const int nact = (int)((len + clen - 1) / clen);
+    if (chunk >= nact) return;                    // past the end: no record
+    const int64_t t0 = (int64_t)chunk * clen;
+    const int64_t t1 = t0 + clen < len ? t0 + clen : len;
     // FROM_QKV: the cache holds positions < pos; position pos comes from qkv
     // and is folded in by the one chunk that contains it
     const bool holds_pos = FROM_QKV && t1 == len;
@@ -448,10 +469,11 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     }
     const int64_t len = a.pos_dev != nullptr ? *a.pos_dev + 1 : a.len;
     const int64_t pos = len - 1;
-    const int nact = (int)((len + kAttnChunk - 1) / kAttnChunk);
+    const int64_t clen = gqa_chunk_len(len, nchunks);
+    const int nact = (int)((len + clen - 1) / clen);
     if (chunk >= nact) return;
-    const int64_t t0 = (int64_t)chunk * kAttnChunk;
-    const int64_t t1 = t0 + kAttnChunk < len ? t0 + kAttnChunk : len;
+    const int64_t t0 = (int64_t)chunk * clen;
+    const int64_t t1 = t0 + clen < len ? t0 + clen : len;
     const int QKV = (a.QH + 2 * a.KVH) * HD;
     Tiles& tl = reinterpret_cast<Tiles*>(lds)[wave];
 
@@ -971,7 +993,7 @@ static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void
                         int64_t QH, int64_t KVH, int64_t HD, hipStream_t st,
                         const DepthRead* depth = nullptr) {
     const int G = (int)(QH / KVH);
-    const int nchunks = (int)ceil_div(len, kAttnChunk);
+    const int nchunks = gqa_nchunks(B, KVH, len);
     // the depth read rides in the attention grid when the rows can take the
     // paired 4-byte loads of depth_row (else it is its own launch, after)
     const bool fuse_depth =
@@ -1129,7 +1151,7 @@ using namespace loom;
 extern "C" int64_t loom_gqa_workspace_bytes(int64_t B, int64_t max_len, int64_t QH, int64_t KVH,
                                             int64_t HD) {
     const int64_t G = QH / KVH;
-    const int64_t nchunks = ceil_div(max_len, kAttnChunk);
+    const int64_t nchunks = gqa_nchunks(B, KVH, max_len);
     return B * KVH * nchunks * (2 * G + 2 * G * HD) * (int64_t)sizeof(float);
 }
 

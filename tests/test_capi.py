@@ -30,8 +30,9 @@ def test_library_exports_every_declared_symbol():
     compute = [s for s in syms if s not in ("loom_last_error", "loom_abi_version")]
     bound = set(_lib.SIGNATURES) | set(_lib.QUERIES)
     assert set(compute) == bound, set(compute) ^ bound
-    # chunk records [B, KVH, chunks of 256, record] fp32
-    assert lib.loom_gqa_workspace_bytes(2, 300, 8, 2, 96) == 2 * 2 * 2 * (8 + 2 * 4 * 96) * 4
+    # chunk records [B, KVH, chunks, record] fp32; chunks = min(~1.5 blocks per CU over
+    # the B*KVH rows, ceil(max_len / 128)) = min(96, 3) with no device (256 CUs assumed)
+    assert lib.loom_gqa_workspace_bytes(2, 300, 8, 2, 96) == 2 * 2 * 3 * (8 + 2 * 4 * 96) * 4
     # the ctypes mirror of the descriptor struct has the C layout
     assert lib.loom_linear_multi_desc_bytes() == ctypes.sizeof(_lib.LinearMultiDesc)
     assert lib.loom_ffn_decode_desc_bytes() == ctypes.sizeof(_lib.FfnDecodeDesc)

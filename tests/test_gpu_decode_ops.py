@@ -90,7 +90,8 @@ def test_rope_append(dtype):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("B,QH,KVH,HD,length", [(4, 8, 2, 96, 1), (2, 8, 2, 96, 255), (2, 8, 2, 96, 256),
                                                  (2, 8, 2, 96, 257), (3, 8, 2, 96, 1000),
-                                                 (3, 4, 2, 8, 37), (2, 4, 1, 64, 300)])
+                                                 (3, 4, 2, 8, 37), (2, 4, 1, 64, 300),
+                                                 (32, 8, 2, 96, 2100)])
 def test_gqa_decode_attention(dtype, B, QH, KVH, HD, length):
     from loom_amd import _lib
     max_len = length + 5
