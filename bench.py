@@ -245,9 +245,9 @@ def bench_tr_pipeline(iters):
 
 
 def bench_gqa(iters):
-    """The decode step's attention (its largest kernel): B=32, 8 q heads over 2
-    kv heads of 96, a head-major bf16 cache at 2176 positions (the middle of
-    the timed decode), RoPE + append + attention + merge in one launch."""
+    """The decode step's attention: B=32, 8 q heads over 2 kv heads of 96, a
+    head-major bf16 cache at 2176 positions (the middle of the timed decode),
+    RoPE + append + attention in one launch and the chunk merge in a second."""
     import torch
     from loom_amd import _lib
 
@@ -271,6 +271,36 @@ def bench_gqa(iters):
                   QH, KVH, HD, _lib.stream_of(qkv))
     ms = timed(fn, iters)
     nbytes = 2 * B * KVH * L * HD * 2
+    return dict(ms=ms, bytes=nbytes, GBs=nbytes / (ms * 1e-3) / 1e9)
+
+
+def bench_decode_gemm(iters):
+    """The decode step's largest kernel class, a weight-streaming projection at
+    M = 32: history K/V (kv_weight [1536, 768]) and W_real ([3072, 768] + bias)
+    of one hidden state in one launch, as the engine issues it.  Weights rotate
+    over 24 sets (170 MB) so consecutive launches do not find them in cache."""
+    import torch
+    from loom_amd import _lib
+
+    dev, bf = "cuda", torch.bfloat16
+    B, N, H, NS = 32, 768, 3072, 24
+    g = torch.Generator(device=dev).manual_seed(7)
+    x = torch.randn(B, N, generator=g, device=dev).to(bf)
+    kvw = [(torch.randn(2 * N, N, generator=g, device=dev) * 0.03).to(bf) for _ in range(NS)]
+    w1r = [(torch.randn(H, N, generator=g, device=dev) * 0.03).to(bf) for _ in range(NS)]
+    b1r = torch.zeros(H, device=dev)
+    o_kv = torch.empty(B, 2 * N, device=dev, dtype=bf)
+    o_r = torch.empty(B, H, device=dev, dtype=bf)
+    descs = [_lib.linear_multi_desc(x, [dict(w=kvw[i], out=o_kv), dict(w=w1r[i], out=o_r, bias=b1r)])
+             for i in range(NS)]
+    it = [0]
+
+    def fn():
+        d = descs[it[0] % NS]
+        it[0] += 1
+        _lib.call("loom_linear_multi", 1, _lib.ctypes.byref(d), _lib.stream_of(x))
+    ms = timed(fn, max(iters, NS))
+    nbytes = (2 * N + H) * N * 2 + B * N * 2 + B * (2 * N + H) * 2
     return dict(ms=ms, bytes=nbytes, GBs=nbytes / (ms * 1e-3) / 1e9)
 
 
@@ -436,6 +466,8 @@ def main():
         log(f"TR pipeline: {json.dumps({k: round(v, 3) for k, v in trp.items()})}")
         gq = bench_gqa(args.micro_iters)
         log(f"GQA decode: {json.dumps({k: round(v, 3) for k, v in gq.items()})}")
+        dg = bench_decode_gemm(args.micro_iters)
+        log(f"decode GEMM: {json.dumps({k: round(v, 3) for k, v in dg.items()})}")
         copy_gbs = copy_bandwidth()
         kernels = {
             "paraplex_pointwise": {"ms": px["pointwise_ms"], "GB/s": px["pointwise_GBs"],
@@ -454,6 +486,8 @@ def main():
                         "frac": px["w2_TFLOPs"] / BF16_PEAK_TFLOPS},
             "gqa_decode_ctx2176": {"ms": gq["ms"], "GB/s": gq["GBs"], "frac": gq["GBs"] / HBM_PEAK_GBS,
                                    "algorithmic_bytes": gq["bytes"]},
+            "decode_gemm_kv_wreal_m32": {"ms": dg["ms"], "GB/s": dg["GBs"], "frac": dg["GBs"] / HBM_PEAK_GBS,
+                                         "algorithmic_bytes": dg["bytes"]},
             "paraplex_ffn_total_ms": px["ffn_ms"],
             "device_copy_GB/s": copy_gbs,
         }
