@@ -933,8 +933,9 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
     const int64_t ntiles = ceil_div(g.n, 16);
     for (int s2 = 0; s2 <= kMaxSeg; ++s2) a.nstart[s2] = s2 == 0 ? 0 : ntiles * 16;
     const int64_t steps = ceil_div(d->k, 32) + ceil_div(d->k2, 32);
-    // enough k-splits to give every CU a block, at least 4 k-steps per split
-    int64_t ns = ceil_div(4 * (int64_t)device_cus() / 4, ntiles);
+    // about two blocks per CU (up to kMaxSplit k-splits; measured best over 1x-4x),
+    // at least 4 k-steps per split
+    int64_t ns = ceil_div(2 * (int64_t)device_cus(), ntiles);
     if (ns > kMaxSplit) ns = kMaxSplit;
     if (ns > steps / 4) ns = steps / 4 > 0 ? steps / 4 : 1;
     a.nsplit = (int)ns;
