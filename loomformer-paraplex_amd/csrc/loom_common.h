@@ -318,26 +318,6 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
-// ------------------------------------------------------------------ cross-block hand-off
-// Device-coherent single-word store/load (relaxed atomics at agent scope: one
-// store/load with the sc1 bit, which goes through to the coherence point; no
-// whole-cache write-back or invalidate, unlike __threadfence()).  A block
-// publishes data with st_coherent, waits for its stores (__syncthreads waits
-// on vmcnt), then bumps an arrival counter; the block that arrives last reads
-// the data with ld_coherent.
-__device__ __forceinline__ void st_coherent(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_coherent(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int arrive(int* counter) {
-    return __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void reset_counter(int* counter) {
-    __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace loom
