@@ -22,13 +22,33 @@ constexpr int kTriaThreads = 256;
 template <typename T>
 __device__ __forceinline__ void stage_in(float* lds, const T* src, int n9) {
     constexpr int V = 16 / (int)sizeof(T);
+    // pieces per thread when the block stages kTriaThreads records of 9
+    constexpr int kPer = (kTriaThreads * 9 / V + kTriaThreads - 1) / kTriaThreads;
     if (((uintptr_t)src & 15) == 0 && n9 % V == 0) {
-        for (int c = threadIdx.x; c < n9 / V; c += blockDim.x) {
+        // every piece requested before the first LDS store (one memory round
+        // trip per block), nontemporally: each record is read once
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 w[kPer];
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) {
+            const int c = threadIdx.x + r * kTriaThreads;
+            if (c < n9 / V) w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + c);
+        }
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) {
+            const int c = threadIdx.x + r * kTriaThreads;
+            if (c >= n9 / V) continue;
             float v[V];
-            if constexpr (V == 8) Vec8<T>::load(src + c * 8, v);
-            else {
-                const float4 x = *reinterpret_cast<const float4*>(src + c * 4);
-                v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+            if constexpr (V == 8) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const T lo{(uint16_t)(w[r][k] & 0xffffu)}, hi{(uint16_t)(w[r][k] >> 16)};
+                    v[2 * k] = ld(&lo);
+                    v[2 * k + 1] = ld(&hi);
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[k] = __uint_as_float(w[r][k]);
             }
 #pragma unroll
             for (int e = 0; e < V; ++e) lds[c * V + e] = v[e];

@@ -86,19 +86,20 @@ __device__ __forceinline__ const char* uniform_ptr(const char* p) {
 // scalar and each lane adds only its 32-bit byte offset, so a load costs no
 // vector address arithmetic.  Offsets past `bytes` read zero.
 constexpr int kBufferDword3 = 0x00020000;   // gfx9 raw-buffer format word
+constexpr int kBufNT = 2;                   // cache policy: nontemporal (r, i, o are read once)
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const char* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void*)uniform_ptr(base), (short)0, (int)bytes,
                                              kBufferDword3);
 }
 template <typename T> __device__ __forceinline__ float ld_buf(__amdgpu_buffer_rsrc_t r, uint32_t off);
 template <> __device__ __forceinline__ float ld_buf<float>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, kBufNT));
 }
 template <> __device__ __forceinline__ float ld_buf<bf16_t>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0));
+    return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, kBufNT));
 }
 template <> __device__ __forceinline__ float ld_buf<f16_t>(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __half2float(__ushort_as_half(__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0)));
+    return __half2float(__ushort_as_half(__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, kBufNT)));
 }
 
 // Byte offsets of a layer slice: 32-bit when one slice is under 4 GiB (the
