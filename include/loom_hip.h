@@ -126,6 +126,8 @@ typedef struct {
     int64_t m;
     int32_t nseg;         /* 1..4 */
     loom_linear_segment seg[4];
+    const uint8_t* only_if;   /* optional [only_if_n] device flags: when none is set the */
+    int64_t only_if_n;        /* bf16 fused launch leaves every output untouched */
 } loom_linear_multi_desc;
 
 /* Several decode projections in one launch (no counterpart in the reference;
@@ -135,7 +137,10 @@ typedef struct {
  * Concatenation along k sums two products in one accumulator (o-projection
  * plus depth read-out before LayerNorm); segments share x (e.g. the depth
  * history projection and W_real of the same hidden state).  bf16 with m <= 64
- * runs as one fused MFMA launch; other dtypes run one product per piece. */
+ * runs as one fused MFMA launch; other dtypes run one product per piece.
+ * only_if (may be NULL) lets a captured step skip a product it needs only on
+ * some steps: the fused launch reads the flags on the device and does nothing
+ * when none is set (the other paths compute the product anyway). */
 int loom_linear_multi(int dtype, const loom_linear_multi_desc* desc, void* stream);
 
 /* sizeof(loom_linear_multi_desc), so an FFI binding can check its layout. */
@@ -444,6 +449,9 @@ int loom_tria_decode_temporal(int dtype, const void* depth, const void* prev,
  * proj_w^T + proj_b (proj_w [32,9]), a_out[b] = z @ up_w^T + up_b (up_w [N,32],
  * 16-byte aligned).  pooled and z are rounded to dtype between the steps as the
  * separate ops store them.  proj_b, up_b: fp32 or NULL.  H <= 32768.
+ * With fire != NULL and no row firing, only doc is written (the readout
+ * feeds only the keys staged at a fire, tria.py:1576-1582); a_out is left as
+ * it is.
  * workspace: fp32 scratch of loom_decode_tria_readout_workspace_bytes(B, H)
  * bytes (per-block pool records); two launches on stream.  Replaces
  * loom_tria_decode_temporal + loom_slot_attention_pool_forward + two

@@ -817,6 +817,9 @@ decode_temporal_kernel(const T* __restrict__ depth, const T* __restrict__ prev,
 //   decode_readout_rows_kernel, grid (N / kReadCols, B): merges row b's
 //     records into pooled, then proj Linear(9, 32) and kReadCols outputs of up
 //     Linear(32, N) (tria.py:1436-1441).
+// The readout feeds only the final-CA keys staged at a fire (tria.py:1576-1582),
+// so with fire flags given and none set both launches stop after the state
+// update and a_out is left as it is.
 // pooled and z are rounded to T before use, as the unfused ops store them.
 constexpr int kReadHeads = 256;
 constexpr int kReadCols = 128;
@@ -858,6 +861,12 @@ decode_readout_heads_kernel(const T* __restrict__ depth, const T* prev,
         }
         m = sc;
         l = 1.0f;                          // one head: p = e^(sc - m) = 1
+    }
+    // the readout feeds only the keys staged at a fire: without one, stop here
+    if (fire != nullptr) {
+        bool any = false;
+        for (int q = 0; q < (int)gridDim.y; ++q) any |= fire[q] != 0;
+        if (!any) return;
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -901,7 +910,8 @@ template <typename T>
 __global__ void __launch_bounds__(kReadCols)
 decode_readout_rows_kernel(const float* __restrict__ rec, int nrec, const T* __restrict__ proj_w,
                            const float* __restrict__ proj_b, const T* __restrict__ up_w,
-                           const float* __restrict__ up_b, T* __restrict__ a_out, int N) {
+                           const float* __restrict__ up_b, T* __restrict__ a_out, int N,
+                           const uint8_t* __restrict__ fire) {
     constexpr int kMaxRec = kReadCols;     // records per row (H <= kReadHeads * kReadCols)
     __shared__ float rs[kMaxRec * kReadRec];
     __shared__ float xs[9];
@@ -909,6 +919,11 @@ decode_readout_rows_kernel(const float* __restrict__ rec, int nrec, const T* __r
     const int tid = threadIdx.x;
     const int64_t b = blockIdx.y;
     const int n = blockIdx.x * kReadCols + tid;
+    if (fire != nullptr) {                 // no fire: no key to stage, a_out is left as it is
+        bool any = false;
+        for (int q = 0; q < (int)gridDim.y; ++q) any |= fire[q] != 0;
+        if (!any) return;
+    }
     // every load first: this row's records, the proj row of thread tid < 32 and
     // the up row of column n
     const float* rb = rec + b * nrec * kReadRec;
@@ -1131,7 +1146,7 @@ static int readout_dispatch(const void* depth, const void* prev, const uint8_t* 
     if (rc != LOOM_OK) return rc;
     hipLaunchKernelGGL((decode_readout_rows_kernel<T>), dim3((unsigned)ceil_div(N, kReadCols), (unsigned)B),
                        dim3(kReadCols), 0, st, ws, nrec, (const T*)proj_w, proj_b, (const T*)up_w,
-                       up_b, (T*)a_out, (int)N);
+                       up_b, (T*)a_out, (int)N, fire);
     return launch_status("loom_decode_tria_readout");
 }
 

@@ -428,6 +428,8 @@ struct LinArgs {
     float* partial;
     int64_t ldp;
     int nsplit;
+    const uint8_t* only_if;   // with only_if_n flags: the launch does nothing unless one is set
+    int only_if_n;
 };
 
 template <int MT, int NW, int UN>
@@ -435,6 +437,11 @@ __global__ void __launch_bounds__(NW * 64)
 gemm_bf16_skinny_multi_kernel(LinArgs a) {
     __shared__ float red[NW][MT][4][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (a.only_if != nullptr) {              // block-uniform: every thread reads all flags
+        bool any = false;
+        for (int i = 0; i < a.only_if_n; ++i) any |= a.only_if[i] != 0;
+        if (!any) return;
+    }
     const int64_t ng = (int64_t)blockIdx.x * 16;
     int s = 0;
 #pragma unroll
@@ -764,6 +771,8 @@ static int linear_multi_dispatch(const loom_linear_multi_desc& d, hipStream_t st
         a.X = (const uint16_t*)d.x; a.ldx = d.ldx; a.K = d.k;
         a.X2 = (const uint16_t*)d.x2; a.ldx2 = d.ldx2; a.K2 = d.k2;
         a.M = d.m; a.nseg = d.nseg; a.nsplit = 1;
+        a.only_if = d.only_if;
+        a.only_if_n = (int)d.only_if_n;
         int64_t ncols = 0;
         for (int s = 0; s < d.nseg; ++s) {
             const loom_linear_segment& g = d.seg[s];
@@ -805,6 +814,8 @@ extern "C" int64_t loom_linear_multi_desc_bytes(void) { return (int64_t)sizeof(l
 extern "C" int loom_linear_multi(int dtype, const loom_linear_multi_desc* d, void* stream) {
     clear_error();
     LOOM_CHECK(d != nullptr && d->x != nullptr, "linear_multi: null descriptor or input");
+    LOOM_CHECK(d->only_if == nullptr || (d->only_if_n >= 1 && d->only_if_n <= 1024),
+               "linear_multi: only_if_n=%lld outside [1, 1024]", (long long)d->only_if_n);
     LOOM_CHECK(d->nseg >= 1 && d->nseg <= kMaxSeg, "linear_multi: nseg=%d outside [1, %d]",
                (int)d->nseg, kMaxSeg);
     LOOM_CHECK(d->m >= 0 && d->k >= 1 && d->ldx >= d->k && d->k2 >= 0,

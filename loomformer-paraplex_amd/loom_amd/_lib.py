@@ -28,7 +28,7 @@ class LinearMultiDesc(ctypes.Structure):
     """loom_linear_multi_desc (include/loom_hip.h)."""
     _fields_ = [("x", c_void_p), ("ldx", c_int64), ("k", c_int64), ("x2", c_void_p),
                 ("ldx2", c_int64), ("k2", c_int64), ("m", c_int64), ("nseg", ctypes.c_int32),
-                ("seg", LinearSegment * 4)]
+                ("seg", LinearSegment * 4), ("only_if", c_void_p), ("only_if_n", c_int64)]
 
 # name -> argument types (all return c_int status)
 SIGNATURES = {
@@ -158,10 +158,11 @@ class FfnDecodeDesc(ctypes.Structure):
                 ("alpha", c_float), ("axis", ctypes.c_int32)]
 
 
-def linear_multi_desc(x, segments, x2=None, m=None):
+def linear_multi_desc(x, segments, x2=None, m=None, only_if=None):
     """Build a LinearMultiDesc.  x, x2: [m, k] tensors (row-strided views are
     fine); segments: dicts with w, out and optional w2, bias, gate_p,
-    gate_alpha (tensors keep their own row strides)."""
+    gate_alpha (tensors keep their own row strides); only_if: optional uint8
+    device flags (the fused launch skips the product when none is set)."""
     d = LinearMultiDesc()
     d.x, d.ldx, d.k = x.data_ptr(), x.stride(0), x.shape[1]
     if x2 is not None:
@@ -170,6 +171,8 @@ def linear_multi_desc(x, segments, x2=None, m=None):
     if not 1 <= len(segments) <= 4:
         raise ValueError("linear_multi takes 1 to 4 segments")
     d.nseg = len(segments)
+    if only_if is not None:
+        d.only_if, d.only_if_n = only_if.data_ptr(), only_if.numel()
     for i, sg in enumerate(segments):
         e = d.seg[i]
         w, out = sg["w"], sg["out"]

@@ -180,12 +180,12 @@ class LoomDecoder:
         self._call("loom_linear", self.code, _P(x), ldx or K, _P(w), K, _P(bias), _P(gate_p),
                    float(gate_alpha), _P(residual), _P(out), ldc or Nout, M, Nout, K, self._stream())
 
-    def _multi(self, key, x, segments, x2=None) -> None:
+    def _multi(self, key, x, segments, x2=None, only_if=None) -> None:
         """loom_linear_multi with a descriptor built once per call site (every
         pointer in it is a persistent engine buffer or weight)."""
         d = self._descs.get(key)
         if d is None:
-            d = _lib.linear_multi_desc(x, segments, x2=x2)
+            d = _lib.linear_multi_desc(x, segments, x2=x2, only_if=only_if)
             self._descs[key] = d
         self._call("loom_linear_multi", self.code, _lib.ctypes.byref(d), self._stream())
 
@@ -300,10 +300,11 @@ class LoomDecoder:
                    _P(self.fire), _P(self.doc), _P(self.score_w), _P(self.proj_w), _P(self.proj_b),
                    _P(self.up_w), _P(self.up_b), _P(self.a_t), _P(self.rd_ws), self.rd_ws_bytes, B, H, N,
                    float(c.polarm_beta), 1e-6, st)
-        # ---- final cross-attention step (tria.py:1560-1595): stage k/v, append on
-        # fire (+ end-of-step bookkeeping), then attend over the appended keys
+        # ---- final cross-attention step (tria.py:1560-1595): stage k/v (computed
+        # only on steps where a row fires, as the readout above), append on fire
+        # (+ end-of-step bookkeeping), then attend over the appended keys
         self._multi("stage", self.a_t, [dict(w=self.wqk, out=self.stage_k),
-                                        dict(w=self.wv, out=self.stage_v)])
+                                        dict(w=self.wv, out=self.stage_v)], only_if=self.fire)
         self._call("loom_decode_epilogue", self.code, _P(self.stage_k), _P(self.stage_v),
                    _P(self.ca_k), _P(self.ca_v), _P(self.ca_valid), _P(self.ca_len), _P(self.fire),
                    _P(self.pending), _P(self.pos_dev), B, N, self.max_keys, st)

@@ -348,6 +348,16 @@ def test_decode_tria_readout(dtype, H, N):
              S(depth))
     check(doc, wd, dtype)
     check(a, wa, dtype)
+    # no row fires: the state is updated, the readout (keys for a fire) is not
+    calm = torch.zeros(B, dtype=torch.uint8, device=DEV)
+    doc = prev.clone()
+    a.fill_(3.0)
+    L().call("loom_decode_tria_readout", code(depth), P(depth), P(doc), P(reset_d), P(calm),
+             P(doc), P(sw), P(pw), P(pb), P(uw), P(ub), P(a), P(ws), nb, B, H, N, 0.1, 1e-6,
+             S(depth))
+    D, Pv = host(depth), host(prev)
+    check(doc, rnd(torch.where(reset.bool()[:, None, None, None], D, ref.local_normalize(D @ Pv))), dtype)
+    assert bool((a == 3.0).all())
     # first token: no previous state (no reset flags needed)
     wd, wa = want(host(depth), None)
     L().call("loom_decode_tria_readout", code(depth), P(depth), None, None, P(fire_d), P(doc),
@@ -398,6 +408,17 @@ def test_linear_multi(dtype, M):
     d = _lib.linear_multi_desc(x, [dict(w=wa, w2=wc, out=out, bias=bb)], x2=x3)
     _lib.call("loom_linear_multi", code(x), ctypes.byref(d), S(x))
     check(out, X @ host(wa).T + host(x3) @ host(wc).T + host(bb), dtype)
+    # device flags: with none set the bf16 fused launch leaves the outputs as
+    # they are; with one set it computes them
+    flags = torch.zeros(5, dtype=torch.uint8, device=DEV)
+    out3 = torch.full((M, 96), 7.0, device=DEV, dtype=dtype)
+    d = _lib.linear_multi_desc(x, [dict(w=w1, out=out3, bias=b1)], only_if=flags)
+    _lib.call("loom_linear_multi", code(x), ctypes.byref(d), S(x))
+    if dtype == torch.bfloat16:
+        assert bool((out3 == 7.0).all())
+    flags[3] = 1
+    _lib.call("loom_linear_multi", code(x), ctypes.byref(d), S(x))
+    check(out3, X @ host(w1).T + host(b1), dtype)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
