@@ -46,6 +46,10 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Dword 3 of a gfx9 raw-buffer descriptor (untyped 32-bit data format).
+constexpr int kBufferDword3 = 0x00020000;
 
 // two floats -> packed bf16 pair (low = a), one conversion instruction
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
@@ -118,7 +122,6 @@ template <> struct Vec8<bf16_t> : Vec8_16<bf16_t> {
     }
     // write-once output: one nontemporal 16-byte store
     __device__ __forceinline__ static void store_nt(bf16_t* p, const float v[8]) {
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
         const u32x4 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
                          pack_bf16x2(v[6], v[7])};
         __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(p));

@@ -5,7 +5,10 @@
 // phase I_base[t-1] is carried in registers from the previous iteration, so
 // the only extra HBM read is one beta row per chunk (1/TC overhead).  Loads
 // and stores are whole 16-byte vectors, so a wavefront touches 64*16 = 1 KiB
-// of contiguous memory per tensor and per token.
+// of contiguous memory per tensor and per token.  Aligned rows (H % 8 == 0)
+// go to paraplex_chunk_kernel, whose blocks each cover one (row, chunk) so
+// that addressing and loop control are scalar; the rest to
+// paraplex_forward_kernel.
 #include <type_traits>
 
 #include "loom_common.h"
@@ -85,6 +88,7 @@ struct VecIO {
 };
 
 constexpr int kPxPrefetch = 2;   // tokens of R / beta (/ gate_src) in flight per thread
+constexpr int kPxUnrolled = 16;  // longest token chunk; a full chunk runs unrolled
 
 template <typename T, int VEC, bool SAME_GATE, bool HAS_RESET>
 __global__ void __launch_bounds__(256)
@@ -180,6 +184,200 @@ paraplex_forward_kernel(const T* __restrict__ p_real, const T* __restrict__ gate
     if (t0 + n == T_) VecIO<T, VEC>::store(next_trace + (int64_t)b * H + h0, prev);
 }
 
+// Eight elements as 16-byte raw-buffer pieces (one for 16-bit types, two for
+// fp32).  `soff` is a scalar byte offset shared by the wave, `voff` the lane's.
+constexpr int kBufCoherent = 0;
+constexpr int kBufStream = 2;      // nontemporal: write-once outputs
+template <typename T>
+__device__ __forceinline__ void buf_load8(RawVec<T, 8>& v, __amdgpu_buffer_rsrc_t r,
+                                          uint32_t voff, uint32_t soff) {
+#pragma unroll
+    for (int q = 0; q < RawVec<T, 8>::NW / 4; ++q) {
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(voff + 16 * q), (int)soff,
+                                                              kBufCoherent);
+        v.w[4 * q] = x.x; v.w[4 * q + 1] = x.y; v.w[4 * q + 2] = x.z; v.w[4 * q + 3] = x.w;
+    }
+}
+// Eight outputs packed into the 16-byte pieces a store writes.
+template <typename T>
+struct Packed8 {
+    static constexpr int NQ = sizeof(T) == 4 ? 2 : 1;
+    u32x4 q[NQ];
+};
+template <typename T>
+__device__ __forceinline__ Packed8<T> pack8(const float v[8]) {
+    Packed8<T> x;
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+            x.q[q] = (u32x4){__float_as_uint(v[4 * q]), __float_as_uint(v[4 * q + 1]),
+                             __float_as_uint(v[4 * q + 2]), __float_as_uint(v[4 * q + 3])};
+    } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if constexpr (std::is_same<T, bf16_t>::value) {
+                w[k] = pack_bf16x2(v[2 * k], v[2 * k + 1]);
+            } else {
+                T lo, hi;
+                st(&lo, v[2 * k]);
+                st(&hi, v[2 * k + 1]);
+                w[k] = (uint32_t)lo.x | ((uint32_t)hi.x << 16);
+            }
+        }
+        x.q[0] = (u32x4){w[0], w[1], w[2], w[3]};
+    }
+    return x;
+}
+template <typename T>
+__device__ __forceinline__ void buf_store8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                           const Packed8<T>& x) {
+#pragma unroll
+    for (int q = 0; q < Packed8<T>::NQ; ++q)
+        __builtin_amdgcn_raw_buffer_store_b128(x.q[q], r, (int)(voff + 16 * q), (int)soff,
+                                               sizeof(T) == 2 ? kBufStream : kBufCoherent);
+}
+// Keeps a stored vector's registers reserved up to this point.  A VALU write
+// issued right after a 16-byte buffer store to the store's own data registers
+// has been seen to reach memory in place of the stored data (a few lanes of
+// the first dword), so the chain keeps each token's store data untouched until
+// the next token's stores are issued.
+template <typename T>
+__device__ __forceinline__ void hold(const Packed8<T>& x) {
+#pragma unroll
+    for (int q = 0; q < Packed8<T>::NQ; ++q) asm volatile("" ::"v"(x.q[q]));
+}
+
+// The same chain with one block per (batch row, token chunk, run of hidden
+// units): the chunk bounds, the token loop and the reset flags are uniform
+// across the block, and every tensor access is a raw-buffer access over the
+// chunk's slice with the lane's 32-bit byte offset (its hidden units) and a
+// scalar token offset, so the loop spends no vector instructions on
+// addresses or loop control.  The host guarantees H % 8 == 0, 16-byte
+// aligned tensors and TC * H * sizeof(T) < 2^31.
+template <typename T, bool SAME_GATE, bool HAS_RESET, int TCU>
+__global__ void __launch_bounds__(256)
+paraplex_chunk_kernel(const T* __restrict__ p_real, const T* __restrict__ gate_src,
+                      const T* __restrict__ beta_lin, const float* __restrict__ bias,
+                      const T* __restrict__ trace, const float* __restrict__ trace_w,
+                      const uint8_t* __restrict__ reset, const float* __restrict__ anchor,
+                      T* __restrict__ act, T* __restrict__ s_out, T* __restrict__ next_trace,
+                      float* __restrict__ anchor_snap, int T_, int H, int TC, float m) {
+    constexpr int VEC = 8;
+    constexpr int PF = kPxPrefetch;
+    const int b = blockIdx.z;
+    const int t0 = blockIdx.y * TC;
+    const int n = min(TC, T_ - t0);
+    const int h0 = (blockIdx.x * blockDim.x + threadIdx.x) * VEC;
+    if ((blockIdx.x | blockIdx.y | blockIdx.z | threadIdx.x) == 0 && anchor_snap != nullptr)
+        anchor_snap[0] = anchor[0];
+    if (h0 >= H) return;
+
+    float bv[VEC], tw[VEC], prev[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+        bv[k] = bias[h0 + k];
+        tw[k] = trace_w[h0 + k];
+    }
+    const int64_t base0 = ((int64_t)b * T_ + t0) * H;
+    if (t0 == 0) {
+        VecIO<T, VEC>::load(trace + (int64_t)b * H + h0, prev);
+    } else {
+        float bl[VEC];
+        VecIO<T, VEC>::load(beta_lin + base0 - H + h0, bl);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) prev[k] = phase_of(bl[k] + bv[k]);
+    }
+    const uint32_t step = (uint32_t)H * (uint32_t)sizeof(T);
+    const uint32_t bytes = (uint32_t)n * step;
+    const uint32_t voff = (uint32_t)h0 * (uint32_t)sizeof(T);
+    const auto rR = __builtin_amdgcn_make_buffer_rsrc((void*)(p_real + base0), (short)0, (int)bytes, kBufferDword3);
+    const auto rG = __builtin_amdgcn_make_buffer_rsrc((void*)(gate_src + base0), (short)0, (int)bytes, kBufferDword3);
+    const auto rB = __builtin_amdgcn_make_buffer_rsrc((void*)(beta_lin + base0), (short)0, (int)bytes, kBufferDword3);
+    const auto rA = __builtin_amdgcn_make_buffer_rsrc((void*)(act + base0), (short)0, (int)bytes, kBufferDword3);
+    const auto rS = __builtin_amdgcn_make_buffer_rsrc((void*)(s_out + base0), (short)0, (int)bytes, kBufferDword3);
+    const uint8_t* prs = HAS_RESET ? reset + (int64_t)b * T_ + t0 : nullptr;
+
+    RawVec<T, VEC> rr[PF], rb[PF], rg[PF];
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+        if (p < n) {
+            buf_load8<T>(rr[p], rR, voff, p * step);
+            buf_load8<T>(rb[p], rB, voff, p * step);
+            if constexpr (!SAME_GATE) buf_load8<T>(rg[p], rG, voff, p * step);
+        }
+    }
+    Packed8<T> keep_s{}, keep_a{};
+    // token `it` from ring slot p; with `refill`, token it+PF's loads go out
+    // ahead of the math (at raised wave priority, so every wave's loads issue early)
+    auto token = [&](int p, int it, bool refill) {
+        float r[VEC], bl[VEC], g[VEC];
+        rr[p].to_float(r);
+        rb[p].to_float(bl);
+        if constexpr (!SAME_GATE) rg[p].to_float(g);
+        // unpacked into registers of their own before the refill is issued, so
+        // the load lands in the slot's registers with no copies
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            asm volatile("" : "+v"(r[k]), "+v"(bl[k]));
+            if constexpr (!SAME_GATE) asm volatile("" : "+v"(g[k]));
+        }
+        if (refill) {
+            __builtin_amdgcn_s_setprio(3);
+            buf_load8<T>(rr[p], rR, voff, (it + PF) * step);
+            buf_load8<T>(rb[p], rB, voff, (it + PF) * step);
+            if constexpr (!SAME_GATE) buf_load8<T>(rg[p], rG, voff, (it + PF) * step);
+            __builtin_amdgcn_s_setprio(0);
+        }
+        const bool rs = HAS_RESET && prs[it] != 0;
+        float so[VEC], ao[VEC];
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            const float s0 = phase_of(bl[k] + bv[k]);
+            const float raw = rs ? s0 : fmaf(prev[k], tw[k], s0);
+            const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
+            float amp, gate;
+            softplus_gate<!std::is_same<T, bf16_t>::value>(SAME_GATE ? r[k] : g[k], m, amp, gate);
+            so[k] = sv;
+            ao[k] = fmaf(amp, sv, r[k]) * gate;
+            prev[k] = s0;
+        }
+        const Packed8<T> xs = pack8<T>(so), xa = pack8<T>(ao);
+        hold(keep_s);
+        hold(keep_a);
+        buf_store8<T>(rS, voff, it * step, xs);
+        buf_store8<T>(rA, voff, it * step, xa);
+        keep_s = xs;
+        keep_a = xa;
+    };
+    if constexpr (TCU > 0) {
+        if (n == TCU) {
+            // a whole chunk as straight-line code: the ring slots are fixed
+            // registers and every wait covers exactly the loads it needs
+#pragma unroll
+            for (int it = 0; it < TCU; ++it) token(it % PF, it, it + PF < TCU);
+            if (t0 + n == T_) VecIO<T, VEC>::store(next_trace + (int64_t)b * H + h0, prev);
+            return;
+        }
+    }
+    // every slot is refilled while PF more tokens follow the group, so the
+    // ring registers are overwritten in place; the last one or two groups
+    // refill only what is left
+    int it0 = 0;
+    for (; it0 + 2 * PF <= n; it0 += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) token(p, it0 + p, true);
+    }
+    for (; it0 < n; it0 += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            if (it0 + p >= n) break;
+            token(p, it0 + p, it0 + p + PF < n);
+        }
+    }
+    if (t0 + n == T_) VecIO<T, VEC>::store(next_trace + (int64_t)b * H + h0, prev);
+}
+
 template <typename T, int VEC>
 __global__ void __launch_bounds__(256)
 phase_sin_kernel(const T* __restrict__ beta, T* __restrict__ out, int64_t nvec) {
@@ -216,9 +414,10 @@ static int launch_paraplex(const void* p_real, const void* gate_src, const void*
                            const uint8_t* reset, const float* anchor, void* act, void* s,
                            void* next_trace, float* anchor_snap, int64_t B, int64_t T_,
                            int64_t H, float m, hipStream_t stream) {
-    // Tokens per thread: the longest run of t that still gives every SIMD at
-    // least 3 waves (enough to hide memory latency behind the math).  Longer
-    // runs mean fewer per-chunk restarts (each recomputes one carried phase).
+    // Tokens per thread: the longest run of t, up to kPxUnrolled, that still
+    // gives every SIMD at least 3 waves (enough to hide memory latency behind
+    // the math).  Longer runs mean fewer per-chunk restarts (each reads one
+    // more beta row, 1/TC of the beta stream).
     const int64_t HV = H / VEC;
     const bool same = gate_src == p_real;
     auto kern = same ? (reset ? paraplex_forward_kernel<T, VEC, true, true>
@@ -226,9 +425,31 @@ static int launch_paraplex(const void* p_real, const void* gate_src, const void*
                      : (reset ? paraplex_forward_kernel<T, VEC, false, true>
                               : paraplex_forward_kernel<T, VEC, false, false>);
     const int64_t simds = 4 * (int64_t)device_cus();
-    int TC = 64;
+    int TC = kPxUnrolled;
     while (TC > 1 && B * ceil_div(T_, TC) * HV < 3 * 64 * simds) --TC;
     const int64_t nchunks = ceil_div(T_, TC);
+    if (VEC == 8 && nchunks <= 65535 && B <= 65535 &&
+        (int64_t)TC * H * (int64_t)sizeof(T) < ((int64_t)1 << 31)) {
+        // one block per (b, chunk, run of hidden units): the widest block of
+        // 1-4 waves that splits the row's waves evenly
+        const int64_t waves = ceil_div(HV, 64);
+        const int w = waves % 4 == 0 ? 4 : waves % 3 == 0 ? 3 : waves % 2 == 0 ? 2 : (waves < 4 ? (int)waves : 4);
+        const dim3 grid((unsigned)ceil_div(HV, 64 * w), (unsigned)nchunks, (unsigned)B);
+        // a full chunk of 16-bit rows runs as straight-line code (fp32 keeps
+        // the loop: unrolled, its registers would allow only 2 waves per SIMD)
+        auto ck = same ? (reset ? paraplex_chunk_kernel<T, true, true, 0> : paraplex_chunk_kernel<T, true, false, 0>)
+                       : (reset ? paraplex_chunk_kernel<T, false, true, 0> : paraplex_chunk_kernel<T, false, false, 0>);
+        if (TC == kPxUnrolled && sizeof(T) == 2)
+            ck = same ? (reset ? paraplex_chunk_kernel<T, true, true, kPxUnrolled>
+                               : paraplex_chunk_kernel<T, true, false, kPxUnrolled>)
+                      : (reset ? paraplex_chunk_kernel<T, false, true, kPxUnrolled>
+                               : paraplex_chunk_kernel<T, false, false, kPxUnrolled>);
+        hipLaunchKernelGGL(ck, grid, dim3(64 * w), 0, stream, (const T*)p_real,
+                           (const T*)gate_src, (const T*)beta_lin, bias, (const T*)trace, trace_w,
+                           reset, anchor, (T*)act, (T*)s, (T*)next_trace, anchor_snap, (int)T_,
+                           (int)H, TC, m);
+        return launch_status("loom_paraplex_forward");
+    }
     const int64_t total = B * nchunks * HV;
     LOOM_CHECK(total < ((int64_t)1 << 31) && T_ < ((int64_t)1 << 31) && H < ((int64_t)1 << 31),
                "paraplex: %lld x %lld x %lld exceeds the 32-bit thread index", (long long)B,

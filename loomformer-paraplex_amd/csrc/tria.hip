@@ -27,7 +27,6 @@ __device__ __forceinline__ void stage_in(float* lds, const T* src, int n9) {
     if (((uintptr_t)src & 15) == 0 && n9 % V == 0) {
         // every piece requested before the first LDS store (one memory round
         // trip per block), nontemporally: each record is read once
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
         u32x4 w[kPer];
 #pragma unroll
         for (int r = 0; r < kPer; ++r) {

@@ -85,7 +85,6 @@ __device__ __forceinline__ const char* uniform_ptr(const char* p) {
 // Raw buffer loads over one layer slice: the descriptor (base, byte size) is
 // scalar and each lane adds only its 32-bit byte offset, so a load costs no
 // vector address arithmetic.  Offsets past `bytes` read zero.
-constexpr int kBufferDword3 = 0x00020000;   // gfx9 raw-buffer format word
 constexpr int kBufNT = 2;                   // cache policy: nontemporal (r, i, o are read once)
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const char* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc((void*)uniform_ptr(base), (short)0, (int)bytes,

@@ -64,6 +64,9 @@ DTYPES = [torch.float32, torch.bfloat16]
 @pytest.mark.parametrize("B,T,H,same_gate,with_reset", [
     (2, 5, 24, True, False), (2, 7, 20, False, True), (3, 37, 3072, True, True),
     (1, 1, 3072, True, False), (32, 1, 3072, True, False), (2, 300, 256, False, False),
+    # chunks of 16 tokens (the unrolled path for 16-bit rows) with a ragged last
+    # chunk, and chunks of 15 tokens
+    (8, 1030, 3072, True, True), (4, 2000, 3072, False, False),
 ])
 def test_paraplex_forward(dtype, B, T, H, same_gate, with_reset):
     from loom_amd import ops
@@ -88,6 +91,11 @@ def test_paraplex_forward(dtype, B, T, H, same_gate, with_reset):
     check(act, w_act, dtype)
     check(nt, w_nt, dtype)
     assert float(snap) == 1.0
+    # a second call writes the same bits (every stored lane holds its own result)
+    act2, s2, nt2, _ = ops.paraplex_forward(r, gs, beta, bias, trace, tw,
+                                            dev(reset, torch.bool) if with_reset else torch.empty(0, dtype=torch.bool, device=DEV),
+                                            anchor, 1, False, 0.99, 3.0)
+    assert torch.equal(act2, act) and torch.equal(s2, s) and torch.equal(nt2, nt)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
