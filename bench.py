@@ -492,14 +492,14 @@ def main():
             "device_copy_GB/s": copy_gbs,
         }
         traffic = measured_traffic()
-        for key, name in (("paraplex_forward_kernel_px", "paraplex_pointwise"),
+        for key, name in (("paraplex_chunk_kernel_px", "paraplex_pointwise"),
                           ("depth_attn_kernel_da", "depth_attn"),
                           ("tria_depth_kernel_step_gate_tr", "tria_step_gate")):
             kernels[name]["hbm_traffic_bytes"] = traffic.get(key)
-        roofline = {"bound": "hbm", "kernel": "paraplex_forward_kernel (PX: 8x1024x3072 bf16)",
+        roofline = {"bound": "hbm", "kernel": "paraplex_chunk_kernel (PX: 8x1024x3072 bf16)",
                     "achieved": px["pointwise_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": px["pointwise_GBs"] / HBM_PEAK_GBS,
-                    "traffic": traffic.get("paraplex_forward_kernel_px"),
+                    "traffic": traffic.get("paraplex_chunk_kernel_px"),
                     "algorithmic_bytes": px["pointwise_bytes"]}
     cpu = None
     cpu_mi = None
