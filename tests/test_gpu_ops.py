@@ -67,6 +67,8 @@ DTYPES = [torch.float32, torch.bfloat16]
     # chunks of 16 tokens (the unrolled path for 16-bit rows) with a ragged last
     # chunk, and chunks of 15 tokens
     (8, 1030, 3072, True, True), (4, 2000, 3072, False, False),
+    # chunks of 8 tokens (the chunked prefill's [32, 128] tokens, the loop form)
+    (32, 128, 3072, True, False),
 ])
 def test_paraplex_forward(dtype, B, T, H, same_gate, with_reset):
     from loom_amd import ops
