@@ -64,8 +64,21 @@ __device__ __forceinline__ void stage_out(T* dst, const float* lds, int n9) {
             float v[V];
 #pragma unroll
             for (int e = 0; e < V; ++e) v[e] = lds[c * V + e];
-            if constexpr (V == 8) Vec8<T>::store(dst + c * 8, v);
-            else *reinterpret_cast<float4*>(dst + c * 4) = make_float4(v[0], v[1], v[2], v[3]);
+            // the staged records are written once: nontemporal 16-byte stores
+            u32x4 x;
+            if constexpr (V == 8) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    T lo, hi;
+                    st(&lo, v[2 * k]);
+                    st(&hi, v[2 * k + 1]);
+                    x[k] = (uint32_t)lo.x | ((uint32_t)hi.x << 16);
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) x[k] = __float_as_uint(v[k]);
+            }
+            __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dst) + c);
         }
         return;
     }
