@@ -100,6 +100,34 @@ def test_paraplex_forward(dtype, B, T, H, same_gate, with_reset):
     assert torch.equal(act2, act) and torch.equal(s2, s) and torch.equal(nt2, nt)
 
 
+@pytest.mark.parametrize("B,T,H,same_gate,with_reset", [
+    (3, 37, 3072, True, True), (8, 1030, 3072, False, True), (2, 7, 20, True, False),
+])
+def test_paraplex_forward_f16(B, T, H, same_gate, with_reset):
+    """fp16 rows through the same kernels (16-bit rows like bf16, with the exact
+    log1p softplus); fp16 keeps 11 significant bits, so the bound is rtol 5e-3."""
+    from loom_amd import ops
+    dtype = torch.float16
+    g = gen(B * 999 + T * 10 + H)
+    r = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    gs = r if same_gate else dev(rnd(g, B, T, H, scale=3.0), dtype)
+    beta = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    bias = dev(rnd(g, H, scale=0.5), torch.float32)
+    trace = dev(rnd(g, B, H, scale=0.5), dtype)
+    tw = dev(torch.rand(H, generator=g) - 0.5, torch.float32)
+    reset = torch.zeros(B, T, dtype=torch.bool)
+    if with_reset:
+        reset[0, min(2, T - 1)] = True
+        reset[-1, 0] = True
+    rs = dev(reset, torch.bool) if with_reset else torch.empty(0, dtype=torch.bool, device=DEV)
+    anchor = torch.ones((), device=DEV)
+    act, s, nt, _ = ops.paraplex_forward(r, gs, beta, bias, trace, tw, rs, anchor, 1, False, 0.99, 3.0)
+    w_act, w_s, w_nt = ref.paraplex_pointwise(host(r), host(gs), host(beta), host(bias), host(trace),
+                                              host(tw), reset if with_reset else None, 3.0)
+    for got, want in ((s, w_s), (act, w_act), (nt, w_nt)):
+        torch.testing.assert_close(host(got), want.float(), rtol=5e-3, atol=2e-3)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_phase_sin_and_pvpowlu(dtype):
     from loom_amd import ops
