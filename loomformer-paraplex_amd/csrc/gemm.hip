@@ -327,16 +327,14 @@ struct FfnArgs {
 __device__ __forceinline__ float bf(uint16_t x) { return bf16_to_f32(x); }
 __device__ __forceinline__ float round_bf(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
+// cp: the carried (or seed) record of element e, loaded by the caller with
+// the rest of the epilogue's operands; used when carry_in is set.
 template <int AXIS>
-__device__ __forceinline__ void ffn_tria(const FfnArgs& f, int64_t e, int64_t m, float r, float i,
-                                         float o) {
+__device__ __forceinline__ void ffn_tria(const FfnArgs& f, int64_t e, float r, float i, float o,
+                                         const float (&cp)[9], bool carry_in) {
     float mt[9], pre[9];
     carrier9<AXIS>(r, i, o, f.alpha, mt);
-    if (f.mode == 1 || (f.mode == 2 && f.valid[m] != 0)) {
-        const uint16_t* src = (f.mode == 1 ? f.prev : f.seed) + e * 9;
-        float cp[9];
-#pragma unroll
-        for (int k = 0; k < 9; ++k) cp[k] = bf(src[k]);
+    if (carry_in) {
         mm3(mt, cp, pre);
     } else {
 #pragma unroll
@@ -367,12 +365,23 @@ ffn_decode_kernel(FfnArgs f) {
         const int64_t m = mi, h = n0 + nn;
         if (m >= f.g.M || h >= H) continue;
         const int64_t e = m * H + h;
+        // every operand of the element is requested before the first store
+        // (the carried record could alias an output, so its loads would
+        // otherwise wait for the Paraplex half), one memory round trip
+        const bool carry_in = f.mode == 1 || (f.mode == 2 && f.valid[m] != 0);
+        float cp[9];
+        if (carry_in) {
+            const uint16_t* src = (f.mode == 1 ? f.prev : f.seed) + e * 9;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) cp[k] = bf(src[k]);
+        }
+        const float tr = bf(f.trace[e]);
+        const float x = bf(f.R[e]);
         const float beta = skinny_sum<MT, NW>(red, mi, nn);
         // Paraplex pointwise, one token: prev phase = the carried trace
         const float s0 = phase_of(beta + f.ib[h]);
-        const float raw = fmaf(bf(f.trace[e]), f.tw[h], s0);
+        const float raw = fmaf(tr, f.tw[h], s0);
         const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
-        const float x = bf(f.R[e]);
         float amp, gate;
         softplus_gate<false>(x, f.m, amp, gate);   // bf16 outputs (see softplus_gate)
         const float act = fmaf(amp, sv, x) * gate;
@@ -382,9 +391,9 @@ ffn_decode_kernel(FfnArgs f) {
         // Tria depth op on (r, i, o) = (R, I, O) as stored
         const float i_ = round_bf(sv), o_ = round_bf(act);
         switch (f.axis) {
-            case 0: ffn_tria<0>(f, e, m, x, i_, o_); break;
-            case 1: ffn_tria<1>(f, e, m, x, i_, o_); break;
-            default: ffn_tria<2>(f, e, m, x, i_, o_); break;
+            case 0: ffn_tria<0>(f, e, x, i_, o_, cp, carry_in); break;
+            case 1: ffn_tria<1>(f, e, x, i_, o_, cp, carry_in); break;
+            default: ffn_tria<2>(f, e, x, i_, o_, cp, carry_in); break;
         }
     }
 }
