@@ -504,7 +504,25 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
         for (int r = 0; r < 4; ++r) red[wave][j][r][lane] = acc[j][r];
     __syncthreads();
     uint16_t* out = (uint16_t*)sg.out;
-    for (int o = tid; o < MT * 256; o += NW * 64) {
+    // the gate and bias operands of all of this thread's outputs are loaded
+    // before its first store (an output could alias them, so later loads
+    // would otherwise wait for the earlier stores' round trip)
+    constexpr int kIt = (MT * 256 + NW * 64 - 1) / (NW * 64);
+    float gmul[kIt], badd[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+        const int o = tid + it * NW * 64;
+        const int64_t m = o >> 4, nidx = n0 + (o & 15);
+        const bool ok = o < MT * 256 && m < a.M && nidx < sg.n && a.partial == nullptr;
+        gmul[it] = (ok && sg.gate_p != nullptr)
+                       ? 1.0f + sg.gate_alpha * ld((const bf16_t*)sg.gate_p + m * sg.gate_ld + nidx)
+                       : 1.0f;
+        badd[it] = (ok && sg.bias != nullptr) ? sg.bias[nidx] : 0.0f;
+    }
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+        const int o = tid + it * NW * 64;
+        if (o >= MT * 256) break;
         const int nn = o & 15, mi = o >> 4;
         const int j = mi >> 4, ml = mi & 15;
         const int64_t m = mi, nidx = n0 + nn;
@@ -517,9 +535,8 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
             a.partial[((int64_t)blockIdx.y * a.M + m) * a.ldp + nidx] = v;
             continue;
         }
-        if (sg.gate_p != nullptr)
-            v *= 1.0f + sg.gate_alpha * ld((const bf16_t*)sg.gate_p + m * sg.gate_ld + nidx);
-        if (sg.bias != nullptr) v += sg.bias[nidx];
+        v *= gmul[it];
+        v += badd[it];
         out[m * sg.ldc + nidx] = f32_to_bf16(v);
     }
 }
