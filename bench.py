@@ -101,6 +101,7 @@ def bench_decode(args):
     eng.prefill(prompt)
     torch.cuda.synchronize()
     t_prefill = time.perf_counter() - t0
+    eng.warm_graphs()                                  # capture every graph replay_steps uses
     eng.replay_steps(W)                                # warm-up greedy steps
     torch.cuda.synchronize()
     log(f"prefill {t_prefill * 1e3:.1f} ms ({B * P / t_prefill:.0f} tokens/s); timing {K} greedy steps")

@@ -229,23 +229,22 @@ __device__ __forceinline__ Packed8<T> pack8(const float v[8]) {
     }
     return x;
 }
+// 16-byte raw-buffer stores take their whole offset in the VGPR operand and a
+// constant-zero soffset.  A VALU write to the data registers of a store wider
+// than 8 bytes, issued in the next cycle, can reach memory in place of the
+// stored data (the ">8-byte store data" hazard).  The compiler's hazard
+// recognizer inserts the wait state for this hazard only when soffset is not a
+// register; with the token offset in an SGPR soffset it placed such writes
+// back to back after the store, and a few lanes of the first dword then held
+// the next instruction's result.  With soffset = 0 the wait states are
+// inserted (one v_add per token forms the offset).
 template <typename T>
 __device__ __forceinline__ void buf_store8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                            const Packed8<T>& x) {
 #pragma unroll
     for (int q = 0; q < Packed8<T>::NQ; ++q)
-        __builtin_amdgcn_raw_buffer_store_b128(x.q[q], r, (int)(voff + 16 * q), (int)soff,
+        __builtin_amdgcn_raw_buffer_store_b128(x.q[q], r, (int)(voff + soff + 16 * q), 0,
                                                sizeof(T) == 2 ? kBufStream : kBufCoherent);
-}
-// Keeps a stored vector's registers reserved up to this point.  A VALU write
-// issued right after a 16-byte buffer store to the store's own data registers
-// has been seen to reach memory in place of the stored data (a few lanes of
-// the first dword), so the chain keeps each token's store data untouched until
-// the next token's stores are issued.
-template <typename T>
-__device__ __forceinline__ void hold(const Packed8<T>& x) {
-#pragma unroll
-    for (int q = 0; q < Packed8<T>::NQ; ++q) asm volatile("" ::"v"(x.q[q]));
 }
 
 // The same chain with one block per (batch row, token chunk, run of hidden
@@ -307,7 +306,6 @@ paraplex_chunk_kernel(const T* __restrict__ p_real, const T* __restrict__ gate_s
             if constexpr (!SAME_GATE) buf_load8<T>(rg[p], rG, voff, p * step);
         }
     }
-    Packed8<T> keep_s{}, keep_a{};
     // token `it` from ring slot p; with `refill`, token it+PF's loads go out
     // ahead of the math (at raised wave priority, so every wave's loads issue early)
     auto token = [&](int p, int it, bool refill) {
@@ -342,13 +340,8 @@ paraplex_chunk_kernel(const T* __restrict__ p_real, const T* __restrict__ gate_s
             ao[k] = fmaf(amp, sv, r[k]) * gate;
             prev[k] = s0;
         }
-        const Packed8<T> xs = pack8<T>(so), xa = pack8<T>(ao);
-        hold(keep_s);
-        hold(keep_a);
-        buf_store8<T>(rS, voff, it * step, xs);
-        buf_store8<T>(rA, voff, it * step, xa);
-        keep_s = xs;
-        keep_a = xa;
+        buf_store8<T>(rS, voff, it * step, pack8<T>(so));
+        buf_store8<T>(rA, voff, it * step, pack8<T>(ao));
     };
     if constexpr (TCU > 0) {
         if (n == TCU) {

@@ -50,6 +50,12 @@ class ModelConfig:
     rope_beta_fast: float = 32.0
     rope_beta_slow: float = 1.0
     rope_attention_factor: Optional[float] = None
+    # model variants a checkpoint can carry (Config, loomformer.py:272-274, :358, :366)
+    gate_proj: bool = False              # paraplex_gate_proj: amp = softplus(gate_proj(u))
+    depth_qkv_rms: bool = False          # depth_attn_qkv_rms: fixed-RMS depth q/k/v
+    residual_rms_cap: Optional[float] = None   # residual_branch_rms_cap
+    final_norm: bool = False             # RMSNorm before the head
+    depth_readout: str = "shared"        # depth_attn_readout: shared | per-sublayer
 
     @property
     def G(self) -> int:
@@ -126,6 +132,27 @@ class ModelConfig:
         act = str(d.get("activation", "gelu")).lower()
         if act != "pvpowlu":
             raise ValueError(f"the fused Paraplex path needs activation=pvpowlu, got {act}")
+        # the variant flags, validated as apply_config does (loomformer.py:1034-1044)
+        readout = str(d.get("depth_attn_readout", "shared") or "shared").lower()
+        if readout not in ("shared", "per-sublayer"):
+            raise ValueError(f"depth_attn_readout must be 'shared' or 'per-sublayer', got {readout!r}")
+        cap = d.get("residual_branch_rms_cap")
+        if cap is not None:
+            cap = float(cap)
+            if not math.isfinite(cap) or cap <= 0:
+                raise ValueError("residual_branch_rms_cap must be positive or null")
+        variants = dict(gate_proj=bool(d.get("paraplex_gate_proj", False)),
+                        depth_qkv_rms=bool(d.get("depth_attn_qkv_rms", False)),
+                        residual_rms_cap=cap, final_norm=bool(d.get("final_norm", False)),
+                        depth_readout=readout)
+        unsupported = [k for k, v in (("paraplex_gate_proj", variants["gate_proj"]),
+                                      ("depth_attn_qkv_rms", variants["depth_qkv_rms"]),
+                                      ("residual_branch_rms_cap", cap is not None),
+                                      ("final_norm", variants["final_norm"]),
+                                      ("depth_attn_readout", readout != "shared")) if v]
+        if unsupported:
+            raise ValueError(f"the decode engine does not implement {unsupported} "
+                             "(it would compute a different model)")
         return ModelConfig(
             V=int(d.get("vocab", 256)), N=N, QH=QH, HD=HD, KVH=KVH, H=H, L=int(d.get("layers", 3)),
             seq_len=seq_len, sectors=str(d.get("phase_sectors", "head")).lower(),
@@ -142,4 +169,5 @@ class ModelConfig:
             rope_beta_slow=float(d.get("rope_beta_slow", 1.0) or 1.0),
             rope_attention_factor=(None if d.get("rope_attention_factor") is None
                                    else float(d["rope_attention_factor"])),
+            **variants,
         )

@@ -438,17 +438,27 @@ class LoomDecoder:
         prefill(self, prompt)
 
     @torch.no_grad()
+    def warm_graphs(self) -> None:
+        """Capture both graphs ``replay_steps`` replays (the chained
+        STEPS_PER_GRAPH-step graph and the single step) for the current prompt,
+        so that later replays do no capture work on the host."""
+        self._graph_for(self._prompt_len, self.STEPS_PER_GRAPH)
+        self._graph_for(self._prompt_len)
+
+    @torch.no_grad()
     def replay_steps(self, n: int) -> None:
         """Advance ``n`` positions with the captured step (prompt tokens while
-        pos < P, greedy argmax after)."""
+        pos < P, greedy argmax after): n // STEPS_PER_GRAPH replays of the
+        chained graph, then single-step replays for the rest."""
         self._check_capacity(self.pos + n - 1)
         if n >= self.STEPS_PER_GRAPH:
             g = self._graph_for(self._prompt_len, self.STEPS_PER_GRAPH)
             for _ in range(n // self.STEPS_PER_GRAPH):
                 g.replay()
-        g = self._graph_for(self._prompt_len)
-        for _ in range(n % self.STEPS_PER_GRAPH):
-            g.replay()
+        if n % self.STEPS_PER_GRAPH:
+            g = self._graph_for(self._prompt_len)
+            for _ in range(n % self.STEPS_PER_GRAPH):
+                g.replay()
         self.pos += n
 
     def generated(self) -> torch.Tensor:

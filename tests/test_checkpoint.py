@@ -111,3 +111,28 @@ def test_aio_suffix_required(tmp_path):
     from loom_amd.checkpoint import load_aio
     with pytest.raises(ValueError, match="only .aio"):
         load_aio(str(tmp_path / "x.pt"))
+
+
+@pytest.mark.parametrize("flag,value", [("paraplex_gate_proj", True), ("depth_attn_qkv_rms", True),
+                                        ("residual_branch_rms_cap", 2.0), ("final_norm", True),
+                                        ("depth_attn_readout", "per-sublayer")])
+def test_config_refuses_variant_flags_the_engine_lacks(flag, value):
+    """A math-changing model flag the engine does not compute is refused, not
+    silently dropped (loomformer.py:272-274, :358, :366)."""
+    from loom_amd.config import ModelConfig
+    cfg, _ = _tiny()
+    with pytest.raises(ValueError, match=flag):
+        ModelConfig.from_dict(dict(cfg, **{flag: value}))
+
+
+def test_config_validates_variant_values_like_apply_config():
+    from loom_amd.config import ModelConfig
+    cfg, _ = _tiny()
+    with pytest.raises(ValueError, match="shared' or 'per-sublayer"):
+        ModelConfig.from_dict(dict(cfg, depth_attn_readout="per-head"))
+    with pytest.raises(ValueError, match="positive or null"):
+        ModelConfig.from_dict(dict(cfg, residual_branch_rms_cap=0.0))
+    # defaults spelled out are accepted
+    ModelConfig.from_dict(dict(cfg, paraplex_gate_proj=False, depth_attn_qkv_rms=False,
+                               residual_branch_rms_cap=None, final_norm=False,
+                               depth_attn_readout="shared"))

@@ -100,6 +100,38 @@ def test_paraplex_forward(dtype, B, T, H, same_gate, with_reset):
     assert torch.equal(act2, act) and torch.equal(s2, s) and torch.equal(nt2, nt)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("B,T,H", [(4, 16, 3072), (2, 33, 3072), (8, 1024, 3072), (3, 47, 256),
+                                   (32, 128, 3072)])
+def test_paraplex_row_end_tokens(dtype, B, T, H):
+    """The last token of each row (the final store of the chunk that ends the
+    row, followed by the next-trace store) and the next trace, element by
+    element against the oracle, over three launches with identical bits."""
+    from loom_amd import ops
+    g = gen(B * 77 + T * 5 + H)
+    r = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    beta = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    bias = dev(rnd(g, H, scale=0.5), torch.float32)
+    trace = dev(rnd(g, B, H, scale=0.5), dtype)
+    tw = dev(torch.rand(H, generator=g) - 0.5, torch.float32)
+    no_reset = torch.empty(0, dtype=torch.bool, device=DEV)
+    anchor = torch.ones((), device=DEV)
+    w_act, w_s, w_nt = ref.paraplex_pointwise(host(r), host(r), host(beta), host(bias), host(trace),
+                                              host(tw), None, 3.0)
+    tol = TOL[dtype] if dtype in TOL else dict(rtol=5e-3, atol=5e-3)
+    first = None
+    for _ in range(3):
+        act, s_, nt, _ = ops.paraplex_forward(r, r, beta, bias, trace, tw, no_reset, anchor, 1,
+                                              False, 0.99, 3.0)
+        torch.testing.assert_close(host(act[:, -1]), w_act[:, -1], **tol)
+        torch.testing.assert_close(host(s_[:, -1]), w_s[:, -1], **tol)
+        torch.testing.assert_close(host(nt), w_nt, **tol)
+        if first is None:
+            first = (act.clone(), s_.clone(), nt.clone())
+        else:
+            assert torch.equal(first[0], act) and torch.equal(first[1], s_) and torch.equal(first[2], nt)
+
+
 @pytest.mark.parametrize("B,T,H,same_gate,with_reset", [
     (3, 37, 3072, True, True), (8, 1030, 3072, False, True), (2, 7, 20, True, False),
 ])
