@@ -425,6 +425,26 @@ int loom_gqa_decode_step_depth(int dtype, const void* qkv, void* k_cache, void* 
                                const void* hist_v, int64_t hist_stride_bt, int64_t hist_stride_s,
                                int64_t S, void* depth_out, void* stream);
 
+/* Size of the static per-device scratch of loom_gqa_decode_step_noalloc. */
+#define LOOM_GQA_NOALLOC_SCRATCH_BYTES (4 << 20)
+
+/* loom_gqa_decode_step without a workspace argument: the partial records live
+ * in a static device array of LOOM_GQA_NOALLOC_SCRATCH_BYTES per GPU (held
+ * until the process ends), so the call allocates nothing (no hipMalloc, no
+ * library allocation).  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving
+ * loops that forbid it).  Shapes whose records exceed the scratch
+ * (loom_gqa_workspace_bytes(B, len, QH, KVH, HD) > LOOM_GQA_NOALLOC_SCRATCH_BYTES)
+ * are rejected with LOOM_ERR_INVALID.  Calls on one GPU share the array, so
+ * calls that overlap on one GPU (concurrent streams or threads) race. */
+int loom_gqa_decode_step_noalloc(int dtype, const void* qkv, void* k_cache, void* v_cache,
+                                 int64_t cache_stride_b, int64_t cache_stride_t,
+                                 int64_t cache_stride_h, const float* cos_table,
+                                 const float* sin_table, void* q_out, void* c_out, void* kctx_out,
+                                 int64_t out_stride_b, int64_t B, int64_t len,
+                                 const int64_t* pos_dev, int64_t QH, int64_t KVH, int64_t HD,
+                                 void* stream);
+
 /* out = LayerNorm(a + b) (b may be NULL) over rows of N <= 2048, fp32 gamma and
  * beta, biased variance.  Replaces ln_attn/ln_ffn(skip + branch)
  * (loomformer.py:4000, :4045). */

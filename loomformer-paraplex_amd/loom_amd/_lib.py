@@ -67,6 +67,9 @@ SIGNATURES = {
     "loom_gqa_decode_step": [c_int, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P,
                              c_int64, _P, c_int64, c_int64, c_int64, _P, c_int64, c_int64, c_int64,
                              _P],
+    "loom_gqa_decode_step_noalloc": [c_int, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P,
+                                     _P, c_int64, c_int64, c_int64, _P, c_int64, c_int64, c_int64,
+                                     _P],
     "loom_gqa_prefill": [c_int, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P,
                          _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
                          c_int64, _P],
