@@ -171,8 +171,10 @@ typedef struct {
     const void* w_compact;
     int64_t M, N, H, imag_in, hidden_per_q_head, head_dim, n_q_heads;
     int32_t open_sectors;
-    /* Paraplex pointwise, as loom_paraplex_forward with T = 1 and gate_src = p_real */
+    /* Paraplex pointwise, as loom_paraplex_forward with T = 1 */
     const void* p_real;        /* R [M, H] */
+    const void* gate_src;      /* [M, H] amplitude source, or NULL for p_real (paraplex_gate_proj
+                                  off, loomformer.py:2849) */
     const float* imag_bias;    /* [H] */
     void* trace;               /* [M, H]: previous phase in, this token's phase out */
     const float* trace_w;      /* [H] */
@@ -222,6 +224,19 @@ int loom_depth_attn_forward(int dtype, const void* q, const void* hist_k, const 
                             int64_t stride_bt, int64_t stride_s, void* d_out, void* w_out,
                             float* lse_out, int64_t BT, int64_t S, int64_t QH, int64_t HD,
                             void* stream);
+
+/* loom_depth_attn_forward for DepthAttn under depth_attn_qkv_rms
+ * (loomformer.py:3397-3407): the query, key and value rows are read as
+ * fixed-RMS vectors x * t / sqrt(mean(x^2) + 1e-6) with targets q_target
+ * (fanin_std(HD) in the reference), k_target (FANIN_GAIN) and v_target
+ * (FANIN_GAIN * DEEPNORM_BETA); the history itself is stored as projected.
+ * Same layout and outputs as loom_depth_attn_forward; targets must be > 0.
+ * No counterpart in the reference's kernels (its module rescales q, k, v
+ * with torch ops before calling depth_attn_forward_cuda). */
+int loom_depth_attn_forward_rms(int dtype, const void* q, const void* hist_k, const void* hist_v,
+                                int64_t stride_bt, int64_t stride_s, void* d_out, void* w_out,
+                                float* lse_out, int64_t BT, int64_t S, int64_t QH, int64_t HD,
+                                float q_target, float k_target, float v_target, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Tria (all math fp32; carry tensors [n,3,3] row-major per element)
@@ -451,6 +466,13 @@ int loom_gqa_decode_step_noalloc(int dtype, const void* qkv, void* k_cache, void
 int loom_add_layernorm(int dtype, const void* a, const void* b, const float* gamma,
                        const float* beta, void* out, int64_t rows, int64_t N, float eps,
                        void* stream);
+
+/* RMSNorm of final_norm before the head (RMSNorm.forward, loomformer.py:3460-3464):
+ * out = round(round(x / sqrt(mean(x^2) + eps)) * weight) per row of N <= 2048,
+ * statistics in fp32, rounding to dtype as the reference's .to(dtype) and
+ * product in the model dtype.  x, weight, out: dtype. */
+int loom_rms_norm(int dtype, const void* x, const void* weight, void* out, int64_t rows, int64_t N,
+                  float eps, void* stream);
 
 /* Decode-time temporal Tria update of one token (loomformer.py:4056-4085):
  *   out[b] = depth[b]                      if prev == NULL or reset_now[b]

@@ -687,6 +687,38 @@ add_layernorm_kernel(const T* __restrict__ a, const T* __restrict__ bsrc,
     }
 }
 
+// out = round(round(x / sqrt(mean(x^2) + eps)) * w) over rows of N, the
+// RMSNorm of final_norm (loomformer.py:3460-3464: fp32 statistics, the
+// normalised row rounded to the storage type, then the learned scale in it);
+// one wavefront per row.
+template <typename T>
+__global__ void __launch_bounds__(256)
+rms_norm_kernel(const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ out,
+                int64_t rows, int N, float eps) {
+    const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    constexpr int kMax = 32;  // N <= 64 * 32
+    float v[kMax];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMax; ++k) {
+        const int c = lane + 64 * k;
+        v[k] = c < N ? ld(x + row * N + c) : 0.0f;
+        ss = fmaf(v[k], v[k], ss);
+    }
+    const float r = 1.0f / sqrtf(wave_sum(ss) / N + eps);
+#pragma unroll
+    for (int k = 0; k < kMax; ++k) {
+        const int c = lane + 64 * k;
+        if (c < N) {
+            T nrm;
+            st(&nrm, v[k] * r);
+            st(out + row * N + c, ld(&nrm) * ld(w + c));
+        }
+    }
+}
+
 // Vector form for N % 8 == 0 (N <= 64*8*4): lane owns 8-element vectors
 // lane, lane+64, ...; two wave reductions (mean, variance).
 template <typename T, int NV>
@@ -1564,6 +1596,24 @@ extern "C" int loom_add_layernorm(int dtype, const void* a, const void* b, const
     LOOM_CHECK(N >= 1 && N <= 64 * 32, "add_layernorm: N=%lld outside [1, 2048]", (long long)N);
     if (rows == 0) return LOOM_OK;
     LOOM_DTYPE_SWITCH(dtype, ln_dispatch, a, b, gamma, beta, out, rows, N, eps, (hipStream_t)stream)
+}
+
+template <typename T>
+static int rms_dispatch(const void* x, const void* w, void* out, int64_t rows, int64_t N,
+                        float eps, hipStream_t st) {
+    hipLaunchKernelGGL((rms_norm_kernel<T>), dim3((unsigned)ceil_div(rows * 64, 256)), dim3(256),
+                       0, st, (const T*)x, (const T*)w, (T*)out, rows, (int)N, eps);
+    return launch_status("loom_rms_norm");
+}
+
+extern "C" int loom_rms_norm(int dtype, const void* x, const void* weight, void* out,
+                             int64_t rows, int64_t N, float eps, void* stream) {
+    clear_error();
+    LOOM_CHECK(x && weight && out, "rms_norm: null argument");
+    LOOM_CHECK(N >= 1 && N <= 64 * 32, "rms_norm: N=%lld outside [1, 2048]", (long long)N);
+    LOOM_CHECK(rows >= 0, "rms_norm: rows=%lld", (long long)rows);
+    if (rows == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, rms_dispatch, x, weight, out, rows, N, eps, (hipStream_t)stream)
 }
 
 extern "C" int loom_tria_decode_temporal(int dtype, const void* depth, const void* prev,

@@ -16,51 +16,61 @@
 
 namespace loom {
 
-template <typename T, int EPL, int C>
+template <typename T, int EPL, int C, bool RMS>
 __global__ void __launch_bounds__(256)
 depth_attn_kernel(const T* __restrict__ q, const T* __restrict__ hk, const T* __restrict__ hv,
                   int64_t sbt, int64_t ss, T* __restrict__ d_out, T* __restrict__ w_out,
-                  float* __restrict__ lse_out, int rows, int S, int QH, float scale) {
+                  float* __restrict__ lse_out, int rows, int S, int QH, float scale, DepthRms rms) {
     const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 4);
     if (row >= rows) return;  // all 16 lanes of a group leave together
-    depth_row<T, EPL, C>(q, hk, hv, sbt, ss, d_out, w_out, lse_out, row, threadIdx.x & 15, S, QH,
-                         scale);
+    depth_row<T, EPL, C, RMS>(q, hk, hv, sbt, ss, d_out, w_out, lse_out, row, threadIdx.x & 15, S,
+                              QH, scale, rms);
 }
 
-// Any HD: one thread per (bt, qh) row, online softmax, scalar loads.
+// target / sqrt(mean(x^2) + 1e-6) of the HD-element row at p, or 1 when target == 0
+template <typename T>
+__device__ __forceinline__ float row_rms_scale(const T* p, int HD, float target) {
+    if (target == 0.0f) return 1.0f;
+    float ss = 0.0f;
+    for (int d = 0; d < HD; ++d) {
+        const float x = ld(p + d);
+        ss = fmaf(x, x, ss);
+    }
+    return target * frsq(ss / (float)HD + 1e-6f);
+}
+
+// Any HD: one thread per (bt, qh) row, online softmax, scalar loads.  With
+// nonzero targets in rms the q, k, v rows are read as fixed-RMS vectors.
 template <typename T>
 __global__ void __launch_bounds__(256)
 depth_attn_generic_kernel(const T* __restrict__ q, const T* __restrict__ hk,
                           const T* __restrict__ hv, int64_t sbt, int64_t ss,
                           T* __restrict__ d_out, T* __restrict__ w_out, float* __restrict__ lse_out,
-                          int64_t rows, int S, int QH, int HD, float scale) {
+                          int64_t rows, int S, int QH, int HD, float scale, DepthRms rms) {
     const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (row >= rows) return;
     const int qh = (int)(row % QH);
     const int64_t bt = row / QH;
     const T* kp = hk + bt * sbt + qh * HD;
     const T* vp = hv + bt * sbt + qh * HD;
+    const float qsc = scale * row_rms_scale(q + qh * HD, HD, rms.qt);
+    auto score = [&](int s) {
+        float dot = 0.0f;
+        for (int d = 0; d < HD; ++d) dot = fmaf(ld(q + qh * HD + d), ld(kp + s * ss + d), dot);
+        return dot * qsc * row_rms_scale(kp + s * ss, HD, rms.kt);
+    };
     float m = -INFINITY, l = 0.0f;
+    for (int s = 0; s < S; ++s) m = fmaxf(m, score(s));
     for (int s = 0; s < S; ++s) {
-        float dot = 0.0f;
-        for (int d = 0; d < HD; ++d) dot = fmaf(ld(q + qh * HD + d), ld(kp + s * ss + d), dot);
-        m = fmaxf(m, dot * scale);
-    }
-    for (int s = 0; s < S; ++s) {
-        float dot = 0.0f;
-        for (int d = 0; d < HD; ++d) dot = fmaf(ld(q + qh * HD + d), ld(kp + s * ss + d), dot);
-        const float p = fexp(dot * scale - m);
+        const float p = fexp(score(s) - m);
         l += p;
         if (w_out != nullptr) st(w_out + row * S + s, p);
     }
     const float inv_l = 1.0f / l;
     for (int d = 0; d < HD; ++d) {
         float a = 0.0f;
-        for (int s = 0; s < S; ++s) {
-            float dot = 0.0f;
-            for (int e = 0; e < HD; ++e) dot = fmaf(ld(q + qh * HD + e), ld(kp + s * ss + e), dot);
-            a = fmaf(fexp(dot * scale - m), ld(vp + s * ss + d), a);
-        }
+        for (int s = 0; s < S; ++s)
+            a = fmaf(fexp(score(s) - m) * row_rms_scale(vp + s * ss, HD, rms.vt), ld(vp + s * ss + d), a);
         st(d_out + row * HD + d, a * inv_l);
     }
     if (w_out != nullptr)
@@ -71,7 +81,8 @@ depth_attn_generic_kernel(const T* __restrict__ q, const T* __restrict__ hk,
 template <typename T>
 static int dispatch_depth(const void* q, const void* hk, const void* hv, int64_t sbt, int64_t ss,
                           void* d_out, void* w_out, float* lse_out, int64_t BT, int64_t S,
-                          int64_t QH, int64_t HD, hipStream_t stream) {
+                          int64_t QH, int64_t HD, hipStream_t stream, DepthRms rms = DepthRms{}) {
+    const bool with_rms = rms.qt != 0.0f || rms.kt != 0.0f || rms.vt != 0.0f;
     const int64_t rows = BT * QH;
     const float scale = 1.0f / sqrtf((float)HD);
     // a small launch (a decode step's rows) takes one wave per block so it
@@ -83,13 +94,17 @@ static int dispatch_depth(const void* q, const void* hk, const void* hv, int64_t
                          (((uintptr_t)hk | (uintptr_t)hv | (uintptr_t)q | (uintptr_t)d_out) % 8 == 0) &&
                          rows * 16 < ((int64_t)1 << 31) && BT * sbt < ((int64_t)1 << 62);
     const int epl = (HD % 16 == 0) ? (int)(HD / 16) : 0;
-#define LOOM_DA_LAUNCH(E, C)                                                                     \
-        hipLaunchKernelGGL((depth_attn_kernel<T, E, C>), dim3((unsigned)ceil_div(rows * 16, threads)), \
+#define LOOM_DA_LAUNCH(E, C, R)                                                                  \
+        hipLaunchKernelGGL((depth_attn_kernel<T, E, C, R>), dim3((unsigned)ceil_div(rows * 16, threads)), \
                            dim3(threads), 0, stream, (const T*)q, (const T*)hk, (const T*)hv, sbt, \
-                           ss, (T*)d_out, (T*)w_out, lse_out, (int)rows, (int)S, (int)QH, scale);
+                           ss, (T*)d_out, (T*)w_out, lse_out, (int)rows, (int)S, (int)QH, scale, rms);
 #define LOOM_DA_CASE(E)                                                                          \
     case E:                                                                                      \
-        LOOM_DA_LAUNCH(E, kDepthChunk)                                                           \
+        if (with_rms) {                                                                          \
+            LOOM_DA_LAUNCH(E, kDepthChunk, true)                                                 \
+        } else {                                                                                 \
+            LOOM_DA_LAUNCH(E, kDepthChunk, false)                                                \
+        }                                                                                        \
         return launch_status("loom_depth_attn_forward");
     if (aligned) {
         switch (epl) {
@@ -104,7 +119,7 @@ static int dispatch_depth(const void* q, const void* hk, const void* hv, int64_t
 #undef LOOM_DA_LAUNCH
     hipLaunchKernelGGL((depth_attn_generic_kernel<T>), dim3((unsigned)ceil_div(rows, threads)),
                        dim3(threads), 0, stream, (const T*)q, (const T*)hk, (const T*)hv, sbt, ss,
-                       (T*)d_out, (T*)w_out, lse_out, rows, (int)S, (int)QH, (int)HD, scale);
+                       (T*)d_out, (T*)w_out, lse_out, rows, (int)S, (int)QH, (int)HD, scale, rms);
     return launch_status("loom_depth_attn_forward");
 }
 
@@ -112,11 +127,10 @@ static int dispatch_depth(const void* q, const void* hk, const void* hv, int64_t
 
 using namespace loom;
 
-extern "C" int loom_depth_attn_forward(int dtype, const void* q, const void* hist_k,
-                                       const void* hist_v, int64_t stride_bt, int64_t stride_s,
-                                       void* d_out, void* w_out, float* lse_out, int64_t BT,
-                                       int64_t S, int64_t QH, int64_t HD, void* stream) {
-    clear_error();
+static int depth_entry(int dtype, const void* q, const void* hist_k, const void* hist_v,
+                       int64_t stride_bt, int64_t stride_s, void* d_out, void* w_out,
+                       float* lse_out, int64_t BT, int64_t S, int64_t QH, int64_t HD,
+                       void* stream, DepthRms rms) {
     LOOM_CHECK(q && hist_k && hist_v && d_out, "depth_attn: null tensor argument");
     LOOM_CHECK(BT >= 0 && S >= 1 && QH >= 1 && HD >= 1, "depth_attn: bad shape BT=%lld S=%lld",
                (long long)BT, (long long)S);
@@ -128,14 +142,37 @@ extern "C" int loom_depth_attn_forward(int dtype, const void* q, const void* his
     switch (dtype) {
         case LOOM_F32:
             return dispatch_depth<float>(q, hist_k, hist_v, stride_bt, stride_s, d_out, w_out,
-                                         lse_out, BT, S, QH, HD, st);
+                                         lse_out, BT, S, QH, HD, st, rms);
         case LOOM_BF16:
             return dispatch_depth<bf16_t>(q, hist_k, hist_v, stride_bt, stride_s, d_out, w_out,
-                                          lse_out, BT, S, QH, HD, st);
+                                          lse_out, BT, S, QH, HD, st, rms);
         case LOOM_F16:
             return dispatch_depth<f16_t>(q, hist_k, hist_v, stride_bt, stride_s, d_out, w_out,
-                                         lse_out, BT, S, QH, HD, st);
+                                         lse_out, BT, S, QH, HD, st, rms);
     }
     set_error("depth_attn: unsupported dtype %d", dtype);
     return LOOM_ERR_INVALID;
+}
+
+extern "C" int loom_depth_attn_forward(int dtype, const void* q, const void* hist_k,
+                                       const void* hist_v, int64_t stride_bt, int64_t stride_s,
+                                       void* d_out, void* w_out, float* lse_out, int64_t BT,
+                                       int64_t S, int64_t QH, int64_t HD, void* stream) {
+    clear_error();
+    return depth_entry(dtype, q, hist_k, hist_v, stride_bt, stride_s, d_out, w_out, lse_out, BT, S,
+                       QH, HD, stream, DepthRms{});
+}
+
+extern "C" int loom_depth_attn_forward_rms(int dtype, const void* q, const void* hist_k,
+                                           const void* hist_v, int64_t stride_bt,
+                                           int64_t stride_s, void* d_out, void* w_out,
+                                           float* lse_out, int64_t BT, int64_t S, int64_t QH,
+                                           int64_t HD, float q_target, float k_target,
+                                           float v_target, void* stream) {
+    clear_error();
+    LOOM_CHECK(q_target > 0.0f && k_target > 0.0f && v_target > 0.0f,
+               "depth_attn_rms: targets must be positive (q %g, k %g, v %g)", (double)q_target,
+               (double)k_target, (double)v_target);
+    return depth_entry(dtype, q, hist_k, hist_v, stride_bt, stride_s, d_out, w_out, lse_out, BT, S,
+                       QH, HD, stream, DepthRms{q_target, k_target, v_target});
 }

@@ -7,6 +7,12 @@
 // read (8 independent K loads in flight per lane), then folded into an fp32
 // online softmax in log2 units.  The K/V rows are read
 // once, with nontemporal loads.
+//
+// With RMS (DepthAttn under depth_attn_qkv_rms, loomformer.py:3397-3407) the
+// query, key and value rows are read as fixed-RMS vectors: x * t / sqrt(mean(x^2)
+// + 1e-6) with targets qt, kt, vt.  The key scale multiplies the group-summed
+// score and the value scale the softmax weight of its row, so the stored
+// history stays as projected.
 #pragma once
 
 #include "loom_common.h"
@@ -15,12 +21,26 @@ namespace loom {
 
 constexpr int kDepthChunk = 8;
 
-template <typename T, int EPL, int C = kDepthChunk>
+// target / sqrt(mean(x^2) + 1e-6) of a 16-lane row whose lanes hold EPL elements each
+template <int EPL>
+__device__ __forceinline__ float rms_scale(const float (&x)[EPL], float target) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) ss = fmaf(x[k], x[k], ss);
+    ss = group_sum<16>(ss);
+    return target * frsq(fmaf(ss, 1.0f / (float)(EPL * 16), 1e-6f));
+}
+
+struct DepthRms {
+    float qt, kt, vt;
+};
+
+template <typename T, int EPL, int C = kDepthChunk, bool RMS = false>
 __device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __restrict__ hk,
                                           const T* __restrict__ hv, int64_t sbt, int64_t ss,
                                           T* __restrict__ d_out, T* __restrict__ w_out,
                                           float* __restrict__ lse_out, int row, int j, int S,
-                                          int QH, float scale) {
+                                          int QH, float scale, DepthRms rms = DepthRms{}) {
     constexpr int HD = EPL * 16;
     const int qh = row % QH;
     const int bt = row / QH;
@@ -28,8 +48,10 @@ __device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __re
 
     float qv[EPL];
     RowIO<T, EPL>::load(q + qh * HD + d0, qv);
+    float qs = scale * kLog2e;                              // scores in log2 units
+    if constexpr (RMS) qs *= rms_scale<EPL>(qv, rms.qt);
 #pragma unroll
-    for (int k = 0; k < EPL; ++k) qv[k] *= scale * kLog2e;   // scores in log2 units
+    for (int k = 0; k < EPL; ++k) qv[k] *= qs;
 
     const T* kp = hk + (int64_t)bt * sbt + qh * HD + d0;
     const T* vp = hv + (int64_t)bt * sbt + qh * HD + d0;
@@ -56,11 +78,12 @@ __device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __re
 #pragma unroll
             for (int k = 0; k < EPL; ++k) dot = fmaf(qv[k], kv[k], dot);
             sc[c] = dot;
+            if constexpr (RMS) sc[c] = group_sum<16>(sc[c]) * rms_scale<EPL>(kv, rms.kt);
         }
         float cmax = -INFINITY;
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-            sc[c] = group_sum<16>(sc[c]);
+            if constexpr (!RMS) sc[c] = group_sum<16>(sc[c]);
             if (s0 + c < S) cmax = fmaxf(cmax, sc[c]);
         }
         const float m_new = fmaxf(m, cmax);
@@ -74,8 +97,9 @@ __device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __re
             vr[c].to_float(vv);
             const float p = s0 + c < S ? __builtin_amdgcn_exp2f(sc[c] - m_new) : 0.0f;
             l += p;
+            const float pv = RMS ? p * rms_scale<EPL>(vv, rms.vt) : p;
 #pragma unroll
-            for (int k = 0; k < EPL; ++k) acc[k] = fmaf(p, vv[k], acc[k]);
+            for (int k = 0; k < EPL; ++k) acc[k] = fmaf(pv, vv[k], acc[k]);
         }
         m = m_new;
     }
@@ -93,6 +117,7 @@ __device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __re
 #pragma unroll
             for (int k = 0; k < EPL; ++k) dot = fmaf(qv[k], kv[k], dot);
             dot = group_sum<16>(dot);
+            if constexpr (RMS) dot *= rms_scale<EPL>(kv, rms.kt);
             if (j == 0) st(w_out + (int64_t)row * S + s, __builtin_amdgcn_exp2f(dot - m) * inv_l);
         }
     }

@@ -308,6 +308,7 @@ gemm_bf16_skinny_kernel(GemmArgs a) {
 struct FfnArgs {
     GemmArgs g;                 // beta space: out unused
     const uint16_t* R;          // p_real [M, H]
+    const uint16_t* G;          // amplitude source [M, H]: R, or gate_proj(u)
     const float* ib;            // w1_imag_bias [H]
     uint16_t* trace;            // [M, H]: previous phase in, this token's phase out
     const float* tw;            // [H]
@@ -377,13 +378,14 @@ ffn_decode_kernel(FfnArgs f) {
         }
         const float tr = bf(f.trace[e]);
         const float x = bf(f.R[e]);
+        const float gsrc = f.G == f.R ? x : bf(f.G[e]);
         const float beta = skinny_sum<MT, NW>(red, mi, nn);
         // Paraplex pointwise, one token: prev phase = the carried trace
         const float s0 = phase_of(beta + f.ib[h]);
         const float raw = fmaf(tr, f.tw[h], s0);
         const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
         float amp, gate;
-        softplus_gate<false>(x, f.m, amp, gate);   // bf16 outputs (see softplus_gate)
+        softplus_gate<false>(gsrc, f.m, amp, gate);   // bf16 outputs (see softplus_gate)
         const float act = fmaf(amp, sv, x) * gate;
         f.trace[e] = f32_to_bf16(s0);
         f.act[e] = f32_to_bf16(act);
@@ -1046,6 +1048,7 @@ extern "C" int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* d, void* s
         a.Nm = d->N; a.HD = d->head_dim; a.Hq = d->hidden_per_q_head; a.open = d->open_sectors ? 1 : 0;
         a.X = d->u; a.ldx = d->N;
         f.R = (const uint16_t*)d->p_real; f.ib = d->imag_bias; f.trace = (uint16_t*)d->trace;
+        f.G = (const uint16_t*)(d->gate_src ? d->gate_src : d->p_real);
         f.tw = d->trace_w; f.m = d->powlu_m; f.act = (uint16_t*)d->act; f.s = (uint16_t*)d->s;
         f.prev = (const uint16_t*)d->carry_prev; f.seed = (const uint16_t*)d->seed;
         f.valid = d->seed_valid; f.gate_w = (const uint16_t*)d->gate_w;
@@ -1067,7 +1070,8 @@ extern "C" int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* d, void* s
                                d->beta, nullptr, d->M, d->N, d->H, d->imag_in, d->hidden_per_q_head,
                                d->head_dim, d->n_q_heads, d->open_sectors, stream);
     if (rc != LOOM_OK) return rc;
-    rc = loom_paraplex_forward(dtype, d->p_real, d->p_real, d->beta, d->imag_bias, d->trace,
+    rc = loom_paraplex_forward(dtype, d->p_real, d->gate_src ? d->gate_src : d->p_real, d->beta,
+                               d->imag_bias, d->trace,
                                d->trace_w, nullptr, nullptr, d->act, d->s, d->trace, nullptr, d->M,
                                1, d->H, d->powlu_m, stream);
     if (rc != LOOM_OK) return rc;

@@ -67,6 +67,9 @@ SIGNATURES = {
     "loom_gqa_decode_step": [c_int, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P,
                              c_int64, _P, c_int64, c_int64, c_int64, _P, c_int64, c_int64, c_int64,
                              _P],
+    "loom_depth_attn_forward_rms": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64,
+                                    c_int64, c_int64, c_int64, c_float, c_float, c_float, _P],
+    "loom_rms_norm": [c_int, _P, _P, _P, c_int64, c_int64, c_float, _P],
     "loom_gqa_decode_step_noalloc": [c_int, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P,
                                      _P, c_int64, c_int64, c_int64, _P, c_int64, c_int64, c_int64,
                                      _P],
@@ -153,7 +156,8 @@ class FfnDecodeDesc(ctypes.Structure):
                 ("M", c_int64), ("N", c_int64), ("H", c_int64), ("imag_in", c_int64),
                 ("hidden_per_q_head", c_int64), ("head_dim", c_int64), ("n_q_heads", c_int64),
                 ("open_sectors", ctypes.c_int32),
-                ("p_real", c_void_p), ("imag_bias", c_void_p), ("trace", c_void_p),
+                ("p_real", c_void_p), ("gate_src", c_void_p), ("imag_bias", c_void_p),
+                ("trace", c_void_p),
                 ("trace_w", c_void_p), ("powlu_m", c_float),
                 ("act", c_void_p), ("s", c_void_p), ("beta", c_void_p),
                 ("carry_prev", c_void_p), ("seed", c_void_p), ("seed_valid", c_void_p),

@@ -20,6 +20,7 @@ from typing import Any, Dict, Mapping, Optional
 import torch
 
 from .config import ModelConfig
+from .weights import state_keys
 
 AIO_FORMAT = "loom.aio"
 AIO_VERSION = 1
@@ -127,8 +128,16 @@ def _from_checkpoint(ck: Mapping[str, Any], vocab: Optional[int] = None) -> Load
     cfg = ModelConfig.from_dict(raw)
     state = canonicalize_state_dict(ck["model"], cfg.L)
     state = {k: v for k, v in state.items() if torch.is_tensor(v)}
-    if cfg.tied and "head.weight" not in state:
+    if cfg.tied and "head.weight" not in state and "emb.weight" in state:
         state["head.weight"] = state["emb.weight"]
+    # the strict load of load_model_blob_into (loomformer.py:4424): the keys must
+    # be exactly the config's model (a variant flag without its weights, or
+    # weights of a variant the config does not set, is refused)
+    want = set(state_keys(cfg))
+    missing, unexpected = sorted(want - set(state)), sorted(set(state) - want)
+    if missing or unexpected:
+        raise ValueError(f"checkpoint state_dict does not match its config: missing keys "
+                         f"{missing[:8]}, unexpected keys {unexpected[:8]}")
     emb = state.get("emb.weight")
     if emb is None or emb.shape != (cfg.V, cfg.N):
         raise ValueError(f"emb.weight {None if emb is None else tuple(emb.shape)} does not match "

@@ -74,6 +74,10 @@ class ModelConfig:
         return self.N + 4 * self.HD if self.sectors == "head" else 4 * self.N + self.HD
 
     @property
+    def fanin_gain(self) -> float:
+        return 0.88                      # FANIN_GAIN (loomformer.py:808)
+
+    @property
     def deepnorm_beta(self) -> float:
         return (8.0 * max(1, self.L)) ** -0.25
 
@@ -145,14 +149,6 @@ class ModelConfig:
                         depth_qkv_rms=bool(d.get("depth_attn_qkv_rms", False)),
                         residual_rms_cap=cap, final_norm=bool(d.get("final_norm", False)),
                         depth_readout=readout)
-        unsupported = [k for k, v in (("paraplex_gate_proj", variants["gate_proj"]),
-                                      ("depth_attn_qkv_rms", variants["depth_qkv_rms"]),
-                                      ("residual_branch_rms_cap", cap is not None),
-                                      ("final_norm", variants["final_norm"]),
-                                      ("depth_attn_readout", readout != "shared")) if v]
-        if unsupported:
-            raise ValueError(f"the decode engine does not implement {unsupported} "
-                             "(it would compute a different model)")
         return ModelConfig(
             V=int(d.get("vocab", 256)), N=N, QH=QH, HD=HD, KVH=KVH, H=H, L=int(d.get("layers", 3)),
             seq_len=seq_len, sectors=str(d.get("phase_sectors", "head")).lower(),

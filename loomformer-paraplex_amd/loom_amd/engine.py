@@ -86,9 +86,20 @@ class LoomDecoder:
                 alpha=0.25 * math.tanh(raw_alpha),                      # IdentityAnchoredGate
                 anchor=torch.ones((), device=dev),
             ))
+            if c.gate_proj:                      # independent amplitude source (:2849)
+                self.blocks[-1].update(gpw=mat(p + "ffn.gate_proj.weight"),
+                                       gpb=f32(p + "ffn.gate_proj.bias"))
         self.kvw = mat("depth_attn.kv_weight")
-        self.wo = mat("depth_attn.w_o.weight")
+        # depth readouts: one shared [N, N], or one per sublayer [2L, N, N] (:3424-3428)
+        if c.depth_readout == "per-sublayer":
+            self.wo_sub = mat("depth_attn.w_o_weight")
+        else:
+            self.wo = mat("depth_attn.w_o.weight")
         self.qp = mat("depth_attn.q_params")
+        # depth_attn_qkv_rms targets of q, k, v (loomformer.py:3397-3407)
+        self.depth_rms = ((c.fanin_gain / math.sqrt(c.HD), c.fanin_gain,
+                           c.fanin_gain * c.deepnorm_beta) if c.depth_qkv_rms else None)
+        self.ln_final = mat("ln_final.weight") if c.final_norm else None
         key_w = state["tria_agg.reader.key_proj.weight"].detach().float()
         query = state["tria_agg.pool.query"].detach().float()
         lsr = state["tria_agg.pool.logit_scale_raw"].detach().float()
@@ -146,6 +157,7 @@ class LoomDecoder:
         self.attn_out = z(B, N)
         self.skip = z(B, N)
         self.R = z(B, H)
+        self.G = z(B, H) if c.gate_proj else None      # gate_proj(u), the amplitude source
         self.beta = z(B, H)
         self.act = z(B, H)
         self.s = z(B, H)
@@ -159,6 +171,7 @@ class LoomDecoder:
         self.stage_k = z(B, N)
         self.stage_v = z(B, N)
         self.q_ca = z(B, N)
+        self.h3 = z(B, N) if c.final_norm else None     # RMSNorm(h) before the head
         self.logits = z(B, c.V)
         self.snap = torch.empty((), dtype=torch.float32, device=dev)
         self.pos = 0
@@ -174,6 +187,31 @@ class LoomDecoder:
 
     def _stream(self):
         return _lib.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+
+    def wo_for(self, sub: int) -> torch.Tensor:
+        """The depth readout of sublayer `sub` (DepthAttn.forward, loomformer.py:3424-3428)."""
+        return self.wo_sub[sub] if self.cfg.depth_readout == "per-sublayer" else self.wo
+
+    def head_logits(self, x: torch.Tensor, out: torch.Tensor, rows: int) -> None:
+        """Model._head_in (loomformer.py:3527-3529): the optional final RMSNorm
+        (eps 1e-6), then the head."""
+        if self.ln_final is not None:
+            self._call("loom_rms_norm", self.code, _P(x), _P(self.ln_final), _P(self.h3), rows,
+                       self.cfg.N, 1e-6, self._stream())
+            x = self.h3
+        self._linear(x, self.head, out, rows, self.cfg.V, self.cfg.N)
+
+    def depth_read(self, sub: int, hist: torch.Tensor, out: torch.Tensor, rows: int) -> None:
+        """DepthAttn read over history slots [0, sub] of `hist` [rows, 2L, 2N]
+        (loomformer.py:3404-3429, tensor branch), fixed-RMS q/k/v under
+        depth_attn_qkv_rms."""
+        c, N, L = self.cfg, self.cfg.N, self.cfg.L
+        args = [self.code, _P(self.qp[sub]), _P(hist), _P(hist[:, :, N:]), 2 * L * 2 * N, 2 * N,
+                _P(out), None, None, rows, sub + 1, c.QH, c.HD]
+        if self.depth_rms is None:
+            self._call("loom_depth_attn_forward", *args, self._stream())
+        else:
+            self._call("loom_depth_attn_forward_rms", *args, *self.depth_rms, self._stream())
 
     def _linear(self, x, w, out, M, Nout, K, bias=None, ldx=None, ldc=None, gate_p=None,
                 gate_alpha=0.0, residual=None):
@@ -238,25 +276,36 @@ class LoomDecoder:
             # ---- attention step (loomformer.py:3300-3332): RoPE + cache append +
             # attention + chunk merge, one launch
             # with the depth read 2*bi of this token (loomformer.py:3999) in the same launch
-            self._call("loom_gqa_decode_step_depth", self.code, _P(self.qkv), _P(kc), _P(vc),
-                       cache_sb, cache_st, cache_sh, _P(self.cos), _P(self.sin), _P(self.q),
-                       _P(self.c), _P(self.kctx), N,
-                       _P(self.ws), self.ws_bytes, B, self.max_len, _P(self.pos_dev), c.QH, c.KVH,
-                       c.HD, _P(self.qp[sub]), _P(self.hist), _P(self.hist[:, :, N:]),
-                       2 * L * 2 * N, 2 * N, sub + 1, _P(self.d), st)
+            if self.depth_rms is None:
+                self._call("loom_gqa_decode_step_depth", self.code, _P(self.qkv), _P(kc), _P(vc),
+                           cache_sb, cache_st, cache_sh, _P(self.cos), _P(self.sin), _P(self.q),
+                           _P(self.c), _P(self.kctx), N,
+                           _P(self.ws), self.ws_bytes, B, self.max_len, _P(self.pos_dev), c.QH,
+                           c.KVH, c.HD, _P(self.qp[sub]), _P(self.hist), _P(self.hist[:, :, N:]),
+                           2 * L * 2 * N, 2 * N, sub + 1, _P(self.d), st)
+            else:
+                self._call("loom_gqa_decode_step", self.code, _P(self.qkv), _P(kc), _P(vc),
+                           cache_sb, cache_st, cache_sh, _P(self.cos), _P(self.sin), _P(self.q),
+                           _P(self.c), _P(self.kctx), N, _P(self.ws), self.ws_bytes, B,
+                           self.max_len, _P(self.pos_dev), c.QH, c.KVH, c.HD, st)
+                self.depth_read(sub, self.hist, self.d, B)
             # ---- LN(o(c) + w_o(d)) (loomformer.py:3999-4000): both products
             # accumulate in one launch
             self._linear_ln(("attn", bi), self.c.view(B, N),
-                            dict(w=blk["o"], w2=self.wo, out=self.y), self.d.view(B, N),
+                            dict(w=blk["o"], w2=self.wo_for(sub), out=self.y), self.d.view(B, N),
                             blk["ln1_w"], blk["ln1_b"])
             # ---- history slot 2*bi+1 (loomformer.py:4004) and W_real of the same h
-            # (+ IdentityAnchoredGate with the previous block's p, loomformer.py:2839)
+            # (+ IdentityAnchoredGate with the previous block's p, loomformer.py:2839;
+            # + gate_proj(h), the amplitude source under paraplex_gate_proj, :2849)
             sub += 1
             real = dict(w=blk["w1r"], out=self.R, bias=blk["b1r"])
             if p_i is not None:
                 real.update(gate_p=self.p[p_i], gate_alpha=blk["alpha"])
-            self._multi(("kvr", bi), self.h, [dict(w=self.kvw, out=hist[:, sub]), real])
-            self._depth(sub, self.dh)
+            segs = [dict(w=self.kvw, out=hist[:, sub]), real]
+            if c.gate_proj:
+                segs.append(dict(w=blk["gpw"], out=self.G, bias=blk["gpb"]))
+            self._multi(("kvr", bi), self.h, segs)
+            self.depth_read(sub, self.hist, self.dh, B)
             # ---- Paraplex FFN core (beta space, fused pointwise chain; loomformer.py:
             # 2818-2893, :2533-2560) and the Tria depth op (loomformer.py:4012-4040,
             # axis = bi % 3) of this token, one launch in bf16
@@ -271,7 +320,8 @@ class LoomDecoder:
                     u=self.h, q_h=self.q, k_ctx_h=self.kctx, c_h=self.c, d_h=self.dh,
                     w_compact=blk["w1i"], M=B, N=N, H=H, imag_in=c.imag_in, hidden_per_q_head=c.Hq,
                     head_dim=c.HD, n_q_heads=c.QH, open_sectors=1 if c.sectors == "open" else 0,
-                    p_real=self.R, imag_bias=blk["ib"], trace=self.trace[bi], trace_w=blk["tw"],
+                    p_real=self.R, gate_src=self.G, imag_bias=blk["ib"], trace=self.trace[bi],
+                    trace_w=blk["tw"],
                     powlu_m=float(c.powlu_m), act=self.act, s=self.s, beta=self.beta,
                     carry_prev=None if (carry_i is None or use_seed) else self.carry[carry_i],
                     seed=self.doc if use_seed else None,
@@ -283,8 +333,8 @@ class LoomDecoder:
             carry_i, p_i = out_i, new_p
             # ---- LN(w_o(d_h) + W2(act) + b2) (loomformer.py:4045): one launch + LN
             self._linear_ln(("ffn", bi), self.dh.view(B, N),
-                            dict(w=self.wo, w2=blk["w2"], out=self.y, bias=blk["b2"]), self.act,
-                            blk["ln2_w"], blk["ln2_b"])
+                            dict(w=self.wo_for(sub), w2=blk["w2"], out=self.y, bias=blk["b2"]),
+                            self.act, blk["ln2_w"], blk["ln2_b"])
             if not last:
                 # next history slot (loomformer.py:4050) and the next block's qkv
                 sub += 1
@@ -312,20 +362,12 @@ class LoomDecoder:
                    _P(self.ca_v), self.max_keys * N, _P(self.ca_valid), self.max_keys,
                    _P(self.h), float(self.gamma), _P(self.h2), None, B, 1, self.max_keys,
                    _P(self.ca_len), N, float(N ** -0.5), st)
-        self._linear(self.h2, self.head, self.logits, B, c.V, N)
+        self.head_logits(self.h2, self.logits, B)
 
     def _argmax(self) -> None:
         """ids = argmax(logits) per row (infer's greedy pick, loomformer.py:5306)."""
         self._call("loom_argmax_rows", self.code, _P(self.logits), self.B, self.cfg.V, _P(self.ids),
                    self._stream())
-
-    def _depth(self, sub: int, out: torch.Tensor) -> None:
-        """DepthAttn read over history slots [0, sub] (loomformer.py:3404-3429, tensor branch)."""
-        c, N, L = self.cfg, self.cfg.N, self.cfg.L
-        hist_bt = 2 * L * 2 * N
-        self._call("loom_depth_attn_forward", self.code, _P(self.qp[sub]), _P(self.hist),
-                   _P(self.hist[:, :, N:]), hist_bt, 2 * N, _P(out), None, None, self.B, sub + 1,
-                   c.QH, c.HD, self._stream())
 
     def _check_ids(self, ids: torch.Tensor) -> None:
         """Token ids must index the embedding table (nn.Embedding raises otherwise)."""

@@ -80,6 +80,7 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     d = z(M, N)
     dh = z(M, N)
     R = z(M, H)
+    gbuf = z(M, H) if c.gate_proj else None
     beta = z(M, H)
     act = z(M, H)
     sbuf = z(M, H)
@@ -93,7 +94,6 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     stage_k, stage_v = z(B, N), z(B, N)
     snap = torch.empty((), dtype=torch.float32, device=dev)
     empty_reset = None
-    hist_bt = 2 * L * 2 * N
     cache_sb = KVH * eng.max_len * HD
     cache_st = HD
     cache_sh = eng.max_len * HD
@@ -102,8 +102,7 @@ def prefill(eng, prompt: torch.Tensor) -> None:
         eng._linear(x, w, out, rows, nout, k, **kw)
 
     def depth(sub, out, rows):
-        call("loom_depth_attn_forward", code, _P(eng.qp[sub]), _P(hist), _P(hist[:, :, N:]),
-             hist_bt, 2 * N, _P(out), None, None, rows, sub + 1, QH, HD, st)
+        eng.depth_read(sub, hist, out, rows)
 
     have_state = False
     tin = 0
@@ -130,7 +129,7 @@ def prefill(eng, prompt: torch.Tensor) -> None:
             # ---- LN(o(C) + w_o(depth read 2*bi)) (loomformer.py:3999-4000)
             depth(sub, d, rows)
             lin(cbuf, blk["o"], y, rows, N, N)
-            lin(d, eng.wo, y, rows, N, N, residual=y)
+            lin(d, eng.wo_for(sub), y, rows, N, N, residual=y)
             call("loom_add_layernorm", code, _P(y), None, _P(blk["ln1_w"]), _P(blk["ln1_b"]),
                  _P(h), rows, N, 1e-5, st)
             # ---- history slot 2*bi+1, W_real (+ gate with the previous block's p)
@@ -143,11 +142,16 @@ def prefill(eng, prompt: torch.Tensor) -> None:
                     gate_alpha=blk["alpha"])
             depth(sub, dh, rows)
             # ---- Paraplex FFN (loomformer.py:2818-2893): beta space, fused pointwise
-            # chain with the phase trace carried from the previous chunk
+            # chain with the phase trace carried from the previous chunk; the
+            # amplitude source is R, or gate_proj(h) under paraplex_gate_proj (:2849)
             call("loom_beta_forward", code, _P(h), _P(q), _P(kctx), _P(cbuf), _P(dh),
                  _P(blk["w1i"]), _P(beta), None, rows, N, H, c.imag_in, c.Hq, HD, QH,
                  1 if c.sectors == "open" else 0, st)
-            call("loom_paraplex_forward", code, _P(R), _P(R), _P(beta), _P(blk["ib"]),
+            gsrc = R
+            if c.gate_proj:
+                gsrc = gbuf
+                lin(h, blk["gpw"], gbuf, rows, H, N, bias=blk["gpb"])
+            call("loom_paraplex_forward", code, _P(R), _P(gsrc), _P(beta), _P(blk["ib"]),
                  _P(traces[tin, bi]), _P(blk["tw"]), empty_reset, _P(blk["anchor"]), _P(act),
                  _P(sbuf), _P(traces[1 - tin, bi]), _P(snap), B, Tc, H, float(c.powlu_m), st)
             # ---- Tria depth op of the block (loomformer.py:3588-3617), axis bi % 3
@@ -163,7 +167,7 @@ def prefill(eng, prompt: torch.Tensor) -> None:
                  bi % 3, st)
             carry_i, p_i = out_i, new_p
             # ---- LN(w_o(d_h) + W2(act) + b2) (loomformer.py:4045)
-            lin(dh, eng.wo, y, rows, N, N)
+            lin(dh, eng.wo_for(sub), y, rows, N, N)
             lin(act, blk["w2"], y, rows, N, H, bias=blk["b2"], residual=y)
             call("loom_add_layernorm", code, _P(y), None, _P(blk["ln2_w"]), _P(blk["ln2_b"]),
                  _P(h), rows, N, 1e-5, st)
@@ -213,7 +217,7 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     call("loom_final_ca_sparse_strided", code, _P(eng.q_ca), _P(eng.ca_k), _P(eng.ca_v),
          eng.max_keys * N, _P(eng.ca_valid), eng.max_keys, _P(eng.h), float(eng.gamma),
          _P(eng.h2), None, B, 1, eng.max_keys, _P(eng.ca_len), N, float(N ** -0.5), st)
-    lin(eng.h2, eng.head, eng.logits, B, c.V, N)
+    eng.head_logits(eng.h2, eng.logits, B)
     # ---- the engine's decode state after position P-1
     eng.trace.copy_(traces[tin])
     eng.doc.copy_(state)

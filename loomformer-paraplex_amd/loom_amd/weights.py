@@ -52,6 +52,8 @@ def init_state_dict(cfg: ModelConfig, seed: int) -> Dict[str, torch.Tensor]:
         w1r, b1r = _linear(H, N)
         w1i = torch.empty(H, cfg.imag_in)
         w2, b2 = _linear(N, H)
+        if cfg.gate_proj:                                # ParaplexFFN.gate_proj (:2704-2707)
+            gpw, gpb = _linear(H, N)
         nn.init.normal_(w1r, 0.0, _fanin(N))
         b1r.zero_()
         nn.init.normal_(w1i, 0.0, _fanin(cfg.imag_in))
@@ -64,14 +66,23 @@ def init_state_dict(cfg: ModelConfig, seed: int) -> Dict[str, torch.Tensor]:
         sd[p + "ffn.beta_anchor"] = torch.tensor(1.0)
         sd[p + "ffn.gate_selector.logits"] = torch.zeros(9)
         sd[p + "ffn.identity_gate.raw_alpha"] = torch.zeros(())
+        if cfg.gate_proj:                                # init_linear_fanin (:2717-2718)
+            nn.init.normal_(gpw, 0.0, _fanin(N))
+            gpb.zero_()
+            sd[p + "ffn.gate_proj.weight"], sd[p + "ffn.gate_proj.bias"] = gpw, gpb
     kvw = torch.empty(2 * N, N)
-    wo, _ = _linear(N, N, bias=False)
+    if cfg.depth_readout == "per-sublayer":              # DepthAttn.__init__ (:3373-3378)
+        wo = torch.empty(2 * L, N, N)
+    else:
+        wo, _ = _linear(N, N, bias=False)
     qp = torch.empty(2 * L, cfg.QH, cfg.HD)
     nn.init.normal_(kvw[:N], 0.0, _fanin(N))
     nn.init.normal_(kvw[N:], 0.0, _fanin(N) * rbeta)
     nn.init.normal_(wo, 0.0, _fanin(N) * rbeta)
     nn.init.normal_(qp, 0.0, _fanin(cfg.HD))
-    sd["depth_attn.kv_weight"], sd["depth_attn.w_o.weight"], sd["depth_attn.q_params"] = kvw, wo, qp
+    sd["depth_attn.kv_weight"] = kvw
+    sd["depth_attn.w_o_weight" if cfg.depth_readout == "per-sublayer" else "depth_attn.w_o.weight"] = wo
+    sd["depth_attn.q_params"] = qp
     head, _ = _linear(cfg.V, N, bias=False)
     proj_w, proj_b = _linear(32, 9)
     key_w, _ = _linear(32, 9, bias=False)
@@ -82,6 +93,8 @@ def init_state_dict(cfg: ModelConfig, seed: int) -> Dict[str, torch.Tensor]:
     nn.init.normal_(emb, 0.0, _fanin(N))
     sd["emb.weight"] = emb
     sd["head.weight"] = emb if cfg.tied else head
+    if cfg.final_norm:                                   # Model.ln_final (:3490)
+        sd["ln_final.weight"] = torch.ones(N)
     sd["tria_agg.reader.proj.weight"], sd["tria_agg.reader.proj.bias"] = proj_w, proj_b
     sd["tria_agg.reader.key_proj.weight"] = key_w
     sd["tria_agg.pool.query"] = torch.zeros(32)
@@ -90,6 +103,31 @@ def init_state_dict(cfg: ModelConfig, seed: int) -> Dict[str, torch.Tensor]:
     sd["tria_final_ca.w_qk.weight"], sd["tria_final_ca.w_v.weight"] = wqk, wv
     sd["tria_final_ca.raw_gamma"] = torch.tensor(float(cfg.raw_gamma_init))
     return sd
+
+
+def state_keys(cfg: ModelConfig):
+    """The state_dict keys of the reference's Model for `cfg` (what
+    init_state_dict returns and a checkpoint of that config holds)."""
+    keys = ["emb.weight"]
+    for bi in range(cfg.L):
+        p = f"blocks.{bi}."
+        keys += [p + k for k in (
+            "ln_attn.weight", "ln_attn.bias", "attn.qkv_weight", "attn.o.weight", "ln_ffn.weight",
+            "ln_ffn.bias", "ffn.w1_real.weight", "ffn.w1_real.bias", "ffn.w1_imag",
+            "ffn.w1_imag_trace", "ffn.w1_imag_bias", "ffn.w2.weight", "ffn.w2.bias",
+            "ffn.beta_anchor", "ffn.gate_selector.logits", "ffn.identity_gate.raw_alpha")]
+        if cfg.gate_proj:
+            keys += [p + "ffn.gate_proj.weight", p + "ffn.gate_proj.bias"]
+    keys += ["depth_attn.kv_weight", "depth_attn.q_params",
+             "depth_attn.w_o_weight" if cfg.depth_readout == "per-sublayer" else "depth_attn.w_o.weight",
+             "head.weight"]
+    if cfg.final_norm:
+        keys.append("ln_final.weight")
+    keys += ["tria_agg.reader.proj.weight", "tria_agg.reader.proj.bias",
+             "tria_agg.reader.key_proj.weight", "tria_agg.pool.query", "tria_agg.pool.logit_scale_raw",
+             "tria_agg.up.weight", "tria_agg.up.bias", "tria_final_ca.w_qk.weight",
+             "tria_final_ca.w_v.weight", "tria_final_ca.raw_gamma"]
+    return keys
 
 
 def rope_tables(cfg: ModelConfig, length: int) -> Tuple[torch.Tensor, torch.Tensor]:

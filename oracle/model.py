@@ -55,6 +55,12 @@ class Shapes:
     rope_beta_slow: float = 1.0
     rope_attention_factor: Optional[float] = None
     carry_token_id: Optional[int] = None
+    # model variants (Config, loomformer.py:272-274, :358, :366)
+    gate_proj: bool = False
+    qkv_rms: bool = False
+    rms_cap: Optional[float] = None
+    final_norm: bool = False
+    readout: str = "shared"
 
     @property
     def Hq(self) -> int:
@@ -130,6 +136,12 @@ class Shapes:
             rope_attention_factor=(None if d.get("rope_attention_factor") is None
                                    else float(d["rope_attention_factor"])),
             carry_token_id=(None if d.get("carry_token_id") is None else int(d["carry_token_id"])),
+            gate_proj=bool(d.get("paraplex_gate_proj", False)),
+            qkv_rms=bool(d.get("depth_attn_qkv_rms", False)),
+            rms_cap=(None if d.get("residual_branch_rms_cap") is None
+                     else float(d["residual_branch_rms_cap"])),
+            final_norm=bool(d.get("final_norm", False)),
+            readout=str(d.get("depth_attn_readout", "shared") or "shared").lower(),
         )
 
     @staticmethod
@@ -141,8 +153,32 @@ class Shapes:
 
 
 def fanin_std(fan_in: int, gain: float = FANIN_GAIN) -> float:
-    """loomformer.py:826-829."""
+    """loomformer.py:829-832."""
     return gain / math.sqrt(float(fan_in))
+
+
+def fixed_rms(x: torch.Tensor, target: float = 1.0, eps: float = 1e-6) -> torch.Tensor:
+    """Each last-dim vector scaled by target / sqrt(mean(x^2) + eps), the scale
+    rounded to x's dtype (loomformer.py:840-844)."""
+    work = x.float() if x.dtype in (torch.float16, torch.bfloat16) else x
+    scale = torch.rsqrt(work.square().mean(dim=-1, keepdim=True) + eps) * float(target)
+    return x * scale.to(dtype=x.dtype)
+
+
+def capped_rms(x: torch.Tensor, maximum: float = 1.0, eps: float = 1e-6) -> torch.Tensor:
+    """RMS scaling down to `maximum`, never up (loomformer.py:847-852)."""
+    work = x.float() if x.dtype in (torch.float16, torch.bfloat16) else x
+    rms = torch.sqrt(work.square().mean(dim=-1, keepdim=True) + eps)
+    scale = (float(maximum) / rms).clamp(max=1.0)
+    return x * scale.to(dtype=x.dtype)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm.forward (loomformer.py:3460-3464): fp32 statistics, the
+    normalised row rounded to x's dtype, then the learned scale."""
+    xf = x.float()
+    rms = torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return (xf * rms).to(x.dtype) * weight
 
 
 # --------------------------------------------------------------------------
@@ -189,12 +225,17 @@ class _FFN(nn.Module):
         self.register_buffer("beta_anchor", torch.tensor(1.0), persistent=True)
         self.gate_selector = _GateSelector()
         self.identity_gate = _IdentityGate()
+        # the independent amplitude source of paraplex_gate_proj (loomformer.py:2704-2707)
+        self.gate_proj = nn.Linear(S.N, S.H) if S.gate_proj else None
         rstd = fanin_std(S.H) * (S.deepnorm_beta if S.residual_init == "beta" else 1.0)
         nn.init.normal_(self.w1_real.weight, mean=0.0, std=fanin_std(S.N))
         nn.init.zeros_(self.w1_real.bias)
         nn.init.normal_(self.w1_imag, mean=0.0, std=fanin_std(S.imag_in))
         nn.init.normal_(self.w2.weight, mean=0.0, std=rstd)
         nn.init.zeros_(self.w2.bias)
+        if self.gate_proj is not None:                      # loomformer.py:2717-2718
+            nn.init.normal_(self.gate_proj.weight, mean=0.0, std=fanin_std(S.N))
+            nn.init.zeros_(self.gate_proj.bias)
 
 
 class _Block(nn.Module):
@@ -207,18 +248,31 @@ class _Block(nn.Module):
 
 
 class _DepthAttn(nn.Module):
-    """DepthAttn parameters, shared readout (loomformer.py:3367-3389)."""
+    """DepthAttn parameters (loomformer.py:3367-3389): one shared readout w_o,
+    or with depth_attn_readout = per-sublayer one [N, N] readout per sublayer
+    in w_o_weight [2L, N, N]."""
 
     def __init__(self, S: Shapes) -> None:
         super().__init__()
         self.kv_weight = nn.Parameter(torch.empty(2 * S.N, S.N))
-        self.w_o = nn.Linear(S.N, S.N, bias=False)
+        if S.readout == "per-sublayer":
+            self.w_o_weight = nn.Parameter(torch.empty(2 * S.L, S.N, S.N))
+            self.w_o = None
+        else:
+            self.w_o_weight = None
+            self.w_o = nn.Linear(S.N, S.N, bias=False)
         self.q_params = nn.Parameter(torch.empty(2 * S.L, S.QH, S.HD))
         rstd = fanin_std(S.N) * (S.deepnorm_beta if S.residual_init == "beta" else 1.0)
         nn.init.normal_(self.kv_weight[:S.N], mean=0.0, std=fanin_std(S.N))
         nn.init.normal_(self.kv_weight[S.N:], mean=0.0, std=rstd)
-        nn.init.normal_(self.w_o.weight, mean=0.0, std=rstd)
+        nn.init.normal_(self.w_o_weight if self.w_o is None else self.w_o.weight, mean=0.0, std=rstd)
         nn.init.normal_(self.q_params, mean=0.0, std=fanin_std(S.HD))
+
+
+class _RMSNormParams(nn.Module):
+    def __init__(self, dim: int) -> None:   # RMSNorm.__init__ (loomformer.py:3452-3458)
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
 
 
 class _Reader(nn.Module):
@@ -297,10 +351,18 @@ class OracleModel(nn.Module):
         self.head = nn.Linear(S.N, S.V, bias=False)
         if S.tied:
             self.head.weight = self.emb.weight
+        # final_norm: one RMSNorm before the head (loomformer.py:3490)
+        self.ln_final = _RMSNormParams(S.N) if S.final_norm else None
         reader = _Reader(k=32)
         self.tria_agg = _Agg(reader, S.N)
         self.tria_final_ca = _FinalCA(S.N, S.gamma_max, S.raw_gamma_init)
         nn.init.normal_(self.emb.weight, mean=0.0, std=fanin_std(S.N))
+        # Model.step never applies residual_branch_rms_cap: only _block_core, the
+        # sequence forward, caps its branches (loomformer.py:3568-3570, :3627-3629;
+        # step's sublayer tails are :3998-4000, :4045).  Setting this to a cap
+        # applies it in step too; tests use that to show the fixtures tell the
+        # two apart.
+        self.step_branch_cap: Optional[float] = None
         inv_freq, att = ops.yarn_inv_freq(S.HD, S.rope_theta, S.rope_factor, S.rope_original,
                                           S.rope_beta_fast, S.rope_beta_slow,
                                           S.rope_attention_factor)
@@ -314,14 +376,24 @@ class OracleModel(nn.Module):
         B, T, _ = h.shape
         kv = F.linear(h, self.depth_attn.kv_weight)
         k, v = torch.split(kv, (S.N, S.N), dim=-1)
-        return k.reshape(B, T, S.QH, S.HD), v.reshape(B, T, S.QH, S.HD)
+        k, v = k.reshape(B, T, S.QH, S.HD), v.reshape(B, T, S.QH, S.HD)
+        if S.qkv_rms:                                  # loomformer.py:3397-3401
+            k = fixed_rms(k, FANIN_GAIN)
+            v = fixed_rms(v, FANIN_GAIN * S.deepnorm_beta)
+        return k, v
 
     def depth_read(self, sub_idx: int, hist_k, hist_v) -> Tuple[torch.Tensor, torch.Tensor]:
         """DepthAttn.forward, tensor-history branch (loomformer.py:3404-3429)."""
         S = self.S
-        d = ops.depth_attn_online(self.depth_attn.q_params[sub_idx], hist_k, hist_v)
+        q_row = self.depth_attn.q_params[sub_idx]
+        if S.qkv_rms:                                  # loomformer.py:3406-3407
+            q_row = fixed_rms(q_row, fanin_std(S.HD))
+        d = ops.depth_attn_online(q_row, hist_k, hist_v)
         B, T = hist_k.shape[:2]
-        return self.depth_attn.w_o(d.reshape(B, T, S.N)), d
+        d_flat = d.reshape(B, T, S.N)
+        if self.depth_attn.w_o is None:                # per-sublayer readout (:3424-3428)
+            return F.linear(d_flat, self.depth_attn.w_o_weight[sub_idx]), d
+        return self.depth_attn.w_o(d_flat), d
 
     def attn_step(self, blk: _Block, z: torch.Tensor, pos: int, cache: LayerCache):
         """GroupedQueryCausalSelfAttention.step (loomformer.py:3300-3332)."""
@@ -373,8 +445,10 @@ class OracleModel(nn.Module):
         r_all = torch.cat([q_h.reshape(B, -1, S.N), k_ctx_h.reshape(B, -1, S.N),
                            c_h.reshape(B, -1, S.N), u, d_h.reshape(B, -1, S.N)], dim=-1)
         beta_lin = F.linear(r_all, f._dense_w)                   # loomformer.py:2771-2777
+        # amplitude source: p_real itself, or gate_proj(u) (loomformer.py:2849)
+        gate_src = p_real if f.gate_proj is None else f.gate_proj(u)
         act, s, next_trace = ops.paraplex_pointwise(
-            p_real, p_real, beta_lin, f.w1_imag_bias, phase_trace, f.w1_imag_trace, None, S.powlu_m)
+            p_real, gate_src, beta_lin, f.w1_imag_bias, phase_trace, f.w1_imag_trace, None, S.powlu_m)
         return f.w2(act), next_trace, (p_real, s, act)
 
     def tria_agg_fn(self, carry: torch.Tensor) -> torch.Tensor:
@@ -436,6 +510,9 @@ class OracleModel(nn.Module):
             last = bi == S.L - 1
             attn_out, q_h, kctx_h, c_h = self.attn_step(blk, h, pos, cache)
             skip, _ = self.depth_read(sub, hist_k[:, :, :sub + 1], hist_v[:, :, :sub + 1])
+            if self.step_branch_cap is not None:
+                skip = capped_rms(skip, self.step_branch_cap)
+                attn_out = capped_rms(attn_out, self.step_branch_cap)
             h = F.layer_norm(skip + attn_out, (S.N,), blk.ln_attn.weight, blk.ln_attn.bias, 1e-5)
             k_i, v_i = self.kv_project(h)
             sub += 1
@@ -446,6 +523,9 @@ class OracleModel(nn.Module):
                                                       cache.phase_trace, p)
             w = torch.softmax(blk.ffn.gate_selector.logits, dim=0)
             carry, p = tria_layer_op(bi, last, r, i, o, carry, seed, seed_valid, w, S.tria_alpha)
+            if self.step_branch_cap is not None:
+                skip = capped_rms(skip, self.step_branch_cap)
+                ffn_out = capped_rms(ffn_out, self.step_branch_cap)
             h = F.layer_norm(skip + ffn_out, (S.N,), blk.ln_ffn.weight, blk.ln_ffn.bias, 1e-5)
             if not last:
                 k_i, v_i = self.kv_project(h)
@@ -463,7 +543,13 @@ class OracleModel(nn.Module):
         a_t = self.tria_agg_fn(doc.unsqueeze(1))
         h = self.final_ca_step(a_t, h, state.ca, fire)
         state.temporal = TemporalState(carry=doc, pending=fire)
-        return self.head(h[:, -1, :]), state
+        return self.head_in(h[:, -1, :]), state
+
+    def head_in(self, x: torch.Tensor) -> torch.Tensor:
+        """Model._head_in (loomformer.py:3527-3529): the optional final RMSNorm, then the head."""
+        if self.ln_final is not None:
+            x = rms_norm(x, self.ln_final.weight)
+        return self.head(x)
 
 
 def tria_layer_op(bi: int, last: bool, r, i, o, carry, seed, seed_valid, w, alpha: float):

@@ -12,9 +12,13 @@ expected outputs); nothing of the reference's source is stored.
 
 Fixtures:
   init_sha256.json   per-tensor sha256 of Model(cfg).state_dict() for
-                     nano.yaml seed 0, nano_chk.yaml seed 2, and the tiny config
+                     nano.yaml seed 0, nano_chk.yaml seed 2, the tiny config
+                     and the tiny config with every variant flag
   tiny_decode.npz    tiny config: perturbed weights, prompts, per-step logits and
                      greedy ids of Model.step (with and without a <CARRY> id)
+  variants_decode.npz  the same for the tiny config with every model variant
+                     flag set (gate_proj, qkv_rms, branch cap, final_norm,
+                     per-sublayer depth readout)
   nano_cpu_ref.npz   nano.yaml seed 0, B=1, 128-token prompt + 64 greedy ids,
                      per-step top-5 logits
   ops.npz            per-op input/output vectors at small shapes
@@ -45,6 +49,12 @@ TINY = dict(
     use_cuda_beta_space=False, use_cuda_phase_sin=False, use_cuda_pvpowlu=False,
     use_cuda_depth_attn=False, amp_dtype="fp32", device="cpu",
 )
+
+# the tiny config with every math-changing model variant a checkpoint can carry
+# (Config, loomformer.py:272-274, :358, :366); the branch cap is small enough
+# to bind wherever it is applied
+VARIANTS = dict(paraplex_gate_proj=True, depth_attn_qkv_rms=True, residual_branch_rms_cap=0.05,
+                final_norm=True, depth_attn_readout="per-sublayer")
 
 NO_CUDA = dict(use_cuda_tria=False, use_cuda_beta_space=False, use_cuda_phase_sin=False,
                use_cuda_pvpowlu=False, use_cuda_depth_attn=False, device="cpu", amp_dtype="fp32")
@@ -81,7 +91,8 @@ def state_sha(model) -> dict:
 
 PERTURB = ("identity_gate.raw_alpha", "w1_imag_trace", "w1_imag_bias", "w1_real.bias",
            "w2.bias", "gate_selector.logits", "pool.query", "ln_attn.weight", "ln_attn.bias",
-           "ln_ffn.weight", "ln_ffn.bias", "up.bias", "proj.bias", "raw_gamma")
+           "ln_ffn.weight", "ln_ffn.bias", "up.bias", "proj.bias", "raw_gamma",
+           "gate_proj.bias", "ln_final.weight")
 
 
 def perturb(model, seed: int) -> None:
@@ -121,7 +132,37 @@ def golden_init(lf, ref: str) -> dict:
     cfg = make_cfg(lf, None, **TINY)
     torch.manual_seed(0)
     out["tiny_seed0"] = state_sha(lf.Model(cfg))
+    cfg = make_cfg(lf, None, **dict(TINY, **VARIANTS))
+    torch.manual_seed(0)
+    out["tiny_variants_seed0"] = state_sha(lf.Model(cfg))
+    make_cfg(lf, None, **TINY)
     return out
+
+
+def golden_variants(lf) -> dict:
+    """Model.step of the tiny config with every variant flag set, perturbed
+    weights, with and without <CARRY> ids."""
+    cfg = make_cfg(lf, None, **dict(TINY, **VARIANTS))
+    torch.manual_seed(0)
+    model = lf.Model(cfg).eval()
+    perturb(model, 321)
+    arrays = {f"w::{k}": v.detach().numpy() for k, v in model.state_dict().items()}
+    g = torch.Generator().manual_seed(17)
+    prompt = torch.randint(0, TINY["vocab"], (3, 20), generator=g)
+    lf.CARRY_TOKEN_ID = None
+    ids, logits = run_decode(lf, model, prompt, 12)
+    arrays["prompt"], arrays["greedy"], arrays["logits"] = prompt.numpy(), ids.numpy(), logits.numpy()
+    prompt2 = prompt.clone()
+    prompt2[0, 6] = 5
+    prompt2[1, 2] = 5
+    prompt2[2, 11] = 5
+    lf.CARRY_TOKEN_ID = 5
+    ids2, logits2 = run_decode(lf, model, prompt2, 12)
+    lf.CARRY_TOKEN_ID = None
+    arrays["prompt_carry"], arrays["greedy_carry"] = prompt2.numpy(), ids2.numpy()
+    arrays["logits_carry"] = logits2.numpy()
+    make_cfg(lf, None, **TINY)
+    return arrays
 
 
 def golden_tiny_decode(lf) -> dict:
@@ -347,6 +388,7 @@ def main() -> None:
                 d = yaml.safe_load(f)
             cfgs[name] = {k: d[k] for k in keep if k in d}
         cfgs["tiny"] = {k: v for k, v in TINY.items() if k in keep}
+        cfgs["tiny_variants"] = dict(cfgs["tiny"], **VARIANTS)
         with open(os.path.join(HERE, "configs.json"), "w") as f:
             json.dump(cfgs, f, indent=1, sort_keys=True)
         print("wrote configs.json")
@@ -357,6 +399,9 @@ def main() -> None:
     if not only or "tiny" in only:
         np.savez_compressed(os.path.join(HERE, "tiny_decode.npz"), **golden_tiny_decode(lf))
         print("wrote tiny_decode.npz")
+    if not only or "variants" in only:
+        np.savez_compressed(os.path.join(HERE, "variants_decode.npz"), **golden_variants(lf))
+        print("wrote variants_decode.npz")
     if not only or "ops" in only:
         np.savez_compressed(os.path.join(HERE, "ops.npz"), **golden_ops(lf, tr))
         print("wrote ops.npz")

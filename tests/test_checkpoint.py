@@ -113,16 +113,39 @@ def test_aio_suffix_required(tmp_path):
         load_aio(str(tmp_path / "x.pt"))
 
 
-@pytest.mark.parametrize("flag,value", [("paraplex_gate_proj", True), ("depth_attn_qkv_rms", True),
-                                        ("residual_branch_rms_cap", 2.0), ("final_norm", True),
-                                        ("depth_attn_readout", "per-sublayer")])
-def test_config_refuses_variant_flags_the_engine_lacks(flag, value):
-    """A math-changing model flag the engine does not compute is refused, not
-    silently dropped (loomformer.py:272-274, :358, :366)."""
+@pytest.mark.parametrize("flag,value,field,want", [
+    ("paraplex_gate_proj", True, "gate_proj", True), ("depth_attn_qkv_rms", True, "depth_qkv_rms", True),
+    ("residual_branch_rms_cap", 2.0, "residual_rms_cap", 2.0), ("final_norm", True, "final_norm", True),
+    ("depth_attn_readout", "Per-Sublayer", "depth_readout", "per-sublayer")])
+def test_config_carries_variant_flags(flag, value, field, want):
+    """The math-changing model flags (loomformer.py:272-274, :358, :366) reach
+    the engine's config instead of being dropped."""
     from loom_amd.config import ModelConfig
     cfg, _ = _tiny()
-    with pytest.raises(ValueError, match=flag):
-        ModelConfig.from_dict(dict(cfg, **{flag: value}))
+    assert getattr(ModelConfig.from_dict(dict(cfg, **{flag: value})), field) == want
+
+
+@pytest.mark.parametrize("flag,value", [("paraplex_gate_proj", True), ("final_norm", True),
+                                        ("depth_attn_readout", "per-sublayer")])
+def test_checkpoint_refuses_weights_that_do_not_match_its_variant_flags(tmp_path, flag, value):
+    """A config that sets a variant whose weights the state dict lacks (or the
+    other way round) is refused like the reference's strict load, not decoded
+    as a different model."""
+    from loom_amd.checkpoint import load_checkpoint
+    cfg, state = _tiny()
+    path = tmp_path / "ck.pt"
+    torch.save({"cfg": dict(cfg, **{flag: value}), "model": state}, path)
+    with pytest.raises(ValueError, match="does not match its config"):
+        load_checkpoint(str(path))
+    # and the variant's own checkpoint loads
+    z = np.load(os.path.join(GOLD, "variants_decode.npz"))
+    with open(os.path.join(GOLD, "configs.json")) as f:
+        vcfg = json.load(f)["tiny_variants"]
+    vstate = {k[3:]: torch.from_numpy(z[k]) for k in z.files if k.startswith("w::")}
+    torch.save({"cfg": vcfg, "model": vstate}, path)
+    loaded = load_checkpoint(str(path))
+    assert loaded.cfg.gate_proj and loaded.cfg.final_norm
+    assert loaded.cfg.depth_readout == "per-sublayer"
 
 
 def test_config_validates_variant_values_like_apply_config():

@@ -48,6 +48,21 @@ def check(got, want, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rows,N", [(32, 768), (3, 32), (5, 20), (1, 2048)])
+def test_rms_norm(dtype, rows, N):
+    """final_norm's RMSNorm (loomformer.py:3460-3464) against the oracle's
+    restatement, with the weight in the model dtype."""
+    from oracle.model import rms_norm
+    g = torch.Generator().manual_seed(rows * 7 + N)
+    x = (torch.randn(rows, N, generator=g) * 3).to(DEV, dtype)
+    w = (torch.randn(N, generator=g) * 0.5 + 1).to(DEV, dtype)
+    out = torch.empty_like(x)
+    L().call("loom_rms_norm", code(x), P(x), P(w), P(out), rows, N, 1e-6, S(x))
+    want = rms_norm(x.cpu(), w.cpu()).float()     # in the model dtype, as the reference rounds
+    check(out, want, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,N", [(32, 768), (3, 32), (5, 20), (1, 2048)])
 def test_add_layernorm(dtype, rows, N):
     g = torch.Generator().manual_seed(rows + N)
     a = torch.randn(rows, N, generator=g).to(DEV, dtype)
@@ -422,14 +437,17 @@ def test_linear_multi(dtype, M):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("mode,gate,axis", [(1, True, 0), (1, True, 1), (1, False, 2),
-                                            (0, True, 2), (2, True, 1), (2, False, 0)])
-def test_ffn_decode(dtype, mode, gate, axis):
+@pytest.mark.parametrize("mode,gate,axis,gsrc", [(1, True, 0, False), (1, True, 1, False),
+                                                 (1, False, 2, False), (0, True, 2, False),
+                                                 (2, True, 1, False), (2, False, 0, False),
+                                                 (1, True, 1, True), (2, False, 2, True)])
+def test_ffn_decode(dtype, mode, gate, axis, gsrc):
     """One decode token of beta space -> Paraplex chain -> Tria depth op (one
     launch in bf16) against the oracle: beta_space_grouped, paraplex_pointwise
-    and tria_*_and_gate on the same (dtype-rounded) inputs."""
+    and tria_*_and_gate on the same (dtype-rounded) inputs; with gsrc the
+    amplitude comes from a separate gate source (paraplex_gate_proj)."""
     from loom_amd import _lib
-    g = torch.Generator().manual_seed(10 * mode + axis + (5 if gate else 0))
+    g = torch.Generator().manual_seed(10 * mode + axis + (5 if gate else 0) + (50 if gsrc else 0))
     M, QH, HD, H = 32, 8, 96, 3072
     N = QH * HD
     K = N + 4 * HD
@@ -438,6 +456,7 @@ def test_ffn_decode(dtype, mode, gate, axis):
     q, kc, c, d = (r(M, QH, HD) for _ in range(4))
     w = r(H, K, sc=K ** -0.5)
     R = r(M, H, sc=2.0)
+    G = r(M, H, sc=2.0) if gsrc else None
     ib = (torch.randn(H, generator=g) * 0.3).to(DEV)
     tw = (torch.rand(H, generator=g) - 0.5).to(DEV)
     trace0 = r(M, H, sc=0.5)
@@ -451,16 +470,16 @@ def test_ffn_decode(dtype, mode, gate, axis):
     desc = _lib.ffn_decode_desc(
         u=u, q_h=q, k_ctx_h=kc, c_h=c, d_h=d, w_compact=w, M=M, N=N, H=H, imag_in=K,
         hidden_per_q_head=H // QH, head_dim=HD, n_q_heads=QH, open_sectors=0,
-        p_real=R, imag_bias=ib, trace=trace, trace_w=tw, powlu_m=3.0, act=act, s=s, beta=beta,
-        carry_prev=prev if mode == 1 else None, seed=prev if mode == 2 else None,
+        p_real=R, gate_src=G, imag_bias=ib, trace=trace, trace_w=tw, powlu_m=3.0, act=act, s=s,
+        beta=beta, carry_prev=prev if mode == 1 else None, seed=prev if mode == 2 else None,
         seed_valid=valid if mode == 2 else None, gate_w=gw if gate else None, carry_out=carry,
         p_out=p if gate else None, alpha=0.0375, axis=axis)
     _lib.call("loom_ffn_decode", code(u), ctypes.byref(desc), S(u))
     # oracle, fp32 on the host
     be = ref.beta_space_grouped(host(u)[:, None], host(q)[:, None], host(kc)[:, None],
                                 host(c)[:, None], host(d)[:, None], host(w), QH, HD, "head")
-    wa, ws_, wt = ref.paraplex_pointwise(host(R)[:, None], host(R)[:, None], be, host(ib),
-                                         host(trace0), host(tw), None, 3.0)
+    wa, ws_, wt = ref.paraplex_pointwise(host(R)[:, None], host(G if gsrc else R)[:, None], be,
+                                         host(ib), host(trace0), host(tw), None, 3.0)
     check(act, wa[:, 0], dtype)
     check(s, ws_[:, 0], dtype)
     check(trace, wt, dtype)

@@ -218,3 +218,55 @@ def test_bf16_chunked_prefill_tracks_token_steps():
         print(f"{name}: bf16 token {e_tok:.4f}, bf16 chunked {e_pre:.4f}")
         assert e_pre < max(2 * e_tok, 0.02), (name, e_tok, e_pre)
     assert rel(pre.logits, ref.logits) < 0.08
+
+
+def _variants():
+    z = np.load(os.path.join(GOLD, "variants_decode.npz"))
+    state = {k[3:]: torch.from_numpy(z[k]) for k in z.files if k.startswith("w::")}
+    return z, state, _cfg("tiny_variants")
+
+
+@pytest.mark.parametrize("carry", [False, True])
+@pytest.mark.parametrize("chunked", [False, True])
+def test_variants_engine_matches_reference(carry, chunked):
+    """Every math-changing model variant set at once (independent gate_proj
+    amplitude, fixed-RMS depth q/k/v, the branch RMS cap that Model.step
+    leaves unapplied, final RMSNorm, per-sublayer depth readouts): fp32 logits
+    and greedy ids equal the reference's Model.step, token by token and after
+    the chunked prefill."""
+    from loom_amd.engine import LoomDecoder
+    z, state, cfg = _variants()
+    assert cfg.gate_proj and cfg.depth_qkv_rms and cfg.final_norm
+    assert cfg.residual_rms_cap == 0.05 and cfg.depth_readout == "per-sublayer"
+    sfx = "_carry" if carry else ""
+    prompt = torch.from_numpy(z["prompt" + sfx])
+    P = prompt.shape[1]
+    eng = LoomDecoder(cfg, state, batch=prompt.shape[0], dtype=torch.float32,
+                      carry_token_id=5 if carry else None)
+    ids, logits = eng.generate(prompt, 12, return_logits=True, chunked_prefill=chunked)
+    want = torch.from_numpy(z["logits" + sfx])
+    if chunked:
+        want = want[:, P - 1:]
+    torch.testing.assert_close(logits.cpu(), want, rtol=1e-3, atol=1e-4)
+    assert torch.equal(ids.cpu(), torch.from_numpy(z["greedy" + sfx]))
+
+
+def test_variants_bf16_engine_tracks_fp32_and_graph_equals_eager():
+    from loom_amd.engine import LoomDecoder
+    z, state, cfg = _variants()
+    state = {k: (v.to(torch.bfloat16).float() if v.dim() >= 2 else v) for k, v in state.items()}
+    prompt = torch.from_numpy(z["prompt_carry"])
+    e32 = LoomDecoder(cfg, state, batch=3, dtype=torch.float32, carry_token_id=5)
+    ids32, l32 = e32.generate(prompt, 10, return_logits=True)
+    runs = []
+    for use_graph in (False, True):
+        e16 = LoomDecoder(cfg, state, batch=3, dtype=torch.bfloat16, carry_token_id=5)
+        runs.append(e16.generate(prompt, 10, return_logits=True, use_graph=use_graph))
+    assert torch.equal(runs[0][0], runs[1][0]) and torch.equal(runs[0][1], runs[1][1])
+    e16 = LoomDecoder(cfg, state, batch=3, dtype=torch.bfloat16, carry_token_id=5)
+    seq = torch.cat([prompt.to(ids32.device), ids32], 1)
+    rel = []
+    for pos in range(seq.shape[1] - 1):
+        l16 = e16.step(seq[:, pos], pos).float()
+        rel.append(float((l16 - l32[:, pos]).norm() / l32[:, pos].norm()))
+    assert max(rel) < 0.08, max(rel)

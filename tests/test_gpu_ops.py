@@ -245,6 +245,38 @@ def test_depth_attn_decode_strided_view(dtype, HD):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("HD,S", [(96, 20), (96, 1), (8, 7), (64, 9)])
+def test_depth_attn_fixed_rms(dtype, HD, S):
+    """DepthAttn under depth_attn_qkv_rms (loomformer.py:3397-3407): the entry
+    point reads q, k, v as fixed-RMS rows; against the oracle's fixed_rms
+    applied first, then the plain softmax read (d, weights and lse)."""
+    from loom_amd import _lib
+    from oracle.model import fixed_rms
+    g = gen(HD * 31 + S)
+    BT, QH = 37, 8
+    hk = dev(rnd(g, BT, S, QH, HD, scale=3.0), dtype)
+    hv = dev(rnd(g, BT, S, QH, HD, scale=0.2), dtype)
+    q = dev(rnd(g, QH, HD, scale=0.7), dtype)
+    qt, kt, vt = 0.88 / HD ** 0.5, 0.88, 0.88 * 0.4
+    d = torch.empty(BT, QH, HD, device=DEV, dtype=dtype)
+    w = torch.empty(BT, QH, S, device=DEV, dtype=dtype)
+    lse = torch.empty(BT, QH, device=DEV)
+    _lib.call("loom_depth_attn_forward_rms", _lib.dtype_code(q), _lib.ptr(q), _lib.ptr(hk),
+              _lib.ptr(hv), S * QH * HD, QH * HD, _lib.ptr(d), _lib.ptr(w), _lib.ptr(lse), BT, S,
+              QH, HD, qt, kt, vt, _lib.stream_of(q))
+    qn = fixed_rms(host(q), qt)
+    kn, vn = fixed_rms(host(hk), kt), fixed_rms(host(hv), vt)
+    want_d, want_w, want_lse = ref.depth_attn_softmax(qn, kn[None], vn[None])
+    check(d, want_d[0], dtype)
+    check(w, want_w[0], dtype)
+    check(lse, want_lse[0], torch.float32, rtol=1e-3, atol=1e-3)
+    with pytest.raises(RuntimeError, match="targets must be positive"):
+        _lib.call("loom_depth_attn_forward_rms", _lib.dtype_code(q), _lib.ptr(q), _lib.ptr(hk),
+                  _lib.ptr(hv), S * QH * HD, QH * HD, _lib.ptr(d), None, None, BT, S, QH, HD,
+                  0.0, kt, vt, _lib.stream_of(q))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("BT,S", [(50, 24), (7, 33), (1, 1), (4096, 24)])
 def test_depth_attn_stacked(dtype, BT, S):
     from loom_amd import ops

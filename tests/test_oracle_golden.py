@@ -53,6 +53,7 @@ def tiny_shapes(**kw):
     ("tiny_seed0", None, 0),
     ("nano_seed0", "nano", 0),
     ("nano_chk_seed2", "nano_chk", 2),
+    ("tiny_variants_seed0", "tiny_variants", 0),
 ])
 def test_init_stream_matches_reference(name, cfg, seed):
     with open(os.path.join(GOLD, "init_sha256.json")) as f:
@@ -84,6 +85,64 @@ def test_tiny_decode_matches_reference(carry):
     ids, logits = greedy_decode(m, prompt, 12)
     close(logits, z["logits" + suffix], rtol=1e-4, atol=1e-5)
     assert torch.equal(ids, T(z["greedy" + suffix]))
+
+
+def _variants_model(z, carry_token_id=None, **flags):
+    S = cfg_shapes("tiny_variants", carry_token_id=carry_token_id, **flags)
+    m = OracleModel(S).eval()
+    sd = {k[3:]: torch.from_numpy(z[k]) for k in z.files if k.startswith("w::")}
+    m.load_state_dict(sd, strict=True)
+    return m
+
+
+@pytest.mark.parametrize("carry", [False, True])
+def test_variants_decode_matches_reference(carry):
+    """Every math-changing variant flag set (independent gate_proj amplitude,
+    fixed-RMS depth q/k/v, branch RMS cap, final RMSNorm, per-sublayer depth
+    readouts): per-step logits and greedy ids of Model.step."""
+    z = np.load(os.path.join(GOLD, "variants_decode.npz"))
+    sfx = "_carry" if carry else ""
+    m = _variants_model(z, 5 if carry else None)
+    ids, logits = greedy_decode(m, T(z["prompt" + sfx]), 12)
+    close(logits, z["logits" + sfx], rtol=1e-4, atol=1e-5)
+    assert torch.equal(ids, T(z["greedy" + sfx]))
+
+
+def test_variants_fixture_sees_every_flag():
+    """The fixture pins each flag: restating any one of them differently
+    (dropped, or for the branch cap applied inside Model.step, which never
+    applies it) moves the logits far outside the tolerance."""
+    z = np.load(os.path.join(GOLD, "variants_decode.npz"))
+    prompt = T(z["prompt"])[:, :10]
+    want = T(z["logits"])[:, :10]
+    ref_m = _variants_model(z)
+    _, base = greedy_decode(ref_m, prompt, 1)
+    close(base[:, :10], want, rtol=1e-4, atol=1e-5)
+    m = _variants_model(z)
+    m.S = Shapes(**{**m.S.__dict__, "qkv_rms": False})
+    _, got = greedy_decode(m, prompt, 1)
+    assert float((got[:, :10] - want).abs().max()) > 1e-2
+    m = _variants_model(z)
+    m.ln_final = None
+    _, got = greedy_decode(m, prompt, 1)
+    assert float((got[:, :10] - want).abs().max()) > 1e-2
+    # gate_proj off: amplitude from p_real again
+    m = _variants_model(z)
+    for blk in m.blocks:
+        blk.ffn.gate_proj = None
+    _, got = greedy_decode(m, prompt, 1)
+    assert float((got[:, :10] - want).abs().max()) > 1e-2
+    # per-sublayer readouts replaced by one shared readout (sublayer 0's)
+    m = _variants_model(z)
+    w0 = m.depth_attn.w_o_weight.data[0].clone()
+    m.depth_attn.w_o_weight.data[:] = w0
+    _, got = greedy_decode(m, prompt, 1)
+    assert float((got[:, :10] - want).abs().max()) > 1e-2
+    # the branch cap applied where _block_core applies it (loomformer.py:3568-3570,
+    # :3627-3629): Model.step does not, and the fixture shows it
+    ref_m.step_branch_cap = 0.05
+    _, got = greedy_decode(ref_m, prompt, 1)
+    assert float((got[:, :10] - want).abs().max()) > 1e-2
 
 
 def test_nano_cpu_reference_greedy_ids():
@@ -246,7 +305,8 @@ def test_rope_and_attention_step():
 
 # ---------------------------------------------------------------- product-side init
 
-@pytest.mark.parametrize("name,cfg,seed", [("nano_chk_seed2", "nano_chk", 2), ("tiny_seed0", "tiny", 0)])
+@pytest.mark.parametrize("name,cfg,seed", [("nano_chk_seed2", "nano_chk", 2), ("tiny_seed0", "tiny", 0),
+                                           ("tiny_variants_seed0", "tiny_variants", 0)])
 def test_engine_init_stream_matches_reference(name, cfg, seed):
     """loom_amd.weights (the engine's seeded init) against the reference's sha256."""
     from loom_amd.config import ModelConfig
@@ -255,8 +315,12 @@ def test_engine_init_stream_matches_reference(name, cfg, seed):
         want = json.load(f)[name]
     with open(os.path.join(GOLD, "configs.json")) as f:
         d = json.load(f)[cfg]
-    sd = init_state_dict(ModelConfig.from_dict(d), seed)
+    mc = ModelConfig.from_dict(d)
+    sd = init_state_dict(mc, seed)
     assert set(sd) == set(want)
+    # the key set the checkpoint loader holds a state dict to (its strict load)
+    from loom_amd.weights import state_keys
+    assert sorted(state_keys(mc)) == sorted(want)
     bad = [k for k, v in sd.items() if _sha(v) != want[k]["sha256"]]
     assert not bad, f"init differs for {bad[:5]}"
 
