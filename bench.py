@@ -21,9 +21,12 @@ HBM-bound kernel): algorithmic bytes (R, beta in; I, O out = 8 B/elem in
 bf16) per launch over its mean launch time, against 8 TB/s.
 
 ``cpu_baseline`` is the CPU oracle (fp32 PyTorch restatement of the
-reference's unfused path) decoding on the host cores on a bounded sample;
-``cpu_micro`` times the same oracle on PX and DA at full size and on a slice
-of TR scaled to its full size.
+reference's unfused path) running the e2e decode step on all host cores on a
+bounded sample (B=32 from position 2048 on a synthetic state of that size);
+``cpu_reference_config`` times BASELINE's CPU-reference config (nano.yaml,
+B=1, 128 + 64 tokens, fp32) on the host cores and on the fp32 GPU engine;
+``cpu_micro`` times the oracle on PX and DA at full size and on a slice of TR
+scaled to its full size.  CPU figures are 1 warm-up plus the median of 3.
 
 Prints ONE JSON line.  One GPU only: --gpus above 1 exits with a message.
 """
@@ -151,8 +154,27 @@ def bench_px(iters):
     res = {}
     res["w_real_ms"] = timed(lambda: ops.linear(u, w_real, b_real, out=R), iters)
     res["w_imag_ms"] = timed(lambda: ops.beta_forward_cuda(u, q, kc, c, d, w_imag, H // QH, HD, QH, False), iters)
-    res["pointwise_ms"] = timed(lambda: ops.paraplex_forward(R, R, beta, imag_bias, trace, trace_w,
-                                                              empty_reset, anchor, 1, False, 0.99, 3.0), iters)
+    # the pointwise chain on one set of R / beta / I / O (201 MB, inside the 256 MB
+    # Infinity Cache: the cache-warm figure) and rotating over three sets (604 MB:
+    # every launch streams its operands from HBM, the figure the roofline uses)
+    res["pointwise_warm_ms"] = timed(lambda: ops.paraplex_forward(R, R, beta, imag_bias, trace, trace_w,
+                                                                   empty_reset, anchor, 1, False, 0.99, 3.0), iters)
+    from loom_amd import _lib
+    sets = [(R, beta)] + [(R.clone(), beta.clone()) for _ in range(2)]
+    outs = [(torch.empty_like(R), torch.empty_like(R)) for _ in sets]
+    nt = torch.empty(B, H, device=dev, dtype=bf)
+    snap = torch.empty((), device=dev)
+    rot = [0]
+
+    def pointwise_rotated():
+        k = rot[0] % len(sets)
+        rot[0] += 1
+        (r_, b_), (a_, s_) = sets[k], outs[k]
+        _lib.call("loom_paraplex_forward", 1, _lib.ptr(r_), _lib.ptr(r_), _lib.ptr(b_), _lib.ptr(imag_bias),
+                  _lib.ptr(trace), _lib.ptr(trace_w), None, _lib.ptr(anchor), _lib.ptr(a_), _lib.ptr(s_),
+                  _lib.ptr(nt), _lib.ptr(snap), B, T, H, 3.0, _lib.stream_of(r_))
+    res["pointwise_ms"] = timed(pointwise_rotated, max(iters, 3 * 8))
+    del sets, outs
     out = torch.empty(B, T, N, device=dev, dtype=bf)
     res["w2_ms"] = timed(lambda: ops.linear(act, w2, b2, out=out), iters)
 
@@ -166,6 +188,7 @@ def bench_px(iters):
     elems = M * H
     res["pointwise_bytes"] = elems * 8            # R, beta in; I, O out (bf16)
     res["pointwise_GBs"] = res["pointwise_bytes"] / (res["pointwise_ms"] * 1e-3) / 1e9
+    res["pointwise_warm_GBs"] = res["pointwise_bytes"] / (res["pointwise_warm_ms"] * 1e-3) / 1e9
     fl = {"w_real": 2 * M * N * H, "w_imag": 2 * M * K_imag * H, "w2": 2 * M * H * N}
     for k, v in fl.items():
         res[f"{k}_TFLOPs"] = v / (res[f"{k}_ms"] * 1e-3) / 1e12
@@ -199,10 +222,19 @@ def bench_tr(iters):
     prev = torch.randn(B, T, H, 3, 3, generator=g, device=dev)
     prev /= prev.square().mean(dim=(-1, -2), keepdim=True).add(1e-6).sqrt()
     w = torch.full((9,), 1.0 / 9.0, device=dev)
-    ms = timed(lambda: ops.tria_step_gate_forward(r, i, o, prev, w, 0.025, 1), iters)
+    # the reference API (carry, p and the backward-only scale: 92 B per element)
+    ms92 = timed(lambda: ops.tria_step_gate_forward(r, i, o, prev, w, 0.025, 1), iters)
+    # the inference form tria_step_and_gate uses (no scale output): 88 B per element
+    from loom_amd import _lib
+    carry = torch.empty(B, T, H, 3, 3, device=dev)
+    p = torch.empty(B, T, H, device=dev)
+    P = _lib.ptr
+    ms = timed(lambda: _lib.call("loom_tria_depth_forward", 0, P(r), P(i), P(o), P(prev), None, None,
+                                 P(w), P(carry), P(p), None, B, T, H, 0.025, 1, _lib.stream_of(r)),
+               iters)
     n = B * T * H
-    nbytes = n * (12 + 36 + 36 + 4 + 4)          # r,i,o; C_prev; C; p; scale (fp32)
-    del prev
+    nbytes = n * (12 + 36 + 36 + 4)               # r,i,o; C_prev; C; p (fp32)
+    del prev, carry, p
     depth = torch.randn(B, 64, H, 3, 3, generator=g, device=dev)
     reset = torch.zeros(B, 64, dtype=torch.bool, device=dev)
     empty = torch.empty(0, device=dev)
@@ -210,6 +242,8 @@ def bench_tr(iters):
                                                                torch.empty(0, dtype=torch.bool, device=dev)), iters)
     end_bytes = depth.numel() * 4 + B * H * 9 * 8
     return dict(step_gate_ms=ms, step_gate_bytes=nbytes, step_gate_GBs=nbytes / (ms * 1e-3) / 1e9,
+                step_gate_with_scale_ms=ms92,
+                step_gate_with_scale_GBs=n * 92 / (ms92 * 1e-3) / 1e9,
                 endpoint_w64_ms=ms_end, endpoint_w64_GBs=end_bytes / (ms_end * 1e-3) / 1e9)
 
 
@@ -326,35 +360,154 @@ def measured_traffic():
 
 # ----------------------------------------------------------------------------- cpu
 
-def cpu_baseline(args):
+def _host_cores() -> int:
+    return len(os.sched_getaffinity(0))
+
+
+def _synthetic_state(model, B: int, ctx: int, big):
+    """A decode state of the oracle at position `ctx`: KV caches of `ctx`
+    positions, phase traces, a Tria document state and ctx // W final-CA keys,
+    holding the seeded values of `big` (reused between timed runs; a step only
+    appends rows past `ctx`).  The per-step cost of the fp32 step depends on
+    the context only through these shapes."""
     import torch
-    from oracle.model import OracleModel, Shapes, greedy_decode  # the checker, timed as baseline
+    from oracle.model import CACache, LayerCache, StepState, TemporalState
+    S = model.S
+    caches = [LayerCache(k=big["k"][l], v=big["v"][l], phase_trace=big["trace"][l].clone(),
+                         cache_len=ctx) for l in range(S.L)]
+    ca = CACache(k=big["ca_k"], v=big["ca_v"], valid=torch.ones(B, big["ca_k"].shape[1], dtype=torch.bool),
+                 cache_len=ctx // S.window)
+    temporal = TemporalState(carry=big["doc"].clone(), pending=torch.zeros(B, dtype=torch.bool))
+    return StepState(caches=caches, ca=ca, temporal=temporal)
+
+
+def _synthetic_tensors(S, B: int, cap: int, seed: int):
+    """Seeded cache contents for `cap` positions (the timed steps append below cap)."""
+    import torch
+    from oracle import ops as ref
+    g = torch.Generator().manual_seed(seed)
+    rn = lambda *shape: torch.randn(*shape, generator=g)
+    return {"k": [rn(B, cap, S.KVH, S.HD) for _ in range(S.L)],
+            "v": [rn(B, cap, S.KVH, S.HD) for _ in range(S.L)],
+            "trace": [rn(B, S.H).tanh() for _ in range(S.L)],
+            "ca_k": rn(B, cap // S.window + 2, S.N), "ca_v": rn(B, cap // S.window + 2, S.N),
+            "doc": ref.local_normalize(rn(B, S.H, 3, 3))}
+
+
+def cpu_baseline(args):
+    """The e2e workload's decode step on the host cores: the fp32 oracle
+    Model.step at B = 32 from position 2048 (the GPU's decode starts there),
+    on a synthetic decode state of that size; 1 warm-up step, then the median
+    of 3 timed runs of `cpu_steps` greedy steps."""
+    import torch
+    from oracle.model import OracleModel, Shapes  # the checker, timed as baseline
     from loom_amd.config import NANO_CHK
 
-    cores = min(16, len(os.sched_getaffinity(0)))
+    cores = _host_cores()
     torch.set_num_threads(cores)
     S = Shapes.from_dict(dict(NANO_CHK, seq_len=4096))
     torch.manual_seed(2)
     model = OracleModel(S).eval()
-    B, P, K = args.batch, args.cpu_prompt, args.cpu_steps
+    B, ctx, K = args.batch, args.prompt, args.cpu_steps
     g = torch.Generator().manual_seed(2)
-    prompt = torch.randint(0, S.V, (B, P), generator=g)
-    state = None
-    logits = None
+    ids = torch.randint(0, S.V, (B,), generator=g)
+    times = []
+    big = _synthetic_tensors(S, B, ctx + K + 1, 5)
     with torch.no_grad():
-        for pos in range(P):
-            logits, state = model.step(prompt[:, pos], pos, state)
+        for rep in range(4):                         # run 0 is the warm-up
+            state = _synthetic_state(model, B, ctx, big)
+            nxt = ids
+            t0 = time.perf_counter()
+            for i in range(K if rep else 1):
+                logits, state = model.step(nxt, ctx + i, state)
+                nxt = torch.argmax(logits, dim=-1)
+            if rep:
+                times.append(time.perf_counter() - t0)
+    dt = sorted(times)[1]
+    return dict(value=B * K / dt, unit="tokens/s", cores=cores, kind="port", cpu=_cpu_model(),
+                sample=f"fp32 oracle Model.step (the reference's unfused path restated), nano_chk shape "
+                       f"seed 2, B={B}, {K} greedy steps from position {ctx} on a synthetic decode "
+                       f"state of that size; 1 warm-up step, median of 3 runs")
+
+
+def cpu_reference_config(args):
+    """BASELINE's CPU-reference config: cfg/nano.yaml weights from seed 0,
+    fp32, B = 1, a 128-token prompt (ids from a generator seeded 0), 128
+    prefill steps and 64 greedy steps (Model.step each, as infer runs them).
+    Timed with the fp32 oracle on the host cores (1 warm-up, median of 3)
+    and with the fp32 GPU engine (token-by-token prefill through the
+    captured step); the greedy ids of the two are compared."""
+    import torch
+    from oracle.model import OracleModel, Shapes  # the checker, timed as baseline
+    from loom_amd.config import NANO, ModelConfig
+    from loom_amd.engine import LoomDecoder
+    from loom_amd.weights import init_state_dict
+
+    cores = _host_cores()
+    torch.set_num_threads(cores)
+    P, K = 128, 64
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, NANO["vocab"], (1, P), generator=g)
+    torch.manual_seed(0)
+    model = OracleModel(Shapes.from_dict(NANO)).eval()
+
+    def cpu_run():
+        state, logits, out = None, None, []
         t0 = time.perf_counter()
-        for i in range(K):
-            nxt = torch.argmax(logits, dim=-1)
-            logits, state = model.step(nxt, P + i, state)
-        dt = time.perf_counter() - t0
-    return dict(value=B * K / dt, unit="tokens/s", cores=cores, kind="port",
-                sample=f"fp32 oracle Model.step, nano_chk shape seed 2, B={B}, prompt {P} tokens "
-                       f"(untimed), {K} timed greedy steps (context {P}-{P + K}, vs 2048-2304 on GPU)")
+        with torch.no_grad():
+            for pos in range(P):
+                logits, state = model.step(prompt[:, pos], pos, state)
+            t1 = time.perf_counter()
+            for i in range(K):
+                nxt = torch.argmax(logits, dim=-1)
+                out.append(nxt)
+                logits, state = model.step(nxt, P + i, state)
+        t2 = time.perf_counter()
+        return t1 - t0, t2 - t1, torch.stack(out, 1)
+    runs = [cpu_run() for _ in range(4)][1:]
+    pre_s = sorted(r[0] for r in runs)[1]
+    dec_s = sorted(r[1] for r in runs)[1]
+    ids_cpu = runs[0][2]
+
+    cfg = ModelConfig.from_dict(NANO)
+    eng = LoomDecoder(cfg, init_state_dict(cfg, 0), batch=1, dtype=torch.float32, max_len=P + K + 1)
+    gpu = []
+    for rep in range(4):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        eng.start(prompt)
+        eng.replay_steps(P - 1)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        eng.replay_steps(K)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        if rep == 0:
+            eng.warm_graphs()
+        else:
+            gpu.append((t1 - t0, t2 - t1))
+    gpre = sorted(x[0] for x in gpu)[1]
+    gdec = sorted(x[1] for x in gpu)[1]
+    ids_gpu = eng.generated()[:, :K].cpu()
+    return {"config": "cfg/nano.yaml seed 0, fp32, B=1, 128-token prompt + 64 greedy tokens",
+            "cpu": {"prefill_tokens_per_s": P / pre_s, "decode_tokens_per_s": K / dec_s,
+                    "cores": cores, "kind": "port", "cpu": _cpu_model()},
+            "gpu_fp32": {"prefill_tokens_per_s": P / gpre, "decode_tokens_per_s": K / gdec,
+                         "note": "token-by-token prefill through the captured step, host wall clock"},
+            "greedy_ids_equal": bool(torch.equal(ids_cpu, ids_gpu))}
 
 
 def _cpu_model() -> str:
+    """The host CPU's model string (lscpu's, which names the part where
+    /proc/cpuinfo may give only the family)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -383,7 +536,7 @@ def cpu_micro():
     import torch
     from oracle import ops as ref  # the checker, timed as baseline
 
-    cores = min(16, len(os.sched_getaffinity(0)))
+    cores = _host_cores()
     torch.set_num_threads(cores)
     out = {"cores": cores, "cpu": _cpu_model(), "kind": "port"}
     with torch.no_grad():
@@ -436,8 +589,8 @@ def main():
     ap.add_argument("--no-e2e", action="store_true",
                     help="microbenchmarks only (for counter passes); value is then null")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-prompt", type=int, default=32)
-    ap.add_argument("--cpu-steps", type=int, default=8)
+    ap.add_argument("--cpu-steps", type=int, default=4,
+                    help="greedy steps per timed CPU run of the e2e decode sample")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -472,10 +625,18 @@ def main():
         copy_gbs = copy_bandwidth()
         kernels = {
             "paraplex_pointwise": {"ms": px["pointwise_ms"], "GB/s": px["pointwise_GBs"],
-                                   "frac": px["pointwise_GBs"] / HBM_PEAK_GBS},
+                                   "frac": px["pointwise_GBs"] / HBM_PEAK_GBS,
+                                   "note": "rotating over 3 operand sets (604 MB, beyond the 256 MB "
+                                           "Infinity Cache)",
+                                   "cache_warm_ms": px["pointwise_warm_ms"],
+                                   "cache_warm_GB/s": px["pointwise_warm_GBs"]},
             "depth_attn": {"ms": da["ms"], "GB/s": da["GBs"], "frac": da["GBs"] / HBM_PEAK_GBS},
             "tria_step_gate": {"ms": tr["step_gate_ms"], "GB/s": tr["step_gate_GBs"],
-                               "frac": tr["step_gate_GBs"] / HBM_PEAK_GBS},
+                               "frac": tr["step_gate_GBs"] / HBM_PEAK_GBS,
+                               "basis": "88 B per element (r,i,o; C_prev; C; p), the inference form "
+                                        "without the backward-only scale",
+                               "with_scale_ms": tr["step_gate_with_scale_ms"],
+                               "with_scale_GB/s_92B": tr["step_gate_with_scale_GBs"]},
             "temporal_endpoint_w64": {"ms": tr["endpoint_w64_ms"], "GB/s": tr["endpoint_w64_GBs"]},
             "tria_chunked_tr": {"ms": trp["ms"], "GB/s": trp["GBs"], "frac": trp["GBs"] / HBM_PEAK_GBS,
                                 "algorithmic_bytes": trp["bytes"], "readout_ms": trp["readout_ms"]},
@@ -501,13 +662,21 @@ def main():
                     "achieved": px["pointwise_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": px["pointwise_GBs"] / HBM_PEAK_GBS,
                     "traffic": traffic.get("paraplex_chunk_kernel_px"),
-                    "algorithmic_bytes": px["pointwise_bytes"]}
+                    "traffic_source": "profiles/hbm_traffic.json (rocprofv3 FETCH_SIZE and WRITE_SIZE "
+                                      "passes, committed; not measured in this run)",
+                    "algorithmic_bytes": px["pointwise_bytes"],
+                    "timing": "HIP events over a replayed graph of launches rotating over 3 operand sets",
+                    "cache_warm_GB/s": px["pointwise_warm_GBs"]}
     cpu = None
     cpu_mi = None
+    cpu_ref = None
     if not args.no_cpu:
         log("CPU baseline (oracle on host cores)")
         cpu = cpu_baseline(args)
         log(f"CPU: {cpu['value']:.2f} tok/s on {cpu['cores']} cores")
+        log("CPU-reference config (nano.yaml, B=1, fp32) on host cores and on the GPU engine")
+        cpu_ref = cpu_reference_config(args)
+        log(f"CPU-reference config: {json.dumps(cpu_ref)}")
         if not args.no_micro:
             log("CPU microbenchmarks (oracle on host cores)")
             cpu_mi = cpu_micro()
@@ -522,6 +691,7 @@ def main():
                                f"{args.warmup} untimed then {args.steps} timed greedy steps",
                    "batch": args.batch, "prompt": args.prompt, "decode_steps": args.steps},
         "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels, "cpu_micro": cpu_mi,
+        "cpu_reference_config": cpu_ref,
         "prefill_tokens_per_s": dec["prefill_tokens_per_s"],
     }
     print(json.dumps(line), flush=True)
