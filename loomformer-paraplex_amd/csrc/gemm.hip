@@ -202,6 +202,303 @@ gemm_bf16_mfma_kernel(GemmArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ big bf16 (M >= 256)
+// Block tile 256 (m) x 128 (n) x 64 (k), eight waves (two per SIMD, so one
+// wave's MFMAs cover the other's LDS waits) in a 4 (m) x 2 (n) grid, each
+// owning 64 x 64 as 4 x 4 MFMA tiles (v_mfma_f32_16x16x32_bf16).  Operand
+// tiles travel from global memory straight into LDS (buffer_load_dwordx4 ...
+// lds, no register staging) through three stages, each its own LDS array so
+// the compiler's waits name exactly the stage they need: k-tile t+2 is
+// requested while t is computed.
+//
+// LDS layout of a stage: [k-half h][row][4 chunks of 8 k] (64 B rows), chunk c
+// of row r stored at position c ^ ((r >> 2) & 3), so the 16-row fragment
+// reads spread over the banks.  One DMA instruction of a wave fills 16 rows of
+// one k-half (lane l: row l/4, position l%4; the lane fetches the chunk the
+// swizzle puts there), so its 32 k lie in one gather sector and the source
+// and column offset are uniform (scalar) per instruction; per lane only a
+// 32-bit row offset per 16-row group is held, and the k advance is the
+// scalar soffset.  Requires K % 192 == 0 (whole rounds of the three stages);
+// 144 KB of LDS, one block per CU.
+constexpr int BG_M = 256, BG_N = 128, BG_K = 64;
+constexpr int BG_WAVES = 8, BG_WGM = 4;                    // waves along m; BG_WAVES / BG_WGM along n
+constexpr int BG_WTM = BG_M / BG_WGM, BG_WTN = BG_N / (BG_WAVES / BG_WGM);   // 64 x 64 per wave
+constexpr int BG_FJ = BG_WTM / 16, BG_FI = BG_WTN / 16;    // x and w fragments per k-step
+constexpr int BG_XG = BG_M / 16 / BG_WAVES, BG_WG = BG_N / 16 / BG_WAVES;   // DMA row groups per wave
+constexpr int BG_DMA = 2 * (BG_XG + BG_WG);                // DMA instructions per lane per stage
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// 16 bytes per lane from a raw buffer straight into LDS (lane l lands at lds + 16*l)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const uint16_t* lds, uint32_t voff,
+                                      uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
+}
+
+// Source and element offset (within the source's row) of the 32 packed
+// columns [kk, kk + 32) of group g in gather mode; they lie in one sector.
+__device__ __forceinline__ void gather_half(const GemmArgs& a, int64_t kk, int64_t g,
+                                            const void*& src, int64_t& col) {
+    const int64_t HD = a.HD, Nm = a.Nm;
+    if (!a.open) {                                   // [Q_g | Kctx_g | C_g | U | D_g]
+        if (kk < HD) { src = a.src[0]; col = g * HD + kk; }
+        else if (kk < 2 * HD) { src = a.src[1]; col = g * HD + kk - HD; }
+        else if (kk < 3 * HD) { src = a.src[2]; col = g * HD + kk - 2 * HD; }
+        else if (kk < 3 * HD + Nm) { src = a.src[3]; col = kk - 3 * HD; }
+        else { src = a.src[4]; col = g * HD + kk - 3 * HD - Nm; }
+    } else {                                         // [Q_g | Kctx | C | U | D]
+        if (kk < HD) { src = a.src[0]; col = g * HD + kk; }
+        else if (kk < HD + Nm) { src = a.src[1]; col = kk - HD; }
+        else if (kk < HD + 2 * Nm) { src = a.src[2]; col = kk - HD - Nm; }
+        else if (kk < HD + 3 * Nm) { src = a.src[3]; col = kk - HD - 2 * Nm; }
+        else { src = a.src[4]; col = kk - HD - 3 * Nm; }
+    }
+}
+
+template <bool GATHER>
+__global__ void __launch_bounds__(64 * BG_WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm_bf16_big_kernel(GemmArgs a) {
+    constexpr int XH = BG_M * 32, WH = BG_N * 32;   // elements per k-half of a stage
+    __shared__ __attribute__((aligned(16))) uint16_t X0[2 * XH], X1[2 * XH], X2[2 * XH];
+    __shared__ __attribute__((aligned(16))) uint16_t W0[2 * WH], W1[2 * WH], W2[2 * WH];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave % BG_WGM, wn = wave / BG_WGM;
+    // Tile of this block.  Blocks are dispatched round-robin over the 8 XCDs
+    // (block b runs on XCD b % 8), each with its own L2: when the m-tiles
+    // split evenly, XCD x takes m-tiles [x*MT/8, (x+1)*MT/8) and walks the
+    // n-tiles with its m-tiles innermost, so the tiles resident on one XCD at
+    // a time share their X rows and a few W column blocks in its L2.
+    const int64_t MT = ceil_div(a.M, BG_M), NT = ceil_div(a.N, BG_N);
+    const int64_t b = blockIdx.x;
+    int64_t mt, nt;
+    if (MT % 8 == 0) {
+        const int64_t mpx = MT / 8, li = b / 8;
+        mt = (b % 8) * mpx + li % mpx;
+        nt = li / mpx;
+    } else {
+        mt = b / NT;
+        nt = b % NT;
+    }
+    const int64_t n0 = nt * BG_N;
+    const int64_t m0 = mt * BG_M;
+    const int64_t g = GATHER ? n0 / a.Hq : 0;
+    const int64_t ldx = GATHER ? a.Nm : a.ldx;
+
+    // DMA slots: X 16-row groups BG_XG*wave + q, W groups BG_WG*wave + q, each
+    // for both k-halves; lane: row 16*group + lane/4, chunk (lane%4) ^
+    // ((row >> 2) & 3); rows past M / N read the last row (their results are
+    // not stored)
+    uint32_t xv[BG_XG], wv[BG_WG];
+#pragma unroll
+    for (int q = 0; q < BG_XG; ++q) {
+        const int r = 16 * (BG_XG * wave + q) + (lane >> 2);
+        const int64_t rr = m0 + r < a.M ? r : a.M - 1 - m0;
+        xv[q] = (uint32_t)((rr * ldx + 8 * ((lane & 3) ^ ((r >> 2) & 3))) * 2);
+    }
+#pragma unroll
+    for (int q = 0; q < BG_WG; ++q) {
+        const int r = 16 * (BG_WG * wave + q) + (lane >> 2);
+        const int64_t rr = n0 + r < a.N ? r : a.N - 1 - n0;
+        wv[q] = (uint32_t)((rr * a.ldw + 8 * ((lane & 3) ^ ((r >> 2) & 3))) * 2);
+    }
+    const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint16_t*)a.W + n0 * a.ldw),
+                                                      (short)0, 0x7fffffff, kBufferDword3);
+    const auto rx = __builtin_amdgcn_make_buffer_rsrc(
+        GATHER ? (void*)nullptr : (void*)((const uint16_t*)a.X + m0 * a.ldx), (short)0, 0x7fffffff,
+        kBufferDword3);
+    auto issue = [&](int64_t k0, uint16_t* Xs, uint16_t* Ws) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            auto rxh = rx;
+            uint32_t sx = (uint32_t)((k0 + 32 * h) * 2);
+            if constexpr (GATHER) {
+                const void* src;
+                int64_t col;
+                gather_half(a, k0 + 32 * h, g, src, col);
+                rxh = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint16_t*)src + m0 * a.Nm),
+                                                        (short)0, 0x7fffffff, kBufferDword3);
+                sx = (uint32_t)(col * 2);
+            }
+#pragma unroll
+            for (int q = 0; q < BG_XG; ++q)
+                dma16(rxh, Xs + h * XH + 16 * (BG_XG * wave + q) * 32, xv[q], sx);
+#pragma unroll
+            for (int q = 0; q < BG_WG; ++q)
+                dma16(rw, Ws + h * WH + 16 * (BG_WG * wave + q) * 32, wv[q],
+                      (uint32_t)((k0 + 32 * h) * 2));
+        }
+    };
+
+    f32x4 acc[BG_FI][BG_FJ];
+#pragma unroll
+    for (int i = 0; i < BG_FI; ++i)
+#pragma unroll
+        for (int j = 0; j < BG_FJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // fragment of k-step kk: row base + 16*i + fr of half kk, chunk fc at its
+    // swizzled position ((row >> 2) & 3 = (fr >> 2) & 3 for every tile)
+    const int fr = lane & 15, fc = lane >> 4;
+    const int lo = fr * 32 + ((fc ^ ((fr >> 2) & 3)) << 3);
+    struct Frags {
+        bf16x8 w[BG_FI], x[BG_FJ];
+    };
+    auto read = [&](Frags& f, const uint16_t* Xs, const uint16_t* Ws, int kk) {
+#pragma unroll
+        for (int i = 0; i < BG_FI; ++i)
+            f.w[i] = *reinterpret_cast<const bf16x8*>(&Ws[kk * WH + (wn * BG_WTN + i * 16) * 32 + lo]);
+#pragma unroll
+        for (int j = 0; j < BG_FJ; ++j)
+            f.x[j] = *reinterpret_cast<const bf16x8*>(&Xs[kk * XH + (wm * BG_WTM + j * 16) * 32 + lo]);
+    };
+    auto mma = [&](const Frags& f) {
+#pragma unroll
+        for (int i = 0; i < BG_FI; ++i)
+#pragma unroll
+            for (int j = 0; j < BG_FJ; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.w[i], f.x[j], acc[i][j], 0, 0, 0);
+    };
+    constexpr int NR = BG_FI + BG_FJ;        // fragment reads per k-step
+    constexpr int NM = BG_FI * BG_FJ;        // MFMAs per k-step
+
+    // Tile t lives in stage t % 3, requested two tiles ahead (nk = K / 64 is a
+    // multiple of 3).  Iteration t, with k-step 0 of t already in registers
+    // (f0): read k-step 1 of t; MFMAs of k-step 0; wait for tile t+1's DMA and
+    // every wave's reads of t (barrier); request tile t+3 into t's stage; read
+    // k-step 0 of t+1; MFMAs of k-step 1.  Straight-line code per stage, so
+    // every wait is a constant.
+    const int64_t nk = a.K / BG_K;
+    issue(0, X0, W0);
+    issue(BG_K, X1, W1);
+    issue(2 * BG_K, X2, W2);
+    wait_vmcnt<2 * BG_DMA>();
+    __builtin_amdgcn_s_barrier();
+    Frags f0, f1;
+    read(f0, X0, W0, 0);
+    // NEXT: tile t+1 exists; MORE: tile t+2 exists; ISSUE: tile t+3 exists
+    auto iter = [&](auto next_, auto more_, auto issue_, int64_t t, uint16_t* Xc, uint16_t* Wc,
+                    const uint16_t* Xn, const uint16_t* Wn) {
+        constexpr bool NEXT = decltype(next_)::value, MORE = decltype(more_)::value,
+                       ISSUE = decltype(issue_)::value;
+        // the fragment reads of the next k-step interleaved with the MFMAs of
+        // this one (one 16-byte LDS read per two MFMAs), likewise the DMA requests
+        read(f1, Xc, Wc, 1);
+        mma(f0);
+#pragma unroll
+        for (int q = 0; q < NR; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // DS read
+            __builtin_amdgcn_sched_group_barrier(0x0008, NM / NR, 0);   // MFMA
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (NEXT) {
+            if constexpr (MORE) wait_vmcnt<BG_DMA>(); else wait_vmcnt<0>();
+            __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0): this wave's reads of t landed
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (ISSUE) issue((t + 3) * BG_K, Xc, Wc);
+            read(f0, Xn, Wn, 0);
+        }
+        mma(f1);
+        if constexpr (NEXT) {
+#pragma unroll
+            for (int q = 0; q < NR; ++q) {
+                if constexpr (ISSUE)
+                    if (q < BG_DMA) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 1);   // VMEM read
+                __builtin_amdgcn_sched_group_barrier(0x0100, 1, 1);   // DS read
+                __builtin_amdgcn_sched_group_barrier(0x0008, NM / NR, 1);   // MFMA
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    for (int64_t t = 0; t < nk - 3; t += 3) {
+        iter(T_{}, T_{}, T_{}, t, X0, W0, X1, W1);
+        iter(T_{}, T_{}, T_{}, t + 1, X1, W1, X2, W2);
+        iter(T_{}, T_{}, T_{}, t + 2, X2, W2, X0, W0);
+    }
+    iter(T_{}, T_{}, F_{}, nk - 3, X0, W0, X1, W1);
+    iter(T_{}, F_{}, F_{}, nk - 2, X1, W1, X2, W2);
+    iter(F_{}, F_{}, F_{}, nk - 1, X2, W2, X0, W0);
+
+    // epilogue: lane holds n = nb + 0..3 of row m for each (i, j).  Whole
+    // tiles take straight-line code with 8-byte stores (one variant per
+    // gate / residual combination, chosen once per block); edge tiles check
+    // every element.
+    uint16_t* out = (uint16_t*)a.out;
+    const uint16_t* gp = (const uint16_t*)a.gate_p;
+    const uint16_t* rs = (const uint16_t*)a.residual;
+    const int64_t ldc = a.ldc;
+    const int64_t mrow = m0 + wm * BG_WTM + (lane & 15);
+    const int64_t ncol = n0 + wn * BG_WTN + (lane >> 4) * 4;
+    const bool whole = m0 + BG_M <= a.M && n0 + BG_N <= a.N && (ldc & 3) == 0 &&
+                       (((uintptr_t)out | (uintptr_t)gp | (uintptr_t)rs) & 7) == 0 &&
+                       ((uintptr_t)a.bias & 15) == 0;
+    auto bf4 = [](uint2 w, float (&x)[4]) {
+        x[0] = __uint_as_float(w.x << 16); x[1] = __uint_as_float(w.x & 0xffff0000u);
+        x[2] = __uint_as_float(w.y << 16); x[3] = __uint_as_float(w.y & 0xffff0000u);
+    };
+    auto whole_tile = [&](auto gate_, auto res_) {
+        constexpr bool GATE = decltype(gate_)::value, RES = decltype(res_)::value;
+#pragma unroll
+        for (int i = 0; i < BG_FI; ++i) {
+            const int64_t nb = ncol + i * 16;
+            float bias4[4] = {0.f, 0.f, 0.f, 0.f};
+            if (a.bias != nullptr) {
+                const float4 bv = *reinterpret_cast<const float4*>(a.bias + nb);
+                bias4[0] = bv.x; bias4[1] = bv.y; bias4[2] = bv.z; bias4[3] = bv.w;
+            }
+#pragma unroll
+            for (int j = 0; j < BG_FJ; ++j) {
+                const int64_t e = (mrow + j * 16) * ldc + nb;
+                float v[4], gv[4], rv[4];
+                if constexpr (GATE) bf4(*reinterpret_cast<const uint2*>(gp + e), gv);
+                if constexpr (RES) bf4(*reinterpret_cast<const uint2*>(rs + e), rv);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    v[r] = acc[i][j][r];
+                    if constexpr (GATE) v[r] *= 1.0f + a.gate_alpha * gv[r];
+                    v[r] += bias4[r];
+                    if constexpr (RES) v[r] += rv[r];
+                }
+                *reinterpret_cast<uint2*>(out + e) =
+                    make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+            }
+        }
+    };
+    if (whole) {
+        if (gp == nullptr && rs == nullptr) whole_tile(F_{}, F_{});
+        else if (gp != nullptr && rs == nullptr) whole_tile(T_{}, F_{});
+        else if (gp == nullptr && rs != nullptr) whole_tile(F_{}, T_{});
+        else whole_tile(T_{}, T_{});
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < BG_FI; ++i) {
+        const int64_t nb = ncol + i * 16;
+        if (nb >= a.N) continue;
+#pragma unroll
+        for (int j = 0; j < BG_FJ; ++j) {
+            const int64_t m = mrow + j * 16;
+            if (m >= a.M) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (nb + r >= a.N) continue;
+                const int64_t e = m * ldc + nb + r;
+                float v = acc[i][j][r];
+                if (gp != nullptr) v *= 1.0f + a.gate_alpha * bf16_to_f32(gp[e]);
+                if (a.bias != nullptr) v += a.bias[nb + r];
+                if (rs != nullptr) v += bf16_to_f32(rs[e]);
+                out[e] = f32_to_bf16(v);
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ skinny bf16 (M <= 64)
 // Decode-shaped products: the weight is streamed once and dominates traffic.
 // Block = 16 weight rows (one MFMA n-tile) x all M rows (MT m-tiles of 16);
@@ -681,6 +978,12 @@ static int run_gemm(const GemmArgs& a, hipStream_t st, const char* what) {
         ok = ok && a.ldw % 8 == 0 && ((uintptr_t)a.W & 15) == 0;
         if (GATHER)
             for (int s = 0; s < 5; ++s) ok = ok && ((uintptr_t)a.src[s] & 15) == 0;
+        // many rows and whole 64-wide k-tiles: the 256 x 128 tile with DMA stages
+        if (ok && a.M >= BG_M && a.K % (3 * BG_K) == 0 && (!GATHER || a.Hq % BG_N == 0)) {
+            dim3 grid((unsigned)(ceil_div(a.N, BG_N) * ceil_div(a.M, BG_M)));
+            hipLaunchKernelGGL((gemm_bf16_big_kernel<GATHER>), grid, dim3(64 * BG_WAVES), 0, st, a);
+            return launch_status(what);
+        }
         if (ok) {
             dim3 grid((unsigned)ceil_div(a.N, MB_N), (unsigned)ceil_div(a.M, MB_M));
             hipLaunchKernelGGL((gemm_bf16_mfma_kernel<GATHER>), grid, dim3(256), 0, st, a);

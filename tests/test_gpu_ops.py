@@ -207,7 +207,8 @@ def test_linear(dtype, M, N, K):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("QH,HD,Hq,M,sectors", [(4, 8, 32, 10, "head"), (8, 96, 384, 40, "head"),
                                                  (8, 96, 384, 300, "head"), (4, 8, 32, 6, "open"),
-                                                 (8, 96, 384, 20, "open"), (8, 96, 384, 8200, "head")])
+                                                 (8, 96, 384, 20, "open"), (8, 96, 384, 8200, "head"),
+                                                 (8, 96, 384, 600, "open")])
 def test_beta_forward(dtype, QH, HD, Hq, M, sectors):
     from loom_amd import ops
     N, H = QH * HD, QH * Hq
