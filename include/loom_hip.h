@@ -299,7 +299,8 @@ int loom_polarm_forward(int dtype, const void* in, void* out, const uint8_t* mas
                         int64_t n, int64_t per_mask, float beta, float eps, void* stream);
 
 /* Tria path of the chunked sequence forward (Model._forward_chunked,
- * loomformer.py:3788-3883) on the fixed fire grid every W tokens, in two
+ * loomformer.py:3788-3883) on the fixed fire grid every W tokens (no <CARRY>
+ * id; loom_tria_chunked_forward_fires below takes explicit fires), in two
  * launches: every token's L-layer depth composition (axis l % 3, C_1 = N(T_1),
  * C_l = N(T_l C_{l-1})) folded into per-chunk temporal products, then the scan
  * over chunk boundaries (seeded chunk starts, temporal restarts at document
@@ -321,6 +322,31 @@ int loom_tria_chunked_forward(int dtype, const void* r, const void* i, const voi
                               float* keys, void* depth_out, void* ws, int64_t ws_bytes,
                               int64_t B, int64_t T, int64_t H, int64_t W, float alpha,
                               float polarm_beta, float eps, void* stream);
+
+/* The same with explicit <CARRY> fires (Model._forward_chunked with a carry
+ * token id, loomformer.py:3797-3815, :3852-3861): boundaries are the grid
+ * positions plus every position where any row fires explicitly, so chunks are
+ * ragged and T-1 can be a boundary; a row's fire at boundary t is
+ * (grid(t) & ~reset[t+1]) | explicit_fire[t], and every boundary emits a key
+ * for every row with that fire as its validity.
+ *   explicit_fire: [B,T] uint8 on the device (NULL = none);
+ *   bounds: HOST array of the n_bounds boundary positions, strictly increasing
+ *   in [0, T), holding every grid position ((t+1) % W == 0, t < T-1): the
+ *   reference's boundary_positions, (grid | explicit_fire.any(0)).nonzero(),
+ *   which it too builds on the host (:3814);
+ *   keys: [B, n_bounds, H, 3, 3] float; key_valid: [B, n_bounds] uint8 or NULL;
+ *   ws: loom_tria_chunked_fires_workspace_bytes(B,T,H,bounds,n_bounds) bytes.
+ * The chunk ends are uploaded from the host array and the stream synchronised
+ * before the launches (not capturable in a graph). */
+int64_t loom_tria_chunked_fires_workspace_bytes(int64_t B, int64_t T, int64_t H,
+                                                const int64_t* bounds, int64_t n_bounds);
+int loom_tria_chunked_forward_fires(int dtype, const void* r, const void* i, const void* o,
+                                    int64_t layer_stride, int64_t L, const uint8_t* reset,
+                                    const uint8_t* explicit_fire, const int64_t* bounds,
+                                    int64_t n_bounds, float* keys, uint8_t* key_valid,
+                                    void* depth_out, void* ws, int64_t ws_bytes, int64_t B,
+                                    int64_t T, int64_t H, int64_t W, float alpha,
+                                    float polarm_beta, float eps, void* stream);
 
 /* Causal GQA attention of a chunk of T prompt tokens at positions
  * start .. start+T-1, for prefilling the decode state chunk by chunk (the

@@ -1,11 +1,15 @@
-// Tria path of the chunked sequence forward on a fixed fire grid: per-token
-// depth composition through L layers, the boundary-to-boundary temporal carry
-// and PolARM at fires, producing the document keys the Tria readout pools.
+// Tria path of the chunked sequence forward: per-token depth composition
+// through L layers, the boundary-to-boundary temporal carry and PolARM at
+// fires, producing the document keys the Tria readout pools.
 //
 // Restates the Tria part of Model._forward_chunked (loomformer.py:3788-3883):
-//   chunks [cW, min(cW+W, T)); a chunk end e-1 < T-1 is a boundary (the grid
-//   positions (t+1) % W == 0, never t = T-1, :3802-3805); its fire is valid
-//   unless token e starts a document (hard_fire & ~next_is_reset, :3808-3810);
+//   boundaries are the grid positions (t+1) % W == 0 (never t = T-1,
+//   :3802-3805) plus, with explicit <CARRY> fires, every position where any
+//   row fires (:3797-3801, :3811-3815); chunks run from one boundary to the
+//   next ([cW, min(cW+W, T)) on the grid alone) and the last one ends at T-1;
+//   a row's fire at a boundary t is (grid(t) & ~reset[t+1]) | explicit[t]
+//   (hard_fire & ~next_is_reset | explicit_fire, :3808-3810), and every
+//   boundary emits a key for every row with that fire as its validity;
 //   layer l of token t uses axis l % 3: C_1 = N(T_1), C_l = N(T_l C_{l-1})
 //   (_block_core :3588-3617; tria_init / tria_step, tria.py:814-910), and the
 //   first token of chunk c >= 1 starts from the seed when it is valid
@@ -14,7 +18,7 @@
 //   document resets and at a seeded first token
 //   (temporal_carry_endpoint_reference, tria.py:1089-1123);
 //   at a boundary the state becomes polarm(state) where the fire is valid
-//   (tria.py:128-139) and is the chunk's document key.
+//   (tria.py:128-139) and is the boundary's document key.
 //
 // Work split.  N is a positive rescale, so every carry is a positive multiple
 // of the plain product of its local matrices, and the seed enters a chunk only
@@ -30,8 +34,12 @@
 //   tria_chunk_scan_kernel: one thread per (b, h) runs the short sequential
 //     scan over chunks: state = E_c (restart) or N(E_c state), PolARM at valid
 //     fires, keys out, and the seeded first-token rows of the optional
-//     per-token depth output.
+//     per-token depth output.  Seeded or not, the next chunk's endpoint is
+//     N(E_c state) unless a document starts inside it: a seeded first token
+//     restarts the endpoint at D_s ~ D_s(unseeded) state, an unseeded one
+//     continues from state.
 #include <cmath>
+#include <vector>
 
 #include "loom_common.h"
 #include "tria_math.h"
@@ -50,11 +58,25 @@ struct TriaChunkArgs {
     float* E;                  // [B, NC, 9, H] chunk products (slot-major, coalesced in h)
     uint8_t* restarted;        // [B, NC]: a reset lies inside the chunk
     void* depth_out;           // [B,T,H,9] dtype or null
-    float* keys;               // [B, NC-1, H, 9] fp32
+    float* keys;               // [B, K, H, 9] fp32
+    const int32_t* cend;       // [NC] exclusive chunk ends, or null: the grid [cW, min(cW+W, T))
+    const uint8_t* efire;      // [B,T] explicit fires or null
+    uint8_t* key_valid;        // [B, K] or null
     int64_t B, T, H;
-    int W, NC, HB;
+    int W, NC, HB, K;          // K = boundaries = keys: NC-1, or NC when T-1 is one
     float alpha, polarm_beta, eps;
 };
+
+// First position and length of chunk c.
+__device__ __forceinline__ void chunk_span(const TriaChunkArgs& a, int c, int64_t& s, int& nt) {
+    if (a.cend != nullptr) {
+        s = c == 0 ? 0 : a.cend[c - 1];
+        nt = (int)(a.cend[c] - s);
+    } else {
+        s = (int64_t)c * a.W;
+        nt = (int)((a.T - s) < a.W ? (a.T - s) : a.W);
+    }
+}
 
 // C <- T(r,i,o) C.  A token's first layer starts from C = I, for which the
 // product is exactly T (every term is a multiply by 1 or an add of 0), so one
@@ -117,8 +139,9 @@ tria_chunk_kernel(TriaChunkArgs a) {
     const int c = (int)(blk % a.NC);
     const int64_t b = blk / a.NC;
     const int64_t h = (int64_t)hb * kChunkThreads + threadIdx.x;
-    const int64_t s = (int64_t)c * a.W;
-    const int nt = (int)((a.T - s) < a.W ? (a.T - s) : a.W);
+    int64_t s;
+    int nt;
+    chunk_span(a, c, s, nt);
     const uint8_t* rst = a.reset != nullptr ? a.reset + b * a.T + s : nullptr;
     if (h == 0) {
         uint8_t any = 0;
@@ -232,7 +255,7 @@ tria_chunk_scan_kernel(TriaChunkArgs a) {
     if (sid >= a.B * a.H) return;
     const int64_t b = sid / a.H;
     const int64_t h = sid - b * a.H;
-    const int K = a.NC - 1;
+    const int K = a.K;
     float S[9];
 #pragma unroll
     for (int k = 0; k < 9; ++k) S[k] = 0.0f;
@@ -261,15 +284,24 @@ tria_chunk_scan_kernel(TriaChunkArgs a) {
 #pragma unroll
             for (int k = 0; k < 9; ++k) S[k] = pre[k] * inv;
         }
-        const int64_t snext = (int64_t)(c + 1) * a.W;   // first token of the next chunk (< T)
-        const bool valid = a.reset == nullptr || a.reset[b * a.T + snext] == 0;
+        // boundary t = snext - 1; snext == T only for a fire at T-1
+        int64_t snext;
+        int nt;
+        chunk_span(a, c, snext, nt);
+        snext += nt;
+        const bool next_reset = snext < a.T && a.reset != nullptr && a.reset[b * a.T + snext] != 0;
+        const bool grid = a.cend == nullptr || (snext % a.W == 0 && snext < a.T);
+        const bool valid = (grid && !next_reset) ||
+                           (a.efire != nullptr && a.efire[b * a.T + snext - 1] != 0);
         if (valid) polarm9(S, a.polarm_beta, a.eps);
         float* kp = a.keys + ((b * K + c) * a.H + h) * 9;
 #pragma unroll
         for (int k = 0; k < 9; ++k) kp[k] = S[k];
+        if (a.key_valid != nullptr && h == 0) a.key_valid[b * K + c] = valid ? 1 : 0;
         if constexpr (DOUT) {
-            // the next chunk's first token was seeded: D = N(T_L ... N(T_1 seed))
-            if (valid) {
+            // the next chunk's first token was seeded (seed_valid = fire &
+            // ~reset there): D = N(T_L ... N(T_1 seed))
+            if (valid && !next_reset && snext < a.T) {
                 T* d = (T*)a.depth_out + ((b * a.T + snext) * a.H + h) * 9;
                 float u[9], pre[9];
 #pragma unroll
@@ -303,19 +335,38 @@ static int chunked_dispatch(TriaChunkArgs a, hipStream_t st) {
     if (a.depth_out != nullptr) {
         if (full) launch_chunk<T, true, true>(a, g1, st);
         else launch_chunk<T, true, false>(a, g1, st);
-        if (a.NC > 1) hipLaunchKernelGGL((tria_chunk_scan_kernel<T, true>), g2, blk, 0, st, a);
+        if (a.K > 0) hipLaunchKernelGGL((tria_chunk_scan_kernel<T, true>), g2, blk, 0, st, a);
     } else {
         if (full) launch_chunk<T, false, true>(a, g1, st);
         else launch_chunk<T, false, false>(a, g1, st);
-        if (a.NC > 1) hipLaunchKernelGGL((tria_chunk_scan_kernel<T, false>), g2, blk, 0, st, a);
+        if (a.K > 0) hipLaunchKernelGGL((tria_chunk_scan_kernel<T, false>), g2, blk, 0, st, a);
     }
     return launch_status("loom_tria_chunked_forward");
 }
 
+// Workspace of NC chunks: E, the restart flags, the chunk ends.
+static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+static int64_t chunks_ws_bytes(int64_t B, int64_t H, int64_t NC) {
+    return align256(B * NC * 9 * H * 4) + align256(B * NC) + align256(NC * 4);
+}
 static int64_t chunked_ws_bytes(int64_t B, int64_t T, int64_t H, int64_t W) {
-    const int64_t NC = ceil_div(T, W);
-    const int64_t e_bytes = ((B * NC * 9 * H * 4) + 255) / 256 * 256;
-    return e_bytes + (B * NC + 255) / 256 * 256;
+    return chunks_ws_bytes(B, H, ceil_div(T, W));
+}
+
+// Chunk count of a boundary list: one chunk per boundary, plus the tail when
+// T-1 is not a boundary.
+static int64_t chunks_of(int64_t T, const int64_t* bounds, int64_t n_bounds) {
+    return n_bounds + ((n_bounds == 0 || bounds[n_bounds - 1] != T - 1) ? 1 : 0);
+}
+
+static int chunked_dtype_dispatch(int dtype, const TriaChunkArgs& a, hipStream_t st) {
+    switch (dtype) {
+        case LOOM_F32: return chunked_dispatch<float>(a, st);
+        case LOOM_BF16: return chunked_dispatch<bf16_t>(a, st);
+        case LOOM_F16: return chunked_dispatch<f16_t>(a, st);
+    }
+    set_error("tria_chunked: unsupported dtype %d", dtype);
+    return LOOM_ERR_INVALID;
 }
 
 }  // namespace loom
@@ -327,43 +378,102 @@ extern "C" int64_t loom_tria_chunked_workspace_bytes(int64_t B, int64_t T, int64
     return chunked_ws_bytes(B, T, H, W);
 }
 
-extern "C" int loom_tria_chunked_forward(int dtype, const void* r, const void* i, const void* o,
-                                         int64_t layer_stride, int64_t L, const uint8_t* reset,
-                                         float* keys, void* depth_out, void* ws, int64_t ws_bytes,
-                                         int64_t B, int64_t T, int64_t H, int64_t W, float alpha,
-                                         float polarm_beta, float eps, void* stream) {
-    clear_error();
+// Shape checks and argument block shared by both entry points.
+static int chunked_args(TriaChunkArgs& a, const void* r, const void* i, const void* o,
+                        int64_t layer_stride, int64_t L, const uint8_t* reset, float* keys,
+                        void* depth_out, int64_t B, int64_t T, int64_t H, int64_t W, int64_t NC,
+                        int64_t K, float alpha, float polarm_beta, float eps, void* ws,
+                        int64_t ws_bytes) {
     LOOM_CHECK(r && i && o, "tria_chunked: null r/i/o");
     LOOM_CHECK(B >= 0 && T >= 1 && H >= 0 && L >= 1 && W >= 1,
                "tria_chunked: bad shape B=%lld T=%lld H=%lld L=%lld W=%lld", (long long)B,
                (long long)T, (long long)H, (long long)L, (long long)W);
     LOOM_CHECK(L <= 4096, "tria_chunked: L=%lld layers is beyond the supported 4096", (long long)L);
     LOOM_CHECK(W <= (1 << 20), "tria_chunked: window W=%lld too large", (long long)W);
+    LOOM_CHECK(T < (1LL << 31), "tria_chunked: T=%lld too large", (long long)T);
     LOOM_CHECK(layer_stride >= B * T * H || L == 1,
                "tria_chunked: layer_stride %lld smaller than one [B,T,H] slice",
                (long long)layer_stride);
     LOOM_CHECK(polarm_beta >= 0.0f && polarm_beta < 1.0f,
                "PolARM beta must be finite and in [0, 1), got %g", (double)polarm_beta);
-    const int64_t NC = ceil_div(T, W);
-    LOOM_CHECK(NC == 1 || keys != nullptr, "tria_chunked: keys output required when T > W");
-    LOOM_CHECK(ws != nullptr && ws_bytes >= chunked_ws_bytes(B, T, H, W),
+    LOOM_CHECK(K == 0 || keys != nullptr, "tria_chunked: keys output required (%lld boundaries)",
+               (long long)K);
+    LOOM_CHECK(ws != nullptr && ws_bytes >= chunks_ws_bytes(B, H, NC),
                "tria_chunked: workspace of %lld bytes, need %lld", (long long)ws_bytes,
-               (long long)chunked_ws_bytes(B, T, H, W));
+               (long long)chunks_ws_bytes(B, H, NC));
     LOOM_CHECK(B * NC * ceil_div(H, kChunkThreads) < (1LL << 31), "tria_chunked: grid too large");
-    if (B * H == 0) return LOOM_OK;
-    TriaChunkArgs a{};
     a.r = r; a.i = i; a.o = o; a.layer_stride = layer_stride; a.L = (int)L; a.reset = reset;
     a.E = (float*)ws;
-    a.restarted = (uint8_t*)ws + (((B * NC * 9 * H * 4) + 255) / 256 * 256);
+    a.restarted = (uint8_t*)ws + align256(B * NC * 9 * H * 4);
     a.depth_out = depth_out; a.keys = keys;
-    a.B = B; a.T = T; a.H = H; a.W = (int)W; a.NC = (int)NC;
+    a.B = B; a.T = T; a.H = H; a.W = (int)W; a.NC = (int)NC; a.K = (int)K;
     a.HB = (int)ceil_div(H, kChunkThreads);
     a.alpha = alpha; a.polarm_beta = polarm_beta; a.eps = eps;
-    switch (dtype) {
-        case LOOM_F32: return chunked_dispatch<float>(a, (hipStream_t)stream);
-        case LOOM_BF16: return chunked_dispatch<bf16_t>(a, (hipStream_t)stream);
-        case LOOM_F16: return chunked_dispatch<f16_t>(a, (hipStream_t)stream);
+    return LOOM_OK;
+}
+
+extern "C" int loom_tria_chunked_forward(int dtype, const void* r, const void* i, const void* o,
+                                         int64_t layer_stride, int64_t L, const uint8_t* reset,
+                                         float* keys, void* depth_out, void* ws, int64_t ws_bytes,
+                                         int64_t B, int64_t T, int64_t H, int64_t W, float alpha,
+                                         float polarm_beta, float eps, void* stream) {
+    clear_error();
+    LOOM_CHECK(T >= 1 && W >= 1, "tria_chunked: need T >= 1 and W >= 1");
+    const int64_t NC = ceil_div(T, W);
+    TriaChunkArgs a{};
+    int rc = chunked_args(a, r, i, o, layer_stride, L, reset, keys, depth_out, B, T, H, W, NC, NC - 1,
+                          alpha, polarm_beta, eps, ws, ws_bytes);
+    if (rc != LOOM_OK || B * H == 0) return rc;
+    return chunked_dtype_dispatch(dtype, a, (hipStream_t)stream);
+}
+
+extern "C" int64_t loom_tria_chunked_fires_workspace_bytes(int64_t B, int64_t T, int64_t H,
+                                                           const int64_t* bounds, int64_t n_bounds) {
+    if (B < 0 || T < 1 || H < 0 || n_bounds < 0 || (n_bounds > 0 && bounds == nullptr)) return -1;
+    return chunks_ws_bytes(B, H, chunks_of(T, bounds, n_bounds));
+}
+
+extern "C" int loom_tria_chunked_forward_fires(int dtype, const void* r, const void* i,
+                                               const void* o, int64_t layer_stride, int64_t L,
+                                               const uint8_t* reset, const uint8_t* explicit_fire,
+                                               const int64_t* bounds, int64_t n_bounds, float* keys,
+                                               uint8_t* key_valid, void* depth_out, void* ws,
+                                               int64_t ws_bytes, int64_t B, int64_t T, int64_t H,
+                                               int64_t W, float alpha, float polarm_beta, float eps,
+                                               void* stream) {
+    clear_error();
+    LOOM_CHECK(T >= 1 && W >= 1, "tria_chunked: need T >= 1 and W >= 1");
+    LOOM_CHECK(n_bounds >= 0 && (n_bounds == 0 || bounds != nullptr), "tria_chunked: null boundary list");
+    // the boundary list is the grid plus the explicit fire positions: sorted,
+    // in range, and holding every grid position
+    int64_t grid_seen = 0;
+    for (int64_t k = 0; k < n_bounds; ++k) {
+        LOOM_CHECK(bounds[k] >= 0 && bounds[k] < T, "tria_chunked: boundary %lld outside [0, %lld)",
+                   (long long)bounds[k], (long long)T);
+        LOOM_CHECK(k == 0 || bounds[k] > bounds[k - 1], "tria_chunked: boundaries must increase");
+        grid_seen += ((bounds[k] + 1) % W == 0 && bounds[k] != T - 1) ? 1 : 0;
     }
-    set_error("tria_chunked: unsupported dtype %d", dtype);
-    return LOOM_ERR_INVALID;
+    LOOM_CHECK(grid_seen == (T - 1) / W,
+               "tria_chunked: the boundary list lacks %lld of the %lld grid positions (t+1) %% %lld == 0",
+               (long long)((T - 1) / W - grid_seen), (long long)((T - 1) / W), (long long)W);
+    const int64_t NC = chunks_of(T, bounds, n_bounds);
+    TriaChunkArgs a{};
+    int rc = chunked_args(a, r, i, o, layer_stride, L, reset, keys, depth_out, B, T, H, W, NC, n_bounds,
+                          alpha, polarm_beta, eps, ws, ws_bytes);
+    if (rc != LOOM_OK || B * H == 0) return rc;
+    // exclusive chunk ends, uploaded to the workspace; the stream is synchronised
+    // so the host array may go out of scope (the caller built the list on the host,
+    // after a device-to-host read of the fire mask, as the reference does)
+    std::vector<int32_t> ends((size_t)NC);
+    for (int64_t k = 0; k < n_bounds; ++k) ends[(size_t)k] = (int32_t)(bounds[k] + 1);
+    ends[(size_t)NC - 1] = (int32_t)T;
+    int32_t* dend = (int32_t*)((uint8_t*)ws + align256(B * NC * 9 * H * 4) + align256(B * NC));
+    hipStream_t st = (hipStream_t)stream;
+    LOOM_CHECK(hipMemcpyAsync(dend, ends.data(), (size_t)NC * sizeof(int32_t), hipMemcpyHostToDevice, st) ==
+                   hipSuccess && hipStreamSynchronize(st) == hipSuccess,
+               "tria_chunked: chunk-end upload failed");
+    a.cend = dend;
+    a.efire = explicit_fire;
+    a.key_valid = key_valid;
+    return chunked_dtype_dispatch(dtype, a, st);
 }

@@ -56,6 +56,9 @@ SIGNATURES = {
     "loom_tria_chunked_forward": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, _P, c_int64,
                                   c_int64, c_int64, c_int64, c_int64, c_float, c_float, c_float,
                                   _P],
+    "loom_tria_chunked_forward_fires": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64,
+                                        _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64,
+                                        c_float, c_float, c_float, _P],
     "loom_final_ca_sparse_forward": [c_int, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64,
                                      c_int64, c_float, _P],
     "loom_final_ca_sparse_strided": [c_int, _P, _P, _P, c_int64, _P, c_int64, _P, c_float, _P,
@@ -99,7 +102,9 @@ QUERIES = {"loom_gqa_workspace_bytes": ([c_int64] * 5, c_int64),
            "loom_decode_tria_readout_workspace_bytes": ([c_int64, c_int64], c_int64),
            "loom_ffn_decode_desc_bytes": ([], c_int64),
            "loom_linear_ln_workspace_bytes": ([c_int64, c_int64], c_int64),
-           "loom_tria_chunked_workspace_bytes": ([c_int64] * 4, c_int64)}
+           "loom_tria_chunked_workspace_bytes": ([c_int64] * 4, c_int64),
+           "loom_tria_chunked_fires_workspace_bytes": ([c_int64, c_int64, c_int64, _P, c_int64],
+                                                       c_int64)}
 
 _lib = None
 _lock = threading.Lock()

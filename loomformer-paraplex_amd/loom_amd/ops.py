@@ -8,6 +8,8 @@ launchers do; every launch goes on the current HIP stream.
 """
 from __future__ import annotations
 
+import ctypes
+
 import math
 from typing import List, Optional, Sequence, Tuple
 
@@ -436,13 +438,18 @@ def polarm(matrix: torch.Tensor, beta: float = 0.1, eps: float = 1e-6,
 def tria_chunked_forward(r: torch.Tensor, i: torch.Tensor, o: torch.Tensor, alpha: float,
                          window: int, polarm_beta: float = 0.1,
                          reset: Optional[torch.Tensor] = None, want_depth: bool = False,
-                         eps: float = 1e-6):
-    """Tria part of Model._forward_chunked (loomformer.py:3788-3883) on the
-    fixed fire grid: r, i, o are [L,B,T,H] stacks of the per-layer summaries
-    (layer l uses axis l % 3).  Returns (keys [B,K,H,3,3] float32 with
-    K = ceil(T/window) - 1, depth [B,T,H,3,3] or None): the document keys
-    (state after each boundary's PolARM) and optionally each token's
-    final-layer depth carry."""
+                         eps: float = 1e-6, explicit_fire: Optional[torch.Tensor] = None,
+                         return_valid: bool = False):
+    """Tria part of Model._forward_chunked (loomformer.py:3788-3883): r, i, o
+    are [L,B,T,H] stacks of the per-layer summaries (layer l uses axis l % 3).
+    Boundaries are the grid positions (t+1) % window == 0 (t < T-1) and, with
+    explicit_fire ([B,T] bool, the <CARRY> positions), every position where any
+    row fires (:3797-3815; the list is built on the host, as the reference's
+    boundary_positions is).  Returns (keys [B,K,H,3,3] float32, depth
+    [B,T,H,3,3] or None) with K = the boundary count: the document keys (state
+    after each boundary's PolARM where the row fired) and optionally each
+    token's final-layer depth carry; with return_valid also the key validity
+    [B,K] bool (the row's fire at the boundary, :3856)."""
     name = "tria_chunked_forward"
     _cuda(r, i, o, name=name)
     _same_dtype(r, i, o, name=name)
@@ -455,14 +462,40 @@ def tria_chunked_forward(r: torch.Tensor, i: torch.Tensor, o: torch.Tensor, alph
         _check(reset.is_cuda and reset.dtype == torch.bool and reset.shape == (B, T),
                f"{name}: reset must be a CUDA [B,T] bool tensor")
         rs = reset.contiguous()
-    K = -(-T // window) - 1
-    keys = torch.empty(B, max(K, 0), H, 3, 3, dtype=torch.float32, device=r.device)
     depth = torch.empty(B, T, H, 3, 3, dtype=r.dtype, device=r.device) if want_depth else None
-    nbytes = _lib.load().loom_tria_chunked_workspace_bytes(B, T, H, window)
+    lib = _lib.load()
+    if explicit_fire is None:
+        K = -(-T // window) - 1
+        keys = torch.empty(B, max(K, 0), H, 3, 3, dtype=torch.float32, device=r.device)
+        nbytes = lib.loom_tria_chunked_workspace_bytes(B, T, H, window)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=r.device)
+        call("loom_tria_chunked_forward", dtype_code(rc), ptr(rc), ptr(ic), ptr(oc), B * T * H, L,
+             ptr(rs), ptr(keys) if K > 0 else None, ptr(depth), ptr(ws), nbytes, B, T, H, window,
+             float(alpha), float(polarm_beta), float(eps), stream_of(rc))
+        if not return_valid:
+            return keys, depth
+        valid = torch.ones(B, max(K, 0), dtype=torch.bool, device=r.device)
+        if K > 0 and reset is not None:
+            valid = ~reset[:, window::window][:, :K]
+        return keys, depth, valid
+    _check(explicit_fire.is_cuda and explicit_fire.dtype == torch.bool and explicit_fire.shape == (B, T),
+           f"{name}: explicit_fire must be a CUDA [B,T] bool tensor")
+    grid = (torch.arange(T) + 1) % window == 0
+    grid[-1] = False
+    bounds = (grid | explicit_fire.any(dim=0).cpu()).nonzero().flatten().to(torch.int64).contiguous()
+    K = bounds.numel()
+    keys = torch.empty(B, K, H, 3, 3, dtype=torch.float32, device=r.device)
+    kv = torch.empty(B, K, dtype=torch.uint8, device=r.device)
+    ef = explicit_fire.contiguous().view(torch.uint8)
+    bptr = ctypes.c_void_p(bounds.data_ptr())
+    nbytes = lib.loom_tria_chunked_fires_workspace_bytes(B, T, H, bptr, K)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=r.device)
-    call("loom_tria_chunked_forward", dtype_code(rc), ptr(rc), ptr(ic), ptr(oc), B * T * H, L,
-         ptr(rs), ptr(keys) if K > 0 else None, ptr(depth), ptr(ws), nbytes, B, T, H, window,
-         float(alpha), float(polarm_beta), float(eps), stream_of(rc))
+    call("loom_tria_chunked_forward_fires", dtype_code(rc), ptr(rc), ptr(ic), ptr(oc), B * T * H, L,
+         ptr(rs), ptr(ef), bptr, K, ptr(keys) if K > 0 else None, ptr(kv) if K > 0 else None,
+         ptr(depth), ptr(ws), nbytes, B, T, H, window, float(alpha), float(polarm_beta), float(eps),
+         stream_of(rc))
+    if return_valid:
+        return keys, depth, kv.bool()
     return keys, depth
 
 

@@ -355,31 +355,38 @@ def polarm(matrix: torch.Tensor, beta: float = 0.1, eps: float = 1e-6) -> torch.
 
 
 def tria_chunked(r: torch.Tensor, i: torch.Tensor, o: torch.Tensor, alpha: float, window: int,
-                 polarm_beta: float = 0.1, reset: Optional[torch.Tensor] = None):
-    """Tria part of Model._forward_chunked (loomformer.py:3788-3883) with hard
-    fires on the grid only (no <CARRY> tokens), chunk by chunk as the reference
-    runs it: layer l of the chunk uses axis l % 3 (oracle.model's block loop,
-    loomformer.py:3588-3617); layer 0 of chunk c >= 1 is seeded with the
-    temporal state where seed_valid = fire[s-1] & ~reset[s] (:3826-3828);
-    the endpoint restarts at local resets and at a valid seed (:3834-3850);
-    at a boundary the state becomes polarm(state) where the fire is valid
-    (:3852-3858).  r, i, o: [L,B,T,H]; reset: [B,T] bool document starts
-    (None = position-0 only, :3534-3542).  Returns (keys [B,K,H,3,3],
-    depth [B,T,H,3,3])."""
+                 polarm_beta: float = 0.1, reset: Optional[torch.Tensor] = None,
+                 explicit_fire: Optional[torch.Tensor] = None, return_valid: bool = False):
+    """Tria part of Model._forward_chunked (loomformer.py:3788-3883), chunk by
+    chunk as the reference runs it.  Boundaries are the hard-fire grid
+    positions ((t+1) % W == 0, never T-1) plus every position where any row
+    has an explicit <CARRY> fire (:3797-3815); a row's fire at a boundary is
+    hard_fire & ~next_is_reset | explicit (:3808-3810).  Layer l of the chunk
+    uses axis l % 3 (oracle.model's block loop, loomformer.py:3588-3617);
+    layer 0 of chunk c >= 1 is seeded with the temporal state where
+    seed_valid = fire[s-1] & ~reset[s] (:3826-3828); the endpoint restarts at
+    local resets and at a valid seed (:3834-3850); at a boundary the state
+    becomes polarm(state) where the fire is valid and is appended as a key for
+    every row (:3852-3861).  r, i, o: [L,B,T,H]; reset: [B,T] bool document
+    starts (None = position-0 only, :3534-3542); explicit_fire: [B,T] bool
+    (None = no <CARRY> id).  Returns (keys [B,K,H,3,3], depth [B,T,H,3,3]),
+    plus the key validity [B,K] with return_valid."""
     L, B, T, H = r.shape
     W = int(window)
     doc_reset = torch.zeros(B, T, dtype=torch.bool) if reset is None else reset.bool().clone()
     doc_reset[:, 0] = True
+    explicit = (torch.zeros(B, T, dtype=torch.bool) if explicit_fire is None
+                else explicit_fire.bool())
     grid = ((torch.arange(T) + 1) % W) == 0
     grid[-1] = False
     next_is_reset = torch.zeros(B, T, dtype=torch.bool)
     next_is_reset[:, :-1] = doc_reset[:, 1:]
-    fire = grid[None, :] & ~next_is_reset
-    bounds = grid.nonzero().flatten().tolist()
+    fire = (grid[None, :] & ~next_is_reset) | explicit
+    bounds = (grid | explicit.any(dim=0)).nonzero().flatten().tolist()
     bset = set(bounds)
     stops = bounds + ([T - 1] if not bounds or bounds[-1] != T - 1 else [])
     state = None
-    keys, depth = [], []
+    keys, depth, valids = [], [], []
     s = 0
     for bp in stops:
         e = min(bp + 1, T)
@@ -406,8 +413,12 @@ def tria_chunked(r: torch.Tensor, i: torch.Tensor, o: torch.Tensor, alpha: float
             valid = fire[:, e - 1]
             state = torch.where(valid[:, None, None, None], polarm(state, polarm_beta), state)
             keys.append(state)
+            valids.append(valid)
         s = e
     keys_t = torch.stack(keys, dim=1) if keys else torch.zeros(B, 0, H, 3, 3)
+    if return_valid:
+        valid_t = torch.stack(valids, dim=1) if valids else torch.zeros(B, 0, dtype=torch.bool)
+        return keys_t, torch.cat(depth, dim=1), valid_t
     return keys_t, torch.cat(depth, dim=1)
 
 

@@ -22,6 +22,9 @@ Fixtures:
   nano_cpu_ref.npz   nano.yaml seed 0, B=1, 128-token prompt + 64 greedy ids,
                      per-step top-5 logits
   ops.npz            per-op input/output vectors at small shapes
+  chunked_keys.npz   Model._forward_chunked's Tria inputs (per-layer r, i, o),
+                     document keys and fire mask on the tiny config with
+                     explicit <CARRY> fires and mid-row document starts
   configs.json       the model-shape keys of cfg/nano.yaml and cfg/nano_chk.yaml
 """
 from __future__ import annotations
@@ -191,6 +194,54 @@ def golden_tiny_decode(lf) -> dict:
     arrays["greedy_carry"] = ids2.numpy()
     arrays["logits_carry"] = logits2.numpy()
     return arrays
+
+
+def golden_chunked(lf, tr) -> dict:
+    """Model._forward_chunked (loomformer.py:3788-3883) on the tiny config with
+    explicit <CARRY> fires: the per-layer r, i, o the Tria ops consumed
+    (captured at tria.record_depth_replay, which _block_core calls with each
+    layer's summaries, :3586), the document keys, the fire mask and the
+    document resets.  Rows differ: a fire at T-1 (the tail chunk becomes a
+    boundary), a document restart after a grid position (its hard fire is
+    invalid), consecutive fires, a fire on a grid position and a restart right
+    after an explicit fire (valid fire, no seed)."""
+    cfg = make_cfg(lf, None, **TINY)
+    torch.manual_seed(0)
+    model = lf.Model(cfg).eval()
+    perturb(model, 123)
+    B, T, carry = 3, 30, 5
+    g = torch.Generator().manual_seed(21)
+    idx = torch.randint(0, TINY["vocab"] - 1, (B, T), generator=g)
+    idx[idx >= carry] += 1                       # no accidental <CARRY>
+    for b, t in ((0, 3), (0, 29), (1, 10), (2, 4), (2, 5), (2, 15)):
+        idx[b, t] = carry
+    pos = torch.arange(T).repeat(B, 1)
+    pos[1, 16:] = torch.arange(T - 16)           # row 1: a document starts at 16
+    pos[2, 6:] = torch.arange(T - 6)             # row 2: a document starts at 6
+    rec = []
+    orig = tr.record_depth_replay
+    tr.record_depth_replay = lambda r, i, o, axis: rec.append((r.detach().clone(), i.detach().clone(),
+                                                              o.detach().clone(), axis))
+    lf.CARRY_TOKEN_ID = carry
+    model.capture_tria_depth_carry = True
+    try:
+        with torch.no_grad():
+            model(idx, position_ids=pos)
+    finally:
+        tr.record_depth_replay = orig
+        lf.CARRY_TOKEN_ID = None
+    L = len(model.blocks)
+    assert len(rec) % L == 0
+    per_layer = [[rec[c * L + l] for c in range(len(rec) // L)] for l in range(L)]
+    for l in range(L):
+        assert all(x[3] == l % 3 for x in per_layer[l])
+    stack = lambda k: torch.stack([torch.cat([x[k] for x in per_layer[l]], dim=1) for l in range(L)])
+    return {"r": stack(0).numpy(), "i": stack(1).numpy(), "o": stack(2).numpy(),
+            "idx": idx.numpy(), "position_ids": pos.numpy(), "reset": pos.eq(0).numpy(),
+            "explicit_fire": idx.eq(carry).numpy(), "fire_mask": model.last_tria_fire_mask.numpy(),
+            "keys": model.last_tria_document_carry.numpy(),
+            "window": np.array(TINY["tria_temporal_window"]), "alpha": np.array(TINY["tria_carrier_alpha"]),
+            "polarm_beta": np.array(TINY["tria_polarm_beta"])}
 
 
 def golden_nano_cpu(lf, ref: str) -> dict:
@@ -405,6 +456,9 @@ def main() -> None:
     if not only or "ops" in only:
         np.savez_compressed(os.path.join(HERE, "ops.npz"), **golden_ops(lf, tr))
         print("wrote ops.npz")
+    if not only or "chunked" in only:
+        np.savez_compressed(os.path.join(HERE, "chunked_keys.npz"), **golden_chunked(lf, tr))
+        print("wrote chunked_keys.npz")
     if not only or "nano" in only:
         np.savez_compressed(os.path.join(HERE, "nano_cpu_ref.npz"), **golden_nano_cpu(lf, args.ref))
         print("wrote nano_cpu_ref.npz")

@@ -70,3 +70,21 @@ def test_mirror_rejects_cpu_tensors_like_the_reference():
         ops.tria_step_forward(x, x, x, torch.zeros(2, 3, 8, 3, 3), 0.05, 0)
     with pytest.raises(RuntimeError, match="training-only"):
         ops.paraplex_backward()
+
+
+def test_tria_chunked_fires_rejects_bad_boundary_lists():
+    """The boundary list is validated on the host before any device work."""
+    from loom_amd import _lib
+    lib = _lib.load()
+    arr = lambda *v: (ctypes.c_int64 * len(v))(*v)
+    # T=30, W=8: grid positions 7, 15, 23 must be present
+    assert lib.loom_tria_chunked_fires_workspace_bytes(3, 30, 128, arr(7, 15, 23), 3) > 0
+    args = lambda b, n: (0, ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 3 * 30 * 4, 4,
+                         None, None, b, n, ctypes.c_void_p(16), None, None, ctypes.c_void_p(16),
+                         1 << 30, 3, 30, 4, 8, 0.05, 0.1, 1e-6, None)
+    with pytest.raises(RuntimeError, match="lacks 1 of the 3 grid positions"):
+        _lib.call("loom_tria_chunked_forward_fires", *args(arr(3, 7, 23), 3))
+    with pytest.raises(RuntimeError, match="must increase"):
+        _lib.call("loom_tria_chunked_forward_fires", *args(arr(7, 7, 15, 23), 4))
+    with pytest.raises(RuntimeError, match="outside"):
+        _lib.call("loom_tria_chunked_forward_fires", *args(arr(7, 15, 23, 30), 4))

@@ -102,6 +102,65 @@ def test_tria_chunked_strided_layers_and_repeat():
         torch.testing.assert_close(keys.cpu(), w_keys, rtol=1e-3, atol=1e-4)
 
 
+def test_tria_chunked_explicit_fires_match_reference_keys():
+    """loom_tria_chunked_forward_fires on the fixture Model._forward_chunked
+    wrote with <CARRY> fires: keys and validity against the reference's own,
+    the depth output against the oracle."""
+    import numpy as np
+    import os
+    from loom_amd import ops
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "chunked_keys.npz"))
+    t = lambda k: torch.from_numpy(z[k])
+    r, i, o = t("r"), t("i"), t("o")
+    alpha, W, beta = float(z["alpha"]), int(z["window"]), float(z["polarm_beta"])
+    keys, depth, valid = ops.tria_chunked_forward(
+        r.to(DEV), i.to(DEV), o.to(DEV), alpha, W, beta, reset=t("reset").to(DEV), want_depth=True,
+        explicit_fire=t("explicit_fire").to(DEV), return_valid=True)
+    torch.testing.assert_close(keys.cpu(), t("keys"), rtol=1e-3, atol=1e-4)
+    bounds = [3, 4, 5, 7, 10, 15, 23, 29]
+    assert torch.equal(valid.cpu(), t("fire_mask")[:, bounds])
+    _, w_depth = ref.tria_chunked(r, i, o, alpha, W, beta, t("reset"), t("explicit_fire"))
+    torch.testing.assert_close(depth.cpu(), w_depth, rtol=1e-3, atol=1e-4)
+
+
+@pytest.mark.parametrize("L,B,T,H,W,density,dtype", [
+    (5, 4, 70, 40, 16, 0.05, torch.float32),    # sparse ragged fires, L not a multiple of 3
+    (6, 3, 33, 300, 8, 0.5, torch.float32),     # dense fires: many one-token chunks
+    (10, 2, 130, 64, 32, 0.03, torch.bfloat16),
+])
+def test_tria_chunked_explicit_fires_match_oracle(L, B, T, H, W, density, dtype):
+    from loom_amd import ops
+    r, i, o = _inputs(31 + T, L, B, T, H, dtype)
+    g = torch.Generator().manual_seed(5 + T)
+    fire = torch.rand(B, T, generator=g) < density
+    fire[0, T - 1] = True                       # the tail chunk becomes a boundary
+    fire[B - 1, W - 1] = True                   # an explicit fire on a grid position
+    reset = torch.rand(B, T, generator=g) < 0.03
+    reset[:, 0] = True
+    reset[1, W] = True                          # a document start after a grid boundary
+    keys, depth, valid = ops.tria_chunked_forward(
+        r.to(DEV), i.to(DEV), o.to(DEV), 0.2, W, 0.1, reset=reset.to(DEV), want_depth=True,
+        explicit_fire=fire.to(DEV), return_valid=True)
+    w_keys, w_depth, w_valid = ref.tria_chunked(r.float(), i.float(), o.float(), 0.2, W, 0.1, reset,
+                                                fire, return_valid=True)
+    assert keys.shape == w_keys.shape
+    assert torch.equal(valid.cpu(), w_valid)
+    torch.testing.assert_close(keys.cpu(), w_keys, rtol=1e-3, atol=1e-4)
+    tol = dict(rtol=1e-3, atol=1e-4) if dtype == torch.float32 else dict(rtol=2e-2, atol=1e-2)
+    torch.testing.assert_close(depth.float().cpu(), w_depth, **tol)
+
+
+def test_tria_chunked_fires_without_explicit_equals_grid_entry():
+    """An explicit-fire mask with no fires gives the grid entry's keys."""
+    from loom_amd import ops
+    L, B, T, H, W = 4, 2, 64, 33, 16
+    r, i, o = (x.to(DEV) for x in _inputs(13, L, B, T, H))
+    k1, _ = ops.tria_chunked_forward(r, i, o, 0.2, W, 0.1)
+    k2, _ = ops.tria_chunked_forward(r, i, o, 0.2, W, 0.1,
+                                     explicit_fire=torch.zeros(B, T, dtype=torch.bool, device=DEV))
+    assert torch.equal(k1, k2)
+
+
 def test_tria_readout_matches_oracle():
     from loom_amd import ops
     g = torch.Generator().manual_seed(12)

@@ -331,3 +331,43 @@ def test_engine_config_presets_match_fixture_configs():
         d = json.load(f)
     assert ModelConfig.from_dict(NANO) == ModelConfig.from_dict(d["nano"])
     assert ModelConfig.from_dict(NANO_CHK) == ModelConfig.from_dict(d["nano_chk"])
+
+
+# ---------------------------------------------------------------- chunked Tria keys
+
+def _chunked_fixture():
+    z = np.load(os.path.join(GOLD, "chunked_keys.npz"))
+    return {k: T(z[k]) for k in z.files}
+
+
+def test_chunked_keys_match_reference():
+    """oracle.ops.tria_chunked with explicit <CARRY> fires against the keys and
+    fire mask Model._forward_chunked wrote (per-row fires, a fire at T-1,
+    consecutive fires, document starts after a grid position and after an
+    explicit fire)."""
+    z = _chunked_fixture()
+    keys, depth, valid = ops.tria_chunked(z["r"], z["i"], z["o"], float(z["alpha"]), int(z["window"]),
+                                          float(z["polarm_beta"]), z["reset"], z["explicit_fire"],
+                                          return_valid=True)
+    close(keys, z["keys"], rtol=1e-5, atol=1e-6)
+    T_ = z["r"].shape[2]
+    grid = (torch.arange(T_) + 1) % int(z["window"]) == 0
+    grid[-1] = False
+    bounds = (grid | z["explicit_fire"].any(0)).nonzero().flatten()
+    assert bounds.tolist() == [3, 4, 5, 7, 10, 15, 23, 29]
+    assert torch.equal(valid, z["fire_mask"][:, bounds])
+    # the fixture exercises both outcomes at a shared boundary
+    assert not bool(valid.all()) and bool(valid.any(0).all())
+    assert depth.shape == (3, T_, 128, 3, 3)
+
+
+def test_chunked_keys_fixture_needs_the_explicit_fires():
+    """Without the <CARRY> positions the oracle has only the grid keys, and the
+    grid keys it shares with the fixture differ (the explicit fires restart the
+    temporal state earlier)."""
+    z = _chunked_fixture()
+    keys, _ = ops.tria_chunked(z["r"], z["i"], z["o"], float(z["alpha"]), int(z["window"]),
+                               float(z["polarm_beta"]), z["reset"])
+    assert keys.shape[1] == 3
+    grid_idx = [3, 5, 6]          # boundaries 7, 15, 23 in the fixture's list
+    assert not torch.allclose(keys[0], z["keys"][0, grid_idx], rtol=1e-3, atol=1e-4)
