@@ -438,16 +438,69 @@ __device__ __forceinline__ void rope8(const bf16_t* head, const float* cr, const
     for (int e = 0; e < 8; ++e) out[e] = fmaf(x[e], c[e], sg * y[e] * sn[e]);
 }
 
-// 3 waves per SIMD (<= 168 VGPRs): all chunk blocks of a decode step resident in one round
+// Piece swizzle of the row-major K / V tiles: piece c of row r sits at
+// c ^ kv_swz(r) (bits 1, 2 of r to bits 1, 0), so the 8 rows of a 16-byte
+// fragment read and the 4 rows x 32 B of a transposing read fall in distinct
+// banks.  The pieces of a row stay a permutation of 0..HD/8-1.
+__device__ __forceinline__ int kv_swz(int r) { return (((r >> 1) & 1) << 1) | ((r >> 2) & 1); }
+
+typedef short gqa_v4s __attribute__((ext_vector_type(4)));
+typedef uint32_t gqa_u4 __attribute__((ext_vector_type(4)));   // a 16-byte piece as a native vector
+
+__device__ __forceinline__ f32x4_t mfma16(gqa_u4 a, uint4 b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// B fragment of 32 positions x 16 dims (dims 16*dt..) from a row-major tile:
+// lane l gets positions 8*(l/16)..+7 of dim 16*dt + l%16, as two transposing
+// 8-byte reads (lane r of a 16-lane group points at row k0 + r/4, dims
+// 16*dt + 4*(r%4)..+3 and receives rows k0..k0+3 of dim 16*dt + r).
+template <int CPR>
+__device__ __forceinline__ uint4 tile_tr_frag(const gqa_u4* tile, int dt, int lq, int lr) {
+    uint32_t w[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int row = 8 * lq + 4 * h + (lr >> 2);
+        const int c = 2 * dt + ((lr & 3) >> 1);
+        const char* p = reinterpret_cast<const char*>(tile + row * CPR + (c ^ kv_swz(row))) + 8 * (lr & 1);
+        const gqa_v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) gqa_v4s*)(p));
+        w[2 * h] = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
+        w[2 * h + 1] = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// LDS ordering inside one wave (its LDS operations execute in order): keeps
+// the compiler from moving LDS accesses across; no wait, no s_barrier.
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Each wave takes 32 positions at a time.  Their K and V rows are loaded as
+// whole 16-byte pieces in cache order (piece j of the tile: row j / (HD/8),
+// piece j % (HD/8): 1 KB contiguous per load instruction when the position
+// stride is HD), stored to the wave's LDS tiles row-major, and read back as
+//   S^T = K Q^T      A = 16 K rows (16-byte reads), B = the G query heads;
+//   C = P V, Kctx = P K   B = 8 positions of one dimension per lane through
+//                    the gfx950 transposing LDS read (ds_read_b64_tr_b16).
+// The next tile's loads are in flight while a tile is computed; the waves
+// never wait for each other inside the loop.
+// 2 waves per SIMD (<= 256 VGPRs; the chunking makes about 1.5 blocks per CU):
+// all chunk blocks of a decode step resident in one round
 template <int HD, int G, bool FROM_QKV>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     constexpr int KK = HD / 32;            // 32-wide k-steps of a head
     constexpr int DT = HD / 16;            // 16-wide output tiles of a head
+    constexpr int CPR = HD / 8;            // 16-byte pieces per row
+    constexpr int NI = kMfTile * CPR / 64; // load instructions per tile (K or V)
     constexpr int REC = 2 * G + 2 * G * HD;
     struct Tiles {
-        uint16_t kt[HD][kMfTile];          // K tile transposed: [dim][position]
-        uint16_t vt[HD][kMfTile];
+        gqa_u4 k[kMfTile * CPR];           // K tile, row-major (swizzled pieces)
+        gqa_u4 v[kMfTile * CPR];
         uint16_t pt[16][kMfTile];          // P: [head][position]
         float cr[16];                      // per-head rescale of this step
     };
@@ -500,27 +553,37 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     const bf16_t* kb = a.kc + b * a.csb + kvh * a.csh;
     const bf16_t* vb = a.vc + b * a.csb + kvh * a.csh;
     const int nstep = (int)((t1 - t0 + 4 * kMfTile - 1) / (4 * kMfTile));
-    // K and V rows ts + 16*hf + lr, dims 32*kk + 8*lq (row clamped in range; masked
-    // below); the next step's rows are requested as soon as this step's are in LDS
-    uint4 kr[2][KK], vr[2][KK];
+    // piece j = i*64 + lane of the tile at ts: row j / CPR (clamped in range,
+    // masked below), piece j % CPR; the next tile's pieces are requested as
+    // soon as this tile's are in LDS
+    gqa_u4 kr[NI], vr[NI];
+    const gqa_u4* kn_lds = reinterpret_cast<const gqa_u4*>(knew);
+    const gqa_u4* vn_lds = reinterpret_cast<const gqa_u4*>(vnew);
     auto load_kv = [&](int64_t ts) {
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            int64_t t = ts + 16 * hf + lr;
+        for (int i = 0; i < NI; ++i) {
+            const int j = i * 64 + lane, row = j / CPR, c = j - row * CPR;
+            int64_t t = ts + row;
             t = t < t1 ? t : t1 - 1;
-            if (FROM_QKV && t == pos) {            // this token: the row staged in LDS
-#pragma unroll
-                for (int kk = 0; kk < KK; ++kk) {
-                    kr[hf][kk] = knew[4 * kk + lq];
-                    vr[hf][kk] = vnew[4 * kk + lq];
-                }
-                continue;
+            kr[i] = *reinterpret_cast<const gqa_u4*>(kb + t * a.cst + 8 * c);
+            vr[i] = *reinterpret_cast<const gqa_u4*>(vb + t * a.cst + 8 * c);
+            if constexpr (FROM_QKV) {
+                // this token: the row staged in LDS (its cache row is being
+                // written by this block; the loaded value is discarded)
+                const gqa_u4 kn = kn_lds[c], vn = vn_lds[c];
+                const bool here = t == pos;
+                kr[i] = here ? kn : kr[i];
+                vr[i] = here ? vn : vr[i];
             }
+        }
+    };
+    auto store_kv = [&]() {
 #pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-                kr[hf][kk] = *reinterpret_cast<const uint4*>(kb + t * a.cst + 32 * kk + 8 * lq);
-                vr[hf][kk] = *reinterpret_cast<const uint4*>(vb + t * a.cst + 32 * kk + 8 * lq);
-            }
+        for (int i = 0; i < NI; ++i) {
+            const int j = i * 64 + lane, row = j / CPR, c = j - row * CPR;
+            const int slot = row * CPR + (c ^ kv_swz(row));
+            tl.k[slot] = kr[i];
+            tl.v[slot] = vr[i];
         }
     };
     load_kv(t0 + wave * kMfTile);
@@ -550,17 +613,22 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) accC[dt] = accK[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // every wave runs the same number of steps (the loop holds barriers); a
-    // step past t1 is fully masked
+    // every wave runs the same number of steps; a step past t1 is fully masked
     for (int it = 0; it < nstep; ++it) {
         const int64_t ts = t0 + wave * kMfTile + (int64_t)it * 4 * kMfTile;
+        wave_lds_fence();                  // the previous tile's reads came first
+        store_kv();
+        if (it + 1 < nstep) load_kv(ts + 4 * kMfTile);
+        wave_lds_fence();
         // S^T[position 16*hf + 4*lq + r][head lr]
         f32x4_t sc[2];
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
             sc[hf] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            const int row = 16 * hf + lr;
 #pragma unroll
-            for (int kk = 0; kk < KK; ++kk) sc[hf] = mfma16(kr[hf][kk], qf[kk], sc[hf]);
+            for (int kk = 0; kk < KK; ++kk)
+                sc[hf] = mfma16(tl.k[row * CPR + ((4 * kk + lq) ^ kv_swz(row))], qf[kk], sc[hf]);
         }
         float mx = -INFINITY;
         float sv[2][4];
@@ -591,22 +659,7 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
         lh = fmaf(lh, corr, ls);
         mh = mnew;
         if (lq == 0) tl.cr[lr] = corr;
-        // K, V transposed into LDS: [dim 32*kk + 8*lq + e][position 16*hf + lr]
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-            for (int kk = 0; kk < KK; ++kk) {
-                const uint32_t kw[4] = {kr[hf][kk].x, kr[hf][kk].y, kr[hf][kk].z, kr[hf][kk].w};
-                const uint32_t vw[4] = {vr[hf][kk].x, vr[hf][kk].y, vr[hf][kk].z, vr[hf][kk].w};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int d = 32 * kk + 8 * lq + e;
-                    tl.kt[d][16 * hf + lr] = (uint16_t)(kw[e >> 1] >> (16 * (e & 1)));
-                    tl.vt[d][16 * hf + lr] = (uint16_t)(vw[e >> 1] >> (16 * (e & 1)));
-                }
-            }
-        if (it + 1 < nstep) load_kv(ts + 4 * kMfTile);
-        lds_barrier();
+        wave_lds_fence();
         // rescale the accumulators (rows = heads 4*lq + r) and add P V, P K
         float cf[4];
 #pragma unroll
@@ -619,13 +672,11 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
                 accC[dt][r] *= cf[r];
                 accK[dt][r] *= cf[r];
             }
-            const uint4 vbf = *reinterpret_cast<const uint4*>(&tl.vt[16 * dt + lr][8 * lq]);
-            const uint4 kbf = *reinterpret_cast<const uint4*>(&tl.kt[16 * dt + lr][8 * lq]);
-            accC[dt] = mfma16(pa, vbf, accC[dt]);
-            accK[dt] = mfma16(pa, kbf, accK[dt]);
+            accC[dt] = mfma16(pa, tile_tr_frag<CPR>(tl.v, dt, lq, lr), accC[dt]);
+            accK[dt] = mfma16(pa, tile_tr_frag<CPR>(tl.k, dt, lq, lr), accK[dt]);
         }
-        lds_barrier();                     // tiles are rewritten next step
     }
+    __syncthreads();                       // every wave is done with its tiles (wred aliases them)
     // this wave's partials -> wred[wave] = [m | l | c | k] (unnormalised)
     float (*wred)[REC] = reinterpret_cast<float (*)[REC]>(lds);
     if (lq == 0 && lr < G) {
