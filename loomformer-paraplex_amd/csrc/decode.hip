@@ -438,6 +438,9 @@ __device__ __forceinline__ void rope8(const bf16_t* head, const float* cr, const
     for (int e = 0; e < 8; ++e) out[e] = fmaf(x[e], c[e], sg * y[e] * sn[e]);
 }
 
+// Cache policy of the K / V stream loads (2: nontemporal; 0: default).
+constexpr int kKvLoadPolicy = 2;
+
 // Piece swizzle of the row-major K / V tiles: piece c of row r sits at
 // c ^ kv_swz(r) (bits 1, 2 of r to bits 1, 0), so the 8 rows of a 16-byte
 // fragment read and the 4 rows x 32 B of a transposing read fall in distinct
@@ -557,6 +560,11 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     // masked below), piece j % CPR; the next tile's pieces are requested as
     // soon as this tile's are in LDS
     gqa_u4 kr[NI], vr[NI];
+    // raw buffer views of this (b, kv head)'s rows < t1 (byte offsets fit 31 bits:
+    // checked by the host)
+    const int kv_bytes = (int)(t1 * a.cst * 2);
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)kb, (short)0, kv_bytes, kBufferDword3);
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0, kv_bytes, kBufferDword3);
     const gqa_u4* kn_lds = reinterpret_cast<const gqa_u4*>(knew);
     const gqa_u4* vn_lds = reinterpret_cast<const gqa_u4*>(vnew);
     auto load_kv = [&](int64_t ts) {
@@ -565,8 +573,9 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
             const int j = i * 64 + lane, row = j / CPR, c = j - row * CPR;
             int64_t t = ts + row;
             t = t < t1 ? t : t1 - 1;
-            kr[i] = *reinterpret_cast<const gqa_u4*>(kb + t * a.cst + 8 * c);
-            vr[i] = *reinterpret_cast<const gqa_u4*>(vb + t * a.cst + 8 * c);
+            const int off = (int)(t * a.cst * 2) + 16 * c;
+            kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, kKvLoadPolicy);
+            vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, kKvLoadPolicy);
             if constexpr (FROM_QKV) {
                 // this token: the row staged in LDS (its cache row is being
                 // written by this block; the loaded value is discarded)
@@ -1289,6 +1298,10 @@ static int gqa_checks(const char* who, const void* k_cache, const void* v_cache,
                "%s: caches must be 16-byte aligned with strides divisible by 8", who);
     LOOM_CHECK(cache_stride_t >= HD && cache_stride_h >= HD,
                "%s: cache strides smaller than a head row", who);
+    // the MFMA form addresses the rows of one (b, kv head) with 31-bit byte offsets
+    LOOM_CHECK(len * cache_stride_t * 2 < (1LL << 31),
+               "%s: %lld positions at stride %lld exceed the 2 GiB per-head row span", who,
+               (long long)len, (long long)cache_stride_t);
     return LOOM_OK;
 }
 
