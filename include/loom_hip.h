@@ -128,7 +128,20 @@ typedef struct {
     loom_linear_segment seg[4];
     const uint8_t* only_if;   /* optional [only_if_n] device flags: when none is set the */
     int64_t only_if_n;        /* bf16 fused launch leaves every output untouched */
+    const void* x_frag;   /* optional fragment-major copy of x (k % 32 == 0), else NULL */
+    const void* x2_frag;  /* optional fragment-major copy of x2 (k2 % 32 == 0), else NULL */
 } loom_linear_multi_desc;
+
+/* Fragment-major layout of an [m, k] bf16 matrix (m <= 64, k % 32 == 0), the
+ * operand order of v_mfma_f32_16x16x32_bf16: the 16-byte piece at index
+ * (j*(k/32) + s)*64 + l (j < ceil(m/16), s < k/32, l < 64) holds row
+ * 16*j + l%16, columns 32*s + 8*(l/16) .. +7; rows >= m are never read.  A
+ * decode projection reads its activations from such a copy as whole 1 KB
+ * runs per load instruction instead of 16 rows x 64 B (measured about 2 us
+ * faster per launch for the 32 x 768 decode activations).  The fused bf16
+ * launch of loom_linear_multi reads x_frag / x2_frag instead of x / x2 when
+ * they are set (they must hold the same values); loom_linear_ln can write one
+ * (out_frag). */
 
 /* Several decode projections in one launch (no counterpart in the reference;
  * the engine's restatement of Model.step, loomformer.py:3951-4091, uses it to
@@ -154,10 +167,11 @@ int64_t loom_linear_multi_desc_bytes(void);
  * blocks, writing fp32 partial sums to the workspace (at least
  * loom_linear_ln_workspace_bytes(m, n), 16-byte aligned), and the LayerNorm
  * kernel adds them up; other cases write x w^T + x2 w2^T + bias to seg[0].out
- * (dense [m, n]) and normalise that. */
+ * (dense [m, n]) and normalise that.  out_frag (optional, the bf16 split-K form
+ * with n % 32 == 0 only): the result also in fragment-major order. */
 int loom_linear_ln(int dtype, const loom_linear_multi_desc* desc, const float* gamma,
                    const float* beta, float eps, void* out, int64_t ldo, float* workspace,
-                   int64_t workspace_bytes, void* stream);
+                   int64_t workspace_bytes, void* out_frag, void* stream);
 int64_t loom_linear_ln_workspace_bytes(int64_t M, int64_t N);
 
 /* One decode token (T = 1) of the Paraplex FFN core and the Tria depth op. */
@@ -191,6 +205,7 @@ typedef struct {
     void* p_out;
     float alpha;
     int32_t axis;
+    void* act_frag;            /* optional fragment-major copy of act (fused path, H % 32 == 0) */
 } loom_ffn_decode_desc;
 
 /* beta = beta_space(u, q, kctx, c, d); (act, s, trace) = paraplex(R, beta);

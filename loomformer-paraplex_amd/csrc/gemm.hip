@@ -620,6 +620,7 @@ struct FfnArgs {
     uint16_t* p;                // [M, H] (with gate_w)
     float alpha;
     int mode, axis;
+    uint16_t* actf;             // fragment-major copy of act, or null
 };
 
 __device__ __forceinline__ float bf(uint16_t x) { return bf16_to_f32(x); }
@@ -686,6 +687,9 @@ ffn_decode_kernel(FfnArgs f) {
         const float act = fmaf(amp, sv, x) * gate;
         f.trace[e] = f32_to_bf16(s0);
         f.act[e] = f32_to_bf16(act);
+        if (f.actf != nullptr)
+            f.actf[(((m >> 4) * (H >> 5) + (h >> 5)) * 64 + (m & 15) + 16 * ((h & 31) >> 3)) * 8 + (h & 7)] =
+                f32_to_bf16(act);
         if (f.s != nullptr) f.s[e] = f32_to_bf16(sv);
         // Tria depth op on (r, i, o) = (R, I, O) as stored
         const float i_ = round_bf(sv), o_ = round_bf(act);
@@ -738,6 +742,8 @@ struct LinArgs {
     int nsplit;
     const uint8_t* only_if;   // with only_if_n flags: the launch does nothing unless one is set
     int only_if_n;
+    const uint4* Xf;          // fragment-major copies of X / X2 (or null): piece
+    const uint4* X2f;         // (j*(K/32) + step)*64 + lane is the MFMA B fragment
 };
 
 template <int MT, int NW, int UN>
@@ -781,12 +787,15 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
             const uint16_t* wrow = first ? sg.W + n * sg.ldw : sg.W2 + n * sg.ldw2;
             const uint16_t* xb = first ? a.X : a.X2;
             const int64_t ldx = first ? a.ldx : a.ldx2;
+            const uint4* xf = first ? a.Xf : a.X2f;
+            const int64_t fs = first ? step : step - S1, fS = first ? S1 : S2;
             wv[u] = (kin && nvalid) ? *reinterpret_cast<const uint4*>(wrow + k) : make_uint4(0, 0, 0, 0);
 #pragma unroll
             for (int j = 0; j < MT; ++j) {
                 const int64_t m = j * 16 + fr;
-                xv[u][j] = (kin && m < a.M) ? *reinterpret_cast<const uint4*>(xb + m * ldx + k)
-                                            : make_uint4(0, 0, 0, 0);
+                xv[u][j] = !(kin && m < a.M) ? make_uint4(0, 0, 0, 0)
+                           : xf != nullptr ? xf[(j * fS + fs) * 64 + lane]
+                                           : *reinterpret_cast<const uint4*>(xb + m * ldx + k);
             }
         }
 #pragma unroll
@@ -1084,13 +1093,19 @@ static void launch_skinny_multi(const LinArgs& a, dim3 grid, int mt, int64_t ste
     }
 }
 
+// Fragment-major activation copies: whole 32-wide k-steps, 16-byte aligned.
+static bool frag_ok(const loom_linear_multi_desc& d) {
+    return (d.x_frag == nullptr || (d.k % 32 == 0 && ((uintptr_t)d.x_frag & 15) == 0)) &&
+           (d.x2_frag == nullptr || (d.k2 > 0 && d.k2 % 32 == 0 && ((uintptr_t)d.x2_frag & 15) == 0));
+}
+
 // Host side of loom_linear_multi: one fused launch for bf16 when every piece
 // is 16-byte aligned, otherwise (and for fp32 / fp16) one product per segment
 // and input, the second input accumulated through the residual epilogue.
 template <typename T>
 static int linear_multi_dispatch(const loom_linear_multi_desc& d, hipStream_t st) {
     bool fused = std::is_same<T, bf16_t>::value && d.m <= 64 && d.k % 8 == 0 && d.ldx % 8 == 0 &&
-                 ((uintptr_t)d.x & 15) == 0;
+                 ((uintptr_t)d.x & 15) == 0 && frag_ok(d);
     if (d.k2 > 0) fused = fused && d.k2 % 8 == 0 && d.ldx2 % 8 == 0 && ((uintptr_t)d.x2 & 15) == 0;
     for (int s = 0; s < d.nseg; ++s) {
         const loom_linear_segment& g = d.seg[s];
@@ -1104,6 +1119,8 @@ static int linear_multi_dispatch(const loom_linear_multi_desc& d, hipStream_t st
         a.M = d.m; a.nseg = d.nseg; a.nsplit = 1;
         a.only_if = d.only_if;
         a.only_if_n = (int)d.only_if_n;
+        a.Xf = (const uint4*)d.x_frag;
+        a.X2f = (const uint4*)d.x2_frag;
         int64_t ncols = 0;
         for (int s = 0; s < d.nseg; ++s) {
             const loom_linear_segment& g = d.seg[s];
@@ -1187,7 +1204,7 @@ __global__ void __launch_bounds__(64 * KV)
 splitk_ln_kernel(const float* __restrict__ partial, int64_t ldp,
                  const float* __restrict__ bias, const float* __restrict__ gamma,
                  const float* __restrict__ beta, T* __restrict__ out, int64_t ldo, int64_t rows,
-                 int N, float eps) {
+                 int N, float eps, T* __restrict__ outf) {
     __shared__ float red[2][KV];
     const int64_t row = blockIdx.x;
     const int lane = threadIdx.x & 63, k = threadIdx.x >> 6;
@@ -1231,8 +1248,18 @@ splitk_ln_kernel(const float* __restrict__ partial, int64_t ldp,
     if (!in) return;
     const float g[4] = {gv.x, gv.y, gv.z, gv.w};
     const float e4[4] = {ev.x, ev.y, ev.z, ev.w};
+    T y[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) st(out + row * ldo + c + e, fmaf((x[e] - mean) * rstd, g[e], e4[e]));
+    for (int e = 0; e < 4; ++e) {
+        st(&y[e], fmaf((x[e] - mean) * rstd, g[e], e4[e]));
+        out[row * ldo + c + e] = y[e];
+    }
+    if (outf != nullptr) {
+        // fragment-major copy: piece (row/16, c/32, row%16 + 16*((c%32)/8)), elements c%8 ..
+        const int64_t piece = ((row >> 4) * (N >> 5) + (c >> 5)) * 64 + (row & 15) + 16 * ((c & 31) >> 3);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) outf[piece * 8 + (c & 7) + e] = y[e];
+    }
 }
 
 extern "C" int64_t loom_linear_ln_workspace_bytes(int64_t M, int64_t N) {
@@ -1241,7 +1268,7 @@ extern "C" int64_t loom_linear_ln_workspace_bytes(int64_t M, int64_t N) {
 
 extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const float* gamma,
                               const float* beta, float eps, void* out, int64_t ldo, float* workspace,
-                              int64_t workspace_bytes, void* stream) {
+                              int64_t workspace_bytes, void* out_frag, void* stream) {
     clear_error();
     LOOM_CHECK(d != nullptr && d->nseg == 1, "linear_ln: one output segment expected");
     LOOM_CHECK(gamma && beta && out, "linear_ln: null LayerNorm argument");
@@ -1254,10 +1281,12 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
                  ((uintptr_t)d->x & 15) == 0 && g.ldw % 8 == 0 && ((uintptr_t)g.w & 15) == 0 &&
                  g.n % 4 == 0 && workspace != nullptr && ((uintptr_t)workspace & 15) == 0 &&
                  ((((uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)g.bias) & 15) == 0) &&
-                 workspace_bytes >= loom_linear_ln_workspace_bytes(d->m, g.n);
+                 workspace_bytes >= loom_linear_ln_workspace_bytes(d->m, g.n) && frag_ok(*d);
     if (d->k2 > 0)
         fused = fused && d->k2 % 8 == 0 && d->ldx2 % 8 == 0 && ((uintptr_t)d->x2 & 15) == 0 &&
                 g.ldw2 % 8 == 0 && ((uintptr_t)g.w2 & 15) == 0;
+    LOOM_CHECK(out_frag == nullptr || (fused && g.n % 32 == 0 && ((uintptr_t)out_frag & 15) == 0),
+               "linear_ln: out_frag needs the bf16 split-K form (m <= 64, aligned) and n %% 32 == 0");
     if (!fused) {
         // y = product (+ bias) into seg.out, then LayerNorm of y
         int rc = loom_linear_multi(dtype, d, stream);
@@ -1270,6 +1299,8 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
     a.X = (const uint16_t*)d->x; a.ldx = d->ldx; a.K = d->k;
     a.X2 = (const uint16_t*)d->x2; a.ldx2 = d->ldx2; a.K2 = d->k2;
     a.M = d->m; a.nseg = 1;
+    a.Xf = (const uint4*)d->x_frag;
+    a.X2f = (const uint4*)d->x2_frag;
     a.seg[0] = LinSeg{(const uint16_t*)g.w, g.ldw, (const uint16_t*)g.w2, g.ldw2, g.out, g.ldc,
                       nullptr, nullptr, 0, 0.0f, g.n};
     const int64_t ntiles = ceil_div(g.n, 16);
@@ -1290,7 +1321,7 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
 #define LOOM_SLN_KV(NS, KV)                                                                   \
     hipLaunchKernelGGL((splitk_ln_kernel<bf16_t, NS, KV>), dim3((unsigned)d->m), dim3(64 * (KV)), \
                        0, st, workspace, g.n, g.bias, gamma, beta, (bf16_t*)out, ldo, d->m,     \
-                       (int)g.n, eps);
+                       (int)g.n, eps, (bf16_t*)out_frag);
 #define LOOM_SLN(NS)                                                                          \
     case NS:                                                                                  \
         if (kv <= 1) { LOOM_SLN_KV(NS, 1) }                                                   \
@@ -1358,6 +1389,8 @@ extern "C" int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* d, void* s
         f.carry = (uint16_t*)d->carry_out; f.p = (uint16_t*)d->p_out; f.alpha = d->alpha;
         f.mode = d->carry_prev ? 1 : (d->seed ? 2 : 0);
         f.axis = d->axis;
+        LOOM_CHECK(d->act_frag == nullptr || d->H % 32 == 0, "ffn_decode: act_frag needs H %% 32 == 0");
+        f.actf = (uint16_t*)d->act_frag;
         const dim3 grid((unsigned)ceil_div(d->H, 16));
         hipStream_t st = (hipStream_t)stream;
         switch ((int)ceil_div(d->M, 16)) {
@@ -1369,6 +1402,7 @@ extern "C" int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* d, void* s
         return launch_status("loom_ffn_decode");
     }
     LOOM_CHECK(d->beta && d->s, "ffn_decode: the unfused path needs the beta and s buffers");
+    LOOM_CHECK(d->act_frag == nullptr, "ffn_decode: act_frag needs the fused bf16 path (M <= 64, aligned)");
     int rc = loom_beta_forward(dtype, d->u, d->q_h, d->k_ctx_h, d->c_h, d->d_h, d->w_compact,
                                d->beta, nullptr, d->M, d->N, d->H, d->imag_in, d->hidden_per_q_head,
                                d->head_dim, d->n_q_heads, d->open_sectors, stream);

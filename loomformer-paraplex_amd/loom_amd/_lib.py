@@ -28,7 +28,8 @@ class LinearMultiDesc(ctypes.Structure):
     """loom_linear_multi_desc (include/loom_hip.h)."""
     _fields_ = [("x", c_void_p), ("ldx", c_int64), ("k", c_int64), ("x2", c_void_p),
                 ("ldx2", c_int64), ("k2", c_int64), ("m", c_int64), ("nseg", ctypes.c_int32),
-                ("seg", LinearSegment * 4), ("only_if", c_void_p), ("only_if_n", c_int64)]
+                ("seg", LinearSegment * 4), ("only_if", c_void_p), ("only_if_n", c_int64),
+                ("x_frag", c_void_p), ("x2_frag", c_void_p)]
 
 # name -> argument types (all return c_int status)
 SIGNATURES = {
@@ -40,7 +41,7 @@ SIGNATURES = {
                           c_int64, c_int64, c_int64, c_int64, c_int, _P],
     "loom_linear_multi": [c_int, _P, _P],
     "loom_ffn_decode": [c_int, _P, _P],
-    "loom_linear_ln": [c_int, _P, _P, _P, c_float, _P, c_int64, _P, c_int64, _P],
+    "loom_linear_ln": [c_int, _P, _P, _P, c_float, _P, c_int64, _P, c_int64, _P, _P],
     "loom_linear": [c_int, _P, c_int64, _P, c_int64, _P, _P, c_float, _P, _P, c_int64,
                     c_int64, c_int64, c_int64, _P],
     "loom_depth_attn_forward": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64,
@@ -167,15 +168,20 @@ class FfnDecodeDesc(ctypes.Structure):
                 ("act", c_void_p), ("s", c_void_p), ("beta", c_void_p),
                 ("carry_prev", c_void_p), ("seed", c_void_p), ("seed_valid", c_void_p),
                 ("gate_w", c_void_p), ("carry_out", c_void_p), ("p_out", c_void_p),
-                ("alpha", c_float), ("axis", ctypes.c_int32)]
+                ("alpha", c_float), ("axis", ctypes.c_int32), ("act_frag", c_void_p)]
 
 
-def linear_multi_desc(x, segments, x2=None, m=None, only_if=None):
+def linear_multi_desc(x, segments, x2=None, m=None, only_if=None, x_frag=None, x2_frag=None):
     """Build a LinearMultiDesc.  x, x2: [m, k] tensors (row-strided views are
     fine); segments: dicts with w, out and optional w2, bias, gate_p,
     gate_alpha (tensors keep their own row strides); only_if: optional uint8
-    device flags (the fused launch skips the product when none is set)."""
+    device flags (the fused launch skips the product when none is set);
+    x_frag / x2_frag: optional fragment-major copies of x / x2."""
     d = LinearMultiDesc()
+    if x_frag is not None:
+        d.x_frag = x_frag.data_ptr()
+    if x2_frag is not None:
+        d.x2_frag = x2_frag.data_ptr()
     d.x, d.ldx, d.k = x.data_ptr(), x.stride(0), x.shape[1]
     if x2 is not None:
         d.x2, d.ldx2, d.k2 = x2.data_ptr(), x2.stride(0), x2.shape[1]
@@ -208,6 +214,18 @@ def ffn_decode_desc(**kw):
             v = v.data_ptr()
         setattr(d, k, v)
     return d
+
+
+def frag_major(x: torch.Tensor) -> torch.Tensor:
+    """The fragment-major copy of an [m, k] matrix (m <= 64, k % 32 == 0) as
+    loom_linear_multi_desc.x_frag expects it (rows padded to a multiple of 16
+    with zeros), built with torch ops (tests and one-off callers)."""
+    m, k = x.shape
+    mp = -(-m // 16) * 16
+    xp = torch.zeros(mp, k, dtype=x.dtype, device=x.device)
+    xp[:m] = x
+    # [j, r, s, q, e] -> [j, s, q, r, e]: piece (j, s, l = r + 16 q) holds row 16j + r, cols 32s + 8q ..
+    return xp.view(mp // 16, 16, k // 32, 4, 8).permute(0, 2, 3, 1, 4).contiguous().view(-1)
 
 
 def ptr(t):

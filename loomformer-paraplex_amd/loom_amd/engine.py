@@ -147,6 +147,10 @@ class LoomDecoder:
         self.rd_ws_bytes = rb
         # activations
         self.h = z(B, N)
+        # fragment-major copy of h written by the sublayer LayerNorms (bf16 fused
+        # form), read by the projections of h that follow them
+        self.h_frag = (z(-(-B // 16) * 16 * N) if dtype == torch.bfloat16 and B <= 64 and N % 32 == 0
+                       else None)
         self.h2 = z(B, N)
         self.qkv = z(B, N + 2 * c.KV)
         self.q = z(B, c.QH, c.HD)
@@ -160,6 +164,8 @@ class LoomDecoder:
         self.G = z(B, H) if c.gate_proj else None      # gate_proj(u), the amplitude source
         self.beta = z(B, H)
         self.act = z(B, H)
+        self.act_frag = (z(-(-B // 16) * 16 * H) if self.h_frag is not None and H % 32 == 0
+                         else None)
         self.s = z(B, H)
         self.ffn_out = z(B, N)
         self.y = z(B, N)                # pre-LayerNorm sum of a sublayer (unfused path)
@@ -218,23 +224,25 @@ class LoomDecoder:
         self._call("loom_linear", self.code, _P(x), ldx or K, _P(w), K, _P(bias), _P(gate_p),
                    float(gate_alpha), _P(residual), _P(out), ldc or Nout, M, Nout, K, self._stream())
 
-    def _multi(self, key, x, segments, x2=None, only_if=None) -> None:
+    def _multi(self, key, x, segments, x2=None, only_if=None, x_frag=None) -> None:
         """loom_linear_multi with a descriptor built once per call site (every
         pointer in it is a persistent engine buffer or weight)."""
         d = self._descs.get(key)
         if d is None:
-            d = _lib.linear_multi_desc(x, segments, x2=x2, only_if=only_if)
+            d = _lib.linear_multi_desc(x, segments, x2=x2, only_if=only_if, x_frag=x_frag)
             self._descs[key] = d
         self._call("loom_linear_multi", self.code, _lib.ctypes.byref(d), self._stream())
 
-    def _linear_ln(self, key, x, segment, x2, gamma, beta) -> None:
-        """h = LayerNorm(x w^T + x2 w2^T + bias) through loom_linear_ln."""
+    def _linear_ln(self, key, x, segment, x2, gamma, beta, x2_frag=None) -> None:
+        """h = LayerNorm(x w^T + x2 w2^T + bias) through loom_linear_ln (h and
+        its fragment-major copy)."""
         d = self._descs.get(key)
         if d is None:
-            d = _lib.linear_multi_desc(x, [segment], x2=x2)
+            d = _lib.linear_multi_desc(x, [segment], x2=x2, x2_frag=x2_frag)
             self._descs[key] = d
         self._call("loom_linear_ln", self.code, _lib.ctypes.byref(d), _P(gamma), _P(beta), 1e-5,
-                   _P(self.h), self.cfg.N, _P(self.ln_ws), self.ln_ws.numel() * 4, self._stream())
+                   _P(self.h), self.cfg.N, _P(self.ln_ws), self.ln_ws.numel() * 4, _P(self.h_frag),
+                   self._stream())
 
     def reset(self) -> None:
         """Forget all sequence state (Model.step at pos 0 starts afresh)."""
@@ -304,7 +312,7 @@ class LoomDecoder:
             segs = [dict(w=self.kvw, out=hist[:, sub]), real]
             if c.gate_proj:
                 segs.append(dict(w=blk["gpw"], out=self.G, bias=blk["gpb"]))
-            self._multi(("kvr", bi), self.h, segs)
+            self._multi(("kvr", bi), self.h, segs, x_frag=self.h_frag)
             self.depth_read(sub, self.hist, self.dh, B)
             # ---- Paraplex FFN core (beta space, fused pointwise chain; loomformer.py:
             # 2818-2893, :2533-2560) and the Tria depth op (loomformer.py:4012-4040,
@@ -327,22 +335,25 @@ class LoomDecoder:
                     seed=self.doc if use_seed else None,
                     seed_valid=self.pending if use_seed else None,
                     gate_w=blk["gate_w"] if gate else None, carry_out=self.carry[out_i],
-                    p_out=self.p[new_p] if gate else None, alpha=float(c.tria_alpha), axis=bi % 3)
+                    p_out=self.p[new_p] if gate else None, alpha=float(c.tria_alpha), axis=bi % 3,
+                    act_frag=self.act_frag)
                 self._descs[key] = d
             self._call("loom_ffn_decode", self.code, _lib.ctypes.byref(d), st)
             carry_i, p_i = out_i, new_p
             # ---- LN(w_o(d_h) + W2(act) + b2) (loomformer.py:4045): one launch + LN
             self._linear_ln(("ffn", bi), self.dh.view(B, N),
                             dict(w=self.wo_for(sub), w2=blk["w2"], out=self.y, bias=blk["b2"]),
-                            self.act, blk["ln2_w"], blk["ln2_b"])
+                            self.act, blk["ln2_w"], blk["ln2_b"], x2_frag=self.act_frag)
             if not last:
                 # next history slot (loomformer.py:4050) and the next block's qkv
                 sub += 1
                 self._multi(("next", bi), self.h, [dict(w=self.kvw, out=hist[:, sub]),
-                                                   dict(w=self.blocks[bi + 1]["qkv"], out=self.qkv)])
+                                                   dict(w=self.blocks[bi + 1]["qkv"], out=self.qkv)],
+                            x_frag=self.h_frag)
             else:
                 # the final-CA query of the last hidden state (tria.py:1580)
-                self._multi(("next", bi), self.h, [dict(w=self.wqk, out=self.q_ca)])
+                self._multi(("next", bi), self.h, [dict(w=self.wqk, out=self.q_ca)],
+                            x_frag=self.h_frag)
         # ---- temporal carry + PolARM on fires (loomformer.py:4053-4085), in place,
         # and the TriaAggregator readout of the new state (tria.py:1436-1441): one launch
         self._call("loom_decode_tria_readout", self.code, _P(self.carry[carry_i]),

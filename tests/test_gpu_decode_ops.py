@@ -467,14 +467,18 @@ def test_ffn_decode(dtype, mode, gate, axis, gsrc):
     act, s, beta = (torch.empty(M, H, device=DEV, dtype=dtype) for _ in range(3))
     carry = torch.empty(M, H, 3, 3, device=DEV, dtype=dtype)
     p = torch.empty(M, H, device=DEV, dtype=dtype)
+    # the fragment-major copy of act (bf16 fused path)
+    act_frag = torch.empty(M * H, device=DEV, dtype=dtype) if dtype == torch.bfloat16 else None
     desc = _lib.ffn_decode_desc(
         u=u, q_h=q, k_ctx_h=kc, c_h=c, d_h=d, w_compact=w, M=M, N=N, H=H, imag_in=K,
         hidden_per_q_head=H // QH, head_dim=HD, n_q_heads=QH, open_sectors=0,
         p_real=R, gate_src=G, imag_bias=ib, trace=trace, trace_w=tw, powlu_m=3.0, act=act, s=s,
         beta=beta, carry_prev=prev if mode == 1 else None, seed=prev if mode == 2 else None,
         seed_valid=valid if mode == 2 else None, gate_w=gw if gate else None, carry_out=carry,
-        p_out=p if gate else None, alpha=0.0375, axis=axis)
+        p_out=p if gate else None, alpha=0.0375, axis=axis, act_frag=act_frag)
     _lib.call("loom_ffn_decode", code(u), ctypes.byref(desc), S(u))
+    if act_frag is not None:
+        assert torch.equal(act_frag, _lib.frag_major(act))
     # oracle, fp32 on the host
     be = ref.beta_space_grouped(host(u)[:, None], host(q)[:, None], host(kc)[:, None],
                                 host(c)[:, None], host(d)[:, None], host(w), QH, HD, "head")
@@ -518,12 +522,57 @@ def test_linear_ln(dtype, M, K2):
     ws = torch.empty(nb // 4, device=DEV)
     d = _lib.linear_multi_desc(x, [dict(w=w, w2=w2, out=y, bias=b)], x2=x2)
     _lib.call("loom_linear_ln", code(x), ctypes.byref(d), P(gam), P(bet), 1e-5, P(out), N, P(ws),
-              nb, S(x))
+              nb, None, S(x))
     pre = host(x) @ host(w).T + host(b)
     if K2:
         pre = pre + host(x2) @ host(w2).T
     want = torch.nn.functional.layer_norm(pre, (N,), host(gam), host(bet), 1e-5)
     check(out, want, dtype)
+
+
+@pytest.mark.parametrize("M,K2", [(32, 768), (32, 3072), (20, 0), (64, 768)])
+def test_fragment_major_activations(M, K2):
+    """loom_linear_ln's out_frag is the fragment-major copy of its output, and
+    loom_linear_ln / loom_linear_multi reading x_frag / x2_frag give the same
+    bits as reading x / x2 (bf16 fused launch)."""
+    from loom_amd import _lib
+    g = torch.Generator().manual_seed(3 + M + K2)
+    N, K, bf = 768, 768, torch.bfloat16
+    r = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(DEV, bf)
+    x, w = r(M, K), r(N, K, sc=K ** -0.5)
+    x2 = r(M, K2) if K2 else None
+    w2 = r(N, K2, sc=K2 ** -0.5) if K2 else None
+    b = torch.randn(N, generator=g).to(DEV)
+    gam = (torch.rand(N, generator=g) + 0.5).to(DEV)
+    bet = torch.randn(N, generator=g).to(DEV)
+    nb = _lib.load().loom_linear_ln_workspace_bytes(M, N)
+    ws = torch.empty(nb // 4, device=DEV)
+    wq = r(1152, N, sc=N ** -0.5)
+    outs = []
+    for frag in (False, True):
+        y = torch.zeros(M, N, device=DEV, dtype=bf)
+        out = torch.zeros(M, N, device=DEV, dtype=bf)
+        of = torch.full((-(-M // 16) * 16 * N,), float("nan"), device=DEV, dtype=bf)
+        d = _lib.linear_multi_desc(x, [dict(w=w, w2=w2, out=y, bias=b)], x2=x2,
+                                   x_frag=_lib.frag_major(x) if frag else None,
+                                   x2_frag=_lib.frag_major(x2) if frag and K2 else None)
+        _lib.call("loom_linear_ln", code(x), ctypes.byref(d), P(gam), P(bet), 1e-5, P(out), N,
+                  P(ws), nb, P(of), S(x))
+        torch.cuda.synchronize()
+        got = of.view(-1)[:_lib.frag_major(out).numel()]
+        want = _lib.frag_major(out)
+        rows = torch.arange(want.numel(), device=DEV) // 8 % 64 % 16 + \
+            16 * (torch.arange(want.numel(), device=DEV) // 8 // 64 // (N // 32))
+        assert torch.equal(got[rows < M], want[rows < M])
+        outs.append(out)
+        # a projection of the normalised rows through the copy
+        q = torch.zeros(M, 1152, device=DEV, dtype=bf)
+        dq = _lib.linear_multi_desc(out, [dict(w=wq, out=q)], x_frag=of if frag else None)
+        _lib.call("loom_linear_multi", code(x), ctypes.byref(dq), S(x))
+        outs.append(q)
+    assert torch.equal(outs[0], outs[2])
+    torch.cuda.synchronize()
+    assert torch.equal(outs[1], outs[3])
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
