@@ -206,6 +206,8 @@ typedef struct {
     float alpha;
     int32_t axis;
     void* act_frag;            /* optional fragment-major copy of act (fused path, H % 32 == 0) */
+    const void* u_frag;        /* optional fragment-major copy of u (head sectors, head_dim and N
+                                  multiples of 32): the fused path reads the u sector from it */
 } loom_ffn_decode_desc;
 
 /* beta = beta_space(u, q, kctx, c, d); (act, s, trace) = paraplex(R, beta);

@@ -43,6 +43,8 @@ struct GemmArgs {
     const void* src[5];  // Q, Kctx, C, U, D  (each [M, Nm] row-major)
     int64_t Nm, HD, Hq;
     int open;
+    const uint4* Uf;     // head sectors: fragment-major copy of U (the skinny form reads its
+                         // sector from it), or null
 };
 
 // Element offset of packed column kk of group g, and which source it is in.
@@ -544,10 +546,16 @@ __device__ __forceinline__ void skinny_mainloop(const GemmArgs& a, int64_t n0,
                 const int64_t m = j * 16 + fr;
                 uint4 v = make_uint4(0, 0, 0, 0);
                 if (kin && m < a.M) {
-                    if constexpr (GATHER)
-                        v = *reinterpret_cast<const uint4*>(gather_ptr(a, m, k, g, 2));
-                    else
+                    if constexpr (GATHER) {
+                        // a 32-wide step lies in one sector (HD % 32 == 0 with Uf)
+                        const int64_t ku = k - 3 * a.HD;
+                        if (a.Uf != nullptr && ku >= 0 && ku < a.Nm)
+                            v = a.Uf[(j * (a.Nm >> 5) + (ku >> 5)) * 64 + (threadIdx.x & 63)];
+                        else
+                            v = *reinterpret_cast<const uint4*>(gather_ptr(a, m, k, g, 2));
+                    } else {
                         v = *reinterpret_cast<const uint4*>(X + m * a.ldx + k);
+                    }
                 }
                 xv[u][j] = v;
             }
@@ -1391,6 +1399,10 @@ extern "C" int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* d, void* s
         f.axis = d->axis;
         LOOM_CHECK(d->act_frag == nullptr || d->H % 32 == 0, "ffn_decode: act_frag needs H %% 32 == 0");
         f.actf = (uint16_t*)d->act_frag;
+        LOOM_CHECK(d->u_frag == nullptr || (!d->open_sectors && d->head_dim % 32 == 0 && d->N % 32 == 0 &&
+                                           ((uintptr_t)d->u_frag & 15) == 0),
+                   "ffn_decode: u_frag needs head sectors, head_dim and N multiples of 32, 16-byte alignment");
+        a.Uf = (const uint4*)d->u_frag;
         const dim3 grid((unsigned)ceil_div(d->H, 16));
         hipStream_t st = (hipStream_t)stream;
         switch ((int)ceil_div(d->M, 16)) {
@@ -1403,6 +1415,7 @@ extern "C" int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* d, void* s
     }
     LOOM_CHECK(d->beta && d->s, "ffn_decode: the unfused path needs the beta and s buffers");
     LOOM_CHECK(d->act_frag == nullptr, "ffn_decode: act_frag needs the fused bf16 path (M <= 64, aligned)");
+    // (u_frag is only read, and u holds the same values: the unfused path reads u)
     int rc = loom_beta_forward(dtype, d->u, d->q_h, d->k_ctx_h, d->c_h, d->d_h, d->w_compact,
                                d->beta, nullptr, d->M, d->N, d->H, d->imag_in, d->hidden_per_q_head,
                                d->head_dim, d->n_q_heads, d->open_sectors, stream);

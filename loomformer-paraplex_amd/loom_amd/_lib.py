@@ -168,7 +168,8 @@ class FfnDecodeDesc(ctypes.Structure):
                 ("act", c_void_p), ("s", c_void_p), ("beta", c_void_p),
                 ("carry_prev", c_void_p), ("seed", c_void_p), ("seed_valid", c_void_p),
                 ("gate_w", c_void_p), ("carry_out", c_void_p), ("p_out", c_void_p),
-                ("alpha", c_float), ("axis", ctypes.c_int32), ("act_frag", c_void_p)]
+                ("alpha", c_float), ("axis", ctypes.c_int32), ("act_frag", c_void_p),
+                ("u_frag", c_void_p)]
 
 
 def linear_multi_desc(x, segments, x2=None, m=None, only_if=None, x_frag=None, x2_frag=None):

@@ -336,7 +336,8 @@ class LoomDecoder:
                     seed_valid=self.pending if use_seed else None,
                     gate_w=blk["gate_w"] if gate else None, carry_out=self.carry[out_i],
                     p_out=self.p[new_p] if gate else None, alpha=float(c.tria_alpha), axis=bi % 3,
-                    act_frag=self.act_frag)
+                    act_frag=self.act_frag,
+                    u_frag=self.h_frag if (c.sectors != "open" and c.HD % 32 == 0) else None)
                 self._descs[key] = d
             self._call("loom_ffn_decode", self.code, _lib.ctypes.byref(d), st)
             carry_i, p_i = out_i, new_p

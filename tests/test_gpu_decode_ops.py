@@ -469,13 +469,16 @@ def test_ffn_decode(dtype, mode, gate, axis, gsrc):
     p = torch.empty(M, H, device=DEV, dtype=dtype)
     # the fragment-major copy of act (bf16 fused path)
     act_frag = torch.empty(M * H, device=DEV, dtype=dtype) if dtype == torch.bfloat16 else None
+    # and the u sector read from a fragment-major copy of u
+    u_frag = _lib.frag_major(u) if act_frag is not None and mode != 0 else None
     desc = _lib.ffn_decode_desc(
         u=u, q_h=q, k_ctx_h=kc, c_h=c, d_h=d, w_compact=w, M=M, N=N, H=H, imag_in=K,
         hidden_per_q_head=H // QH, head_dim=HD, n_q_heads=QH, open_sectors=0,
         p_real=R, gate_src=G, imag_bias=ib, trace=trace, trace_w=tw, powlu_m=3.0, act=act, s=s,
         beta=beta, carry_prev=prev if mode == 1 else None, seed=prev if mode == 2 else None,
         seed_valid=valid if mode == 2 else None, gate_w=gw if gate else None, carry_out=carry,
-        p_out=p if gate else None, alpha=0.0375, axis=axis, act_frag=act_frag)
+        p_out=p if gate else None, alpha=0.0375, axis=axis, act_frag=act_frag,
+        u_frag=u_frag)
     _lib.call("loom_ffn_decode", code(u), ctypes.byref(desc), S(u))
     if act_frag is not None:
         assert torch.equal(act_frag, _lib.frag_major(act))
