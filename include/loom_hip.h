@@ -208,6 +208,19 @@ typedef struct {
     void* act_frag;            /* optional fragment-major copy of act (fused path, H % 32 == 0) */
     const void* u_frag;        /* optional fragment-major copy of u (head sectors, head_dim and N
                                   multiples of 32): the fused path reads the u sector from it */
+    /* optional: d_h is computed by this call, not read: D = DepthAttn over
+       history slots 0..depth_S-1 (DepthAttn.forward, loomformer.py:3404-3429;
+       as loom_depth_attn_forward, or _rms with depth_rms) is written to d_h.
+       bf16 head sectors with M <= 32 and head_dim 64/96/128 read it inside the
+       launch (each column block recomputes its head's rows, the first block of
+       each head writes them); other cases run the depth launch first. */
+    const void* depth_q;       /* [n_q_heads, head_dim] learned queries of the slot, or NULL */
+    const void* depth_k;       /* history keys (b, slot, head) at b*depth_sbt + slot*depth_ss + head*head_dim */
+    const void* depth_v;
+    int64_t depth_sbt, depth_ss;
+    int32_t depth_S;
+    int32_t depth_rms;         /* nonzero: fixed-RMS q/k/v with the targets below */
+    float depth_qt, depth_kt, depth_vt;
 } loom_ffn_decode_desc;
 
 /* beta = beta_space(u, q, kctx, c, d); (act, s, trace) = paraplex(R, beta);

@@ -35,18 +35,21 @@ struct DepthRms {
     float qt, kt, vt;
 };
 
-template <typename T, int EPL, int C = kDepthChunk, bool RMS = false>
-__device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __restrict__ hk,
-                                          const T* __restrict__ hv, int64_t sbt, int64_t ss,
-                                          T* __restrict__ d_out, T* __restrict__ w_out,
-                                          float* __restrict__ lse_out, int row, int j, int S,
-                                          int QH, float scale, DepthRms rms = DepthRms{}) {
+// The read of row (bt, qh) = (row / QH, row % QH) on lane j of its 16:
+// acc = unnormalised sum of p*v over the S slots, m / l the running max and
+// sum (log2 units), qv the scaled query.  NT: the K/V rows are read once
+// (nontemporal loads); otherwise they stay cached for other readers.
+template <typename T, int EPL, int C, bool RMS, bool NT>
+__device__ __forceinline__ void depth_row_core(const T* __restrict__ q, const T* __restrict__ hk,
+                                               const T* __restrict__ hv, int64_t sbt, int64_t ss,
+                                               int row, int j, int S, int QH, float scale,
+                                               DepthRms rms, float (&qv)[EPL], float (&acc)[EPL],
+                                               float& m, float& l) {
     constexpr int HD = EPL * 16;
     const int qh = row % QH;
     const int bt = row / QH;
     const int d0 = j * EPL;
 
-    float qv[EPL];
     RowIO<T, EPL>::load(q + qh * HD + d0, qv);
     float qs = scale * kLog2e;                              // scores in log2 units
     if constexpr (RMS) qs *= rms_scale<EPL>(qv, rms.qt);
@@ -55,7 +58,8 @@ __device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __re
 
     const T* kp = hk + (int64_t)bt * sbt + qh * HD + d0;
     const T* vp = hv + (int64_t)bt * sbt + qh * HD + d0;
-    float m = -INFINITY, l = 0.0f, acc[EPL];
+    m = -INFINITY;
+    l = 0.0f;
 #pragma unroll
     for (int k = 0; k < EPL; ++k) acc[k] = 0.0f;
 
@@ -66,8 +70,13 @@ __device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __re
 #pragma unroll
         for (int c = 0; c < C; ++c) {
             const int sc_ = s0 + c < S ? s0 + c : S - 1;   // in range; masked below
-            kr[c].load_nt(kp + (int64_t)sc_ * ss);
-            vr[c].load_nt(vp + (int64_t)sc_ * ss);
+            if constexpr (NT) {
+                kr[c].load_nt(kp + (int64_t)sc_ * ss);
+                vr[c].load_nt(vp + (int64_t)sc_ * ss);
+            } else {
+                kr[c].load(kp + (int64_t)sc_ * ss);
+                vr[c].load(vp + (int64_t)sc_ * ss);
+            }
         }
         float sc[C];
 #pragma unroll
@@ -103,6 +112,21 @@ __device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __re
         }
         m = m_new;
     }
+}
+
+template <typename T, int EPL, int C = kDepthChunk, bool RMS = false>
+__device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __restrict__ hk,
+                                          const T* __restrict__ hv, int64_t sbt, int64_t ss,
+                                          T* __restrict__ d_out, T* __restrict__ w_out,
+                                          float* __restrict__ lse_out, int row, int j, int S,
+                                          int QH, float scale, DepthRms rms = DepthRms{}) {
+    constexpr int HD = EPL * 16;
+    const int qh = row % QH;
+    const int bt = row / QH;
+    const int d0 = j * EPL;
+    const T* kp = hk + (int64_t)bt * sbt + qh * HD + d0;
+    float qv[EPL], acc[EPL], m, l;
+    depth_row_core<T, EPL, C, RMS, true>(q, hk, hv, sbt, ss, row, j, S, QH, scale, rms, qv, acc, m, l);
     const float inv_l = 1.0f / l;
 #pragma unroll
     for (int k = 0; k < EPL; ++k) acc[k] *= inv_l;

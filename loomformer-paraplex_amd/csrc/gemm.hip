@@ -18,6 +18,7 @@
 #include <cmath>
 #include <type_traits>
 
+#include "depth_row.h"
 #include "loom_common.h"
 #include "paraplex_math.h"
 #include "tria_math.h"
@@ -512,9 +513,11 @@ gemm_bf16_big_kernel(GemmArgs a) {
 // Main loop of the skinny product for the 16 columns starting at n0: every
 // wave accumulates its k-range, the partial tiles land in red[] (summed by the
 // caller's epilogue after the barrier).
+// dl (gather, head sectors): the D sector comes from LDS rows dl + m*HD.
 template <int MT, bool GATHER, int NW, int UN>
 __device__ __forceinline__ void skinny_mainloop(const GemmArgs& a, int64_t n0,
-                                                float (&red)[NW][MT][4][64]) {
+                                                float (&red)[NW][MT][4][64],
+                                                const uint16_t* dl = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t g = GATHER ? n0 / a.Hq : 0;
     const int fr = lane & 15, fk = (lane >> 4) * 8;
@@ -551,6 +554,8 @@ __device__ __forceinline__ void skinny_mainloop(const GemmArgs& a, int64_t n0,
                         const int64_t ku = k - 3 * a.HD;
                         if (a.Uf != nullptr && ku >= 0 && ku < a.Nm)
                             v = a.Uf[(j * (a.Nm >> 5) + (ku >> 5)) * 64 + (threadIdx.x & 63)];
+                        else if (dl != nullptr && ku >= a.Nm)   // head sectors: D from LDS
+                            v = *reinterpret_cast<const uint4*>(dl + m * a.HD + (ku - a.Nm));
                         else
                             v = *reinterpret_cast<const uint4*>(gather_ptr(a, m, k, g, 2));
                     } else {
@@ -629,6 +634,16 @@ struct FfnArgs {
     float alpha;
     int mode, axis;
     uint16_t* actf;             // fragment-major copy of act, or null
+    // optional depth read of the block's head computed in the launch (head
+    // sectors): D = DepthAttn over history slots 0..dS-1, into LDS for the
+    // gather and, by the first column block of each head, into src[4]
+    const uint16_t* dq;         // [QH, HD] queries of the slot, or null
+    const uint16_t* dk;
+    const uint16_t* dv;
+    int64_t dsbt, dss;
+    int dS;
+    float dscale;
+    DepthRms drms;
 };
 
 __device__ __forceinline__ float bf(uint16_t x) { return bf16_to_f32(x); }
@@ -660,13 +675,52 @@ __device__ __forceinline__ void ffn_tria(const FfnArgs& f, int64_t e, float r, f
     for (int k = 0; k < 9; ++k) f.carry[e * 9 + k] = f32_to_bf16(pre[k]);
 }
 
-template <int MT, int NW, int UN>
+// DE > 0: the depth read is part of the launch (head_dim = 16*DE, DR: fixed-
+// RMS q/k/v); the column blocks of a head then sit on one XCD (block b takes
+// head b % QH, so with 8 heads each XCD's L2 serves one head's history rows to
+// the head's blocks).
+template <int MT, int NW, int UN, int DE = 0, bool DR = false>
 __global__ void __launch_bounds__(NW * 64)
 ffn_decode_kernel(FfnArgs f) {
     __shared__ float red[NW][MT][4][64];
-    const int64_t n0 = (int64_t)blockIdx.x * 16;
-    skinny_mainloop<MT, true, NW, UN>(f.g, n0, red);
+    __shared__ __align__(16) uint16_t dsh[DE > 0 ? MT * 16 * 16 * DE : 8];   // D rows of the head
     const int64_t H = f.g.N;
+    int64_t n0 = (int64_t)blockIdx.x * 16;
+    const int QH = DE > 0 ? (int)(H / f.g.Hq) : 1;
+    const int g = (int)(blockIdx.x % QH), t = (int)(blockIdx.x / QH);
+    if constexpr (DE > 0) n0 = (int64_t)g * f.g.Hq + (int64_t)t * 16;
+    // the depth read of the block's head (before the main loop: with the first
+    // weight loads held across it the 16-wave block runs out of registers)
+    auto depth = [&]() {
+      if constexpr (DE > 0) {
+        const int tid = threadIdx.x;
+        if (tid < f.g.M * 16) {
+            const int b = tid >> 4, j = tid & 15;
+            float qv[DE], acc[DE], m, l;
+            depth_row_core<bf16_t, DE, 4, DR, false>(
+                (const bf16_t*)f.dq, (const bf16_t*)f.dk, (const bf16_t*)f.dv, f.dsbt, f.dss,
+                b * QH + g, j, f.dS, QH, f.dscale, f.drms, qv, acc, m, l);
+            const float inv_l = 1.0f / l;
+            uint16_t o16[DE];
+#pragma unroll
+            for (int k = 0; k < DE; ++k) o16[k] = f32_to_bf16(acc[k] * inv_l);
+#pragma unroll
+            for (int k = 0; k < DE; ++k) dsh[b * 16 * DE + j * DE + k] = o16[k];
+            if (t == 0) {
+                uint16_t* dg = (uint16_t*)f.g.src[4] + (int64_t)b * f.g.Nm + (int64_t)g * 16 * DE + j * DE;
+#pragma unroll
+                for (int k = 0; k < DE; ++k) dg[k] = o16[k];
+            }
+        }
+        __syncthreads();
+      }
+    };
+    if constexpr (DE > 0) {
+        depth();
+        skinny_mainloop<MT, true, NW, UN>(f.g, n0, red, dsh);
+    } else {
+        skinny_mainloop<MT, true, NW, UN>(f.g, n0, red);
+    }
     for (int o = threadIdx.x; o < MT * 256; o += NW * 64) {
         const int nn = o & 15, mi = o >> 4;
         const int64_t m = mi, h = n0 + nn;
@@ -1350,13 +1404,38 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
 
 extern "C" int64_t loom_ffn_decode_desc_bytes(void) { return (int64_t)sizeof(loom_ffn_decode_desc); }
 
-template <int MT>
+template <int MT, int DE = 0, bool DR = false>
 static void launch_ffn_mt(const FfnArgs& f, dim3 grid, hipStream_t st) {
     int nw, un;
     skinny_shape(ceil_div(f.g.K, 32), MT, nw, un);
-    if (nw == 4) hipLaunchKernelGGL((ffn_decode_kernel<MT, 4, 4>), grid, dim3(256), 0, st, f);
-    else if (nw == 8) hipLaunchKernelGGL((ffn_decode_kernel<MT, 8, 4>), grid, dim3(512), 0, st, f);
-    else if constexpr (MT <= 3) hipLaunchKernelGGL((ffn_decode_kernel<MT, 16, 4>), grid, dim3(1024), 0, st, f);
+    if (nw == 4) hipLaunchKernelGGL((ffn_decode_kernel<MT, 4, 4, DE, DR>), grid, dim3(256), 0, st, f);
+    else if (nw == 8) hipLaunchKernelGGL((ffn_decode_kernel<MT, 8, 4, DE, DR>), grid, dim3(512), 0, st, f);
+    else if constexpr (MT <= 3) hipLaunchKernelGGL((ffn_decode_kernel<MT, 16, 4, DE, DR>), grid, dim3(1024), 0, st, f);
+}
+
+// The depth read fused into the launch: rows <= 32 (MT <= 2), head_dim 64/96/128.
+template <int MT>
+static bool launch_ffn_depth(const FfnArgs& f, dim3 grid, bool rms, hipStream_t st) {
+    if constexpr (MT <= 2) {
+        switch (f.g.HD) {
+            case 64: rms ? launch_ffn_mt<MT, 4, true>(f, grid, st) : launch_ffn_mt<MT, 4, false>(f, grid, st); return true;
+            case 96: rms ? launch_ffn_mt<MT, 6, true>(f, grid, st) : launch_ffn_mt<MT, 6, false>(f, grid, st); return true;
+            case 128: rms ? launch_ffn_mt<MT, 8, true>(f, grid, st) : launch_ffn_mt<MT, 8, false>(f, grid, st); return true;
+        }
+    }
+    return false;
+}
+
+// The depth read of an ffn_decode descriptor as its own launch, into d_h.
+static int ffn_depth_launch(int dtype, const loom_ffn_decode_desc* d, void* stream) {
+    if (d->depth_rms != 0)
+        return loom_depth_attn_forward_rms(dtype, d->depth_q, d->depth_k, d->depth_v, d->depth_sbt,
+                                           d->depth_ss, (void*)d->d_h, nullptr, nullptr, d->M,
+                                           d->depth_S, d->n_q_heads, d->head_dim, d->depth_qt,
+                                           d->depth_kt, d->depth_vt, stream);
+    return loom_depth_attn_forward(dtype, d->depth_q, d->depth_k, d->depth_v, d->depth_sbt,
+                                   d->depth_ss, (void*)d->d_h, nullptr, nullptr, d->M, d->depth_S,
+                                   d->n_q_heads, d->head_dim, stream);
 }
 
 extern "C" int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* d, void* stream) {
@@ -1376,6 +1455,11 @@ extern "C" int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* d, void* s
     const int64_t want = d->open_sectors ? 4 * d->N + d->head_dim : d->N + 4 * d->head_dim;
     LOOM_CHECK(d->imag_in == want, "ffn_decode: imag_in=%lld, expected %lld", (long long)d->imag_in,
                (long long)want);
+    LOOM_CHECK(d->depth_q == nullptr || (d->depth_k && d->depth_v && d->depth_S >= 1 &&
+                                         d->depth_ss >= d->N && d->depth_sbt >= d->depth_S * d->depth_ss),
+               "ffn_decode: depth read needs k/v history, S >= 1 and non-overlapping strides");
+    LOOM_CHECK(d->depth_rms == 0 || (d->depth_qt > 0.0f && d->depth_kt > 0.0f && d->depth_vt > 0.0f),
+               "ffn_decode: fixed-RMS depth targets must be > 0");
     if (d->M == 0) return LOOM_OK;
     const uintptr_t al = (uintptr_t)d->u | (uintptr_t)d->q_h | (uintptr_t)d->k_ctx_h |
                          (uintptr_t)d->c_h | (uintptr_t)d->d_h | (uintptr_t)d->w_compact;
@@ -1405,6 +1489,25 @@ extern "C" int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* d, void* s
         a.Uf = (const uint4*)d->u_frag;
         const dim3 grid((unsigned)ceil_div(d->H, 16));
         hipStream_t st = (hipStream_t)stream;
+        if (d->depth_q != nullptr) {
+            // the depth read D of this sublayer: in the launch when it can be, else its own
+            // launch first (D then comes from d_h as usual)
+            const bool rms = d->depth_rms != 0;
+            const bool fusable = !d->open_sectors && d->M <= 32 && d->H % 16 == 0 &&
+                                 d->depth_sbt % 2 == 0 && d->depth_ss % 2 == 0 &&
+                                 ((((uintptr_t)d->depth_q | (uintptr_t)d->depth_k | (uintptr_t)d->depth_v) & 7) == 0);
+            if (fusable) {
+                f.dq = (const uint16_t*)d->depth_q; f.dk = (const uint16_t*)d->depth_k;
+                f.dv = (const uint16_t*)d->depth_v; f.dsbt = d->depth_sbt; f.dss = d->depth_ss;
+                f.dS = d->depth_S; f.dscale = 1.0f / sqrtf((float)d->head_dim);
+                f.drms = DepthRms{d->depth_qt, d->depth_kt, d->depth_vt};
+                const bool done = d->M <= 16 ? launch_ffn_depth<1>(f, grid, rms, st)
+                                             : launch_ffn_depth<2>(f, grid, rms, st);
+                if (done) return launch_status("loom_ffn_decode");
+            }
+            const int rc = ffn_depth_launch(dtype, d, stream);
+            if (rc != LOOM_OK) return rc;
+        }
         switch ((int)ceil_div(d->M, 16)) {
             case 1: launch_ffn_mt<1>(f, grid, st); break;
             case 2: launch_ffn_mt<2>(f, grid, st); break;
@@ -1414,6 +1517,10 @@ extern "C" int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* d, void* s
         return launch_status("loom_ffn_decode");
     }
     LOOM_CHECK(d->beta && d->s, "ffn_decode: the unfused path needs the beta and s buffers");
+    if (d->depth_q != nullptr) {
+        const int rc0 = ffn_depth_launch(dtype, d, stream);
+        if (rc0 != LOOM_OK) return rc0;
+    }
     LOOM_CHECK(d->act_frag == nullptr, "ffn_decode: act_frag needs the fused bf16 path (M <= 64, aligned)");
     // (u_frag is only read, and u holds the same values: the unfused path reads u)
     int rc = loom_beta_forward(dtype, d->u, d->q_h, d->k_ctx_h, d->c_h, d->d_h, d->w_compact,

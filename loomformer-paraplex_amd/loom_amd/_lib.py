@@ -169,7 +169,10 @@ class FfnDecodeDesc(ctypes.Structure):
                 ("carry_prev", c_void_p), ("seed", c_void_p), ("seed_valid", c_void_p),
                 ("gate_w", c_void_p), ("carry_out", c_void_p), ("p_out", c_void_p),
                 ("alpha", c_float), ("axis", ctypes.c_int32), ("act_frag", c_void_p),
-                ("u_frag", c_void_p)]
+                ("u_frag", c_void_p), ("depth_q", c_void_p), ("depth_k", c_void_p),
+                ("depth_v", c_void_p), ("depth_sbt", c_int64), ("depth_ss", c_int64),
+                ("depth_S", ctypes.c_int32), ("depth_rms", ctypes.c_int32), ("depth_qt", c_float),
+                ("depth_kt", c_float), ("depth_vt", c_float)]
 
 
 def linear_multi_desc(x, segments, x2=None, m=None, only_if=None, x_frag=None, x2_frag=None):

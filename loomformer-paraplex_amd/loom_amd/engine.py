@@ -313,7 +313,6 @@ class LoomDecoder:
             if c.gate_proj:
                 segs.append(dict(w=blk["gpw"], out=self.G, bias=blk["gpb"]))
             self._multi(("kvr", bi), self.h, segs, x_frag=self.h_frag)
-            self.depth_read(sub, self.hist, self.dh, B)
             # ---- Paraplex FFN core (beta space, fused pointwise chain; loomformer.py:
             # 2818-2893, :2533-2560) and the Tria depth op (loomformer.py:4012-4040,
             # axis = bi % 3) of this token, one launch in bf16
@@ -337,7 +336,14 @@ class LoomDecoder:
                     gate_w=blk["gate_w"] if gate else None, carry_out=self.carry[out_i],
                     p_out=self.p[new_p] if gate else None, alpha=float(c.tria_alpha), axis=bi % 3,
                     act_frag=self.act_frag,
-                    u_frag=self.h_frag if (c.sectors != "open" and c.HD % 32 == 0) else None)
+                    u_frag=self.h_frag if (c.sectors != "open" and c.HD % 32 == 0) else None,
+                    # the depth read of history slot `sub` (loomformer.py:4004-4006), d_h,
+                    # computed by this launch
+                    depth_q=self.qp[sub], depth_k=self.hist, depth_v=self.hist[:, :, N:],
+                    depth_sbt=2 * L * 2 * N, depth_ss=2 * N, depth_S=sub + 1,
+                    depth_rms=0 if self.depth_rms is None else 1,
+                    **({} if self.depth_rms is None else
+                       dict(zip(("depth_qt", "depth_kt", "depth_vt"), self.depth_rms))))
                 self._descs[key] = d
             self._call("loom_ffn_decode", self.code, _lib.ctypes.byref(d), st)
             carry_i, p_i = out_i, new_p

@@ -504,6 +504,61 @@ def test_ffn_decode(dtype, mode, gate, axis, gsrc):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("M,rms,slots", [(32, False, 4), (32, True, 11), (9, False, 20), (40, False, 7)])
+def test_ffn_decode_with_depth_read(dtype, M, rms, slots):
+    """ffn_decode computing its own d_h: the depth read of history slot S-1
+    (DepthAttn over slots 0..S-1, fixed-RMS q/k/v with rms) inside the launch
+    (bf16, M <= 32) or as a launch before it (fp32, M > 32).  d_h against the
+    oracle's depth read, the FFN outputs against the oracle fed with that d_h."""
+    from loom_amd import _lib
+    from oracle.model import fixed_rms
+    g = torch.Generator().manual_seed(M * 7 + slots + (3 if rms else 0))
+    QH, HD, H, L2 = 8, 96, 3072, 20
+    N = QH * HD
+    K = N + 4 * HD
+    r = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(DEV, dtype)
+    u = r(M, N)
+    q, kc, c = (r(M, QH, HD) for _ in range(3))
+    d = torch.full((M, QH, HD), float("nan"), device=DEV, dtype=dtype)   # written by the call
+    hist = r(M, L2, 2 * N, sc=2.0)
+    dq = r(QH, HD, sc=0.5)
+    w = r(H, K, sc=K ** -0.5)
+    R = r(M, H, sc=2.0)
+    ib = (torch.randn(H, generator=g) * 0.3).to(DEV)
+    tw = (torch.rand(H, generator=g) - 0.5).to(DEV)
+    trace0 = r(M, H, sc=0.5)
+    trace = trace0.clone()
+    prev = ref.local_normalize(torch.randn(M, H, 3, 3, generator=g)).to(DEV, dtype)
+    gw = torch.softmax(torch.randn(9, generator=g), 0).to(DEV, dtype)
+    act, s, beta = (torch.empty(M, H, device=DEV, dtype=dtype) for _ in range(3))
+    carry = torch.empty(M, H, 3, 3, device=DEV, dtype=dtype)
+    p = torch.empty(M, H, device=DEV, dtype=dtype)
+    tg = (0.88 / HD ** 0.5, 0.88, 0.88 * 0.4)
+    desc = _lib.ffn_decode_desc(
+        u=u, q_h=q, k_ctx_h=kc, c_h=c, d_h=d, w_compact=w, M=M, N=N, H=H, imag_in=K,
+        hidden_per_q_head=H // QH, head_dim=HD, n_q_heads=QH, open_sectors=0,
+        p_real=R, gate_src=None, imag_bias=ib, trace=trace, trace_w=tw, powlu_m=3.0, act=act, s=s,
+        beta=beta, carry_prev=prev, seed=None, seed_valid=None, gate_w=gw, carry_out=carry, p_out=p,
+        alpha=0.0375, axis=1, depth_q=dq, depth_k=hist, depth_v=hist[:, :, N:],
+        depth_sbt=L2 * 2 * N, depth_ss=2 * N, depth_S=slots, depth_rms=1 if rms else 0,
+        **(dict(zip(("depth_qt", "depth_kt", "depth_vt"), tg)) if rms else {}))
+    _lib.call("loom_ffn_decode", code(u), ctypes.byref(desc), S(u))
+    hk = host(hist)[:, :slots, :N].reshape(M, slots, QH, HD)
+    hv = host(hist)[:, :slots, N:].reshape(M, slots, QH, HD)
+    qd = host(dq)
+    if rms:
+        qd, hk, hv = fixed_rms(qd, tg[0]), fixed_rms(hk, tg[1]), fixed_rms(hv, tg[2])
+    want_d, _, _ = ref.depth_attn_softmax(qd, hk[:, None], hv[:, None])
+    check(d, want_d[:, 0], dtype)
+    be = ref.beta_space_grouped(host(u)[:, None], host(q)[:, None], host(kc)[:, None],
+                                host(c)[:, None], host(d)[:, None], host(w), QH, HD, "head")
+    wa, ws_, wt = ref.paraplex_pointwise(host(R)[:, None], host(R)[:, None], be, host(ib),
+                                         host(trace0), host(tw), None, 3.0)
+    check(act, wa[:, 0], dtype)
+    check(trace, wt, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("M,K2", [(1, 768), (32, 768), (32, 3072), (64, 3072), (7, 0)])
 def test_linear_ln(dtype, M, K2):
     """LayerNorm(x w^T + x2 w2^T + b): split-K partial sums reduced inside the
