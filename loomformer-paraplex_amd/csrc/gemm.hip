@@ -911,6 +911,64 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ fp32 GEMV (M <= 8)
+// Decode-shaped fp32 products: one wave per output column n, its lanes stride
+// the row of W in 16-byte pieces (4 in flight per lane) against the MR
+// activation rows, a wave reduction per row, the epilogue on lane 0.  The
+// weight row is read once, whole lines at a time.
+template <int MR, bool GATHER>
+__global__ void __launch_bounds__(256)
+gemv_f32_kernel(GemmArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= a.N) return;                         // whole wave
+    const int64_t g = GATHER ? n / a.Hq : 0;
+    const float* W = (const float*)a.W + n * a.ldw;
+    const float* X = (const float*)a.X;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
+    constexpr int U = 4;
+    for (int64_t k0 = 4 * lane; k0 < a.K; k0 += 256 * U) {
+        float4 w[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t k = k0 + 256 * u;
+            w[u] = k < a.K ? *reinterpret_cast<const float4*>(W + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            if (m >= a.M) break;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t k = k0 + 256 * u;
+                if (k >= a.K) break;
+                float4 x;
+                if constexpr (GATHER)
+                    x = *reinterpret_cast<const float4*>(gather_ptr(a, m, k, g, 4));
+                else
+                    x = *reinterpret_cast<const float4*>(X + m * a.ldx + k);
+                acc[m] = fmaf(w[u].x, x.x, fmaf(w[u].y, x.y, fmaf(w[u].z, x.z, fmaf(w[u].w, x.w, acc[m]))));
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        if (m >= a.M) break;
+        const float v = wave_sum(acc[m]);
+        if (lane == 0) ((float*)a.out)[m * a.ldc + n] = epilogue<float>(a, m, n, v);
+    }
+}
+
+template <bool GATHER>
+static void launch_gemv_f32(const GemmArgs& a, hipStream_t st) {
+    const dim3 grid((unsigned)ceil_div(a.N, 4));
+    if (a.M <= 1) hipLaunchKernelGGL((gemv_f32_kernel<1, GATHER>), grid, dim3(256), 0, st, a);
+    else if (a.M <= 2) hipLaunchKernelGGL((gemv_f32_kernel<2, GATHER>), grid, dim3(256), 0, st, a);
+    else if (a.M <= 4) hipLaunchKernelGGL((gemv_f32_kernel<4, GATHER>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((gemv_f32_kernel<8, GATHER>), grid, dim3(256), 0, st, a);
+}
+
 // ------------------------------------------------------------------ SIMT
 
 constexpr int SB_M = 64, SB_N = 64, SB_K = 16;
@@ -1058,6 +1116,21 @@ static int run_gemm(const GemmArgs& a, hipStream_t st, const char* what) {
         if (ok) {
             dim3 grid((unsigned)ceil_div(a.N, MB_N), (unsigned)ceil_div(a.M, MB_M));
             hipLaunchKernelGGL((gemm_bf16_mfma_kernel<GATHER>), grid, dim3(256), 0, st, a);
+            return launch_status(what);
+        }
+    }
+    if constexpr (std::is_same<T, float>::value) {
+        // few rows: the fp32 GEMV (16-byte pieces: K, ldw, ldx multiples of 4, aligned bases;
+        // gather pieces stay inside one sector: head_dim and the model width multiples of 4)
+        bool gv = a.M <= 8 && a.K % 4 == 0 && a.ldw % 4 == 0 && ((uintptr_t)a.W & 15) == 0;
+        if (GATHER)
+            gv = gv && a.HD % 4 == 0 && a.Nm % 4 == 0 &&
+                 ((uintptr_t)a.src[0] | (uintptr_t)a.src[1] | (uintptr_t)a.src[2] |
+                  (uintptr_t)a.src[3] | (uintptr_t)a.src[4]) % 16 == 0;
+        else
+            gv = gv && a.ldx % 4 == 0 && ((uintptr_t)a.X & 15) == 0;
+        if (gv) {
+            launch_gemv_f32<GATHER>(a, st);
             return launch_status(what);
         }
     }

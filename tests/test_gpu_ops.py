@@ -186,7 +186,7 @@ def test_golden_phase_and_pvpowlu_vs_reference():
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("M,N,K", [(1, 16, 8), (37, 100, 72), (32, 3072, 768), (130, 768, 3072),
-                                   (256, 256, 1152), (5, 4096, 768),
+                                   (256, 256, 1152), (5, 4096, 768), (3, 768, 3072), (8, 1000, 772),
                                    # the large-M MFMA tiles 256x128, 128x128 and 128x64, ragged
                                    (8229, 3000, 768), (6000, 1536, 1152), (4100, 770, 3072)])
 def test_linear(dtype, M, N, K):
@@ -208,7 +208,8 @@ def test_linear(dtype, M, N, K):
 @pytest.mark.parametrize("QH,HD,Hq,M,sectors", [(4, 8, 32, 10, "head"), (8, 96, 384, 40, "head"),
                                                  (8, 96, 384, 300, "head"), (4, 8, 32, 6, "open"),
                                                  (8, 96, 384, 20, "open"), (8, 96, 384, 8200, "head"),
-                                                 (8, 96, 384, 600, "open")])
+                                                 (8, 96, 384, 600, "open"), (8, 96, 384, 1, "head"),
+                                                 (4, 8, 32, 3, "open")])
 def test_beta_forward(dtype, QH, HD, Hq, M, sectors):
     from loom_amd import ops
     N, H = QH * HD, QH * Hq
