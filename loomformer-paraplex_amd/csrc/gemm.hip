@@ -215,8 +215,10 @@ gemm_bf16_mfma_kernel(GemmArgs a) {
 // requested while t is computed.
 //
 // LDS layout of a stage: [k-half h][row][4 chunks of 8 k] (64 B rows), chunk c
-// of row r stored at position c ^ ((r >> 2) & 3), so the 16-row fragment
-// reads spread over the banks.  One DMA instruction of a wave fills 16 rows of
+// of row r stored at position c ^ bg_swz(r) (r bits 1-2, flipped by bit 3), so
+// a 16-byte fragment read is conflict-free both 8 lanes at a time over 128 B
+// of banks and 16 lanes over 256 B (with (r >> 2) & 3 rows r and r+2 shared
+// banks: 50% of the LDS cycles were conflicts).  One DMA instruction of a wave fills 16 rows of
 // one k-half (lane l: row l/4, position l%4; the lane fetches the chunk the
 // swizzle puts there), so its 32 k lie in one gather sector and the source
 // and column offset are uniform (scalar) per instruction; per lane only a
@@ -224,6 +226,7 @@ gemm_bf16_mfma_kernel(GemmArgs a) {
 // scalar soffset.  Requires K % 192 == 0 (whole rounds of the three stages);
 // 144 KB of LDS, one block per CU.
 constexpr int BG_M = 256, BG_N = 128, BG_K = 64;
+__host__ __device__ constexpr int bg_swz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 constexpr int BG_WAVES = 8, BG_WGM = 4;                    // waves along m; BG_WAVES / BG_WGM along n
 constexpr int BG_WTM = BG_M / BG_WGM, BG_WTN = BG_N / (BG_WAVES / BG_WGM);   // 64 x 64 per wave
 constexpr int BG_FJ = BG_WTM / 16, BG_FI = BG_WTN / 16;    // x and w fragments per k-step
@@ -294,20 +297,20 @@ gemm_bf16_big_kernel(GemmArgs a) {
 
     // DMA slots: X 16-row groups BG_XG*wave + q, W groups BG_WG*wave + q, each
     // for both k-halves; lane: row 16*group + lane/4, chunk (lane%4) ^
-    // ((row >> 2) & 3); rows past M / N read the last row (their results are
-    // not stored)
+    // bg_swz(row); rows past M / N read the last row (their results are not
+    // stored)
     uint32_t xv[BG_XG], wv[BG_WG];
 #pragma unroll
     for (int q = 0; q < BG_XG; ++q) {
         const int r = 16 * (BG_XG * wave + q) + (lane >> 2);
         const int64_t rr = m0 + r < a.M ? r : a.M - 1 - m0;
-        xv[q] = (uint32_t)((rr * ldx + 8 * ((lane & 3) ^ ((r >> 2) & 3))) * 2);
+        xv[q] = (uint32_t)((rr * ldx + 8 * ((lane & 3) ^ bg_swz(r))) * 2);
     }
 #pragma unroll
     for (int q = 0; q < BG_WG; ++q) {
         const int r = 16 * (BG_WG * wave + q) + (lane >> 2);
         const int64_t rr = n0 + r < a.N ? r : a.N - 1 - n0;
-        wv[q] = (uint32_t)((rr * a.ldw + 8 * ((lane & 3) ^ ((r >> 2) & 3))) * 2);
+        wv[q] = (uint32_t)((rr * a.ldw + 8 * ((lane & 3) ^ bg_swz(r))) * 2);
     }
     const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint16_t*)a.W + n0 * a.ldw),
                                                       (short)0, 0x7fffffff, kBufferDword3);
@@ -344,9 +347,10 @@ gemm_bf16_big_kernel(GemmArgs a) {
         for (int j = 0; j < BG_FJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // fragment of k-step kk: row base + 16*i + fr of half kk, chunk fc at its
-    // swizzled position ((row >> 2) & 3 = (fr >> 2) & 3 for every tile)
+    // swizzled position (bg_swz(row) = bg_swz(fr) for every tile: bases are
+    // multiples of 16)
     const int fr = lane & 15, fc = lane >> 4;
-    const int lo = fr * 32 + ((fc ^ ((fr >> 2) & 3)) << 3);
+    const int lo = fr * 32 + ((fc ^ bg_swz(fr)) << 3);
     struct Frags {
         bf16x8 w[BG_FI], x[BG_FJ];
     };
