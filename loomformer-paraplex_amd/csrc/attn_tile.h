@@ -1,0 +1,47 @@
+// Row-major K / V tiles in LDS for the MFMA attention kernels (decode and
+// prefill): 16-byte pieces of each row stored swizzled, read back as the A
+// operand of S^T = K Q^T (16-byte reads of whole rows) and, through the gfx950
+// transposing LDS read, as the B operand of C = P V and Kctx = P K.
+#pragma once
+
+#include "loom_common.h"
+
+namespace loom {
+
+// Piece swizzle: piece c of row r sits at c ^ kv_swz(r) (bits 1, 2 of r to
+// bits 1, 0), so the 8 rows of a 16-byte fragment read and the 4 rows x 32 B
+// of a transposing read fall in distinct banks.  The pieces of a row stay a
+// permutation of 0..HD/8-1.
+__device__ __forceinline__ int kv_swz(int r) { return (((r >> 1) & 1) << 1) | ((r >> 2) & 1); }
+
+typedef short gqa_v4s __attribute__((ext_vector_type(4)));
+typedef uint32_t gqa_u4 __attribute__((ext_vector_type(4)));   // a 16-byte piece as a native vector
+
+// B fragment of 32 positions x 16 dims (dims 16*dt..) from a row-major tile:
+// lane l gets positions 8*(l/16)..+7 of dim 16*dt + l%16, as two transposing
+// 8-byte reads (lane r of a 16-lane group points at row k0 + r/4, dims
+// 16*dt + 4*(r%4)..+3 and receives rows k0..k0+3 of dim 16*dt + r).
+template <int CPR>
+__device__ __forceinline__ uint4 tile_tr_frag(const gqa_u4* tile, int dt, int lq, int lr) {
+    uint32_t w[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int row = 8 * lq + 4 * h + (lr >> 2);
+        const int c = 2 * dt + ((lr & 3) >> 1);
+        const char* p = reinterpret_cast<const char*>(tile + row * CPR + (c ^ kv_swz(row))) + 8 * (lr & 1);
+        const gqa_v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) gqa_v4s*)(p));
+        w[2 * h] = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
+        w[2 * h + 1] = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// LDS ordering inside one wave (its LDS operations execute in order): keeps
+// the compiler from moving LDS accesses across; no wait, no s_barrier.
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+}  // namespace loom

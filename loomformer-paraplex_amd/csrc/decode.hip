@@ -4,6 +4,7 @@
 #include <cmath>
 #include <type_traits>
 
+#include "attn_tile.h"
 #include "loom_common.h"
 #include "depth_row.h"
 
@@ -441,45 +442,9 @@ __device__ __forceinline__ void rope8(const bf16_t* head, const float* cr, const
 // Cache policy of the K / V stream loads (2: nontemporal; 0: default).
 constexpr int kKvLoadPolicy = 2;
 
-// Piece swizzle of the row-major K / V tiles: piece c of row r sits at
-// c ^ kv_swz(r) (bits 1, 2 of r to bits 1, 0), so the 8 rows of a 16-byte
-// fragment read and the 4 rows x 32 B of a transposing read fall in distinct
-// banks.  The pieces of a row stay a permutation of 0..HD/8-1.
-__device__ __forceinline__ int kv_swz(int r) { return (((r >> 1) & 1) << 1) | ((r >> 2) & 1); }
-
-typedef short gqa_v4s __attribute__((ext_vector_type(4)));
-typedef uint32_t gqa_u4 __attribute__((ext_vector_type(4)));   // a 16-byte piece as a native vector
-
 __device__ __forceinline__ f32x4_t mfma16(gqa_u4 a, uint4 b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
-
-// B fragment of 32 positions x 16 dims (dims 16*dt..) from a row-major tile:
-// lane l gets positions 8*(l/16)..+7 of dim 16*dt + l%16, as two transposing
-// 8-byte reads (lane r of a 16-lane group points at row k0 + r/4, dims
-// 16*dt + 4*(r%4)..+3 and receives rows k0..k0+3 of dim 16*dt + r).
-template <int CPR>
-__device__ __forceinline__ uint4 tile_tr_frag(const gqa_u4* tile, int dt, int lq, int lr) {
-    uint32_t w[4];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int row = 8 * lq + 4 * h + (lr >> 2);
-        const int c = 2 * dt + ((lr & 3) >> 1);
-        const char* p = reinterpret_cast<const char*>(tile + row * CPR + (c ^ kv_swz(row))) + 8 * (lr & 1);
-        const gqa_v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) gqa_v4s*)(p));
-        w[2 * h] = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
-        w[2 * h + 1] = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
-    }
-    return make_uint4(w[0], w[1], w[2], w[3]);
-}
-
-// LDS ordering inside one wave (its LDS operations execute in order): keeps
-// the compiler from moving LDS accesses across; no wait, no s_barrier.
-__device__ __forceinline__ void wave_lds_fence() {
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    __builtin_amdgcn_wave_barrier();
 }
 
 // Each wave takes 32 positions at a time.  Their K and V rows are loaded as

@@ -20,6 +20,7 @@
 // block per (token, kv head).
 #include <cmath>
 
+#include "attn_tile.h"
 #include "loom_common.h"
 
 namespace loom {
@@ -215,15 +216,23 @@ gqa_prefill_kernel(PrefillArgs<T> a) {
 // ------------------------------------------------------------------ MFMA form (bf16)
 // v_mfma_f32_16x16x32_bf16 (A: 16 rows x 32 k, B: 32 k x 16 columns; lane l
 // holds row/column l%16, k = 8*(l/16)..+7; result [4*(l/16)+r][l%16] in r):
-//   S^T = K Q^T   A = 16 cached rows as stored, B = 16 query positions of one head
+//   S^T = K Q^T   A = 16 cached rows (16-byte reads of the row-major K tile),
+//                 B = 16 query positions of one head
 //   C   = P V     A = P (rows = query positions, k = 32 cached rows, bf16),
-//   Kctx= P K     B = V / K transposed through LDS.
+//   Kctx= P K     B = V / K through the transposing LDS read (attn_tile.h).
 // Block (x, y, b): y = kvh * HSPLIT + part; wave w takes head
 // kvh*G + part*GP + w%GP and query tile x*QTB + w/GP (16 positions each).
+// The block streams 32 cached rows per step into two LDS buffers: the next
+// tile's loads are in flight while a tile is computed and land in the other
+// buffer, one block barrier per step.
 typedef __bf16 bf16x8_p __attribute__((ext_vector_type(8)));
 typedef float f32x4_p __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x4_p mfma16p(uint4 x, uint4 y, f32x4_p c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_p, x),
+                                                   __builtin_bit_cast(bf16x8_p, y), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_p mfma16p(gqa_u4 x, uint4 y, f32x4_p c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_p, x),
                                                    __builtin_bit_cast(bf16x8_p, y), c, 0, 0, 0);
 }
@@ -241,13 +250,13 @@ __global__ void __launch_bounds__(256)
 gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     constexpr int KK = HD / 32;
     constexpr int DT = HD / 16;
+    constexpr int CPR = HD / 8;                 // 16-byte pieces per row
     constexpr int QTB = 4 / GP;                 // query tiles per block
     constexpr int G = GP * HSPLIT;
-    constexpr int PIECES = kPfRows * HD / 8;    // 16-byte pieces of one 32-row tile
+    constexpr int PIECES = kPfRows * CPR;       // pieces of one tensor's 32-row tile
     constexpr int PPT = (2 * PIECES + 255) / 256;
-    __shared__ __align__(16) uint16_t kn[kPfRows][HD];   // K rows as stored
-    __shared__ __align__(16) uint16_t kt[HD][kPfRows];   // K transposed
-    __shared__ __align__(16) uint16_t vt[HD][kPfRows];   // V transposed
+    __shared__ __align__(16) gqa_u4 tk[2][PIECES];       // K tile, row-major, two buffers
+    __shared__ __align__(16) gqa_u4 tv[2][PIECES];       // V tile
     __shared__ __align__(16) uint16_t pt[4][16][kPfRows];
     __shared__ float cr[4][16];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -268,40 +277,31 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
 
     const bf16_t* kb = a.kc + b * a.csb + kvh * a.csh;
     const bf16_t* vb = a.vc + b * a.csb + kvh * a.csh;
-    // one 32-row tile: piece p -> (tensor, row, 8-dim chunk), rows clamped to kmax
-    uint4 reg[PPT];
+    // one 32-row tile: piece p -> (tensor, row, piece of the row), rows clamped to kmax
+    gqa_u4 reg[PPT];
     auto load_tile = [&](int64_t r0) {
 #pragma unroll
         for (int u = 0; u < PPT; ++u) {
             const int p = tid + 256 * u;
             if (p < 2 * PIECES) {
                 const int tensor = p / PIECES, q = p % PIECES;
-                const int row = q / (HD / 8), ch = q % (HD / 8);
+                const int row = q / CPR, ch = q % CPR;
                 int64_t r = r0 + row;
                 r = r <= kmax ? r : kmax;
                 const bf16_t* src = (tensor == 0 ? kb : vb) + r * a.cst + 8 * ch;
-                reg[u] = *reinterpret_cast<const uint4*>(src);
+                reg[u] = *reinterpret_cast<const gqa_u4*>(src);
             }
         }
     };
-    auto store_tile = [&]() {
+    auto store_tile = [&](int buf) {
 #pragma unroll
         for (int u = 0; u < PPT; ++u) {
             const int p = tid + 256 * u;
             if (p < 2 * PIECES) {
                 const int tensor = p / PIECES, q = p % PIECES;
-                const int row = q / (HD / 8), ch = q % (HD / 8);
-                const uint32_t w[4] = {reg[u].x, reg[u].y, reg[u].z, reg[u].w};
-                if (tensor == 0) {
-                    *reinterpret_cast<uint4*>(&kn[row][8 * ch]) = reg[u];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        kt[8 * ch + e][row] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        vt[8 * ch + e][row] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
-                }
+                const int row = q / CPR, ch = q % CPR;
+                gqa_u4* dst = tensor == 0 ? tk[buf] : tv[buf];
+                dst[row * CPR + (ch ^ kv_swz(row))] = reg[u];
             }
         }
     };
@@ -315,7 +315,7 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
         for (int kk = 0; kk < KK; ++kk)
             qf[kk] = *reinterpret_cast<const uint4*>(qp + 32 * kk + 8 * lq);
     }
-    store_tile();
+    store_tile(0);
     lds_sync();
 
     float mh = -INFINITY, lh = 0.0f;      // running max / sum of query column lr
@@ -324,6 +324,7 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     for (int dt = 0; dt < DT; ++dt) accC[dt] = accK[dt] = f32x4_p{0.f, 0.f, 0.f, 0.f};
 
     for (int it = 0; it < nsteps; ++it) {
+        const int cur = it & 1;
         const int64_t r0 = (int64_t)it * kPfRows;
         if (it + 1 < nsteps) load_tile(r0 + kPfRows);
         const bool active = r0 <= wave_kmax;                 // wave-uniform
@@ -332,11 +333,10 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
                 sc[hf] = f32x4_p{0.f, 0.f, 0.f, 0.f};
+                const int row = 16 * hf + lr;
 #pragma unroll
-                for (int kk = 0; kk < KK; ++kk) {
-                    const uint4 ka = *reinterpret_cast<const uint4*>(&kn[16 * hf + lr][32 * kk + 8 * lq]);
-                    sc[hf] = mfma16p(ka, qf[kk], sc[hf]);
-                }
+                for (int kk = 0; kk < KK; ++kk)
+                    sc[hf] = mfma16p(tk[cur][row * CPR + ((4 * kk + lq) ^ kv_swz(row))], qf[kk], sc[hf]);
             }
             // S^T[row 16*hf + 4*lq + r][query column lr]
             float sv[2][4];
@@ -367,9 +367,7 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
             lh = fmaf(lh, corr, ls);
             mh = mnew;
             if (lq == 0) cr[wave][lr] = corr;
-        }
-        lds_sync();
-        if (active) {
+            wave_lds_fence();                  // P and the rescale of this wave
             float cf[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) cf[r] = cr[wave][4 * lq + r];
@@ -381,17 +379,15 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
                     accC[dt][r] *= cf[r];
                     accK[dt][r] *= cf[r];
                 }
-                const uint4 vbf = *reinterpret_cast<const uint4*>(&vt[16 * dt + lr][8 * lq]);
-                const uint4 kbf = *reinterpret_cast<const uint4*>(&kt[16 * dt + lr][8 * lq]);
-                accC[dt] = mfma16p(pa, vbf, accC[dt]);
-                accK[dt] = mfma16p(pa, kbf, accK[dt]);
+                accC[dt] = mfma16p(pa, tile_tr_frag<CPR>(tv[cur], dt, lq, lr), accC[dt]);
+                accK[dt] = mfma16p(pa, tile_tr_frag<CPR>(tk[cur], dt, lq, lr), accK[dt]);
             }
+            wave_lds_fence();                  // pt / cr are rewritten next step
         }
-        lds_sync();                            // every wave is done with this tile
-        if (it + 1 < nsteps) {
-            store_tile();
-            lds_sync();
-        }
+        // the next tile into the other buffer (last read two steps ago, before
+        // the previous barrier), then one barrier for both
+        if (it + 1 < nsteps) store_tile(cur ^ 1);
+        lds_sync();
     }
     // normalise: the sum of query column c lives in lanes with lr == c
     if (lq == 0) cr[wave][lr] = lh;
