@@ -136,6 +136,48 @@ def test_gqa_decode_attention(dtype, B, QH, KVH, HD, length):
     check(kx, (a @ K).squeeze(2), dtype)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,QH,KVH,HD,start,Tc", [(2, 8, 2, 96, 0, 128), (3, 8, 2, 96, 300, 70),
+                                                  (2, 4, 1, 64, 64, 33), (2, 8, 1, 128, 5, 40),
+                                                  (2, 4, 2, 32, 17, 100), (1, 8, 4, 96, 1000, 16)])
+def test_gqa_prefill_matches_causal_attention(dtype, B, QH, KVH, HD, start, Tc):
+    """loom_gqa_prefill: RoPE + cache append of a chunk of Tc tokens at
+    positions start.., then token t attends to cache rows 0..start+t (the
+    earlier chunks' rows already in the cache); both readouts against a torch
+    fp32 causal attention over the same (rounded) rows."""
+    from loom_amd import _lib
+    g = torch.Generator().manual_seed(B + QH + HD + start + Tc)
+    max_len = start + Tc + 3
+    cos, sin = _rope_tables(HD, max_len)
+    cos_d, sin_d = cos.to(DEV), sin.to(DEV)
+    kc = torch.zeros(B, max_len, KVH, HD, device=DEV, dtype=dtype)
+    vc = torch.zeros_like(kc)
+    kc[:, :start] = torch.randn(B, start, KVH, HD, generator=g).to(DEV, dtype)
+    vc[:, :start] = torch.randn(B, start, KVH, HD, generator=g).to(DEV, dtype)
+    W = (QH + 2 * KVH) * HD
+    qkv = torch.randn(B, Tc, W, generator=g).to(DEV, dtype)
+    q = torch.empty(B, Tc, QH, HD, device=DEV, dtype=dtype)
+    c = torch.empty(B, Tc, QH * HD, device=DEV, dtype=dtype)
+    kx = torch.empty_like(c)
+    _lib.call("loom_gqa_prefill", code(qkv), P(qkv), W, P(kc), P(vc), max_len * KVH * HD, KVH * HD, HD,
+              P(cos_d), P(sin_d), P(q), P(c), P(kx), QH * HD, B, Tc, start, max_len, QH, KVH, HD, S(qkv))
+    x = host(qkv)
+    cs, sn = cos[start:start + Tc].view(1, Tc, 1, HD), sin[start:start + Tc].view(1, Tc, 1, HD)
+    wq = ref.apply_rope(x[..., :QH * HD].reshape(B, Tc, QH, HD), cs, sn)
+    wk = ref.apply_rope(x[..., QH * HD:(QH + KVH) * HD].reshape(B, Tc, KVH, HD), cs, sn)
+    check(q, wq, dtype)
+    check(kc[:, start:start + Tc], wk, dtype)
+    # attention over the cache as stored (rounded to dtype), rows 0..start+t
+    Kall = host(kc)[:, :start + Tc].repeat_interleave(QH // KVH, dim=2).transpose(1, 2)   # [B,QH,L,HD]
+    Vall = host(vc)[:, :start + Tc].repeat_interleave(QH // KVH, dim=2).transpose(1, 2)
+    qq = host(q).transpose(1, 2)                                                         # [B,QH,Tc,HD]
+    sc = (qq @ Kall.transpose(-1, -2)) / math.sqrt(HD)
+    mask = torch.arange(start + Tc)[None, :] <= (start + torch.arange(Tc))[:, None]
+    a = torch.softmax(sc.masked_fill(~mask, float("-inf")), dim=-1)
+    check(c, (a @ Vall).transpose(1, 2).reshape(B, Tc, QH * HD), dtype)
+    check(kx, (a @ Kall).transpose(1, 2).reshape(B, Tc, QH * HD), dtype)
+
+
 def _rope_tables(HD, n):
     inv, af = ref.yarn_inv_freq(HD, 10000.0, 4.0, 256, 32.0, 1.0)
     return ref.yarn_cos_sin(inv, af, n)
