@@ -17,6 +17,7 @@
 // the packed matrix is never written to HBM.
 #include <cmath>
 #include <type_traits>
+#include <utility>
 
 #include "depth_row.h"
 #include "loom_common.h"
@@ -206,32 +207,41 @@ gemm_bf16_mfma_kernel(GemmArgs a) {
 }
 
 // ------------------------------------------------------------------ big bf16 (M >= 256)
-// Block tile 256 (m) x 128 (n) x 64 (k), eight waves (two per SIMD, so one
-// wave's MFMAs cover the other's LDS waits) in a 4 (m) x 2 (n) grid, each
-// owning 64 x 64 as 4 x 4 MFMA tiles (v_mfma_f32_16x16x32_bf16).  Operand
-// tiles travel from global memory straight into LDS (buffer_load_dwordx4 ...
-// lds, no register staging) through three stages, each its own LDS array so
-// the compiler's waits name exactly the stage they need: k-tile t+2 is
-// requested while t is computed.
+// Block tile 256 (m) x 128 (n), v_mfma_f32_16x16x32_bf16 with fp32
+// accumulators.  BgCfg<WAVES, WGM, KH, WPE, NS> sets the waves of a block (WGM of
+// them along m, so a wave owns a (256/WGM) x (128*WGM/WAVES) sub-tile), the
+// 32-wide k-halves per pipeline stage (KH) and the waves per SIMD the register
+// budget is sized for.  Operand tiles travel from global memory straight into
+// LDS (buffer_load_dwordx4 ... lds, no register staging) through NS stages,
+// each its own LDS array so the compiler's waits name exactly the stage they
+// need: k-tiles t+1 .. t+NS-1 are in flight while t is computed.
 //
 // LDS layout of a stage: [k-half h][row][4 chunks of 8 k] (64 B rows), chunk c
 // of row r stored at position c ^ bg_swz(r) (r bits 1-2, flipped by bit 3), so
 // a 16-byte fragment read is conflict-free both 8 lanes at a time over 128 B
-// of banks and 16 lanes over 256 B (with (r >> 2) & 3 rows r and r+2 shared
-// banks: 50% of the LDS cycles were conflicts).  One DMA instruction of a wave fills 16 rows of
-// one k-half (lane l: row l/4, position l%4; the lane fetches the chunk the
-// swizzle puts there), so its 32 k lie in one gather sector and the source
-// and column offset are uniform (scalar) per instruction; per lane only a
-// 32-bit row offset per 16-row group is held, and the k advance is the
-// scalar soffset.  Requires K % 192 == 0 (whole rounds of the three stages);
-// 144 KB of LDS, one block per CU.
-constexpr int BG_M = 256, BG_N = 128, BG_K = 64;
+// of banks and 16 lanes over 256 B.  One DMA instruction of a wave fills 16
+// rows of one k-half (lane l: row l/4, position l%4; the lane fetches the
+// chunk the swizzle puts there), so its 32 k lie in one gather sector and the
+// source and column offset are uniform (scalar) per instruction; per lane only
+// a 32-bit row offset per 16-row group is held, and the k advance is the
+// scalar soffset.  Requires K % (32 * KH * NS) == 0 (whole rounds of the
+// stages).
 __host__ __device__ constexpr int bg_swz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
-constexpr int BG_WAVES = 8, BG_WGM = 4;                    // waves along m; BG_WAVES / BG_WGM along n
-constexpr int BG_WTM = BG_M / BG_WGM, BG_WTN = BG_N / (BG_WAVES / BG_WGM);   // 64 x 64 per wave
-constexpr int BG_FJ = BG_WTM / 16, BG_FI = BG_WTN / 16;    // x and w fragments per k-step
-constexpr int BG_XG = BG_M / 16 / BG_WAVES, BG_WG = BG_N / 16 / BG_WAVES;   // DMA row groups per wave
-constexpr int BG_DMA = 2 * (BG_XG + BG_WG);                // DMA instructions per lane per stage
+
+template <int BM_, int BN_, int WAVES_, int WGM_, int KH_, int WPE_, int NS_>
+struct BgCfg {
+    static constexpr int BG_M = BM_, BG_N = BN_;               // block tile
+    static constexpr int WAVES = WAVES_, WGM = WGM_, KH = KH_, WPE = WPE_, NS = NS_;
+    static constexpr int BK = 32 * KH;                         // k per stage
+    static constexpr int WTM = BG_M / WGM, WTN = BG_N / (WAVES / WGM);   // wave sub-tile
+    static constexpr int FJ = WTM / 16, FI = WTN / 16;         // x and w fragments per k-step
+    static constexpr int XG = BG_M / 16 / WAVES, WG = BG_N / 16 / WAVES;   // DMA row groups per wave
+    static constexpr int DMA = KH * (XG + WG);                 // DMA instructions per lane per stage
+    static constexpr int LDS = NS * KH * (BG_M + BG_N) * 32 * 2;
+    static_assert(WAVES % WGM == 0 && XG >= 1 && WG >= 1 && (KH == 1 || KH == 2), "big GEMM shape");
+    static_assert(NS >= 3 && NS <= 6 && (NS - 1) * DMA < 64 && LDS <= 160 * 1024, "big GEMM stages");
+};
+using BgConf = BgCfg<256, 128, 8, 4, 2, 2, 3>;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 template <int N>
@@ -266,14 +276,57 @@ __device__ __forceinline__ void gather_half(const GemmArgs& a, int64_t kk, int64
     }
 }
 
-template <bool GATHER>
-__global__ void __launch_bounds__(64 * BG_WAVES) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// Scheduling hints of one k-step: NR fragment reads (and the first ND of them
+// each preceded by a DMA request) spread evenly over NMM MFMAs, group GRP.
+template <int NMM, int NR, int ND, int GRP, int Q>
+__device__ __forceinline__ void bg_sched_step() {
+    if constexpr (Q < ND) __builtin_amdgcn_sched_group_barrier(0x0020, 1, GRP);   // VMEM read
+    __builtin_amdgcn_sched_group_barrier(0x0100, 1, GRP);                         // DS read
+    constexpr int n = NMM * (Q + 1) / NR - NMM * Q / NR;
+    if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x0008, n, GRP);    // MFMA
+}
+// f(integral_constant<int, s>) for s = 0 .. N-1, in order
+template <class F, int... S>
+__device__ __forceinline__ void bg_static_for_(F&& f, std::integer_sequence<int, S...>) {
+    (f(std::integral_constant<int, S>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void bg_static_for(F&& f) {
+    bg_static_for_(f, std::make_integer_sequence<int, N>{});
+}
+template <int NMM, int NR, int ND, int GRP, int... Q>
+__device__ __forceinline__ void bg_interleave(std::integer_sequence<int, Q...>) {
+    static_assert(ND <= NR, "more DMA requests than fragment reads");
+    (bg_sched_step<NMM, NR, ND, GRP, Q>(), ...);
+}
+
+template <bool GATHER, class C>
+__global__ void __launch_bounds__(64 * C::WAVES) __attribute__((amdgpu_waves_per_eu(C::WPE, C::WPE)))
 gemm_bf16_big_kernel(GemmArgs a) {
+    constexpr int BG_M = C::BG_M, BG_N = C::BG_N;
     constexpr int XH = BG_M * 32, WH = BG_N * 32;   // elements per k-half of a stage
-    __shared__ __attribute__((aligned(16))) uint16_t X0[2 * XH], X1[2 * XH], X2[2 * XH];
-    __shared__ __attribute__((aligned(16))) uint16_t W0[2 * WH], W1[2 * WH], W2[2 * WH];
+    constexpr int KH = C::KH, FI = C::FI, FJ = C::FJ, XG = C::XG, WG = C::WG, DMA = C::DMA;
+    constexpr int NS = C::NS;
+    // stage s: X_s, W_s (separate arrays, so a wait for one stage's DMA never
+    // covers another's reads); arrays of stages >= NS are not referenced
+    __shared__ __attribute__((aligned(16))) uint16_t X0[KH * XH], X1[KH * XH], X2[KH * XH],
+        X3[NS > 3 ? KH * XH : 8], X4[NS > 4 ? KH * XH : 8], X5[NS > 5 ? KH * XH : 8];
+    __shared__ __attribute__((aligned(16))) uint16_t W0[KH * WH], W1[KH * WH], W2[KH * WH],
+        W3[NS > 3 ? KH * WH : 8], W4[NS > 4 ? KH * WH : 8], W5[NS > 5 ? KH * WH : 8];
+    auto xs = [&](auto s_) -> uint16_t* {
+        constexpr int S = decltype(s_)::value;
+        if constexpr (S == 0) return X0; else if constexpr (S == 1) return X1;
+        else if constexpr (S == 2) return X2; else if constexpr (S == 3) return X3;
+        else if constexpr (S == 4) return X4; else return X5;
+    };
+    auto ws = [&](auto s_) -> uint16_t* {
+        constexpr int S = decltype(s_)::value;
+        if constexpr (S == 0) return W0; else if constexpr (S == 1) return W1;
+        else if constexpr (S == 2) return W2; else if constexpr (S == 3) return W3;
+        else if constexpr (S == 4) return W4; else return W5;
+    };
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave % BG_WGM, wn = wave / BG_WGM;
+    const int wm = wave % C::WGM, wn = wave / C::WGM;
     // Tile of this block.  Blocks are dispatched round-robin over the 8 XCDs
     // (block b runs on XCD b % 8), each with its own L2: when the m-tiles
     // split evenly, XCD x takes m-tiles [x*MT/8, (x+1)*MT/8) and walks the
@@ -295,20 +348,19 @@ gemm_bf16_big_kernel(GemmArgs a) {
     const int64_t g = GATHER ? n0 / a.Hq : 0;
     const int64_t ldx = GATHER ? a.Nm : a.ldx;
 
-    // DMA slots: X 16-row groups BG_XG*wave + q, W groups BG_WG*wave + q, each
-    // for both k-halves; lane: row 16*group + lane/4, chunk (lane%4) ^
-    // bg_swz(row); rows past M / N read the last row (their results are not
-    // stored)
-    uint32_t xv[BG_XG], wv[BG_WG];
+    // DMA slots: X 16-row groups XG*wave + q, W groups WG*wave + q, each for
+    // every k-half; lane: row 16*group + lane/4, chunk (lane%4) ^ bg_swz(row);
+    // rows past M / N read the last row (their results are not stored)
+    uint32_t xv[XG], wv[WG];
 #pragma unroll
-    for (int q = 0; q < BG_XG; ++q) {
-        const int r = 16 * (BG_XG * wave + q) + (lane >> 2);
+    for (int q = 0; q < XG; ++q) {
+        const int r = 16 * (XG * wave + q) + (lane >> 2);
         const int64_t rr = m0 + r < a.M ? r : a.M - 1 - m0;
         xv[q] = (uint32_t)((rr * ldx + 8 * ((lane & 3) ^ bg_swz(r))) * 2);
     }
 #pragma unroll
-    for (int q = 0; q < BG_WG; ++q) {
-        const int r = 16 * (BG_WG * wave + q) + (lane >> 2);
+    for (int q = 0; q < WG; ++q) {
+        const int r = 16 * (WG * wave + q) + (lane >> 2);
         const int64_t rr = n0 + r < a.N ? r : a.N - 1 - n0;
         wv[q] = (uint32_t)((rr * a.ldw + 8 * ((lane & 3) ^ bg_swz(r))) * 2);
     }
@@ -317,9 +369,11 @@ gemm_bf16_big_kernel(GemmArgs a) {
     const auto rx = __builtin_amdgcn_make_buffer_rsrc(
         GATHER ? (void*)nullptr : (void*)((const uint16_t*)a.X + m0 * a.ldx), (short)0, 0x7fffffff,
         kBufferDword3);
-    auto issue = [&](int64_t k0, uint16_t* Xs, uint16_t* Ws) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
+    // the DMA requests of the stage holding k-tile k0 / C::BK, one instruction
+    // per call of dma_one(q), q < DMA (so they can be spread over the MFMAs)
+    auto dma_one = [&](int q, int64_t k0, uint16_t* Xs, uint16_t* Ws) {
+        const int h = q / (XG + WG), p = q % (XG + WG);
+        if (p < XG) {
             auto rxh = rx;
             uint32_t sx = (uint32_t)((k0 + 32 * h) * 2);
             if constexpr (GATHER) {
@@ -330,21 +384,22 @@ gemm_bf16_big_kernel(GemmArgs a) {
                                                         (short)0, 0x7fffffff, kBufferDword3);
                 sx = (uint32_t)(col * 2);
             }
-#pragma unroll
-            for (int q = 0; q < BG_XG; ++q)
-                dma16(rxh, Xs + h * XH + 16 * (BG_XG * wave + q) * 32, xv[q], sx);
-#pragma unroll
-            for (int q = 0; q < BG_WG; ++q)
-                dma16(rw, Ws + h * WH + 16 * (BG_WG * wave + q) * 32, wv[q],
-                      (uint32_t)((k0 + 32 * h) * 2));
+            dma16(rxh, Xs + h * XH + 16 * (XG * wave + p) * 32, xv[p], sx);
+        } else {
+            const int w = p - XG;
+            dma16(rw, Ws + h * WH + 16 * (WG * wave + w) * 32, wv[w], (uint32_t)((k0 + 32 * h) * 2));
         }
     };
+    auto issue = [&](int64_t k0, uint16_t* Xs, uint16_t* Ws) {
+#pragma unroll
+        for (int q = 0; q < DMA; ++q) dma_one(q, k0, Xs, Ws);
+    };
 
-    f32x4 acc[BG_FI][BG_FJ];
+    f32x4 acc[FI][FJ];
 #pragma unroll
-    for (int i = 0; i < BG_FI; ++i)
+    for (int i = 0; i < FI; ++i)
 #pragma unroll
-        for (int j = 0; j < BG_FJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < FJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // fragment of k-step kk: row base + 16*i + fr of half kk, chunk fc at its
     // swizzled position (bg_swz(row) = bg_swz(fr) for every tile: bases are
@@ -352,85 +407,102 @@ gemm_bf16_big_kernel(GemmArgs a) {
     const int fr = lane & 15, fc = lane >> 4;
     const int lo = fr * 32 + ((fc ^ bg_swz(fr)) << 3);
     struct Frags {
-        bf16x8 w[BG_FI], x[BG_FJ];
+        bf16x8 w[FI], x[FJ];
     };
     auto read = [&](Frags& f, const uint16_t* Xs, const uint16_t* Ws, int kk) {
 #pragma unroll
-        for (int i = 0; i < BG_FI; ++i)
-            f.w[i] = *reinterpret_cast<const bf16x8*>(&Ws[kk * WH + (wn * BG_WTN + i * 16) * 32 + lo]);
+        for (int i = 0; i < FI; ++i)
+            f.w[i] = *reinterpret_cast<const bf16x8*>(&Ws[kk * WH + (wn * C::WTN + i * 16) * 32 + lo]);
 #pragma unroll
-        for (int j = 0; j < BG_FJ; ++j)
-            f.x[j] = *reinterpret_cast<const bf16x8*>(&Xs[kk * XH + (wm * BG_WTM + j * 16) * 32 + lo]);
+        for (int j = 0; j < FJ; ++j)
+            f.x[j] = *reinterpret_cast<const bf16x8*>(&Xs[kk * XH + (wm * C::WTM + j * 16) * 32 + lo]);
     };
-    auto mma = [&](const Frags& f) {
+    // MFMAs of x-fragments [j0, j1) (the fragments of a half die after it)
+    auto mma = [&](const Frags& f, auto j0_, auto j1_) {
+        constexpr int j0 = decltype(j0_)::value, j1 = decltype(j1_)::value;
 #pragma unroll
-        for (int i = 0; i < BG_FI; ++i)
+        for (int j = j0; j < j1; ++j)
 #pragma unroll
-            for (int j = 0; j < BG_FJ; ++j)
+            for (int i = 0; i < FI; ++i)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.w[i], f.x[j], acc[i][j], 0, 0, 0);
     };
-    constexpr int NR = BG_FI + BG_FJ;        // fragment reads per k-step
-    constexpr int NM = BG_FI * BG_FJ;        // MFMAs per k-step
+    using I0 = std::integral_constant<int, 0>;
+    using IH = std::integral_constant<int, FJ / 2>;
+    using IF = std::integral_constant<int, FJ>;
+    constexpr int NR = FI + FJ;        // fragment reads per k-step
+    constexpr int NM = FI * FJ;        // MFMAs per k-step
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    using SEQ = std::make_integer_sequence<int, NR>;
 
-    // Tile t lives in stage t % 3, requested two tiles ahead (nk = K / 64 is a
-    // multiple of 3).  Iteration t, with k-step 0 of t already in registers
-    // (f0): read k-step 1 of t; MFMAs of k-step 0; wait for tile t+1's DMA and
-    // every wave's reads of t (barrier); request tile t+3 into t's stage; read
-    // k-step 0 of t+1; MFMAs of k-step 1.  Straight-line code per stage, so
-    // every wait is a constant.
-    const int64_t nk = a.K / BG_K;
-    issue(0, X0, W0);
-    issue(BG_K, X1, W1);
-    issue(2 * BG_K, X2, W2);
-    wait_vmcnt<2 * BG_DMA>();
+    // Tile t lives in stage t % NS; all NS stages are requested up front and
+    // tile t+NS into t's stage as soon as every wave has read t (nk = K / BK
+    // is a multiple of NS).  Straight-line code per stage, so every wait is a
+    // constant.  Iteration t (f0 = the first k-step of t, already in
+    // registers):
+    //   KH = 2: read k-step 1 of t; MFMAs of k-step 0; wait for tile t+1's DMA
+    //           and every wave's reads of t (barrier); request tile t+NS into
+    //           t's stage; read k-step 0 of t+1 (f0); MFMAs of k-step 1.
+    //   KH = 1: MFMAs of the first half of the x-fragments; wait and barrier;
+    //           request tile t+NS; read tile t+1 (f1); the second half; f0 = f1.
+    const int64_t nk = a.K / C::BK;
+    bg_static_for<NS>([&](auto s_) { issue(decltype(s_)::value * C::BK, xs(s_), ws(s_)); });
+    wait_vmcnt<(NS - 1) * DMA>();
     __builtin_amdgcn_s_barrier();
     Frags f0, f1;
     read(f0, X0, W0, 0);
-    // NEXT: tile t+1 exists; MORE: tile t+2 exists; ISSUE: tile t+3 exists
-    auto iter = [&](auto next_, auto more_, auto issue_, int64_t t, uint16_t* Xc, uint16_t* Wc,
-                    const uint16_t* Xn, const uint16_t* Wn) {
-        constexpr bool NEXT = decltype(next_)::value, MORE = decltype(more_)::value,
-                       ISSUE = decltype(issue_)::value;
-        // the fragment reads of the next k-step interleaved with the MFMAs of
-        // this one (one 16-byte LDS read per two MFMAs), likewise the DMA requests
-        read(f1, Xc, Wc, 1);
-        mma(f0);
-#pragma unroll
-        for (int q = 0; q < NR; ++q) {
-            __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // DS read
-            __builtin_amdgcn_sched_group_barrier(0x0008, NM / NR, 0);   // MFMA
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (NEXT) {
-            if constexpr (MORE) wait_vmcnt<BG_DMA>(); else wait_vmcnt<0>();
-            __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0): this wave's reads of t landed
-            __builtin_amdgcn_s_barrier();
+    // S: stage of tile t; NEXT: tile t+1 exists; OUT: tiles after t+1 that
+    // may still be in flight at its wait; ISSUE: tile t+NS exists
+    auto iter = [&](auto s_, auto next_, auto out_, auto issue_, int64_t t) {
+        constexpr int S = decltype(s_)::value, OUT = decltype(out_)::value;
+        constexpr bool NEXT = decltype(next_)::value, ISSUE = decltype(issue_)::value;
+        uint16_t* Xc = xs(s_);
+        uint16_t* Wc = ws(s_);
+        const uint16_t* Xn = xs(std::integral_constant<int, (S + 1) % NS>{});
+        const uint16_t* Wn = ws(std::integral_constant<int, (S + 1) % NS>{});
+        if constexpr (KH == 2) {
+            read(f1, Xc, Wc, 1);
+            mma(f0, I0{}, IF{});
+            bg_interleave<NM, NR, 0, 0>(SEQ{});
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (ISSUE) issue((t + 3) * BG_K, Xc, Wc);
-            read(f0, Xn, Wn, 0);
-        }
-        mma(f1);
-        if constexpr (NEXT) {
-#pragma unroll
-            for (int q = 0; q < NR; ++q) {
-                if constexpr (ISSUE)
-                    if (q < BG_DMA) __builtin_amdgcn_sched_group_barrier(0x0020, 1, 1);   // VMEM read
-                __builtin_amdgcn_sched_group_barrier(0x0100, 1, 1);   // DS read
-                __builtin_amdgcn_sched_group_barrier(0x0008, NM / NR, 1);   // MFMA
+            if constexpr (NEXT) {
+                wait_vmcnt<OUT * DMA>();
+                __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's reads of t landed
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (ISSUE) issue((t + NS) * C::BK, Xc, Wc);
+                read(f0, Xn, Wn, 0);
             }
+            mma(f1, I0{}, IF{});
+            if constexpr (NEXT) bg_interleave<NM, NR, ISSUE ? DMA : 0, 1>(SEQ{});
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            mma(f0, I0{}, IH{});
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (NEXT) {
+                wait_vmcnt<OUT * DMA>();
+                __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's reads of t landed
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (ISSUE) issue((t + NS) * C::BK, Xc, Wc);
+                read(f1, Xn, Wn, 0);
+            }
+            mma(f0, IH{}, IF{});
+            if constexpr (NEXT) bg_interleave<NM - NM / 2, NR, ISSUE ? DMA : 0, 1>(SEQ{});
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (NEXT) f0 = f1;
         }
-        __builtin_amdgcn_sched_barrier(0);
     };
-    using T_ = std::true_type;
-    using F_ = std::false_type;
-    for (int64_t t = 0; t < nk - 3; t += 3) {
-        iter(T_{}, T_{}, T_{}, t, X0, W0, X1, W1);
-        iter(T_{}, T_{}, T_{}, t + 1, X1, W1, X2, W2);
-        iter(T_{}, T_{}, T_{}, t + 2, X2, W2, X0, W0);
+    for (int64_t t = 0; t < nk - NS; t += NS) {
+        bg_static_for<NS>([&](auto s_) {
+            iter(s_, T_{}, std::integral_constant<int, NS - 2>{}, T_{}, t + decltype(s_)::value);
+        });
     }
-    iter(T_{}, T_{}, F_{}, nk - 3, X0, W0, X1, W1);
-    iter(T_{}, F_{}, F_{}, nk - 2, X1, W1, X2, W2);
-    iter(F_{}, F_{}, F_{}, nk - 1, X2, W2, X0, W0);
+    bg_static_for<NS>([&](auto s_) {
+        constexpr int S = decltype(s_)::value;
+        iter(s_, std::bool_constant<(S < NS - 1)>{}, std::integral_constant<int, (S < NS - 1 ? NS - 2 - S : 0)>{},
+             F_{}, nk - NS + S);
+    });
 
     // epilogue: lane holds n = nb + 0..3 of row m for each (i, j).  Whole
     // tiles take straight-line code with 8-byte stores (one variant per
@@ -440,8 +512,8 @@ gemm_bf16_big_kernel(GemmArgs a) {
     const uint16_t* gp = (const uint16_t*)a.gate_p;
     const uint16_t* rs = (const uint16_t*)a.residual;
     const int64_t ldc = a.ldc;
-    const int64_t mrow = m0 + wm * BG_WTM + (lane & 15);
-    const int64_t ncol = n0 + wn * BG_WTN + (lane >> 4) * 4;
+    const int64_t mrow = m0 + wm * C::WTM + (lane & 15);
+    const int64_t ncol = n0 + wn * C::WTN + (lane >> 4) * 4;
     const bool whole = m0 + BG_M <= a.M && n0 + BG_N <= a.N && (ldc & 3) == 0 &&
                        (((uintptr_t)out | (uintptr_t)gp | (uintptr_t)rs) & 7) == 0 &&
                        ((uintptr_t)a.bias & 15) == 0;
@@ -452,7 +524,7 @@ gemm_bf16_big_kernel(GemmArgs a) {
     auto whole_tile = [&](auto gate_, auto res_) {
         constexpr bool GATE = decltype(gate_)::value, RES = decltype(res_)::value;
 #pragma unroll
-        for (int i = 0; i < BG_FI; ++i) {
+        for (int i = 0; i < FI; ++i) {
             const int64_t nb = ncol + i * 16;
             float bias4[4] = {0.f, 0.f, 0.f, 0.f};
             if (a.bias != nullptr) {
@@ -460,7 +532,7 @@ gemm_bf16_big_kernel(GemmArgs a) {
                 bias4[0] = bv.x; bias4[1] = bv.y; bias4[2] = bv.z; bias4[3] = bv.w;
             }
 #pragma unroll
-            for (int j = 0; j < BG_FJ; ++j) {
+            for (int j = 0; j < FJ; ++j) {
                 const int64_t e = (mrow + j * 16) * ldc + nb;
                 float v[4], gv[4], rv[4];
                 if constexpr (GATE) bf4(*reinterpret_cast<const uint2*>(gp + e), gv);
@@ -485,11 +557,11 @@ gemm_bf16_big_kernel(GemmArgs a) {
         return;
     }
 #pragma unroll
-    for (int i = 0; i < BG_FI; ++i) {
+    for (int i = 0; i < FI; ++i) {
         const int64_t nb = ncol + i * 16;
         if (nb >= a.N) continue;
 #pragma unroll
-        for (int j = 0; j < BG_FJ; ++j) {
+        for (int j = 0; j < FJ; ++j) {
             const int64_t m = mrow + j * 16;
             if (m >= a.M) continue;
 #pragma unroll
@@ -1112,9 +1184,11 @@ static int run_gemm(const GemmArgs& a, hipStream_t st, const char* what) {
         if (GATHER)
             for (int s = 0; s < 5; ++s) ok = ok && ((uintptr_t)a.src[s] & 15) == 0;
         // many rows and whole 64-wide k-tiles: the 256 x 128 tile with DMA stages
-        if (ok && a.M >= BG_M && a.K % (3 * BG_K) == 0 && (!GATHER || a.Hq % BG_N == 0)) {
-            dim3 grid((unsigned)(ceil_div(a.N, BG_N) * ceil_div(a.M, BG_M)));
-            hipLaunchKernelGGL((gemm_bf16_big_kernel<GATHER>), grid, dim3(64 * BG_WAVES), 0, st, a);
+        using C = BgConf;
+        if (ok && a.M >= C::BG_M && a.K % (C::NS * C::BK) == 0 && (!GATHER || a.Hq % C::BG_N == 0)) {
+            dim3 grid((unsigned)(ceil_div(a.N, C::BG_N) * ceil_div(a.M, C::BG_M)));
+            hipLaunchKernelGGL((gemm_bf16_big_kernel<GATHER, BgConf>), grid, dim3(64 * BgConf::WAVES), 0,
+                               st, a);
             return launch_status(what);
         }
         if (ok) {

@@ -69,6 +69,47 @@ prefill_rope_append_kernel(const T* __restrict__ qkv, int64_t qkv_ld, T* __restr
     }
 }
 
+// Same contract, one thread per 8 consecutive dims of one head of one token
+// (head_dim a multiple of 16, so a group never straddles the rotate-half
+// boundary and its partner group is whole too): 16-byte loads of x, its
+// partner and the two table rows, one 16-byte store.  The rotation is the
+// scalar kernel's fma(x, cos, rot * sin) to the bit.
+template <typename T>
+__global__ void __launch_bounds__(256)
+prefill_rope_append8_kernel(const T* __restrict__ qkv, int64_t qkv_ld, T* __restrict__ q_out,
+                            T* __restrict__ kc, T* __restrict__ vc, const float* __restrict__ cosv,
+                            const float* __restrict__ sinv, int total, int Tc, int64_t start, int QH,
+                            int KVH, int HD, int64_t csb, int64_t cst, int64_t csh) {
+    const int id = blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const int P = HD >> 3, heads = QH + 2 * KVH;
+    const int bt = id / (heads * P);
+    const int rem = id - bt * heads * P;
+    const int hs = rem / P, d0 = (rem - hs * P) * 8;
+    const int b = bt / Tc, t = bt - b * Tc;
+    const int64_t pos = start + t;
+    const T* head = qkv + (int64_t)bt * qkv_ld + hs * HD;
+    float v[8];
+    if (hs < QH + KVH) {
+        const int half = HD >> 1;
+        float x[8], y[8], c[8], sn[8];
+        Vec8<T>::load(head + d0, x);
+        Vec8<T>::load(head + (d0 < half ? d0 + half : d0 - half), y);
+        Vec8<float>::load(cosv + pos * HD + d0, c);
+        Vec8<float>::load(sinv + pos * HD + d0, sn);
+        const float sg = d0 < half ? -1.0f : 1.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = fmaf(x[e], c[e], (sg * y[e]) * sn[e]);
+        if (hs < QH)
+            Vec8<T>::store(q_out + ((int64_t)bt * QH + hs) * HD + d0, v);
+        else
+            Vec8<T>::store(kc + b * csb + pos * cst + (hs - QH) * csh + d0, v);
+    } else {
+        Vec8<T>::load(head + d0, v);
+        Vec8<T>::store(vc + b * csb + pos * cst + (hs - QH - KVH) * csh + d0, v);
+    }
+}
+
 // ------------------------------------------------------------------ VALU form
 // Block (t, kvh, b): 256 / LPR row groups of LPR lanes (HD = EPL * LPR); group
 // r takes cache rows r, r + NG, ... up to the token's position, in batches of
@@ -414,9 +455,21 @@ static int prefill_dispatch(const void* qkv, int64_t qkv_ld, void* kc, void* vc,
                             int64_t Tc, int64_t start, int64_t QH, int64_t KVH, int64_t HD,
                             hipStream_t st) {
     const int64_t total = B * Tc * (QH + 2 * KVH) * HD;
-    hipLaunchKernelGGL((prefill_rope_append_kernel<T>), dim3((unsigned)ceil_div(total, 256)),
-                       dim3(256), 0, st, (const T*)qkv, qkv_ld, (T*)q_out, (T*)kc, (T*)vc, cosv,
-                       sinv, B, Tc, start, (int)QH, (int)KVH, (int)HD, csb, cst, csh);
+    // 16-byte groups: every row base and stride a multiple of 8 elements
+    // (16 bytes for 16-bit types, 32 for fp32) and 16-byte aligned pointers
+    const bool vec = HD % 16 == 0 && total / 8 < (1LL << 31) && qkv_ld % 8 == 0 && csb % 8 == 0 &&
+                     cst % 8 == 0 && csh % 8 == 0 &&
+                     (((uintptr_t)qkv | (uintptr_t)kc | (uintptr_t)vc | (uintptr_t)q_out |
+                       (uintptr_t)cosv | (uintptr_t)sinv) & 15) == 0;
+    if (vec)
+        hipLaunchKernelGGL((prefill_rope_append8_kernel<T>), dim3((unsigned)ceil_div(total / 8, 256)),
+                           dim3(256), 0, st, (const T*)qkv, qkv_ld, (T*)q_out, (T*)kc, (T*)vc, cosv,
+                           sinv, (int)(total / 8), (int)Tc, start, (int)QH, (int)KVH, (int)HD, csb,
+                           cst, csh);
+    else
+        hipLaunchKernelGGL((prefill_rope_append_kernel<T>), dim3((unsigned)ceil_div(total, 256)),
+                           dim3(256), 0, st, (const T*)qkv, qkv_ld, (T*)q_out, (T*)kc, (T*)vc, cosv,
+                           sinv, B, Tc, start, (int)QH, (int)KVH, (int)HD, csb, cst, csh);
     int rc = launch_status("loom_gqa_prefill (rope/append)");
     if (rc != LOOM_OK) return rc;
     PrefillArgs<T> a{};

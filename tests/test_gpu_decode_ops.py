@@ -139,12 +139,14 @@ def test_gqa_decode_attention(dtype, B, QH, KVH, HD, length):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("B,QH,KVH,HD,start,Tc", [(2, 8, 2, 96, 0, 128), (3, 8, 2, 96, 300, 70),
                                                   (2, 4, 1, 64, 64, 33), (2, 8, 1, 128, 5, 40),
-                                                  (2, 4, 2, 32, 17, 100), (1, 8, 4, 96, 1000, 16)])
+                                                  (2, 4, 2, 32, 17, 100), (1, 8, 4, 96, 1000, 16),
+                                                  (2, 4, 2, 8, 9, 20)])
 def test_gqa_prefill_matches_causal_attention(dtype, B, QH, KVH, HD, start, Tc):
     """loom_gqa_prefill: RoPE + cache append of a chunk of Tc tokens at
     positions start.., then token t attends to cache rows 0..start+t (the
     earlier chunks' rows already in the cache); both readouts against a torch
-    fp32 causal attention over the same (rounded) rows."""
+    fp32 causal attention over the same (rounded) rows.  head_dim 8 takes the
+    element-per-thread RoPE/append kernel, the others the 16-byte one."""
     from loom_amd import _lib
     g = torch.Generator().manual_seed(B + QH + HD + start + Tc)
     max_len = start + Tc + 3
