@@ -498,9 +498,36 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     const int QKV = (a.QH + 2 * a.KVH) * HD;
     Tiles& tl = reinterpret_cast<Tiles*>(lds)[wave];
 
+    const bf16_t* kb = a.kc + b * a.csb + kvh * a.csh;
+    const bf16_t* vb = a.vc + b * a.csb + kvh * a.csh;
+    const int nstep = (int)((t1 - t0 + 4 * kMfTile - 1) / (4 * kMfTile));
+    // piece j = i*64 + lane of the tile at ts: row j / CPR (clamped in range,
+    // masked below), piece j % CPR; the next tile's pieces are requested as
+    // soon as this tile's are in LDS
+    gqa_u4 kr[NI], vr[NI];
+    // raw buffer views of this (b, kv head)'s rows < t1 (byte offsets fit 31 bits:
+    // checked by the host)
+    const int kv_bytes = (int)(t1 * a.cst * 2);
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)kb, (short)0, kv_bytes, kBufferDword3);
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0, kv_bytes, kBufferDword3);
+    auto load_kv = [&](int64_t ts) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int j = i * 64 + lane, row = j / CPR, c = j - row * CPR;
+            int64_t t = ts + row;
+            t = t < t1 ? t : t1 - 1;
+            const int off = (int)(t * a.cst * 2) + 16 * c;
+            kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, kKvLoadPolicy);
+            vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, kKvLoadPolicy);
+        }
+    };
+    // the first tile is requested before anything else of the block
+    load_kv(t0 + wave * kMfTile);
+
     // FROM_QKV: the block holding pos appends this token's (k_roped, v) to the
-    // caches; its own attention takes that row from the qkv registers below,
-    // so nothing in this launch reads the appended row back
+    // caches and stages it in LDS; its attention takes that row from the
+    // staged copy (store_kv below), so nothing in this launch depends on the
+    // appended cache row
     const bf16_t* krow_new = a.q + b * QKV + (a.QH + kvh) * HD;
     const bf16_t* vrow_new = krow_new + a.KVH * HD;
     __shared__ uint4 knew[HD / 8], vnew[HD / 8];   // this token's (k_roped, v) as bf16
@@ -516,42 +543,24 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
             knew[tid] = kw;
             vnew[tid] = vw;
         }
-        lds_barrier();
     }
-    const bf16_t* kb = a.kc + b * a.csb + kvh * a.csh;
-    const bf16_t* vb = a.vc + b * a.csb + kvh * a.csh;
-    const int nstep = (int)((t1 - t0 + 4 * kMfTile - 1) / (4 * kMfTile));
-    // piece j = i*64 + lane of the tile at ts: row j / CPR (clamped in range,
-    // masked below), piece j % CPR; the next tile's pieces are requested as
-    // soon as this tile's are in LDS
-    gqa_u4 kr[NI], vr[NI];
-    // raw buffer views of this (b, kv head)'s rows < t1 (byte offsets fit 31 bits:
-    // checked by the host)
-    const int kv_bytes = (int)(t1 * a.cst * 2);
-    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)kb, (short)0, kv_bytes, kBufferDword3);
-    const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0, kv_bytes, kBufferDword3);
     const gqa_u4* kn_lds = reinterpret_cast<const gqa_u4*>(knew);
     const gqa_u4* vn_lds = reinterpret_cast<const gqa_u4*>(vnew);
-    auto load_kv = [&](int64_t ts) {
+    // this wave's tile at ts into its LDS tiles; FROM_QKV: the row of this
+    // token from the staged copy (the loaded value may predate the append)
+    auto store_kv = [&](int64_t ts) {
+        if constexpr (FROM_QKV) {
+            if (pos >= ts && pos < ts + kMfTile) {   // wave-uniform: the tile holds the token
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int j = i * 64 + lane, row = j / CPR, c = j - row * CPR;
-            int64_t t = ts + row;
-            t = t < t1 ? t : t1 - 1;
-            const int off = (int)(t * a.cst * 2) + 16 * c;
-            kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, kKvLoadPolicy);
-            vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, kKvLoadPolicy);
-            if constexpr (FROM_QKV) {
-                // this token: the row staged in LDS (its cache row is being
-                // written by this block; the loaded value is discarded)
-                const gqa_u4 kn = kn_lds[c], vn = vn_lds[c];
-                const bool here = t == pos;
-                kr[i] = here ? kn : kr[i];
-                vr[i] = here ? vn : vr[i];
+                for (int i = 0; i < NI; ++i) {
+                    const int j = i * 64 + lane, row = j / CPR, c = j - row * CPR;
+                    if (ts + row == pos) {
+                        kr[i] = kn_lds[c];
+                        vr[i] = vn_lds[c];
+                    }
+                }
             }
         }
-    };
-    auto store_kv = [&]() {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int j = i * 64 + lane, row = j / CPR, c = j - row * CPR;
@@ -560,7 +569,6 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
             tl.v[slot] = vr[i];
         }
     };
-    load_kv(t0 + wave * kMfTile);
     // B operand of S^T: q of head lr, dims 32*kk + 8*lq .. +7, rounded to bf16
     uint4 qf[KK];
 #pragma unroll
@@ -586,12 +594,13 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     f32x4_t accC[DT], accK[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) accC[dt] = accK[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if constexpr (FROM_QKV) lds_barrier();   // the staged row is visible to every wave
 
     // every wave runs the same number of steps; a step past t1 is fully masked
     for (int it = 0; it < nstep; ++it) {
         const int64_t ts = t0 + wave * kMfTile + (int64_t)it * 4 * kMfTile;
         wave_lds_fence();                  // the previous tile's reads came first
-        store_kv();
+        store_kv(ts);
         if (it + 1 < nstep) load_kv(ts + 4 * kMfTile);
         wave_lds_fence();
         // S^T[position 16*hf + 4*lq + r][head lr]

@@ -12,6 +12,8 @@ from ctypes import c_float, c_int, c_int64, c_void_p
 
 import torch
 
+# descriptor layouts and signatures below are those of loom_abi_version() == 5
+ABI_VERSION = 5
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libloom_hip.so")
 
 _P = c_void_p
@@ -127,6 +129,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         lib.loom_last_error.restype = ctypes.c_char_p
         lib.loom_last_error.argtypes = []
         lib.loom_abi_version.restype = c_int
+        if lib.loom_abi_version() != ABI_VERSION:
+            raise RuntimeError(
+                f"{path} implements C ABI version {lib.loom_abi_version()}, this binding "
+                f"declares version {ABI_VERSION}; rebuild the library")
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes
