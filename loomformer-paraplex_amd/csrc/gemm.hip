@@ -47,6 +47,17 @@ struct GemmArgs {
     int open;
     const uint4* Uf;     // head sectors: fragment-major copy of U (the skinny form reads its
                          // sector from it), or null
+    // big kernel only (not gather): a second input along K, k >= K1 reading
+    // X2 / W2 at k - K1 (X2 null: one input), and split-K, the K range in
+    // nsplit equal parts with fp32 sums to partial[(split*M + m)*ldp + n] and
+    // no epilogue (partial null: the epilogue, nsplit 1)
+    const void* X2;
+    int64_t ldx2;
+    const void* W2;
+    int64_t ldw2, K1;
+    float* partial;
+    int64_t ldp;
+    int nsplit;
 };
 
 // Element offset of packed column kk of group g, and which source it is in.
@@ -333,7 +344,11 @@ gemm_bf16_big_kernel(GemmArgs a) {
     // n-tiles with its m-tiles innermost, so the tiles resident on one XCD at
     // a time share their X rows and a few W column blocks in its L2.
     const int64_t MT = ceil_div(a.M, BG_M), NT = ceil_div(a.N, BG_N);
-    const int64_t b = blockIdx.x;
+    // split-K: block x takes split x / (MT*NT) of the K range, tile x % (MT*NT)
+    const int64_t split = a.partial != nullptr ? (int64_t)blockIdx.x / (MT * NT) : 0;
+    const int64_t b = (int64_t)blockIdx.x - split * MT * NT;
+    const int64_t kspan = a.partial != nullptr ? a.K / a.nsplit : a.K;
+    const int64_t kbase = split * kspan;
     int64_t mt, nt;
     if (MT % 8 == 0) {
         const int64_t mpx = MT / 8, li = b / 8;
@@ -369,25 +384,51 @@ gemm_bf16_big_kernel(GemmArgs a) {
     const auto rx = __builtin_amdgcn_make_buffer_rsrc(
         GATHER ? (void*)nullptr : (void*)((const uint16_t*)a.X + m0 * a.ldx), (short)0, 0x7fffffff,
         kBufferDword3);
+    // second input (k >= K1): its own row offsets and descriptors
+    const bool dual = !GATHER && a.X2 != nullptr;
+    const int64_t K1 = dual ? a.K1 : a.K;
+    uint32_t xv2[XG], wv2[WG];
+#pragma unroll
+    for (int q = 0; q < XG; ++q) {
+        const int r = 16 * (XG * wave + q) + (lane >> 2);
+        const int64_t rr = m0 + r < a.M ? r : a.M - 1 - m0;
+        xv2[q] = dual ? (uint32_t)((rr * a.ldx2 + 8 * ((lane & 3) ^ bg_swz(r))) * 2) : 0u;
+    }
+#pragma unroll
+    for (int q = 0; q < WG; ++q) {
+        const int r = 16 * (WG * wave + q) + (lane >> 2);
+        const int64_t rr = n0 + r < a.N ? r : a.N - 1 - n0;
+        wv2[q] = dual ? (uint32_t)((rr * a.ldw2 + 8 * ((lane & 3) ^ bg_swz(r))) * 2) : 0u;
+    }
+    const auto rw2 = __builtin_amdgcn_make_buffer_rsrc(
+        dual ? (void*)((const uint16_t*)a.W2 + n0 * a.ldw2) : (void*)nullptr, (short)0, 0x7fffffff,
+        kBufferDword3);
+    const auto rx2 = __builtin_amdgcn_make_buffer_rsrc(
+        dual ? (void*)((const uint16_t*)a.X2 + m0 * a.ldx2) : (void*)nullptr, (short)0, 0x7fffffff,
+        kBufferDword3);
     // the DMA requests of the stage holding k-tile k0 / C::BK, one instruction
     // per call of dma_one(q), q < DMA (so they can be spread over the MFMAs)
     auto dma_one = [&](int q, int64_t k0, uint16_t* Xs, uint16_t* Ws) {
         const int h = q / (XG + WG), p = q % (XG + WG);
+        const int64_t k = k0 + 32 * h;
+        const bool second = !GATHER && k >= K1;     // uniform: K1 is a multiple of the stage k
+        const uint32_t sk = (uint32_t)((second ? k - K1 : k) * 2);
         if (p < XG) {
-            auto rxh = rx;
-            uint32_t sx = (uint32_t)((k0 + 32 * h) * 2);
+            auto rxh = second ? rx2 : rx;
+            uint32_t sx = sk;
             if constexpr (GATHER) {
                 const void* src;
                 int64_t col;
-                gather_half(a, k0 + 32 * h, g, src, col);
+                gather_half(a, k, g, src, col);
                 rxh = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint16_t*)src + m0 * a.Nm),
                                                         (short)0, 0x7fffffff, kBufferDword3);
                 sx = (uint32_t)(col * 2);
             }
-            dma16(rxh, Xs + h * XH + 16 * (XG * wave + p) * 32, xv[p], sx);
+            dma16(rxh, Xs + h * XH + 16 * (XG * wave + p) * 32, second ? xv2[p] : xv[p], sx);
         } else {
             const int w = p - XG;
-            dma16(rw, Ws + h * WH + 16 * (WG * wave + w) * 32, wv[w], (uint32_t)((k0 + 32 * h) * 2));
+            dma16(second ? rw2 : rw, Ws + h * WH + 16 * (WG * wave + w) * 32, second ? wv2[w] : wv[w],
+                  sk);
         }
     };
     auto issue = [&](int64_t k0, uint16_t* Xs, uint16_t* Ws) {
@@ -445,8 +486,8 @@ gemm_bf16_big_kernel(GemmArgs a) {
     //           t's stage; read k-step 0 of t+1 (f0); MFMAs of k-step 1.
     //   KH = 1: MFMAs of the first half of the x-fragments; wait and barrier;
     //           request tile t+NS; read tile t+1 (f1); the second half; f0 = f1.
-    const int64_t nk = a.K / C::BK;
-    bg_static_for<NS>([&](auto s_) { issue(decltype(s_)::value * C::BK, xs(s_), ws(s_)); });
+    const int64_t nk = kspan / C::BK;
+    bg_static_for<NS>([&](auto s_) { issue(kbase + decltype(s_)::value * C::BK, xs(s_), ws(s_)); });
     wait_vmcnt<(NS - 1) * DMA>();
     __builtin_amdgcn_s_barrier();
     Frags f0, f1;
@@ -470,7 +511,7 @@ gemm_bf16_big_kernel(GemmArgs a) {
                 __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's reads of t landed
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (ISSUE) issue((t + NS) * C::BK, Xc, Wc);
+                if constexpr (ISSUE) issue(kbase + (t + NS) * C::BK, Xc, Wc);
                 read(f0, Xn, Wn, 0);
             }
             mma(f1, I0{}, IF{});
@@ -484,7 +525,7 @@ gemm_bf16_big_kernel(GemmArgs a) {
                 __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's reads of t landed
                 __builtin_amdgcn_s_barrier();
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (ISSUE) issue((t + NS) * C::BK, Xc, Wc);
+                if constexpr (ISSUE) issue(kbase + (t + NS) * C::BK, Xc, Wc);
                 read(f1, Xn, Wn, 0);
             }
             mma(f0, IH{}, IF{});
@@ -508,12 +549,36 @@ gemm_bf16_big_kernel(GemmArgs a) {
     // tiles take straight-line code with 8-byte stores (one variant per
     // gate / residual combination, chosen once per block); edge tiles check
     // every element.
+    const int64_t mrow = m0 + wm * C::WTM + (lane & 15);
+    const int64_t ncol = n0 + wn * C::WTN + (lane >> 4) * 4;
+    if (a.partial != nullptr) {
+        // split-K: raw fp32 sums of this split, 16-byte stores where all four
+        // columns are in range
+        float* part = a.partial + split * a.M * a.ldp;
+#pragma unroll
+        for (int i = 0; i < FI; ++i) {
+            const int64_t nb = ncol + i * 16;
+#pragma unroll
+            for (int j = 0; j < FJ; ++j) {
+                const int64_t m = mrow + j * 16;
+                if (m >= a.M || nb >= a.N) continue;
+                float* po = part + m * a.ldp + nb;
+                if (nb + 3 < a.N && ((a.ldp | nb) & 3) == 0) {
+                    *reinterpret_cast<float4*>(po) =
+                        make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (nb + r < a.N) po[r] = acc[i][j][r];
+                }
+            }
+        }
+        return;
+    }
     uint16_t* out = (uint16_t*)a.out;
     const uint16_t* gp = (const uint16_t*)a.gate_p;
     const uint16_t* rs = (const uint16_t*)a.residual;
     const int64_t ldc = a.ldc;
-    const int64_t mrow = m0 + wm * C::WTM + (lane & 15);
-    const int64_t ncol = n0 + wn * C::WTN + (lane >> 4) * 4;
     const bool whole = m0 + BG_M <= a.M && n0 + BG_N <= a.N && (ldc & 3) == 0 &&
                        (((uintptr_t)out | (uintptr_t)gp | (uintptr_t)rs) & 7) == 0 &&
                        ((uintptr_t)a.bias & 15) == 0;
@@ -1479,6 +1544,33 @@ extern "C" int64_t loom_linear_ln_workspace_bytes(int64_t M, int64_t N) {
     return kMaxSplit * M * N * (int64_t)sizeof(float);
 }
 
+// LayerNorm of the ns split-K partial sums (+ bias) of d's product, one block per row
+static int launch_splitk_ln(int64_t ns, const loom_linear_multi_desc* d, const float* workspace,
+                            const float* gamma, const float* beta, float eps, void* out, int64_t ldo,
+                            void* out_frag, hipStream_t st) {
+    const loom_linear_segment& g = d->seg[0];
+#define LOOM_SLN_KV(NS, KV)                                                                   \
+    hipLaunchKernelGGL((splitk_ln_kernel<bf16_t, NS, KV>), dim3((unsigned)d->m), dim3(64 * (KV)), \
+                       0, st, workspace, g.n, g.bias, gamma, beta, (bf16_t*)out, ldo, d->m,     \
+                       (int)g.n, eps, (bf16_t*)out_frag);
+#define LOOM_SLN(NS)                                                                          \
+    case NS:                                                                                  \
+        if (kv <= 1) { LOOM_SLN_KV(NS, 1) }                                                   \
+        else if (kv == 2) { LOOM_SLN_KV(NS, 2) }                                              \
+        else if (kv == 3) { LOOM_SLN_KV(NS, 3) }                                              \
+        else if (kv == 4) { LOOM_SLN_KV(NS, 4) }                                              \
+        else { LOOM_SLN_KV(NS, 8) }                                                           \
+        break;
+    const int kv = (int)ceil_div(g.n, 256);
+    switch (ns) {
+        LOOM_SLN(1) LOOM_SLN(2) LOOM_SLN(3) LOOM_SLN(4) LOOM_SLN(5) LOOM_SLN(6) LOOM_SLN(7)
+        LOOM_SLN(8)
+    }
+#undef LOOM_SLN_KV
+#undef LOOM_SLN
+    return launch_status("loom_linear_ln(layernorm)");
+}
+
 extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const float* gamma,
                               const float* beta, float eps, void* out, int64_t ldo, float* workspace,
                               int64_t workspace_bytes, void* out_frag, void* stream) {
@@ -1490,17 +1582,46 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
     LOOM_CHECK(g.n >= 1 && g.n <= 64 * 4 * kLnVec && ldo >= g.n,
                "linear_ln: N=%lld outside [1, %d]", (long long)g.n, 64 * 4 * kLnVec);
     hipStream_t st = (hipStream_t)stream;
-    bool fused = dtype == LOOM_BF16 && d->m >= 1 && d->m <= 64 && d->k % 8 == 0 && d->ldx % 8 == 0 &&
-                 ((uintptr_t)d->x & 15) == 0 && g.ldw % 8 == 0 && ((uintptr_t)g.w & 15) == 0 &&
-                 g.n % 4 == 0 && workspace != nullptr && ((uintptr_t)workspace & 15) == 0 &&
-                 ((((uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)g.bias) & 15) == 0) &&
-                 workspace_bytes >= loom_linear_ln_workspace_bytes(d->m, g.n) && frag_ok(*d);
+    // operands of the bf16 split-K forms (both read 16-byte pieces)
+    bool aligned = dtype == LOOM_BF16 && d->k % 8 == 0 && d->ldx % 8 == 0 &&
+                   ((uintptr_t)d->x & 15) == 0 && g.ldw % 8 == 0 && ((uintptr_t)g.w & 15) == 0 &&
+                   g.n % 4 == 0 && workspace != nullptr && ((uintptr_t)workspace & 15) == 0 &&
+                   ((((uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)g.bias) & 15) == 0) &&
+                   workspace_bytes >= loom_linear_ln_workspace_bytes(d->m, g.n);
     if (d->k2 > 0)
-        fused = fused && d->k2 % 8 == 0 && d->ldx2 % 8 == 0 && ((uintptr_t)d->x2 & 15) == 0 &&
-                g.ldw2 % 8 == 0 && ((uintptr_t)g.w2 & 15) == 0;
+        aligned = aligned && d->k2 % 8 == 0 && d->ldx2 % 8 == 0 && ((uintptr_t)d->x2 & 15) == 0 &&
+                  g.ldw2 % 8 == 0 && ((uintptr_t)g.w2 & 15) == 0;
+    const bool fused = aligned && d->m >= 1 && d->m <= 64 && frag_ok(*d);
     LOOM_CHECK(out_frag == nullptr || (fused && g.n % 32 == 0 && ((uintptr_t)out_frag & 15) == 0),
                "linear_ln: out_frag needs the bf16 split-K form (m <= 64, aligned) and n %% 32 == 0");
     if (!fused) {
+        // many rows: the 256 x 128 MFMA kernel over both inputs, split-K sums
+        // in the workspace, reduced with the bias in the LayerNorm kernel.
+        // Splits: whole rounds of the stages each; fewest block rounds times
+        // (k per split + ~320, the measured fixed cost of a block in k units).
+        using C = BgConf;
+        const int64_t K = d->k + d->k2;
+        const int64_t tiles = ceil_div(d->m, C::BG_M) * ceil_div(g.n, C::BG_N);
+        int64_t ns = 0, best = 0;
+        if (aligned && d->m >= C::BG_M && d->k % C::BK == 0)
+            for (int64_t q = 1; q <= kMaxSplit; ++q) {
+                if (K % (q * C::NS * C::BK) != 0) continue;
+                const int64_t cost = ceil_div(tiles * q, (int64_t)device_cus()) * (K / q + 320);
+                if (ns == 0 || cost < best) { ns = q; best = cost; }
+            }
+        if (ns > 0) {
+            GemmArgs a{};
+            a.X = d->x; a.ldx = d->ldx; a.W = g.w; a.ldw = g.ldw;
+            a.X2 = d->k2 > 0 ? d->x2 : nullptr; a.ldx2 = d->ldx2; a.W2 = g.w2; a.ldw2 = g.ldw2;
+            a.K1 = d->k;
+            a.M = d->m; a.N = g.n; a.K = K;
+            a.partial = workspace; a.ldp = g.n; a.nsplit = (int)ns;
+            hipLaunchKernelGGL((gemm_bf16_big_kernel<false, C>), dim3((unsigned)(tiles * ns)),
+                               dim3(64 * C::WAVES), 0, st, a);
+            const int rc = launch_status("loom_linear_ln");
+            if (rc != LOOM_OK) return rc;
+            return launch_splitk_ln(ns, d, workspace, gamma, beta, eps, out, ldo, nullptr, st);
+        }
         // y = product (+ bias) into seg.out, then LayerNorm of y
         int rc = loom_linear_multi(dtype, d, stream);
         if (rc != LOOM_OK) return rc;
@@ -1531,26 +1652,7 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
     launch_skinny_multi(a, grid, (int)ceil_div(d->m, 16), ceil_div(steps, ns), st);
     int rc = launch_status("loom_linear_ln");
     if (rc != LOOM_OK) return rc;
-#define LOOM_SLN_KV(NS, KV)                                                                   \
-    hipLaunchKernelGGL((splitk_ln_kernel<bf16_t, NS, KV>), dim3((unsigned)d->m), dim3(64 * (KV)), \
-                       0, st, workspace, g.n, g.bias, gamma, beta, (bf16_t*)out, ldo, d->m,     \
-                       (int)g.n, eps, (bf16_t*)out_frag);
-#define LOOM_SLN(NS)                                                                          \
-    case NS:                                                                                  \
-        if (kv <= 1) { LOOM_SLN_KV(NS, 1) }                                                   \
-        else if (kv == 2) { LOOM_SLN_KV(NS, 2) }                                              \
-        else if (kv == 3) { LOOM_SLN_KV(NS, 3) }                                              \
-        else if (kv == 4) { LOOM_SLN_KV(NS, 4) }                                              \
-        else { LOOM_SLN_KV(NS, 8) }                                                           \
-        break;
-    const int kv = (int)ceil_div(g.n, 256);
-    switch (ns) {
-        LOOM_SLN(1) LOOM_SLN(2) LOOM_SLN(3) LOOM_SLN(4) LOOM_SLN(5) LOOM_SLN(6) LOOM_SLN(7)
-        LOOM_SLN(8)
-    }
-#undef LOOM_SLN_KV
-#undef LOOM_SLN
-    return launch_status("loom_linear_ln(layernorm)");
+    return launch_splitk_ln(ns, d, workspace, gamma, beta, eps, out, ldo, out_frag, st);
 }
 
 extern "C" int64_t loom_ffn_decode_desc_bytes(void) { return (int64_t)sizeof(loom_ffn_decode_desc); }

@@ -101,6 +101,20 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     def lin(x, w, out, rows, nout, k, **kw):
         eng._linear(x, w, out, rows, nout, k, **kw)
 
+    # LayerNorm(x w^T + x2 w2^T + bias) -> h (y: the product, on the unfused path)
+    ln_ws = torch.empty(_lib.load().loom_linear_ln_workspace_bytes(M, N) // 4, dtype=torch.float32,
+                        device=dev)
+
+    descs = {}
+
+    def lin_ln(key, x, w, x2, w2, bias, gamma, beta_ln, rows):
+        dsc = descs.get((key, rows))
+        if dsc is None:
+            dsc = descs[(key, rows)] = _lib.linear_multi_desc(
+                x[:rows], [dict(w=w, w2=w2, out=y[:rows], bias=bias)], x2=x2[:rows])
+        call("loom_linear_ln", code, _lib.ctypes.byref(dsc), _P(gamma), _P(beta_ln), 1e-5, _P(h), N,
+             _P(ln_ws), ln_ws.numel() * 4, None, st)
+
     def depth(sub, out, rows):
         eng.depth_read(sub, hist, out, rows)
 
@@ -128,10 +142,8 @@ def prefill(eng, prompt: torch.Tensor) -> None:
                  _P(q), _P(cbuf), _P(kctx), N, B, Tc, s, eng.max_len, QH, KVH, HD, st)
             # ---- LN(o(C) + w_o(depth read 2*bi)) (loomformer.py:3999-4000)
             depth(sub, d, rows)
-            lin(cbuf, blk["o"], y, rows, N, N)
-            lin(d, eng.wo_for(sub), y, rows, N, N, residual=y)
-            call("loom_add_layernorm", code, _P(y), None, _P(blk["ln1_w"]), _P(blk["ln1_b"]),
-                 _P(h), rows, N, 1e-5, st)
+            lin_ln(("attn", bi), cbuf, blk["o"], d, eng.wo_for(sub), None, blk["ln1_w"], blk["ln1_b"],
+                   rows)
             # ---- history slot 2*bi+1, W_real (+ gate with the previous block's p)
             sub += 1
             lin(h, eng.kvw, hv[:, sub], rows, 2 * N, N, ldc=2 * L * 2 * N)
@@ -167,10 +179,8 @@ def prefill(eng, prompt: torch.Tensor) -> None:
                  bi % 3, st)
             carry_i, p_i = out_i, new_p
             # ---- LN(w_o(d_h) + W2(act) + b2) (loomformer.py:4045)
-            lin(dh, eng.wo_for(sub), y, rows, N, N)
-            lin(act, blk["w2"], y, rows, N, H, bias=blk["b2"], residual=y)
-            call("loom_add_layernorm", code, _P(y), None, _P(blk["ln2_w"]), _P(blk["ln2_b"]),
-                 _P(h), rows, N, 1e-5, st)
+            lin_ln(("ffn", bi), dh, eng.wo_for(sub), act, blk["w2"], blk["b2"], blk["ln2_w"],
+                   blk["ln2_b"], rows)
             if not last:
                 sub += 1
                 lin(h, eng.kvw, hv[:, sub], rows, 2 * N, N, ldc=2 * L * 2 * N)

@@ -603,13 +603,17 @@ def test_ffn_decode_with_depth_read(dtype, M, rms, slots):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("M,K2", [(1, 768), (32, 768), (32, 3072), (64, 3072), (7, 0)])
-def test_linear_ln(dtype, M, K2):
+@pytest.mark.parametrize("M,K2,N", [(1, 768, 768), (32, 768, 768), (32, 3072, 768), (64, 3072, 768),
+                                    (7, 0, 768), (4096, 768, 768), (4096, 3072, 768),
+                                    (300, 768, 768), (512, 0, 768), (520, 768, 200)])
+def test_linear_ln(dtype, M, K2, N):
     """LayerNorm(x w^T + x2 w2^T + b): split-K partial sums reduced inside the
-    LayerNorm kernel (bf16) or product + LayerNorm (fp32), against torch."""
+    LayerNorm kernel (bf16: the skinny form up to 64 rows, the 256 x 128 MFMA
+    tiles over both inputs from 256 rows on, edge rows and columns included) or
+    product + LayerNorm (fp32), against torch."""
     from loom_amd import _lib
-    g = torch.Generator().manual_seed(M + K2)
-    N, K = 768, 768
+    g = torch.Generator().manual_seed(M + K2 + N)
+    K = 768
     r = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(DEV, dtype)
     x = r(M, K)
     w = r(N, K, sc=K ** -0.5)
