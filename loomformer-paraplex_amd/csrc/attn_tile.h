@@ -17,16 +17,20 @@ __device__ __forceinline__ int kv_swz(int r) { return (((r >> 1) & 1) << 1) | ((
 typedef short gqa_v4s __attribute__((ext_vector_type(4)));
 typedef uint32_t gqa_u4 __attribute__((ext_vector_type(4)));   // a 16-byte piece as a native vector
 
-// B fragment of 32 positions x 16 dims (dims 16*dt..) from a row-major tile:
-// lane l gets positions 8*(l/16)..+7 of dim 16*dt + l%16, as two transposing
-// 8-byte reads (lane r of a 16-lane group points at row k0 + r/4, dims
-// 16*dt + 4*(r%4)..+3 and receives rows k0..k0+3 of dim 16*dt + r).
+// B fragment of 32 positions x 16 dims (dims 16*dt..) from a row-major tile,
+// its 8 positions per lane in the order of a score tile's registers: lane
+// group q (= l/16) gets rows 4q..4q+3 and 16+4q..16+4q+3 of dim 16*dt + l%16,
+// the positions whose probabilities the lanes of group q hold after
+// S^T = K Q^T (result register r of 16-row half hf is row 16*hf + 4q + r), so
+// P feeds P V and P K straight from registers.  Two transposing 8-byte reads:
+// lane r of a 16-lane group points at row k0 + r/4, dims 16*dt + 4*(r%4)..+3
+// and receives rows k0..k0+3 of dim 16*dt + r (k0 = 16*h + 4q).
 template <int CPR>
 __device__ __forceinline__ uint4 tile_tr_frag(const gqa_u4* tile, int dt, int lq, int lr) {
     uint32_t w[4];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const int row = 8 * lq + 4 * h + (lr >> 2);
+        const int row = 16 * h + 4 * lq + (lr >> 2);
         const int c = 2 * dt + ((lr & 3) >> 1);
         const char* p = reinterpret_cast<const char*>(tile + row * CPR + (c ^ kv_swz(row))) + 8 * (lr & 1);
         const gqa_v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(

@@ -452,8 +452,10 @@ __device__ __forceinline__ f32x4_t mfma16(gqa_u4 a, uint4 b, f32x4_t c) {
 // piece j % (HD/8): 1 KB contiguous per load instruction when the position
 // stride is HD), stored to the wave's LDS tiles row-major, and read back as
 //   S^T = K Q^T      A = 16 K rows (16-byte reads), B = the G query heads;
-//   C = P V, Kctx = P K   B = 8 positions of one dimension per lane through
-//                    the gfx950 transposing LDS read (ds_read_b64_tr_b16).
+//   C = P V, Kctx = P K   A = P straight from the score registers,
+//                    B = 8 positions of one dimension per lane through the
+//                    gfx950 transposing LDS read (ds_read_b64_tr_b16), in the
+//                    score registers' position order (tile_tr_frag).
 // The next tile's loads are in flight while a tile is computed; the waves
 // never wait for each other inside the loop.
 // 2 waves per SIMD (<= 256 VGPRs; the chunking makes about 1.5 blocks per CU):
@@ -469,8 +471,6 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     struct Tiles {
         gqa_u4 k[kMfTile * CPR];           // K tile, row-major (swizzled pieces)
         gqa_u4 v[kMfTile * CPR];
-        uint16_t pt[16][kMfTile];          // P: [head][position]
-        float cr[16];                      // per-head rescale of this step
     };
     constexpr int kTileBytes = 4 * (int)sizeof(Tiles);
     constexpr int kRedBytes = 4 * REC * (int)sizeof(float);
@@ -628,26 +628,28 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
         const float mnew = fmaxf(mh, mx);
         // nothing seen yet (mnew = -inf): keep the zero state; otherwise 0 on the first step
         const float corr = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(mh - mnew);
-        float ls = 0.0f;
+        float ls = 0.0f, pv[2][4];
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float pv = sv[hf][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[hf][r] - mnew);
-                ls += pv;
-                tl.pt[lr][16 * hf + 4 * lq + r] = f32_to_bf16(pv);
+                pv[hf][r] = sv[hf][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[hf][r] - mnew);
+                ls += pv[hf][r];
             }
         ls += __shfl_xor(ls, 16, 64);
         ls += __shfl_xor(ls, 32, 64);
         lh = fmaf(lh, corr, ls);
         mh = mnew;
-        if (lq == 0) tl.cr[lr] = corr;
-        wave_lds_fence();
-        // rescale the accumulators (rows = heads 4*lq + r) and add P V, P K
+        // A operand of P V / P K straight from the score registers: head lr,
+        // positions 4*lq + r and 16 + 4*lq + r (bf16 like the reference's
+        // softmax output), matched by tile_tr_frag
+        const uint4 pa = make_uint4(pack_bf16x2(pv[0][0], pv[0][1]), pack_bf16x2(pv[0][2], pv[0][3]),
+                                    pack_bf16x2(pv[1][0], pv[1][1]), pack_bf16x2(pv[1][2], pv[1][3]));
+        // rescale the accumulators (rows = heads 4*lq + r: their factors from
+        // the lanes of those heads) and add P V, P K
         float cf[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) cf[r] = tl.cr[4 * lq + r];
-        const uint4 pa = *reinterpret_cast<const uint4*>(&tl.pt[lr][8 * lq]);
+        for (int r = 0; r < 4; ++r) cf[r] = __shfl(corr, 4 * lq + r, 64);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll

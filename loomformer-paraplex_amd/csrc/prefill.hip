@@ -259,8 +259,10 @@ gqa_prefill_kernel(PrefillArgs<T> a) {
 // holds row/column l%16, k = 8*(l/16)..+7; result [4*(l/16)+r][l%16] in r):
 //   S^T = K Q^T   A = 16 cached rows (16-byte reads of the row-major K tile),
 //                 B = 16 query positions of one head
-//   C   = P V     A = P (rows = query positions, k = 32 cached rows, bf16),
-//   Kctx= P K     B = V / K through the transposing LDS read (attn_tile.h).
+//   C   = P V     A = P (rows = query positions, k = 32 cached rows, bf16)
+//   Kctx= P K         straight from the score registers,
+//                 B = V / K through the transposing LDS read in the score
+//                 registers' row order (tile_tr_frag, attn_tile.h).
 // Block (x, y, b): y = kvh * HSPLIT + part; wave w takes head
 // kvh*G + part*GP + w%GP and query tile x*QTB + w/GP (16 positions each).
 // The block streams 32 cached rows per step into two LDS buffers: the next
@@ -298,8 +300,7 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     constexpr int PPT = (2 * PIECES + 255) / 256;
     __shared__ __align__(16) gqa_u4 tk[2][PIECES];       // K tile, row-major, two buffers
     __shared__ __align__(16) gqa_u4 tv[2][PIECES];       // V tile
-    __shared__ __align__(16) uint16_t pt[4][16][kPfRows];
-    __shared__ float cr[4][16];
+    __shared__ float cr[4][16];                           // per-column rescale of a step
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 15, lq = lane >> 4;
     const int kvh = blockIdx.y / HSPLIT, part = blockIdx.y % HSPLIT;
@@ -394,25 +395,31 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
             const float mnew = fmaxf(mh, mx);               // finite: row 0 is seen at step 0
             const float corr = __builtin_amdgcn_exp2f(mh - mnew);
-            float ls = 0.0f;
+            float ls = 0.0f, pv[2][4];
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float p = sv[hf][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[hf][r] - mnew);
-                    ls += p;
-                    pt[wave][lr][16 * hf + 4 * lq + r] = f32_to_bf16(p);
+                    pv[hf][r] = sv[hf][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[hf][r] - mnew);
+                    ls += pv[hf][r];
                 }
             ls += __shfl_xor(ls, 16, 64);
             ls += __shfl_xor(ls, 32, 64);
             lh = fmaf(lh, corr, ls);
             mh = mnew;
+            // A operand of P V / P K straight from the score registers: query
+            // column lr, positions 4*lq + r and 16 + 4*lq + r (bf16 like the
+            // reference's softmax output), matched by tile_tr_frag
+            const uint4 pa = make_uint4(pack_bf16x2(pv[0][0], pv[0][1]), pack_bf16x2(pv[0][2], pv[0][3]),
+                                        pack_bf16x2(pv[1][0], pv[1][1]), pack_bf16x2(pv[1][2], pv[1][3]));
+            // the accumulator rows are query columns 4*lq + r: their rescale
+            // from the lanes that hold those columns, through LDS (measured
+            // faster here than four cross-lane permutes)
             if (lq == 0) cr[wave][lr] = corr;
-            wave_lds_fence();                  // P and the rescale of this wave
+            wave_lds_fence();
             float cf[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) cf[r] = cr[wave][4 * lq + r];
-            const uint4 pa = *reinterpret_cast<const uint4*>(&pt[wave][lr][8 * lq]);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
@@ -423,7 +430,7 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
                 accC[dt] = mfma16p(pa, tile_tr_frag<CPR>(tv[cur], dt, lq, lr), accC[dt]);
                 accK[dt] = mfma16p(pa, tile_tr_frag<CPR>(tk[cur], dt, lq, lr), accK[dt]);
             }
-            wave_lds_fence();                  // pt / cr are rewritten next step
+            wave_lds_fence();                  // cr is rewritten next step
         }
         // the next tile into the other buffer (last read two steps ago, before
         // the previous barrier), then one barrier for both
@@ -431,14 +438,13 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
         lds_sync();
     }
     // normalise: the sum of query column c lives in lanes with lr == c
-    if (lq == 0) cr[wave][lr] = lh;
-    lds_sync();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int col = 4 * lq + r;
         const int qi = q0 + col;
+        const float lsum = __shfl(lh, col, 64);
         if (qi >= a.Tc) continue;
-        const float inv = 1.0f / cr[wave][col];
+        const float inv = 1.0f / lsum;
         const int64_t o = (b * a.Tc + qi) * a.out_ld + (int64_t)head * HD;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
