@@ -118,6 +118,15 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     def depth(sub, out, rows):
         eng.depth_read(sub, hist, out, rows)
 
+    main = torch.cuda.current_stream(dev)
+    aux = torch.cuda.Stream(device=dev)
+
+    def fork():                 # aux continues after everything queued on main so far
+        aux.wait_stream(main)
+
+    def join():                 # main continues after everything queued on aux so far
+        main.wait_stream(aux)
+
     have_state = False
     tin = 0
     seed_valid = z(B, dtype=torch.uint8)
@@ -134,24 +143,35 @@ def prefill(eng, prompt: torch.Tensor) -> None:
         lin(h, eng.blocks[0]["qkv"], qkv, rows, N + 2 * c.KV, N)
         sub = 0
         carry_i, p_i = None, None
+        # Two streams, default priority: `aux` runs the work of a layer that
+        # does not depend on the depth history (qkv -> attention, W_real) while
+        # the main stream runs the history projections and depth reads; they
+        # meet before every product that needs both.
+        fork()
         for bi, blk in enumerate(eng.blocks):
             last = bi == L - 1
-            # ---- attention over the cache (rows < s) and this chunk (loomformer.py:3215-3332)
-            call("loom_gqa_prefill", code, _P(qkv), N + 2 * c.KV, _P(eng.k_cache[bi]),
-                 _P(eng.v_cache[bi]), cache_sb, cache_st, cache_sh, _P(eng.cos), _P(eng.sin),
-                 _P(q), _P(cbuf), _P(kctx), N, B, Tc, s, eng.max_len, QH, KVH, HD, st)
-            # ---- LN(o(C) + w_o(depth read 2*bi)) (loomformer.py:3999-4000)
+            # ---- attention over the cache (rows < s) and this chunk (loomformer.py:3215-3332),
+            # on aux after this layer's qkv; the depth read 2*bi on main
+            with torch.cuda.stream(aux):
+                call("loom_gqa_prefill", code, _P(qkv), N + 2 * c.KV, _P(eng.k_cache[bi]),
+                     _P(eng.v_cache[bi]), cache_sb, cache_st, cache_sh, _P(eng.cos), _P(eng.sin),
+                     _P(q), _P(cbuf), _P(kctx), N, B, Tc, s, eng.max_len, QH, KVH, HD, eng._stream())
             depth(sub, d, rows)
+            join()
+            # ---- LN(o(C) + w_o(depth read 2*bi)) (loomformer.py:3999-4000)
             lin_ln(("attn", bi), cbuf, blk["o"], d, eng.wo_for(sub), None, blk["ln1_w"], blk["ln1_b"],
                    rows)
-            # ---- history slot 2*bi+1, W_real (+ gate with the previous block's p)
+            # ---- W_real (+ gate with the previous block's p) on aux; history slot
+            # 2*bi+1 and its depth read on main
             sub += 1
+            fork()
+            with torch.cuda.stream(aux):
+                if p_i is None:
+                    lin(h, blk["w1r"], R, rows, H, N, bias=blk["b1r"])
+                else:
+                    lin(h, blk["w1r"], R, rows, H, N, bias=blk["b1r"], gate_p=pbuf[p_i],
+                        gate_alpha=blk["alpha"])
             lin(h, eng.kvw, hv[:, sub], rows, 2 * N, N, ldc=2 * L * 2 * N)
-            if p_i is None:
-                lin(h, blk["w1r"], R, rows, H, N, bias=blk["b1r"])
-            else:
-                lin(h, blk["w1r"], R, rows, H, N, bias=blk["b1r"], gate_p=pbuf[p_i],
-                    gate_alpha=blk["alpha"])
             depth(sub, dh, rows)
             # ---- Paraplex FFN (loomformer.py:2818-2893): beta space, fused pointwise
             # chain with the phase trace carried from the previous chunk; the
@@ -163,6 +183,7 @@ def prefill(eng, prompt: torch.Tensor) -> None:
             if c.gate_proj:
                 gsrc = gbuf
                 lin(h, blk["gpw"], gbuf, rows, H, N, bias=blk["gpb"])
+            join()
             call("loom_paraplex_forward", code, _P(R), _P(gsrc), _P(beta), _P(blk["ib"]),
                  _P(traces[tin, bi]), _P(blk["tw"]), empty_reset, _P(blk["anchor"]), _P(act),
                  _P(sbuf), _P(traces[1 - tin, bi]), _P(snap), B, Tc, H, float(c.powlu_m), st)
@@ -182,9 +203,12 @@ def prefill(eng, prompt: torch.Tensor) -> None:
             lin_ln(("ffn", bi), dh, eng.wo_for(sub), act, blk["w2"], blk["b2"], blk["ln2_w"],
                    blk["ln2_b"], rows)
             if not last:
+                # next history slot (main) and the next block's qkv (aux)
                 sub += 1
+                fork()
+                with torch.cuda.stream(aux):
+                    lin(h, eng.blocks[bi + 1]["qkv"], qkv, rows, N + 2 * c.KV, N)
                 lin(h, eng.kvw, hv[:, sub], rows, 2 * N, N, ldc=2 * L * 2 * N)
-                lin(h, eng.blocks[bi + 1]["qkv"], qkv, rows, N + 2 * c.KV, N)
         # ---- temporal carry over the chunk: restart at position 0 and at a
         # seeded first token, else continue from the state (loomformer.py:3834-3850)
         reset = z(B, Tc, dtype=torch.uint8)
