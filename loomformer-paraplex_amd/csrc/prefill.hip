@@ -319,9 +319,12 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
 
     const bf16_t* kb = a.kc + b * a.csb + kvh * a.csh;
     const bf16_t* vb = a.vc + b * a.csb + kvh * a.csh;
-    // one 32-row tile: piece p -> (tensor, row, piece of the row), rows clamped to kmax
-    gqa_u4 reg[PPT];
-    auto load_tile = [&](int64_t r0) {
+    // one 32-row tile: piece p -> (tensor, row, piece of the row), rows clamped
+    // to kmax; two register sets, so a tile is requested two steps before its
+    // LDS store (tile t in set t % 2)
+    gqa_u4 reg[2][PPT];
+    auto load_tile = [&](auto set_, int64_t r0) {
+        constexpr int SET = decltype(set_)::value;
 #pragma unroll
         for (int u = 0; u < PPT; ++u) {
             const int p = tid + 256 * u;
@@ -331,23 +334,27 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
                 int64_t r = r0 + row;
                 r = r <= kmax ? r : kmax;
                 const bf16_t* src = (tensor == 0 ? kb : vb) + r * a.cst + 8 * ch;
-                reg[u] = *reinterpret_cast<const gqa_u4*>(src);
+                reg[SET][u] = *reinterpret_cast<const gqa_u4*>(src);
             }
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_tile = [&](auto set_) {      // into LDS buffer SET
+        constexpr int SET = decltype(set_)::value;
 #pragma unroll
         for (int u = 0; u < PPT; ++u) {
             const int p = tid + 256 * u;
             if (p < 2 * PIECES) {
                 const int tensor = p / PIECES, q = p % PIECES;
                 const int row = q / CPR, ch = q % CPR;
-                gqa_u4* dst = tensor == 0 ? tk[buf] : tv[buf];
-                dst[row * CPR + (ch ^ kv_swz(row))] = reg[u];
+                gqa_u4* dst = tensor == 0 ? tk[SET] : tv[SET];
+                dst[row * CPR + (ch ^ kv_swz(row))] = reg[SET][u];
             }
         }
     };
-    load_tile(0);
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    load_tile(S0{}, 0);
+    if (nsteps > 1) load_tile(S1{}, kPfRows);
     // B operand of S^T: q of query column lr, dims 32*kk + 8*lq .. +7
     uint4 qf[KK];
     {
@@ -357,7 +364,7 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
         for (int kk = 0; kk < KK; ++kk)
             qf[kk] = *reinterpret_cast<const uint4*>(qp + 32 * kk + 8 * lq);
     }
-    store_tile(0);
+    store_tile(S0{});
     lds_sync();
 
     float mh = -INFINITY, lh = 0.0f;      // running max / sum of query column lr
@@ -365,10 +372,13 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) accC[dt] = accK[dt] = f32x4_p{0.f, 0.f, 0.f, 0.f};
 
-    for (int it = 0; it < nsteps; ++it) {
-        const int cur = it & 1;
+    // step it computes tile it from LDS buffer it % 2, requests tile it+2 into
+    // register set it % 2 (its tile it went to LDS a step ago) and stores
+    // tile it+1 (requested a step ago) into the other buffer
+    auto step = [&](auto set_, int it) {
+        constexpr int cur = decltype(set_)::value;
         const int64_t r0 = (int64_t)it * kPfRows;
-        if (it + 1 < nsteps) load_tile(r0 + kPfRows);
+        if (it + 2 < nsteps) load_tile(set_, r0 + 2 * kPfRows);
         const bool active = r0 <= wave_kmax;                 // wave-uniform
         if (active) {
             f32x4_p sc[2];
@@ -434,8 +444,12 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
         }
         // the next tile into the other buffer (last read two steps ago, before
         // the previous barrier), then one barrier for both
-        if (it + 1 < nsteps) store_tile(cur ^ 1);
+        if (it + 1 < nsteps) store_tile(std::integral_constant<int, cur ^ 1>{});
         lds_sync();
+    };
+    for (int it = 0; it < nsteps; it += 2) {
+        step(S0{}, it);
+        if (it + 1 < nsteps) step(S1{}, it + 1);
     }
     // normalise: the sum of query column c lives in lanes with lr == c
 #pragma unroll
