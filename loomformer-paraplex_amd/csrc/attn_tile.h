@@ -17,6 +17,45 @@ __device__ __forceinline__ int kv_swz(int r) { return (((r >> 1) & 1) << 1) | ((
 typedef short gqa_v4s __attribute__((ext_vector_type(4)));
 typedef uint32_t gqa_u4 __attribute__((ext_vector_type(4)));   // a 16-byte piece as a native vector
 
+// Lane constants of the fragment reads of a row-major tile (byte offsets
+// within the tile), computed once per kernel so that every read is one LDS
+// instruction with a compile-time offset:
+//   s_off[hf]: the A operand of S^T = K Q^T, 16-byte read of row 16*hf + l%16,
+//     piece 4*kk + l/16 -> s_off[hf] + 64*kk (the swizzle only touches the
+//     piece's low two bits);
+//   t_off[p][h]: tile_tr_frag's read h of dim tile dt with dt % 2 == p ->
+//     t_off[p][h] + 64*(dt/2) (piece (2*dt + b) ^ kv_swz(row) is
+//     4*(dt/2) + a lane constant for each parity of dt).
+template <int CPR>
+struct TileLane {
+    uint32_t s_off[2];
+    uint32_t t_off[2][2];
+    __device__ __forceinline__ TileLane(int lq, int lr) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int row = 16 * hf + lr;
+            s_off[hf] = (uint32_t)((row * CPR + (lq ^ kv_swz(row))) * 16);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int row = 16 * h + 4 * lq + (lr >> 2);
+            const int sw = kv_swz(row), b1 = (lr & 3) >> 1;
+#pragma unroll
+            for (int par = 0; par < 2; ++par) {
+                const int q = ((par ^ (sw >> 1)) << 1) | (b1 ^ (sw & 1));
+                t_off[par][h] = (uint32_t)((row * CPR + q) * 16 + 8 * (lr & 1));
+            }
+        }
+    }
+};
+
+// A operand of S^T (16 K rows x 32 dims of k-step kk) from a row-major tile
+template <int CPR>
+__device__ __forceinline__ gqa_u4 tile_s_frag(const gqa_u4* tile, const TileLane<CPR>& L, int hf,
+                                              int kk) {
+    return *reinterpret_cast<const gqa_u4*>(reinterpret_cast<const char*>(tile) + L.s_off[hf] + 64 * kk);
+}
+
 // B fragment of 32 positions x 16 dims (dims 16*dt..) from a row-major tile,
 // its 8 positions per lane in the order of a score tile's registers: lane
 // group q (= l/16) gets rows 4q..4q+3 and 16+4q..16+4q+3 of dim 16*dt + l%16,
@@ -26,19 +65,15 @@ typedef uint32_t gqa_u4 __attribute__((ext_vector_type(4)));   // a 16-byte piec
 // lane r of a 16-lane group points at row k0 + r/4, dims 16*dt + 4*(r%4)..+3
 // and receives rows k0..k0+3 of dim 16*dt + r (k0 = 16*h + 4q).
 template <int CPR>
-__device__ __forceinline__ uint4 tile_tr_frag(const gqa_u4* tile, int dt, int lq, int lr) {
-    uint32_t w[4];
+__device__ __forceinline__ uint4 tile_tr_frag(const gqa_u4* tile, const TileLane<CPR>& L, int dt) {
+    uint2 w[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const int row = 16 * h + 4 * lq + (lr >> 2);
-        const int c = 2 * dt + ((lr & 3) >> 1);
-        const char* p = reinterpret_cast<const char*>(tile + row * CPR + (c ^ kv_swz(row))) + 8 * (lr & 1);
-        const gqa_v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) gqa_v4s*)(p));
-        w[2 * h] = (uint32_t)(uint16_t)x[0] | ((uint32_t)(uint16_t)x[1] << 16);
-        w[2 * h + 1] = (uint32_t)(uint16_t)x[2] | ((uint32_t)(uint16_t)x[3] << 16);
+        const char* p = reinterpret_cast<const char*>(tile) + L.t_off[dt & 1][h] + 64 * (dt >> 1);
+        w[h] = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                             (__attribute__((address_space(3))) gqa_v4s*)(p)));
     }
-    return make_uint4(w[0], w[1], w[2], w[3]);
+    return make_uint4(w[0].x, w[0].y, w[1].x, w[1].y);
 }
 
 // LDS ordering inside one wave (its LDS operations execute in order): keeps

@@ -497,6 +497,8 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     const int64_t t1 = t0 + clen < len ? t0 + clen : len;
     const int QKV = (a.QH + 2 * a.KVH) * HD;
     Tiles& tl = reinterpret_cast<Tiles*>(lds)[wave];
+    const TileLane<CPR> tln(lq, lr);
+    const int span = (int)(t1 - t0);         // positions of this chunk (< 2^31)
 
     const bf16_t* kb = a.kc + b * a.csb + kvh * a.csh;
     const bf16_t* vb = a.vc + b * a.csb + kvh * a.csh;
@@ -608,10 +610,9 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
             sc[hf] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            const int row = 16 * hf + lr;
 #pragma unroll
             for (int kk = 0; kk < KK; ++kk)
-                sc[hf] = mfma16(tl.k[row * CPR + ((4 * kk + lq) ^ kv_swz(row))], qf[kk], sc[hf]);
+                sc[hf] = mfma16(tile_s_frag<CPR>(tl.k, tln, hf, kk), qf[kk], sc[hf]);
         }
         float mx = -INFINITY;
         float sv[2][4];
@@ -619,7 +620,7 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const bool ok = ts + 16 * hf + 4 * lq + r < t1;
+                const bool ok = (int)(ts - t0) + 16 * hf + 4 * lq + r < span;
                 sv[hf][r] = ok ? sc[hf][r] * a.qscale : -INFINITY;
                 mx = fmaxf(mx, sv[hf][r]);
             }
@@ -647,18 +648,23 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
                                     pack_bf16x2(pv[1][0], pv[1][1]), pack_bf16x2(pv[1][2], pv[1][3]));
         // rescale the accumulators (rows = heads 4*lq + r: their factors from
         // the lanes of those heads) and add P V, P K
-        float cf[4];
+        // (skipped when no head's max moved: every factor exactly 1)
+        if (__any(corr != 1.0f)) {
+            float cf[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) cf[r] = __shfl(corr, 4 * lq + r, 64);
+            for (int r = 0; r < 4; ++r) cf[r] = __shfl(corr, 4 * lq + r, 64);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    accC[dt][r] *= cf[r];
+                    accK[dt][r] *= cf[r];
+                }
+        }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                accC[dt][r] *= cf[r];
-                accK[dt][r] *= cf[r];
-            }
-            accC[dt] = mfma16(pa, tile_tr_frag<CPR>(tl.v, dt, lq, lr), accC[dt]);
-            accK[dt] = mfma16(pa, tile_tr_frag<CPR>(tl.k, dt, lq, lr), accK[dt]);
+            accC[dt] = mfma16(pa, tile_tr_frag<CPR>(tl.v, tln, dt), accC[dt]);
+            accK[dt] = mfma16(pa, tile_tr_frag<CPR>(tl.k, tln, dt), accK[dt]);
         }
     }
     __syncthreads();                       // every wave is done with its tiles (wred aliases them)

@@ -314,6 +314,8 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     // attends to row 0 only (finite, never stored)
     const int qcol = q0 + lr;
     const int64_t qpos = qcol < a.Tc ? a.start + qcol : 0;
+    const int qpos32 = (int)qpos;          // positions fit 31 bits (checked by the host)
+    const TileLane<CPR> tl(lq, lr);
     const int wave_qlast = min(q0 + 15, a.Tc - 1);
     const int64_t wave_kmax = q0 < a.Tc ? a.start + wave_qlast : -1;
 
@@ -385,10 +387,9 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
                 sc[hf] = f32x4_p{0.f, 0.f, 0.f, 0.f};
-                const int row = 16 * hf + lr;
 #pragma unroll
                 for (int kk = 0; kk < KK; ++kk)
-                    sc[hf] = mfma16p(tk[cur][row * CPR + ((4 * kk + lq) ^ kv_swz(row))], qf[kk], sc[hf]);
+                    sc[hf] = mfma16p(tile_s_frag<CPR>(tk[cur], tl, hf, kk), qf[kk], sc[hf]);
             }
             // S^T[row 16*hf + 4*lq + r][query column lr]
             float sv[2][4];
@@ -397,8 +398,8 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
             for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int64_t row = r0 + 16 * hf + 4 * lq + r;
-                    sv[hf][r] = row <= qpos ? sc[hf][r] * a.qscale : -INFINITY;
+                    const int row = (int)r0 + 16 * hf + 4 * lq + r;
+                    sv[hf][r] = row <= qpos32 ? sc[hf][r] * a.qscale : -INFINITY;
                     mx = fmaxf(mx, sv[hf][r]);
                 }
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -424,23 +425,28 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
                                         pack_bf16x2(pv[1][0], pv[1][1]), pack_bf16x2(pv[1][2], pv[1][3]));
             // the accumulator rows are query columns 4*lq + r: their rescale
             // from the lanes that hold those columns, through LDS (measured
-            // faster here than four cross-lane permutes)
-            if (lq == 0) cr[wave][lr] = corr;
-            wave_lds_fence();
-            float cf[4];
+            // faster here than four cross-lane permutes); skipped when no
+            // column's max moved (every factor exactly 1)
+            if (__any(corr != 1.0f)) {
+                if (lq == 0) cr[wave][lr] = corr;
+                wave_lds_fence();
+                float cf[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) cf[r] = cr[wave][4 * lq + r];
+                for (int r = 0; r < 4; ++r) cf[r] = cr[wave][4 * lq + r];
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        accC[dt][r] *= cf[r];
+                        accK[dt][r] *= cf[r];
+                    }
+                wave_lds_fence();              // cr is rewritten next step
+            }
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    accC[dt][r] *= cf[r];
-                    accK[dt][r] *= cf[r];
-                }
-                accC[dt] = mfma16p(pa, tile_tr_frag<CPR>(tv[cur], dt, lq, lr), accC[dt]);
-                accK[dt] = mfma16p(pa, tile_tr_frag<CPR>(tk[cur], dt, lq, lr), accK[dt]);
+                accC[dt] = mfma16p(pa, tile_tr_frag<CPR>(tv[cur], tl, dt), accC[dt]);
+                accK[dt] = mfma16p(pa, tile_tr_frag<CPR>(tk[cur], tl, dt), accK[dt]);
             }
-            wave_lds_fence();                  // cr is rewritten next step
         }
         // the next tile into the other buffer (last read two steps ago, before
         // the previous barrier), then one barrier for both
@@ -572,6 +578,7 @@ extern "C" int loom_gqa_prefill(int dtype, const void* qkv, int64_t qkv_ld, void
     LOOM_CHECK(cache_stride_t >= HD && cache_stride_h >= HD,
                "gqa_prefill: cache strides smaller than a head row");
     LOOM_CHECK(T <= (1 << 20), "gqa_prefill: chunk of %lld tokens too long", (long long)T);
+    LOOM_CHECK(start + T < (1LL << 31), "gqa_prefill: positions beyond 2^31");
     LOOM_CHECK(start + T <= cache_len,
                "gqa_prefill: positions %lld..%lld beyond the cache capacity %lld", (long long)start,
                (long long)(start + T - 1), (long long)cache_len);
