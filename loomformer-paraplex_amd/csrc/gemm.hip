@@ -1640,10 +1640,13 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
     const int64_t ntiles = ceil_div(g.n, 16);
     for (int s2 = 0; s2 <= kMaxSeg; ++s2) a.nstart[s2] = s2 == 0 ? 0 : ntiles * 16;
     const int64_t steps = ceil_div(d->k, 32) + ceil_div(d->k2, 32);
-    // about two blocks per CU (up to kMaxSplit k-splits; measured best over 1x-4x),
-    // at least 4 k-steps per split
+    // about two blocks per CU, at most kSkinnyLnSplit k-splits (each split is
+    // one more partial row the LayerNorm kernel reads: at N = 768, K = 1536 /
+    // 3840, 4 splits measured 6.8 / 8.3 us per call against 7.3 / 8.7 with 8
+    // and 7.5 / 11.0 with 2), at least 4 k-steps per split
+    constexpr int64_t kSkinnyLnSplit = 4;
     int64_t ns = ceil_div(2 * (int64_t)device_cus(), ntiles);
-    if (ns > kMaxSplit) ns = kMaxSplit;
+    if (ns > kSkinnyLnSplit) ns = kSkinnyLnSplit;
     if (ns > steps / 4) ns = steps / 4 > 0 ? steps / 4 : 1;
     a.nsplit = (int)ns;
     a.partial = workspace;

@@ -603,8 +603,8 @@ def test_ffn_decode_with_depth_read(dtype, M, rms, slots):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("M,K2,N", [(1, 768, 768), (32, 768, 768), (32, 3072, 768), (64, 3072, 768),
-                                    (7, 0, 768), (4096, 768, 768), (4096, 3072, 768),
+@pytest.mark.parametrize("M,K2,N", [(1, 768, 768), (4, 3072, 768), (32, 768, 768), (32, 3072, 768),
+                                    (64, 3072, 768), (7, 0, 768), (4096, 768, 768), (4096, 3072, 768),
                                     (300, 768, 768), (512, 0, 768), (520, 768, 200)])
 def test_linear_ln(dtype, M, K2, N):
     """LayerNorm(x w^T + x2 w2^T + b): split-K partial sums reduced inside the
@@ -636,7 +636,7 @@ def test_linear_ln(dtype, M, K2, N):
     check(out, want, dtype)
 
 
-@pytest.mark.parametrize("M,K2", [(32, 768), (32, 3072), (20, 0), (64, 768)])
+@pytest.mark.parametrize("M,K2", [(4, 3072), (32, 768), (32, 3072), (20, 0), (64, 768)])
 def test_fragment_major_activations(M, K2):
     """loom_linear_ln's out_frag is the fragment-major copy of its output, and
     loom_linear_ln / loom_linear_multi reading x_frag / x2_frag give the same

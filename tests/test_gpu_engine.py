@@ -190,20 +190,22 @@ def test_bf16_chunked_prefill_tracks_token_steps():
     the fp32 token-by-token engine (same bf16-rounded weights), the state left
     by the bf16 chunked prefill is as close as the bf16 token-by-token one
     (within 2x of its error, or 2%), and its last logits within the 8% the
-    bf16 engine is held to."""
+    bf16 engine is held to.  Every position is a prompt token (no greedy pick
+    whose near-ties could send the engines down different tokens)."""
     from loom_amd.engine import LoomDecoder
     from loom_amd.weights import init_state_dict
     cfg = _cfg("nano_chk", layers=3, tria_temporal_window=32, seq_len=256)
     state = {k: (v.to(torch.bfloat16).float() if v.dim() >= 2 else v)
              for k, v in init_state_dict(cfg, 3).items()}
     g = torch.Generator().manual_seed(7)
-    prompt = torch.randint(0, cfg.V, (4, 100), generator=g)
+    prompt = torch.randint(0, cfg.V, (4, 101), generator=g)
     ref = LoomDecoder(cfg, state, batch=4, dtype=torch.float32)
     tok = LoomDecoder(cfg, state, batch=4, dtype=torch.bfloat16)
     pre = LoomDecoder(cfg, state, batch=4, dtype=torch.bfloat16)
-    ref.generate(prompt, 1)                     # positions 0 .. 99 token by token, then 100
-    tok.generate(prompt, 1)
-    pre.generate(prompt, 1, chunked_prefill=True)
+    for e in (ref, tok):                        # positions 0 .. 100 token by token
+        e.start(prompt)
+        e.replay_steps(100)
+    pre.prefill(prompt)                         # the same positions, chunked
 
     def rel(x, y):                              # relative Frobenius error
         x, y = x.float(), y.float()
