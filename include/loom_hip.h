@@ -292,6 +292,27 @@ int loom_tria_depth_forward(int dtype, const void* r, const void* i, const void*
                             const void* w, void* carry_out, void* p_out, float* scale_out,
                             int64_t B, int64_t T, int64_t H, float alpha, int axis, void* stream);
 
+/* (act, next_trace) = paraplex(R, beta) and (carry_out, p_out) =
+ * tria_depth(R, I, act) in one pass over a [B, T, H] sequence: the sequence
+ * form of loom_paraplex_forward (no reset, no anchor snapshot) followed by
+ * loom_tria_depth_forward, with the phase I never stored.  Restates
+ * ParaplexFFN's pointwise core (loomformer.py:2856-2885) and the block's
+ * _tria_depth_op (:3588-3617) as the chunked forward runs them (:3788-3883);
+ * no counterpart in the reference as one call.  The Tria op reads I and act
+ * rounded to dtype, as the separate ops see them, so the outputs equal theirs.
+ *   p_real, gate_src (== p_real when paraplex_gate_proj is off), beta_linear:
+ *   [B,T,H] dtype; bias, trace_w: [H] float; trace: [B,H] dtype (the base phase
+ *   of the token before t = 0); act: [B,T,H] out; next_trace: [B,H] out (the
+ *   base phase of t = T-1); carry_prev / seed / seed_valid / w / carry_out /
+ *   p_out as loom_tria_depth_forward (carry_out required, no scale_out). */
+int loom_paraplex_tria_forward(int dtype, const void* p_real, const void* gate_src,
+                               const void* beta_linear, const float* bias, const void* trace,
+                               const float* trace_w, float m, const void* carry_prev,
+                               const void* seed, const uint8_t* seed_valid, const void* w,
+                               void* act, void* next_trace, void* carry_out, void* p_out,
+                               int64_t B, int64_t T, int64_t H, float alpha, int axis,
+                               void* stream);
+
 /* p[e] = sum_k w[k] * carry[e][k].  Replaces gate_slot_mix_forward
  * (kernels/tria/bindings.cpp:97). carry: [n,9] dtype, w: [9] dtype, p: [n] dtype. */
 int loom_gate_slot_mix_forward(int dtype, const void* carry, const void* w, void* p, int64_t n,

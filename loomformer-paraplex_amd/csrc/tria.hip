@@ -9,6 +9,7 @@
 #include <cmath>
 
 #include "loom_common.h"
+#include "paraplex_math.h"
 #include "tria_math.h"
 
 namespace loom {
@@ -151,6 +152,110 @@ tria_depth_kernel(const T* __restrict__ r, const T* __restrict__ i_, const T* __
         __syncthreads();
         stage_out(carry_out + e0 * 9, tile, cnt * 9);
     }
+}
+
+// The Paraplex pointwise chain and the block's Tria depth op in one pass over
+// a [B, T, H] sequence (the sequence form of ParaplexFFN's core, loomformer.py:
+// 2856-2885, followed by _tria_depth_op, :3588-3617): per element the phase
+// I from beta (+ bias) and the previous token's base phase (the carried trace
+// at t = 0), O = (R + A*I) * G(A), then the carrier of (R, I, O) as the
+// separate ops would read them back (I and O rounded to the storage type) and
+// its composition with the carried record.  I is never stored; O goes out for
+// W2, and the base phase of the sequence's last token as the next trace.
+// Same staging of the 9-value records as tria_depth_kernel.
+template <typename T>
+struct PxTriaArgs {
+    const T* r;            // R [B, T, H]
+    const T* gsrc;         // the amplitude source (R itself, or gate_proj(u))
+    const T* beta;         // beta_linear [B, T, H] (bias not added)
+    const float* bias;     // [H]
+    const T* trace;        // [B, H] base phase of the token before t = 0
+    const float* trace_w;  // [H]
+    const T* prev;         // MODE 1: carried records [B, T, H, 9]
+    const T* seed;         // MODE 2: [B, H, 9] for t == 0 where valid[b]
+    const uint8_t* valid;
+    const T* w;            // GATE: [9]
+    T* act;                // O [B, T, H]
+    T* next_trace;         // [B, H]
+    T* carry_out;          // [B, T, H, 9]
+    T* p_out;              // GATE: [B, T, H]
+    int T_, H;
+    int64_t n;
+    float m, alpha;
+};
+
+template <typename T, int MODE, bool GATE, int AXIS, bool SAME_GATE>
+__global__ void __launch_bounds__(kTriaThreads)
+paraplex_tria_kernel(PxTriaArgs<T> a) {
+    __shared__ float tile[kTriaThreads * 9];
+    const int64_t e0 = (int64_t)blockIdx.x * kTriaThreads;
+    const int cnt = (int)((a.n - e0) < kTriaThreads ? (a.n - e0) : kTriaThreads);
+    const int64_t e = e0 + threadIdx.x;
+    const bool live = threadIdx.x < cnt;
+    if constexpr (MODE == 1) {
+        stage_in(tile, a.prev + e0 * 9, cnt * 9);
+        __syncthreads();
+    }
+    float pre[9];
+    if (live) {
+        const int64_t bt = e / a.H;
+        const int h = (int)(e - bt * a.H);
+        const int t = (int)(bt % a.T_);
+        const int64_t b = bt / a.T_;
+        // Paraplex chain (as paraplex_chunk_kernel / paraplex_forward_kernel)
+        const float x = ld(a.r + e);
+        const float bv = a.bias[h];
+        const float s0 = phase_of(ld(a.beta + e) + bv);
+        const float prevs = t == 0 ? ld(a.trace + b * a.H + h) : phase_of(ld(a.beta + e - a.H) + bv);
+        const float raw = fmaf(prevs, a.trace_w[h], s0);
+        const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
+        float amp, gate;
+        softplus_gate<!std::is_same<T, bf16_t>::value>(SAME_GATE ? x : ld(a.gsrc + e), a.m, amp, gate);
+        const float act = fmaf(amp, sv, x) * gate;
+        T ts, to;
+        st(&ts, sv);
+        st(&to, act);
+        a.act[e] = to;
+        if (t == a.T_ - 1) st(a.next_trace + b * a.H + h, s0);
+        // Tria depth op on (R, I, O) as stored
+        float mt[9];
+        carrier9<AXIS>(x, ld(&ts), ld(&to), a.alpha, mt);
+        if constexpr (MODE == 1) {
+            float cp[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) cp[k] = tile[threadIdx.x * 9 + k];
+            mm3(mt, cp, pre);
+        } else if constexpr (MODE == 2) {
+            if (t == 0 && a.valid[b] != 0) {
+                float sd[9];
+#pragma unroll
+                for (int k = 0; k < 9; ++k) sd[k] = ld(a.seed + (b * a.H + h) * 9 + k);
+                mm3(mt, sd, pre);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 9; ++k) pre[k] = mt[k];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 9; ++k) pre[k] = mt[k];
+        }
+        const float inv = 1.0f / rms9(pre);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) pre[k] *= inv;
+        if constexpr (GATE) {
+            float pv = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) pv = fmaf(pre[k], ld(a.w + k), pv);
+            st(a.p_out + e, pv);
+        }
+    }
+    if constexpr (MODE == 1) __syncthreads();  // everyone has read tile
+    if (live) {
+#pragma unroll
+        for (int k = 0; k < 9; ++k) tile[threadIdx.x * 9 + k] = pre[k];
+    }
+    __syncthreads();
+    stage_out(a.carry_out + e0 * 9, tile, cnt * 9);
 }
 
 template <typename T>
@@ -658,6 +763,44 @@ static int tria_depth_dispatch(const void* r, const void* i, const void* o, cons
     return launch_status("loom_tria_depth_forward");
 }
 
+template <typename T>
+static int px_tria_dispatch(const PxTriaArgs<T>& a, int mode, bool gate, bool same, int axis,
+                            hipStream_t st) {
+    const dim3 grid((unsigned)ceil_div(a.n, kTriaThreads)), blk(kTriaThreads);
+#define LOOM_PT(M, G, A, S) hipLaunchKernelGGL((paraplex_tria_kernel<T, M, G, A, S>), grid, blk, 0, st, a)
+#define LOOM_PT_AXIS(M, G, S)                     \
+    switch (axis) {                               \
+        case 0: LOOM_PT(M, G, 0, S); break;       \
+        case 1: LOOM_PT(M, G, 1, S); break;       \
+        default: LOOM_PT(M, G, 2, S); break;      \
+    }
+#define LOOM_PT_SAME(M, G)                                          \
+    if (same) { LOOM_PT_AXIS(M, G, true) } else { LOOM_PT_AXIS(M, G, false) }
+    if (mode == 0) { if (gate) { LOOM_PT_SAME(0, true) } else { LOOM_PT_SAME(0, false) } }
+    else if (mode == 1) { if (gate) { LOOM_PT_SAME(1, true) } else { LOOM_PT_SAME(1, false) } }
+    else { if (gate) { LOOM_PT_SAME(2, true) } else { LOOM_PT_SAME(2, false) } }
+#undef LOOM_PT_SAME
+#undef LOOM_PT_AXIS
+#undef LOOM_PT
+    return launch_status("loom_paraplex_tria_forward");
+}
+
+template <typename T>
+static int px_tria_typed(const void* r, const void* gsrc, const void* beta, const float* bias,
+                         const void* trace, const float* trace_w, float m, const void* prev,
+                         const void* seed, const uint8_t* valid, const void* w, void* act,
+                         void* next_trace, void* carry_out, void* p_out, int64_t B, int64_t T_,
+                         int64_t H, float alpha, int axis, hipStream_t st) {
+    PxTriaArgs<T> a{};
+    a.r = (const T*)r; a.gsrc = (const T*)gsrc; a.beta = (const T*)beta; a.bias = bias;
+    a.trace = (const T*)trace; a.trace_w = trace_w; a.prev = (const T*)prev;
+    a.seed = (const T*)seed; a.valid = valid; a.w = (const T*)w; a.act = (T*)act;
+    a.next_trace = (T*)next_trace; a.carry_out = (T*)carry_out; a.p_out = (T*)p_out;
+    a.T_ = (int)T_; a.H = (int)H; a.n = B * T_ * H; a.m = m; a.alpha = alpha;
+    const int mode = prev ? 1 : (seed ? 2 : 0);
+    return px_tria_dispatch<T>(a, mode, w != nullptr, gsrc == r, axis, st);
+}
+
 #define LOOM_DTYPE_SWITCH(dtype, FN, ...)                            \
     switch (dtype) {                                                 \
         case LOOM_F32: return FN<float>(__VA_ARGS__);                \
@@ -755,6 +898,30 @@ extern "C" int loom_tria_depth_forward(int dtype, const void* r, const void* i, 
     if (B * T * H == 0) return LOOM_OK;
     LOOM_DTYPE_SWITCH(dtype, tria_depth_dispatch, r, i, o, carry_prev, seed, seed_valid, w,
                       carry_out, p_out, scale_out, B, T, H, alpha, axis, (hipStream_t)stream)
+}
+
+extern "C" int loom_paraplex_tria_forward(int dtype, const void* p_real, const void* gate_src,
+                                          const void* beta_linear, const float* bias,
+                                          const void* trace, const float* trace_w, float m,
+                                          const void* carry_prev, const void* seed,
+                                          const uint8_t* seed_valid, const void* w, void* act,
+                                          void* next_trace, void* carry_out, void* p_out,
+                                          int64_t B, int64_t T, int64_t H, float alpha, int axis,
+                                          void* stream) {
+    clear_error();
+    LOOM_CHECK(p_real && gate_src && beta_linear && bias && trace && trace_w && act && next_trace &&
+                   carry_out,
+               "paraplex_tria: a required tensor is null");
+    LOOM_CHECK(axis >= 0 && axis <= 2, "paraplex_tria: axis must be 0(z), 1(x), or 2(y), got %d", axis);
+    LOOM_CHECK(!(carry_prev && seed), "paraplex_tria: carry_prev and seed are mutually exclusive");
+    LOOM_CHECK(!seed || seed_valid, "paraplex_tria: seed needs seed_valid");
+    LOOM_CHECK(!w || p_out, "paraplex_tria: gate weights need p_out");
+    LOOM_CHECK(B >= 0 && T >= 0 && H >= 0 && T < (1LL << 31) && H < (1LL << 31),
+               "paraplex_tria: bad shape");
+    if (B * T * H == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, px_tria_typed, p_real, gate_src, beta_linear, bias, trace, trace_w, m,
+                      carry_prev, seed, seed_valid, w, act, next_trace, carry_out, p_out, B, T, H,
+                      alpha, axis, (hipStream_t)stream)
 }
 
 extern "C" int loom_gate_slot_mix_forward(int dtype, const void* carry, const void* w, void* p,

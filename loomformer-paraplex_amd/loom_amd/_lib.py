@@ -50,6 +50,8 @@ SIGNATURES = {
                                 c_int64, c_int64, c_int64, _P],
     "loom_tria_depth_forward": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64,
                                 c_int64, c_int64, c_float, c_int, _P],
+    "loom_paraplex_tria_forward": [c_int, _P, _P, _P, _P, _P, _P, c_float, _P, _P, _P, _P, _P, _P,
+                                   _P, _P, c_int64, c_int64, c_int64, c_float, c_int, _P],
     "loom_gate_slot_mix_forward": [c_int, _P, _P, _P, c_int64, _P],
     "loom_slot_attention_pool_forward": [c_int, _P, _P, _P, _P, c_int64, c_int64, _P],
     "loom_temporal_carry_forward": [c_int, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P],

@@ -83,7 +83,6 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     gbuf = z(M, H) if c.gate_proj else None
     beta = z(M, H)
     act = z(M, H)
-    sbuf = z(M, H)
     hist = z(M, 2 * L, 2 * N)
     carry = z(2, M, H, 3, 3)
     pbuf = z(2, M, H)
@@ -92,8 +91,6 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     state32 = torch.empty(B, H, 3, 3, dtype=torch.float32, device=dev)
     pooled, z32, a_key = z(B, 9), z(B, 32), z(B, N)
     stage_k, stage_v = z(B, N), z(B, N)
-    snap = torch.empty((), dtype=torch.float32, device=dev)
-    empty_reset = None
     cache_sb = KVH * eng.max_len * HD
     cache_st = HD
     cache_sh = eng.max_len * HD
@@ -184,20 +181,19 @@ def prefill(eng, prompt: torch.Tensor) -> None:
                 gsrc = gbuf
                 lin(h, blk["gpw"], gbuf, rows, H, N, bias=blk["gpb"])
             join()
-            call("loom_paraplex_forward", code, _P(R), _P(gsrc), _P(beta), _P(blk["ib"]),
-                 _P(traces[tin, bi]), _P(blk["tw"]), empty_reset, _P(blk["anchor"]), _P(act),
-                 _P(sbuf), _P(traces[1 - tin, bi]), _P(snap), B, Tc, H, float(c.powlu_m), st)
-            # ---- Tria depth op of the block (loomformer.py:3588-3617), axis bi % 3
+            # ---- with the block's Tria depth op (loomformer.py:3588-3617), axis bi % 3,
+            # in the same pass: the phase I never leaves the chip
             out_i = 0 if carry_i != 0 else 1
             gate = not last
             new_p = (0 if p_i != 0 else 1) if gate else None
             seeded = bi == 0 and have_state
-            call("loom_tria_depth_forward", code, _P(R), _P(sbuf), _P(act),
+            call("loom_paraplex_tria_forward", code, _P(R), _P(gsrc), _P(beta), _P(blk["ib"]),
+                 _P(traces[tin, bi]), _P(blk["tw"]), float(c.powlu_m),
                  None if (carry_i is None or seeded) else _P(carry[carry_i]),
                  _P(state) if seeded else None, _P(seed_valid) if seeded else None,
-                 _P(blk["gate_w"]) if gate else None, _P(carry[out_i]),
-                 _P(pbuf[new_p]) if gate else None, None, B, Tc, H, float(c.tria_alpha),
-                 bi % 3, st)
+                 _P(blk["gate_w"]) if gate else None, _P(act), _P(traces[1 - tin, bi]),
+                 _P(carry[out_i]), _P(pbuf[new_p]) if gate else None, B, Tc, H,
+                 float(c.tria_alpha), bi % 3, st)
             carry_i, p_i = out_i, new_p
             # ---- LN(w_o(d_h) + W2(act) + b2) (loomformer.py:4045)
             lin_ln(("ffn", bi), dh, eng.wo_for(sub), act, blk["w2"], blk["b2"], blk["ln2_w"],

@@ -357,6 +357,98 @@ def test_tria_depth_family(dtype, axis, B, T, H):
     torch.testing.assert_close(rms, torch.ones_like(rms), rtol=2e-2 if dtype == torch.bfloat16 else 1e-5, atol=0)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,T,H,mode,gate,axis,same", [
+    (2, 5, 24, "init", False, 0, True), (2, 5, 24, "step", True, 1, False),
+    (3, 4, 6, "seed", True, 2, True), (3, 9, 20, "seed", False, 1, False),
+    (1, 1, 3072, "step", False, 2, True), (4, 33, 1000, "init", True, 2, False),
+    # the chunked prefill's shape: [32, 128] tokens of 3072
+    (32, 128, 3072, "step", True, 1, True), (32, 128, 3072, "init", True, 0, True),
+    (32, 128, 3072, "seed", True, 2, True), (32, 128, 3072, "step", False, 0, False),
+])
+def test_paraplex_tria_fused(dtype, B, T, H, mode, gate, axis, same):
+    """loom_paraplex_tria_forward against the two launches it replaces
+    (loom_paraplex_forward then loom_tria_depth_forward on the stored I and O):
+    the same bits for act, the next trace, the carry and p; and against the
+    oracle's composition paraplex_pointwise -> tria_* on I and O rounded to
+    dtype (the reference stores both before the Tria op reads them)."""
+    from loom_amd import ops
+    from loom_amd._lib import call, dtype_code, ptr, stream_of
+    g = gen(B * 131 + T * 7 + H + axis)
+    r = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    gs = r if same else dev(rnd(g, B, T, H, scale=3.0), dtype)
+    beta = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    bias = dev(rnd(g, H, scale=0.5), torch.float32)
+    trace = dev(rnd(g, B, H, scale=0.5), dtype)
+    tw = dev(torch.rand(H, generator=g) - 0.5, torch.float32)
+    prev = dev(ref.local_normalize(rnd(g, B, T, H, 3, 3)), dtype) if mode == "step" else None
+    seed = dev(ref.local_normalize(rnd(g, B, H, 3, 3)), dtype) if mode == "seed" else None
+    valid = torch.rand(B, generator=g) > 0.4
+    valid[0] = True
+    valid = dev(valid, torch.bool) if mode == "seed" else None
+    w = dev(torch.softmax(rnd(g, 9), 0), dtype) if gate else None
+    a, m = 0.0375, 3.0
+
+    # the two launches
+    no_reset = torch.empty(0, dtype=torch.bool, device=DEV)
+    act2, s2, nt2, _ = ops.paraplex_forward(r, gs, beta, bias, trace, tw, no_reset,
+                                            torch.ones((), device=DEV), 1, False, 0.99, m)
+    carry2, p2, _ = ops._tria_call(r, s2, act2, prev, seed, valid, w, False, a, axis)
+
+    for _ in range(2):  # a second call writes the same bits
+        act = torch.full_like(r, float("nan"))
+        nt = torch.full_like(trace, float("nan"))
+        carry = torch.full((B, T, H, 3, 3), float("nan"), dtype=dtype, device=DEV)
+        p = torch.full_like(r, float("nan")) if gate else None
+        call("loom_paraplex_tria_forward", dtype_code(r), ptr(r), ptr(gs), ptr(beta), ptr(bias),
+             ptr(trace), ptr(tw), m, ptr(prev), ptr(seed), ptr(valid), ptr(w), ptr(act), ptr(nt),
+             ptr(carry), ptr(p), B, T, H, a, axis, stream_of(r))
+        torch.cuda.synchronize()
+        assert torch.equal(act, act2)
+        assert torch.equal(nt, nt2)
+        assert torch.equal(carry, carry2)
+        if gate:
+            assert torch.equal(p, p2)
+
+    w_act, w_s, w_nt = ref.paraplex_pointwise(host(r), host(gs), host(beta), host(bias), host(trace),
+                                              host(tw), None, m)
+    check(act, w_act, dtype)
+    check(nt, w_nt, dtype)
+    R, I, O = host(r), w_s.to(dtype).float(), w_act.to(dtype).float()
+    if mode == "init":
+        wc = ref.tria_init(R, I, O, a, axis)
+    elif mode == "step":
+        wc = ref.tria_step(R, I, O, host(prev), a, axis)
+    else:
+        wc = ref.tria_init_seed(R, I, O, host(seed), valid.cpu(), a, axis)
+    # bf16: the carrier of O rounded on the GPU vs O rounded in the oracle
+    # (one ulp apart where the fp32 values straddle a rounding boundary)
+    tol = dict(rtol=2e-2, atol=2e-2) if dtype == torch.bfloat16 else {}
+    check(carry, wc, dtype, **tol)
+    if gate:
+        check(p, ref.gate_slot_mix(wc, host(w)), dtype, **tol)
+
+
+def test_paraplex_tria_argument_errors():
+    from loom_amd._lib import call, ptr
+    x = torch.zeros(2, 3, 4, device=DEV)
+    t = torch.zeros(2, 4, device=DEV)
+    h = torch.zeros(4, device=DEV)
+    c = torch.zeros(2, 3, 4, 9, device=DEV)
+    base = [0, ptr(x), ptr(x), ptr(x), ptr(h), ptr(t), ptr(h), 3.0, None, None, None, None,
+            ptr(x), ptr(t), ptr(c), None, 2, 3, 4, 0.0375, 0, None]
+    cases = {20: [(20, 3)], 8: [(8, ptr(c)), (9, ptr(c)), (10, ptr(x))], 11: [(11, ptr(h))],
+             12: [(12, None)]}
+    for edits in cases.values():
+        args = list(base)
+        for k, v in edits:
+            args[k] = v
+        with pytest.raises(RuntimeError, match="paraplex_tria"):
+            call("loom_paraplex_tria_forward", *args)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(c) == 0  # nothing was launched
+
+
 def test_golden_tria_vs_reference():
     from loom_amd import ops
     z = np.load(os.path.join(GOLD, "ops.npz"))
