@@ -237,6 +237,16 @@ struct RawRow {
 // Built directly on the gfx950 transcendental instructions (v_exp_f32 = 2^x,
 // v_log_f32 = log2 x, v_sin_f32 = sin(2*pi*x), v_rsq_f32, v_rcp_f32,
 // v_sqrt_f32); each is accurate to about one ulp over the ranges used here.
+// Position in the work order of block L of a 1-D launch of n blocks, such
+// that each XCD works through one contiguous share of that order: blocks are
+// dealt round-robin to the 8 XCDs (block L runs on XCD L % 8), so XCD k's
+// blocks L = 8*slot + k take work items k*(n/8) + min(k, n%8) + slot.  Work
+// items next to each other in the order then share an L2.
+__device__ __forceinline__ int xcd_contiguous(int L, int n) {
+    const int k = L & 7, slot = L >> 3;
+    return k * (n >> 3) + min(k, n & 7) + slot;
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 

@@ -303,11 +303,17 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     __shared__ float cr[4][16];                           // per-column rescale of a step
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 15, lq = lane >> 4;
-    const int kvh = blockIdx.y / HSPLIT, part = blockIdx.y % HSPLIT;
-    const int64_t b = blockIdx.z;
+    // work item (query tile, head group, row) in query-tile-fastest order; the
+    // query tiles of one (row, kv head) read the same K/V rows, so they share
+    // an XCD and its L2
+    const int ntile = (a.Tc + 16 * QTB - 1) / (16 * QTB), ngrp = a.KVH * HSPLIT;
+    const int w = xcd_contiguous((int)blockIdx.x, (int)gridDim.x);
+    const int bx = w % ntile, by = (w / ntile) % ngrp;
+    const int kvh = by / HSPLIT, part = by % HSPLIT;
+    const int64_t b = w / (ntile * ngrp);
     const int head = kvh * G + part * GP + wave % GP;
-    const int q0 = (blockIdx.x * QTB + wave / GP) * 16;          // first query of the wave's tile
-    const int qlast_blk = min((int)(blockIdx.x + 1) * QTB * 16, a.Tc) - 1;
+    const int q0 = (bx * QTB + wave / GP) * 16;                  // first query of the wave's tile
+    const int qlast_blk = min((bx + 1) * QTB * 16, a.Tc) - 1;
     const int64_t kmax = a.start + qlast_blk;                    // last cached row the block reads
     const int nsteps = (int)((kmax + kPfRows) / kPfRows);
     // this lane's query column (lr): its position; a column past the chunk
@@ -521,16 +527,16 @@ static int prefill_dispatch(const void* qkv, int64_t qkv_ld, void* kc, void* vc,
 #define LOOM_PF_MF(HDV)                                                                          \
             if (HD == HDV) {                                                                     \
                 if (G == 4) {                                                                    \
-                    dim3 g((unsigned)ceil_div(Tc, 16), (unsigned)KVH, (unsigned)B);             \
+                    const dim3 g((unsigned)(ceil_div(Tc, 16) * KVH * B));                        \
                     hipLaunchKernelGGL((gqa_prefill_mfma_kernel<HDV, 4, 1>), g, dim3(256), 0, st, a); \
                 } else if (G == 8) {                                                             \
-                    dim3 g((unsigned)ceil_div(Tc, 16), (unsigned)(KVH * 2), (unsigned)B);       \
+                    const dim3 g((unsigned)(ceil_div(Tc, 16) * KVH * 2 * B));                    \
                     hipLaunchKernelGGL((gqa_prefill_mfma_kernel<HDV, 4, 2>), g, dim3(256), 0, st, a); \
                 } else if (G == 2) {                                                             \
-                    dim3 g((unsigned)ceil_div(Tc, 32), (unsigned)KVH, (unsigned)B);             \
+                    const dim3 g((unsigned)(ceil_div(Tc, 32) * KVH * B));                        \
                     hipLaunchKernelGGL((gqa_prefill_mfma_kernel<HDV, 2, 1>), g, dim3(256), 0, st, a); \
                 } else {                                                                         \
-                    dim3 g((unsigned)ceil_div(Tc, 64), (unsigned)KVH, (unsigned)B);             \
+                    const dim3 g((unsigned)(ceil_div(Tc, 64) * KVH * B));                        \
                     hipLaunchKernelGGL((gqa_prefill_mfma_kernel<HDV, 1, 1>), g, dim3(256), 0, st, a); \
                 }                                                                                \
                 return launch_status("loom_gqa_prefill");                                       \
@@ -579,6 +585,9 @@ extern "C" int loom_gqa_prefill(int dtype, const void* qkv, int64_t qkv_ld, void
                "gqa_prefill: cache strides smaller than a head row");
     LOOM_CHECK(T <= (1 << 20), "gqa_prefill: chunk of %lld tokens too long", (long long)T);
     LOOM_CHECK(start + T < (1LL << 31), "gqa_prefill: positions beyond 2^31");
+    LOOM_CHECK(ceil_div(T, 16) * QH * B <= (1LL << 23),
+               "gqa_prefill: %lld rows x %lld tokens x %lld heads exceed one launch", (long long)B,
+               (long long)T, (long long)QH);
     LOOM_CHECK(start + T <= cache_len,
                "gqa_prefill: positions %lld..%lld beyond the cache capacity %lld", (long long)start,
                (long long)(start + T - 1), (long long)cache_len);
