@@ -20,11 +20,11 @@ constexpr int kTriaThreads = 256;
 // coalesced accesses: whole 16-byte pieces (8 values of a 16-bit type, 4 of
 // fp32) when the slice is 16-byte aligned and a whole number of pieces, single
 // values otherwise.
-template <typename T>
+template <typename T, int REC = kTriaThreads>
 __device__ __forceinline__ void stage_in(float* lds, const T* src, int n9) {
     constexpr int V = 16 / (int)sizeof(T);
-    // pieces per thread when the block stages kTriaThreads records of 9
-    constexpr int kPer = (kTriaThreads * 9 / V + kTriaThreads - 1) / kTriaThreads;
+    // pieces per thread when the block stages REC records of 9
+    constexpr int kPer = (REC * 9 / V + kTriaThreads - 1) / kTriaThreads;
     if (((uintptr_t)src & 15) == 0 && n9 % V == 0) {
         // every piece requested before the first LDS store (one memory round
         // trip per block), nontemporally: each record is read once
@@ -163,6 +163,8 @@ tria_depth_kernel(const T* __restrict__ r, const T* __restrict__ i_, const T* __
 // its composition with the carried record.  I is never stored; O goes out for
 // W2, and the base phase of the sequence's last token as the next trace.
 // Same staging of the 9-value records as tria_depth_kernel.
+constexpr int kPxTriaPerThread = 2;   // elements per thread of paraplex_tria_kernel
+
 template <typename T>
 struct PxTriaArgs {
     const T* r;            // R [B, T, H]
@@ -184,75 +186,86 @@ struct PxTriaArgs {
     float m, alpha;
 };
 
-template <typename T, int MODE, bool GATE, int AXIS, bool SAME_GATE>
+// Each thread computes EPT elements (tid + 256 u), so a block's two memory
+// round trips (the carried records, then R and beta) move EPT times the bytes.
+template <typename T, int MODE, bool GATE, int AXIS, bool SAME_GATE, int EPT>
 __global__ void __launch_bounds__(kTriaThreads)
 paraplex_tria_kernel(PxTriaArgs<T> a) {
-    __shared__ float tile[kTriaThreads * 9];
-    const int64_t e0 = (int64_t)blockIdx.x * kTriaThreads;
-    const int cnt = (int)((a.n - e0) < kTriaThreads ? (a.n - e0) : kTriaThreads);
-    const int64_t e = e0 + threadIdx.x;
-    const bool live = threadIdx.x < cnt;
+    constexpr int REC = kTriaThreads * EPT;
+    __shared__ float tile[REC * 9];
+    const int64_t e0 = (int64_t)blockIdx.x * REC;
+    const int cnt = (int)((a.n - e0) < REC ? (a.n - e0) : REC);
     if constexpr (MODE == 1) {
-        stage_in(tile, a.prev + e0 * 9, cnt * 9);
+        stage_in<T, REC>(tile, a.prev + e0 * 9, cnt * 9);
         __syncthreads();
     }
-    float pre[9];
-    if (live) {
-        const int64_t bt = e / a.H;
-        const int h = (int)(e - bt * a.H);
-        const int t = (int)(bt % a.T_);
-        const int64_t b = bt / a.T_;
-        // Paraplex chain (as paraplex_chunk_kernel / paraplex_forward_kernel)
-        const float x = ld(a.r + e);
-        const float bv = a.bias[h];
-        const float s0 = phase_of(ld(a.beta + e) + bv);
-        const float prevs = t == 0 ? ld(a.trace + b * a.H + h) : phase_of(ld(a.beta + e - a.H) + bv);
-        const float raw = fmaf(prevs, a.trace_w[h], s0);
-        const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
-        float amp, gate;
-        softplus_gate<!std::is_same<T, bf16_t>::value>(SAME_GATE ? x : ld(a.gsrc + e), a.m, amp, gate);
-        const float act = fmaf(amp, sv, x) * gate;
-        T ts, to;
-        st(&ts, sv);
-        st(&to, act);
-        a.act[e] = to;
-        if (t == a.T_ - 1) st(a.next_trace + b * a.H + h, s0);
-        // Tria depth op on (R, I, O) as stored
-        float mt[9];
-        carrier9<AXIS>(x, ld(&ts), ld(&to), a.alpha, mt);
-        if constexpr (MODE == 1) {
-            float cp[9];
+    float pre[EPT][9];
 #pragma unroll
-            for (int k = 0; k < 9; ++k) cp[k] = tile[threadIdx.x * 9 + k];
-            mm3(mt, cp, pre);
-        } else if constexpr (MODE == 2) {
-            if (t == 0 && a.valid[b] != 0) {
-                float sd[9];
+    for (int u = 0; u < EPT; ++u) {
+        const int idx = (int)threadIdx.x + u * kTriaThreads;
+        const int64_t e = e0 + idx;
+        if (idx < cnt) {
+            const int64_t bt = e / a.H;
+            const int h = (int)(e - bt * a.H);
+            const int t = (int)(bt % a.T_);
+            const int64_t b = bt / a.T_;
+            // Paraplex chain (as paraplex_chunk_kernel / paraplex_forward_kernel)
+            const float x = ld(a.r + e);
+            const float bv = a.bias[h];
+            const float s0 = phase_of(ld(a.beta + e) + bv);
+            const float prevs = t == 0 ? ld(a.trace + b * a.H + h) : phase_of(ld(a.beta + e - a.H) + bv);
+            const float raw = fmaf(prevs, a.trace_w[h], s0);
+            const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
+            float amp, gate;
+            softplus_gate<!std::is_same<T, bf16_t>::value>(SAME_GATE ? x : ld(a.gsrc + e), a.m, amp, gate);
+            const float act = fmaf(amp, sv, x) * gate;
+            T ts, to;
+            st(&ts, sv);
+            st(&to, act);
+            a.act[e] = to;
+            if (t == a.T_ - 1) st(a.next_trace + b * a.H + h, s0);
+            // Tria depth op on (R, I, O) as stored
+            float mt[9];
+            float* pr = pre[u];
+            carrier9<AXIS>(x, ld(&ts), ld(&to), a.alpha, mt);
+            if constexpr (MODE == 1) {
+                float cp[9];
 #pragma unroll
-                for (int k = 0; k < 9; ++k) sd[k] = ld(a.seed + (b * a.H + h) * 9 + k);
-                mm3(mt, sd, pre);
+                for (int k = 0; k < 9; ++k) cp[k] = tile[idx * 9 + k];
+                mm3(mt, cp, pr);
+            } else if constexpr (MODE == 2) {
+                if (t == 0 && a.valid[b] != 0) {
+                    float sd[9];
+#pragma unroll
+                    for (int k = 0; k < 9; ++k) sd[k] = ld(a.seed + (b * a.H + h) * 9 + k);
+                    mm3(mt, sd, pr);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 9; ++k) pr[k] = mt[k];
+                }
             } else {
 #pragma unroll
-                for (int k = 0; k < 9; ++k) pre[k] = mt[k];
+                for (int k = 0; k < 9; ++k) pr[k] = mt[k];
             }
-        } else {
+            const float inv = 1.0f / rms9(pr);
 #pragma unroll
-            for (int k = 0; k < 9; ++k) pre[k] = mt[k];
-        }
-        const float inv = 1.0f / rms9(pre);
+            for (int k = 0; k < 9; ++k) pr[k] *= inv;
+            if constexpr (GATE) {
+                float pv = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 9; ++k) pre[k] *= inv;
-        if constexpr (GATE) {
-            float pv = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 9; ++k) pv = fmaf(pre[k], ld(a.w + k), pv);
-            st(a.p_out + e, pv);
+                for (int k = 0; k < 9; ++k) pv = fmaf(pr[k], ld(a.w + k), pv);
+                st(a.p_out + e, pv);
+            }
         }
     }
     if constexpr (MODE == 1) __syncthreads();  // everyone has read tile
-    if (live) {
 #pragma unroll
-        for (int k = 0; k < 9; ++k) tile[threadIdx.x * 9 + k] = pre[k];
+    for (int u = 0; u < EPT; ++u) {
+        const int idx = (int)threadIdx.x + u * kTriaThreads;
+        if (idx < cnt) {
+#pragma unroll
+            for (int k = 0; k < 9; ++k) tile[idx * 9 + k] = pre[u][k];
+        }
     }
     __syncthreads();
     stage_out(a.carry_out + e0 * 9, tile, cnt * 9);
@@ -766,8 +779,9 @@ static int tria_depth_dispatch(const void* r, const void* i, const void* o, cons
 template <typename T>
 static int px_tria_dispatch(const PxTriaArgs<T>& a, int mode, bool gate, bool same, int axis,
                             hipStream_t st) {
-    const dim3 grid((unsigned)ceil_div(a.n, kTriaThreads)), blk(kTriaThreads);
-#define LOOM_PT(M, G, A, S) hipLaunchKernelGGL((paraplex_tria_kernel<T, M, G, A, S>), grid, blk, 0, st, a)
+    constexpr int EPT = kPxTriaPerThread;
+    const dim3 grid((unsigned)ceil_div(a.n, kTriaThreads * EPT)), blk(kTriaThreads);
+#define LOOM_PT(M, G, A, S) hipLaunchKernelGGL((paraplex_tria_kernel<T, M, G, A, S, EPT>), grid, blk, 0, st, a)
 #define LOOM_PT_AXIS(M, G, S)                     \
     switch (axis) {                               \
         case 0: LOOM_PT(M, G, 0, S); break;       \
