@@ -116,7 +116,7 @@ def prefill(eng, prompt: torch.Tensor) -> None:
         eng.depth_read(sub, hist, out, rows)
 
     main = torch.cuda.current_stream(dev)
-    aux = torch.cuda.Stream(device=dev)
+    aux = eng.aux_stream
 
     def fork():                 # aux continues after everything queued on main so far
         aux.wait_stream(main)
