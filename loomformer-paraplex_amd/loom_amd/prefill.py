@@ -83,7 +83,10 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     gbuf = z(M, H) if c.gate_proj else None
     beta = z(M, H)
     act = z(M, H)
-    hist = z(M, 2 * L, 2 * N)
+    # depth histories of two chunks: the next chunk's slot 0 is projected while
+    # this chunk's slots are still read
+    hists = (z(M, 2 * L, 2 * N), z(M, 2 * L, 2 * N))
+    h0 = z(M, N)                 # token embeddings of a chunk
     carry = z(2, M, H, 3, 3)
     pbuf = z(2, M, H)
     traces = z(2, L, B, H)       # phase traces in / out of a chunk (swapped per chunk)
@@ -115,6 +118,25 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     def depth(sub, out, rows):
         eng.depth_read(sub, hist, out, rows)
 
+    spans = list(zip([0] + [x + 1 for x in ends[:-1]], ends))
+
+    def chunk_head(ci):
+        """Layer 0's attention sublayer inputs of chunk ci, which need only the
+        chunk's tokens and the layer-0 K/V rows of earlier chunks: embeddings,
+        history slot 0 and its depth read, qkv, RoPE + cache append + attention
+        (on the current stream)."""
+        s_, e_ = spans[ci]
+        rows_ = B * (e_ - s_ + 1)
+        hist_ = hists[ci % 2]
+        torch.index_select(eng.emb, 0, prompt_d[:, s_:e_ + 1].reshape(-1), out=h0[:rows_])
+        lin(h0, eng.kvw, hist_[:rows_, 0], rows_, 2 * N, N, ldc=2 * L * 2 * N)
+        eng.depth_read(0, hist_, d, rows_)
+        lin(h0, eng.blocks[0]["qkv"], qkv, rows_, N + 2 * c.KV, N)
+        call("loom_gqa_prefill", code, _P(qkv), N + 2 * c.KV, _P(eng.k_cache[0]),
+             _P(eng.v_cache[0]), cache_sb, cache_st, cache_sh, _P(eng.cos), _P(eng.sin),
+             _P(q), _P(cbuf), _P(kctx), N, B, e_ - s_ + 1, s_, eng.max_len, QH, KVH, HD,
+             eng._stream())
+
     main = torch.cuda.current_stream(dev)
     aux = eng.aux_stream
 
@@ -128,32 +150,34 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     tin = 0
     seed_valid = z(B, dtype=torch.uint8)
     ca_len = 0
-    s = 0
-    for e in ends:
+    # Two streams, default priority: `aux` runs the work of a layer that does
+    # not depend on the depth history (qkv -> attention, W_real) while the main
+    # stream runs the history projections and depth reads; they meet before
+    # every product that needs both.  Layer 0's attention inputs of the next
+    # chunk run on aux while main finishes the chunk (its last Paraplex + Tria,
+    # FFN tail and temporal carry).
+    fork()
+    with torch.cuda.stream(aux):
+        chunk_head(0)
+    for ci, (s, e) in enumerate(spans):
         Tc = e - s + 1
         rows = B * Tc
-        # token rows (b, t) of this chunk, b-major
-        ids = prompt_d[:, s:e + 1].reshape(-1)
-        torch.index_select(eng.emb, 0, ids, out=h[:rows])
+        hist = hists[ci % 2]
         hv = hist[:rows]
-        lin(h, eng.kvw, hv[:, 0], rows, 2 * N, N, ldc=2 * L * 2 * N)
-        lin(h, eng.blocks[0]["qkv"], qkv, rows, N + 2 * c.KV, N)
         sub = 0
         carry_i, p_i = None, None
-        # Two streams, default priority: `aux` runs the work of a layer that
-        # does not depend on the depth history (qkv -> attention, W_real) while
-        # the main stream runs the history projections and depth reads; they
-        # meet before every product that needs both.
-        fork()
         for bi, blk in enumerate(eng.blocks):
             last = bi == L - 1
             # ---- attention over the cache (rows < s) and this chunk (loomformer.py:3215-3332),
-            # on aux after this layer's qkv; the depth read 2*bi on main
-            with torch.cuda.stream(aux):
-                call("loom_gqa_prefill", code, _P(qkv), N + 2 * c.KV, _P(eng.k_cache[bi]),
-                     _P(eng.v_cache[bi]), cache_sb, cache_st, cache_sh, _P(eng.cos), _P(eng.sin),
-                     _P(q), _P(cbuf), _P(kctx), N, B, Tc, s, eng.max_len, QH, KVH, HD, eng._stream())
-            depth(sub, d, rows)
+            # on aux after this layer's qkv; the depth read 2*bi on main (layer 0's
+            # ran ahead on aux)
+            if bi > 0:
+                with torch.cuda.stream(aux):
+                    call("loom_gqa_prefill", code, _P(qkv), N + 2 * c.KV, _P(eng.k_cache[bi]),
+                         _P(eng.v_cache[bi]), cache_sb, cache_st, cache_sh, _P(eng.cos),
+                         _P(eng.sin), _P(q), _P(cbuf), _P(kctx), N, B, Tc, s, eng.max_len, QH,
+                         KVH, HD, eng._stream())
+                depth(sub, d, rows)
             join()
             # ---- LN(o(C) + w_o(depth read 2*bi)) (loomformer.py:3999-4000)
             lin_ln(("attn", bi), cbuf, blk["o"], d, eng.wo_for(sub), None, blk["ln1_w"], blk["ln1_b"],
@@ -181,6 +205,12 @@ def prefill(eng, prompt: torch.Tensor) -> None:
                 gsrc = gbuf
                 lin(h, blk["gpw"], gbuf, rows, H, N, bias=blk["gpb"])
             join()
+            if last and ci + 1 < len(spans):
+                # the next chunk's layer-0 attention inputs, after this layer's
+                # beta space has read q, kctx and c
+                fork()
+                with torch.cuda.stream(aux):
+                    chunk_head(ci + 1)
             # ---- with the block's Tria depth op (loomformer.py:3588-3617), axis bi % 3,
             # in the same pass: the phase I never leaves the chip
             out_i = 0 if carry_i != 0 else 1
@@ -237,7 +267,6 @@ def prefill(eng, prompt: torch.Tensor) -> None:
         else:
             seed_valid.zero_()
         tin = 1 - tin
-        s = e + 1
     # ---- final cross-attention and head of the last prompt token (tria.py:1560-1595)
     Tc = ends[-1] - (ends[-2] + 1 if len(ends) > 1 else 0) + 1
     h_last = h[:B * Tc].view(B, Tc, N)[:, Tc - 1].contiguous()
