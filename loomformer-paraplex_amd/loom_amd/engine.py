@@ -183,10 +183,11 @@ class LoomDecoder:
         self.pos = 0
         self._graphs: Dict[int, torch.cuda.CUDAGraph] = {}
         self._descs: Dict[object, object] = {}
-        # the chunked prefill's second stream, created once: HIP deals new
+        # the chunked prefill's second and third streams, created once: HIP deals new
         # streams round-robin over a few hardware queues, so a stream made per
         # call would in time share the main stream's queue and serialise
         self.aux_stream = torch.cuda.Stream(device=dev)
+        self.tail_stream = torch.cuda.Stream(device=dev)
 
     # ------------------------------------------------------------------ helpers
 

@@ -139,6 +139,8 @@ def prefill(eng, prompt: torch.Tensor) -> None:
 
     main = torch.cuda.current_stream(dev)
     aux = eng.aux_stream
+    tail = eng.tail_stream        # a chunk's temporal carry and document key
+    tail_st = _lib.c_void_p(tail.cuda_stream)
 
     def fork():                 # aux continues after everything queued on main so far
         aux.wait_stream(main)
@@ -217,6 +219,8 @@ def prefill(eng, prompt: torch.Tensor) -> None:
             gate = not last
             new_p = (0 if p_i != 0 else 1) if gate else None
             seeded = bi == 0 and have_state
+            if seeded:
+                main.wait_stream(tail)      # the state after the previous chunk
             call("loom_paraplex_tria_forward", code, _P(R), _P(gsrc), _P(beta), _P(blk["ib"]),
                  _P(traces[tin, bi]), _P(blk["tw"]), float(c.powlu_m),
                  None if (carry_i is None or seeded) else _P(carry[carry_i]),
@@ -225,6 +229,8 @@ def prefill(eng, prompt: torch.Tensor) -> None:
                  _P(carry[out_i]), _P(pbuf[new_p]) if gate else None, B, Tc, H,
                  float(c.tria_alpha), bi % 3, st)
             carry_i, p_i = out_i, new_p
+            if last:
+                tail.wait_stream(main)      # the chunk's last carry is written
             # ---- LN(w_o(d_h) + W2(act) + b2) (loomformer.py:4045)
             lin_ln(("ffn", bi), dh, eng.wo_for(sub), act, blk["w2"], blk["b2"], blk["ln2_w"],
                    blk["ln2_b"], rows)
@@ -235,38 +241,41 @@ def prefill(eng, prompt: torch.Tensor) -> None:
                 with torch.cuda.stream(aux):
                     lin(h, eng.blocks[bi + 1]["qkv"], qkv, rows, N + 2 * c.KV, N)
                 lin(h, eng.kvw, hv[:, sub], rows, 2 * N, N, ldc=2 * L * 2 * N)
-        # ---- temporal carry over the chunk: restart at position 0 and at a
-        # seeded first token, else continue from the state (loomformer.py:3834-3850)
-        reset = z(B, Tc, dtype=torch.uint8)
-        if s == 0:
-            reset[:, 0] = 1
-        else:
-            reset[:, 0] = seed_valid
-        call("loom_temporal_carry_endpoint_forward", code, _P(carry[carry_i]), _P(reset),
-             _P(state) if have_state else None, None, _P(state), _P(state32), B, Tc, H, st)
-        have_state = True
-        fire_e = fire_all_d[:, e]
-        if bool(fire_all[:, e].any()):
-            # PolARM where the row fired, then the document key of this boundary
-            fmask = fire_e.to(torch.uint8)
-            call("loom_polarm_forward", code, _P(state), _P(state), _P(fmask), B * H, H,
-                 float(c.polarm_beta), 1e-6, st)
-            call("loom_slot_attention_pool_forward", code, _P(state), _P(eng.score_w),
-                 _P(pooled), None, B, H, st)
-            lin(pooled, eng.proj_w, z32, B, 32, 9, bias=eng.proj_b)
-            lin(z32, eng.up_w, a_key, B, N, 32, bias=eng.up_b)
-            lin(a_key, eng.wqk, stage_k, B, N, N)
-            lin(a_key, eng.wv, stage_v, B, N, N)
-            if ca_len >= eng.max_keys:
-                raise ValueError("final-CA key cache is full")
-            eng.ca_k[:, ca_len].copy_(stage_k)
-            eng.ca_v[:, ca_len].copy_(stage_v)
-            eng.ca_valid[:, ca_len].copy_(fmask)
-            ca_len += 1
-            seed_valid.copy_(fmask)
-        else:
-            seed_valid.zero_()
+        # ---- on the third stream, beside the next chunk's first sublayer: the
+        # temporal carry over the chunk, restarting at position 0 and at a
+        # seeded first token, else continuing from the state (loomformer.py:3834-3850)
+        with torch.cuda.stream(tail):
+            reset = z(B, Tc, dtype=torch.uint8)
+            if s == 0:
+                reset[:, 0] = 1
+            else:
+                reset[:, 0] = seed_valid
+            call("loom_temporal_carry_endpoint_forward", code, _P(carry[carry_i]), _P(reset),
+                 _P(state) if have_state else None, None, _P(state), _P(state32), B, Tc, H, tail_st)
+            have_state = True
+            fire_e = fire_all_d[:, e]
+            if bool(fire_all[:, e].any()):
+                # PolARM where the row fired, then the document key of this boundary
+                fmask = fire_e.to(torch.uint8)
+                call("loom_polarm_forward", code, _P(state), _P(state), _P(fmask), B * H, H,
+                     float(c.polarm_beta), 1e-6, tail_st)
+                call("loom_slot_attention_pool_forward", code, _P(state), _P(eng.score_w),
+                     _P(pooled), None, B, H, tail_st)
+                lin(pooled, eng.proj_w, z32, B, 32, 9, bias=eng.proj_b)
+                lin(z32, eng.up_w, a_key, B, N, 32, bias=eng.up_b)
+                lin(a_key, eng.wqk, stage_k, B, N, N)
+                lin(a_key, eng.wv, stage_v, B, N, N)
+                if ca_len >= eng.max_keys:
+                    raise ValueError("final-CA key cache is full")
+                eng.ca_k[:, ca_len].copy_(stage_k)
+                eng.ca_v[:, ca_len].copy_(stage_v)
+                eng.ca_valid[:, ca_len].copy_(fmask)
+                ca_len += 1
+                seed_valid.copy_(fmask)
+            else:
+                seed_valid.zero_()
         tin = 1 - tin
+    main.wait_stream(tail)
     # ---- final cross-attention and head of the last prompt token (tria.py:1560-1595)
     Tc = ends[-1] - (ends[-2] + 1 if len(ends) > 1 else 0) + 1
     h_last = h[:B * Tc].view(B, Tc, N)[:, Tc - 1].contiguous()
