@@ -83,9 +83,7 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     gbuf = z(M, H) if c.gate_proj else None
     beta = z(M, H)
     act = z(M, H)
-    # depth histories of two chunks: the next chunk's slot 0 is projected while
-    # this chunk's slots are still read
-    hists = (z(M, 2 * L, 2 * N), z(M, 2 * L, 2 * N))
+    hist = z(M, 2 * L, 2 * N)
     h0 = z(M, N)                 # token embeddings of a chunk
     carry = z(2, M, H, 3, 3)
     pbuf = z(2, M, H)
@@ -120,17 +118,17 @@ def prefill(eng, prompt: torch.Tensor) -> None:
 
     spans = list(zip([0] + [x + 1 for x in ends[:-1]], ends))
 
+    gathered = torch.cuda.Event()
+
     def chunk_head(ci):
-        """Layer 0's attention sublayer inputs of chunk ci, which need only the
-        chunk's tokens and the layer-0 K/V rows of earlier chunks: embeddings,
-        history slot 0 and its depth read, qkv, RoPE + cache append + attention
-        (on the current stream)."""
+        """Layer 0's attention inputs of chunk ci, which need only the chunk's
+        tokens and the layer-0 K/V rows of earlier chunks: embeddings, qkv,
+        RoPE + cache append + attention (on the current stream; `gathered` is
+        recorded once the embeddings are in h0)."""
         s_, e_ = spans[ci]
         rows_ = B * (e_ - s_ + 1)
-        hist_ = hists[ci % 2]
         torch.index_select(eng.emb, 0, prompt_d[:, s_:e_ + 1].reshape(-1), out=h0[:rows_])
-        lin(h0, eng.kvw, hist_[:rows_, 0], rows_, 2 * N, N, ldc=2 * L * 2 * N)
-        eng.depth_read(0, hist_, d, rows_)
+        gathered.record()
         lin(h0, eng.blocks[0]["qkv"], qkv, rows_, N + 2 * c.KV, N)
         call("loom_gqa_prefill", code, _P(qkv), N + 2 * c.KV, _P(eng.k_cache[0]),
              _P(eng.v_cache[0]), cache_sb, cache_st, cache_sh, _P(eng.cos), _P(eng.sin),
@@ -152,21 +150,26 @@ def prefill(eng, prompt: torch.Tensor) -> None:
     tin = 0
     seed_valid = z(B, dtype=torch.uint8)
     ca_len = 0
-    # Two streams, default priority: `aux` runs the work of a layer that does
+    # Three streams, default priority: `aux` runs the work of a layer that does
     # not depend on the depth history (qkv -> attention, W_real) while the main
     # stream runs the history projections and depth reads; they meet before
-    # every product that needs both.  Layer 0's attention inputs of the next
-    # chunk run on aux while main finishes the chunk (its last Paraplex + Tria,
-    # FFN tail and temporal carry).
+    # every product that needs both.  Layer 0's attention of the next chunk
+    # runs on aux while main finishes the chunk (its last Paraplex + Tria and
+    # FFN tail), and `tail` takes the chunk's temporal carry and document key
+    # beside the next chunk's first sublayer.
     fork()
     with torch.cuda.stream(aux):
         chunk_head(0)
     for ci, (s, e) in enumerate(spans):
         Tc = e - s + 1
         rows = B * Tc
-        hist = hists[ci % 2]
         hv = hist[:rows]
         sub = 0
+        # history slot 0 of the chunk and its depth read, on main once the
+        # embeddings are gathered
+        main.wait_event(gathered)
+        lin(h0, eng.kvw, hv[:, 0], rows, 2 * N, N, ldc=2 * L * 2 * N)
+        depth(0, d, rows)
         carry_i, p_i = None, None
         for bi, blk in enumerate(eng.blocks):
             last = bi == L - 1
