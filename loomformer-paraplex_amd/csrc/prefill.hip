@@ -336,7 +336,7 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
 #pragma unroll
         for (int u = 0; u < PPT; ++u) {
             const int p = tid + 256 * u;
-            if (p < 2 * PIECES) {
+            if ((2 * PIECES) % 256 == 0 || p < 2 * PIECES) {
                 const int tensor = p / PIECES, q = p % PIECES;
                 const int row = q / CPR, ch = q % CPR;
                 int64_t r = r0 + row;
@@ -351,7 +351,7 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
 #pragma unroll
         for (int u = 0; u < PPT; ++u) {
             const int p = tid + 256 * u;
-            if (p < 2 * PIECES) {
+            if ((2 * PIECES) % 256 == 0 || p < 2 * PIECES) {
                 const int tensor = p / PIECES, q = p % PIECES;
                 const int row = q / CPR, ch = q % CPR;
                 gqa_u4* dst = tensor == 0 ? tk[SET] : tv[SET];
@@ -361,9 +361,10 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
-    load_tile(S0{}, 0);
-    if (nsteps > 1) load_tile(S1{}, kPfRows);
-    // B operand of S^T: q of query column lr, dims 32*kk + 8*lq .. +7
+    // B operand of S^T: q of query column lr, dims 32*kk + 8*lq .. +7; loaded
+    // first and complete before the loop (a register loaded ahead of a loop
+    // whose own loads stay in flight would be waited for inside it, and that
+    // wait would also drain the tile prefetches)
     uint4 qf[KK];
     {
         const int qrow = qcol < a.Tc ? qcol : a.Tc - 1;
@@ -372,6 +373,11 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
         for (int kk = 0; kk < KK; ++kk)
             qf[kk] = *reinterpret_cast<const uint4*>(qp + 32 * kk + 8 * lq);
     }
+    load_tile(S0{}, 0);
+    load_tile(S1{}, kPfRows);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+        asm volatile("" : "+v"(qf[kk].x), "+v"(qf[kk].y), "+v"(qf[kk].z), "+v"(qf[kk].w));
     store_tile(S0{});
     lds_sync();
 
@@ -382,11 +388,13 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
 
     // step it computes tile it from LDS buffer it % 2, requests tile it+2 into
     // register set it % 2 (its tile it went to LDS a step ago) and stores
-    // tile it+1 (requested a step ago) into the other buffer
+    // tile it+1 (requested a step ago) into the other buffer.  Every step
+    // requests a tile (rows past kmax clamp to it), so the loads in flight are
+    // the same on every path and each store waits for its own tile only.
     auto step = [&](auto set_, int it) {
         constexpr int cur = decltype(set_)::value;
         const int64_t r0 = (int64_t)it * kPfRows;
-        if (it + 2 < nsteps) load_tile(set_, r0 + 2 * kPfRows);
+        load_tile(set_, r0 + 2 * kPfRows);
         const bool active = r0 <= wave_kmax;                 // wave-uniform
         if (active) {
             f32x4_p sc[2];
@@ -459,9 +467,10 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
         if (it + 1 < nsteps) store_tile(std::integral_constant<int, cur ^ 1>{});
         lds_sync();
     };
+    // an even number of steps (a last step past kmax computes nothing)
     for (int it = 0; it < nsteps; it += 2) {
         step(S0{}, it);
-        if (it + 1 < nsteps) step(S1{}, it + 1);
+        step(S1{}, it + 1);
     }
     // normalise: the sum of query column c lives in lanes with lr == c
 #pragma unroll
