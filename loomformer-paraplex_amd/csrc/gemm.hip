@@ -79,7 +79,14 @@ __device__ __forceinline__ const void* gather_ptr(const GemmArgs& a, int64_t m, 
         else if (kk < HD + 3 * Nm) { s = 3; col = kk - HD - 2 * Nm; }
         else { s = 4; col = kk - HD - 3 * Nm; }
     }
-    return (const char*)a.src[s] + (m * Nm + col) * elem_size;
+    // the source picked by masks over constant indices, so the pointers stay
+    // in scalar registers: an array indexed by a per-lane value is read from
+    // memory, and the wait for that read also drains the operand loads in
+    // flight (a select chain is folded back into such a read)
+    uintptr_t base = 0;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) base |= (uintptr_t)a.src[i] & (uintptr_t)(-(intptr_t)(s == i));
+    return (const char*)base + (m * Nm + col) * elem_size;
 }
 
 template <typename T>
