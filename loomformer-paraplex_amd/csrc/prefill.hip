@@ -323,26 +323,38 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     const int qpos32 = (int)qpos;          // positions fit 31 bits (checked by the host)
     const TileLane<CPR> tl(lq, lr);
     const int wave_qlast = min(q0 + 15, a.Tc - 1);
+    const int wave_qpos0 = (int)a.start + q0;    // position of the wave's first query
     const int64_t wave_kmax = q0 < a.Tc ? a.start + wave_qlast : -1;
 
     const bf16_t* kb = a.kc + b * a.csb + kvh * a.csh;
     const bf16_t* vb = a.vc + b * a.csb + kvh * a.csh;
-    // one 32-row tile: piece p -> (tensor, row, piece of the row), rows clamped
-    // to kmax; two register sets, so a tile is requested two steps before its
-    // LDS store (tile t in set t % 2)
+    // one 32-row tile: piece p -> (tensor, row, piece of the row), read through
+    // buffer resources that end after row kmax: rows past it read as zero
+    // (positions after every query of the block, masked out), so a load needs
+    // no clamp and its offset is a per-thread constant plus the step's rows.
+    // The tensor of a piece is the same across a wave (PIECES is a multiple
+    // of 64).  Two register sets, so a tile is requested two steps before
+    // its LDS store (tile t in set t % 2).
+    const int kv_bytes = (int)((kmax + 1) * a.cst * 2);
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)kb, (short)0, kv_bytes, kBufferDword3);
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0, kv_bytes, kBufferDword3);
+    const uint32_t row_bytes = (uint32_t)(a.cst * 2);
+    uint32_t voff[PPT];
+#pragma unroll
+    for (int u = 0; u < PPT; ++u) {
+        const int q = (tid + 256 * u) % PIECES;
+        voff[u] = (uint32_t)(q / CPR) * row_bytes + (uint32_t)(q % CPR) * 16u;
+    }
     gqa_u4 reg[2][PPT];
     auto load_tile = [&](auto set_, int64_t r0) {
         constexpr int SET = decltype(set_)::value;
+        const uint32_t base = (uint32_t)r0 * row_bytes;
 #pragma unroll
         for (int u = 0; u < PPT; ++u) {
             const int p = tid + 256 * u;
             if ((2 * PIECES) % 256 == 0 || p < 2 * PIECES) {
-                const int tensor = p / PIECES, q = p % PIECES;
-                const int row = q / CPR, ch = q % CPR;
-                int64_t r = r0 + row;
-                r = r <= kmax ? r : kmax;
-                const bf16_t* src = (tensor == 0 ? kb : vb) + r * a.cst + 8 * ch;
-                reg[SET][u] = *reinterpret_cast<const gqa_u4*>(src);
+                const bool is_k = __builtin_amdgcn_readfirstlane(p / PIECES) == 0;
+                reg[SET][u] = __builtin_amdgcn_raw_buffer_load_b128(is_k ? rk : rv, voff[u] + base, 0, 0);
             }
         }
     };
@@ -389,8 +401,8 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     // step it computes tile it from LDS buffer it % 2, requests tile it+2 into
     // register set it % 2 (its tile it went to LDS a step ago) and stores
     // tile it+1 (requested a step ago) into the other buffer.  Every step
-    // requests a tile (rows past kmax clamp to it), so the loads in flight are
-    // the same on every path and each store waits for its own tile only.
+    // requests a tile (rows past kmax read as zero), so the loads in flight
+    // are the same on every path and each store waits for its own tile only.
     auto step = [&](auto set_, int it) {
         constexpr int cur = decltype(set_)::value;
         const int64_t r0 = (int64_t)it * kPfRows;
@@ -405,27 +417,41 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
                 for (int kk = 0; kk < KK; ++kk)
                     sc[hf] = mfma16p(tile_s_frag<CPR>(tk[cur], tl, hf, kk), qf[kk], sc[hf]);
             }
-            // S^T[row 16*hf + 4*lq + r][query column lr]
+            // S^T[row 16*hf + 4*lq + r][query column lr], unscaled; rows after
+            // a column's position are masked only in the tiles that reach the
+            // wave's first query (the scale is applied inside the exponent:
+            // the maximum of the scaled scores is the scaled maximum)
             float sv[2][4];
             float mx = -INFINITY;
+            if ((int)r0 + kPfRows - 1 <= wave_qpos0) {     // wave-uniform
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf)
+                for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int row = (int)r0 + 16 * hf + 4 * lq + r;
-                    sv[hf][r] = row <= qpos32 ? sc[hf][r] * a.qscale : -INFINITY;
-                    mx = fmaxf(mx, sv[hf][r]);
-                }
+                    for (int r = 0; r < 4; ++r) {
+                        sv[hf][r] = sc[hf][r];
+                        mx = fmaxf(mx, sv[hf][r]);
+                    }
+            } else {
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int row = (int)r0 + 16 * hf + 4 * lq + r;
+                        sv[hf][r] = row <= qpos32 ? sc[hf][r] : -INFINITY;
+                        mx = fmaxf(mx, sv[hf][r]);
+                    }
+            }
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mnew = fmaxf(mh, mx);               // finite: row 0 is seen at step 0
+            const float mnew = fmaxf(mh, mx * a.qscale);    // finite: row 0 is seen at step 0
             const float corr = __builtin_amdgcn_exp2f(mh - mnew);
             float ls = 0.0f, pv[2][4];
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    pv[hf][r] = sv[hf][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[hf][r] - mnew);
+                    // a masked score gives exp2(-inf) = 0
+                    pv[hf][r] = __builtin_amdgcn_exp2f(fmaf(sv[hf][r], a.qscale, -mnew));
                     ls += pv[hf][r];
                 }
             ls += __shfl_xor(ls, 16, 64);
@@ -530,8 +556,11 @@ static int prefill_dispatch(const void* qkv, int64_t qkv_ld, void* kc, void* vc,
     a.qscale = kLog2e / sqrtf((float)HD);
     const int G = (int)(QH / KVH);
     if constexpr (std::is_same<T, bf16_t>::value) {
+        // the MFMA form addresses a (row, kv head)'s cache rows with 32-bit
+        // byte offsets, up to four tiles past the chunk's last position
         const bool mf_ok = (HD == 32 || HD == 64 || HD == 96 || HD == 128) &&
-                           (G == 1 || G == 2 || G == 4 || G == 8);
+                           (G == 1 || G == 2 || G == 4 || G == 8) &&
+                           (start + Tc + 4 * kPfRows) * cst * 2 < ((int64_t)1 << 31);
         if (mf_ok) {
 #define LOOM_PF_MF(HDV)                                                                          \
             if (HD == HDV) {                                                                     \
