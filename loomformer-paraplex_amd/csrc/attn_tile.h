@@ -26,7 +26,9 @@ typedef uint32_t gqa_u4 __attribute__((ext_vector_type(4)));   // a 16-byte piec
 //   t_off[p][h]: tile_tr_frag's read h of dim tile dt with dt % 2 == p ->
 //     t_off[p][h] + 64*(dt/2) (piece (2*dt + b) ^ kv_swz(row) is
 //     4*(dt/2) + a lane constant for each parity of dt).
-template <int CPR>
+// PITCH: pieces per LDS row (CPR, or more to spread rows over the banks);
+// SWZ: pieces stored at c ^ kv_swz(r) (else at c).
+template <int CPR, int PITCH = CPR, bool SWZ = true>
 struct TileLane {
     uint32_t s_off[2];
     uint32_t t_off[2][2];
@@ -34,25 +36,25 @@ struct TileLane {
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
             const int row = 16 * hf + lr;
-            s_off[hf] = (uint32_t)((row * CPR + (lq ^ kv_swz(row))) * 16);
+            s_off[hf] = (uint32_t)((row * PITCH + (SWZ ? lq ^ kv_swz(row) : lq)) * 16);
         }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int row = 16 * h + 4 * lq + (lr >> 2);
-            const int sw = kv_swz(row), b1 = (lr & 3) >> 1;
+            const int sw = SWZ ? kv_swz(row) : 0, b1 = (lr & 3) >> 1;
 #pragma unroll
             for (int par = 0; par < 2; ++par) {
                 const int q = ((par ^ (sw >> 1)) << 1) | (b1 ^ (sw & 1));
-                t_off[par][h] = (uint32_t)((row * CPR + q) * 16 + 8 * (lr & 1));
+                t_off[par][h] = (uint32_t)((row * PITCH + q) * 16 + 8 * (lr & 1));
             }
         }
     }
 };
 
 // A operand of S^T (16 K rows x 32 dims of k-step kk) from a row-major tile
-template <int CPR>
-__device__ __forceinline__ gqa_u4 tile_s_frag(const gqa_u4* tile, const TileLane<CPR>& L, int hf,
-                                              int kk) {
+template <int CPR, int PITCH, bool SWZ>
+__device__ __forceinline__ gqa_u4 tile_s_frag(const gqa_u4* tile, const TileLane<CPR, PITCH, SWZ>& L,
+                                              int hf, int kk) {
     return *reinterpret_cast<const gqa_u4*>(reinterpret_cast<const char*>(tile) + L.s_off[hf] + 64 * kk);
 }
 
@@ -64,8 +66,9 @@ __device__ __forceinline__ gqa_u4 tile_s_frag(const gqa_u4* tile, const TileLane
 // P feeds P V and P K straight from registers.  Two transposing 8-byte reads:
 // lane r of a 16-lane group points at row k0 + r/4, dims 16*dt + 4*(r%4)..+3
 // and receives rows k0..k0+3 of dim 16*dt + r (k0 = 16*h + 4q).
-template <int CPR>
-__device__ __forceinline__ uint4 tile_tr_frag(const gqa_u4* tile, const TileLane<CPR>& L, int dt) {
+template <int CPR, int PITCH, bool SWZ>
+__device__ __forceinline__ uint4 tile_tr_frag(const gqa_u4* tile, const TileLane<CPR, PITCH, SWZ>& L,
+                                              int dt) {
     uint2 w[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {

@@ -298,8 +298,12 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     constexpr int G = GP * HSPLIT;
     constexpr int PIECES = kPfRows * CPR;       // pieces of one tensor's 32-row tile
     constexpr int PPT = (2 * PIECES + 255) / 256;
-    __shared__ __align__(16) gqa_u4 tk[2][PIECES];       // K tile, row-major, two buffers
-    __shared__ __align__(16) gqa_u4 tv[2][PIECES];       // V tile
+    // LDS rows one piece longer than a head row: with HD = 96 (12 pieces) the
+    // 16 rows of a fragment read, and the 4 rows of a transposing read, start
+    // in distinct banks, with no swizzle
+    constexpr int PITCH = CPR + 1;
+    __shared__ __align__(16) gqa_u4 tk[2][kPfRows * PITCH];   // K tile, row-major, two buffers
+    __shared__ __align__(16) gqa_u4 tv[2][kPfRows * PITCH];   // V tile
     __shared__ float cr[4][16];                           // per-column rescale of a step
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 15, lq = lane >> 4;
@@ -321,7 +325,7 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     const int qcol = q0 + lr;
     const int64_t qpos = qcol < a.Tc ? a.start + qcol : 0;
     const int qpos32 = (int)qpos;          // positions fit 31 bits (checked by the host)
-    const TileLane<CPR> tl(lq, lr);
+    const TileLane<CPR, PITCH, false> tl(lq, lr);
     const int wave_qlast = min(q0 + 15, a.Tc - 1);
     const int wave_qpos0 = (int)a.start + q0;    // position of the wave's first query
     const int64_t wave_kmax = q0 < a.Tc ? a.start + wave_qlast : -1;
@@ -367,7 +371,7 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
                 const int tensor = p / PIECES, q = p % PIECES;
                 const int row = q / CPR, ch = q % CPR;
                 gqa_u4* dst = tensor == 0 ? tk[SET] : tv[SET];
-                dst[row * CPR + (ch ^ kv_swz(row))] = reg[SET][u];
+                dst[row * PITCH + ch] = reg[SET][u];
             }
         }
     };
