@@ -937,10 +937,11 @@ decode_readout_heads_kernel(const T* __restrict__ depth, const T* prev,
         l = 1.0f;                          // one head: p = e^(sc - m) = 1
     }
     // the readout feeds only the keys staged at a fire: without one, stop here
+    // (one flag per thread, OR over the block: one memory round trip)
     if (fire != nullptr) {
-        bool any = false;
-        for (int q = 0; q < (int)gridDim.y; ++q) any |= fire[q] != 0;
-        if (!any) return;
+        int any = 0;
+        for (int q = tid; q < (int)gridDim.y; q += kReadHeads) any |= fire[q] != 0;
+        if (!__syncthreads_or(any)) return;
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -994,9 +995,9 @@ decode_readout_rows_kernel(const float* __restrict__ rec, int nrec, const T* __r
     const int64_t b = blockIdx.y;
     const int n = blockIdx.x * kReadCols + tid;
     if (fire != nullptr) {                 // no fire: no key to stage, a_out is left as it is
-        bool any = false;
-        for (int q = 0; q < (int)gridDim.y; ++q) any |= fire[q] != 0;
-        if (!any) return;
+        int any = 0;
+        for (int q = tid; q < (int)gridDim.y; q += kReadCols) any |= fire[q] != 0;
+        if (!__syncthreads_or(any)) return;
     }
     // every load first: this row's records, the proj row of thread tid < 32 and
     // the up row of column n
@@ -1438,15 +1439,11 @@ decode_epilogue_kernel(const T* __restrict__ stage_k, const T* __restrict__ stag
                        int64_t* __restrict__ ca_len, const uint8_t* __restrict__ fire,
                        uint8_t* __restrict__ pending, int64_t* __restrict__ pos_dev, int64_t B,
                        int64_t N, int64_t max_keys) {
-    __shared__ int any;
     __shared__ int64_t slot;
-    if (threadIdx.x == 0) {
-        int a = 0;
-        for (int64_t b = 0; b < B; ++b) a |= fire[b];
-        any = a;
-        slot = *ca_len;
-    }
-    __syncthreads();
+    int a = 0;
+    for (int64_t b = threadIdx.x; b < B; b += blockDim.x) a |= fire[b];
+    if (threadIdx.x == 0) slot = *ca_len;
+    const int any = __syncthreads_or(a);   // also orders slot's store before its reads
     if (any && slot < max_keys) {
         for (int64_t e = threadIdx.x; e < B * N; e += blockDim.x) {
             const int64_t b = e / N, d = e - b * N;

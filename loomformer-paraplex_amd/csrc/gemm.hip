@@ -961,10 +961,10 @@ __global__ void __launch_bounds__(NW * 64)
 gemm_bf16_skinny_multi_kernel(LinArgs a) {
     __shared__ float red[NW][MT][4][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (a.only_if != nullptr) {              // block-uniform: every thread reads all flags
-        bool any = false;
-        for (int i = 0; i < a.only_if_n; ++i) any |= a.only_if[i] != 0;
-        if (!any) return;
+    if (a.only_if != nullptr) {              // one flag per thread, OR over the block
+        int any = 0;
+        for (int i = tid; i < a.only_if_n; i += NW * 64) any |= a.only_if[i] != 0;
+        if (!__syncthreads_or(any)) return;  // block-uniform
     }
     const int64_t ng = (int64_t)blockIdx.x * 16;
     int s = 0;
