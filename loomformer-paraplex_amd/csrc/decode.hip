@@ -911,13 +911,21 @@ decode_readout_heads_kernel(const T* __restrict__ depth, const T* prev,
     const int h = blockIdx.x * kReadHeads + tid;
     const bool cont = prev != nullptr && reset_now[b] == 0;
     const bool fires = fire != nullptr && fire[b] != 0;
-    const int64_t e = (b * H + h) * 9;
+    // every load unconditional (a lane past H reads head H-1, then drops it),
+    // so all of them are in flight at once instead of one round trip each
+    const int64_t e = (b * H + (h < H ? h : H - 1)) * 9;
+    const T* pp = prev != nullptr ? prev : depth;
     float M[9], P[9], sw[9];
 #pragma unroll
     for (int k = 0; k < 9; ++k) {
-        M[k] = h < H ? ld(depth + e + k) : 0.0f;
-        P[k] = (cont && h < H) ? ld(prev + e + k) : 0.0f;
+        M[k] = ld(depth + e + k);
+        P[k] = ld(pp + e + k);
         sw[k] = ld(score_w + k);
+    }
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        M[k] = h < H ? M[k] : 0.0f;
+        P[k] = (cont && h < H) ? P[k] : 0.0f;
     }
     float m = -INFINITY, l = 0.0f, acc[9];
 #pragma unroll
@@ -999,20 +1007,23 @@ decode_readout_rows_kernel(const float* __restrict__ rec, int nrec, const T* __r
         for (int q = tid; q < (int)gridDim.y; q += kReadCols) any |= fire[q] != 0;
         if (!__syncthreads_or(any)) return;
     }
-    // every load first: this row's records, the proj row of thread tid < 32 and
+    // every load first, unconditionally (clamped rows, so they are all in
+    // flight at once): this row's records, the proj row of thread tid < 32 and
     // the up row of column n
     const float* rb = rec + b * nrec * kReadRec;
-    for (int i = tid; i < nrec * kReadRec; i += kReadCols) rs[i] = rb[i];
+    const int tot = nrec * kReadRec;
+    const float r0 = rb[min(tid, tot - 1)], r1 = rb[min(tid + kReadCols, tot - 1)];
+    const int pt = min(tid, 31), nn = min(n, N - 1);
     float pw[9], uw[32];
-    float pbias = 0.0f, ubias = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 9; ++k) pw[k] = tid < 32 ? ld(proj_w + tid * 9 + k) : 0.0f;
-    if (tid < 32 && proj_b != nullptr) pbias = proj_b[tid];
-    if (n < N) {
+    for (int k = 0; k < 9; ++k) pw[k] = ld(proj_w + pt * 9 + k);
+    const float pbias = proj_b != nullptr ? proj_b[pt] : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 32; j += 8) Vec8<T>::load(up_w + (int64_t)n * 32 + j, uw + j);
-        if (up_b != nullptr) ubias = up_b[n];
-    }
+    for (int j = 0; j < 32; j += 8) Vec8<T>::load(up_w + (int64_t)nn * 32 + j, uw + j);
+    const float ubias = up_b != nullptr ? up_b[nn] : 0.0f;
+    if (tid < tot) rs[tid] = r0;
+    if (tid + kReadCols < tot) rs[tid + kReadCols] = r1;
+    for (int i = tid + 2 * kReadCols; i < tot; i += kReadCols) rs[i] = rb[i];
     __syncthreads();
     if (tid < 9) {
         float Mx = -INFINITY;
@@ -1504,9 +1515,9 @@ argmax_rows_vec_kernel(const T* __restrict__ logits, int64_t V, int64_t* __restr
     const int nvec = (int)(V / 8);
     float vals[VPT][8];
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
+    for (int i = 0; i < VPT; ++i) {   // unconditional (clamped), so all are in flight at once
         const int v = threadIdx.x + 256 * i;
-        if (v < nvec) Vec8<T>::load(x + 8 * v, vals[i]);
+        Vec8<T>::load(x + 8 * (v < nvec ? v : nvec - 1), vals[i]);
     }
     float best = -INFINITY;
     int idx = (int)V;                      // NaN-free rows always replace this

@@ -1495,14 +1495,17 @@ splitk_ln_kernel(const float* __restrict__ partial, int64_t ldp,
     const int lane = threadIdx.x & 63, k = threadIdx.x >> 6;
     const int c = (lane + 64 * k) * 4;
     const bool in = c < N;
+    // every load unconditional, at column 0 for lanes past N (their values are
+    // never used), so all of a row's loads are in flight at once
+    const int cl = in ? c : 0;
     float4 v[NS], bv, gv, ev;
 #pragma unroll
     for (int sp = 0; sp < NS; ++sp)
-        v[sp] = in ? *reinterpret_cast<const float4*>(partial + (sp * rows + row) * ldp + c)
-                   : make_float4(0.f, 0.f, 0.f, 0.f);
-    bv = (in && bias != nullptr) ? *reinterpret_cast<const float4*>(bias + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-    gv = in ? *reinterpret_cast<const float4*>(gamma + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-    ev = in ? *reinterpret_cast<const float4*>(beta + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[sp] = *reinterpret_cast<const float4*>(partial + (sp * rows + row) * ldp + cl);
+    bv = *reinterpret_cast<const float4*>((bias != nullptr ? bias : gamma) + cl);
+    if (bias == nullptr) bv = make_float4(0.f, 0.f, 0.f, 0.f);
+    gv = *reinterpret_cast<const float4*>(gamma + cl);
+    ev = *reinterpret_cast<const float4*>(beta + cl);
     float x[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
     for (int sp = 0; sp < NS; ++sp) {
