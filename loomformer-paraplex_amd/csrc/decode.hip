@@ -169,26 +169,39 @@ gqa_merge_kernel(const float* __restrict__ rec, int nchunks, int64_t len,
     const int64_t b = e / ((int64_t)HD * QH);
     const int G = QH / KVH, kvh = h / G, g = h % G;
     const int REC = 2 * G + 2 * G * HD;
-    const int64_t n = pos_dev != nullptr ? *pos_dev + 1 : len;
-    const int64_t clen = gqa_chunk_len(n, nchunks);
-    const int nact = (int)((n + clen - 1) / clen);
+    // the records of a batch of chunks are requested before the position is
+    // used (a record past the active chunks is read and then ignored: the
+    // workspace holds nchunks records), so a merge of up to kMergeBatch chunks
+    // is one memory round trip
     const float* recs = rec + (b * KVH + kvh) * (int64_t)nchunks * REC;
     float M = -INFINITY, L = 0.0f, C = 0.0f, K = 0.0f;
-    for (int c0 = 0; c0 < nact; c0 += kMergeBatch) {
+    auto batch = [&](int c0) {
         float m[kMergeBatch], l[kMergeBatch], cv[kMergeBatch], kv[kMergeBatch];
 #pragma unroll
         for (int u = 0; u < kMergeBatch; ++u) {
-            const float* r = recs + (int64_t)(c0 + u) * REC;
-            const bool ok = c0 + u < nact;
-            m[u] = ok ? r[g] : -INFINITY;
-            l[u] = ok ? r[G + g] : 0.0f;
-            cv[u] = ok ? r[2 * G + g * HD + d] : 0.0f;
-            kv[u] = ok ? r[2 * G + G * HD + g * HD + d] : 0.0f;
+            const float* r = recs + (int64_t)(c0 + u < nchunks ? c0 + u : 0) * REC;
+            m[u] = r[g];
+            l[u] = r[G + g];
+            cv[u] = r[2 * G + g * HD + d];
+            kv[u] = r[2 * G + G * HD + g * HD + d];
+        }
+        __builtin_amdgcn_sched_barrier(0);   // the position's wait stays after the requests
+        const int64_t n = pos_dev != nullptr ? *pos_dev + 1 : len;
+        const int64_t clen = gqa_chunk_len(n, nchunks);
+        const int nact = (int)((n + clen - 1) / clen);
+        if (c0 >= nact) return false;
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+            if (c0 + u < nact) continue;
+            m[u] = -INFINITY;
+            l[u] = 0.0f;
+            cv[u] = 0.0f;
+            kv[u] = 0.0f;
         }
         float Mb = M;
 #pragma unroll
         for (int u = 0; u < kMergeBatch; ++u) Mb = fmaxf(Mb, m[u]);
-        if (Mb == -INFINITY) continue;
+        if (Mb == -INFINITY) return true;
         const float r0 = __builtin_amdgcn_exp2f(M - Mb);   // 0 while M is -inf
         L *= r0;
         C *= r0;
@@ -202,7 +215,11 @@ gqa_merge_kernel(const float* __restrict__ rec, int nchunks, int64_t len,
             K = fmaf(kv[u], w, K);
         }
         M = Mb;
-    }
+        return true;
+    };
+    if (batch(0))
+        for (int c0 = kMergeBatch; c0 < nchunks; c0 += kMergeBatch)
+            if (!batch(c0)) break;
     const float inv = 1.0f / L;
     const int64_t o = b * out_sb + h * HD + d;
     st(c_out + o, C * inv);
