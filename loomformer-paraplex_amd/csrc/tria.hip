@@ -651,43 +651,53 @@ final_ca_row_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* _
     __shared__ float wts[kCaRowKeys];
     __shared__ float part[4][128][9];      // [subset][chunk][8] (+1: bank spread)
     __shared__ float red[2];
-    if (k_dev != nullptr) K = *k_dev < K ? *k_dev : K;
+    // every load first and none waiting on the device key count: keys and
+    // values of all K slots the cache holds (slots past the count are read and
+    // masked), q and the residual as raw words, the key mask
+    const int64_t Kcap = K;
     const int64_t row = blockIdx.x;
     const int64_t b = row / T_;
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const int nch = D / 8;
     const T* kb = k + b * kv_stride_b;
     const T* vb = v + b * kv_stride_b;
-    // every load first: q and key chunks for the scores, value chunks for P.V
-    float qf[2][8];
-    uint4 kr[KW][2], vr[KS];
+    uint4 qw[2], kr[KW][2], vr[KS], rw;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-        const int ch = lane + 64 * c;
-        if (ch < nch) {
-            Vec8<T>::load(q + row * D + ch * 8, qf[c]);
+        const int ch = min(lane + 64 * c, nch - 1);
+        qw[c] = *reinterpret_cast<const uint4*>(q + row * D + ch * 8);
 #pragma unroll
-            for (int i = 0; i < KW; ++i) {
-                const int64_t j = wid + 8 * i;
-                if (j < K) kr[i][c] = *reinterpret_cast<const uint4*>(kb + j * D + ch * 8);
-            }
+        for (int i = 0; i < KW; ++i) {
+            const int64_t j = wid + 8 * i;
+            if (j < Kcap) kr[i][c] = *reinterpret_cast<const uint4*>(kb + j * D + ch * 8);
+        }
+    }
+    const int c2 = tid & 127, s2 = tid >> 7;
+    {
+        const int cc = min(c2, nch - 1);
+#pragma unroll
+        for (int i = 0; i < KS; ++i) {
+            const int64_t j = s2 + 4 * i;
+            if (j < Kcap) vr[i] = *reinterpret_cast<const uint4*>(vb + j * D + cc * 8);
+        }
+    }
+    const uint8_t al = (wid == 0 && lane < Kcap) ? allowed[row * allowed_stride + lane] : 0;
+    if (residual != nullptr)
+        rw = *reinterpret_cast<const uint4*>(residual + row * D + min(tid, nch - 1) * 8);
+    if (k_dev != nullptr) K = *k_dev < Kcap ? *k_dev : Kcap;
+    float qf[2][8];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        if (lane + 64 * c < nch) {
+            unpack8<T>(qw[c], qf[c]);
         } else {
 #pragma unroll
             for (int e = 0; e < 8; ++e) qf[c][e] = 0.0f;
         }
     }
-    const int c2 = tid & 127, s2 = tid >> 7;
-    if (c2 < nch) {
-#pragma unroll
-        for (int i = 0; i < KS; ++i) {
-            const int64_t j = s2 + 4 * i;
-            if (j < K) vr[i] = *reinterpret_cast<const uint4*>(vb + j * D + c2 * 8);
-        }
-    }
-    // the key mask (wave 0, lane = key) and the residual chunk, in the same round
-    const bool ok = wid == 0 && lane < K && allowed[row * allowed_stride + lane] != 0;
+    const bool ok = wid == 0 && lane < K && al != 0;
     float rr[8];
-    if (residual != nullptr && tid < nch) Vec8<T>::load(residual + row * D + tid * 8, rr);
+    if (residual != nullptr) unpack8<T>(rw, rr);
 #pragma unroll
     for (int i = 0; i < KW; ++i) {
         const int64_t j = wid + 8 * i;
