@@ -981,6 +981,20 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
     const int64_t s_begin = sb + wave * per;
     const int64_t s_end = s_begin + per < se ? s_begin + per : se;
 
+    // the gate and bias operands of this thread's outputs, requested with the
+    // main loop's loads (they do not depend on the product), at clamped indices
+    // so no load waits inside a condition; selected in the epilogue
+    constexpr int kIt = (MT * 256 + NW * 64 - 1) / (NW * 64);
+    float graw[kIt], braw[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+        const int o = tid + it * NW * 64;
+        const int64_t m = o >> 4, nidx = n0 + (o & 15);
+        const int64_t mc = m < a.M ? m : a.M - 1, nc = nidx < sg.n ? nidx : sg.n - 1;
+        graw[it] = sg.gate_p != nullptr ? ld((const bf16_t*)sg.gate_p + mc * sg.gate_ld + nc) : 0.0f;
+        braw[it] = sg.bias != nullptr ? sg.bias[nc] : 0.0f;
+    }
+
     f32x4 acc[MT];
 #pragma unroll
     for (int j = 0; j < MT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1022,20 +1036,14 @@ gemm_bf16_skinny_multi_kernel(LinArgs a) {
         for (int r = 0; r < 4; ++r) red[wave][j][r][lane] = acc[j][r];
     __syncthreads();
     uint16_t* out = (uint16_t*)sg.out;
-    // the gate and bias operands of all of this thread's outputs are loaded
-    // before its first store (an output could alias them, so later loads
-    // would otherwise wait for the earlier stores' round trip)
-    constexpr int kIt = (MT * 256 + NW * 64 - 1) / (NW * 64);
     float gmul[kIt], badd[kIt];
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
         const int o = tid + it * NW * 64;
         const int64_t m = o >> 4, nidx = n0 + (o & 15);
         const bool ok = o < MT * 256 && m < a.M && nidx < sg.n && a.partial == nullptr;
-        gmul[it] = (ok && sg.gate_p != nullptr)
-                       ? 1.0f + sg.gate_alpha * ld((const bf16_t*)sg.gate_p + m * sg.gate_ld + nidx)
-                       : 1.0f;
-        badd[it] = (ok && sg.bias != nullptr) ? sg.bias[nidx] : 0.0f;
+        gmul[it] = (ok && sg.gate_p != nullptr) ? 1.0f + sg.gate_alpha * graw[it] : 1.0f;
+        badd[it] = (ok && sg.bias != nullptr) ? braw[it] : 0.0f;
     }
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
