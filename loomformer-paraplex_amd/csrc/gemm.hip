@@ -863,34 +863,56 @@ ffn_decode_kernel(FfnArgs f) {
         __syncthreads();
       }
     };
+    // The epilogue's operands of this thread's elements (kIt of the block's
+    // 16 x MT*16 outputs) do not depend on the product: they are requested
+    // first, at clamped indices, and arrive during the depth read and the main
+    // loop (the carried record is read whether or not it is used, from R's
+    // first elements without one)
+    constexpr int kIt = (MT * 256 + NW * 64 - 1) / (NW * 64);
+    uint16_t e_cr[kIt][9], e_tr[kIt], e_x[kIt], e_g[kIt];
+    float e_ib[kIt], e_tw[kIt];
+    uint8_t e_valid[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+        const int o0 = (int)threadIdx.x + it * NW * 64;
+        const int o = o0 < MT * 256 ? o0 : MT * 256 - 1;
+        const int64_t mc = (o >> 4) < f.g.M ? (o >> 4) : f.g.M - 1;
+        const int64_t hc = n0 + (o & 15) < H ? n0 + (o & 15) : H - 1;
+        const int64_t e = mc * H + hc;
+        const uint16_t* src = f.mode == 1 ? f.prev + e * 9 : f.mode == 2 ? f.seed + e * 9 : f.R;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) e_cr[it][k] = src[k];
+        e_tr[it] = f.trace[e];
+        e_x[it] = f.R[e];
+        e_g[it] = f.G[e];
+        e_ib[it] = f.ib[hc];
+        e_tw[it] = f.tw[hc];
+        e_valid[it] = f.mode == 2 ? f.valid[mc] : 0;
+    }
     if constexpr (DE > 0) {
         depth();
         skinny_mainloop<MT, true, NW, UN>(f.g, n0, red, dsh);
     } else {
         skinny_mainloop<MT, true, NW, UN>(f.g, n0, red);
     }
-    for (int o = threadIdx.x; o < MT * 256; o += NW * 64) {
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+        const int o = (int)threadIdx.x + it * NW * 64;
         const int nn = o & 15, mi = o >> 4;
         const int64_t m = mi, h = n0 + nn;
-        if (m >= f.g.M || h >= H) continue;
+        if (o >= MT * 256 || m >= f.g.M || h >= H) continue;
         const int64_t e = m * H + h;
-        // every operand of the element is requested before the first store
-        // (the carried record could alias an output, so its loads would
-        // otherwise wait for the Paraplex half), one memory round trip
-        const bool carry_in = f.mode == 1 || (f.mode == 2 && f.valid[m] != 0);
+        const bool carry_in = f.mode == 1 || (f.mode == 2 && e_valid[it] != 0);
         float cp[9];
-        if (carry_in) {
-            const uint16_t* src = (f.mode == 1 ? f.prev : f.seed) + e * 9;
 #pragma unroll
-            for (int k = 0; k < 9; ++k) cp[k] = bf(src[k]);
-        }
-        const float tr = bf(f.trace[e]);
-        const float x = bf(f.R[e]);
-        const float gsrc = f.G == f.R ? x : bf(f.G[e]);
+        for (int k = 0; k < 9; ++k) cp[k] = bf(e_cr[it][k]);
+        const float tr = bf(e_tr[it]);
+        const float x = bf(e_x[it]);
+        const float gsrc = f.G == f.R ? x : bf(e_g[it]);
         const float beta = skinny_sum<MT, NW>(red, mi, nn);
         // Paraplex pointwise, one token: prev phase = the carried trace
-        const float s0 = phase_of(beta + f.ib[h]);
-        const float raw = fmaf(tr, f.tw[h], s0);
+        const float s0 = phase_of(beta + e_ib[it]);
+        const float raw = fmaf(tr, e_tw[it], s0);
         const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
         float amp, gate;
         softplus_gate<false>(gsrc, f.m, amp, gate);   // bf16 outputs (see softplus_gate)
