@@ -595,20 +595,33 @@ gemm_bf16_big_kernel(GemmArgs a) {
     };
     auto whole_tile = [&](auto gate_, auto res_) {
         constexpr bool GATE = decltype(gate_)::value, RES = decltype(res_)::value;
+        // every operand of the wave's outputs requested before the first store
+        // (an output may alias them as far as the compiler knows, so a load
+        // after a store would wait for it: one round trip per fragment)
+        float4 bv[FI];
+        uint2 gw[FI][FJ], rw[FI][FJ];
 #pragma unroll
         for (int i = 0; i < FI; ++i) {
             const int64_t nb = ncol + i * 16;
-            float bias4[4] = {0.f, 0.f, 0.f, 0.f};
-            if (a.bias != nullptr) {
-                const float4 bv = *reinterpret_cast<const float4*>(a.bias + nb);
-                bias4[0] = bv.x; bias4[1] = bv.y; bias4[2] = bv.z; bias4[3] = bv.w;
+            bv[i] = a.bias != nullptr ? *reinterpret_cast<const float4*>(a.bias + nb)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int j = 0; j < FJ; ++j) {
+                const int64_t e = (mrow + j * 16) * ldc + nb;
+                if constexpr (GATE) gw[i][j] = *reinterpret_cast<const uint2*>(gp + e);
+                if constexpr (RES) rw[i][j] = *reinterpret_cast<const uint2*>(rs + e);
             }
+        }
+#pragma unroll
+        for (int i = 0; i < FI; ++i) {
+            const int64_t nb = ncol + i * 16;
+            const float bias4[4] = {bv[i].x, bv[i].y, bv[i].z, bv[i].w};
 #pragma unroll
             for (int j = 0; j < FJ; ++j) {
                 const int64_t e = (mrow + j * 16) * ldc + nb;
                 float v[4], gv[4], rv[4];
-                if constexpr (GATE) bf4(*reinterpret_cast<const uint2*>(gp + e), gv);
-                if constexpr (RES) bf4(*reinterpret_cast<const uint2*>(rs + e), rv);
+                if constexpr (GATE) bf4(gw[i][j], gv);
+                if constexpr (RES) bf4(rw[i][j], rv);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     v[r] = acc[i][j][r];
