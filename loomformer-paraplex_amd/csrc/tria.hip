@@ -199,25 +199,54 @@ paraplex_tria_kernel(PxTriaArgs<T> a) {
         stage_in<T, REC>(tile, a.prev + e0 * 9, cnt * 9);
         __syncthreads();
     }
+    // every operand of the thread's elements requested before any store (an
+    // output may alias them as far as the compiler knows, so a later load
+    // would wait for the earlier stores), at clamped indices; the gate
+    // weights once
+    float wv[9];
+    if constexpr (GATE) {
+#pragma unroll
+        for (int k = 0; k < 9; ++k) wv[k] = ld(a.w + k);
+    }
+    float xr[EPT], bl[EPT], bp[EPT], tr[EPT], gs[EPT], bias_u[EPT], tw_u[EPT];
+    int t_u[EPT], h_u[EPT];
+    int64_t b_u[EPT];
+#pragma unroll
+    for (int u = 0; u < EPT; ++u) {
+        const int idx = (int)threadIdx.x + u * kTriaThreads;
+        const int64_t e = e0 + (idx < cnt ? idx : cnt - 1);
+        const int64_t bt = e / a.H;
+        const int h = (int)(e - bt * a.H);
+        const int t = (int)(bt % a.T_);
+        const int64_t b = bt / a.T_;
+        xr[u] = ld(a.r + e);
+        bl[u] = ld(a.beta + e);
+        bp[u] = ld(a.beta + (t > 0 ? e - a.H : e));   // the previous token's beta
+        tr[u] = ld(a.trace + b * a.H + h);              // the carried phase (t == 0)
+        gs[u] = SAME_GATE ? 0.0f : ld(a.gsrc + e);
+        bias_u[u] = a.bias[h];
+        tw_u[u] = a.trace_w[h];
+        t_u[u] = t;
+        h_u[u] = h;
+        b_u[u] = b;
+    }
     float pre[EPT][9];
 #pragma unroll
     for (int u = 0; u < EPT; ++u) {
         const int idx = (int)threadIdx.x + u * kTriaThreads;
         const int64_t e = e0 + idx;
         if (idx < cnt) {
-            const int64_t bt = e / a.H;
-            const int h = (int)(e - bt * a.H);
-            const int t = (int)(bt % a.T_);
-            const int64_t b = bt / a.T_;
+            const int h = h_u[u], t = t_u[u];
+            const int64_t b = b_u[u];
             // Paraplex chain (as paraplex_chunk_kernel / paraplex_forward_kernel)
-            const float x = ld(a.r + e);
-            const float bv = a.bias[h];
-            const float s0 = phase_of(ld(a.beta + e) + bv);
-            const float prevs = t == 0 ? ld(a.trace + b * a.H + h) : phase_of(ld(a.beta + e - a.H) + bv);
-            const float raw = fmaf(prevs, a.trace_w[h], s0);
+            const float x = xr[u];
+            const float bv = bias_u[u];
+            const float s0 = phase_of(bl[u] + bv);
+            const float prevs = t == 0 ? tr[u] : phase_of(bp[u] + bv);
+            const float raw = fmaf(prevs, tw_u[u], s0);
             const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
             float amp, gate;
-            softplus_gate<!std::is_same<T, bf16_t>::value>(SAME_GATE ? x : ld(a.gsrc + e), a.m, amp, gate);
+            softplus_gate<!std::is_same<T, bf16_t>::value>(SAME_GATE ? x : gs[u], a.m, amp, gate);
             const float act = fmaf(amp, sv, x) * gate;
             T ts, to;
             st(&ts, sv);
@@ -253,7 +282,7 @@ paraplex_tria_kernel(PxTriaArgs<T> a) {
             if constexpr (GATE) {
                 float pv = 0.0f;
 #pragma unroll
-                for (int k = 0; k < 9; ++k) pv = fmaf(pr[k], ld(a.w + k), pv);
+                for (int k = 0; k < 9; ++k) pv = fmaf(pr[k], wv[k], pv);
                 st(a.p_out + e, pv);
             }
         }
