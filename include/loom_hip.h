@@ -303,8 +303,9 @@ int loom_tria_depth_forward(int dtype, const void* r, const void* i, const void*
  *   p_real, gate_src (== p_real when paraplex_gate_proj is off), beta_linear:
  *   [B,T,H] dtype; bias, trace_w: [H] float; trace: [B,H] dtype (the base phase
  *   of the token before t = 0); act: [B,T,H] out; next_trace: [B,H] out (the
- *   base phase of t = T-1); carry_prev / seed / seed_valid / w / carry_out /
- *   p_out as loom_tria_depth_forward (carry_out required, no scale_out). */
+ *   base phase of t = T-1; it must not be the trace buffer when T > 1, which
+ *   is rejected); carry_prev / seed / seed_valid / w / carry_out / p_out as
+ *   loom_tria_depth_forward (carry_out required, no scale_out). */
 int loom_paraplex_tria_forward(int dtype, const void* p_real, const void* gate_src,
                                const void* beta_linear, const float* bias, const void* trace,
                                const float* trace_w, float m, const void* carry_prev,

@@ -53,11 +53,15 @@ depth_attn_generic_kernel(const T* __restrict__ q, const T* __restrict__ hk,
     const int64_t bt = row / QH;
     const T* kp = hk + bt * sbt + qh * HD;
     const T* vp = hv + bt * sbt + qh * HD;
-    const float qsc = scale * row_rms_scale(q + qh * HD, HD, rms.qt);
+    // fixed-RMS rows as fixed_rms forms them: scale and scaled elements rounded
+    // to T (with target 0 the scale is 1 and the rows are read as stored)
+    const float qsc = round_to<T>(row_rms_scale(q + qh * HD, HD, rms.qt));
     auto score = [&](int s) {
+        const float ksc = round_to<T>(row_rms_scale(kp + s * ss, HD, rms.kt));
         float dot = 0.0f;
-        for (int d = 0; d < HD; ++d) dot = fmaf(ld(q + qh * HD + d), ld(kp + s * ss + d), dot);
-        return dot * qsc * row_rms_scale(kp + s * ss, HD, rms.kt);
+        for (int d = 0; d < HD; ++d)
+            dot = fmaf(round_to<T>(ld(q + qh * HD + d) * qsc), round_to<T>(ld(kp + s * ss + d) * ksc), dot);
+        return dot * scale;
     };
     float m = -INFINITY, l = 0.0f;
     for (int s = 0; s < S; ++s) m = fmaxf(m, score(s));
@@ -70,7 +74,8 @@ depth_attn_generic_kernel(const T* __restrict__ q, const T* __restrict__ hk,
     for (int d = 0; d < HD; ++d) {
         float a = 0.0f;
         for (int s = 0; s < S; ++s)
-            a = fmaf(fexp(score(s) - m) * row_rms_scale(vp + s * ss, HD, rms.vt), ld(vp + s * ss + d), a);
+            a = fmaf(fexp(score(s) - m),
+                     round_to<T>(ld(vp + s * ss + d) * round_to<T>(row_rms_scale(vp + s * ss, HD, rms.vt))), a);
         st(d_out + row * HD + d, a * inv_l);
     }
     if (w_out != nullptr)

@@ -9,10 +9,11 @@
 // once, with nontemporal loads.
 //
 // With RMS (DepthAttn under depth_attn_qkv_rms, loomformer.py:3397-3407) the
-// query, key and value rows are read as fixed-RMS vectors: x * t / sqrt(mean(x^2)
-// + 1e-6) with targets qt, kt, vt.  The key scale multiplies the group-summed
-// score and the value scale the softmax weight of its row, so the stored
-// history stays as projected.
+// query, key and value rows are read as fixed-RMS vectors, as fixed_rms
+// (loomformer.py:840-844) forms them: the scale t / sqrt(mean(x^2) + 1e-6) with
+// target qt, kt or vt is computed in fp32 from the stored row, rounded to the
+// storage type, and each element x * scale rounded to the storage type again
+// (both roundings vanish in fp32).  The stored history stays as projected.
 #pragma once
 
 #include "loom_common.h"
@@ -29,6 +30,15 @@ __device__ __forceinline__ float rms_scale(const float (&x)[EPL], float target) 
     for (int k = 0; k < EPL; ++k) ss = fmaf(x[k], x[k], ss);
     ss = group_sum<16>(ss);
     return target * frsq(fmaf(ss, 1.0f / (float)(EPL * 16), 1e-6f));
+}
+
+// x <- x * scale in place, each term rounded to T as fixed_rms's bf16/fp16
+// product is (scale itself rounded to T first)
+template <typename T, int EPL>
+__device__ __forceinline__ void fixed_rms_row(float (&x)[EPL], float target) {
+    const float s = round_to<T>(rms_scale<EPL>(x, target));
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) x[k] = round_to<T>(x[k] * s);
 }
 
 struct DepthRms {
@@ -51,8 +61,8 @@ __device__ __forceinline__ void depth_row_core(const T* __restrict__ q, const T*
     const int d0 = j * EPL;
 
     RowIO<T, EPL>::load(q + qh * HD + d0, qv);
-    float qs = scale * kLog2e;                              // scores in log2 units
-    if constexpr (RMS) qs *= rms_scale<EPL>(qv, rms.qt);
+    if constexpr (RMS) fixed_rms_row<T, EPL>(qv, rms.qt);
+    const float qs = scale * kLog2e;                        // scores in log2 units
 #pragma unroll
     for (int k = 0; k < EPL; ++k) qv[k] *= qs;
 
@@ -83,16 +93,16 @@ __device__ __forceinline__ void depth_row_core(const T* __restrict__ q, const T*
         for (int c = 0; c < C; ++c) {
             float kv[EPL];
             kr[c].to_float(kv);
+            if constexpr (RMS) fixed_rms_row<T, EPL>(kv, rms.kt);
             float dot = 0.0f;
 #pragma unroll
             for (int k = 0; k < EPL; ++k) dot = fmaf(qv[k], kv[k], dot);
             sc[c] = dot;
-            if constexpr (RMS) sc[c] = group_sum<16>(sc[c]) * rms_scale<EPL>(kv, rms.kt);
         }
         float cmax = -INFINITY;
 #pragma unroll
         for (int c = 0; c < C; ++c) {
-            if constexpr (!RMS) sc[c] = group_sum<16>(sc[c]);
+            sc[c] = group_sum<16>(sc[c]);
             if (s0 + c < S) cmax = fmaxf(cmax, sc[c]);
         }
         const float m_new = fmaxf(m, cmax);
@@ -104,11 +114,11 @@ __device__ __forceinline__ void depth_row_core(const T* __restrict__ q, const T*
         for (int c = 0; c < C; ++c) {
             float vv[EPL];
             vr[c].to_float(vv);
+            if constexpr (RMS) fixed_rms_row<T, EPL>(vv, rms.vt);
             const float p = s0 + c < S ? __builtin_amdgcn_exp2f(sc[c] - m_new) : 0.0f;
             l += p;
-            const float pv = RMS ? p * rms_scale<EPL>(vv, rms.vt) : p;
 #pragma unroll
-            for (int k = 0; k < EPL; ++k) acc[k] = fmaf(pv, vv[k], acc[k]);
+            for (int k = 0; k < EPL; ++k) acc[k] = fmaf(p, vv[k], acc[k]);
         }
         m = m_new;
     }
@@ -137,11 +147,11 @@ __device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __re
         for (int s = 0; s < S; ++s) {
             float kv[EPL];
             RowIO<T, EPL>::load(kp + (int64_t)s * ss, kv);
+            if constexpr (RMS) fixed_rms_row<T, EPL>(kv, rms.kt);
             float dot = 0.0f;
 #pragma unroll
             for (int k = 0; k < EPL; ++k) dot = fmaf(qv[k], kv[k], dot);
             dot = group_sum<16>(dot);
-            if constexpr (RMS) dot *= rms_scale<EPL>(kv, rms.kt);
             if (j == 0) st(w_out + (int64_t)row * S + s, __builtin_amdgcn_exp2f(dot - m) * inv_l);
         }
     }

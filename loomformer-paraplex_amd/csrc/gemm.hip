@@ -854,9 +854,10 @@ ffn_decode_kernel(FfnArgs f) {
     // weight loads held across it the 16-wave block runs out of registers)
     auto depth = [&]() {
       if constexpr (DE > 0) {
-        const int tid = threadIdx.x;
-        if (tid < f.g.M * 16) {
-            const int b = tid >> 4, j = tid & 15;
+        // M*16 rows (b, j) over NW*64 threads: up to 512 rows, so a 4-wave
+        // block takes two rounds
+        for (int row = (int)threadIdx.x; row < f.g.M * 16; row += NW * 64) {
+            const int b = row >> 4, j = row & 15;
             float qv[DE], acc[DE], m, l;
             depth_row_core<bf16_t, DE, 4, DR, false>(
                 (const bf16_t*)f.dq, (const bf16_t*)f.dk, (const bf16_t*)f.dv, f.dsbt, f.dss,

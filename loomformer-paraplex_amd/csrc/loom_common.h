@@ -77,6 +77,17 @@ template <> struct Cvt<f16_t> {
 template <typename T> __device__ __forceinline__ float ld(const T* p) { return Cvt<T>::load(p); }
 template <typename T> __device__ __forceinline__ void st(T* p, float v) { Cvt<T>::store(p, v); }
 
+// x rounded to the storage type T and back (the identity for fp32)
+template <typename T> __device__ __forceinline__ float round_to(float x) {
+    if constexpr (std::is_same<T, float>::value) {
+        return x;
+    } else {
+        T t;
+        st(&t, x);
+        return ld(&t);
+    }
+}
+
 // Vector of 8 elements (16 B for 16-bit types, 32 B for fp32) loaded/stored
 // as whole 16-byte transactions.
 template <typename T> struct Vec8;

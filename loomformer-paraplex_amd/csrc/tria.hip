@@ -87,8 +87,11 @@ __device__ __forceinline__ void stage_out(T* dst, const float* lds, int n9) {
 }
 
 // MODE 0: init (pre = M); 1: step (pre = M @ carry_prev[e]);
-// 2: seeded init (pre = M @ seed[b,h] where t == 0 and valid[b], else M)
-template <typename T, int MODE, bool GATE, int AXIS>
+// 2: seeded init (pre = M @ seed[b,h] where t == 0 and valid[b], else M).
+// SCALE: rms(pre) is written to scale_out (the reference API's third output,
+// read only by its backward); the inference form leaves it out, 4 B per
+// element less, and profiles under its own name.
+template <typename T, int MODE, bool GATE, int AXIS, bool SCALE>
 __global__ void __launch_bounds__(kTriaThreads)
 tria_depth_kernel(const T* __restrict__ r, const T* __restrict__ i_, const T* __restrict__ o,
                   const T* __restrict__ prev, const T* __restrict__ seed,
@@ -135,7 +138,7 @@ tria_depth_kernel(const T* __restrict__ r, const T* __restrict__ i_, const T* __
         const float inv = 1.0f / sc;
 #pragma unroll
         for (int k = 0; k < 9; ++k) pre[k] *= inv;
-        if (scale_out != nullptr) scale_out[e] = sc;
+        if constexpr (SCALE) scale_out[e] = sc;
         if constexpr (GATE) {
             float p = 0.0f;
 #pragma unroll
@@ -797,10 +800,13 @@ static int tria_depth_dispatch(const void* r, const void* i, const void* o, cons
     const dim3 grid((unsigned)ceil_div(n, kTriaThreads)), blk(kTriaThreads);
     const int mode = prev ? 1 : (seed ? 2 : 0);
     const bool gate = w != nullptr;
-#define LOOM_TD(M, G, A)                                                                       \
-    hipLaunchKernelGGL((tria_depth_kernel<T, M, G, A>), grid, blk, 0, st, (const T*)r,        \
-                       (const T*)i, (const T*)o, (const T*)prev, (const T*)seed, valid,       \
+#define LOOM_TD_S(M, G, A, S)                                                               \
+    hipLaunchKernelGGL((tria_depth_kernel<T, M, G, A, S>), grid, blk, 0, st, (const T*)r,  \
+                       (const T*)i, (const T*)o, (const T*)prev, (const T*)seed, valid,    \
                        (const T*)w, (T*)carry_out, (T*)p_out, scale_out, n, T_, H, alpha)
+#define LOOM_TD(M, G, A)                                     \
+    if (scale_out != nullptr) { LOOM_TD_S(M, G, A, true); }  \
+    else { LOOM_TD_S(M, G, A, false); }
 #define LOOM_TD_AXIS(M, G)                        \
     switch (axis) {                               \
         case 0: LOOM_TD(M, G, 0); break;          \
@@ -812,6 +818,7 @@ static int tria_depth_dispatch(const void* r, const void* i, const void* o, cons
     else { if (gate) { LOOM_TD_AXIS(2, true) } else { LOOM_TD_AXIS(2, false) } }
 #undef LOOM_TD_AXIS
 #undef LOOM_TD
+#undef LOOM_TD_S
     return launch_status("loom_tria_depth_forward");
 }
 
@@ -971,6 +978,10 @@ extern "C" int loom_paraplex_tria_forward(int dtype, const void* p_real, const v
     LOOM_CHECK(!w || p_out, "paraplex_tria: gate weights need p_out");
     LOOM_CHECK(B >= 0 && T >= 0 && H >= 0 && T < (1LL << 31) && H < (1LL << 31),
                "paraplex_tria: bad shape");
+    // with T > 1 the block of a row's last token stores next_trace while the
+    // block of its first token may still be reading trace
+    LOOM_CHECK(T <= 1 || trace != (const void*)next_trace,
+               "paraplex_tria: trace and next_trace must be distinct buffers when T > 1");
     if (B * T * H == 0) return LOOM_OK;
     LOOM_DTYPE_SWITCH(dtype, px_tria_typed, p_real, gate_src, beta_linear, bias, trace, trace_w, m,
                       carry_prev, seed, seed_valid, w, act, next_trace, carry_out, p_out, B, T, H,

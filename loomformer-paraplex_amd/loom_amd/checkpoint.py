@@ -172,7 +172,7 @@ def _tokenizer_facts(tokenizer_json: bytes):
 def load_aio(path: str) -> LoadedModel:
     """A ``loom.aio`` v1 package (loomchat.load_aio, loomchat.py:278-316)."""
     if not str(path).lower().endswith(".aio"):
-        raise ValueError("loomchat accepts only .aio archives")
+        raise ValueError(f"{path}: not a .aio package (expected the .aio extension)")
     package = torch.load(path, map_location="cpu", weights_only=True)
     if not isinstance(package, Mapping) or package.get("format") != AIO_FORMAT:
         raise ValueError(f"not a {AIO_FORMAT} archive")

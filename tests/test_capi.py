@@ -88,3 +88,17 @@ def test_tria_chunked_fires_rejects_bad_boundary_lists():
         _lib.call("loom_tria_chunked_forward_fires", *args(arr(7, 7, 15, 23), 4))
     with pytest.raises(RuntimeError, match="outside"):
         _lib.call("loom_tria_chunked_forward_fires", *args(arr(7, 15, 23, 30), 4))
+
+
+def test_noalloc_rejects_records_beyond_the_scratch():
+    """The static-scratch decode step refuses shapes whose chunk records exceed
+    its array before any device call (null tensors: nothing is dereferenced)."""
+    from loom_amd import _lib
+    lib = _lib.load()
+    B, QH, KVH, HD, length = 4096, 8, 1, 128, 4096
+    need = lib.loom_gqa_workspace_bytes(B, length, QH, KVH, HD)
+    assert need > 4 << 20
+    with pytest.raises(RuntimeError, match="static scratch"):
+        _lib.call("loom_gqa_decode_step_noalloc", 1, None, None, None, KVH * length * HD, HD,
+                  length * HD, None, None, None, None, None, QH * HD, B, length, None, QH, KVH,
+                  HD, None)

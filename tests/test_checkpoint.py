@@ -109,7 +109,7 @@ def test_aio_rejects(tmp_path, mutate, msg):
 
 def test_aio_suffix_required(tmp_path):
     from loom_amd.checkpoint import load_aio
-    with pytest.raises(ValueError, match="only .aio"):
+    with pytest.raises(ValueError, match="not a .aio package"):
         load_aio(str(tmp_path / "x.pt"))
 
 

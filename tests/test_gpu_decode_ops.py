@@ -548,16 +548,19 @@ def test_ffn_decode(dtype, mode, gate, axis, gsrc):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("M,rms,slots", [(32, False, 4), (32, True, 11), (9, False, 20), (40, False, 7)])
-def test_ffn_decode_with_depth_read(dtype, M, rms, slots):
+@pytest.mark.parametrize("M,rms,slots,QH,HD", [
+    (32, False, 4, 8, 96), (32, True, 11, 8, 96), (9, False, 20, 8, 96), (40, False, 7, 8, 96),
+    # W_imag input 512 wide: 4-wave blocks, so 20 or 32 rows of 16 lanes take two rounds
+    (20, False, 5, 4, 64), (20, True, 7, 4, 64), (32, False, 13, 4, 64), (32, True, 9, 4, 64)])
+def test_ffn_decode_with_depth_read(dtype, M, rms, slots, QH, HD):
     """ffn_decode computing its own d_h: the depth read of history slot S-1
     (DepthAttn over slots 0..S-1, fixed-RMS q/k/v with rms) inside the launch
     (bf16, M <= 32) or as a launch before it (fp32, M > 32).  d_h against the
     oracle's depth read, the FFN outputs against the oracle fed with that d_h."""
     from loom_amd import _lib
     from oracle.model import fixed_rms
-    g = torch.Generator().manual_seed(M * 7 + slots + (3 if rms else 0))
-    QH, HD, H, L2 = 8, 96, 3072, 20
+    g = torch.Generator().manual_seed(M * 7 + slots + (3 if rms else 0) + HD)
+    H, L2 = 3072, 20
     N = QH * HD
     K = N + 4 * HD
     r = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(DEV, dtype)
@@ -587,11 +590,13 @@ def test_ffn_decode_with_depth_read(dtype, M, rms, slots):
         depth_sbt=L2 * 2 * N, depth_ss=2 * N, depth_S=slots, depth_rms=1 if rms else 0,
         **(dict(zip(("depth_qt", "depth_kt", "depth_vt"), tg)) if rms else {}))
     _lib.call("loom_ffn_decode", code(u), ctypes.byref(desc), S(u))
-    hk = host(hist)[:, :slots, :N].reshape(M, slots, QH, HD)
-    hv = host(hist)[:, :slots, N:].reshape(M, slots, QH, HD)
-    qd = host(dq)
+    # fixed_rms on the stored dtype, as the reference applies it
+    hk = hist.cpu()[:, :slots, :N].reshape(M, slots, QH, HD)
+    hv = hist.cpu()[:, :slots, N:].reshape(M, slots, QH, HD)
+    qd = dq.cpu()
     if rms:
         qd, hk, hv = fixed_rms(qd, tg[0]), fixed_rms(hk, tg[1]), fixed_rms(hv, tg[2])
+    qd, hk, hv = qd.float(), hk.float(), hv.float()
     want_d, _, _ = ref.depth_attn_softmax(qd, hk[:, None], hv[:, None])
     check(d, want_d[:, 0], dtype)
     be = ref.beta_space_grouped(host(u)[:, None], host(q)[:, None], host(kc)[:, None],

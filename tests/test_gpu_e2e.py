@@ -9,8 +9,9 @@ uniform ids (generator seeded 2), chunked prefill, then greedy decode.
   relative 1e-3, and the greedy ids that follow agree;
 * bf16: the benchmarked path (chunked prefill + 256 greedy steps replayed in
   chained 8-step graphs) tracks the fp32 engine teacher-forced on its tokens
-  within the 8% relative-logit bound the bf16 engine is held to, and the
-  chained graphs pick the same tokens as single-step replays.
+  within a 4% relative logit error at every position (measured on MI355X:
+  2.1-2.2% at every one of the 257 positions), and the chained graphs pick the
+  same tokens as single-step replays.
 """
 import pytest
 import torch
@@ -90,7 +91,7 @@ def fp32_runs(workload):
     return snap, snap_pre, (ids_tok, lg_tok), (ids_pre, lg_pre)
 
 
-def test_e2e_fp32_chunked_prefill_state_equals_token_steps(fp32_runs):
+def test_e2e_fp32_chunked_prefill_state_equals_token_steps(fp32_runs, measured):
     snap, snap_pre, _, _ = fp32_runs
     # 2048 tokens with W = 128: fires after positions 127, 255, ..., 2047
     assert snap["ca_len"] == snap_pre["ca_len"] == 16
@@ -99,7 +100,7 @@ def test_e2e_fp32_chunked_prefill_state_equals_token_steps(fp32_runs):
     assert int(snap["pending"].min()) == 1            # the last prompt token fired in every row
     for name in ("k_cache", "v_cache", "trace", "doc", "ca_k", "ca_v", "logits"):
         err = _rel(snap_pre[name], snap[name])
-        _log(f"fp32 chunked vs token-by-token {name}: relative error {err:.2e}")
+        measured(f"fp32 chunked vs token-by-token {name} relative error", err)
         assert err < 1e-3, (name, err)
 
 
@@ -122,15 +123,15 @@ def _first_divergence_is_a_tie(ids_a, lg_a, ids_b, lg_b):
     return True
 
 
-def test_e2e_fp32_greedy_ids_agree_after_both_prefills(fp32_runs):
+def test_e2e_fp32_greedy_ids_agree_after_both_prefills(fp32_runs, measured):
     _, _, (ids_tok, lg_tok), (ids_pre, lg_pre) = fp32_runs
     same = int((ids_tok == ids_pre).all(dim=1).sum())
-    _log(f"fp32 greedy ids: {same}/{B} rows identical over {NEW_FP32} steps")
+    measured(f"fp32 greedy rows identical over {NEW_FP32} steps (of {B})", same)
     assert _first_divergence_is_a_tie(ids_tok.cpu(), lg_tok.cpu(), ids_pre.cpu(), lg_pre.cpu())
     assert same >= B - 2
 
 
-def test_e2e_bf16_workload_tracks_fp32(workload):
+def test_e2e_bf16_workload_tracks_fp32(workload, measured):
     """The benchmarked bf16 path against the fp32 engine on the same
     (bf16-rounded) weights, teacher-forced on the bf16 engine's own tokens."""
     from loom_amd.engine import LoomDecoder
@@ -156,6 +157,8 @@ def test_e2e_bf16_workload_tracks_fp32(workload):
         out = e32.step(ids16[:, i], P + i)
         rel.append(_rel(lg16[:, i + 1], out.float()))
     worst = max(rel)
-    _log(f"bf16 vs fp32 relative logit error over {len(rel)} positions: "
-         f"max {worst:.4f} mean {sum(rel) / len(rel):.4f}")
-    assert worst < 0.08, worst
+    measured(f"bf16 vs fp32 relative logit error, max over {len(rel)} positions", worst)
+    measured(f"bf16 vs fp32 relative logit error, mean over {len(rel)} positions",
+             sum(rel) / len(rel))
+    measured("bf16 vs fp32 relative logit error at the first decode position", rel[0])
+    assert worst < 0.04, worst

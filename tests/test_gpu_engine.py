@@ -184,7 +184,7 @@ def test_nano_chunked_prefill_greedy_ids_bit_exact_fp32():
     assert torch.equal(ids.cpu(), torch.from_numpy(z["greedy"]))
 
 
-def test_bf16_chunked_prefill_tracks_token_steps():
+def test_bf16_chunked_prefill_tracks_token_steps(measured):
     """nano_chk-shaped layers in bf16 (head_dim 96, four heads per kv head: the
     MFMA prefill attention), a prompt of 3 chunks plus a ragged tail.  Against
     the fp32 token-by-token engine (same bf16-rounded weights), the state left
@@ -217,7 +217,8 @@ def test_bf16_chunked_prefill_tracks_token_steps():
                       ("doc", lambda e: e.doc), ("trace", lambda e: e.trace),
                       ("ca_k", lambda e: e.ca_k[:, :3]), ("logits", lambda e: e.logits)):
         e_tok, e_pre = rel(get(tok), get(ref)), rel(get(pre), get(ref))
-        print(f"{name}: bf16 token {e_tok:.4f}, bf16 chunked {e_pre:.4f}")
+        measured(f"{name}: bf16 token-by-token vs fp32 relative error", e_tok)
+        measured(f"{name}: bf16 chunked vs fp32 relative error", e_pre)
         assert e_pre < max(2 * e_tok, 0.02), (name, e_tok, e_pre)
     assert rel(pre.logits, ref.logits) < 0.08
 
