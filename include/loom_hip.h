@@ -612,6 +612,27 @@ int loom_decode_prologue_embed(int dtype, int64_t* ids, const int64_t* prompt, i
                                int64_t seq_len, const void* emb, void* h, int64_t N, int64_t V,
                                int64_t B, void* stream);
 
+/* One decode step's prologue in one launch, per batch row b: the token id is
+ * prompt[b, pos] while pos < prompt_len (prompt may be NULL), otherwise
+ * argmax_v logits[b, v] (first index on ties, as loom_argmax_rows; infer's
+ * greedy pick, loomformer.py:5306) or, with logits NULL, ids[b] as written by
+ * the caller; ids[b], tokens[b, pos], fire[b] and reset_now[b] as
+ * loom_decode_prologue; then row id of `table` [V, row_len] is copied to
+ * dst0[b * ld0 + 0 .. n0) and dst1[b * ld1 + 0 .. n1) (table row = [n0 | n1],
+ * n0 + n1 == row_len; n1 may be 0 with dst1 NULL).  The engine's table holds,
+ * per vocabulary id, the first depth-history slot DepthAttn.project(emb[id])
+ * and layer 0's qkv projection of emb[id] (Model.step, loomformer.py:3971-3973,
+ * :3300): the projections are linear in the gathered row, so gathering their
+ * rows equals projecting the gathered embedding.  No reference counterpart as
+ * one call.  logits: [B, V] dtype with V % 8 == 0, V <= 16384, 16-byte aligned. */
+int loom_decode_prologue_gather(int dtype, const void* logits, int64_t* ids, const int64_t* prompt,
+                                int64_t prompt_len, int64_t prompt_ld, int64_t* tokens,
+                                int64_t tokens_ld, const int64_t* pos_dev, const uint8_t* pending,
+                                uint8_t* fire, uint8_t* reset_now, int64_t carry_id, int64_t window,
+                                int64_t seq_len, const void* table, int64_t row_len, int64_t V,
+                                void* dst0, int64_t ld0, int64_t n0, void* dst1, int64_t ld1,
+                                int64_t n1, int64_t B, void* stream);
+
 /* Greedy pick ids[r] = argmax_v logits[r, v] (first index on ties, as
  * torch.argmax), the `argmax(logits)` of infer (loomformer.py:5306).
  * logits: [rows, V] dtype; ids: [rows] int64. */

@@ -1457,6 +1457,117 @@ decode_prologue_embed_kernel(int64_t* __restrict__ ids, const int64_t* __restric
     }
 }
 
+// The step's prologue in one launch (one block per batch row b): the position,
+// the row's logits and its pending flag are requested together; the token id
+// is prompt[b, pos] while pos < prompt_len, otherwise argmax(logits[b]) (first
+// index on ties, as argmax_rows_vec_kernel) or, without logits, ids[b] as the
+// caller wrote it; then ids, tokens, fire and reset_now as
+// decode_prologue_kernel, and row id of the projection table copied into up to
+// two destinations (table row = [seg 0 | seg 1]).  A gathered table row equals
+// the projection of the gathered embedding row (the projection is linear in
+// it), so the step's embedding lookup and its first projections cost one load
+// round trip after the id.
+template <typename T>
+struct PrologueGatherArgs {
+    const T* logits;          // [B, V] or null
+    int64_t* ids;
+    const int64_t* prompt;
+    int64_t prompt_len, prompt_ld;
+    int64_t* tokens;
+    int64_t tokens_ld;
+    const int64_t* pos_dev;
+    const uint8_t* pending;
+    uint8_t* fire;
+    uint8_t* reset_now;
+    int64_t carry_id, window, seq_len;
+    const T* table;           // [V, row_len]
+    int64_t row_len, V;
+    T* dst[2];
+    int64_t ld[2], n[2];
+    bool vec;                 // table rows and destinations take 16-byte pieces
+};
+
+template <typename T, int VPT>
+__global__ void __launch_bounds__(256)
+decode_prologue_gather_kernel(PrologueGatherArgs<T> a) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    __shared__ int64_t s_id;
+    const int64_t b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t pos = *a.pos_dev;
+    // the logits of the row, requested with the position (clamped, unconditional)
+    const int nvec = (int)(a.V / 8);
+    float vals[VPT > 0 ? VPT : 1][8];
+    if constexpr (VPT > 0) {
+        const T* x = a.logits + b * a.V;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int v = tid + 256 * i;
+            Vec8<T>::load(x + 8 * (v < nvec ? v : nvec - 1), vals[i]);
+        }
+    }
+    const uint8_t pend = a.pending[b];
+    const bool from_prompt = a.prompt != nullptr && pos < a.prompt_len;   // block-uniform
+    if (from_prompt) {
+        if (tid == 0) s_id = a.prompt[b * a.prompt_ld + pos];
+    } else if constexpr (VPT > 0) {
+        float best = -INFINITY;
+        int idx = (int)a.V;                  // NaN-free rows always replace this
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int v = tid + 256 * i;
+            if (v >= nvec) continue;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (vals[i][e] > best) { best = vals[i][e]; idx = 8 * v + e; }   // increasing index
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ob = __shfl_xor(best, off, 64);
+            const int oi = __shfl_xor(idx, off, 64);
+            if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+        }
+        const int w = tid >> 6;
+        if ((tid & 63) == 0) { bv[w] = best; bi[w] = idx; }
+        __syncthreads();
+        if (tid == 0) {
+            for (int k = 1; k < 4; ++k)
+                if (bv[k] > best || (bv[k] == best && bi[k] < idx)) { best = bv[k]; idx = bi[k]; }
+            s_id = idx < a.V ? idx : 0;
+        }
+    } else {
+        if (tid == 0) s_id = a.ids[b];
+    }
+    __syncthreads();
+    const int64_t id = s_id;
+    if (tid == 0) {
+        a.ids[b] = id;
+        if (a.tokens != nullptr) a.tokens[b * a.tokens_ld + pos] = id;
+        const bool hard = (pos + 1 < a.seq_len) && ((pos + 1) % a.window == 0);
+        a.fire[b] = (hard || (a.carry_id >= 0 && id == a.carry_id)) ? 1 : 0;
+        a.reset_now[b] = pend;
+    }
+    // out-of-vocabulary ids read a valid row (callers validate prompt ids)
+    const int64_t rid = id < 0 ? 0 : (id >= a.V ? a.V - 1 : id);
+    const T* src = a.table + rid * a.row_len;
+    if (a.vec) {
+        const uint4* s4 = reinterpret_cast<const uint4*>(src);
+        constexpr int E = 16 / (int)sizeof(T);
+        const int n0 = (int)(a.n[0] / E), n1 = (int)(a.n[1] / E);
+        for (int i = tid; i < n0 + n1; i += 256) {
+            const uint4 v = s4[i];
+            if (i < n0) reinterpret_cast<uint4*>(a.dst[0] + b * a.ld[0])[i] = v;
+            else reinterpret_cast<uint4*>(a.dst[1] + b * a.ld[1])[i - n0] = v;
+        }
+    } else {
+        for (int64_t i = tid; i < a.n[0] + a.n[1]; i += 256) {
+            if (i < a.n[0]) a.dst[0][b * a.ld[0] + i] = src[i];
+            else a.dst[1][b * a.ld[1] + i - a.n[0]] = src[i];
+        }
+    }
+}
+
 // Final-CA key append (tria.py:1576-1582) and end-of-step bookkeeping: if any
 // row fires, the staged keys/values of every row are stored at slot ca_len and
 // marked valid where that row fired; then pending = fire and pos += 1.
@@ -1637,6 +1748,68 @@ extern "C" int loom_decode_prologue_embed(int dtype, int64_t* ids, const int64_t
     LOOM_DTYPE_SWITCH(dtype, prologue_embed_dispatch, ids, prompt, prompt_len, prompt_ld, tokens,
                       tokens_ld, pos_dev, pending, fire, reset_now, carry_id, window, seq_len, emb,
                       h, N, V, B, (hipStream_t)stream)
+}
+
+template <typename T>
+static int prologue_gather_dispatch(const PrologueGatherArgs<T>& a0, int64_t B, hipStream_t st) {
+    PrologueGatherArgs<T> a = a0;
+    const int64_t V = a.V;
+    const bool vec = a.logits != nullptr && V % 8 == 0 && V <= 256 * 8 * 8 &&
+                     ((uintptr_t)a.logits & 15) == 0;
+    LOOM_CHECK(a.logits == nullptr || vec,
+               "decode_prologue_gather: logits need V %% 8 == 0, V <= 16384 and 16-byte alignment");
+    constexpr int E = 16 / (int)sizeof(T);
+    a.vec = ((uintptr_t)a.table & 15) == 0 && a.row_len % E == 0 && a.n[0] % E == 0 &&
+            (a.n[1] == 0 || (((uintptr_t)a.dst[1] & 15) == 0 && a.ld[1] % E == 0)) &&
+            ((uintptr_t)a.dst[0] & 15) == 0 && a.ld[0] % E == 0 && a.n[1] % E == 0;
+    const dim3 grid((unsigned)B), blk(256);
+    if (a.logits == nullptr) hipLaunchKernelGGL((decode_prologue_gather_kernel<T, 0>), grid, blk, 0, st, a);
+    else if (V <= 256 * 8) hipLaunchKernelGGL((decode_prologue_gather_kernel<T, 1>), grid, blk, 0, st, a);
+    else if (V <= 256 * 8 * 2) hipLaunchKernelGGL((decode_prologue_gather_kernel<T, 2>), grid, blk, 0, st, a);
+    else if (V <= 256 * 8 * 4) hipLaunchKernelGGL((decode_prologue_gather_kernel<T, 4>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((decode_prologue_gather_kernel<T, 8>), grid, blk, 0, st, a);
+    return launch_status("loom_decode_prologue_gather");
+}
+
+template <typename T>
+static int prologue_gather_typed(const void* logits, int64_t* ids, const int64_t* prompt,
+                                 int64_t prompt_len, int64_t prompt_ld, int64_t* tokens,
+                                 int64_t tokens_ld, const int64_t* pos_dev, const uint8_t* pending,
+                                 uint8_t* fire, uint8_t* reset_now, int64_t carry_id,
+                                 int64_t window, int64_t seq_len, const void* table,
+                                 int64_t row_len, int64_t V, void* dst0, int64_t ld0, int64_t n0,
+                                 void* dst1, int64_t ld1, int64_t n1, int64_t B, hipStream_t st) {
+    PrologueGatherArgs<T> a{};
+    a.logits = (const T*)logits; a.ids = ids; a.prompt = prompt; a.prompt_len = prompt_len;
+    a.prompt_ld = prompt_ld; a.tokens = tokens; a.tokens_ld = tokens_ld; a.pos_dev = pos_dev;
+    a.pending = pending; a.fire = fire; a.reset_now = reset_now; a.carry_id = carry_id;
+    a.window = window; a.seq_len = seq_len; a.table = (const T*)table; a.row_len = row_len;
+    a.V = V; a.dst[0] = (T*)dst0; a.ld[0] = ld0; a.n[0] = n0; a.dst[1] = (T*)dst1;
+    a.ld[1] = ld1; a.n[1] = n1;
+    return prologue_gather_dispatch<T>(a, B, st);
+}
+
+extern "C" int loom_decode_prologue_gather(int dtype, const void* logits, int64_t* ids,
+                                           const int64_t* prompt, int64_t prompt_len,
+                                           int64_t prompt_ld, int64_t* tokens, int64_t tokens_ld,
+                                           const int64_t* pos_dev, const uint8_t* pending,
+                                           uint8_t* fire, uint8_t* reset_now, int64_t carry_id,
+                                           int64_t window, int64_t seq_len, const void* table,
+                                           int64_t row_len, int64_t V, void* dst0, int64_t ld0,
+                                           int64_t n0, void* dst1, int64_t ld1, int64_t n1,
+                                           int64_t B, void* stream) {
+    clear_error();
+    LOOM_CHECK(ids && pos_dev && pending && fire && reset_now && table && dst0,
+               "decode_prologue_gather: null argument");
+    LOOM_CHECK(window >= 1 && B >= 0 && V >= 1 && n0 >= 1 && n1 >= 0 && n0 + n1 == row_len &&
+                   ld0 >= n0 && (n1 == 0 || (dst1 != nullptr && ld1 >= n1)),
+               "decode_prologue_gather: bad shape (n0 + n1 must equal row_len)");
+    LOOM_CHECK(!prompt || prompt_ld >= prompt_len, "decode_prologue_gather: prompt row stride < length");
+    if (B == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, prologue_gather_typed, logits, ids, prompt, prompt_len, prompt_ld,
+                      tokens, tokens_ld, pos_dev, pending, fire, reset_now, carry_id, window,
+                      seq_len, table, row_len, V, dst0, ld0, n0, dst1, ld1, n1, B,
+                      (hipStream_t)stream)
 }
 
 extern "C" int loom_argmax_rows(int dtype, const void* logits, int64_t rows, int64_t V,

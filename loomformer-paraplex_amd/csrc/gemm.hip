@@ -235,16 +235,20 @@ gemm_bf16_mfma_kernel(GemmArgs a) {
 // need: k-tiles t+1 .. t+NS-1 are in flight while t is computed.
 //
 // LDS layout of a stage: [k-half h][row][4 chunks of 8 k] (64 B rows), chunk c
-// of row r stored at position c ^ bg_swz(r) (r bits 1-2, flipped by bit 3), so
-// a 16-byte fragment read is conflict-free both 8 lanes at a time over 128 B
-// of banks and 16 lanes over 256 B.  One DMA instruction of a wave fills 16
+// of row r stored at position c ^ bg_swz(r) = c ^ 2*(bit 3 of r).  gfx950
+// serves a 16-byte ds_read one half-wave per cycle, 8 bytes per lane, from 128
+// banks of 4 bytes, so the 32 lanes of a half-wave are conflict-free when their
+// 16-byte pieces are distinct modulo 512 B.  A fragment read's half-wave takes
+// chunks {0, 1} or {2, 3} of 16 rows; rows r and r + 8 lie 512 B apart, and the
+// swizzle moves the second of them to the other two positions (measured: 4 LDS
+// cycles per read, no bank-conflict cycles).  One DMA instruction of a wave fills 16
 // rows of one k-half (lane l: row l/4, position l%4; the lane fetches the
 // chunk the swizzle puts there), so its 32 k lie in one gather sector and the
 // source and column offset are uniform (scalar) per instruction; per lane only
 // a 32-bit row offset per 16-row group is held, and the k advance is the
 // scalar soffset.  Requires K % (32 * KH * NS) == 0 (whole rounds of the
 // stages).
-__host__ __device__ constexpr int bg_swz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+__host__ __device__ constexpr int bg_swz(int r) { return ((r >> 3) & 1) << 1; }
 
 template <int BM_, int BN_, int WAVES_, int WGM_, int KH_, int WPE_, int NS_>
 struct BgCfg {

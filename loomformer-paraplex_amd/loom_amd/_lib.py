@@ -13,7 +13,7 @@ from ctypes import c_float, c_int, c_int64, c_void_p
 import torch
 
 # descriptor layouts and signatures below are those of loom_abi_version() == 5
-ABI_VERSION = 5
+ABI_VERSION = 6
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libloom_hip.so")
 
 _P = c_void_p
@@ -92,6 +92,9 @@ SIGNATURES = {
                              c_int64, c_int64, c_int64, _P],
     "loom_decode_prologue_embed": [c_int, _P, _P, c_int64, c_int64, _P, c_int64, _P, _P, _P, _P,
                                    c_int64, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, _P],
+    "loom_decode_prologue_gather": [c_int, _P, _P, _P, c_int64, c_int64, _P, c_int64, _P, _P, _P,
+                                    _P, c_int64, c_int64, c_int64, _P, c_int64, c_int64, _P,
+                                    c_int64, c_int64, _P, c_int64, c_int64, c_int64, _P],
     "loom_decode_epilogue": [c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64,
                              _P],
     "loom_argmax_rows": [c_int, _P, c_int64, c_int64, _P, _P],

@@ -42,6 +42,7 @@ class LoomDecoder:
     """Model.step / infer for a batch of sequences on the gfx950 kernels."""
 
     STEPS_PER_GRAPH = 8      # decode steps chained in one replayed graph
+    PROJ_TABLE_MAX_BYTES = 1 << 30   # largest per-vocabulary projection table built
 
     def __init__(self, cfg: ModelConfig, state: Dict[str, torch.Tensor], batch: int,
                  dtype: torch.dtype = torch.bfloat16, device="cuda", max_len: Optional[int] = None,
@@ -109,6 +110,19 @@ class LoomDecoder:
         self.proj_w, self.proj_b = mat("tria_agg.reader.proj.weight"), f32("tria_agg.reader.proj.bias")
         self.up_w, self.up_b = mat("tria_agg.up.weight"), f32("tria_agg.up.bias")
         self.wqk, self.wv = mat("tria_final_ca.w_qk.weight"), mat("tria_final_ca.w_v.weight")
+        # per vocabulary id: [DepthAttn.project(emb[id]) | layer 0's qkv(emb[id])], the
+        # step's first depth-history slot and first qkv row (loomformer.py:3971-3973),
+        # gathered by the step's prologue instead of projected each step (both
+        # projections are linear in the embedding row); built when it is small
+        qkv_w = (c.QH + 2 * c.KVH) * c.HD
+        self.ptab_row = 2 * c.N + qkv_w
+        elt = torch.tensor([], dtype=dt).element_size()
+        self.ptab = None
+        if c.V * self.ptab_row * elt <= self.PROJ_TABLE_MAX_BYTES and c.V % 8 == 0 and c.V <= 16384:
+            self.ptab = torch.empty(c.V, self.ptab_row, dtype=dt, device=dev)
+            self._linear(self.emb, self.kvw, self.ptab, c.V, 2 * c.N, c.N, ldc=self.ptab_row)
+            self._linear(self.emb, self.blocks[0]["qkv"], self.ptab[:, 2 * c.N:], c.V, qkv_w, c.N,
+                         ldc=self.ptab_row)
         self.gamma = c.gamma_max * math.tanh(float(state["tria_final_ca.raw_gamma"]))
         cos, sin = rope_tables(c, self.max_len)
         self.cos, self.sin = cos.to(dev), sin.to(dev)
@@ -260,23 +274,40 @@ class LoomDecoder:
 
     # ------------------------------------------------------------------ the step
 
-    def _launch_step(self, first: bool, prompt_len: int) -> None:
+    def _launch_step(self, first: bool, prompt_len: int, argmax: bool = False) -> None:
         """Enqueue one Model.step for position *pos_dev (device-resident).  `first`
-        selects the position-0 variant (no seed, no previous temporal state)."""
+        selects the position-0 variant (no seed, no previous temporal state);
+        `argmax`: the step's token is the greedy pick of the current logits
+        (infer's argmax, loomformer.py:5306) once the prompt is consumed, else the
+        id the caller wrote into self.ids."""
         c, B, N, H, L = self.cfg, self.B, self.cfg.N, self.cfg.H, self.cfg.L
         st = self._stream()
         carry_id = -1 if self.carry_token_id is None else int(self.carry_token_id)
-        # token ids, fire / reset flags and the embedding row of this step, one launch
-        self._call("loom_decode_prologue_embed", self.code, _P(self.ids),
-                   _P(self.prompt_buf) if prompt_len > 0 else None, prompt_len, self.max_len,
-                   _P(self.tokens), self.max_len, _P(self.pos_dev), _P(self.pending), _P(self.fire),
-                   _P(self.reset_now), carry_id, c.window, c.seq_len, _P(self.emb), _P(self.h), N,
-                   c.V, B, st)
         hist = self.hist
-        # depth history slot 0 = DepthAttn.project(h) (loomformer.py:3973), with
-        # layer 0's qkv projection of the same h in the same launch
-        self._multi("first", self.h, [dict(w=self.kvw, out=hist[:, 0]),
-                                      dict(w=self.blocks[0]["qkv"], out=self.qkv)])
+        if self.ptab is not None:
+            # token ids (greedy pick or prompt), fire / reset flags, and the rows of
+            # depth history slot 0 (DepthAttn.project(emb[id]), loomformer.py:3973) and
+            # layer 0's qkv gathered from the projection table, one launch
+            self._call("loom_decode_prologue_gather", self.code,
+                       _P(self.logits) if argmax else None, _P(self.ids),
+                       _P(self.prompt_buf) if prompt_len > 0 else None, prompt_len, self.max_len,
+                       _P(self.tokens), self.max_len, _P(self.pos_dev), _P(self.pending),
+                       _P(self.fire), _P(self.reset_now), carry_id, c.window, c.seq_len,
+                       _P(self.ptab), self.ptab_row, c.V, _P(hist), hist.stride(0), 2 * N,
+                       _P(self.qkv), self.qkv.stride(0), self.ptab_row - 2 * N, B, st)
+        else:
+            if argmax:
+                self._argmax()
+            # token ids, fire / reset flags and the embedding row of this step, one launch
+            self._call("loom_decode_prologue_embed", self.code, _P(self.ids),
+                       _P(self.prompt_buf) if prompt_len > 0 else None, prompt_len, self.max_len,
+                       _P(self.tokens), self.max_len, _P(self.pos_dev), _P(self.pending),
+                       _P(self.fire), _P(self.reset_now), carry_id, c.window, c.seq_len,
+                       _P(self.emb), _P(self.h), N, c.V, B, st)
+            # depth history slot 0 = DepthAttn.project(h) (loomformer.py:3973), with
+            # layer 0's qkv projection of the same h in the same launch
+            self._multi("first", self.h, [dict(w=self.kvw, out=hist[:, 0]),
+                                          dict(w=self.blocks[0]["qkv"], out=self.qkv)])
         sub = 0
         cache_sb = c.KVH * self.max_len * c.HD
         cache_st = c.HD
@@ -434,8 +465,7 @@ class LoomDecoder:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 for _ in range(steps):
-                    self._argmax()
-                    self._launch_step(first=False, prompt_len=prompt_len)
+                    self._launch_step(first=False, prompt_len=prompt_len, argmax=True)
             self._graphs[key] = g
         return g
 
@@ -471,8 +501,7 @@ class LoomDecoder:
             if graph is not None:
                 graph.replay()
             else:
-                self._argmax()
-                self._launch_step(first=False, prompt_len=P)
+                self._launch_step(first=False, prompt_len=P, argmax=True)
             if return_logits:
                 logits_all.append(self.logits.float().clone())
         self.pos = total

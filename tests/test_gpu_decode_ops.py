@@ -714,3 +714,56 @@ def test_decode_prologue_embed(dtype):
         assert torch.equal(fire.cpu().bool(), torch.tensor(hard) | (want_ids == 7))
         assert torch.equal(reset.cpu(), pending.cpu())
         assert torch.equal(h.cpu(), emb.cpu()[want_ids])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("V", [64, 4096, 5000])
+def test_decode_prologue_gather(dtype, V):
+    """loom_decode_prologue_gather: the id from the prompt while pos < prompt_len,
+    else the greedy pick of the logits (the same ids as loom_argmax_rows, ties
+    included) or, without logits, the caller's ids; fire / reset_now as the
+    prologue; the id's table row split into the two destinations exactly."""
+    B, n1, W = 6, 40, 4
+    n0 = 24 if V % 8 == 0 else 20       # 20: the element-wise copy (rows not 16-byte pieces)
+    g = torch.Generator().manual_seed(V)
+    table = torch.randn(V, n0 + n1, generator=g).to(DEV, dtype)
+    logits = torch.randn(B, V, generator=g)
+    logits[1, V // 3] = logits[1, V - 2] = 50.0          # a tie: the first index wins
+    logits = logits.to(DEV, dtype)
+    prompt = torch.randint(0, V, (B, 6), generator=g)
+    prompt[2, 3] = 7                                      # the carry id at pos 3 in row 2
+    prompt_d = prompt.to(DEV)
+    pending = torch.tensor([1, 0, 1, 0, 0, 1], dtype=torch.uint8, device=DEV)
+    want_argmax = torch.empty(B, dtype=torch.int64, device=DEV)
+    L().call("loom_argmax_rows", code(logits), P(logits), B, V, P(want_argmax), S(logits))
+    assert int(want_argmax[1]) == V // 3
+    for pos, mode in ((3, "prompt"), (7, "argmax"), (8, "ids")):
+        ids = torch.randint(0, V, (B,), generator=g).to(DEV)
+        ids0 = ids.clone()
+        tokens = torch.zeros(B, 10, dtype=torch.int64, device=DEV)
+        fire = torch.empty(B, dtype=torch.uint8, device=DEV)
+        reset = torch.empty(B, dtype=torch.uint8, device=DEV)
+        d0 = torch.full((B, 2 * n0), float("nan"), device=DEV, dtype=dtype)   # row stride 2*n0
+        d1 = torch.full((B, n1), float("nan"), device=DEV, dtype=dtype)
+        pos_d = torch.tensor([pos], dtype=torch.int64, device=DEV)
+        if V % 8 != 0 and mode == "argmax":
+            with pytest.raises(RuntimeError, match="logits need"):
+                L().call("loom_decode_prologue_gather", code(table), P(logits), P(ids), P(prompt_d),
+                         6, 6, P(tokens), 10, P(pos_d), P(pending), P(fire), P(reset), 7, W, 100,
+                         P(table), n0 + n1, V, P(d0), 2 * n0, n0, P(d1), n1, n1, B, S(table))
+            continue
+        L().call("loom_decode_prologue_gather", code(table), P(logits) if mode == "argmax" else None,
+                 P(ids), P(prompt_d) if mode != "ids" else None, 6, 6, P(tokens), 10, P(pos_d),
+                 P(pending), P(fire), P(reset), 7, W, 100, P(table), n0 + n1, V, P(d0), 2 * n0,
+                 n0, P(d1), n1, n1, B, S(table))
+        want = (prompt[:, pos] if mode == "prompt" else want_argmax.cpu() if mode == "argmax"
+                else ids0.cpu())
+        assert torch.equal(ids.cpu(), want)
+        assert torch.equal(tokens[:, pos].cpu(), want)
+        hard = (pos + 1) % W == 0
+        assert torch.equal(fire.cpu().bool(), torch.tensor(hard) | (want == 7))
+        assert torch.equal(reset.cpu(), pending.cpu())
+        rows = table.cpu()[want]
+        assert torch.equal(d0.cpu()[:, :n0], rows[:, :n0])
+        assert torch.isnan(d0.float().cpu()[:, n0:]).all()      # past n0 untouched
+        assert torch.equal(d1.cpu(), rows[:, n0:])
