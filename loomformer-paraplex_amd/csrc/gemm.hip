@@ -264,6 +264,13 @@ struct BgCfg {
     static_assert(NS >= 3 && NS <= 6 && (NS - 1) * DMA < 64 && LDS <= 160 * 1024, "big GEMM stages");
 };
 using BgConf = BgCfg<256, 128, 8, 4, 2, 2, 3>;
+// 128 x 128 tiles (four waves of 64 x 64, one 32-wide k-half per stage, four
+// stages, two blocks per CU) and 128 x 256 tiles (eight waves of 64 x 64):
+// the smaller tile fills the CUs when the 256 x 128 tiles leave many idle or
+// end in a partial round, the wider one serves many-row products with N a
+// multiple of 256
+using BgSmall = BgCfg<128, 128, 4, 2, 1, 2, 4>;
+using BgWide = BgCfg<128, 256, 8, 2, 1, 2, 4>;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 template <int N>
@@ -1276,6 +1283,50 @@ static void launch_skinny(const GemmArgs& a, dim3 grid, hipStream_t st) {
     }
 }
 
+// Tile configuration of a big bf16 product, from the 256 x 128 tile count t
+// against the CU count c:
+//   128 x 256 when N % 256 == 0 and t >= 3c/4 (8192 x 768 x 3072: 49.6
+//     against 53.2 us; 8192 x 3072 x 768: 60.9 against 63.4 us; the chunked
+//     prefill's 4096 x 1536 history projections);
+//   256 x 128 otherwise, and 128 x 128 only where 256 x 128 cannot run (fewer
+//     than 256 rows, K not a whole round of its stages).  Alone, 128 x 128 is
+//     faster whenever 256 x 128 leaves CUs idle (4096 x 768 x 3072: 32.5
+//     against 47.0 us), but inside the chunked prefill, beside the other
+//     streams' kernels, choosing it there measured 74.4-75.2 ms against
+//     73.5-74.0 ms (same box, alternating runs).
+// K must fill whole rounds of the configuration's stages; gather tiles must
+// not straddle a q-head group (Hq % BG_N == 0).
+enum BigTile { kBigNone, kBigStd, kBigSmall, kBigWide };
+template <class C>
+static bool big_fits(int64_t M, int64_t K, bool gather, int64_t Hq) {
+    return M >= C::BG_M && K % (C::NS * C::BK) == 0 && (!gather || Hq % C::BG_N == 0);
+}
+static BigTile big_tile(int64_t M, int64_t N, int64_t K, bool gather, int64_t Hq) {
+    const bool std_ok = big_fits<BgConf>(M, K, gather, Hq);
+    const bool small_ok = big_fits<BgSmall>(M, K, gather, Hq);
+    const bool wide_ok = !gather && N % BgWide::BG_N == 0 && big_fits<BgWide>(M, K, gather, Hq);
+    if (!std_ok) return small_ok ? kBigSmall : (wide_ok ? kBigWide : kBigNone);
+    const int64_t c = device_cus();
+    const int64_t t = ceil_div(M, BgConf::BG_M) * ceil_div(N, BgConf::BG_N);
+    if (wide_ok && 4 * t >= 3 * c) return kBigWide;
+    return kBigStd;
+}
+template <bool GATHER, class C>
+static void launch_big_cfg(const GemmArgs& a, int64_t nsplit, hipStream_t st) {
+    const dim3 grid((unsigned)(ceil_div(a.N, C::BG_N) * ceil_div(a.M, C::BG_M) * nsplit));
+    hipLaunchKernelGGL((gemm_bf16_big_kernel<GATHER, C>), grid, dim3(64 * C::WAVES), 0, st, a);
+}
+template <bool GATHER>
+static void launch_big(const GemmArgs& a, BigTile tile, int64_t nsplit, hipStream_t st) {
+    if (tile == kBigSmall) launch_big_cfg<GATHER, BgSmall>(a, nsplit, st);
+    else if constexpr (!GATHER) {
+        if (tile == kBigWide) launch_big_cfg<GATHER, BgWide>(a, nsplit, st);
+        else launch_big_cfg<GATHER, BgConf>(a, nsplit, st);
+    } else {
+        launch_big_cfg<GATHER, BgConf>(a, nsplit, st);
+    }
+}
+
 template <typename T, bool GATHER>
 static int run_gemm(const GemmArgs& a, hipStream_t st, const char* what) {
     if (a.M == 0 || a.N == 0) return LOOM_OK;
@@ -1303,12 +1354,10 @@ static int run_gemm(const GemmArgs& a, hipStream_t st, const char* what) {
         ok = ok && a.ldw % 8 == 0 && ((uintptr_t)a.W & 15) == 0;
         if (GATHER)
             for (int s = 0; s < 5; ++s) ok = ok && ((uintptr_t)a.src[s] & 15) == 0;
-        // many rows and whole 64-wide k-tiles: the 256 x 128 tile with DMA stages
-        using C = BgConf;
-        if (ok && a.M >= C::BG_M && a.K % (C::NS * C::BK) == 0 && (!GATHER || a.Hq % C::BG_N == 0)) {
-            dim3 grid((unsigned)(ceil_div(a.N, C::BG_N) * ceil_div(a.M, C::BG_M)));
-            hipLaunchKernelGGL((gemm_bf16_big_kernel<GATHER, BgConf>), grid, dim3(64 * BgConf::WAVES), 0,
-                               st, a);
+        // many rows and whole rounds of k-stages: the DMA-staged tiles
+        const BigTile tile = ok ? big_tile(a.M, a.N, a.K, GATHER, a.Hq) : kBigNone;
+        if (tile != kBigNone) {
+            launch_big<GATHER>(a, tile, 1, st);
             return launch_status(what);
         }
         if (ok) {
@@ -1653,18 +1702,28 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
     LOOM_CHECK(out_frag == nullptr || (fused && g.n % 32 == 0 && ((uintptr_t)out_frag & 15) == 0),
                "linear_ln: out_frag needs the bf16 split-K form (m <= 64, aligned) and n %% 32 == 0");
     if (!fused) {
-        // many rows: the 256 x 128 MFMA kernel over both inputs, split-K sums
-        // in the workspace, reduced with the bias in the LayerNorm kernel.
-        // Splits: whole rounds of the stages each; fewest block rounds times
-        // (k per split + ~320, the measured fixed cost of a block in k units).
-        using C = BgConf;
+        // many rows: the DMA-staged MFMA tiles over both inputs (configuration as
+        // big_tile picks it), split-K sums in the workspace, reduced with the bias
+        // in the LayerNorm kernel.  Splits: whole rounds of the stages each;
+        // fewest block rounds times (k per split + ~320, the measured fixed cost
+        // of a block in k units).
         const int64_t K = d->k + d->k2;
-        const int64_t tiles = ceil_div(d->m, C::BG_M) * ceil_div(g.n, C::BG_N);
+        const BigTile tile = aligned ? big_tile(d->m, g.n, K, false, 0) : kBigNone;
+        int64_t bm = BgConf::BG_M, bn = BgConf::BG_N, stage_k = BgConf::NS * BgConf::BK,
+                half_k = BgConf::BK, per_cu = 1;
+        if (tile == kBigSmall) {
+            bm = BgSmall::BG_M; bn = BgSmall::BG_N; stage_k = BgSmall::NS * BgSmall::BK;
+            half_k = BgSmall::BK; per_cu = 2;
+        } else if (tile == kBigWide) {
+            bm = BgWide::BG_M; bn = BgWide::BG_N; stage_k = BgWide::NS * BgWide::BK;
+            half_k = BgWide::BK;
+        }
+        const int64_t tiles = ceil_div(d->m, bm) * ceil_div(g.n, bn);
         int64_t ns = 0, best = 0;
-        if (aligned && d->m >= C::BG_M && d->k % C::BK == 0)
+        if (tile != kBigNone && d->k % half_k == 0)
             for (int64_t q = 1; q <= kMaxSplit; ++q) {
-                if (K % (q * C::NS * C::BK) != 0) continue;
-                const int64_t cost = ceil_div(tiles * q, (int64_t)device_cus()) * (K / q + 320);
+                if (K % (q * stage_k) != 0) continue;
+                const int64_t cost = ceil_div(tiles * q, per_cu * (int64_t)device_cus()) * (K / q + 320);
                 if (ns == 0 || cost < best) { ns = q; best = cost; }
             }
         if (ns > 0) {
@@ -1674,8 +1733,7 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
             a.K1 = d->k;
             a.M = d->m; a.N = g.n; a.K = K;
             a.partial = workspace; a.ldp = g.n; a.nsplit = (int)ns;
-            hipLaunchKernelGGL((gemm_bf16_big_kernel<false, C>), dim3((unsigned)(tiles * ns)),
-                               dim3(64 * C::WAVES), 0, st, a);
+            launch_big<false>(a, tile, ns, st);
             const int rc = launch_status("loom_linear_ln");
             if (rc != LOOM_OK) return rc;
             return launch_splitk_ln(ns, d, workspace, gamma, beta, eps, out, ldo, nullptr, st);

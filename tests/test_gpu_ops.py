@@ -194,8 +194,12 @@ def test_golden_phase_and_pvpowlu_vs_reference():
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("M,N,K", [(1, 16, 8), (37, 100, 72), (32, 3072, 768), (130, 768, 3072),
                                    (256, 256, 1152), (5, 4096, 768), (3, 768, 3072), (8, 1000, 772),
-                                   # the large-M MFMA tiles 256x128, 128x128 and 128x64, ragged
-                                   (8229, 3000, 768), (6000, 1536, 1152), (4100, 770, 3072)])
+                                   # the large-M MFMA tiles: 256 x 128 (ragged), 128 x 256
+                                   # (N % 256 == 0, ragged rows) and 128 x 128 (fewer than
+                                   # 256 rows, or K not a multiple of 192)
+                                   (8229, 3000, 768), (6000, 1536, 1152), (4100, 770, 3072),
+                                   (4096, 1152, 768), (8192, 768, 3072), (4000, 1536, 768),
+                                   (200, 384, 1024), (1000, 640, 512)])
 def test_linear(dtype, M, N, K):
     from loom_amd import ops
     g = gen(M * 7 + N + K)
@@ -216,7 +220,7 @@ def test_linear(dtype, M, N, K):
                                                  (8, 96, 384, 300, "head"), (4, 8, 32, 6, "open"),
                                                  (8, 96, 384, 20, "open"), (8, 96, 384, 8200, "head"),
                                                  (8, 96, 384, 600, "open"), (8, 96, 384, 1, "head"),
-                                                 (4, 8, 32, 3, "open")])
+                                                 (4, 8, 32, 3, "open"), (8, 96, 384, 8192, "head")])
 def test_beta_forward(dtype, QH, HD, Hq, M, sectors):
     from loom_amd import ops
     N, H = QH * HD, QH * Hq
