@@ -221,6 +221,14 @@ typedef struct {
     int32_t depth_S;
     int32_t depth_rms;         /* nonzero: fixed-RMS q/k/v with the targets below */
     float depth_qt, depth_kt, depth_vt;
+    /* optional (plain read, depth_S >= 2, the in-launch form): the read over
+       slots 0..depth_S-2 already done, as normalised fp32 rows depth_part_d
+       [M, n_q_heads, head_dim] (8-byte aligned) and their log-sum-exp
+       depth_part_lse [M, n_q_heads] (natural units), e.g. from
+       loom_gqa_decode_step_depth2; the launch then reads slot depth_S-1 only
+       and combines the two parts in one softmax.  NULL: every slot is read. */
+    const float* depth_part_d;
+    const float* depth_part_lse;
 } loom_ffn_decode_desc;
 
 /* beta = beta_space(u, q, kctx, c, d); (act, s, trace) = paraplex(R, beta);
@@ -517,6 +525,26 @@ int loom_gqa_decode_step_depth(int dtype, const void* qkv, void* k_cache, void* 
                                int64_t KVH, int64_t HD, const void* depth_q, const void* hist_k,
                                const void* hist_v, int64_t hist_stride_bt, int64_t hist_stride_s,
                                int64_t S, void* depth_out, void* stream);
+
+/* loom_gqa_decode_step_depth with a second depth query over the same history
+ * slots 0..S-1 (one load of each slot row for both): depth_q's read is written
+ * to depth_out as there, depth_q2's as the normalised fp32 rows part_d
+ * [B, QH, HD] and their log-sum-exp part_lse [B, QH] (natural units) -- the
+ * part of the next sublayer's read (DepthAttn.forward with that sublayer's
+ * query over slots 0..S, loomformer.py:3404-3429, :4004-4006) that these slots
+ * contribute, which loom_ffn_decode folds with slot S.  bf16 only, head_dim
+ * 32/64/96/128, QH/KVH in {1, 2, 4, 8}, depth rows 8-byte aligned (other
+ * cases are rejected).  No counterpart in the reference as one call. */
+int loom_gqa_decode_step_depth2(int dtype, const void* qkv, void* k_cache, void* v_cache,
+                                int64_t cache_stride_b, int64_t cache_stride_t,
+                                int64_t cache_stride_h, const float* cos_table,
+                                const float* sin_table, void* q_out, void* c_out, void* kctx_out,
+                                int64_t out_stride_b, float* workspace, int64_t workspace_bytes,
+                                int64_t B, int64_t len, const int64_t* pos_dev, int64_t QH,
+                                int64_t KVH, int64_t HD, const void* depth_q, const void* depth_q2,
+                                const void* hist_k, const void* hist_v, int64_t hist_stride_bt,
+                                int64_t hist_stride_s, int64_t S, void* depth_out, float* part_d,
+                                float* part_lse, void* stream);
 
 /* Size of the static per-device scratch of loom_gqa_decode_step_noalloc. */
 #define LOOM_GQA_NOALLOC_SCRATCH_BYTES (4 << 20)

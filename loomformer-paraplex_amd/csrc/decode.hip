@@ -115,6 +115,12 @@ struct GqaArgs {
     T* dout;               // [B, QH, HD]
     int dS;
     float dscale;
+    // optional second query over the same slots (the next sublayer's read):
+    // its normalised read in fp32 and its log-sum-exp, for a later fold of
+    // the one slot that read adds
+    const T* dq2;          // [QH, HD] or null
+    float* dpd;            // [B, QH, HD]
+    float* dpl;            // [B, QH]
 };
 
 // element d of head h of a qkv row, roped for position pos (x*cos + rot(x)*sin)
@@ -499,10 +505,15 @@ gqa_mfma_kernel(GqaArgs<bf16_t> a) {
     const int lr = lane & 15, lq = lane >> 4;
     if (chunk == nchunks) {
         // the depth read of this step: rows (b, heads kvh*G ..), 16 lanes each
-        if (tid < 16 * G)
-            depth_row<bf16_t, HD / 16>(a.dq, a.dk, a.dv, a.dsbt, a.dss, a.dout, nullptr, nullptr,
-                                       (int)b * a.QH + kvh * G + (tid >> 4), tid & 15, a.dS, a.QH,
-                                       a.dscale);
+        if (tid < 16 * G) {
+            const int row = (int)b * a.QH + kvh * G + (tid >> 4);
+            if (a.dq2 != nullptr)
+                depth_row_pair<bf16_t, HD / 16>(a.dq, a.dq2, a.dk, a.dv, a.dsbt, a.dss, a.dout,
+                                                a.dpd, a.dpl, row, tid & 15, a.dS, a.QH, a.dscale);
+            else
+                depth_row<bf16_t, HD / 16>(a.dq, a.dk, a.dv, a.dsbt, a.dss, a.dout, nullptr, nullptr,
+                                           row, tid & 15, a.dS, a.QH, a.dscale);
+        }
         return;
     }
     const int64_t len = a.pos_dev != nullptr ? *a.pos_dev + 1 : a.len;
@@ -1096,6 +1107,9 @@ struct DepthRead {
     const void* hv;
     int64_t sbt, ss, S;
     void* out;             // [B, QH, HD]
+    const void* q2;        // optional second query (bf16 MFMA form only)
+    float* part_d;         // [B, QH, HD]
+    float* part_lse;       // [B, QH]
 };
 
 template <typename T> constexpr int dtype_code();
@@ -1168,6 +1182,9 @@ static int gqa_dispatch(bool from_qkv, const void* q, const void* kc, const void
             a.dout = (T*)depth->out;
             a.dS = (int)depth->S;
             a.dscale = 1.0f / sqrtf((float)HD);
+            a.dq2 = (const T*)depth->q2;
+            a.dpd = depth->part_d;
+            a.dpl = depth->part_lse;
             mgrid.x += 1;
         }
 #define LOOM_GQA_MF(HDV, GG)                                                                      \
@@ -1385,11 +1402,55 @@ extern "C" int loom_gqa_decode_step_depth(int dtype, const void* qkv, void* k_ca
                               QH, KVH, HD);
     if (rc != LOOM_OK) return rc;
     if (B == 0) return LOOM_OK;
-    const DepthRead dr{depth_q, hist_k, hist_v, hist_stride_bt, hist_stride_s, S, depth_out};
+    const DepthRead dr{depth_q, hist_k, hist_v, hist_stride_bt, hist_stride_s, S, depth_out,
+                       nullptr, nullptr, nullptr};
     LOOM_DTYPE_SWITCH(dtype, gqa_dispatch, true, qkv, k_cache, v_cache, cache_stride_b,
                       cache_stride_t, cache_stride_h, cos_table, sin_table, q_out, c_out, kctx_out,
                       out_stride_b, workspace, B, len, pos_dev, QH, KVH, HD, (hipStream_t)stream,
                       &dr)
+}
+
+extern "C" int loom_gqa_decode_step_depth2(int dtype, const void* qkv, void* k_cache, void* v_cache,
+                                           int64_t cache_stride_b, int64_t cache_stride_t,
+                                           int64_t cache_stride_h, const float* cos_table,
+                                           const float* sin_table, void* q_out, void* c_out,
+                                           void* kctx_out, int64_t out_stride_b, float* workspace,
+                                           int64_t workspace_bytes, int64_t B, int64_t len,
+                                           const int64_t* pos_dev, int64_t QH, int64_t KVH,
+                                           int64_t HD, const void* depth_q, const void* depth_q2,
+                                           const void* hist_k, const void* hist_v,
+                                           int64_t hist_stride_bt, int64_t hist_stride_s, int64_t S,
+                                           void* depth_out, float* part_d, float* part_lse,
+                                           void* stream) {
+    clear_error();
+    LOOM_CHECK(qkv && k_cache && v_cache && cos_table && sin_table && c_out && kctx_out &&
+                   workspace && depth_q && depth_q2 && hist_k && hist_v && depth_out && part_d &&
+                   part_lse,
+               "gqa_decode_step_depth2: null argument");
+    LOOM_CHECK(out_stride_b >= QH * HD, "gqa_decode_step_depth2: bad out stride");
+    LOOM_CHECK(S >= 1 && hist_stride_s >= QH * HD && hist_stride_bt >= S * hist_stride_s,
+               "gqa_decode_step_depth2: history strides (bt=%lld, s=%lld) overlap the [S,QH,HD] block",
+               (long long)hist_stride_bt, (long long)hist_stride_s);
+    const int64_t G = KVH > 0 ? QH / KVH : 0;
+    LOOM_CHECK(dtype == LOOM_BF16 && (HD == 32 || HD == 64 || HD == 96 || HD == 128) &&
+                   (G == 1 || G == 2 || G == 4 || G == 8) && hist_stride_bt % 2 == 0 &&
+                   hist_stride_s % 2 == 0 &&
+                   ((((uintptr_t)depth_q | (uintptr_t)depth_q2 | (uintptr_t)hist_k |
+                      (uintptr_t)hist_v | (uintptr_t)depth_out | (uintptr_t)part_d) % 8) == 0) &&
+                   B * QH * 16 < ((int64_t)1 << 31),
+               "gqa_decode_step_depth2: needs the bf16 MFMA form (head_dim 32/64/96/128, group "
+               "1/2/4/8, 8-byte aligned depth rows)");
+    const int rc = gqa_checks("gqa_decode_step_depth2", k_cache, v_cache, cache_stride_b,
+                              cache_stride_t, cache_stride_h, workspace, workspace_bytes, B, len,
+                              QH, KVH, HD);
+    if (rc != LOOM_OK) return rc;
+    if (B == 0) return LOOM_OK;
+    const DepthRead dr{depth_q, hist_k, hist_v, hist_stride_bt, hist_stride_s, S, depth_out,
+                       depth_q2, part_d, part_lse};
+    return gqa_dispatch<bf16_t>(true, qkv, k_cache, v_cache, cache_stride_b, cache_stride_t,
+                                cache_stride_h, cos_table, sin_table, q_out, c_out, kctx_out,
+                                out_stride_b, workspace, B, len, pos_dev, QH, KVH, HD,
+                                (hipStream_t)stream, &dr);
 }
 
 // ---------------------------------------------------------------- step control

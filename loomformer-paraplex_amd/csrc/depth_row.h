@@ -157,4 +157,122 @@ __device__ __forceinline__ void depth_row(const T* __restrict__ q, const T* __re
     }
 }
 
+// Two reads over the same S history slots (one load of each K/V row): query
+// q1's read normalised into d_out, and query q2's read as the normalised fp32
+// row pd_out and its log-sum-exp lse_out (natural units, lane j == 0) -- the
+// part of a later read over slots 0..S that the S slots here contribute.  The
+// online softmax of q1 follows depth_row_core step for step.
+template <typename T, int EPL, int C = kDepthChunk>
+__device__ __forceinline__ void depth_row_pair(const T* __restrict__ q1, const T* __restrict__ q2,
+                                               const T* __restrict__ hk, const T* __restrict__ hv,
+                                               int64_t sbt, int64_t ss, T* __restrict__ d_out,
+                                               float* __restrict__ pd_out,
+                                               float* __restrict__ lse_out, int row, int j, int S,
+                                               int QH, float scale) {
+    constexpr int HD = EPL * 16;
+    const int qh = row % QH;
+    const int bt = row / QH;
+    const int d0 = j * EPL;
+    float qa[EPL], qb[EPL];
+    RowIO<T, EPL>::load(q1 + qh * HD + d0, qa);
+    RowIO<T, EPL>::load(q2 + qh * HD + d0, qb);
+    const float qs = scale * kLog2e;                        // scores in log2 units
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) {
+        qa[k] *= qs;
+        qb[k] *= qs;
+    }
+    const T* kp = hk + (int64_t)bt * sbt + qh * HD + d0;
+    const T* vp = hv + (int64_t)bt * sbt + qh * HD + d0;
+    float ma = -INFINITY, la = 0.0f, mb = -INFINITY, lb = 0.0f, aa[EPL], ab[EPL];
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) aa[k] = ab[k] = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += C) {
+        RawRow<T, EPL> kr[C], vr[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const int sc_ = s0 + c < S ? s0 + c : S - 1;   // in range; masked below
+            kr[c].load_nt(kp + (int64_t)sc_ * ss);
+            vr[c].load_nt(vp + (int64_t)sc_ * ss);
+        }
+        float sa[C], sb[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            float kv[EPL];
+            kr[c].to_float(kv);
+            float da = 0.0f, db = 0.0f;
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) {
+                da = fmaf(qa[k], kv[k], da);
+                db = fmaf(qb[k], kv[k], db);
+            }
+            sa[c] = da;
+            sb[c] = db;
+        }
+        float xa = -INFINITY, xb = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            sa[c] = group_sum<16>(sa[c]);
+            sb[c] = group_sum<16>(sb[c]);
+            if (s0 + c < S) {
+                xa = fmaxf(xa, sa[c]);
+                xb = fmaxf(xb, sb[c]);
+            }
+        }
+        const float na = fmaxf(ma, xa), nb = fmaxf(mb, xb);
+        const float ca = __builtin_amdgcn_exp2f(ma - na), cb = __builtin_amdgcn_exp2f(mb - nb);
+        la *= ca;
+        lb *= cb;
+#pragma unroll
+        for (int k = 0; k < EPL; ++k) {
+            aa[k] *= ca;
+            ab[k] *= cb;
+        }
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            float vv[EPL];
+            vr[c].to_float(vv);
+            const float pa = s0 + c < S ? __builtin_amdgcn_exp2f(sa[c] - na) : 0.0f;
+            const float pb = s0 + c < S ? __builtin_amdgcn_exp2f(sb[c] - nb) : 0.0f;
+            la += pa;
+            lb += pb;
+#pragma unroll
+            for (int k = 0; k < EPL; ++k) {
+                aa[k] = fmaf(pa, vv[k], aa[k]);
+                ab[k] = fmaf(pb, vv[k], ab[k]);
+            }
+        }
+        ma = na;
+        mb = nb;
+    }
+    const float ia = 1.0f / la, ib = 1.0f / lb;
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) {
+        aa[k] *= ia;
+        ab[k] *= ib;
+    }
+    RowIO<T, EPL>::store(d_out + (int64_t)row * HD + d0, aa);
+    RowIO<float, EPL>::store(pd_out + (int64_t)row * HD + d0, ab);
+    if (j == 0) lse_out[row] = (mb + flog2(lb)) * kLn2;
+}
+
+// The read of one head row over slots 0..S-1 from the read over slots 0..S-2
+// (pd: normalised fp32 row of this lane's EPL elements, lse: its log-sum-exp
+// in natural units) and slot S-1's key kn and value vn: one softmax over the
+// two parts.  qv: the query row's lane elements; scale = 1/sqrt(HD).
+template <int EPL>
+__device__ __forceinline__ void depth_fold_last(const float (&qv)[EPL], const float (&kn)[EPL],
+                                                const float (&vn)[EPL], const float (&pd)[EPL],
+                                                float lse, float scale, float (&out)[EPL]) {
+    float dot = 0.0f;
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) dot = fmaf(qv[k], kn[k], dot);
+    const float s = group_sum<16>(dot) * scale;
+    const float m = fmaxf(lse, s);
+    const float w1 = fexp(lse - m), w2 = fexp(s - m);
+    const float inv = 1.0f / (w1 + w2);
+#pragma unroll
+    for (int k = 0; k < EPL; ++k) out[k] = (pd[k] * w1 + vn[k] * w2) * inv;
+}
+
 }  // namespace loom

@@ -816,6 +816,10 @@ struct FfnArgs {
     int dS;
     float dscale;
     DepthRms drms;
+    // optional: the read over slots 0..dS-2 (normalised fp32 rows [M, QH, HD]
+    // and their log-sum-exp [M, QH]); the launch folds in slot dS-1 only
+    const float* dpd;
+    const float* dpl;
 };
 
 __device__ __forceinline__ float bf(uint16_t x) { return bf16_to_f32(x); }
@@ -869,14 +873,28 @@ ffn_decode_kernel(FfnArgs f) {
         // block takes two rounds
         for (int row = (int)threadIdx.x; row < f.g.M * 16; row += NW * 64) {
             const int b = row >> 4, j = row & 15;
-            float qv[DE], acc[DE], m, l;
-            depth_row_core<bf16_t, DE, 4, DR, false>(
-                (const bf16_t*)f.dq, (const bf16_t*)f.dk, (const bf16_t*)f.dv, f.dsbt, f.dss,
-                b * QH + g, j, f.dS, QH, f.dscale, f.drms, qv, acc, m, l);
-            const float inv_l = 1.0f / l;
             uint16_t o16[DE];
+            if (!DR && f.dpd != nullptr) {
+                // the earlier slots' part of the read comes in; fold in slot dS-1
+                const int r = b * QH + g;
+                const int64_t off = (int64_t)b * f.dsbt + (int64_t)(f.dS - 1) * f.dss + g * 16 * DE + j * DE;
+                float qv[DE], kn[DE], vn[DE], pd[DE], out[DE];
+                RowIO<bf16_t, DE>::load((const bf16_t*)f.dq + g * 16 * DE + j * DE, qv);
+                RowIO<bf16_t, DE>::load((const bf16_t*)f.dk + off, kn);
+                RowIO<bf16_t, DE>::load((const bf16_t*)f.dv + off, vn);
+                RowIO<float, DE>::load(f.dpd + (int64_t)r * 16 * DE + j * DE, pd);
+                depth_fold_last<DE>(qv, kn, vn, pd, f.dpl[r], f.dscale, out);
 #pragma unroll
-            for (int k = 0; k < DE; ++k) o16[k] = f32_to_bf16(acc[k] * inv_l);
+                for (int k = 0; k < DE; ++k) o16[k] = f32_to_bf16(out[k]);
+            } else {
+                float qv[DE], acc[DE], m, l;
+                depth_row_core<bf16_t, DE, 4, DR, false>(
+                    (const bf16_t*)f.dq, (const bf16_t*)f.dk, (const bf16_t*)f.dv, f.dsbt, f.dss,
+                    b * QH + g, j, f.dS, QH, f.dscale, f.drms, qv, acc, m, l);
+                const float inv_l = 1.0f / l;
+#pragma unroll
+                for (int k = 0; k < DE; ++k) o16[k] = f32_to_bf16(acc[k] * inv_l);
+            }
 #pragma unroll
             for (int k = 0; k < DE; ++k) dsh[b * 16 * DE + j * DE + k] = o16[k];
             if (t == 0) {
@@ -1873,6 +1891,11 @@ extern "C" int loom_ffn_decode(int dtype, const loom_ffn_decode_desc* d, void* s
                 f.dv = (const uint16_t*)d->depth_v; f.dsbt = d->depth_sbt; f.dss = d->depth_ss;
                 f.dS = d->depth_S; f.dscale = 1.0f / sqrtf((float)d->head_dim);
                 f.drms = DepthRms{d->depth_qt, d->depth_kt, d->depth_vt};
+                // the earlier slots' part, when given, for the plain read over two or more slots
+                const bool part = !rms && d->depth_part_d != nullptr && d->depth_part_lse != nullptr &&
+                                  d->depth_S >= 2 && ((uintptr_t)d->depth_part_d & 7) == 0;
+                f.dpd = part ? d->depth_part_d : nullptr;
+                f.dpl = part ? d->depth_part_lse : nullptr;
                 const bool done = d->M <= 16 ? launch_ffn_depth<1>(f, grid, rms, st)
                                              : launch_ffn_depth<2>(f, grid, rms, st);
                 if (done) return launch_status("loom_ffn_decode");

@@ -13,7 +13,7 @@ from ctypes import c_float, c_int, c_int64, c_void_p
 import torch
 
 # descriptor layouts and signatures below are those of loom_abi_version() == 5
-ABI_VERSION = 6
+ABI_VERSION = 7
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libloom_hip.so")
 
 _P = c_void_p
@@ -88,6 +88,10 @@ SIGNATURES = {
                                    _P, c_int64, _P, c_int64, c_int64, c_int64, _P, c_int64,
                                    c_int64, c_int64, _P, _P, _P, c_int64, c_int64, c_int64, _P,
                                    _P],
+    "loom_gqa_decode_step_depth2": [c_int, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P,
+                                    _P, c_int64, _P, c_int64, c_int64, c_int64, _P, c_int64,
+                                    c_int64, c_int64, _P, _P, _P, _P, c_int64, c_int64, c_int64,
+                                    _P, _P, _P, _P],
     "loom_decode_prologue": [_P, _P, c_int64, c_int64, _P, c_int64, _P, _P, _P, _P, c_int64,
                              c_int64, c_int64, c_int64, _P],
     "loom_decode_prologue_embed": [c_int, _P, _P, c_int64, c_int64, _P, c_int64, _P, _P, _P, _P,
@@ -183,7 +187,8 @@ class FfnDecodeDesc(ctypes.Structure):
                 ("u_frag", c_void_p), ("depth_q", c_void_p), ("depth_k", c_void_p),
                 ("depth_v", c_void_p), ("depth_sbt", c_int64), ("depth_ss", c_int64),
                 ("depth_S", ctypes.c_int32), ("depth_rms", ctypes.c_int32), ("depth_qt", c_float),
-                ("depth_kt", c_float), ("depth_vt", c_float)]
+                ("depth_kt", c_float), ("depth_vt", c_float), ("depth_part_d", c_void_p),
+                ("depth_part_lse", c_void_p)]
 
 
 def linear_multi_desc(x, segments, x2=None, m=None, only_if=None, x_frag=None, x2_frag=None):

@@ -172,6 +172,13 @@ class LoomDecoder:
         self.kctx = z(B, c.QH, c.HD)
         self.d = z(B, c.QH, c.HD)
         self.dh = z(B, c.QH, c.HD)
+        # the attention launch's depth slice also reads history slots 0..2bi with the
+        # FFN sublayer's query (normalised fp32 rows and log-sum-exp); ffn_decode then
+        # folds in slot 2bi+1 alone (bf16 MFMA attention, plain depth read)
+        self.depth_pair = (dtype == torch.bfloat16 and self.depth_rms is None
+                           and c.HD in (32, 64, 96, 128) and c.QH // c.KVH in (1, 2, 4, 8))
+        self.part_d = z(B, c.QH, c.HD, dtype=torch.float32) if self.depth_pair else None
+        self.part_lse = z(B, c.QH, dtype=torch.float32) if self.depth_pair else None
         self.attn_out = z(B, N)
         self.skip = z(B, N)
         self.R = z(B, H)
@@ -320,7 +327,16 @@ class LoomDecoder:
             # ---- attention step (loomformer.py:3300-3332): RoPE + cache append +
             # attention + chunk merge, one launch
             # with the depth read 2*bi of this token (loomformer.py:3999) in the same launch
-            if self.depth_rms is None:
+            if self.depth_pair:
+                # with the FFN sublayer's read (query sub + 1) over the same slots
+                self._call("loom_gqa_decode_step_depth2", self.code, _P(self.qkv), _P(kc), _P(vc),
+                           cache_sb, cache_st, cache_sh, _P(self.cos), _P(self.sin), _P(self.q),
+                           _P(self.c), _P(self.kctx), N,
+                           _P(self.ws), self.ws_bytes, B, self.max_len, _P(self.pos_dev), c.QH,
+                           c.KVH, c.HD, _P(self.qp[sub]), _P(self.qp[sub + 1]), _P(self.hist),
+                           _P(self.hist[:, :, N:]), 2 * L * 2 * N, 2 * N, sub + 1, _P(self.d),
+                           _P(self.part_d), _P(self.part_lse), st)
+            elif self.depth_rms is None:
                 self._call("loom_gqa_decode_step_depth", self.code, _P(self.qkv), _P(kc), _P(vc),
                            cache_sb, cache_st, cache_sh, _P(self.cos), _P(self.sin), _P(self.q),
                            _P(self.c), _P(self.kctx), N,
@@ -378,6 +394,7 @@ class LoomDecoder:
                     depth_q=self.qp[sub], depth_k=self.hist, depth_v=self.hist[:, :, N:],
                     depth_sbt=2 * L * 2 * N, depth_ss=2 * N, depth_S=sub + 1,
                     depth_rms=0 if self.depth_rms is None else 1,
+                    depth_part_d=self.part_d, depth_part_lse=self.part_lse,
                     **({} if self.depth_rms is None else
                        dict(zip(("depth_qt", "depth_kt", "depth_vt"), self.depth_rms))))
                 self._descs[key] = d

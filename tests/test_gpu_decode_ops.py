@@ -233,6 +233,29 @@ def test_gqa_decode_step_depth(dtype, B, QH, KVH, HD, length, S_, L2):
     hv = host(hist)[:, :S_, N:].view(B, S_, QH, HD)
     w = torch.softmax((hk * host(dq)).sum(-1) / math.sqrt(HD), dim=1)      # [B, S, QH]
     check(outs[1][3].view(B, QH, HD), (w.unsqueeze(-1) * hv).sum(1), dtype)
+    # a second query over the same slots (loom_gqa_decode_step_depth2): the
+    # other outputs as before, its read as fp32 rows and log-sum-exp
+    dq2 = (torch.randn(QH, HD, generator=g) * 0.3).to(DEV, dtype)
+    kc, vc = kc0.clone(), vc0.clone()
+    ws = torch.zeros(nb // 4 + 1, device=DEV)
+    c, kx, qo, d = (torch.zeros(B, N, device=DEV, dtype=dtype) for _ in range(4))
+    pd = torch.full((B, QH, HD), float("nan"), device=DEV)
+    pl = torch.full((B, QH), float("nan"), device=DEV)
+    args = (P(qkv), P(kc), P(vc), *strides, P(cos_d), P(sin_d), P(qo), P(c), P(kx), N, P(ws),
+            nb, B, max_len, P(pos_d), QH, KVH, HD, P(dq), P(dq2), P(hist), P(hist[:, :, N:]),
+            L2 * 2 * N, 2 * N, S_, P(d), P(pd), P(pl), S(qkv))
+    if dtype != torch.bfloat16 or HD not in (32, 64, 96, 128):
+        with pytest.raises(RuntimeError, match="bf16 MFMA form"):
+            _lib.call("loom_gqa_decode_step_depth2", code(qkv), *args)
+        return
+    _lib.call("loom_gqa_decode_step_depth2", code(qkv), *args)
+    for x, y in zip([host(t) for t in (c, kx, qo, kc, vc)], [outs[1][i] for i in (0, 1, 2, 4, 5)]):
+        assert torch.equal(x, y)
+    torch.testing.assert_close(host(d), outs[1][3], rtol=1e-2, atol=1e-2)
+    sc2 = (hk * host(dq2)).sum(-1) / math.sqrt(HD)                          # [B, S, QH]
+    w2 = torch.softmax(sc2, dim=1)
+    torch.testing.assert_close(pd.cpu(), (w2.unsqueeze(-1) * hv).sum(1), rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(pl.cpu(), torch.logsumexp(sc2, dim=1), rtol=1e-5, atol=1e-5)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -548,11 +571,17 @@ def test_ffn_decode(dtype, mode, gate, axis, gsrc):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("M,rms,slots,QH,HD", [
-    (32, False, 4, 8, 96), (32, True, 11, 8, 96), (9, False, 20, 8, 96), (40, False, 7, 8, 96),
+@pytest.mark.parametrize("M,rms,slots,QH,HD,part", [
+    (32, False, 4, 8, 96, False), (32, True, 11, 8, 96, False), (9, False, 20, 8, 96, False),
+    (40, False, 7, 8, 96, False),
     # W_imag input 512 wide: 4-wave blocks, so 20 or 32 rows of 16 lanes take two rounds
-    (20, False, 5, 4, 64), (20, True, 7, 4, 64), (32, False, 13, 4, 64), (32, True, 9, 4, 64)])
-def test_ffn_decode_with_depth_read(dtype, M, rms, slots, QH, HD):
+    (20, False, 5, 4, 64, False), (20, True, 7, 4, 64, False), (32, False, 13, 4, 64, False),
+    (32, True, 9, 4, 64, False),
+    # the read over slots 0..S-2 given (normalised fp32 rows + log-sum-exp): the
+    # launch folds in slot S-1 only (the fixed-RMS read ignores the part)
+    (32, False, 20, 8, 96, True), (32, False, 2, 8, 96, True), (20, False, 5, 4, 64, True),
+    (32, True, 11, 8, 96, True), (40, False, 7, 8, 96, True)])
+def test_ffn_decode_with_depth_read(dtype, M, rms, slots, QH, HD, part):
     """ffn_decode computing its own d_h: the depth read of history slot S-1
     (DepthAttn over slots 0..S-1, fixed-RMS q/k/v with rms) inside the launch
     (bf16, M <= 32) or as a launch before it (fp32, M > 32).  d_h against the
@@ -581,6 +610,14 @@ def test_ffn_decode_with_depth_read(dtype, M, rms, slots, QH, HD):
     carry = torch.empty(M, H, 3, 3, device=DEV, dtype=dtype)
     p = torch.empty(M, H, device=DEV, dtype=dtype)
     tg = (0.88 / HD ** 0.5, 0.88, 0.88 * 0.4)
+    pd = pl = None
+    if part:
+        # the oracle's read over slots 0..S-2 with this query, as fp32 rows + log-sum-exp
+        hk0 = host(hist)[:, :slots - 1, :N].reshape(M, slots - 1, QH, HD)
+        hv0 = host(hist)[:, :slots - 1, N:].reshape(M, slots - 1, QH, HD)
+        sc0 = (hk0 * host(dq)).sum(-1) / math.sqrt(HD)
+        pd = (torch.softmax(sc0, dim=1).unsqueeze(-1) * hv0).sum(1).to(DEV)
+        pl = torch.logsumexp(sc0, dim=1).to(DEV)
     desc = _lib.ffn_decode_desc(
         u=u, q_h=q, k_ctx_h=kc, c_h=c, d_h=d, w_compact=w, M=M, N=N, H=H, imag_in=K,
         hidden_per_q_head=H // QH, head_dim=HD, n_q_heads=QH, open_sectors=0,
@@ -588,6 +625,7 @@ def test_ffn_decode_with_depth_read(dtype, M, rms, slots, QH, HD):
         beta=beta, carry_prev=prev, seed=None, seed_valid=None, gate_w=gw, carry_out=carry, p_out=p,
         alpha=0.0375, axis=1, depth_q=dq, depth_k=hist, depth_v=hist[:, :, N:],
         depth_sbt=L2 * 2 * N, depth_ss=2 * N, depth_S=slots, depth_rms=1 if rms else 0,
+        depth_part_d=pd, depth_part_lse=pl,
         **(dict(zip(("depth_qt", "depth_kt", "depth_vt"), tg)) if rms else {}))
     _lib.call("loom_ffn_decode", code(u), ctypes.byref(desc), S(u))
     # fixed_rms on the stored dtype, as the reference applies it
