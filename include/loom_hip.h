@@ -263,6 +263,28 @@ int loom_depth_attn_forward(int dtype, const void* q, const void* hist_k, const 
                             float* lse_out, int64_t BT, int64_t S, int64_t QH, int64_t HD,
                             void* stream);
 
+/* Two DepthAttn reads over the same history slots 0..S-1 in one pass over
+ * them: q1's read d_out [BT,QH,HD] dtype as loom_depth_attn_forward gives it,
+ * and q2's read as normalised fp32 rows part_d [BT,QH,HD] with their
+ * log-sum-exp part_lse [BT,QH] (natural units) -- the part of the next
+ * sublayer's read over slots 0..S (DepthAttn.forward with that sublayer's
+ * query, loomformer.py:3404-3429) that these slots contribute.  head_dim
+ * 32/64/96/128, 8-byte aligned rows, even strides.  No counterpart in the
+ * reference (it reads every slot again for every sublayer). */
+int loom_depth_attn_pair(int dtype, const void* q1, const void* q2, const void* hist_k,
+                         const void* hist_v, int64_t stride_bt, int64_t stride_s, void* d_out,
+                         float* part_d, float* part_lse, int64_t BT, int64_t S, int64_t QH,
+                         int64_t HD, void* stream);
+
+/* The read of query q over slots 0..S-1 (S >= 2) from the read over slots
+ * 0..S-2 given as part_d / part_lse (as loom_depth_attn_pair writes them) and
+ * slot S-1's key and value rows: one softmax over the two parts, written to
+ * d_out [BT,QH,HD] dtype.  Same layouts and limits as loom_depth_attn_pair. */
+int loom_depth_attn_fold(int dtype, const void* q, const void* hist_k, const void* hist_v,
+                         int64_t stride_bt, int64_t stride_s, int64_t S, const float* part_d,
+                         const float* part_lse, void* d_out, int64_t BT, int64_t QH, int64_t HD,
+                         void* stream);
+
 /* loom_depth_attn_forward for DepthAttn under depth_attn_qkv_rms
  * (loomformer.py:3397-3407): the query, key and value rows are read as
  * fixed-RMS vectors x * t / sqrt(mean(x^2) + 1e-6) with targets q_target

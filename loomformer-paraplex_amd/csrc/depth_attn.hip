@@ -128,9 +128,127 @@ static int dispatch_depth(const void* q, const void* hk, const void* hv, int64_t
     return launch_status("loom_depth_attn_forward");
 }
 
+// Two depth queries over the same S slots in one pass (depth_row_pair):
+// q1's read into d_out, q2's as normalised fp32 rows and log-sum-exp.
+template <typename T, int EPL>
+__global__ void __launch_bounds__(256)
+depth_attn_pair_kernel(const T* __restrict__ q1, const T* __restrict__ q2,
+                       const T* __restrict__ hk, const T* __restrict__ hv, int64_t sbt, int64_t ss,
+                       T* __restrict__ d_out, float* __restrict__ pd_out,
+                       float* __restrict__ lse_out, int rows, int S, int QH, float scale) {
+    const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 4);
+    if (row >= rows) return;  // all 16 lanes of a group leave together
+    depth_row_pair<T, EPL>(q1, q2, hk, hv, sbt, ss, d_out, pd_out, lse_out, row,
+                           threadIdx.x & 15, S, QH, scale);
+}
+
+// The read over slots 0..S-1 from the read over slots 0..S-2 (normalised fp32
+// rows and log-sum-exp) and slot S-1: one slot row of K and V per (bt, qh).
+template <typename T, int EPL>
+__global__ void __launch_bounds__(256)
+depth_attn_fold_kernel(const T* __restrict__ q, const T* __restrict__ hk,
+                       const T* __restrict__ hv, int64_t sbt, int64_t ss, int S,
+                       const float* __restrict__ pd, const float* __restrict__ plse,
+                       T* __restrict__ d_out, int rows, int QH, float scale) {
+    constexpr int HD = EPL * 16;
+    const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 4);
+    if (row >= rows) return;
+    const int j = threadIdx.x & 15, qh = row % QH, bt = row / QH, d0 = j * EPL;
+    const int64_t off = (int64_t)bt * sbt + (int64_t)(S - 1) * ss + qh * HD + d0;
+    float qv[EPL], kn[EPL], vn[EPL], part[EPL], out[EPL];
+    RowIO<T, EPL>::load(q + qh * HD + d0, qv);
+    RowIO<T, EPL>::load(hk + off, kn);
+    RowIO<T, EPL>::load(hv + off, vn);
+    RowIO<float, EPL>::load(pd + (int64_t)row * HD + d0, part);
+    depth_fold_last<EPL>(qv, kn, vn, part, plse[row], scale, out);
+    RowIO<T, EPL>::store(d_out + (int64_t)row * HD + d0, out);
+}
+
+template <typename T>
+static int dispatch_pair_fold(bool pair, const void* q1, const void* q2, const void* hk,
+                              const void* hv, int64_t sbt, int64_t ss, int64_t S, void* d_out,
+                              float* pd, float* plse, int64_t BT, int64_t QH, int64_t HD,
+                              hipStream_t stream) {
+    const int64_t rows = BT * QH;
+    const float scale = 1.0f / sqrtf((float)HD);
+    const int threads = rows * 16 >= 256 * 256 ? 256 : 64;
+    const dim3 grid((unsigned)ceil_div(rows * 16, threads));
+#define LOOM_PF_CASE(E)                                                                          \
+    case E:                                                                                      \
+        if (pair)                                                                                \
+            hipLaunchKernelGGL((depth_attn_pair_kernel<T, E>), grid, dim3(threads), 0, stream,   \
+                               (const T*)q1, (const T*)q2, (const T*)hk, (const T*)hv, sbt, ss,  \
+                               (T*)d_out, pd, plse, (int)rows, (int)S, (int)QH, scale);          \
+        else                                                                                     \
+            hipLaunchKernelGGL((depth_attn_fold_kernel<T, E>), grid, dim3(threads), 0, stream,   \
+                               (const T*)q1, (const T*)hk, (const T*)hv, sbt, ss, (int)S, pd,    \
+                               plse, (T*)d_out, (int)rows, (int)QH, scale);                      \
+        return launch_status(pair ? "loom_depth_attn_pair" : "loom_depth_attn_fold");
+    switch (HD / 16) {
+        LOOM_PF_CASE(2)
+        LOOM_PF_CASE(4)
+        LOOM_PF_CASE(6)
+        LOOM_PF_CASE(8)
+    }
+#undef LOOM_PF_CASE
+    set_error("depth_attn_pair/fold: head_dim %lld not supported", (long long)HD);
+    return LOOM_ERR_INVALID;
+}
+
 }  // namespace loom
 
 using namespace loom;
+
+// shape and layout checks shared by loom_depth_attn_pair and loom_depth_attn_fold
+static int pair_fold_entry(bool pair, int dtype, const void* q1, const void* q2, const void* hk,
+                           const void* hv, int64_t sbt, int64_t ss, int64_t S, void* d_out,
+                           float* pd, float* plse, int64_t BT, int64_t QH, int64_t HD,
+                           void* stream) {
+    const char* what = pair ? "depth_attn_pair" : "depth_attn_fold";
+    LOOM_CHECK(q1 && (!pair || q2) && hk && hv && d_out && pd && plse, "%s: null tensor argument", what);
+    LOOM_CHECK(BT >= 0 && S >= (pair ? 1 : 2) && QH >= 1, "%s: bad shape BT=%lld S=%lld", what,
+               (long long)BT, (long long)S);
+    LOOM_CHECK((HD == 32 || HD == 64 || HD == 96 || HD == 128),
+               "%s: head_dim must be 32, 64, 96 or 128, got %lld", what, (long long)HD);
+    LOOM_CHECK(ss >= QH * HD && sbt >= S * ss,
+               "%s: strides (bt=%lld, s=%lld) overlap the [S,QH,HD] block", what, (long long)sbt,
+               (long long)ss);
+    LOOM_CHECK(sbt % 2 == 0 && ss % 2 == 0 &&
+                   ((((uintptr_t)hk | (uintptr_t)hv | (uintptr_t)q1 | (uintptr_t)q2 |
+                      (uintptr_t)d_out | (uintptr_t)pd) % 8) == 0) &&
+                   BT * QH * 16 < ((int64_t)1 << 31),
+               "%s: rows need 8-byte alignment and even strides", what);
+    if (BT == 0) return LOOM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    switch (dtype) {
+        case LOOM_F32:
+            return dispatch_pair_fold<float>(pair, q1, q2, hk, hv, sbt, ss, S, d_out, pd, plse, BT, QH, HD, st);
+        case LOOM_BF16:
+            return dispatch_pair_fold<bf16_t>(pair, q1, q2, hk, hv, sbt, ss, S, d_out, pd, plse, BT, QH, HD, st);
+        case LOOM_F16:
+            return dispatch_pair_fold<f16_t>(pair, q1, q2, hk, hv, sbt, ss, S, d_out, pd, plse, BT, QH, HD, st);
+    }
+    set_error("%s: unsupported dtype %d", what, dtype);
+    return LOOM_ERR_INVALID;
+}
+
+extern "C" int loom_depth_attn_pair(int dtype, const void* q1, const void* q2, const void* hist_k,
+                                    const void* hist_v, int64_t stride_bt, int64_t stride_s,
+                                    void* d_out, float* part_d, float* part_lse, int64_t BT,
+                                    int64_t S, int64_t QH, int64_t HD, void* stream) {
+    clear_error();
+    return pair_fold_entry(true, dtype, q1, q2, hist_k, hist_v, stride_bt, stride_s, S, d_out,
+                           part_d, part_lse, BT, QH, HD, stream);
+}
+
+extern "C" int loom_depth_attn_fold(int dtype, const void* q, const void* hist_k,
+                                    const void* hist_v, int64_t stride_bt, int64_t stride_s,
+                                    int64_t S, const float* part_d, const float* part_lse,
+                                    void* d_out, int64_t BT, int64_t QH, int64_t HD, void* stream) {
+    clear_error();
+    return pair_fold_entry(false, dtype, q, q, hist_k, hist_v, stride_bt, stride_s, S, d_out,
+                           (float*)part_d, (float*)part_lse, BT, QH, HD, stream);
+}
 
 static int depth_entry(int dtype, const void* q, const void* hist_k, const void* hist_v,
                        int64_t stride_bt, int64_t stride_s, void* d_out, void* w_out,

@@ -75,6 +75,10 @@ SIGNATURES = {
     "loom_gqa_decode_step": [c_int, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P,
                              c_int64, _P, c_int64, c_int64, c_int64, _P, c_int64, c_int64, c_int64,
                              _P],
+    "loom_depth_attn_pair": [c_int, _P, _P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64,
+                             c_int64, c_int64, c_int64, _P],
+    "loom_depth_attn_fold": [c_int, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, c_int64,
+                             c_int64, c_int64, _P],
     "loom_depth_attn_forward_rms": [c_int, _P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64,
                                     c_int64, c_int64, c_int64, c_float, c_float, c_float, _P],
     "loom_rms_norm": [c_int, _P, _P, _P, c_int64, c_int64, c_float, _P],

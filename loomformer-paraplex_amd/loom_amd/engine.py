@@ -245,6 +245,30 @@ class LoomDecoder:
         else:
             self._call("loom_depth_attn_forward_rms", *args, *self.depth_rms, self._stream())
 
+    @property
+    def pair_reads(self) -> bool:
+        """The plain depth read at a head size the paired / folded kernels take."""
+        return self.depth_rms is None and self.cfg.HD in (32, 64, 96, 128)
+
+    def depth_read_pair(self, sub: int, hist: torch.Tensor, out: torch.Tensor,
+                        part_d: torch.Tensor, part_lse: torch.Tensor, rows: int) -> None:
+        """DepthAttn reads over history slots [0, sub] for sublayers sub (into out) and
+        sub + 1 (its part over these slots: fp32 rows part_d and log-sum-exp
+        part_lse), one pass over the slots (loomformer.py:3404-3429)."""
+        c, N, L = self.cfg, self.cfg.N, self.cfg.L
+        self._call("loom_depth_attn_pair", self.code, _P(self.qp[sub]), _P(self.qp[sub + 1]),
+                   _P(hist), _P(hist[:, :, N:]), 2 * L * 2 * N, 2 * N, _P(out), _P(part_d),
+                   _P(part_lse), rows, sub + 1, c.QH, c.HD, self._stream())
+
+    def depth_read_fold(self, sub: int, hist: torch.Tensor, out: torch.Tensor,
+                        part_d: torch.Tensor, part_lse: torch.Tensor, rows: int) -> None:
+        """DepthAttn read of sublayer sub over slots [0, sub] from its part over
+        slots [0, sub - 1] (depth_read_pair of sublayer sub - 1) and slot sub."""
+        c, N, L = self.cfg, self.cfg.N, self.cfg.L
+        self._call("loom_depth_attn_fold", self.code, _P(self.qp[sub]), _P(hist),
+                   _P(hist[:, :, N:]), 2 * L * 2 * N, 2 * N, sub + 1, _P(part_d), _P(part_lse),
+                   _P(out), rows, c.QH, c.HD, self._stream())
+
     def _linear(self, x, w, out, M, Nout, K, bias=None, ldx=None, ldc=None, gate_p=None,
                 gate_alpha=0.0, residual=None):
         self._call("loom_linear", self.code, _P(x), ldx or K, _P(w), K, _P(bias), _P(gate_p),

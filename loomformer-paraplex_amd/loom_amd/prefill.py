@@ -113,8 +113,19 @@ def prefill(eng, prompt: torch.Tensor) -> None:
         call("loom_linear_ln", code, _lib.ctypes.byref(dsc), _P(gamma), _P(beta_ln), 1e-5, _P(h), N,
              _P(ln_ws), ln_ws.numel() * 4, None, st)
 
+    # the attention sublayer's read of slots 0..2bi also reads them with the FFN
+    # sublayer's query (its part, fp32); the FFN read then folds in slot 2bi+1
+    pair = eng.pair_reads
+    part_d = torch.empty(M, QH, HD, dtype=torch.float32, device=dev) if pair else None
+    part_lse = torch.empty(M, QH, dtype=torch.float32, device=dev) if pair else None
+
     def depth(sub, out, rows):
-        eng.depth_read(sub, hist, out, rows)
+        if not pair:
+            eng.depth_read(sub, hist, out, rows)
+        elif sub % 2 == 0:
+            eng.depth_read_pair(sub, hist, out, part_d, part_lse, rows)
+        else:
+            eng.depth_read_fold(sub, hist, out, part_d, part_lse, rows)
 
     spans = list(zip([0] + [x + 1 for x in ends[:-1]], ends))
 

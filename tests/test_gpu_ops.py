@@ -310,6 +310,45 @@ def test_depth_attn_stacked(dtype, BT, S):
     check(d, host(hv).mean(2), dtype)
 
 
+@pytest.mark.parametrize("dtype", DTYPES3)
+@pytest.mark.parametrize("BT,S,HD", [(50, 1, 96), (4096, 19, 96), (7, 8, 64), (33, 3, 128), (5, 12, 32)])
+def test_depth_attn_pair_and_fold(dtype, BT, S, HD):
+    """loom_depth_attn_pair: two queries over slots 0..S-1 in one pass (the
+    first as loom_depth_attn_forward, the second as fp32 rows + log-sum-exp);
+    loom_depth_attn_fold: the second query's read over slots 0..S from that
+    part and slot S, against the oracle's read over all S + 1 slots."""
+    from loom_amd import _lib
+    g = gen(BT * 7 + S + HD)
+    QH, L2 = 8, S + 3
+    N = QH * HD
+    hist = dev(rnd(g, BT, L2, 2 * N), dtype)          # slot s = [k | v]
+    q1, q2 = dev(rnd(g, QH, HD, scale=0.4), dtype), dev(rnd(g, QH, HD, scale=0.4), dtype)
+    d1 = torch.empty(BT, QH, HD, device=DEV, dtype=dtype)
+    pd = torch.full((BT, QH, HD), float("nan"), device=DEV)
+    pl = torch.full((BT, QH), float("nan"), device=DEV)
+    st = _lib.stream_of(hist)
+    _lib.call("loom_depth_attn_pair", _lib.dtype_code(hist), _lib.ptr(q1), _lib.ptr(q2), _lib.ptr(hist),
+              _lib.ptr(hist[:, :, N:]), L2 * 2 * N, 2 * N, _lib.ptr(d1), _lib.ptr(pd), _lib.ptr(pl),
+              BT, S, QH, HD, st)
+    hk = host(hist)[:, :, :N].reshape(BT, L2, QH, HD)
+    hv = host(hist)[:, :, N:].reshape(BT, L2, QH, HD)
+    want1, _, _ = ref.depth_attn_softmax(host(q1), hk[:, :S][None], hv[:, :S][None])
+    check(d1, want1[0], dtype)
+    want2, _, lse2 = ref.depth_attn_softmax(host(q2), hk[:, :S][None], hv[:, :S][None])
+    torch.testing.assert_close(pd.cpu(), want2[0], rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(pl.cpu(), lse2[0], rtol=1e-5, atol=1e-5)
+    d2 = torch.empty(BT, QH, HD, device=DEV, dtype=dtype)
+    _lib.call("loom_depth_attn_fold", _lib.dtype_code(hist), _lib.ptr(q2), _lib.ptr(hist),
+              _lib.ptr(hist[:, :, N:]), L2 * 2 * N, 2 * N, S + 1, _lib.ptr(pd), _lib.ptr(pl),
+              _lib.ptr(d2), BT, QH, HD, st)
+    want3, _, _ = ref.depth_attn_softmax(host(q2), hk[:, :S + 1][None], hv[:, :S + 1][None])
+    check(d2, want3[0], dtype)
+    with pytest.raises(RuntimeError, match="head_dim must be"):
+        _lib.call("loom_depth_attn_fold", _lib.dtype_code(hist), _lib.ptr(q2), _lib.ptr(hist),
+                  _lib.ptr(hist[:, :, N:]), L2 * 2 * N, 2 * N, S + 1, _lib.ptr(pd), _lib.ptr(pl),
+                  _lib.ptr(d2), BT, QH, 80, st)          # rejected before any launch
+
+
 def test_golden_depth_attn_vs_reference():
     from loom_amd import ops
     z = np.load(os.path.join(GOLD, "ops.npz"))
