@@ -249,6 +249,13 @@ gemm_bf16_mfma_kernel(GemmArgs a) {
 // scalar soffset.  Requires K % (32 * KH * NS) == 0 (whole rounds of the
 // stages).
 __host__ __device__ constexpr int bg_swz(int r) { return ((r >> 3) & 1) << 1; }
+// Full-line stages (no gather, 64 k per stage): a stage row is the whole
+// 128-byte line [8 chunks of 8 k], chunk c of row r at position c ^ bg_swz8(r).
+// A fragment read's half-wave takes 16 rows x chunks {4kk + 2h, 4kk + 2h + 1};
+// rows r, r+4, r+8, r+12 share their offset modulo 512 B and the swizzle puts
+// their chunk pairs on four distinct pairs of positions.  One DMA instruction
+// then fills 8 whole rows (lane l: row l/8, position l%8), 8 full lines.
+__host__ __device__ constexpr int bg_swz8(int r) { return ((r >> 2) & 3) << 1; }
 
 template <int BM_, int BN_, int WAVES_, int WGM_, int KH_, int WPE_, int NS_>
 struct BgCfg {
@@ -265,12 +272,13 @@ struct BgCfg {
 };
 using BgConf = BgCfg<256, 128, 8, 4, 2, 2, 3>;
 // 128 x 128 tiles (four waves of 64 x 64, one 32-wide k-half per stage, four
-// stages, two blocks per CU) and 128 x 256 tiles (eight waves of 64 x 64):
-// the smaller tile fills the CUs when the 256 x 128 tiles leave many idle or
-// end in a partial round, the wider one serves many-row products with N a
-// multiple of 256
+// stages, two blocks per CU) and 128 x 256 tiles (eight waves of 64 x 64, 64 k
+// per stage in three full-line stages: 8192 x 3072 x 768 52 us against 58-62
+// with four 32-k stages): the smaller tile fills the CUs when the 256 x 128
+// tiles leave many idle or end in a partial round, the wider one serves
+// many-row products with N a multiple of 256
 using BgSmall = BgCfg<128, 128, 4, 2, 1, 2, 4>;
-using BgWide = BgCfg<128, 256, 8, 2, 1, 2, 4>;
+using BgWide = BgCfg<128, 256, 8, 2, 2, 2, 3>;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 template <int N>
@@ -336,6 +344,10 @@ gemm_bf16_big_kernel(GemmArgs a) {
     constexpr int XH = BG_M * 32, WH = BG_N * 32;   // elements per k-half of a stage
     constexpr int KH = C::KH, FI = C::FI, FJ = C::FJ, XG = C::XG, WG = C::WG, DMA = C::DMA;
     constexpr int NS = C::NS;
+    // full-line stages (bg_swz8) for the products without a gather at 64 k per
+    // stage; XQ / WQ DMA slots per wave (8 rows each, else 16 rows of a k-half)
+    constexpr bool FL = !GATHER && KH == 2;
+    constexpr int XQ = FL ? 2 * XG : XG, WQ = FL ? 2 * WG : WG;
     // stage s: X_s, W_s (separate arrays, so a wait for one stage's DMA never
     // covers another's reads); arrays of stages >= NS are not referenced
     __shared__ __attribute__((aligned(16))) uint16_t X0[KH * XH], X1[KH * XH], X2[KH * XH],
@@ -384,18 +396,24 @@ gemm_bf16_big_kernel(GemmArgs a) {
     // DMA slots: X 16-row groups XG*wave + q, W groups WG*wave + q, each for
     // every k-half; lane: row 16*group + lane/4, chunk (lane%4) ^ bg_swz(row);
     // rows past M / N read the last row (their results are not stored)
-    uint32_t xv[XG], wv[WG];
+    // (full-line stages: X groups of 8 rows XQ*wave + q, lane: row 8*group +
+    // lane/8, chunk (lane%8) ^ bg_swz8(row))
+    auto slot_row = [&](int q, int per) {
+        return FL ? 8 * (per * wave + q) + (lane >> 3) : 16 * (per * wave + q) + (lane >> 2);
+    };
+    auto slot_pos = [&](int r) { return FL ? (lane & 7) ^ bg_swz8(r) : (lane & 3) ^ bg_swz(r); };
+    uint32_t xv[XQ], wv[WQ];
 #pragma unroll
-    for (int q = 0; q < XG; ++q) {
-        const int r = 16 * (XG * wave + q) + (lane >> 2);
+    for (int q = 0; q < XQ; ++q) {
+        const int r = slot_row(q, XQ);
         const int64_t rr = m0 + r < a.M ? r : a.M - 1 - m0;
-        xv[q] = (uint32_t)((rr * ldx + 8 * ((lane & 3) ^ bg_swz(r))) * 2);
+        xv[q] = (uint32_t)((rr * ldx + 8 * slot_pos(r)) * 2);
     }
 #pragma unroll
-    for (int q = 0; q < WG; ++q) {
-        const int r = 16 * (WG * wave + q) + (lane >> 2);
+    for (int q = 0; q < WQ; ++q) {
+        const int r = slot_row(q, WQ);
         const int64_t rr = n0 + r < a.N ? r : a.N - 1 - n0;
-        wv[q] = (uint32_t)((rr * a.ldw + 8 * ((lane & 3) ^ bg_swz(r))) * 2);
+        wv[q] = (uint32_t)((rr * a.ldw + 8 * slot_pos(r)) * 2);
     }
     const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)((const uint16_t*)a.W + n0 * a.ldw),
                                                       (short)0, 0x7fffffff, kBufferDword3);
@@ -405,18 +423,18 @@ gemm_bf16_big_kernel(GemmArgs a) {
     // second input (k >= K1): its own row offsets and descriptors
     const bool dual = !GATHER && a.X2 != nullptr;
     const int64_t K1 = dual ? a.K1 : a.K;
-    uint32_t xv2[XG], wv2[WG];
+    uint32_t xv2[XQ], wv2[WQ];
 #pragma unroll
-    for (int q = 0; q < XG; ++q) {
-        const int r = 16 * (XG * wave + q) + (lane >> 2);
+    for (int q = 0; q < XQ; ++q) {
+        const int r = slot_row(q, XQ);
         const int64_t rr = m0 + r < a.M ? r : a.M - 1 - m0;
-        xv2[q] = dual ? (uint32_t)((rr * a.ldx2 + 8 * ((lane & 3) ^ bg_swz(r))) * 2) : 0u;
+        xv2[q] = dual ? (uint32_t)((rr * a.ldx2 + 8 * slot_pos(r)) * 2) : 0u;
     }
 #pragma unroll
-    for (int q = 0; q < WG; ++q) {
-        const int r = 16 * (WG * wave + q) + (lane >> 2);
+    for (int q = 0; q < WQ; ++q) {
+        const int r = slot_row(q, WQ);
         const int64_t rr = n0 + r < a.N ? r : a.N - 1 - n0;
-        wv2[q] = dual ? (uint32_t)((rr * a.ldw2 + 8 * ((lane & 3) ^ bg_swz(r))) * 2) : 0u;
+        wv2[q] = dual ? (uint32_t)((rr * a.ldw2 + 8 * slot_pos(r)) * 2) : 0u;
     }
     const auto rw2 = __builtin_amdgcn_make_buffer_rsrc(
         dual ? (void*)((const uint16_t*)a.W2 + n0 * a.ldw2) : (void*)nullptr, (short)0, 0x7fffffff,
@@ -427,6 +445,16 @@ gemm_bf16_big_kernel(GemmArgs a) {
     // the DMA requests of the stage holding k-tile k0 / C::BK, one instruction
     // per call of dma_one(q), q < DMA (so they can be spread over the MFMAs)
     auto dma_one = [&](int q, int64_t k0, uint16_t* Xs, uint16_t* Ws) {
+        if constexpr (FL) {
+            const bool second = k0 >= K1;           // uniform: K1 is a multiple of the stage k
+            const uint32_t sk = (uint32_t)((second ? k0 - K1 : k0) * 2);
+            if (q < XQ)
+                dma16(second ? rx2 : rx, Xs + 8 * (XQ * wave + q) * 64, second ? xv2[q] : xv[q], sk);
+            else
+                dma16(second ? rw2 : rw, Ws + 8 * (WQ * wave + q - XQ) * 64,
+                      second ? wv2[q - XQ] : wv[q - XQ], sk);
+            return;
+        }
         const int h = q / (XG + WG), p = q % (XG + WG);
         const int64_t k = k0 + 32 * h;
         const bool second = !GATHER && k >= K1;     // uniform: K1 is a multiple of the stage k
@@ -465,10 +493,21 @@ gemm_bf16_big_kernel(GemmArgs a) {
     // multiples of 16)
     const int fr = lane & 15, fc = lane >> 4;
     const int lo = fr * 32 + ((fc ^ bg_swz(fr)) << 3);
+    // full-line stages: k-step kk of row fr at chunk 4*kk + fc
+    const int lo8[2] = {fr * 64 + ((fc ^ bg_swz8(fr)) << 3), fr * 64 + (((4 + fc) ^ bg_swz8(fr)) << 3)};
     struct Frags {
         bf16x8 w[FI], x[FJ];
     };
     auto read = [&](Frags& f, const uint16_t* Xs, const uint16_t* Ws, int kk) {
+        if constexpr (FL) {
+#pragma unroll
+            for (int i = 0; i < FI; ++i)
+                f.w[i] = *reinterpret_cast<const bf16x8*>(&Ws[(wn * C::WTN + i * 16) * 64 + lo8[kk]]);
+#pragma unroll
+            for (int j = 0; j < FJ; ++j)
+                f.x[j] = *reinterpret_cast<const bf16x8*>(&Xs[(wm * C::WTM + j * 16) * 64 + lo8[kk]]);
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < FI; ++i)
             f.w[i] = *reinterpret_cast<const bf16x8*>(&Ws[kk * WH + (wn * C::WTN + i * 16) * 32 + lo]);
@@ -563,32 +602,35 @@ gemm_bf16_big_kernel(GemmArgs a) {
              F_{}, nk - NS + S);
     });
 
-    // epilogue: lane holds n = nb + 0..3 of row m for each (i, j).  Whole
-    // tiles take straight-line code with 8-byte stores (one variant per
-    // gate / residual combination, chosen once per block); edge tiles check
-    // every element.
+    // epilogue: output group gi = (i, j) holds the 4 consecutive columns
+    // gcol(gi) = ncol + 16i .. +3 of row grow(gi) = mrow + 16j; its bias
+    // operand depends on i only.  Whole tiles take straight-line code with
+    // 8-byte stores (one variant per gate / residual combination, chosen once
+    // per block); edge tiles check every element.
+    constexpr int NG = FI * FJ;
+    constexpr int NB = FI;
     const int64_t mrow = m0 + wm * C::WTM + (lane & 15);
     const int64_t ncol = n0 + wn * C::WTN + (lane >> 4) * 4;
+    auto scol = [&](int sl) -> int64_t { return ncol + 16 * sl; };
+    auto gslot = [&](int gi) -> int { return gi / FJ; };
+    auto gcol = [&](int gi) -> int64_t { return scol(gslot(gi)); };
+    auto grow = [&](int gi) -> int64_t { return mrow + 16 * (gi % FJ); };
+    auto gval = [&](int gi, int r) -> float { return acc[gi / FJ][gi % FJ][r]; };
     if (a.partial != nullptr) {
         // split-K: raw fp32 sums of this split, 16-byte stores where all four
         // columns are in range
         float* part = a.partial + split * a.M * a.ldp;
 #pragma unroll
-        for (int i = 0; i < FI; ++i) {
-            const int64_t nb = ncol + i * 16;
+        for (int gi = 0; gi < NG; ++gi) {
+            const int64_t nb = gcol(gi), m = grow(gi);
+            if (m >= a.M || nb >= a.N) continue;
+            float* po = part + m * a.ldp + nb;
+            if (nb + 3 < a.N && ((a.ldp | nb) & 3) == 0) {
+                *reinterpret_cast<float4*>(po) = make_float4(gval(gi, 0), gval(gi, 1), gval(gi, 2), gval(gi, 3));
+            } else {
 #pragma unroll
-            for (int j = 0; j < FJ; ++j) {
-                const int64_t m = mrow + j * 16;
-                if (m >= a.M || nb >= a.N) continue;
-                float* po = part + m * a.ldp + nb;
-                if (nb + 3 < a.N && ((a.ldp | nb) & 3) == 0) {
-                    *reinterpret_cast<float4*>(po) =
-                        make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        if (nb + r < a.N) po[r] = acc[i][j][r];
-                }
+                for (int r = 0; r < 4; ++r)
+                    if (nb + r < a.N) po[r] = gval(gi, r);
             }
         }
         return;
@@ -608,41 +650,35 @@ gemm_bf16_big_kernel(GemmArgs a) {
         constexpr bool GATE = decltype(gate_)::value, RES = decltype(res_)::value;
         // every operand of the wave's outputs requested before the first store
         // (an output may alias them as far as the compiler knows, so a load
-        // after a store would wait for it: one round trip per fragment)
-        float4 bv[FI];
-        uint2 gw[FI][FJ], rw[FI][FJ];
+        // after a store would wait for it: one round trip per group)
+        float4 bv[NB];
+        uint2 gw[NG], rw[NG];
 #pragma unroll
-        for (int i = 0; i < FI; ++i) {
-            const int64_t nb = ncol + i * 16;
-            bv[i] = a.bias != nullptr ? *reinterpret_cast<const float4*>(a.bias + nb)
-                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int sl = 0; sl < NB; ++sl)
+            bv[sl] = a.bias != nullptr ? *reinterpret_cast<const float4*>(a.bias + scol(sl))
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int j = 0; j < FJ; ++j) {
-                const int64_t e = (mrow + j * 16) * ldc + nb;
-                if constexpr (GATE) gw[i][j] = *reinterpret_cast<const uint2*>(gp + e);
-                if constexpr (RES) rw[i][j] = *reinterpret_cast<const uint2*>(rs + e);
-            }
+        for (int gi = 0; gi < NG; ++gi) {
+            const int64_t e = grow(gi) * ldc + gcol(gi);
+            if constexpr (GATE) gw[gi] = *reinterpret_cast<const uint2*>(gp + e);
+            if constexpr (RES) rw[gi] = *reinterpret_cast<const uint2*>(rs + e);
         }
 #pragma unroll
-        for (int i = 0; i < FI; ++i) {
-            const int64_t nb = ncol + i * 16;
-            const float bias4[4] = {bv[i].x, bv[i].y, bv[i].z, bv[i].w};
+        for (int gi = 0; gi < NG; ++gi) {
+            const int64_t e = grow(gi) * ldc + gcol(gi);
+            const float4 b4 = bv[gslot(gi)];
+            const float bias4[4] = {b4.x, b4.y, b4.z, b4.w};
+            float v[4], gv[4], rv[4];
+            if constexpr (GATE) bf4(gw[gi], gv);
+            if constexpr (RES) bf4(rw[gi], rv);
 #pragma unroll
-            for (int j = 0; j < FJ; ++j) {
-                const int64_t e = (mrow + j * 16) * ldc + nb;
-                float v[4], gv[4], rv[4];
-                if constexpr (GATE) bf4(gw[i][j], gv);
-                if constexpr (RES) bf4(rw[i][j], rv);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    v[r] = acc[i][j][r];
-                    if constexpr (GATE) v[r] *= 1.0f + a.gate_alpha * gv[r];
-                    v[r] += bias4[r];
-                    if constexpr (RES) v[r] += rv[r];
-                }
-                *reinterpret_cast<uint2*>(out + e) =
-                    make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+            for (int r = 0; r < 4; ++r) {
+                v[r] = gval(gi, r);
+                if constexpr (GATE) v[r] *= 1.0f + a.gate_alpha * gv[r];
+                v[r] += bias4[r];
+                if constexpr (RES) v[r] += rv[r];
             }
+            *reinterpret_cast<uint2*>(out + e) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
         }
     };
     if (whole) {
@@ -653,23 +689,18 @@ gemm_bf16_big_kernel(GemmArgs a) {
         return;
     }
 #pragma unroll
-    for (int i = 0; i < FI; ++i) {
-        const int64_t nb = ncol + i * 16;
-        if (nb >= a.N) continue;
+    for (int gi = 0; gi < NG; ++gi) {
+        const int64_t nb = gcol(gi), m = grow(gi);
+        if (nb >= a.N || m >= a.M) continue;
 #pragma unroll
-        for (int j = 0; j < FJ; ++j) {
-            const int64_t m = mrow + j * 16;
-            if (m >= a.M) continue;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (nb + r >= a.N) continue;
-                const int64_t e = m * ldc + nb + r;
-                float v = acc[i][j][r];
-                if (gp != nullptr) v *= 1.0f + a.gate_alpha * bf16_to_f32(gp[e]);
-                if (a.bias != nullptr) v += a.bias[nb + r];
-                if (rs != nullptr) v += bf16_to_f32(rs[e]);
-                out[e] = f32_to_bf16(v);
-            }
+        for (int r = 0; r < 4; ++r) {
+            if (nb + r >= a.N) continue;
+            const int64_t e = m * ldc + nb + r;
+            float v = gval(gi, r);
+            if (gp != nullptr) v *= 1.0f + a.gate_alpha * bf16_to_f32(gp[e]);
+            if (a.bias != nullptr) v += a.bias[nb + r];
+            if (rs != nullptr) v += bf16_to_f32(rs[e]);
+            out[e] = f32_to_bf16(v);
         }
     }
 }
