@@ -264,10 +264,15 @@ struct BgCfg {
     static constexpr int BK = 32 * KH;                         // k per stage
     static constexpr int WTM = BG_M / WGM, WTN = BG_N / (WAVES / WGM);   // wave sub-tile
     static constexpr int FJ = WTM / 16, FI = WTN / 16;         // x and w fragments per k-step
-    static constexpr int XG = BG_M / 16 / WAVES, WG = BG_N / 16 / WAVES;   // DMA row groups per wave
+    // DMA row groups per wave; W groups rounded up when BG_N / 16 does not
+    // divide over the waves (the groups past BG_N fetch an in-range row into a
+    // scratch LDS row nobody reads, so every wave issues the same count)
+    static constexpr int XG = BG_M / 16 / WAVES, WG = (BG_N / 16 + WAVES - 1) / WAVES;
+    static constexpr bool WPAD = WG * WAVES * 16 != BG_N;
     static constexpr int DMA = KH * (XG + WG);                 // DMA instructions per lane per stage
-    static constexpr int LDS = NS * KH * (BG_M + BG_N) * 32 * 2;
-    static_assert(WAVES % WGM == 0 && XG >= 1 && WG >= 1 && (KH == 1 || KH == 2), "big GEMM shape");
+    static constexpr int LDS = NS * KH * (BG_M + BG_N) * 32 * 2 + (WPAD ? 1024 : 0);
+    static_assert(WAVES % WGM == 0 && XG * WAVES * 16 == BG_M && WG >= 1 && (KH == 1 || KH == 2),
+                  "big GEMM shape");
     static_assert(NS >= 3 && NS <= 6 && (NS - 1) * DMA < 64 && LDS <= 160 * 1024, "big GEMM stages");
 };
 using BgConf = BgCfg<256, 128, 8, 4, 2, 2, 3>;
@@ -279,6 +284,10 @@ using BgConf = BgCfg<256, 128, 8, 4, 2, 2, 3>;
 // many-row products with N a multiple of 256
 using BgSmall = BgCfg<128, 128, 4, 2, 1, 2, 4>;
 using BgWide = BgCfg<128, 256, 8, 2, 2, 2, 3>;
+// 256 x 192 tiles (eight waves of 64 x 96, four 32-k stages): at M = 4096 and
+// N = 3072 they make 256 tiles, one round of the CUs, where 256 x 128 or
+// 128 x 256 make 384 (a round and a half)
+using BgTall = BgCfg<256, 192, 8, 4, 1, 2, 4>;
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 template <int N>
@@ -354,6 +363,8 @@ gemm_bf16_big_kernel(GemmArgs a) {
         X3[NS > 3 ? KH * XH : 8], X4[NS > 4 ? KH * XH : 8], X5[NS > 5 ? KH * XH : 8];
     __shared__ __attribute__((aligned(16))) uint16_t W0[KH * WH], W1[KH * WH], W2[KH * WH],
         W3[NS > 3 ? KH * WH : 8], W4[NS > 4 ? KH * WH : 8], W5[NS > 5 ? KH * WH : 8];
+    // landing rows of the padding W groups (BgCfg::WPAD), never read
+    __shared__ __attribute__((aligned(16))) uint16_t Wpad[C::WPAD ? 512 : 8];
     auto xs = [&](auto s_) -> uint16_t* {
         constexpr int S = decltype(s_)::value;
         if constexpr (S == 0) return X0; else if constexpr (S == 1) return X1;
@@ -451,8 +462,12 @@ gemm_bf16_big_kernel(GemmArgs a) {
             if (q < XQ)
                 dma16(second ? rx2 : rx, Xs + 8 * (XQ * wave + q) * 64, second ? xv2[q] : xv[q], sk);
             else
-                dma16(second ? rw2 : rw, Ws + 8 * (WQ * wave + q - XQ) * 64,
-                      second ? wv2[q - XQ] : wv[q - XQ], sk);
+            {
+                const int gw = WQ * wave + q - XQ;
+                uint16_t* dst = Ws + 8 * gw * 64;
+                if constexpr (C::WPAD) dst = 8 * gw < BG_N ? dst : Wpad;
+                dma16(second ? rw2 : rw, dst, second ? wv2[q - XQ] : wv[q - XQ], sk);
+            }
             return;
         }
         const int h = q / (XG + WG), p = q % (XG + WG);
@@ -473,8 +488,10 @@ gemm_bf16_big_kernel(GemmArgs a) {
             dma16(rxh, Xs + h * XH + 16 * (XG * wave + p) * 32, second ? xv2[p] : xv[p], sx);
         } else {
             const int w = p - XG;
-            dma16(second ? rw2 : rw, Ws + h * WH + 16 * (WG * wave + w) * 32, second ? wv2[w] : wv[w],
-                  sk);
+            const int gw = WG * wave + w;
+            uint16_t* dst = Ws + h * WH + 16 * gw * 32;
+            if constexpr (C::WPAD) dst = 16 * gw < BG_N ? dst : Wpad;
+            dma16(second ? rw2 : rw, dst, second ? wv2[w] : wv[w], sk);
         }
     };
     auto issue = [&](int64_t k0, uint16_t* Xs, uint16_t* Ws) {
@@ -1345,7 +1362,7 @@ static void launch_skinny(const GemmArgs& a, dim3 grid, hipStream_t st) {
 //     73.5-74.0 ms (same box, alternating runs).
 // K must fill whole rounds of the configuration's stages; gather tiles must
 // not straddle a q-head group (Hq % BG_N == 0).
-enum BigTile { kBigNone, kBigStd, kBigSmall, kBigWide };
+enum BigTile { kBigNone, kBigStd, kBigSmall, kBigWide, kBigTall };
 template <class C>
 static bool big_fits(int64_t M, int64_t K, bool gather, int64_t Hq) {
     return M >= C::BG_M && K % (C::NS * C::BK) == 0 && (!gather || Hq % C::BG_N == 0);
@@ -1357,6 +1374,11 @@ static BigTile big_tile(int64_t M, int64_t N, int64_t K, bool gather, int64_t Hq
     if (!std_ok) return small_ok ? kBigSmall : (wide_ok ? kBigWide : kBigNone);
     const int64_t c = device_cus();
     const int64_t t = ceil_div(M, BgConf::BG_M) * ceil_div(N, BgConf::BG_N);
+    // rounds of the CUs times the work of a tile (in 256 x 64 units): 256 x 192
+    // where it takes fewer
+    const bool tall_ok = N % BgTall::BG_N == 0 && big_fits<BgTall>(M, K, gather, Hq);
+    const int64_t tt = ceil_div(M, BgTall::BG_M) * (N / BgTall::BG_N);
+    if (tall_ok && ceil_div(tt, c) * 3 < ceil_div(t, c) * 2) return kBigTall;
     if (wide_ok && 4 * t >= 3 * c) return kBigWide;
     return kBigStd;
 }
@@ -1370,9 +1392,11 @@ static void launch_big(const GemmArgs& a, BigTile tile, int64_t nsplit, hipStrea
     if (tile == kBigSmall) launch_big_cfg<GATHER, BgSmall>(a, nsplit, st);
     else if constexpr (!GATHER) {
         if (tile == kBigWide) launch_big_cfg<GATHER, BgWide>(a, nsplit, st);
+        else if (tile == kBigTall) launch_big_cfg<GATHER, BgTall>(a, nsplit, st);
         else launch_big_cfg<GATHER, BgConf>(a, nsplit, st);
     } else {
-        launch_big_cfg<GATHER, BgConf>(a, nsplit, st);
+        if (tile == kBigTall) launch_big_cfg<GATHER, BgTall>(a, nsplit, st);
+        else launch_big_cfg<GATHER, BgConf>(a, nsplit, st);
     }
 }
 
@@ -1766,6 +1790,9 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
         } else if (tile == kBigWide) {
             bm = BgWide::BG_M; bn = BgWide::BG_N; stage_k = BgWide::NS * BgWide::BK;
             half_k = BgWide::BK;
+        } else if (tile == kBigTall) {
+            bm = BgTall::BG_M; bn = BgTall::BG_N; stage_k = BgTall::NS * BgTall::BK;
+            half_k = BgTall::BK;
         }
         const int64_t tiles = ceil_div(d->m, bm) * ceil_div(g.n, bn);
         int64_t ns = 0, best = 0;

@@ -195,11 +195,13 @@ def test_golden_phase_and_pvpowlu_vs_reference():
 @pytest.mark.parametrize("M,N,K", [(1, 16, 8), (37, 100, 72), (32, 3072, 768), (130, 768, 3072),
                                    (256, 256, 1152), (5, 4096, 768), (3, 768, 3072), (8, 1000, 772),
                                    # the large-M MFMA tiles: 256 x 128 (ragged), 128 x 256
-                                   # (N % 256 == 0, ragged rows) and 128 x 128 (fewer than
-                                   # 256 rows, or K not a multiple of 192)
+                                   # (N % 256 == 0, ragged rows), 128 x 128 (fewer than
+                                   # 256 rows, or K not a multiple of 192) and 256 x 192
+                                   # (N % 192 == 0 where it takes fewer rounds, ragged rows)
                                    (8229, 3000, 768), (6000, 1536, 1152), (4100, 770, 3072),
                                    (4096, 1152, 768), (8192, 768, 3072), (4000, 1536, 768),
-                                   (200, 384, 1024), (1000, 640, 512)])
+                                   (200, 384, 1024), (1000, 640, 512), (4096, 3072, 768),
+                                   (4000, 3072, 1152)])
 def test_linear(dtype, M, N, K):
     from loom_amd import ops
     g = gen(M * 7 + N + K)
@@ -220,7 +222,9 @@ def test_linear(dtype, M, N, K):
                                                  (8, 96, 384, 300, "head"), (4, 8, 32, 6, "open"),
                                                  (8, 96, 384, 20, "open"), (8, 96, 384, 8200, "head"),
                                                  (8, 96, 384, 600, "open"), (8, 96, 384, 1, "head"),
-                                                 (4, 8, 32, 3, "open"), (8, 96, 384, 8192, "head")])
+                                                 (4, 8, 32, 3, "open"), (8, 96, 384, 8192, "head"),
+                                                 # 256 x 192 tiles (whole and ragged rows)
+                                                 (8, 96, 384, 4096, "head"), (8, 96, 384, 4000, "open")])
 def test_beta_forward(dtype, QH, HD, Hq, M, sectors):
     from loom_amd import ops
     N, H = QH * HD, QH * Hq
