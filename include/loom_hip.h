@@ -439,7 +439,9 @@ int loom_tria_chunked_forward_fires(int dtype, const void* r, const void* i, con
  * appends (k_roped, v) at rows start.. of the caches (strides as in
  * loom_gqa_decode_step; cache_len = their capacity in positions), then
  * attends token t to cache rows 0..start+t.
- *   qkv: rows (b,t) of [q | k | v] ((QH + 2 KVH) HD) at qkv_ld elements apart;
+ *   qkv: rows (b,t) of [q | k | v] ((QH + 2 KVH) HD) at qkv_ld elements apart,
+ *   or NULL: then q_out already holds the chunk's roped q and the caches its
+ *   rows (loom_prefill_qkv wrote them), and only the attention runs;
  *   c_out, kctx_out: rows (b,t) of QH*HD at out_ld elements apart.
  * No counterpart in the reference (its chunked forward uses SDPA per chunk). */
 int loom_gqa_prefill(int dtype, const void* qkv, int64_t qkv_ld, void* k_cache, void* v_cache,
@@ -447,6 +449,24 @@ int loom_gqa_prefill(int dtype, const void* qkv, int64_t qkv_ld, void* k_cache, 
                      const float* cos_table, const float* sin_table, void* q_out, void* c_out,
                      void* kctx_out, int64_t out_ld, int64_t B, int64_t T, int64_t start,
                      int64_t cache_len, int64_t QH, int64_t KVH, int64_t HD, void* stream);
+
+/* The chunked prefill's projections of one hidden state x [B*T, K] (row
+ * stride ldx) for the next block: qkv = x w_qkv^T (the block's
+ * GroupedQueryCausalSelfAttention qkv Linear, loomformer.py:3262), then
+ * loom_gqa_prefill's RoPE + cache append of the chunk (q_out, caches, tables
+ * and strides as there), and, with w_hist set, the depth history slot's
+ * projection hist_out = x w_hist^T (DepthAttn.project, loomformer.py:3397;
+ * n_hist columns at hist_ld elements apart).  Weights are [rows, K] dense.
+ * Follow it with loom_gqa_prefill(qkv = NULL).  bf16 with head_dim 96 and at
+ * least 256 rows runs as one launch that never stores qkv; other shapes use
+ * qkv_scratch ([B*T, (QH + 2 KVH) HD]) and a separate RoPE + append launch.
+ * No counterpart in the reference. */
+int loom_prefill_qkv(int dtype, const void* x, int64_t ldx, const void* w_qkv, const void* w_hist,
+                     void* hist_out, int64_t hist_ld, int64_t n_hist, void* qkv_scratch, void* q_out,
+                     void* k_cache, void* v_cache, int64_t cache_stride_b, int64_t cache_stride_t,
+                     int64_t cache_stride_h, const float* cos_table, const float* sin_table,
+                     int64_t B, int64_t T, int64_t start, int64_t cache_len, int64_t K, int64_t QH,
+                     int64_t KVH, int64_t HD, void* stream);
 
 /* Sparse final cross-attention: per row (b,t) a masked softmax over K keys
  * (scale * q.k), out = sum_j w_j v_j, an all-masked row gives exact zeros and

@@ -29,6 +29,9 @@ namespace loom {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+__device__ __forceinline__ float bf(uint16_t x) { return bf16_to_f32(x); }
+__device__ __forceinline__ float round_bf(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
 struct GemmArgs {
     const void* X;
     int64_t ldx;
@@ -58,6 +61,32 @@ struct GemmArgs {
     float* partial;
     int64_t ldp;
     int nsplit;
+    // big kernel only (not gather, no gate or residual): columns N1 .. N-1 of
+    // the launch are a second product of the same X with weight rows Wb
+    // (stride ldwb), written to outb (stride ldcb) with bias biasb, so two
+    // projections of one activation share a launch; tiles never straddle N1
+    // (N1 0: one product)
+    int64_t N1;
+    const void* Wb;
+    int64_t ldwb;
+    void* outb;
+    int64_t ldcb;
+    const float* biasb;
+    // big kernel with 96-column wave tiles only: the first product's columns
+    // are the heads [q (QH) | k (KVH) | v (KVH)] of 96; with rope.q set its
+    // epilogue applies RoPE to q and k and writes q to rope.q ([M, QH*96]),
+    // k and v into the caches at position start + m % Tc of row b = m / Tc,
+    // instead of writing out
+    struct RopeOut {
+        void* q;
+        void* kc;
+        void* vc;
+        int64_t csb, cst, csh;     // cache strides (elements) of b, t and kv head
+        const float* cosv;         // [*, 96] fp32 tables (attention factor folded in)
+        const float* sinv;
+        int64_t Tc, start;
+        int QH, KVH;
+    } rope;
 };
 
 // Element offset of packed column kk of group g, and which source it is in.
@@ -399,8 +428,19 @@ gemm_bf16_big_kernel(GemmArgs a) {
         mt = b / NT;
         nt = b % NT;
     }
-    const int64_t n0 = nt * BG_N;
+    int64_t n0 = nt * BG_N;
     const int64_t m0 = mt * BG_M;
+    bool seg_b = false;
+    if (!GATHER && a.N1 > 0) {               // block-uniform: this tile's product
+        if (n0 >= a.N1) {
+            seg_b = true;
+            n0 -= a.N1;
+            a.N -= a.N1;
+            a.W = a.Wb; a.ldw = a.ldwb; a.out = a.outb; a.ldc = a.ldcb; a.bias = a.biasb;
+        } else {
+            a.N = a.N1;
+        }
+    }
     const int64_t g = GATHER ? n0 / a.Hq : 0;
     const int64_t ldx = GATHER ? a.Nm : a.ldx;
 
@@ -633,6 +673,55 @@ gemm_bf16_big_kernel(GemmArgs a) {
     auto gcol = [&](int gi) -> int64_t { return scol(gslot(gi)); };
     auto grow = [&](int gi) -> int64_t { return mrow + 16 * (gi % FJ); };
     auto gval = [&](int gi, int r) -> float { return acc[gi / FJ][gi % FJ][r]; };
+    if constexpr (!GATHER && C::WTN == 96) {
+        if (a.rope.q != nullptr && !seg_b) {
+            // the wave's 96 columns are one head; column d's rotation partner
+            // d +- 48 sits in fragment i +- 3 of the same lane and register.
+            // As the unfused path: the product rounded to bf16, then
+            // fma(x, cos, (sign * partner) * sin), rounded on the store
+            const GemmArgs::RopeOut& ro = a.rope;
+            const int hd = (int)((n0 + wn * 96) / 96);
+            const int dl = (lane >> 4) * 4;
+            const bool rot = hd < ro.QH + ro.KVH;
+#pragma unroll
+            for (int j = 0; j < FJ; ++j) {
+                const int64_t m = mrow + 16 * j;
+                if (m >= a.M) continue;
+                const int64_t b = m / ro.Tc, pos = ro.start + (m - b * ro.Tc);
+                uint16_t* dst;
+                if (hd < ro.QH)
+                    dst = (uint16_t*)ro.q + m * (int64_t)(ro.QH * 96) + hd * 96;
+                else if (rot)
+                    dst = (uint16_t*)ro.kc + b * ro.csb + pos * ro.cst + (hd - ro.QH) * ro.csh;
+                else
+                    dst = (uint16_t*)ro.vc + b * ro.csb + pos * ro.cst + (hd - ro.QH - ro.KVH) * ro.csh;
+                float4 cv[FI], sv[FI];
+#pragma unroll
+                for (int i = 0; i < FI; ++i) {
+                    cv[i] = rot ? *reinterpret_cast<const float4*>(ro.cosv + pos * 96 + 16 * i + dl)
+                                : make_float4(1.f, 1.f, 1.f, 1.f);
+                    sv[i] = rot ? *reinterpret_cast<const float4*>(ro.sinv + pos * 96 + 16 * i + dl)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+                for (int i = 0; i < FI; ++i) {
+                    const int ip = i < 3 ? i + 3 : i - 3;
+                    const float sg = i < 3 ? -1.0f : 1.0f;
+                    const float c4[4] = {cv[i].x, cv[i].y, cv[i].z, cv[i].w};
+                    const float s4[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+                    float v[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float x = round_bf(acc[i][j][r]), y = round_bf(acc[ip][j][r]);
+                        v[r] = rot ? fmaf(x, c4[r], (sg * y) * s4[r]) : x;
+                    }
+                    *reinterpret_cast<uint2*>(dst + 16 * i + dl) =
+                        make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                }
+            }
+            return;
+        }
+    }
     if (a.partial != nullptr) {
         // split-K: raw fp32 sums of this split, 16-byte stores where all four
         // columns are in range
@@ -870,8 +959,6 @@ struct FfnArgs {
     const float* dpl;
 };
 
-__device__ __forceinline__ float bf(uint16_t x) { return bf16_to_f32(x); }
-__device__ __forceinline__ float round_bf(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
 // cp: the carried (or seed) record of element e, loaded by the caller with
 // the rest of the epilogue's operands; used when carry_in is set.
@@ -1382,6 +1469,10 @@ static BigTile big_tile(int64_t M, int64_t N, int64_t K, bool gather, int64_t Hq
     if (wide_ok && 4 * t >= 3 * c) return kBigWide;
     return kBigStd;
 }
+static int64_t big_tile_n(BigTile t) {
+    return t == kBigSmall ? BgSmall::BG_N : t == kBigWide ? BgWide::BG_N : t == kBigTall ? BgTall::BG_N
+                                                                                       : BgConf::BG_N;
+}
 template <bool GATHER, class C>
 static void launch_big_cfg(const GemmArgs& a, int64_t nsplit, hipStream_t st) {
     const dim3 grid((unsigned)(ceil_div(a.N, C::BG_N) * ceil_div(a.M, C::BG_M) * nsplit));
@@ -1589,6 +1680,25 @@ static int linear_multi_dispatch(const loom_linear_multi_desc& d, hipStream_t st
         const int64_t steps = ceil_div(d.k, 32) + ceil_div(d.k2, 32);
         launch_skinny_multi(a, grid, (int)ceil_div(d.m, 16), steps, st);
         return launch_status("loom_linear_multi");
+    }
+    if (std::is_same<T, bf16_t>::value && d.nseg == 2 && d.k2 == 0 && d.m > 64) {
+        // two single-input segments on the DMA-staged tiles: one launch when the
+        // first segment ends on a tile boundary
+        const loom_linear_segment& g0 = d.seg[0];
+        const loom_linear_segment& g1 = d.seg[1];
+        bool ok = g0.gate_p == nullptr && g1.gate_p == nullptr && d.k % 8 == 0 && d.ldx % 8 == 0 &&
+                  ((uintptr_t)d.x & 15) == 0 && g0.ldw % 8 == 0 && g1.ldw % 8 == 0 &&
+                  (((uintptr_t)g0.w | (uintptr_t)g1.w) & 15) == 0;
+        const BigTile tile = ok ? big_tile(d.m, g0.n + g1.n, d.k, false, 0) : kBigNone;
+        if (tile != kBigNone && g0.n % big_tile_n(tile) == 0) {
+            GemmArgs a{};
+            a.X = d.x; a.ldx = d.ldx; a.W = g0.w; a.ldw = g0.ldw; a.out = g0.out; a.ldc = g0.ldc;
+            a.bias = g0.bias;
+            a.M = d.m; a.N = g0.n + g1.n; a.K = d.k;
+            a.N1 = g0.n; a.Wb = g1.w; a.ldwb = g1.ldw; a.outb = g1.out; a.ldcb = g1.ldc; a.biasb = g1.bias;
+            launch_big<false>(a, tile, 1, st);
+            return launch_status("loom_linear_multi");
+        }
     }
     for (int s = 0; s < d.nseg; ++s) {
         const loom_linear_segment& g = d.seg[s];
@@ -2019,4 +2129,69 @@ extern "C" int loom_beta_forward(int dtype, const void* u, const void* q_h, cons
     }
     set_error("beta_space: unsupported dtype %d", dtype);
     return LOOM_ERR_INVALID;
+}
+
+// The chunked prefill's projections of one hidden state for the next block:
+// qkv = x w_qkv^T, then RoPE of q and k and the cache append of k and v
+// (as loom_gqa_prefill's first step), and optionally the history projection
+// hist_out = x w_hist^T.  bf16 with 96-wide heads and at least 256 rows: one
+// launch of 256 x 192 tiles, the RoPE and the cache stores in its epilogue
+// (each wave's 96 columns are one head) and the history columns as a second
+// product of the same launch; qkv is never stored.  Otherwise the two
+// products into qkv_scratch / hist_out and the separate RoPE + append launch.
+extern "C" int loom_prefill_qkv(int dtype, const void* x, int64_t ldx, const void* w_qkv,
+                                const void* w_hist, void* hist_out, int64_t hist_ld, int64_t n_hist,
+                                void* qkv_scratch, void* q_out, void* k_cache, void* v_cache,
+                                int64_t cache_stride_b, int64_t cache_stride_t,
+                                int64_t cache_stride_h, const float* cos_table,
+                                const float* sin_table, int64_t B, int64_t T, int64_t start,
+                                int64_t cache_len, int64_t K, int64_t QH, int64_t KVH, int64_t HD,
+                                void* stream) {
+    clear_error();
+    LOOM_CHECK(x && w_qkv && qkv_scratch && q_out && k_cache && v_cache && cos_table && sin_table,
+               "prefill_qkv: null argument");
+    LOOM_CHECK(w_hist == nullptr || (hist_out != nullptr && n_hist >= 1 && hist_ld >= n_hist),
+               "prefill_qkv: history projection without output or width");
+    LOOM_CHECK(B >= 0 && T >= 0 && start >= 0 && K >= 1 && ldx >= K && KVH >= 1 && QH % KVH == 0 &&
+                   HD >= 2 && HD % 2 == 0,
+               "prefill_qkv: bad shape B=%lld T=%lld K=%lld QH=%lld KVH=%lld HD=%lld", (long long)B,
+               (long long)T, (long long)K, (long long)QH, (long long)KVH, (long long)HD);
+    LOOM_CHECK(cache_stride_t >= HD && cache_stride_h >= HD, "prefill_qkv: cache strides smaller than a head row");
+    LOOM_CHECK(start + T <= cache_len && start + T < (1LL << 31),
+               "prefill_qkv: positions %lld..%lld beyond the cache capacity %lld", (long long)start,
+               (long long)(start + T - 1), (long long)cache_len);
+    const int64_t M = B * T, QKV = (QH + 2 * KVH) * HD;
+    if (M == 0) return LOOM_OK;
+    hipStream_t st = (hipStream_t)stream;
+    const uintptr_t a16 = (uintptr_t)x | (uintptr_t)w_qkv | (uintptr_t)w_hist | (uintptr_t)cos_table |
+                          (uintptr_t)sin_table;
+    const uintptr_t a8 = (uintptr_t)q_out | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)hist_out;
+    const bool fused = dtype == LOOM_BF16 && HD == 96 && QKV % BgTall::BG_N == 0 &&
+                       big_fits<BgTall>(M, K, false, 0) && K % 8 == 0 && ldx % 8 == 0 &&
+                       (a16 & 15) == 0 && (a8 & 7) == 0 && cache_stride_b % 4 == 0 &&
+                       cache_stride_t % 4 == 0 && cache_stride_h % 4 == 0 &&
+                       (w_hist == nullptr || hist_ld % 4 == 0);
+    if (fused) {
+        GemmArgs a{};
+        a.X = x; a.ldx = ldx; a.W = w_qkv; a.ldw = K; a.out = qkv_scratch; a.ldc = QKV;
+        a.M = M; a.N = QKV + (w_hist != nullptr ? n_hist : 0); a.K = K;
+        if (w_hist != nullptr) {
+            a.N1 = QKV; a.Wb = w_hist; a.ldwb = K; a.outb = hist_out; a.ldcb = hist_ld;
+        }
+        a.rope = GemmArgs::RopeOut{q_out, k_cache, v_cache, cache_stride_b, cache_stride_t,
+                                   cache_stride_h, cos_table, sin_table, T, start, (int)QH, (int)KVH};
+        launch_big_cfg<false, BgTall>(a, 1, st);
+        return launch_status("loom_prefill_qkv");
+    }
+    int rc = loom_linear(dtype, x, ldx, w_qkv, K, nullptr, nullptr, 0.0f, nullptr, qkv_scratch, QKV, M,
+                         QKV, K, stream);
+    if (rc != LOOM_OK) return rc;
+    if (w_hist != nullptr) {
+        rc = loom_linear(dtype, x, ldx, w_hist, K, nullptr, nullptr, 0.0f, nullptr, hist_out, hist_ld, M,
+                         n_hist, K, stream);
+        if (rc != LOOM_OK) return rc;
+    }
+    return prefill_rope_append(dtype, qkv_scratch, QKV, k_cache, v_cache, cache_stride_b,
+                               cache_stride_t, cache_stride_h, cos_table, sin_table, q_out, B, T, start,
+                               QH, KVH, HD, st);
 }

@@ -22,6 +22,13 @@ int launch_status(const char* what);
 // compute units of the current device; threads of `kernel` it keeps resident
 int device_cus();
 int64_t resident_threads(const void* kernel, int block);
+// the chunked prefill's RoPE + cache append of a qkv chunk (prefill.hip):
+// q_out [B*Tc, QH*HD] roped, k roped and v into the caches at positions
+// start .. start + Tc - 1
+int prefill_rope_append(int dtype, const void* qkv, int64_t qkv_ld, void* kc, void* vc,
+                        int64_t csb, int64_t cst, int64_t csh, const float* cosv,
+                        const float* sinv, void* q_out, int64_t B, int64_t Tc, int64_t start,
+                        int64_t QH, int64_t KVH, int64_t HD, hipStream_t st);
 
 #define LOOM_CHECK(cond, ...)            \
     do {                                 \

@@ -519,12 +519,13 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     }
 }
 
+// RoPE of the chunk's q and k rows of qkv into q_out and the k cache, v into
+// the v cache (positions start .. start + Tc - 1 of every row b).
 template <typename T>
-static int prefill_dispatch(const void* qkv, int64_t qkv_ld, void* kc, void* vc, int64_t csb,
-                            int64_t cst, int64_t csh, const float* cosv, const float* sinv,
-                            void* q_out, void* c_out, void* k_out, int64_t out_ld, int64_t B,
-                            int64_t Tc, int64_t start, int64_t QH, int64_t KVH, int64_t HD,
-                            hipStream_t st) {
+static int rope_append_dispatch(const void* qkv, int64_t qkv_ld, void* kc, void* vc, int64_t csb,
+                                int64_t cst, int64_t csh, const float* cosv, const float* sinv,
+                                void* q_out, int64_t B, int64_t Tc, int64_t start, int64_t QH,
+                                int64_t KVH, int64_t HD, hipStream_t st) {
     const int64_t total = B * Tc * (QH + 2 * KVH) * HD;
     // 16-byte groups: every row base and stride a multiple of 8 elements
     // (16 bytes for 16-bit types, 32 for fp32) and 16-byte aligned pointers
@@ -541,8 +542,40 @@ static int prefill_dispatch(const void* qkv, int64_t qkv_ld, void* kc, void* vc,
         hipLaunchKernelGGL((prefill_rope_append_kernel<T>), dim3((unsigned)ceil_div(total, 256)),
                            dim3(256), 0, st, (const T*)qkv, qkv_ld, (T*)q_out, (T*)kc, (T*)vc, cosv,
                            sinv, B, Tc, start, (int)QH, (int)KVH, (int)HD, csb, cst, csh);
-    int rc = launch_status("loom_gqa_prefill (rope/append)");
-    if (rc != LOOM_OK) return rc;
+    return launch_status("loom_gqa_prefill (rope/append)");
+}
+
+int prefill_rope_append(int dtype, const void* qkv, int64_t qkv_ld, void* kc, void* vc,
+                        int64_t csb, int64_t cst, int64_t csh, const float* cosv,
+                        const float* sinv, void* q_out, int64_t B, int64_t Tc, int64_t start,
+                        int64_t QH, int64_t KVH, int64_t HD, hipStream_t st) {
+    switch (dtype) {
+        case LOOM_F32:
+            return rope_append_dispatch<float>(qkv, qkv_ld, kc, vc, csb, cst, csh, cosv, sinv, q_out,
+                                               B, Tc, start, QH, KVH, HD, st);
+        case LOOM_BF16:
+            return rope_append_dispatch<bf16_t>(qkv, qkv_ld, kc, vc, csb, cst, csh, cosv, sinv, q_out,
+                                                B, Tc, start, QH, KVH, HD, st);
+        case LOOM_F16:
+            return rope_append_dispatch<f16_t>(qkv, qkv_ld, kc, vc, csb, cst, csh, cosv, sinv, q_out,
+                                               B, Tc, start, QH, KVH, HD, st);
+    }
+    set_error("prefill rope/append: unsupported dtype %d", dtype);
+    return LOOM_ERR_INVALID;
+}
+
+// qkv null: q_out already holds the chunk's roped q and the caches its rows
+template <typename T>
+static int prefill_dispatch(const void* qkv, int64_t qkv_ld, void* kc, void* vc, int64_t csb,
+                            int64_t cst, int64_t csh, const float* cosv, const float* sinv,
+                            void* q_out, void* c_out, void* k_out, int64_t out_ld, int64_t B,
+                            int64_t Tc, int64_t start, int64_t QH, int64_t KVH, int64_t HD,
+                            hipStream_t st) {
+    if (qkv != nullptr) {
+        const int rc = rope_append_dispatch<T>(qkv, qkv_ld, kc, vc, csb, cst, csh, cosv, sinv, q_out,
+                                               B, Tc, start, QH, KVH, HD, st);
+        if (rc != LOOM_OK) return rc;
+    }
     PrefillArgs<T> a{};
     a.q = (const T*)q_out;
     a.kc = (const T*)kc;
@@ -615,13 +648,13 @@ extern "C" int loom_gqa_prefill(int dtype, const void* qkv, int64_t qkv_ld, void
                                 int64_t cache_len, int64_t QH, int64_t KVH, int64_t HD,
                                 void* stream) {
     clear_error();
-    LOOM_CHECK(qkv && k_cache && v_cache && cos_table && sin_table && q_out && c_out && kctx_out,
+    LOOM_CHECK(k_cache && v_cache && cos_table && sin_table && q_out && c_out && kctx_out,
                "gqa_prefill: null argument");
     LOOM_CHECK(B >= 0 && T >= 0 && start >= 0 && KVH >= 1 && QH % KVH == 0 && HD % 2 == 0,
                "gqa_prefill: bad shape B=%lld T=%lld start=%lld QH=%lld KVH=%lld HD=%lld",
                (long long)B, (long long)T, (long long)start, (long long)QH, (long long)KVH,
                (long long)HD);
-    LOOM_CHECK(qkv_ld >= (QH + 2 * KVH) * HD && out_ld >= QH * HD,
+    LOOM_CHECK((qkv == nullptr || qkv_ld >= (QH + 2 * KVH) * HD) && out_ld >= QH * HD,
                "gqa_prefill: row strides smaller than the rows");
     LOOM_CHECK(cache_stride_t >= HD && cache_stride_h >= HD,
                "gqa_prefill: cache strides smaller than a head row");

@@ -13,7 +13,7 @@ from ctypes import c_float, c_int, c_int64, c_void_p
 import torch
 
 # descriptor layouts and signatures below are those of loom_abi_version() == 5
-ABI_VERSION = 7
+ABI_VERSION = 8
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libloom_hip.so")
 
 _P = c_void_p
@@ -85,6 +85,9 @@ SIGNATURES = {
     "loom_gqa_decode_step_noalloc": [c_int, _P, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P,
                                      _P, c_int64, c_int64, c_int64, _P, c_int64, c_int64, c_int64,
                                      _P],
+    "loom_prefill_qkv": [c_int, _P, c_int64, _P, _P, _P, c_int64, c_int64, _P, _P, _P, _P, c_int64,
+                         c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64,
+                         c_int64, c_int64, c_int64, _P],
     "loom_gqa_prefill": [c_int, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, _P, _P, _P, _P,
                          _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
                          c_int64, _P],

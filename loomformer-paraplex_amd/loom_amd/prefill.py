@@ -131,20 +131,34 @@ def prefill(eng, prompt: torch.Tensor) -> None:
 
     gathered = torch.cuda.Event()
 
+    def next_qkv(x, bi, sub, s_, Tc_):
+        """Block bi's qkv of x with RoPE + cache append (loomformer.py:3262, :3300-3320)
+        and, unless sub is None, history slot `sub` (DepthAttn.project, :3397): one
+        launch where the shapes allow, on the current stream; the attention then runs
+        with qkv = NULL."""
+        wh = None if sub is None else _P(eng.kvw)
+        ho = None if sub is None else _P(hist[:, sub])
+        call("loom_prefill_qkv", code, _P(x), N, _P(eng.blocks[bi]["qkv"]), wh, ho, 2 * L * 2 * N,
+             2 * N, _P(qkv), _P(q), _P(eng.k_cache[bi]), _P(eng.v_cache[bi]), cache_sb, cache_st,
+             cache_sh, _P(eng.cos), _P(eng.sin), B, Tc_, s_, eng.max_len, N, QH, KVH, HD,
+             eng._stream())
+
+    def attend(bi, s_, Tc_):
+        call("loom_gqa_prefill", code, None, 0, _P(eng.k_cache[bi]), _P(eng.v_cache[bi]),
+             cache_sb, cache_st, cache_sh, _P(eng.cos), _P(eng.sin), _P(q), _P(cbuf), _P(kctx), N,
+             B, Tc_, s_, eng.max_len, QH, KVH, HD, eng._stream())
+
     def chunk_head(ci):
         """Layer 0's attention inputs of chunk ci, which need only the chunk's
-        tokens and the layer-0 K/V rows of earlier chunks: embeddings, qkv,
-        RoPE + cache append + attention (on the current stream; `gathered` is
-        recorded once the embeddings are in h0)."""
+        tokens and the layer-0 K/V rows of earlier chunks: embeddings, qkv with
+        RoPE + cache append and history slot 0, attention (on the current stream;
+        `gathered` is recorded once history slot 0 is written)."""
         s_, e_ = spans[ci]
         rows_ = B * (e_ - s_ + 1)
         torch.index_select(eng.emb, 0, prompt_d[:, s_:e_ + 1].reshape(-1), out=h0[:rows_])
+        next_qkv(h0, 0, 0, s_, e_ - s_ + 1)
         gathered.record()
-        lin(h0, eng.blocks[0]["qkv"], qkv, rows_, N + 2 * c.KV, N)
-        call("loom_gqa_prefill", code, _P(qkv), N + 2 * c.KV, _P(eng.k_cache[0]),
-             _P(eng.v_cache[0]), cache_sb, cache_st, cache_sh, _P(eng.cos), _P(eng.sin),
-             _P(q), _P(cbuf), _P(kctx), N, B, e_ - s_ + 1, s_, eng.max_len, QH, KVH, HD,
-             eng._stream())
+        attend(0, s_, e_ - s_ + 1)
 
     main = torch.cuda.current_stream(dev)
     aux = eng.aux_stream
@@ -176,10 +190,8 @@ def prefill(eng, prompt: torch.Tensor) -> None:
         rows = B * Tc
         hv = hist[:rows]
         sub = 0
-        # history slot 0 of the chunk and its depth read, on main once the
-        # embeddings are gathered
+        # the depth read of history slot 0, on main once the slot is written
         main.wait_event(gathered)
-        lin(h0, eng.kvw, hv[:, 0], rows, 2 * N, N, ldc=2 * L * 2 * N)
         depth(0, d, rows)
         carry_i, p_i = None, None
         for bi, blk in enumerate(eng.blocks):
@@ -189,10 +201,7 @@ def prefill(eng, prompt: torch.Tensor) -> None:
             # ran ahead on aux)
             if bi > 0:
                 with torch.cuda.stream(aux):
-                    call("loom_gqa_prefill", code, _P(qkv), N + 2 * c.KV, _P(eng.k_cache[bi]),
-                         _P(eng.v_cache[bi]), cache_sb, cache_st, cache_sh, _P(eng.cos),
-                         _P(eng.sin), _P(q), _P(cbuf), _P(kctx), N, B, Tc, s, eng.max_len, QH,
-                         KVH, HD, eng._stream())
+                    attend(bi, s, Tc)
                 depth(sub, d, rows)
             join()
             # ---- LN(o(C) + w_o(depth read 2*bi)) (loomformer.py:3999-4000)
@@ -249,11 +258,12 @@ def prefill(eng, prompt: torch.Tensor) -> None:
             lin_ln(("ffn", bi), dh, eng.wo_for(sub), act, blk["w2"], blk["b2"], blk["ln2_w"],
                    blk["ln2_b"], rows)
             if not last:
-                # next history slot (main) and the next block's qkv (aux)
+                # history slot 2*bi+2 (loomformer.py:4050) on main, the next block's
+                # qkv with RoPE + cache append on aux (its attention follows there)
                 sub += 1
                 fork()
                 with torch.cuda.stream(aux):
-                    lin(h, eng.blocks[bi + 1]["qkv"], qkv, rows, N + 2 * c.KV, N)
+                    next_qkv(h, bi + 1, None, s, Tc)
                 lin(h, eng.kvw, hv[:, sub], rows, 2 * N, N, ldc=2 * L * 2 * N)
         # ---- on the third stream, beside the next chunk's first sublayer: the
         # temporal carry over the chunk, restarting at position 0 and at a

@@ -180,6 +180,63 @@ def test_gqa_prefill_matches_causal_attention(dtype, B, QH, KVH, HD, start, Tc):
     check(kx, (a @ Kall).transpose(1, 2).reshape(B, Tc, QH * HD), dtype)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,Tc,start,HD,hist", [(32, 128, 37, 96, True), (16, 17, 500, 96, False),
+                                                (2, 20, 3, 96, True), (4, 70, 9, 64, True)])
+def test_prefill_qkv_matches_products_and_rope(dtype, B, Tc, start, HD, hist):
+    """loom_prefill_qkv = the qkv product, loom_gqa_prefill's RoPE + cache append
+    and the history projection, to the bit (bf16, head_dim 96, >= 256 rows: one
+    launch with the RoPE in the product's epilogue; the rest: the separate
+    products and RoPE launch), and against torch: the product rounded to the
+    dtype, then the oracle's RoPE."""
+    from loom_amd import _lib
+    QH, KVH, N = 8, 2, 768
+    W = (QH + 2 * KVH) * HD
+    M = B * Tc
+    g = torch.Generator().manual_seed(B * Tc + start + HD)
+    max_len = start + Tc + 2
+    cos, sin = _rope_tables(HD, max_len)
+    cos_d, sin_d = cos.to(DEV), sin.to(DEV)
+    x = torch.randn(M, N, generator=g).to(DEV, dtype)
+    wq = (torch.randn(W, N, generator=g) * N ** -0.5).to(DEV, dtype)
+    wh = (torch.randn(2 * N, N, generator=g) * N ** -0.5).to(DEV, dtype)
+    cs = (max_len * KVH * HD, HD, max_len * HD)          # head-major cache [B, KVH, max_len, HD]
+    outs = []
+    for fused in (True, False):
+        kc = torch.zeros(B, KVH, max_len, HD, device=DEV, dtype=dtype)
+        vc = torch.zeros_like(kc)
+        q = torch.zeros(M, QH * HD, device=DEV, dtype=dtype)
+        hs = torch.zeros(M, 3, 2 * N, device=DEV, dtype=dtype)   # history slot 1 of [M, 3, 2N]
+        qkv = torch.zeros(M, W, device=DEV, dtype=dtype)
+        if fused:
+            _lib.call("loom_prefill_qkv", code(x), P(x), N, P(wq), P(wh) if hist else None,
+                      P(hs[:, 1]) if hist else None, 3 * 2 * N, 2 * N, P(qkv), P(q), P(kc), P(vc), *cs,
+                      P(cos_d), P(sin_d), B, Tc, start, max_len, N, QH, KVH, HD, S(x))
+        else:
+            _lib.call("loom_linear", code(x), P(x), N, P(wq), N, None, None, 0.0, None, P(qkv), W, M,
+                      W, N, S(x))
+            if hist:
+                _lib.call("loom_linear", code(x), P(x), N, P(wh), N, None, None, 0.0, None, P(hs[:, 1]),
+                          3 * 2 * N, M, 2 * N, N, S(x))
+            c = torch.empty(M, QH * HD, device=DEV, dtype=dtype)
+            kx = torch.empty_like(c)
+            _lib.call("loom_gqa_prefill", code(x), P(qkv), W, P(kc), P(vc), *cs, P(cos_d), P(sin_d),
+                      P(q), P(c), P(kx), QH * HD, B, Tc, start, max_len, QH, KVH, HD, S(x))
+        torch.cuda.synchronize()
+        outs.append((q, kc, vc, hs))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    q, kc, vc, hs = outs[0]
+    y = (host(x) @ host(wq).t()).to(dtype).float().view(B, Tc, QH + 2 * KVH, HD)
+    csn, snn = cos[start:start + Tc].view(1, Tc, 1, HD), sin[start:start + Tc].view(1, Tc, 1, HD)
+    check(q.view(B, Tc, QH, HD), ref.apply_rope(y[:, :, :QH], csn, snn), dtype)
+    check(kc[:, :, start:start + Tc].transpose(1, 2), ref.apply_rope(y[:, :, QH:QH + KVH], csn, snn), dtype)
+    check(vc[:, :, start:start + Tc].transpose(1, 2), y[:, :, QH + KVH:], dtype)
+    if hist:
+        check(hs[:, 1], host(x) @ host(wh).t(), dtype)
+    assert not kc[:, :, :start].any() and not kc[:, :, start + Tc:].any()
+
+
 def _rope_tables(HD, n):
     inv, af = ref.yarn_inv_freq(HD, 10000.0, 4.0, 256, 32.0, 1.0)
     return ref.yarn_cos_sin(inv, af, n)
@@ -501,6 +558,39 @@ def test_linear_multi(dtype, M):
     flags[3] = 1
     _lib.call("loom_linear_multi", code(x), ctypes.byref(d), S(x))
     check(out3, X @ host(w1).T + host(b1), dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("M,n0,n1", [(4096, 1152, 1536), (1000, 768, 640), (300, 1000, 64)])
+def test_linear_multi_two_segments_many_rows(dtype, M, n0, n1):
+    """Two projections of one activation with many rows: bf16 runs them as one
+    launch of DMA-staged tiles when the first segment ends on a tile boundary
+    (the second product's own weight, strided output and bias); to the bit the
+    two separate products, and against the fp32 products."""
+    from loom_amd import _lib
+    g = torch.Generator().manual_seed(M + n0 + n1)
+    K = 768
+    r = lambda *s: (torch.randn(*s, generator=g) * 0.5).to(DEV, dtype)
+    x = r(M, K)
+    w0, w1 = r(n0, K) * 0.1, r(n1, K) * 0.1
+    b1 = torch.randn(n1, generator=g).to(DEV)
+    outs = []
+    for fused in (True, False):
+        o0 = torch.zeros(M, n0, device=DEV, dtype=dtype)
+        wide = torch.zeros(M, n1 + 40, device=DEV, dtype=dtype)
+        o1 = wide[:, 8:8 + n1]
+        segs = [dict(w=w0, out=o0), dict(w=w1, out=o1, bias=b1)]
+        calls = [segs] if fused else [[sg] for sg in segs]
+        for sg in calls:
+            d = _lib.linear_multi_desc(x, sg)
+            _lib.call("loom_linear_multi", code(x), ctypes.byref(d), S(x))
+        torch.cuda.synchronize()
+        outs.append((o0, wide))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    o0, wide = outs[0]
+    check(o0, host(x) @ host(w0).T, dtype)
+    check(wide[:, 8:8 + n1], host(x) @ host(w1).T + host(b1), dtype)
+    assert not wide[:, :8].any() and not wide[:, 8 + n1:].any()
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
