@@ -265,9 +265,15 @@ gqa_prefill_kernel(PrefillArgs<T> a) {
 //                 registers' row order (tile_tr_frag, attn_tile.h).
 // Block (x, y, b): y = kvh * HSPLIT + part; wave w takes head
 // kvh*G + part*GP + w%GP and query tile x*QTB + w/GP (16 positions each).
-// The block streams 32 cached rows per step into two LDS buffers: the next
+// The block streams 64 cached rows per step into two LDS buffers: the next
 // tile's loads are in flight while a tile is computed and land in the other
-// buffer, one block barrier per step.
+// buffer, one block barrier per step.  A step is two 32-row sub-tiles under
+// one softmax update (at 1920 cached rows 74.4 -> 68.5 us against 32-row
+// steps; 96 and 128 rows measured slower, 86-88 us, from register pressure).
+// Two query tiles per wave (each K / V fragment read feeding two MFMAs)
+// measured 12-14% slower: with 2048 query-tile x head items at the prefill's
+// chunk shape a wave per SIMD is left, and the latency it no longer hides
+// costs more than the halved LDS reads save.
 typedef __bf16 bf16x8_p __attribute__((ext_vector_type(8)));
 typedef float f32x4_p __attribute__((ext_vector_type(4)));
 
@@ -286,7 +292,8 @@ __device__ __forceinline__ void lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-constexpr int kPfRows = 32;   // cached rows per step
+constexpr int kPfSub = 2;     // 32-row sub-tiles per step (one softmax update per step)
+constexpr int kPfRows = 32 * kPfSub;   // cached rows per step
 
 template <int HD, int GP, int HSPLIT>
 __global__ void __launch_bounds__(256)
@@ -296,18 +303,19 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     constexpr int CPR = HD / 8;                 // 16-byte pieces per row
     constexpr int QTB = 4 / GP;                 // query tiles per block
     constexpr int G = GP * HSPLIT;
-    constexpr int PIECES = kPfRows * CPR;       // pieces of one tensor's 32-row tile
+    constexpr int SUB = kPfSub, R = kPfRows;
+    constexpr int PIECES = R * CPR;             // pieces of one tensor's tile of a step
     constexpr int PPT = (2 * PIECES + 255) / 256;
     // LDS rows one piece longer than a head row: with HD = 96 (12 pieces) the
     // 16 rows of a fragment read, and the 4 rows of a transposing read, start
     // in distinct banks, with no swizzle
     constexpr int PITCH = CPR + 1;
-    __shared__ __align__(16) gqa_u4 tk[2][kPfRows * PITCH];   // K tile, row-major, two buffers
-    __shared__ __align__(16) gqa_u4 tv[2][kPfRows * PITCH];   // V tile
+    __shared__ __align__(16) gqa_u4 tk[2][R * PITCH];   // K tile, row-major, two buffers
+    __shared__ __align__(16) gqa_u4 tv[2][R * PITCH];   // V tile
     __shared__ float cr[4][16];                           // per-column rescale of a step
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 15, lq = lane >> 4;
-    // work item (query tile, head group, row) in query-tile-fastest order; the
+    // work item (query tiles, head group, row) in query-tile-fastest order; the
     // query tiles of one (row, kv head) read the same K/V rows, so they share
     // an XCD and its L2
     const int ntile = (a.Tc + 16 * QTB - 1) / (16 * QTB), ngrp = a.KVH * HSPLIT;
@@ -316,23 +324,21 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     const int kvh = by / HSPLIT, part = by % HSPLIT;
     const int64_t b = w / (ntile * ngrp);
     const int head = kvh * G + part * GP + wave % GP;
-    const int q0 = (bx * QTB + wave / GP) * 16;                  // first query of the wave's tile
     const int qlast_blk = min((bx + 1) * QTB * 16, a.Tc) - 1;
     const int64_t kmax = a.start + qlast_blk;                    // last cached row the block reads
-    const int nsteps = (int)((kmax + kPfRows) / kPfRows);
+    const int nsteps = (int)((kmax + R) / R);
+    const int q0 = (bx * QTB + wave / GP) * 16;                  // first query of the wave's tile
     // this lane's query column (lr): its position; a column past the chunk
     // attends to row 0 only (finite, never stored)
     const int qcol = q0 + lr;
-    const int64_t qpos = qcol < a.Tc ? a.start + qcol : 0;
-    const int qpos32 = (int)qpos;          // positions fit 31 bits (checked by the host)
+    const int qpos32 = qcol < a.Tc ? (int)a.start + qcol : 0;    // positions fit 31 bits (host check)
+    const int wave_qpos0 = (int)a.start + q0;                    // position of the wave's first query
+    const int64_t wave_kmax = q0 < a.Tc ? a.start + min(q0 + 15, a.Tc - 1) : -1;
     const TileLane<CPR, PITCH, false> tl(lq, lr);
-    const int wave_qlast = min(q0 + 15, a.Tc - 1);
-    const int wave_qpos0 = (int)a.start + q0;    // position of the wave's first query
-    const int64_t wave_kmax = q0 < a.Tc ? a.start + wave_qlast : -1;
 
     const bf16_t* kb = a.kc + b * a.csb + kvh * a.csh;
     const bf16_t* vb = a.vc + b * a.csb + kvh * a.csh;
-    // one 32-row tile: piece p -> (tensor, row, piece of the row), read through
+    // one step's tile: piece p -> (tensor, row, piece of the row), read through
     // buffer resources that end after row kmax: rows past it read as zero
     // (positions after every query of the block, masked out), so a load needs
     // no clamp and its offset is a per-thread constant plus the step's rows.
@@ -390,7 +396,7 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
             qf[kk] = *reinterpret_cast<const uint4*>(qp + 32 * kk + 8 * lq);
     }
     load_tile(S0{}, 0);
-    load_tile(S1{}, kPfRows);
+    load_tile(S1{}, R);
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk)
         asm volatile("" : "+v"(qf[kk].x), "+v"(qf[kk].y), "+v"(qf[kk].z), "+v"(qf[kk].w));
@@ -407,66 +413,80 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     // tile it+1 (requested a step ago) into the other buffer.  Every step
     // requests a tile (rows past kmax read as zero), so the loads in flight
     // are the same on every path and each store waits for its own tile only.
+    // A step is SUB sub-tiles of 32 rows under one softmax update.
     auto step = [&](auto set_, int it) {
         constexpr int cur = decltype(set_)::value;
-        const int64_t r0 = (int64_t)it * kPfRows;
-        load_tile(set_, r0 + 2 * kPfRows);
+        const int64_t r0 = (int64_t)it * R;
+        load_tile(set_, r0 + 2 * R);
         const bool active = r0 <= wave_kmax;                 // wave-uniform
         if (active) {
-            f32x4_p sc[2];
+            // sub-tile u: rows 32u .. 32u + 31 of the step (tile rows from 32u on);
+            // S^T[row 32u + 16*hf + 4*lq + r][query column lr], unscaled
+            f32x4_p sc[SUB][2];
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                sc[hf] = f32x4_p{0.f, 0.f, 0.f, 0.f};
+            for (int u = 0; u < SUB; ++u)
 #pragma unroll
-                for (int kk = 0; kk < KK; ++kk)
-                    sc[hf] = mfma16p(tile_s_frag<CPR>(tk[cur], tl, hf, kk), qf[kk], sc[hf]);
-            }
-            // S^T[row 16*hf + 4*lq + r][query column lr], unscaled; rows after
-            // a column's position are masked only in the tiles that reach the
-            // wave's first query (the scale is applied inside the exponent:
-            // the maximum of the scaled scores is the scaled maximum)
-            float sv[2][4];
+                for (int hf = 0; hf < 2; ++hf) {
+                    sc[u][hf] = f32x4_p{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kk = 0; kk < KK; ++kk)
+                        sc[u][hf] = mfma16p(tile_s_frag<CPR>(tk[cur] + u * 32 * PITCH, tl, hf, kk), qf[kk],
+                                            sc[u][hf]);
+                }
+            // rows after a column's position are masked only in the steps that
+            // reach the wave's first query (the scale is applied inside the
+            // exponent: the maximum of the scaled scores is the scaled maximum)
+            float sv[SUB][2][4];
             float mx = -INFINITY;
-            if ((int)r0 + kPfRows - 1 <= wave_qpos0) {     // wave-uniform
+            if ((int)r0 + R - 1 <= wave_qpos0) {     // wave-uniform
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf)
+                for (int u = 0; u < SUB; ++u)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        sv[hf][r] = sc[hf][r];
-                        mx = fmaxf(mx, sv[hf][r]);
-                    }
+                    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            sv[u][hf][r] = sc[u][hf][r];
+                            mx = fmaxf(mx, sv[u][hf][r]);
+                        }
             } else {
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf)
+                for (int u = 0; u < SUB; ++u)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int row = (int)r0 + 16 * hf + 4 * lq + r;
-                        sv[hf][r] = row <= qpos32 ? sc[hf][r] : -INFINITY;
-                        mx = fmaxf(mx, sv[hf][r]);
-                    }
+                    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int row = (int)r0 + 32 * u + 16 * hf + 4 * lq + r;
+                            sv[u][hf][r] = row <= qpos32 ? sc[u][hf][r] : -INFINITY;
+                            mx = fmaxf(mx, sv[u][hf][r]);
+                        }
             }
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
             const float mnew = fmaxf(mh, mx * a.qscale);    // finite: row 0 is seen at step 0
             const float corr = __builtin_amdgcn_exp2f(mh - mnew);
-            float ls = 0.0f, pv[2][4];
+            float ls = 0.0f, pv[SUB][2][4];
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf)
+            for (int u = 0; u < SUB; ++u)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    // a masked score gives exp2(-inf) = 0
-                    pv[hf][r] = __builtin_amdgcn_exp2f(fmaf(sv[hf][r], a.qscale, -mnew));
-                    ls += pv[hf][r];
-                }
+                for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        // a masked score gives exp2(-inf) = 0
+                        pv[u][hf][r] = __builtin_amdgcn_exp2f(fmaf(sv[u][hf][r], a.qscale, -mnew));
+                        ls += pv[u][hf][r];
+                    }
             ls += __shfl_xor(ls, 16, 64);
             ls += __shfl_xor(ls, 32, 64);
             lh = fmaf(lh, corr, ls);
             mh = mnew;
-            // A operand of P V / P K straight from the score registers: query
-            // column lr, positions 4*lq + r and 16 + 4*lq + r (bf16 like the
-            // reference's softmax output), matched by tile_tr_frag
-            const uint4 pa = make_uint4(pack_bf16x2(pv[0][0], pv[0][1]), pack_bf16x2(pv[0][2], pv[0][3]),
-                                        pack_bf16x2(pv[1][0], pv[1][1]), pack_bf16x2(pv[1][2], pv[1][3]));
+            // A operands of P V / P K straight from the score registers: query
+            // column lr, positions 32u + 4*lq + r and 32u + 16 + 4*lq + r (bf16
+            // like the reference's softmax output), matched by tile_tr_frag
+            uint4 pa[SUB];
+#pragma unroll
+            for (int u = 0; u < SUB; ++u)
+                pa[u] = make_uint4(pack_bf16x2(pv[u][0][0], pv[u][0][1]), pack_bf16x2(pv[u][0][2], pv[u][0][3]),
+                                   pack_bf16x2(pv[u][1][0], pv[u][1][1]), pack_bf16x2(pv[u][1][2], pv[u][1][3]));
             // the accumulator rows are query columns 4*lq + r: their rescale
             // from the lanes that hold those columns, through LDS (measured
             // faster here than four cross-lane permutes); skipped when no
@@ -487,10 +507,12 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
                 wave_lds_fence();              // cr is rewritten next step
             }
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                accC[dt] = mfma16p(pa, tile_tr_frag<CPR>(tv[cur], tl, dt), accC[dt]);
-                accK[dt] = mfma16p(pa, tile_tr_frag<CPR>(tk[cur], tl, dt), accK[dt]);
-            }
+            for (int u = 0; u < SUB; ++u)
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    accC[dt] = mfma16p(pa[u], tile_tr_frag<CPR>(tv[cur] + u * 32 * PITCH, tl, dt), accC[dt]);
+                    accK[dt] = mfma16p(pa[u], tile_tr_frag<CPR>(tk[cur] + u * 32 * PITCH, tl, dt), accK[dt]);
+                }
         }
         // the next tile into the other buffer (last read two steps ago, before
         // the previous barrier), then one barrier for both
@@ -519,8 +541,6 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     }
 }
 
-// RoPE of the chunk's q and k rows of qkv into q_out and the k cache, v into
-// the v cache (positions start .. start + Tc - 1 of every row b).
 template <typename T>
 static int rope_append_dispatch(const void* qkv, int64_t qkv_ld, void* kc, void* vc, int64_t csb,
                                 int64_t cst, int64_t csh, const float* cosv, const float* sinv,
@@ -602,16 +622,16 @@ static int prefill_dispatch(const void* qkv, int64_t qkv_ld, void* kc, void* vc,
 #define LOOM_PF_MF(HDV)                                                                          \
             if (HD == HDV) {                                                                     \
                 if (G == 4) {                                                                    \
-                    const dim3 g((unsigned)(ceil_div(Tc, 16) * KVH * B));                        \
+                    const dim3 g((unsigned)(ceil_div(Tc, 16) * KVH * B));                \
                     hipLaunchKernelGGL((gqa_prefill_mfma_kernel<HDV, 4, 1>), g, dim3(256), 0, st, a); \
                 } else if (G == 8) {                                                             \
-                    const dim3 g((unsigned)(ceil_div(Tc, 16) * KVH * 2 * B));                    \
+                    const dim3 g((unsigned)(ceil_div(Tc, 16) * KVH * 2 * B));            \
                     hipLaunchKernelGGL((gqa_prefill_mfma_kernel<HDV, 4, 2>), g, dim3(256), 0, st, a); \
                 } else if (G == 2) {                                                             \
-                    const dim3 g((unsigned)(ceil_div(Tc, 32) * KVH * B));                        \
+                    const dim3 g((unsigned)(ceil_div(Tc, 32) * KVH * B));                \
                     hipLaunchKernelGGL((gqa_prefill_mfma_kernel<HDV, 2, 1>), g, dim3(256), 0, st, a); \
                 } else {                                                                         \
-                    const dim3 g((unsigned)(ceil_div(Tc, 64) * KVH * B));                        \
+                    const dim3 g((unsigned)(ceil_div(Tc, 64) * KVH * B));                \
                     hipLaunchKernelGGL((gqa_prefill_mfma_kernel<HDV, 1, 1>), g, dim3(256), 0, st, a); \
                 }                                                                                \
                 return launch_status("loom_gqa_prefill");                                       \
