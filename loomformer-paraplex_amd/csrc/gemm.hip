@@ -279,12 +279,15 @@ gemm_bf16_mfma_kernel(GemmArgs a) {
 // stages).
 __host__ __device__ constexpr int bg_swz(int r) { return ((r >> 3) & 1) << 1; }
 // Full-line stages (no gather, 64 k per stage): a stage row is the whole
-// 128-byte line [8 chunks of 8 k], chunk c of row r at position c ^ bg_swz8(r).
-// A fragment read's half-wave takes 16 rows x chunks {4kk + 2h, 4kk + 2h + 1};
-// rows r, r+4, r+8, r+12 share their offset modulo 512 B and the swizzle puts
-// their chunk pairs on four distinct pairs of positions.  One DMA instruction
-// then fills 8 whole rows (lane l: row l/8, position l%8), 8 full lines.
-__host__ __device__ constexpr int bg_swz8(int r) { return ((r >> 2) & 3) << 1; }
+// 128-byte line [8 chunks of 8 k], chunk c of row r at position c ^ bg_swz8(r)
+// = c ^ (r & 7).  One DMA instruction fills 8 whole rows (lane l: row l/8,
+// position l%8), 8 full lines.  The swizzle was chosen by timing ds_read_b128
+// fragment reads over 128-byte rows (a calibration kernel, 16-row x 4-chunk
+// pattern): c ^ (r & 7) and c ^ ((r >> 1) & 7) read at the rate of a linear
+// 1 KB read (2.7-2.9 ns per wave-read per CU), c ^ 2*((r >> 2) & 3) at 3.5
+// (2-way), no swizzle at 7.0; the model that fits 64-byte rows (a half-wave's
+// pieces distinct modulo 512 B) does not predict these.
+__host__ __device__ constexpr int bg_swz8(int r) { return r & 7; }
 
 template <int BM_, int BN_, int WAVES_, int WGM_, int KH_, int WPE_, int NS_>
 struct BgCfg {
