@@ -9,10 +9,13 @@
 namespace loom {
 
 // Piece swizzle: piece c of row r sits at c ^ kv_swz(r) (bits 1, 2 of r to
-// bits 1, 0), so the 8 rows of a 16-byte fragment read and the 4 rows x 32 B
-// of a transposing read fall in distinct banks.  The pieces of a row stay a
-// permutation of 0..HD/8-1.
-__device__ __forceinline__ int kv_swz(int r) { return (((r >> 1) & 1) << 1) | ((r >> 2) & 1); }
+// bits 0, 1).  Chosen by timing both read forms on gfx950 over every 2-bit
+// swizzle of 192-byte rows (HD = 96): a 16-byte fragment read takes 5.0 LDS
+// cycles and a transposing read 2.6 (the 1024 and 512 bytes they move need
+// 4 and 2), against 8.7 and 4.4 with the two bits crossed (bits 1, 2 to 1, 0)
+// and 9.3 and 4.7 with unswizzled rows padded to 13 pieces.  The pieces of a
+// row stay a permutation of 0..HD/8-1 (HD/8 a multiple of 4).
+__device__ __forceinline__ int kv_swz(int r) { return ((r >> 1) & 1) | (((r >> 2) & 1) << 1); }
 
 typedef short gqa_v4s __attribute__((ext_vector_type(4)));
 typedef uint32_t gqa_u4 __attribute__((ext_vector_type(4)));   // a 16-byte piece as a native vector

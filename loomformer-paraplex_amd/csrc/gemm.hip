@@ -320,19 +320,6 @@ using BgWide = BgCfg<128, 256, 8, 2, 2, 2, 3>;
 // N = 3072 they make 256 tiles, one round of the CUs, where 256 x 128 or
 // 128 x 256 make 384 (a round and a half)
 using BgTall = BgCfg<256, 192, 8, 4, 1, 2, 4>;
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-
-// 16 bytes per lane from a raw buffer straight into LDS (lane l lands at lds + 16*l)
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const uint16_t* lds, uint32_t voff,
-                                      uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
-}
 
 // Source and element offset (within the source's row) of the 32 packed
 // columns [kk, kk + 32) of group g in gather mode; they lie in one sector.

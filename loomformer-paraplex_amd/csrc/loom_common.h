@@ -58,6 +58,23 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // Dword 3 of a gfx9 raw-buffer descriptor (untyped 32-bit data format).
 constexpr int kBufferDword3 = 0x00020000;
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Wait until at most N of this wave's vector-memory operations are in flight
+// (loads straight into LDS included).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// 16 bytes per lane from a raw buffer straight into LDS (lane l lands at
+// lds + 16*l; lds wave-uniform); an offset past the buffer's end lands zeros
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voff,
+                                      uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
+}
+
 // two floats -> packed bf16 pair (low = a), one conversion instruction
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));

@@ -292,6 +292,16 @@ __device__ __forceinline__ void lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Block barrier over LDS filled by loads straight into LDS: this wave's
+// loads but the last N have landed and its LDS reads have completed, then
+// s_barrier.  The asm's memory clobber keeps the compiler from moving memory
+// accesses across it; a workgroup fence would also wait for the N loads.
+template <int N>
+__device__ __forceinline__ void dma_barrier() {
+    wait_vmcnt<N>();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 constexpr int kPfSub = 2;     // 32-row sub-tiles per step (one softmax update per step)
 constexpr int kPfRows = 32 * kPfSub;   // cached rows per step
 
@@ -304,15 +314,23 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     constexpr int QTB = 4 / GP;                 // query tiles per block
     constexpr int G = GP * HSPLIT;
     constexpr int SUB = kPfSub, R = kPfRows;
-    constexpr int PIECES = R * CPR;             // pieces of one tensor's tile of a step
-    constexpr int PPT = (2 * PIECES + 255) / 256;
-    // LDS rows one piece longer than a head row: with HD = 96 (12 pieces) the
-    // 16 rows of a fragment read, and the 4 rows of a transposing read, start
-    // in distinct banks, with no swizzle
-    constexpr int PITCH = CPR + 1;
-    __shared__ __align__(16) gqa_u4 tk[2][R * PITCH];   // K tile, row-major, two buffers
-    __shared__ __align__(16) gqa_u4 tv[2][R * PITCH];   // V tile
+    static_assert(CPR % 4 == 0 && R == 64, "a tile is CPR loads of 64 pieces, split evenly over the 4 waves");
+    constexpr int GPW = CPR / 4;                // loads per tensor per wave and step
+    // LDS rows of CPR pieces, piece c of row r at c ^ kv_swz(r); three stages
+    // (tile t in stage t % 3) as separate arrays, so that a wait for one
+    // stage's loads never covers another stage's reads
+    constexpr int PITCH = CPR;
+    __shared__ __align__(16) gqa_u4 K0[R * PITCH], K1[R * PITCH], K2[R * PITCH];
+    __shared__ __align__(16) gqa_u4 V0[R * PITCH], V1[R * PITCH], V2[R * PITCH];
     __shared__ float cr[4][16];                           // per-column rescale of a step
+    auto kst = [&](auto s_) -> gqa_u4* {
+        constexpr int S = decltype(s_)::value;
+        return S == 0 ? K0 : S == 1 ? K1 : K2;
+    };
+    auto vst = [&](auto s_) -> gqa_u4* {
+        constexpr int S = decltype(s_)::value;
+        return S == 0 ? V0 : S == 1 ? V1 : V2;
+    };
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 15, lq = lane >> 4;
     // work item (query tiles, head group, row) in query-tile-fastest order; the
@@ -334,55 +352,39 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     const int qpos32 = qcol < a.Tc ? (int)a.start + qcol : 0;    // positions fit 31 bits (host check)
     const int wave_qpos0 = (int)a.start + q0;                    // position of the wave's first query
     const int64_t wave_kmax = q0 < a.Tc ? a.start + min(q0 + 15, a.Tc - 1) : -1;
-    const TileLane<CPR, PITCH, false> tl(lq, lr);
+    const TileLane<CPR, PITCH, true> tl(lq, lr);
 
     const bf16_t* kb = a.kc + b * a.csb + kvh * a.csh;
     const bf16_t* vb = a.vc + b * a.csb + kvh * a.csh;
-    // one step's tile: piece p -> (tensor, row, piece of the row), read through
-    // buffer resources that end after row kmax: rows past it read as zero
-    // (positions after every query of the block, masked out), so a load needs
-    // no clamp and its offset is a per-thread constant plus the step's rows.
-    // The tensor of a piece is the same across a wave (PIECES is a multiple
-    // of 64).  Two register sets, so a tile is requested two steps before
-    // its LDS store (tile t in set t % 2).
+    // one step's tiles go from the caches straight into LDS, 16 bytes a lane:
+    // load g (0..CPR-1) of a tensor fills LDS pieces 64g .. 64g+63 of the
+    // stage, lane l piece 64g + l = row * CPR + p, which holds piece
+    // p ^ kv_swz(row) of the row; wave w issues g = w, w+4, ...  Reads go
+    // through buffer resources that end after row kmax: rows past it land as
+    // zero (positions after every query of the block, masked out), so a load
+    // needs no clamp and its offset is a per-lane constant plus the step's rows.
     const int kv_bytes = (int)((kmax + 1) * a.cst * 2);
     const auto rk = __builtin_amdgcn_make_buffer_rsrc((void*)kb, (short)0, kv_bytes, kBufferDword3);
     const auto rv = __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0, kv_bytes, kBufferDword3);
     const uint32_t row_bytes = (uint32_t)(a.cst * 2);
-    uint32_t voff[PPT];
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t voff[GPW];
 #pragma unroll
-    for (int u = 0; u < PPT; ++u) {
-        const int q = (tid + 256 * u) % PIECES;
-        voff[u] = (uint32_t)(q / CPR) * row_bytes + (uint32_t)(q % CPR) * 16u;
+    for (int j = 0; j < GPW; ++j) {
+        const int p = 64 * (wv + 4 * j) + lane, row = p / CPR, c = p % CPR;
+        voff[j] = (uint32_t)row * row_bytes + (uint32_t)(c ^ kv_swz(row)) * 16u;
     }
-    gqa_u4 reg[2][PPT];
-    auto load_tile = [&](auto set_, int64_t r0) {
-        constexpr int SET = decltype(set_)::value;
+    auto load_tile = [&](auto s_, int64_t r0) {     // 2 * GPW loads of this wave
         const uint32_t base = (uint32_t)r0 * row_bytes;
 #pragma unroll
-        for (int u = 0; u < PPT; ++u) {
-            const int p = tid + 256 * u;
-            if ((2 * PIECES) % 256 == 0 || p < 2 * PIECES) {
-                const bool is_k = __builtin_amdgcn_readfirstlane(p / PIECES) == 0;
-                reg[SET][u] = __builtin_amdgcn_raw_buffer_load_b128(is_k ? rk : rv, voff[u] + base, 0, 0);
-            }
-        }
-    };
-    auto store_tile = [&](auto set_) {      // into LDS buffer SET
-        constexpr int SET = decltype(set_)::value;
-#pragma unroll
-        for (int u = 0; u < PPT; ++u) {
-            const int p = tid + 256 * u;
-            if ((2 * PIECES) % 256 == 0 || p < 2 * PIECES) {
-                const int tensor = p / PIECES, q = p % PIECES;
-                const int row = q / CPR, ch = q % CPR;
-                gqa_u4* dst = tensor == 0 ? tk[SET] : tv[SET];
-                dst[row * PITCH + ch] = reg[SET][u];
-            }
+        for (int j = 0; j < GPW; ++j) {
+            dma16(rk, kst(s_) + 64 * (wv + 4 * j), voff[j] + base, 0);
+            dma16(rv, vst(s_) + 64 * (wv + 4 * j), voff[j] + base, 0);
         }
     };
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
     // B operand of S^T: q of query column lr, dims 32*kk + 8*lq .. +7; loaded
     // first and complete before the loop (a register loaded ahead of a loop
     // whose own loads stay in flight would be waited for inside it, and that
@@ -397,27 +399,28 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
     }
     load_tile(S0{}, 0);
     load_tile(S1{}, R);
+    dma_barrier<2 * GPW>();                 // q and tile 0 (tile 1 may be in flight)
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk)
         asm volatile("" : "+v"(qf[kk].x), "+v"(qf[kk].y), "+v"(qf[kk].z), "+v"(qf[kk].w));
-    store_tile(S0{});
-    lds_sync();
 
     float mh = -INFINITY, lh = 0.0f;      // running max / sum of query column lr
     f32x4_p accC[DT], accK[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) accC[dt] = accK[dt] = f32x4_p{0.f, 0.f, 0.f, 0.f};
 
-    // step it computes tile it from LDS buffer it % 2, requests tile it+2 into
-    // register set it % 2 (its tile it went to LDS a step ago) and stores
-    // tile it+1 (requested a step ago) into the other buffer.  Every step
-    // requests a tile (rows past kmax read as zero), so the loads in flight
-    // are the same on every path and each store waits for its own tile only.
-    // A step is SUB sub-tiles of 32 rows under one softmax update.
-    auto step = [&](auto set_, int it) {
-        constexpr int cur = decltype(set_)::value;
+    // step it computes tile it from stage it % 3 and requests tile it+2 into
+    // stage (it+2) % 3 (tile it-1's, read by every wave before the previous
+    // barrier), then waits for tile it+1 and passes one barrier.  Every step
+    // requests a tile (rows past kmax land as zero), so the loads in flight
+    // are the same on every path and each wait is a constant.  A step is SUB
+    // sub-tiles of 32 rows under one softmax update.
+    auto step = [&](auto s_, int it) {
+        constexpr int cur = decltype(s_)::value;
+        const gqa_u4* tk = kst(s_);
+        const gqa_u4* tv = vst(s_);
         const int64_t r0 = (int64_t)it * R;
-        load_tile(set_, r0 + 2 * R);
+        load_tile(std::integral_constant<int, (cur + 2) % 3>{}, r0 + 2 * R);
         const bool active = r0 <= wave_kmax;                 // wave-uniform
         if (active) {
             // sub-tile u: rows 32u .. 32u + 31 of the step (tile rows from 32u on);
@@ -430,7 +433,7 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
                     sc[u][hf] = f32x4_p{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int kk = 0; kk < KK; ++kk)
-                        sc[u][hf] = mfma16p(tile_s_frag<CPR>(tk[cur] + u * 32 * PITCH, tl, hf, kk), qf[kk],
+                        sc[u][hf] = mfma16p(tile_s_frag<CPR>(tk + u * 32 * PITCH, tl, hf, kk), qf[kk],
                                             sc[u][hf]);
                 }
             // rows after a column's position are masked only in the steps that
@@ -510,20 +513,19 @@ gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
             for (int u = 0; u < SUB; ++u)
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
-                    accC[dt] = mfma16p(pa[u], tile_tr_frag<CPR>(tv[cur] + u * 32 * PITCH, tl, dt), accC[dt]);
-                    accK[dt] = mfma16p(pa[u], tile_tr_frag<CPR>(tk[cur] + u * 32 * PITCH, tl, dt), accK[dt]);
+                    accC[dt] = mfma16p(pa[u], tile_tr_frag<CPR>(tv + u * 32 * PITCH, tl, dt), accC[dt]);
+                    accK[dt] = mfma16p(pa[u], tile_tr_frag<CPR>(tk + u * 32 * PITCH, tl, dt), accK[dt]);
                 }
         }
-        // the next tile into the other buffer (last read two steps ago, before
-        // the previous barrier), then one barrier for both
-        if (it + 1 < nsteps) store_tile(std::integral_constant<int, cur ^ 1>{});
-        lds_sync();
+        dma_barrier<2 * GPW>();             // tile it+1 landed (tile it+2 may be in flight)
     };
-    // an even number of steps (a last step past kmax computes nothing)
-    for (int it = 0; it < nsteps; it += 2) {
+    // a multiple of 3 steps (steps past kmax compute nothing)
+    for (int it = 0; it < nsteps; it += 3) {
         step(S0{}, it);
         step(S1{}, it + 1);
+        step(S2{}, it + 2);
     }
+    wait_vmcnt<0>();                        // no load into LDS outlives the loop
     // normalise: the sum of query column c lives in lanes with lr == c
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
