@@ -663,6 +663,38 @@ gemm_bf16_big_kernel(GemmArgs a) {
     auto gcol = [&](int gi) -> int64_t { return scol(gslot(gi)); };
     auto grow = [&](int gi) -> int64_t { return mrow + 16 * (gi % FJ); };
     auto gval = [&](int gi, int r) -> float { return acc[gi / FJ][gi % FJ][r]; };
+    // Staged stores: a wave's finished tile goes to a wave-private LDS region,
+    // row-major with its 16-byte pieces permuted within each row, and each
+    // lane then stores 16 contiguous bytes of a row, so the output leaves in
+    // row runs instead of 16 rows of 32 or 64 bytes per store (the
+    // 8-byte-per-lane form made the bf16 epilogue of 4096 x 3072 x 768 take
+    // 30.4 against 26.2 us with row runs).  The regions are carved out of the
+    // stage arrays, X arrays first, after one barrier (every wave has read its
+    // last stage).
+    auto stage_region = [&](auto bytes_) -> uint16_t* {
+        constexpr int BYTES = decltype(bytes_)::value;
+        constexpr int RX = KH * XH * 2 / BYTES, RW = KH * WH * 2 / BYTES;
+        uint16_t* reg = nullptr;
+        int q = wave;
+        bg_static_for<NS>([&](auto s_) {
+            if (reg == nullptr) {
+                if (q < RX) reg = xs(s_) + q * (BYTES / 2);
+                else q -= RX;
+            }
+        });
+        bg_static_for<NS>([&](auto s_) {
+            if (reg == nullptr) {
+                if (q < RW) reg = ws(s_) + q * (BYTES / 2);
+                else q -= RW;
+            }
+        });
+        return reg;
+    };
+    // regions of BYTES for every wave
+    constexpr int REG2 = C::WTM * C::WTN * 2, REG4 = 2 * REG2;
+    constexpr bool FIT2 = NS * (KH * XH * 2 / REG2 + KH * WH * 2 / REG2) >= C::WAVES;
+    constexpr bool FIT4 = NS * (KH * XH * 2 / REG4 + KH * WH * 2 / REG4) >= C::WAVES;
+    static_assert(FIT2 && C::WTN % 32 == 0, "staging regions");
     if constexpr (!GATHER && C::WTN == 96) {
         if (a.rope.q != nullptr && !seg_b) {
             // the wave's 96 columns are one head; column d's rotation partner
@@ -673,18 +705,28 @@ gemm_bf16_big_kernel(GemmArgs a) {
             const int hd = (int)((n0 + wn * 96) / 96);
             const int dl = (lane >> 4) * 4;
             const bool rot = hd < ro.QH + ro.KVH;
+            // the destination row of output row m (q row, or the cache row of its position)
+            auto row_dst = [&](int64_t m) -> uint16_t* {
+                const int64_t b = m / ro.Tc, pos = ro.start + (m - b * ro.Tc);
+                if (hd < ro.QH) return (uint16_t*)ro.q + m * (int64_t)(ro.QH * 96) + hd * 96;
+                if (rot) return (uint16_t*)ro.kc + b * ro.csb + pos * ro.cst + (hd - ro.QH) * ro.csh;
+                return (uint16_t*)ro.vc + b * ro.csb + pos * ro.cst + (hd - ro.QH - ro.KVH) * ro.csh;
+            };
+            // staged (16-byte row pieces) when the block's rows are all in range
+            // and every destination row is 16-byte aligned
+            const bool st16 = m0 + BG_M <= a.M && ((ro.csb | ro.cst | ro.csh) & 7) == 0 &&
+                              (((uintptr_t)ro.q | (uintptr_t)ro.kc | (uintptr_t)ro.vc) & 15) == 0;
+            uint16_t* reg = nullptr;
+            if (st16) {
+                __syncthreads();            // every wave is done with the stages
+                reg = stage_region(std::integral_constant<int, REG2>{});
+            }
 #pragma unroll
             for (int j = 0; j < FJ; ++j) {
                 const int64_t m = mrow + 16 * j;
                 if (m >= a.M) continue;
-                const int64_t b = m / ro.Tc, pos = ro.start + (m - b * ro.Tc);
-                uint16_t* dst;
-                if (hd < ro.QH)
-                    dst = (uint16_t*)ro.q + m * (int64_t)(ro.QH * 96) + hd * 96;
-                else if (rot)
-                    dst = (uint16_t*)ro.kc + b * ro.csb + pos * ro.cst + (hd - ro.QH) * ro.csh;
-                else
-                    dst = (uint16_t*)ro.vc + b * ro.csb + pos * ro.cst + (hd - ro.QH - ro.KVH) * ro.csh;
+                const int64_t pos = ro.start + (m - (m / ro.Tc) * ro.Tc);
+                uint16_t* dst = st16 ? nullptr : row_dst(m);
                 float4 cv[FI], sv[FI];
 #pragma unroll
                 for (int i = 0; i < FI; ++i) {
@@ -705,8 +747,23 @@ gemm_bf16_big_kernel(GemmArgs a) {
                         const float x = round_bf(acc[i][j][r]), y = round_bf(acc[ip][j][r]);
                         v[r] = rot ? fmaf(x, c4[r], (sg * y) * s4[r]) : x;
                     }
-                    *reinterpret_cast<uint2*>(dst + 16 * i + dl) =
-                        make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                    const uint2 w = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                    if (st16) {
+                        const int rl = 16 * j + (lane & 15), cl = 16 * i + dl;
+                        *reinterpret_cast<uint2*>(reg + rl * 96 + 8 * ((cl >> 3) ^ ((rl >> 1) & 3)) + (cl & 7)) = w;
+                    } else {
+                        *reinterpret_cast<uint2*>(dst + 16 * i + dl) = w;
+                    }
+                }
+            }
+            if (st16) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int it = 0; it < C::WTM * 12 / 64; ++it) {
+                    const int c = it * 64 + lane, row = c / 12, pc = c % 12;
+                    *reinterpret_cast<uint4*>(row_dst(m0 + wm * C::WTM + row) + 8 * pc) =
+                        *reinterpret_cast<const uint4*>(reg + row * 96 + 8 * (pc ^ ((row >> 1) & 3)));
                 }
             }
             return;
@@ -716,6 +773,31 @@ gemm_bf16_big_kernel(GemmArgs a) {
         // split-K: raw fp32 sums of this split, 16-byte stores where all four
         // columns are in range
         float* part = a.partial + split * a.M * a.ldp;
+        if constexpr (FIT4) {
+            if (m0 + BG_M <= a.M && n0 + BG_N <= a.N && (a.ldp & 3) == 0 && ((uintptr_t)part & 15) == 0) {
+                // whole tile, staged: piece p (4 floats) of row r at p ^ (r & 15)
+                __syncthreads();
+                float* reg = reinterpret_cast<float*>(stage_region(std::integral_constant<int, REG4>{}));
+                constexpr int PR = C::WTN / 4;          // 16-byte pieces of a wave-tile row
+#pragma unroll
+                for (int gi = 0; gi < NG; ++gi) {
+                    const int rl = 16 * (gi % FJ) + (lane & 15);
+                    const int pc = 4 * gslot(gi) + (lane >> 4);
+                    *reinterpret_cast<float4*>(reg + rl * C::WTN + 4 * (pc ^ (rl & 15))) =
+                        make_float4(gval(gi, 0), gval(gi, 1), gval(gi, 2), gval(gi, 3));
+                }
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                float* orow = part + (m0 + wm * C::WTM) * a.ldp + n0 + wn * C::WTN;
+#pragma unroll
+                for (int it = 0; it < C::WTM * PR / 64; ++it) {
+                    const int c = it * 64 + lane, row = c / PR, pc = c % PR;
+                    *reinterpret_cast<float4*>(orow + row * a.ldp + 4 * pc) =
+                        *reinterpret_cast<const float4*>(reg + row * C::WTN + 4 * (pc ^ (row & 15)));
+                }
+                return;
+            }
+        }
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) {
             const int64_t nb = gcol(gi), m = grow(gi);
@@ -742,40 +824,14 @@ gemm_bf16_big_kernel(GemmArgs a) {
         x[0] = __uint_as_float(w.x << 16); x[1] = __uint_as_float(w.x & 0xffff0000u);
         x[2] = __uint_as_float(w.y << 16); x[3] = __uint_as_float(w.y & 0xffff0000u);
     };
-    // Staged stores of a whole tile: each wave's WTM x WTN bf16 results go to
-    // a wave-private LDS region (row-major, 16-byte piece p of row r at
-    // p ^ ((r >> 1) & 3)), and each lane then stores 16 contiguous bytes of a
-    // row, so the output leaves in row runs of WTN * 2 bytes instead of 32-byte
-    // pieces of 16 rows (4096 x 3072 x 768: 30.4 -> 26.2 us; 8192 rows:
-    // 54 -> 45.6 us).  The regions reuse the stage arrays once every wave has
-    // read its last stage (one barrier).
-    constexpr int RB = C::WTN * 2, REG = C::WTM * RB;
-    constexpr int RX = KH * XH * 2 / REG, RW = KH * WH * 2 / REG;   // regions per X / W stage array
-    static_assert(NS * (RX + RW) >= C::WAVES && C::WTN % 32 == 0, "staging regions");
+    // whole tiles staged (bf16 piece p of row r at p ^ ((r >> 1) & 3))
     const bool staged = whole && (((uintptr_t)out & 15) == 0) && (ldc & 7) == 0;
-    auto wave_region = [&]() -> uint16_t* {
-        uint16_t* reg = nullptr;
-        int q = wave;
-        bg_static_for<NS>([&](auto s_) {
-            if (reg == nullptr) {
-                if (q < RX) reg = xs(s_) + q * (REG / 2);
-                else q -= RX;
-            }
-        });
-        bg_static_for<NS>([&](auto s_) {
-            if (reg == nullptr) {
-                if (q < RW) reg = ws(s_) + q * (REG / 2);
-                else q -= RW;
-            }
-        });
-        return reg;
-    };
     auto whole_tile = [&](auto gate_, auto res_) {
         constexpr bool GATE = decltype(gate_)::value, RES = decltype(res_)::value;
         uint16_t* reg = nullptr;
         if (staged) {
             __syncthreads();                // every wave is done with the stages
-            reg = wave_region();
+            reg = stage_region(std::integral_constant<int, REG2>{});
         }
         // every operand of the wave's outputs requested before the first store
         // (an output may alias them as far as the compiler knows, so a load
