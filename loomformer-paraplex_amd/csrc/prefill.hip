@@ -305,10 +305,11 @@ __device__ __forceinline__ void dma_barrier() {
 constexpr int kPfSub = 2;     // 32-row sub-tiles per step (one softmax update per step)
 constexpr int kPfRows = 32 * kPfSub;   // cached rows per step
 
-// Two waves per SIMD (<= 256 VGPRs): the accumulators then stay in
-// ordinary VGPRs, where the per-step rescale multiplies them in place (with
-// the default target the compiler keeps them in AGPRs and copies each one out
-// and back, 144 extra VALU operations per step)
+// Two waves per SIMD (<= 256 VGPRs; the grid of a 128-token chunk has two
+// per SIMD).  The file is built with -amdgpu-mfma-vgpr-form, so the
+// accumulators sit in ordinary VGPRs, where the per-step rescale multiplies
+// them in place (in AGPRs each would be copied out and back, 144 VALU
+// operations per step)
 template <int HD, int GP, int HSPLIT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 gqa_prefill_mfma_kernel(PrefillArgs<bf16_t> a) {
