@@ -450,6 +450,17 @@ int loom_gqa_prefill(int dtype, const void* qkv, int64_t qkv_ld, void* k_cache, 
                      void* kctx_out, int64_t out_ld, int64_t B, int64_t T, int64_t start,
                      int64_t cache_len, int64_t QH, int64_t KVH, int64_t HD, void* stream);
 
+/* Shared-tile mode of the many-row products (loom_linear, loom_linear_multi,
+ * loom_linear_ln, loom_beta_forward, loom_prefill_qkv): on = 1 picks tiles of
+ * 128 x 192 (four waves, two blocks per CU) wherever they fit, for products
+ * that run beside another stream's kernels (the chunked prefill); on = 0, the
+ * default, picks the tiles that are fastest alone.  Results agree with the
+ * default mode's to the rounding of the output type (the k order inside an
+ * MFMA, and loom_linear_ln's split-K count, may differ).  Process-wide;
+ * returns the previous mode.
+ * No counterpart in the reference (a scheduling choice of this library). */
+int loom_gemm_shared_tiles(int on);
+
 /* The chunked prefill's projections of one hidden state x [B*T, K] (row
  * stride ldx) for the next block: qkv = x w_qkv^T (the block's
  * GroupedQueryCausalSelfAttention qkv Linear, loomformer.py:3262), then

@@ -15,6 +15,7 @@
 // [Q_g | Kctx_g | C_g | U | D_g] (head sectors) or [Q_g | Kctx | C | U | D]
 // (open sectors); the loader reads each 8-element piece from its sector, so
 // the packed matrix is never written to HBM.
+#include <atomic>
 #include <cmath>
 #include <type_traits>
 #include <utility>
@@ -320,6 +321,13 @@ using BgWide = BgCfg<128, 256, 8, 2, 2, 2, 3>;
 // N = 3072 they make 256 tiles, one round of the CUs, where 256 x 128 or
 // 128 x 256 make 384 (a round and a half)
 using BgTall = BgCfg<256, 192, 8, 4, 1, 2, 4>;
+// 128 x 192 tiles of four waves of 64 x 96 (80 KB, two blocks per CU), for
+// shared-tile mode (loom_gemm_shared_tiles): alone they are slower than
+// 256 x 192 (4096 x 3072 x 768: 32.3 against 30.0 us; 1.4x the operand
+// traffic per flop), but a block holds half a CU, so another stream's
+// kernels run beside the product instead of waiting for a whole CU to drain
+// (the chunked prefill: 63.8 -> 62.0 ms)
+using BgTallS = BgCfg<128, 192, 4, 2, 1, 2, 4>;
 
 // Source and element offset (within the source's row) of the 32 packed
 // columns [kk, kk + 32) of group g in gather mode; they lie in one sector.
@@ -1547,12 +1555,17 @@ static void launch_skinny(const GemmArgs& a, dim3 grid, hipStream_t st) {
 //     73.5-74.0 ms (same box, alternating runs).
 // K must fill whole rounds of the configuration's stages; gather tiles must
 // not straddle a q-head group (Hq % BG_N == 0).
-enum BigTile { kBigNone, kBigStd, kBigSmall, kBigWide, kBigTall };
+enum BigTile { kBigNone, kBigStd, kBigSmall, kBigWide, kBigTall, kBigTallS };
+// shared-tile mode (loom_gemm_shared_tiles): process-wide
+static std::atomic<int> g_shared_tiles{0};
 template <class C>
 static bool big_fits(int64_t M, int64_t K, bool gather, int64_t Hq) {
     return M >= C::BG_M && K % (C::NS * C::BK) == 0 && (!gather || Hq % C::BG_N == 0);
 }
 static BigTile big_tile(int64_t M, int64_t N, int64_t K, bool gather, int64_t Hq) {
+    if (g_shared_tiles.load(std::memory_order_relaxed) != 0 && (gather || N % BgTallS::BG_N == 0) &&
+        big_fits<BgTallS>(M, K, gather, Hq))
+        return kBigTallS;
     const bool std_ok = big_fits<BgConf>(M, K, gather, Hq);
     const bool small_ok = big_fits<BgSmall>(M, K, gather, Hq);
     const bool wide_ok = !gather && N % BgWide::BG_N == 0 && big_fits<BgWide>(M, K, gather, Hq);
@@ -1569,7 +1582,7 @@ static BigTile big_tile(int64_t M, int64_t N, int64_t K, bool gather, int64_t Hq
 }
 static int64_t big_tile_n(BigTile t) {
     return t == kBigSmall ? BgSmall::BG_N : t == kBigWide ? BgWide::BG_N : t == kBigTall ? BgTall::BG_N
-                                                                                       : BgConf::BG_N;
+         : t == kBigTallS ? BgTallS::BG_N : BgConf::BG_N;
 }
 template <bool GATHER, class C>
 static void launch_big_cfg(const GemmArgs& a, int64_t nsplit, hipStream_t st) {
@@ -1579,6 +1592,7 @@ static void launch_big_cfg(const GemmArgs& a, int64_t nsplit, hipStream_t st) {
 template <bool GATHER>
 static void launch_big(const GemmArgs& a, BigTile tile, int64_t nsplit, hipStream_t st) {
     if (tile == kBigSmall) launch_big_cfg<GATHER, BgSmall>(a, nsplit, st);
+    else if (tile == kBigTallS) launch_big_cfg<GATHER, BgTallS>(a, nsplit, st);
     else if constexpr (!GATHER) {
         if (tile == kBigWide) launch_big_cfg<GATHER, BgWide>(a, nsplit, st);
         else if (tile == kBigTall) launch_big_cfg<GATHER, BgTall>(a, nsplit, st);
@@ -2001,6 +2015,12 @@ extern "C" int loom_linear_ln(int dtype, const loom_linear_multi_desc* d, const 
         } else if (tile == kBigTall) {
             bm = BgTall::BG_M; bn = BgTall::BG_N; stage_k = BgTall::NS * BgTall::BK;
             half_k = BgTall::BK;
+        } else if (tile == kBigTallS) {
+            // counted as one block per CU: in shared-tile mode the other
+            // stream's kernels hold part of every CU (two splits at the
+            // prefill's 4096 x 768 tails, measured faster than three)
+            bm = BgTallS::BG_M; bn = BgTallS::BG_N; stage_k = BgTallS::NS * BgTallS::BK;
+            half_k = BgTallS::BK;
         }
         const int64_t tiles = ceil_div(d->m, bm) * ceil_div(g.n, bn);
         int64_t ns = 0, best = 0;
@@ -2237,6 +2257,10 @@ extern "C" int loom_beta_forward(int dtype, const void* u, const void* q_h, cons
 // (each wave's 96 columns are one head) and the history columns as a second
 // product of the same launch; qkv is never stored.  Otherwise the two
 // products into qkv_scratch / hist_out and the separate RoPE + append launch.
+extern "C" int loom_gemm_shared_tiles(int on) {
+    return g_shared_tiles.exchange(on != 0 ? 1 : 0);
+}
+
 extern "C" int loom_prefill_qkv(int dtype, const void* x, int64_t ldx, const void* w_qkv,
                                 const void* w_hist, void* hist_out, int64_t hist_ld, int64_t n_hist,
                                 void* qkv_scratch, void* q_out, void* k_cache, void* v_cache,
@@ -2264,8 +2288,10 @@ extern "C" int loom_prefill_qkv(int dtype, const void* x, int64_t ldx, const voi
     const uintptr_t a16 = (uintptr_t)x | (uintptr_t)w_qkv | (uintptr_t)w_hist | (uintptr_t)cos_table |
                           (uintptr_t)sin_table;
     const uintptr_t a8 = (uintptr_t)q_out | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)hist_out;
+    const bool shared = g_shared_tiles.load(std::memory_order_relaxed) != 0;
     const bool fused = dtype == LOOM_BF16 && HD == 96 && QKV % BgTall::BG_N == 0 &&
-                       big_fits<BgTall>(M, K, false, 0) && K % 8 == 0 && ldx % 8 == 0 &&
+                       (shared ? big_fits<BgTallS>(M, K, false, 0) : big_fits<BgTall>(M, K, false, 0)) &&
+                       K % 8 == 0 && ldx % 8 == 0 &&
                        (a16 & 15) == 0 && (a8 & 7) == 0 && cache_stride_b % 4 == 0 &&
                        cache_stride_t % 4 == 0 && cache_stride_h % 4 == 0 &&
                        (w_hist == nullptr || hist_ld % 4 == 0);
@@ -2278,7 +2304,8 @@ extern "C" int loom_prefill_qkv(int dtype, const void* x, int64_t ldx, const voi
         }
         a.rope = GemmArgs::RopeOut{q_out, k_cache, v_cache, cache_stride_b, cache_stride_t,
                                    cache_stride_h, cos_table, sin_table, T, start, (int)QH, (int)KVH};
-        launch_big_cfg<false, BgTall>(a, 1, st);
+        if (shared) launch_big_cfg<false, BgTallS>(a, 1, st);
+        else launch_big_cfg<false, BgTall>(a, 1, st);
         return launch_status("loom_prefill_qkv");
     }
     int rc = loom_linear(dtype, x, ldx, w_qkv, K, nullptr, nullptr, 0.0f, nullptr, qkv_scratch, QKV, M,

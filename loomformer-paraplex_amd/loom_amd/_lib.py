@@ -12,8 +12,8 @@ from ctypes import c_float, c_int, c_int64, c_void_p
 
 import torch
 
-# descriptor layouts and signatures below are those of loom_abi_version() == 5
-ABI_VERSION = 8
+# descriptor layouts and signatures below are those of loom_abi_version() == ABI_VERSION
+ABI_VERSION = 9
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libloom_hip.so")
 
 _P = c_void_p
@@ -117,6 +117,7 @@ SIGNATURES = {
 }
 # entry points that return a value instead of a status
 QUERIES = {"loom_gqa_workspace_bytes": ([c_int64] * 5, c_int64),
+           "loom_gemm_shared_tiles": ([c_int], c_int),
            "loom_linear_multi_desc_bytes": ([], c_int64),
            "loom_decode_tria_readout_workspace_bytes": ([c_int64, c_int64], c_int64),
            "loom_ffn_decode_desc_bytes": ([], c_int64),

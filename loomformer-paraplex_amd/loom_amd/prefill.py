@@ -45,7 +45,18 @@ def chunk_bounds(prompt_cpu: torch.Tensor, window: int, seq_len: int, carry_id) 
 @torch.no_grad()
 def prefill(eng, prompt: torch.Tensor) -> None:
     """Run ``prompt`` [B, P] through the chunked forward and set ``eng`` up to
-    decode position P (see the module docstring)."""
+    decode position P (see the module docstring).  The many-row products run
+    in the library's shared-tile mode (half-CU blocks), since they run beside
+    the other streams' kernels; the previous mode is restored on return."""
+    lib = _lib.load()
+    prev = lib.loom_gemm_shared_tiles(1)
+    try:
+        _prefill(eng, prompt)
+    finally:
+        lib.loom_gemm_shared_tiles(prev)
+
+
+def _prefill(eng, prompt: torch.Tensor) -> None:
     c = eng.cfg
     B, P = prompt.shape
     if B != eng.B or P < 1:

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     assert "loom_paraplex_forward" in syms and len(syms) >= 15
     missing = [s for s in syms if not hasattr(lib, s)]
     assert not missing, missing
-    assert lib.loom_abi_version() == 8
+    assert lib.loom_abi_version() == 9
     # every declared compute entry point has a ctypes signature
     compute = [s for s in syms if s not in ("loom_last_error", "loom_abi_version")]
     bound = set(_lib.SIGNATURES) | set(_lib.QUERIES)
@@ -102,3 +102,18 @@ def test_noalloc_rejects_records_beyond_the_scratch():
         _lib.call("loom_gqa_decode_step_noalloc", 1, None, None, None, KVH * length * HD, HD,
                   length * HD, None, None, None, None, None, QH * HD, B, length, None, QH, KVH,
                   HD, None)
+
+
+def test_gemm_shared_tiles_is_a_process_switch():
+    """loom_gemm_shared_tiles sets the tile mode and returns the previous one
+    (host-side state: no device needed)."""
+    from loom_amd import _lib
+    lib = _lib.load()
+    prev = lib.loom_gemm_shared_tiles(1)
+    try:
+        assert lib.loom_gemm_shared_tiles(1) == 1
+        assert lib.loom_gemm_shared_tiles(0) == 1
+        assert lib.loom_gemm_shared_tiles(7) == 0      # any nonzero value turns it on
+        assert lib.loom_gemm_shared_tiles(0) == 1
+    finally:
+        lib.loom_gemm_shared_tiles(prev)

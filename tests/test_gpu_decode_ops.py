@@ -1,5 +1,6 @@
 """GPU parity of the decode-step kernels against fp32 references (oracle ops
 or plain torch on the CPU)."""
+import contextlib
 import ctypes
 import math
 
@@ -181,14 +182,23 @@ def test_gqa_prefill_matches_causal_attention(dtype, B, QH, KVH, HD, start, Tc):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("B,Tc,start,HD,hist", [(32, 128, 37, 96, True), (16, 17, 500, 96, False),
-                                                (2, 20, 3, 96, True), (4, 70, 9, 64, True)])
-def test_prefill_qkv_matches_products_and_rope(dtype, B, Tc, start, HD, hist):
+@pytest.mark.parametrize("B,Tc,start,HD,hist,shared", [(32, 128, 37, 96, True, False),
+                                                       (16, 17, 500, 96, False, False),
+                                                       (2, 20, 3, 96, True, False), (4, 70, 9, 64, True, False),
+                                                       (32, 128, 37, 96, True, True),
+                                                       (16, 17, 500, 96, False, True)])
+def test_prefill_qkv_matches_products_and_rope(dtype, B, Tc, start, HD, hist, shared):
     """loom_prefill_qkv = the qkv product, loom_gqa_prefill's RoPE + cache append
     and the history projection, to the bit (bf16, head_dim 96, >= 256 rows: one
     launch with the RoPE in the product's epilogue; the rest: the separate
     products and RoPE launch), and against torch: the product rounded to the
-    dtype, then the oracle's RoPE."""
+    dtype, then the oracle's RoPE.  `shared`: in shared-tile mode (128 x 192
+    tiles), as the chunked prefill runs it."""
+    with shared_tiles(shared):
+        _prefill_qkv_case(dtype, B, Tc, start, HD, hist)
+
+
+def _prefill_qkv_case(dtype, B, Tc, start, HD, hist):
     from loom_amd import _lib
     QH, KVH, N = 8, 2, 768
     W = (QH + 2 * KVH) * HD
@@ -235,6 +245,67 @@ def test_prefill_qkv_matches_products_and_rope(dtype, B, Tc, start, HD, hist):
     if hist:
         check(hs[:, 1], host(x) @ host(wh).t(), dtype)
     assert not kc[:, :, :start].any() and not kc[:, :, start + Tc:].any()
+
+
+@contextlib.contextmanager
+def shared_tiles(on):
+    """The library's shared-tile mode set for the block, restored after."""
+    lib = L().load()
+    prev = lib.loom_gemm_shared_tiles(1 if on else 0)
+    try:
+        yield
+    finally:
+        lib.loom_gemm_shared_tiles(prev)
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 3072, 768), (4000, 1152, 768), (300, 768, 1536),
+                                   (4096, 768, 3072), (4096, 1536, 768)])
+def test_shared_tiles_equal_default_tiles(M, N, K):
+    """Shared-tile mode (128 x 192 tiles of four waves, two blocks per CU)
+    against the default tiles: loom_linear with bias, gate and residual and
+    loom_linear_ln (whose split-K count may differ) against torch in both
+    modes, the W_imag gather product of both modes against each other."""
+    from loom_amd import _lib, ops
+    dt = torch.bfloat16
+    g = torch.Generator().manual_seed(M + N + K)
+    r = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(DEV, dt)
+    x, w = r(M, K), r(N, K, sc=K ** -0.5)
+    bias = torch.randn(N, generator=g).to(DEV)
+    p, res = r(M, N), r(M, N)
+    QH, HD, Hq = 8, 96, 384
+    u = r(1, M, QH * HD)
+    q, kc, c, d = (r(1, M, QH, HD) for _ in range(4))
+    w_imag = r(QH * Hq, ref.imag_in(QH * HD, HD, "head"), sc=0.03)
+    gam = (torch.rand(N, generator=g) + 0.5).to(DEV)
+    bet = torch.randn(N, generator=g).to(DEV)
+    nb = L().load().loom_linear_ln_workspace_bytes(M, N)
+    ws = torch.empty(nb // 4, device=DEV)
+    outs = []
+    for on in (False, True):
+        with shared_tiles(on):
+            y = ops.linear(x, w, bias, gate_p=p, gate_alpha=0.2, residual=res)
+            beta = ops.beta_forward_cuda(u, q, kc, c, d, w_imag, Hq, HD, QH, False)[0]
+            ln = None
+            if N <= 2048:                   # loom_linear_ln's row length limit
+                ln = torch.zeros(M, N, device=DEV, dtype=dt)
+                yy = torch.zeros(M, N, device=DEV, dtype=dt)
+                desc = _lib.linear_multi_desc(x, [dict(w=w, out=yy, bias=bias)])
+                _lib.call("loom_linear_ln", code(x), ctypes.byref(desc), P(gam), P(bet), 1e-5, P(ln), N,
+                          P(ws), nb, None, S(x))
+            torch.cuda.synchronize()
+        outs.append((y, beta, ln))
+    # 64-k full-line stages and 32-k stages give an MFMA's lanes different k,
+    # so the two modes agree to bf16 rounding (to the bit where both pick
+    # 32-k stages, as at 4096 x 3072 x 768)
+    want_y = (host(x) @ host(w).T) * (1.0 + 0.2 * host(p)) + host(bias) + host(res)
+    for o in outs:
+        check(o[0], want_y, dt)
+    check(outs[1][1], host(outs[0][1]), dt)
+    if N <= 2048:
+        want = torch.nn.functional.layer_norm(host(x) @ host(w).T + host(bias), (N,), host(gam), host(bet),
+                                              1e-5)
+        for o in outs:
+            check(o[2], want, dt)
 
 
 def _rope_tables(HD, n):
@@ -561,12 +632,19 @@ def test_linear_multi(dtype, M):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("M,n0,n1", [(4096, 1152, 1536), (1000, 768, 640), (300, 1000, 64)])
-def test_linear_multi_two_segments_many_rows(dtype, M, n0, n1):
+@pytest.mark.parametrize("M,n0,n1,shared", [(4096, 1152, 1536, False), (1000, 768, 640, False),
+                                            (300, 1000, 64, False), (4096, 1152, 1536, True)])
+def test_linear_multi_two_segments_many_rows(dtype, M, n0, n1, shared):
     """Two projections of one activation with many rows: bf16 runs them as one
     launch of DMA-staged tiles when the first segment ends on a tile boundary
     (the second product's own weight, strided output and bias); to the bit the
-    two separate products, and against the fp32 products."""
+    two separate products, and against the fp32 products (`shared`: in
+    shared-tile mode)."""
+    with shared_tiles(shared):
+        _two_segment_case(dtype, M, n0, n1)
+
+
+def _two_segment_case(dtype, M, n0, n1):
     from loom_amd import _lib
     g = torch.Generator().manual_seed(M + n0 + n1)
     K = 768
