@@ -28,6 +28,11 @@ from . import _lib
 
 _P = _lib.ptr
 
+# batch rows of a layer's attention on the aux stream (the rest on main, after
+# its depth read): at B = 32, 24 rows measured 62.2-62.3 ms against 62.5-62.6
+# with all 32 on aux (16 and 20: 62.3-62.4)
+PREFILL_AUX_ROWS = 24
+
 
 def chunk_bounds(prompt_cpu: torch.Tensor, window: int, seq_len: int, carry_id) -> List[int]:
     """Last position of every chunk of a [B, P] prompt (the final one is P-1)."""
@@ -141,6 +146,11 @@ def _prefill(eng, prompt: torch.Tensor) -> None:
     spans = list(zip([0] + [x + 1 for x in ends[:-1]], ends))
 
     gathered = torch.cuda.Event()
+    qkv_ready = torch.cuda.Event()      # a layer's q and cache rows written (aux)
+    # batch rows whose attention runs on aux right after the qkv product; the
+    # rest run on main after its depth read (the two branches then take about
+    # as long)
+    aux_rows = min(B, PREFILL_AUX_ROWS)
 
     def next_qkv(x, bi, sub, s_, Tc_):
         """Block bi's qkv of x with RoPE + cache append (loomformer.py:3262, :3300-3320)
@@ -154,10 +164,13 @@ def _prefill(eng, prompt: torch.Tensor) -> None:
              cache_sh, _P(eng.cos), _P(eng.sin), B, Tc_, s_, eng.max_len, N, QH, KVH, HD,
              eng._stream())
 
-    def attend(bi, s_, Tc_):
-        call("loom_gqa_prefill", code, None, 0, _P(eng.k_cache[bi]), _P(eng.v_cache[bi]),
-             cache_sb, cache_st, cache_sh, _P(eng.cos), _P(eng.sin), _P(q), _P(cbuf), _P(kctx), N,
-             B, Tc_, s_, eng.max_len, QH, KVH, HD, eng._stream())
+    def attend(bi, s_, Tc_, b0=0, b1=B):
+        """Block bi's attention for batch rows b0..b1-1 (their cache rows and
+        chunk rows are contiguous views), on the current stream."""
+        r0 = b0 * Tc_
+        call("loom_gqa_prefill", code, None, 0, _P(eng.k_cache[bi][b0:]), _P(eng.v_cache[bi][b0:]),
+             cache_sb, cache_st, cache_sh, _P(eng.cos), _P(eng.sin), _P(q[r0:]), _P(cbuf[r0:]),
+             _P(kctx[r0:]), N, b1 - b0, Tc_, s_, eng.max_len, QH, KVH, HD, eng._stream())
 
     def chunk_head(ci):
         """Layer 0's attention inputs of chunk ci, which need only the chunk's
@@ -212,8 +225,13 @@ def _prefill(eng, prompt: torch.Tensor) -> None:
             # ran ahead on aux)
             if bi > 0:
                 with torch.cuda.stream(aux):
-                    attend(bi, s, Tc)
+                    attend(bi, s, Tc, 0, aux_rows)
                 depth(sub, d, rows)
+                if aux_rows < B:
+                    # the other rows' attention on main after its depth read,
+                    # once aux has written this layer's q and cache rows
+                    main.wait_event(qkv_ready)
+                    attend(bi, s, Tc, aux_rows, B)
             join()
             # ---- LN(o(C) + w_o(depth read 2*bi)) (loomformer.py:3999-4000)
             lin_ln(("attn", bi), cbuf, blk["o"], d, eng.wo_for(sub), None, blk["ln1_w"], blk["ln1_b"],
@@ -275,6 +293,7 @@ def _prefill(eng, prompt: torch.Tensor) -> None:
                 fork()
                 with torch.cuda.stream(aux):
                     next_qkv(h, bi + 1, None, s, Tc)
+                    qkv_ready.record()
                 lin(h, eng.kvw, hv[:, sub], rows, 2 * N, N, ldc=2 * L * 2 * N)
         # ---- on the third stream, beside the next chunk's first sublayer: the
         # temporal carry over the chunk, restarting at position 0 and at a

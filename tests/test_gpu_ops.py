@@ -564,7 +564,7 @@ def test_gate_mix_and_slot_pool(dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES3)
-@pytest.mark.parametrize("B,T,H", [(3, 9, 6), (2, 64, 1000), (1, 1, 5)])
+@pytest.mark.parametrize("B,T,H", [(3, 9, 6), (2, 64, 1000), (1, 1, 5), (1, 3, 7), (4, 128, 3072)])
 def test_temporal_carry(dtype, B, T, H):
     from loom_amd import ops
     g = gen(B * T + H)
@@ -576,7 +576,12 @@ def test_temporal_carry(dtype, B, T, H):
     D = host(depth)
     doc, scale = ops.temporal_carry_forward(depth, rs)
     full = ref.temporal_carry(D, reset)
-    check(doc, full, torch.float32 if dtype == torch.float32 else dtype)
+    if dtype == torch.float32 and T > 64:
+        # 128 chained fp32 products: the rounding of both sides grows along the
+        # chain (measured up to 1.7e-4 absolute near zero over 14 M entries)
+        torch.testing.assert_close(host(doc), full, rtol=1e-3, atol=5e-4)
+    else:
+        check(doc, full, torch.float32 if dtype == torch.float32 else dtype)
     e, e32 = ops.temporal_carry_endpoint_forward(depth, rs, torch.empty(0, device=DEV, dtype=dtype),
                                                  torch.empty(0, dtype=torch.bool, device=DEV))
     check(e32, full[:, -1], dtype)           # endpoint == last row of the full recurrence
