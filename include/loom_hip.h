@@ -110,7 +110,8 @@ typedef struct {
     void* out;            /* [m, n] output (row stride ldc) */
     int64_t ldc;
     const float* bias;    /* [n] fp32 or NULL */
-    const void* gate_p;   /* [m, n] dtype (row stride gate_ld) or NULL; single-input only */
+    const void* gate_p;   /* [m, n] dtype (row stride gate_ld; over 64 rows gate_ld == ldc) or NULL;
+                             single-input only */
     int64_t gate_ld;
     float gate_alpha;
     int64_t n;

@@ -435,6 +435,7 @@ gemm_bf16_big_kernel(GemmArgs a) {
             n0 -= a.N1;
             a.N -= a.N1;
             a.W = a.Wb; a.ldw = a.ldwb; a.out = a.outb; a.ldc = a.ldcb; a.bias = a.biasb;
+            a.gate_p = nullptr; a.residual = nullptr;     // the first product's only
         } else {
             a.N = a.N1;
         }
@@ -1795,17 +1796,18 @@ static int linear_multi_dispatch(const loom_linear_multi_desc& d, hipStream_t st
     }
     if (std::is_same<T, bf16_t>::value && d.nseg == 2 && d.k2 == 0 && d.m > 64) {
         // two single-input segments on the DMA-staged tiles: one launch when the
-        // first segment ends on a tile boundary
+        // first segment ends on a tile boundary (a gate on the first only)
         const loom_linear_segment& g0 = d.seg[0];
         const loom_linear_segment& g1 = d.seg[1];
-        bool ok = g0.gate_p == nullptr && g1.gate_p == nullptr && d.k % 8 == 0 && d.ldx % 8 == 0 &&
+        bool ok = g1.gate_p == nullptr && (g0.gate_p == nullptr || g0.gate_ld == g0.ldc) &&
+                  d.k % 8 == 0 && d.ldx % 8 == 0 &&
                   ((uintptr_t)d.x & 15) == 0 && g0.ldw % 8 == 0 && g1.ldw % 8 == 0 &&
                   (((uintptr_t)g0.w | (uintptr_t)g1.w) & 15) == 0;
         const BigTile tile = ok ? big_tile(d.m, g0.n + g1.n, d.k, false, 0) : kBigNone;
         if (tile != kBigNone && g0.n % big_tile_n(tile) == 0) {
             GemmArgs a{};
             a.X = d.x; a.ldx = d.ldx; a.W = g0.w; a.ldw = g0.ldw; a.out = g0.out; a.ldc = g0.ldc;
-            a.bias = g0.bias;
+            a.bias = g0.bias; a.gate_p = g0.gate_p; a.gate_alpha = g0.gate_alpha;
             a.M = d.m; a.N = g0.n + g1.n; a.K = d.k;
             a.N1 = g0.n; a.Wb = g1.w; a.ldwb = g1.ldw; a.outb = g1.out; a.ldcb = g1.ldc; a.biasb = g1.bias;
             launch_big<false>(a, tile, 1, st);
@@ -1818,6 +1820,10 @@ static int linear_multi_dispatch(const loom_linear_multi_desc& d, hipStream_t st
         a.X = d.x; a.ldx = d.ldx; a.W = g.w; a.ldw = g.ldw; a.out = g.out; a.ldc = g.ldc;
         a.M = d.m; a.N = g.n; a.K = d.k;
         if (d.k2 == 0) {
+            // the many-row kernels read the gate at the output's row stride
+            LOOM_CHECK(g.gate_p == nullptr || g.gate_ld == g.ldc,
+                       "linear_multi: over 64 rows a gate needs the output's row stride (gate_ld %lld, ldc %lld)",
+                       (long long)g.gate_ld, (long long)g.ldc);
             a.bias = g.bias; a.gate_p = g.gate_p; a.gate_alpha = g.gate_alpha;
             int rc = run_gemm<T, false>(a, st, "loom_linear_multi");
             if (rc != LOOM_OK) return rc;

@@ -236,17 +236,19 @@ def _prefill(eng, prompt: torch.Tensor) -> None:
             # ---- LN(o(C) + w_o(depth read 2*bi)) (loomformer.py:3999-4000)
             lin_ln(("attn", bi), cbuf, blk["o"], d, eng.wo_for(sub), None, blk["ln1_w"], blk["ln1_b"],
                    rows)
-            # ---- W_real (+ gate with the previous block's p) on aux; history slot
-            # 2*bi+1 and its depth read on main
+            # ---- W_real (+ gate with the previous block's p) and history slot 2*bi+1
+            # in one launch of two products of h (one launch's fixed cost fewer than
+            # W_real on aux beside the history projection: 62.2-62.5 -> 61.6-61.9 ms),
+            # then the slot's depth read
             sub += 1
-            fork()
-            with torch.cuda.stream(aux):
-                if p_i is None:
-                    lin(h, blk["w1r"], R, rows, H, N, bias=blk["b1r"])
-                else:
-                    lin(h, blk["w1r"], R, rows, H, N, bias=blk["b1r"], gate_p=pbuf[p_i],
-                        gate_alpha=blk["alpha"])
-            lin(h, eng.kvw, hv[:, sub], rows, 2 * N, N, ldc=2 * L * 2 * N)
+            key = ("kvr", bi, p_i, rows)
+            dsc = descs.get(key)
+            if dsc is None:
+                real = dict(w=blk["w1r"], out=R[:rows], bias=blk["b1r"])
+                if p_i is not None:
+                    real.update(gate_p=pbuf[p_i][:rows], gate_alpha=blk["alpha"])
+                dsc = descs[key] = _lib.linear_multi_desc(h[:rows], [real, dict(w=eng.kvw, out=hv[:, sub])])
+            call("loom_linear_multi", code, _lib.ctypes.byref(dsc), st)
             depth(sub, dh, rows)
             # ---- Paraplex FFN (loomformer.py:2818-2893): beta space, fused pointwise
             # chain with the phase trace carried from the previous chunk; the

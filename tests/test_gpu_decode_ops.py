@@ -632,19 +632,22 @@ def test_linear_multi(dtype, M):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("M,n0,n1,shared", [(4096, 1152, 1536, False), (1000, 768, 640, False),
-                                            (300, 1000, 64, False), (4096, 1152, 1536, True)])
-def test_linear_multi_two_segments_many_rows(dtype, M, n0, n1, shared):
+@pytest.mark.parametrize("M,n0,n1,shared,gate", [(4096, 1152, 1536, False, False),
+                                                 (1000, 768, 640, False, False),
+                                                 (300, 1000, 64, False, False), (4096, 1152, 1536, True, False),
+                                                 (4096, 3072, 1536, True, True), (1000, 768, 640, False, True)])
+def test_linear_multi_two_segments_many_rows(dtype, M, n0, n1, shared, gate):
     """Two projections of one activation with many rows: bf16 runs them as one
     launch of DMA-staged tiles when the first segment ends on a tile boundary
-    (the second product's own weight, strided output and bias); to the bit the
-    two separate products, and against the fp32 products (`shared`: in
-    shared-tile mode)."""
+    (the second product's own weight, strided output and bias; `gate`: the
+    first product with the anchored gate, as W_real beside the history slot);
+    to the bit the two separate products, and against the fp32 products
+    (`shared`: in shared-tile mode)."""
     with shared_tiles(shared):
-        _two_segment_case(dtype, M, n0, n1)
+        _two_segment_case(dtype, M, n0, n1, gate)
 
 
-def _two_segment_case(dtype, M, n0, n1):
+def _two_segment_case(dtype, M, n0, n1, gate=False):
     from loom_amd import _lib
     g = torch.Generator().manual_seed(M + n0 + n1)
     K = 768
@@ -652,12 +655,14 @@ def _two_segment_case(dtype, M, n0, n1):
     x = r(M, K)
     w0, w1 = r(n0, K) * 0.1, r(n1, K) * 0.1
     b1 = torch.randn(n1, generator=g).to(DEV)
+    p0 = r(M, n0)
     outs = []
     for fused in (True, False):
         o0 = torch.zeros(M, n0, device=DEV, dtype=dtype)
         wide = torch.zeros(M, n1 + 40, device=DEV, dtype=dtype)
         o1 = wide[:, 8:8 + n1]
-        segs = [dict(w=w0, out=o0), dict(w=w1, out=o1, bias=b1)]
+        seg0 = dict(w=w0, out=o0, gate_p=p0, gate_alpha=0.3) if gate else dict(w=w0, out=o0)
+        segs = [seg0, dict(w=w1, out=o1, bias=b1)]
         calls = [segs] if fused else [[sg] for sg in segs]
         for sg in calls:
             d = _lib.linear_multi_desc(x, sg)
@@ -666,7 +671,7 @@ def _two_segment_case(dtype, M, n0, n1):
         outs.append((o0, wide))
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
     o0, wide = outs[0]
-    check(o0, host(x) @ host(w0).T, dtype)
+    check(o0, (host(x) @ host(w0).T) * ((1.0 + 0.3 * host(p0)) if gate else 1.0), dtype)
     check(wide[:, 8:8 + n1], host(x) @ host(w1).T + host(b1), dtype)
     assert not wide[:, :8].any() and not wide[:, 8 + n1:].any()
 
