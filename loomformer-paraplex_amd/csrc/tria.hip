@@ -482,114 +482,169 @@ temporal_carry_kernel(const T* __restrict__ depth, const uint8_t* __restrict__ r
 // when a product is small, so it stays a sequential step).  At the chunked
 // prefill's B x H = 98304 chains the sequential form runs 128-step dependency
 // chains at 1.5 waves per SIMD.
-template <typename T>
+// One step's 9-element carrier records of CH adjacent chains (h, h+1, ..),
+// as floats: with 16-bit storage and CH = 2 the pair's 36 bytes start on a
+// 4-byte boundary (h even, H even), so they load as nine dwords instead of
+// eighteen 2-byte loads.
+template <typename T, int CH>
+__device__ __forceinline__ void load_records(const T* p, float (&v)[CH][9]) {
+    if constexpr (CH == 2 && sizeof(T) == 2) {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            const uint32_t x = w[k];
+            T lo, hi;
+            lo.x = (uint16_t)(x & 0xffffu);
+            hi.x = (uint16_t)(x >> 16);
+            const int e0 = 2 * k, e1 = 2 * k + 1;
+            v[e0 / 9][e0 % 9] = ld(&lo);
+            v[e1 / 9][e1 % 9] = ld(&hi);
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int k = 0; k < 9; ++k) v[c][k] = ld(p + c * 9 + k);
+    }
+}
+
+// Endpoint of the temporal carry with each chain's first T-1 steps split over
+// four lanes of a wave (lanes c, c+16, c+32, c+48 hold chain group c's
+// quarters; a lane carries CH adjacent chains, which share b and so their
+// resets): a quarter composes its steps as the sequential form does (restart
+// on a reset, normalised after every product), the quarters are combined
+// later ones on the left, r = q3 (x) q2 (x) q1 (x) q0 with q (x) r = q when q
+// saw a reset, else normalise(q r), and quarter 0's lane takes the last step
+// from r as the sequential form does.  The normalisation divides by a
+// positive scalar, so r has the direction of the sequential state before the
+// last step; only the last normalisation sets the magnitude (the eps inside
+// the rms matters there when a product is small, so it stays a sequential
+// step).  At the chunked prefill's B x H = 98304 chains the sequential form
+// runs 128-step dependency chains at 1.5 waves per SIMD.
+template <typename T, int CH>
 __global__ void __launch_bounds__(kTriaThreads)
 temporal_endpoint_quarters_kernel(const T* __restrict__ depth, const uint8_t* __restrict__ reset,
                                   const T* __restrict__ initial, const uint8_t* __restrict__ init_valid,
                                   T* __restrict__ endpoint, float* __restrict__ end_f32, int64_t B,
                                   int64_t T_, int64_t H) {
     const int lane = threadIdx.x & 63, qt = lane >> 4;
-    const int64_t chains = B * H;
-    const int64_t sid = (((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6) * 16 + (lane & 15);
-    const bool live = sid < chains;
+    const int64_t groups = B * H / CH;              // H % CH == 0 (host check)
+    const int64_t gid = (((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6) * 16 + (lane & 15);
+    const bool live = gid < groups;
     // no early exit: the whole wave takes part in the combining shuffles
-    const int64_t c = live ? sid : chains - 1;
-    const int64_t b = c / H, h = c - b * H;
+    const int64_t c0 = (live ? gid : groups - 1) * CH;   // first chain (b, h) of the group
+    const int64_t b = c0 / H, h = c0 - b * H;
     const int64_t L = (T_ + 3) / 4;
     const int64_t t_begin = min((int64_t)qt * L, T_ - 1), t_end = min(t_begin + L, T_ - 1);
-    float acc[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    float acc[CH][9];
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int k = 0; k < 9; ++k) acc[c][k] = 0.0f;
     bool have = false;
     bool cut = qt == 0;     // this quarter's result ignores everything before it
     if (qt == 0 && initial != nullptr && (init_valid == nullptr || init_valid[b] != 0)) {
-#pragma unroll
-        for (int k = 0; k < 9; ++k) acc[k] = ld(initial + c * 9 + k);
+        load_records<T, CH>(initial + c0 * 9, acc);
         have = true;
     }
     const int64_t step = H * 9;
     const T* p = depth + (b * T_ * H + h) * 9;
-    float buf[kPrefetch][9];
+    float buf[kPrefetch][CH][9];
 #pragma unroll
     for (int u = 0; u < kPrefetch; ++u)
-        if (t_begin + u < t_end) {
-#pragma unroll
-            for (int k = 0; k < 9; ++k) buf[u][k] = ld(p + (t_begin + u) * step + k);
-        }
+        if (t_begin + u < t_end) load_records<T, CH>(p + (t_begin + u) * step, buf[u]);
     for (int64_t t0 = t_begin; t0 < t_end; t0 += kPrefetch) {
 #pragma unroll
         for (int u = 0; u < kPrefetch; ++u) {
             const int64_t t = t0 + u;
             if (t < t_end) {
-                float loc[9], pre[9];
+                float loc[CH][9];
 #pragma unroll
-                for (int k = 0; k < 9; ++k) loc[k] = buf[u][k];
+                for (int c = 0; c < CH; ++c)
+#pragma unroll
+                    for (int k = 0; k < 9; ++k) loc[c][k] = buf[u][c][k];
                 const int64_t tn = t + kPrefetch;
-                if (tn < t_end) {
-#pragma unroll
-                    for (int k = 0; k < 9; ++k) buf[u][k] = ld(p + tn * step + k);
-                }
+                if (tn < t_end) load_records<T, CH>(p + tn * step, buf[u]);
                 const bool rs = reset[b * T_ + t] != 0;
                 cut = cut || rs;
-                if (!have || rs) {
 #pragma unroll
-                    for (int k = 0; k < 9; ++k) pre[k] = loc[k];
-                } else {
-                    mm3(loc, acc, pre);
+                for (int c = 0; c < CH; ++c) {
+                    float pre[9];
+                    if (!have || rs) {
+#pragma unroll
+                        for (int k = 0; k < 9; ++k) pre[k] = loc[c][k];
+                    } else {
+                        mm3(loc[c], acc[c], pre);
+                    }
+                    const float inv = 1.0f / rms9(pre);
+#pragma unroll
+                    for (int k = 0; k < 9; ++k) acc[c][k] = pre[k] * inv;
                 }
-                const float inv = 1.0f / rms9(pre);
-#pragma unroll
-                for (int k = 0; k < 9; ++k) acc[k] = pre[k] * inv;
                 have = true;
             }
         }
     }
     // quarter 0's lane combines: q1, q2, q3 in order, each from its lane
-    float r[9];
+    float r[CH][9];
 #pragma unroll
-    for (int k = 0; k < 9; ++k) r[k] = acc[k];
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int k = 0; k < 9; ++k) r[c][k] = acc[c][k];
     bool have_r = have;
 #pragma unroll
     for (int j = 1; j < 4; ++j) {
-        float qv[9];
+        float qv[CH][9];
 #pragma unroll
-        for (int k = 0; k < 9; ++k) qv[k] = __shfl(acc[k], lane + 16 * j, 64);
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int k = 0; k < 9; ++k) qv[c][k] = __shfl(acc[c][k], lane + 16 * j, 64);
         const int qcut = __shfl((int)cut, lane + 16 * j, 64);
         const int qhave = __shfl((int)have, lane + 16 * j, 64);
         if (qt == 0 && qhave) {
             have_r = true;
-            if (qcut) {
 #pragma unroll
-                for (int k = 0; k < 9; ++k) r[k] = qv[k];
-            } else {
-                float pre[9];
-                mm3(qv, r, pre);
-                const float inv = 1.0f / rms9(pre);
+            for (int c = 0; c < CH; ++c) {
+                if (qcut) {
 #pragma unroll
-                for (int k = 0; k < 9; ++k) r[k] = pre[k] * inv;
+                    for (int k = 0; k < 9; ++k) r[c][k] = qv[c][k];
+                } else {
+                    float pre[9];
+                    mm3(qv[c], r[c], pre);
+                    const float inv = 1.0f / rms9(pre);
+#pragma unroll
+                    for (int k = 0; k < 9; ++k) r[c][k] = pre[k] * inv;
+                }
             }
         }
     }
     // the last step
     {
         const int64_t tl = T_ - 1;
-        float loc[9], pre[9];
+        float loc[CH][9];
+        load_records<T, CH>(p + tl * step, loc);
+        const bool rl = reset[b * T_ + tl] != 0;
 #pragma unroll
-        for (int k = 0; k < 9; ++k) loc[k] = ld(p + tl * step + k);
-        if (!have_r || reset[b * T_ + tl] != 0) {
+        for (int c = 0; c < CH; ++c) {
+            float pre[9];
+            if (!have_r || rl) {
 #pragma unroll
-            for (int k = 0; k < 9; ++k) pre[k] = loc[k];
-        } else {
-            mm3(loc, r, pre);
+                for (int k = 0; k < 9; ++k) pre[k] = loc[c][k];
+            } else {
+                mm3(loc[c], r[c], pre);
+            }
+            const float inv = 1.0f / rms9(pre);
+#pragma unroll
+            for (int k = 0; k < 9; ++k) r[c][k] = pre[k] * inv;
         }
-        const float inv = 1.0f / rms9(pre);
-#pragma unroll
-        for (int k = 0; k < 9; ++k) r[k] = pre[k] * inv;
     }
     if (qt == 0 && live) {
 #pragma unroll
-        for (int k = 0; k < 9; ++k) {
-            if (endpoint != nullptr) st(endpoint + c * 9 + k, r[k]);
-            if (end_f32 != nullptr) end_f32[c * 9 + k] = r[k];
-        }
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                if (endpoint != nullptr) st(endpoint + (c0 + c) * 9 + k, r[c][k]);
+                if (end_f32 != nullptr) end_f32[(c0 + c) * 9 + k] = r[c][k];
+            }
     }
 }
 
@@ -1018,11 +1073,24 @@ static int temporal_dispatch(bool full, const void* depth, const uint8_t* reset,
                            reset, (const T*)nullptr, nullptr, (T*)nullptr, nullptr, doc, scale,
                            B, T_, H);
     else
-        // 16 chains per wave, four lanes each
-        hipLaunchKernelGGL((temporal_endpoint_quarters_kernel<T>),
-                           dim3((unsigned)ceil_div(B * H, kTriaThreads / 4)), blk, 0, st,
-                           (const T*)depth, reset, (const T*)initial, valid, (T*)endpoint, end32, B,
-                           T_, H);
+    {
+        // 16 groups of chains per wave, four lanes each; 16-bit records two
+        // chains per lane when H is even and the tensors 4-byte aligned
+        bool pair = false;
+        if constexpr (sizeof(T) == 2) {
+            pair = H % 2 == 0 && (((uintptr_t)depth | (uintptr_t)initial) & 3) == 0;
+            if (pair)
+                hipLaunchKernelGGL((temporal_endpoint_quarters_kernel<T, 2>),
+                                   dim3((unsigned)ceil_div(B * H / 2, kTriaThreads / 4)), blk, 0, st,
+                                   (const T*)depth, reset, (const T*)initial, valid, (T*)endpoint,
+                                   end32, B, T_, H);
+        }
+        if (!pair)
+            hipLaunchKernelGGL((temporal_endpoint_quarters_kernel<T, 1>),
+                               dim3((unsigned)ceil_div(B * H, kTriaThreads / 4)), blk, 0, st,
+                               (const T*)depth, reset, (const T*)initial, valid, (T*)endpoint, end32, B,
+                               T_, H);
+    }
     return launch_status(full ? "loom_temporal_carry_forward" : "loom_temporal_carry_endpoint_forward");
 }
 
