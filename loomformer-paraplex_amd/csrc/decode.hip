@@ -438,14 +438,6 @@ __device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// Barrier for LDS traffic only: waits for this wave's LDS operations, not
-// for its outstanding global loads (which __syncthreads would also drain).
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Eight consecutive elements d0..d0+7 of a head, roped for one position
 // (d0 a multiple of 8 and HD/2 a multiple of 8: the group never straddles
 // the rotate-half boundary): 16-byte loads of x and its partner half.

@@ -60,6 +60,14 @@ constexpr int kBufferDword3 = 0x00020000;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// Barrier for LDS traffic only: waits for this wave's LDS operations, not
+// for its outstanding global loads (which __syncthreads would also drain).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Wait until at most N of this wave's vector-memory operations are in flight
 // (loads straight into LDS included).
 template <int N>

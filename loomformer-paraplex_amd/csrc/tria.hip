@@ -20,19 +20,31 @@ constexpr int kTriaThreads = 256;
 // coalesced accesses: whole 16-byte pieces (8 values of a 16-bit type, 4 of
 // fp32) when the slice is 16-byte aligned and a whole number of pieces, single
 // values otherwise.
+// The same copy in two halves, so that loads issued between them stay in
+// flight while the records are waited for: issue() requests the block's
+// pieces (all of them before the first LDS store: one memory round trip per
+// block; nontemporally, each record is read once), commit() writes them to
+// LDS as fp32 (an unaligned slice is loaded and written value by value there).
 template <typename T, int REC = kTriaThreads>
-__device__ __forceinline__ void stage_in(float* lds, const T* src, int n9) {
-    constexpr int V = 16 / (int)sizeof(T);
+struct StageIn {
+    static constexpr int V = 16 / (int)sizeof(T);
     // pieces per thread when the block stages REC records of 9
-    constexpr int kPer = (REC * 9 / V + kTriaThreads - 1) / kTriaThreads;
-    if (((uintptr_t)src & 15) == 0 && n9 % V == 0) {
-        // every piece requested before the first LDS store (one memory round
-        // trip per block), nontemporally: each record is read once
-        u32x4 w[kPer];
+    static constexpr int kPer = (REC * 9 / V + kTriaThreads - 1) / kTriaThreads;
+    u32x4 w[kPer];
+    bool vec;
+    __device__ __forceinline__ void issue(const T* src, int n9) {
+        vec = ((uintptr_t)src & 15) == 0 && n9 % V == 0;
+        if (!vec) return;
 #pragma unroll
         for (int r = 0; r < kPer; ++r) {
             const int c = threadIdx.x + r * kTriaThreads;
             if (c < n9 / V) w[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + c);
+        }
+    }
+    __device__ __forceinline__ void commit(float* lds, const T* src, int n9) const {
+        if (!vec) {
+            for (int k = threadIdx.x; k < n9; k += blockDim.x) lds[k] = ld(src + k);
+            return;
         }
 #pragma unroll
         for (int r = 0; r < kPer; ++r) {
@@ -53,9 +65,13 @@ __device__ __forceinline__ void stage_in(float* lds, const T* src, int n9) {
 #pragma unroll
             for (int e = 0; e < V; ++e) lds[c * V + e] = v[e];
         }
-        return;
     }
-    for (int k = threadIdx.x; k < n9; k += blockDim.x) lds[k] = ld(src + k);
+};
+template <typename T, int REC = kTriaThreads>
+__device__ __forceinline__ void stage_in(float* lds, const T* src, int n9) {
+    StageIn<T, REC> s;
+    s.issue(src, n9);
+    s.commit(lds, src, n9);
 }
 template <typename T>
 __device__ __forceinline__ void stage_out(T* dst, const float* lds, int n9) {
@@ -189,19 +205,22 @@ struct PxTriaArgs {
     float m, alpha;
 };
 
-// Each thread computes EPT elements (tid + 256 u), so a block's two memory
-// round trips (the carried records, then R and beta) move EPT times the bytes.
-template <typename T, int MODE, bool GATE, int AXIS, bool SAME_GATE, int EPT>
+// Each thread computes EPT elements: with PAIR the two consecutive elements
+// 2 tid and 2 tid + 1 (EPT == 2, H even, the element operands aligned to two
+// elements), whose operands load and store as one word each; otherwise
+// elements tid + 256 u.  MODE 1: the block's carried records are requested
+// first and every element operand before they are waited for, so a block
+// makes one memory round trip before its math.
+template <typename T, int MODE, bool GATE, int AXIS, bool SAME_GATE, int EPT, bool PAIR>
 __global__ void __launch_bounds__(kTriaThreads)
 paraplex_tria_kernel(PxTriaArgs<T> a) {
+    static_assert(!PAIR || EPT == 2, "paired elements are two per thread");
     constexpr int REC = kTriaThreads * EPT;
     __shared__ float tile[REC * 9];
     const int64_t e0 = (int64_t)blockIdx.x * REC;
     const int cnt = (int)((a.n - e0) < REC ? (a.n - e0) : REC);
-    if constexpr (MODE == 1) {
-        stage_in<T, REC>(tile, a.prev + e0 * 9, cnt * 9);
-        __syncthreads();
-    }
+    StageIn<T, REC> stg;
+    if constexpr (MODE == 1) stg.issue(a.prev + e0 * 9, cnt * 9);
     // every operand of the thread's elements requested before any store (an
     // output may alias them as far as the compiler knows, so a later load
     // would wait for the earlier stores), at clamped indices; the gate
@@ -211,32 +230,67 @@ paraplex_tria_kernel(PxTriaArgs<T> a) {
 #pragma unroll
         for (int k = 0; k < 9; ++k) wv[k] = ld(a.w + k);
     }
+    auto elem = [](int u) {
+        return PAIR ? 2 * (int)threadIdx.x + u : (int)threadIdx.x + u * kTriaThreads;
+    };
     float xr[EPT], bl[EPT], bp[EPT], tr[EPT], gs[EPT], bias_u[EPT], tw_u[EPT];
     int t_u[EPT], h_u[EPT];
     int64_t b_u[EPT];
-#pragma unroll
-    for (int u = 0; u < EPT; ++u) {
-        const int idx = (int)threadIdx.x + u * kTriaThreads;
-        const int64_t e = e0 + (idx < cnt ? idx : cnt - 1);
+    if constexpr (PAIR) {
+        // cnt is even (n is): a pair is whole, and a pair lies in one row (h even)
+        const int i0 = elem(0);
+        const int64_t e = e0 + (i0 < cnt ? i0 : cnt - 2);
         const int64_t bt = e / a.H;
         const int h = (int)(e - bt * a.H);
         const int t = (int)(bt % a.T_);
         const int64_t b = bt / a.T_;
-        xr[u] = ld(a.r + e);
-        bl[u] = ld(a.beta + e);
-        bp[u] = ld(a.beta + (t > 0 ? e - a.H : e));   // the previous token's beta
-        tr[u] = ld(a.trace + b * a.H + h);              // the carried phase (t == 0)
-        gs[u] = SAME_GATE ? 0.0f : ld(a.gsrc + e);
-        bias_u[u] = a.bias[h];
-        tw_u[u] = a.trace_w[h];
-        t_u[u] = t;
-        h_u[u] = h;
-        b_u[u] = b;
+        RowIO<T, 2>::load(a.r + e, xr);
+        RowIO<T, 2>::load(a.beta + e, bl);
+        RowIO<T, 2>::load(a.beta + (t > 0 ? e - a.H : e), bp);   // the previous token's beta
+        RowIO<T, 2>::load(a.trace + b * a.H + h, tr);            // the carried phase (t == 0)
+        if constexpr (SAME_GATE) {
+            gs[0] = gs[1] = 0.0f;
+        } else {
+            RowIO<T, 2>::load(a.gsrc + e, gs);
+        }
+        RowIO<float, 2>::load(a.bias + h, bias_u);
+        RowIO<float, 2>::load(a.trace_w + h, tw_u);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            t_u[u] = t;
+            h_u[u] = h + u;
+            b_u[u] = b;
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < EPT; ++u) {
+            const int idx = elem(u);
+            const int64_t e = e0 + (idx < cnt ? idx : cnt - 1);
+            const int64_t bt = e / a.H;
+            const int h = (int)(e - bt * a.H);
+            const int t = (int)(bt % a.T_);
+            const int64_t b = bt / a.T_;
+            xr[u] = ld(a.r + e);
+            bl[u] = ld(a.beta + e);
+            bp[u] = ld(a.beta + (t > 0 ? e - a.H : e));   // the previous token's beta
+            tr[u] = ld(a.trace + b * a.H + h);              // the carried phase (t == 0)
+            gs[u] = SAME_GATE ? 0.0f : ld(a.gsrc + e);
+            bias_u[u] = a.bias[h];
+            tw_u[u] = a.trace_w[h];
+            t_u[u] = t;
+            h_u[u] = h;
+            b_u[u] = b;
+        }
+    }
+    if constexpr (MODE == 1) {
+        stg.commit(tile, a.prev + e0 * 9, cnt * 9);
+        lds_barrier();
     }
     float pre[EPT][9];
+    float act_u[EPT], s0_u[EPT], p_u[EPT];
 #pragma unroll
     for (int u = 0; u < EPT; ++u) {
-        const int idx = (int)threadIdx.x + u * kTriaThreads;
+        const int idx = elem(u);
         const int64_t e = e0 + idx;
         if (idx < cnt) {
             const int h = h_u[u], t = t_u[u];
@@ -254,8 +308,12 @@ paraplex_tria_kernel(PxTriaArgs<T> a) {
             T ts, to;
             st(&ts, sv);
             st(&to, act);
-            a.act[e] = to;
-            if (t == a.T_ - 1) st(a.next_trace + b * a.H + h, s0);
+            act_u[u] = act;
+            s0_u[u] = s0;
+            if constexpr (!PAIR) {
+                a.act[e] = to;
+                if (t == a.T_ - 1) st(a.next_trace + b * a.H + h, s0);
+            }
             // Tria depth op on (R, I, O) as stored
             float mt[9];
             float* pr = pre[u];
@@ -286,20 +344,29 @@ paraplex_tria_kernel(PxTriaArgs<T> a) {
                 float pv = 0.0f;
 #pragma unroll
                 for (int k = 0; k < 9; ++k) pv = fmaf(pr[k], wv[k], pv);
-                st(a.p_out + e, pv);
+                p_u[u] = pv;
+                if constexpr (!PAIR) st(a.p_out + e, pv);
             }
         }
     }
-    if constexpr (MODE == 1) __syncthreads();  // everyone has read tile
+    if constexpr (PAIR) {
+        if (elem(0) < cnt) {
+            const int64_t e = e0 + elem(0);
+            RowIO<T, 2>::store(a.act + e, act_u);
+            if (t_u[0] == a.T_ - 1) RowIO<T, 2>::store(a.next_trace + b_u[0] * a.H + h_u[0], s0_u);
+            if constexpr (GATE) RowIO<T, 2>::store(a.p_out + e, p_u);
+        }
+    }
+    if constexpr (MODE == 1) lds_barrier();  // everyone has read tile
 #pragma unroll
     for (int u = 0; u < EPT; ++u) {
-        const int idx = (int)threadIdx.x + u * kTriaThreads;
+        const int idx = elem(u);
         if (idx < cnt) {
 #pragma unroll
             for (int k = 0; k < 9; ++k) tile[idx * 9 + k] = pre[u][k];
         }
     }
-    __syncthreads();
+    lds_barrier();
     stage_out(a.carry_out + e0 * 9, tile, cnt * 9);
 }
 
@@ -1000,12 +1067,13 @@ static int tria_depth_dispatch(const void* r, const void* i, const void* o, cons
     return launch_status("loom_tria_depth_forward");
 }
 
-template <typename T>
+template <typename T, bool PAIR>
 static int px_tria_dispatch(const PxTriaArgs<T>& a, int mode, bool gate, bool same, int axis,
                             hipStream_t st) {
     constexpr int EPT = kPxTriaPerThread;
     const dim3 grid((unsigned)ceil_div(a.n, kTriaThreads * EPT)), blk(kTriaThreads);
-#define LOOM_PT(M, G, A, S) hipLaunchKernelGGL((paraplex_tria_kernel<T, M, G, A, S, EPT>), grid, blk, 0, st, a)
+#define LOOM_PT(M, G, A, S) \
+    hipLaunchKernelGGL((paraplex_tria_kernel<T, M, G, A, S, EPT, PAIR>), grid, blk, 0, st, a)
 #define LOOM_PT_AXIS(M, G, S)                     \
     switch (axis) {                               \
         case 0: LOOM_PT(M, G, 0, S); break;       \
@@ -1036,7 +1104,15 @@ static int px_tria_typed(const void* r, const void* gsrc, const void* beta, cons
     a.next_trace = (T*)next_trace; a.carry_out = (T*)carry_out; a.p_out = (T*)p_out;
     a.T_ = (int)T_; a.H = (int)H; a.n = B * T_ * H; a.m = m; a.alpha = alpha;
     const int mode = prev ? 1 : (seed ? 2 : 0);
-    return px_tria_dispatch<T>(a, mode, w != nullptr, gsrc == r, axis, st);
+    // element pairs move as one word: H even, the per-element operands
+    // aligned to two elements, bias and trace_w to two floats
+    auto al = [](const void* p, size_t n) { return p == nullptr || (uintptr_t)p % n == 0; };
+    const size_t two = 2 * sizeof(T);
+    const bool pair = H % 2 == 0 && al(r, two) && al(gsrc, two) && al(beta, two) && al(trace, two) &&
+                      al(act, two) && al(next_trace, two) && al(p_out, two) && al(bias, 8) &&
+                      al(trace_w, 8);
+    if (pair) return px_tria_dispatch<T, true>(a, mode, w != nullptr, gsrc == r, axis, st);
+    return px_tria_dispatch<T, false>(a, mode, w != nullptr, gsrc == r, axis, st);
 }
 
 #define LOOM_DTYPE_SWITCH(dtype, FN, ...)                            \

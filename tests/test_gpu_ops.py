@@ -419,6 +419,9 @@ def test_tria_depth_family(dtype, axis, B, T, H):
     (2, 5, 24, "init", False, 0, True), (2, 5, 24, "step", True, 1, False),
     (3, 4, 6, "seed", True, 2, True), (3, 9, 20, "seed", False, 1, False),
     (1, 1, 3072, "step", False, 2, True), (4, 33, 1000, "init", True, 2, False),
+    # odd H: one element per lane (even H moves element pairs as one word)
+    (2, 3, 25, "step", True, 1, False), (3, 5, 7, "seed", True, 0, True),
+    (2, 4, 9, "init", False, 2, True),
     # the chunked prefill's shape: [32, 128] tokens of 3072
     (32, 128, 3072, "step", True, 1, True), (32, 128, 3072, "init", True, 0, True),
     (32, 128, 3072, "seed", True, 2, True), (32, 128, 3072, "step", False, 0, False),
