@@ -86,28 +86,40 @@ def _prefill(eng, prompt: torch.Tensor) -> None:
     eng.tokens[:, :P].copy_(prompt_d)
     Tmax = max(e - s + 1 for s, e in zip([0] + [x + 1 for x in ends[:-1]], ends))
     z = lambda *s, dtype=dt: torch.zeros(*s, dtype=dtype, device=dev)
+    # the chunk buffers stay on the engine from one prefill to the next (each
+    # is written before it is read; first allocated NaN-filled, so that a read
+    # before the first write shows in the results): no allocation and no fill
+    # launches ahead of the first chunk
+    kept = eng.__dict__.setdefault("_prefill_buffers", {})
+
+    def buf(name, *shape, dtype=dt):
+        t = kept.get(name)
+        if t is None or t.shape != torch.Size(shape) or t.dtype != dtype:
+            t = kept[name] = torch.full(shape, float("nan"), dtype=dtype, device=dev)
+        return t
     M = B * Tmax
-    h = z(M, N)
-    y = z(M, N)
-    qkv = z(M, N + 2 * c.KV)
-    q = z(M, QH, HD)
-    cbuf = z(M, N)
-    kctx = z(M, N)
-    d = z(M, N)
-    dh = z(M, N)
-    R = z(M, H)
-    gbuf = z(M, H) if c.gate_proj else None
-    beta = z(M, H)
-    act = z(M, H)
-    hist = z(M, 2 * L, 2 * N)
-    h0 = z(M, N)                 # token embeddings of a chunk
-    carry = z(2, M, H, 3, 3)
-    pbuf = z(2, M, H)
-    traces = z(2, L, B, H)       # phase traces in / out of a chunk (swapped per chunk)
-    state = z(B, H, 3, 3)
-    state32 = torch.empty(B, H, 3, 3, dtype=torch.float32, device=dev)
-    pooled, z32, a_key = z(B, 9), z(B, 32), z(B, N)
-    stage_k, stage_v = z(B, N), z(B, N)
+    h = buf("h", M, N)
+    y = buf("y", M, N)
+    qkv = buf("qkv", M, N + 2 * c.KV)
+    q = buf("q", M, QH, HD)
+    cbuf = buf("cbuf", M, N)
+    kctx = buf("kctx", M, N)
+    d = buf("d", M, N)
+    dh = buf("dh", M, N)
+    R = buf("R", M, H)
+    gbuf = buf("gbuf", M, H) if c.gate_proj else None
+    beta = buf("beta", M, H)
+    act = buf("act", M, H)
+    hist = buf("hist", M, 2 * L, 2 * N)
+    h0 = buf("h0", M, N)                 # token embeddings of a chunk
+    carry = buf("carry", 2, M, H, 3, 3)
+    pbuf = buf("pbuf", 2, M, H)
+    traces = buf("traces", 2, L, B, H)   # phase traces in / out of a chunk (swapped per chunk)
+    traces[0].zero_()                    # the first chunk starts from a zero trace
+    state = buf("state", B, H, 3, 3)
+    state32 = buf("state32", B, H, 3, 3, dtype=torch.float32)
+    pooled, z32, a_key = buf("pooled", B, 9), buf("z32", B, 32), buf("a_key", B, N)
+    stage_k, stage_v = buf("stage_k", B, N), buf("stage_v", B, N)
     cache_sb = KVH * eng.max_len * HD
     cache_st = HD
     cache_sh = eng.max_len * HD
@@ -116,8 +128,7 @@ def _prefill(eng, prompt: torch.Tensor) -> None:
         eng._linear(x, w, out, rows, nout, k, **kw)
 
     # LayerNorm(x w^T + x2 w2^T + bias) -> h (y: the product, on the unfused path)
-    ln_ws = torch.empty(_lib.load().loom_linear_ln_workspace_bytes(M, N) // 4, dtype=torch.float32,
-                        device=dev)
+    ln_ws = buf("ln_ws", _lib.load().loom_linear_ln_workspace_bytes(M, N) // 4, dtype=torch.float32)
 
     descs = {}
 
@@ -132,8 +143,8 @@ def _prefill(eng, prompt: torch.Tensor) -> None:
     # the attention sublayer's read of slots 0..2bi also reads them with the FFN
     # sublayer's query (its part, fp32); the FFN read then folds in slot 2bi+1
     pair = eng.pair_reads
-    part_d = torch.empty(M, QH, HD, dtype=torch.float32, device=dev) if pair else None
-    part_lse = torch.empty(M, QH, dtype=torch.float32, device=dev) if pair else None
+    part_d = buf("part_d", M, QH, HD, dtype=torch.float32) if pair else None
+    part_lse = buf("part_lse", M, QH, dtype=torch.float32) if pair else None
 
     def depth(sub, out, rows):
         if not pair:
