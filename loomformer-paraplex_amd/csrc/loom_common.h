@@ -102,6 +102,11 @@ template <> struct Cvt<f16_t> {
         return __half2float(__ushort_as_half(p->x));
     }
     __device__ __forceinline__ static void store(f16_t* p, float v) {
+        // the fp32 value first, then its rounding to half: kept opaque so the
+        // compiler cannot fold a preceding multiply or fma into a mixed-precision
+        // instruction that rounds the exact product to half in one step (a
+        // different result wherever the fp32 rounding decides the half one)
+        __asm__("" : "+v"(v));
         p->x = __half_as_ushort(__float2half_rn(v));
     }
 };

@@ -414,7 +414,7 @@ def test_tria_depth_family(dtype, axis, B, T, H):
     torch.testing.assert_close(rms, torch.ones_like(rms), rtol=rms_tol, atol=0)
 
 
-@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dtype", DTYPES3)
 @pytest.mark.parametrize("B,T,H,mode,gate,axis,same", [
     (2, 5, 24, "init", False, 0, True), (2, 5, 24, "step", True, 1, False),
     (3, 4, 6, "seed", True, 2, True), (3, 9, 20, "seed", False, 1, False),
@@ -481,9 +481,10 @@ def test_paraplex_tria_fused(dtype, B, T, H, mode, gate, axis, same):
         wc = ref.tria_step(R, I, O, host(prev), a, axis)
     else:
         wc = ref.tria_init_seed(R, I, O, host(seed), valid.cpu(), a, axis)
-    # bf16: the carrier of O rounded on the GPU vs O rounded in the oracle
-    # (one ulp apart where the fp32 values straddle a rounding boundary)
-    tol = dict(rtol=2e-2, atol=2e-2) if dtype == torch.bfloat16 else {}
+    # 16-bit types: the carrier of O rounded on the GPU vs O rounded in the
+    # oracle (one ulp apart where the fp32 values straddle a rounding boundary)
+    tol = {torch.bfloat16: dict(rtol=2e-2, atol=2e-2),
+           torch.float16: dict(rtol=5e-3, atol=5e-3)}.get(dtype, {})
     check(carry, wc, dtype, **tol)
     if gate:
         check(p, ref.gate_slot_mix(wc, host(w)), dtype, **tol)
