@@ -345,6 +345,30 @@ int loom_paraplex_tria_forward(int dtype, const void* p_real, const void* gate_s
                                int64_t B, int64_t T, int64_t H, float alpha, int axis,
                                void* stream);
 
+/* The last block of a chunk: (act, next_trace) and the Tria step of
+ * loom_paraplex_tria_forward with carried records (no gate), and the chunk's
+ * temporal carry endpoint of the resulting carries, in one pass that never
+ * stores the carries.  The endpoint is the one
+ * loom_temporal_carry_endpoint_forward computes from those carries as
+ * stored (rounded to dtype), bit for bit.  Restates the block sequence of
+ * loomformer.py:2856-2885, :3588-3617 and the chunk endpoint of :3834-3850;
+ * no counterpart in the reference as one call.
+ *   p_real, gate_src, beta_linear, bias, trace, trace_w, carry_prev, act,
+ *   next_trace: as loom_paraplex_tria_forward (carry_prev required);
+ *   reset: [B,T] bool, initial: [B,H,3,3] dtype or NULL, initial_valid: [B]
+ *   bool or NULL, endpoint: [B,H,3,3] dtype out (may be initial),
+ *   endpoint_f32: [B,H,3,3] float out or NULL: as
+ *   loom_temporal_carry_endpoint_forward.  H must be even and the element
+ *   operands aligned to two elements (bias and trace_w to 8 bytes); B < 65536. */
+int loom_paraplex_tria_endpoint_forward(int dtype, const void* p_real, const void* gate_src,
+                                        const void* beta_linear, const float* bias,
+                                        const void* trace, const float* trace_w, float m,
+                                        const void* carry_prev, const uint8_t* reset,
+                                        const void* initial, const uint8_t* initial_valid,
+                                        void* act, void* next_trace, void* endpoint,
+                                        float* endpoint_f32, int64_t B, int64_t T, int64_t H,
+                                        float alpha, int axis, void* stream);
+
 /* p[e] = sum_k w[k] * carry[e][k].  Replaces gate_slot_mix_forward
  * (kernels/tria/bindings.cpp:97). carry: [n,9] dtype, w: [9] dtype, p: [n] dtype. */
 int loom_gate_slot_mix_forward(int dtype, const void* carry, const void* w, void* p, int64_t n,

@@ -72,4 +72,4 @@ int64_t resident_threads(const void* kernel, int block) {
 
 extern "C" const char* loom_last_error(void) { return loom::g_err; }
 
-extern "C" int loom_abi_version(void) { return 9; }
+extern "C" int loom_abi_version(void) { return 10; }

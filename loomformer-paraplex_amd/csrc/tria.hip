@@ -715,6 +715,313 @@ temporal_endpoint_quarters_kernel(const T* __restrict__ depth, const uint8_t* __
     }
 }
 
+// The last block of a chunk in the chunked prefill in one pass: the Paraplex
+// chain and the Tria depth step of paraplex_tria_kernel (carried records in,
+// no gate) for every (b, t, h), and the temporal carry endpoint over the
+// chunk's tokens of the carries it produces (rounded to the storage type, as
+// temporal_endpoint_quarters_kernel reads them back), so the carries are
+// never stored (the sequence of loomformer.py:2856-2885, :3588-3617 and the
+// chunk endpoint of :3834-3850).
+// Block: batch row b, 64 CH hidden columns (lane l takes columns h0 + CH l ..
+// + CH - 1; with CH = 2 a pair's 16-bit operands and 9-value records load as
+// words: 127-128 us at the prefill's [32, 128, 3072] in bf16, against 141-142
+// with one column per lane and 5 waves per SIMD); wave q takes quarter q of
+// the tokens.  Over its quarter a lane runs the
+// per-element chain token by token, the next tokens' operands in flight, and
+// composes the temporal quarter as the endpoint kernel's lane does (restart
+// on a reset, normalised after every product) from the same rounded values;
+// wave 0 then combines the four quarters in the endpoint kernel's order and
+// takes the last token's step, so the endpoint is the same bits.
+template <typename T>
+struct PxTriaEndArgs {
+    const T* r;            // R [B, T, H]
+    const T* gsrc;         // the amplitude source (R itself, or gate_proj(u))
+    const T* beta;         // beta_linear [B, T, H]
+    const float* bias;     // [H]
+    const T* trace;        // [B, H]
+    const float* trace_w;  // [H]
+    const T* prev;         // carried depth records [B, T, H, 9]
+    const uint8_t* reset;  // [B, T]
+    const T* initial;      // [B, H, 9] temporal state before t = 0, or null
+    const uint8_t* init_valid;
+    T* act;                // O [B, T, H]
+    T* next_trace;         // [B, H]
+    T* endpoint;           // [B, H, 9]
+    float* end_f32;        // [B, H, 9] or null
+    int T_, H;
+    float m, alpha;
+};
+
+constexpr int kPxEndPrefetch = 2;   // tokens of operands in flight per lane
+constexpr int kPxEndCols = 2;       // hidden columns per lane
+
+// Operands of CH adjacent columns held as the words loaded (16-bit types
+// stay packed until used, so the loads of a prefetched token are not waited
+// for where they are issued): CH elements, and their CH 9-value records.
+// With CH = 2 and 16-bit types the pair and its 36 record bytes are 4-byte
+// aligned (h even), so they load as one and nine dwords.
+template <typename T, int CH>
+struct RawCols {
+    static constexpr bool WORDS = CH == 2 || sizeof(T) == 4;
+    static constexpr int NW = WORDS ? (int)sizeof(T) * CH / 4 : CH;
+    uint32_t w[NW];
+    __device__ __forceinline__ void load(const T* p) {
+        if constexpr (WORDS) {
+#pragma unroll
+            for (int k = 0; k < NW; ++k) w[k] = reinterpret_cast<const uint32_t*>(p)[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < CH; ++k) w[k] = p[k].x;
+        }
+    }
+    __device__ __forceinline__ void to_float(float v[CH]) const {
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+            if constexpr (sizeof(T) == 4) {
+                v[e] = __uint_as_float(w[e]);
+            } else {
+                const uint32_t x = WORDS ? (e % 2 == 0 ? (w[e / 2] & 0xffffu) : (w[e / 2] >> 16)) : w[e];
+                const T y{(uint16_t)x};
+                v[e] = ld(&y);
+            }
+        }
+    }
+};
+template <typename T, int CH>
+struct RawRecs {
+    static constexpr bool WORDS = CH == 2 || sizeof(T) == 4;
+    static constexpr int NW = WORDS ? (int)sizeof(T) * 9 * CH / 4 : 9 * CH;
+    uint32_t w[NW];
+    __device__ __forceinline__ void load(const T* p) {
+        if constexpr (WORDS) {
+#pragma unroll
+            for (int k = 0; k < NW; ++k) w[k] = reinterpret_cast<const uint32_t*>(p)[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < NW; ++k) w[k] = p[k].x;
+        }
+    }
+    __device__ __forceinline__ void to_float(float (&v)[CH][9]) const {
+#pragma unroll
+        for (int e = 0; e < 9 * CH; ++e) {
+            if constexpr (sizeof(T) == 4) {
+                v[e / 9][e % 9] = __uint_as_float(w[e]);
+            } else {
+                const uint32_t x = WORDS ? (e % 2 == 0 ? (w[e / 2] & 0xffffu) : (w[e / 2] >> 16)) : w[e];
+                const T y{(uint16_t)x};
+                v[e / 9][e % 9] = ld(&y);
+            }
+        }
+    }
+};
+
+template <typename T, int AXIS, bool SAME_GATE, int CH>
+__global__ void __launch_bounds__(kTriaThreads)
+paraplex_tria_endpoint_kernel(PxTriaEndArgs<T> a) {
+    constexpr int PF = kPxEndPrefetch;
+    constexpr int REC = CH * 9 + 2;              // a lane's quarter state: CH records, have, cut
+    __shared__ float xch[4][REC][64];            // quarters' states, [0] the last token's records
+    const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int T_ = a.T_, H = a.H;
+    const int64_t b = blockIdx.y;
+    const int hc = (blockIdx.x * 64 + lane) * CH; // this lane's first column (H % CH == 0)
+    const bool live = hc < H;
+    const int h = live ? hc : H - CH;            // clamped: loads stay in range
+    const int L = (T_ + 3) / 4;
+    const int ta = min(q * L, T_), tb = min(ta + L, T_);
+    const int64_t row0 = b * (int64_t)T_;        // token index of (b, 0)
+    float bv[CH], tw[CH];
+    RowIO<float, CH>::load(a.bias + h, bv);
+    RowIO<float, CH>::load(a.trace_w + h, tw);
+    // the base phase of the token before ta: the carried trace, or that token's beta
+    float prevs[CH];
+    {
+        float v[CH];
+        if (ta == 0) {
+            RowIO<T, CH>::load(a.trace + b * H + h, prevs);
+        } else {
+            RowIO<T, CH>::load(a.beta + (row0 + ta - 1) * H + h, v);
+#pragma unroll
+            for (int c = 0; c < CH; ++c) prevs[c] = phase_of(v[c] + bv[c]);
+        }
+    }
+    // quarter state, as temporal_endpoint_quarters_kernel's lane keeps it
+    float acc[CH][9];
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int k = 0; k < 9; ++k) acc[c][k] = 0.0f;
+    bool have = false, cut = q == 0;
+    if (q == 0 && a.initial != nullptr && (a.init_valid == nullptr || a.init_valid[b] != 0)) {
+        load_records<T, CH>(a.initial + (b * H + h) * 9, acc);
+        have = true;
+    }
+    float last[CH][9];                            // the chunk's last carries (wave holding T-1)
+    // operands of token t into ring slot p
+    RawCols<T, CH> xr[PF], bl[PF], gs[PF];
+    RawRecs<T, CH> cp[PF];
+    auto fetch = [&](int p, int t) {
+        const int64_t e = (row0 + t) * H + h;
+        xr[p].load(a.r + e);
+        bl[p].load(a.beta + e);
+        if constexpr (!SAME_GATE) gs[p].load(a.gsrc + e);
+        cp[p].load(a.prev + e * 9);
+    };
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+        if (ta + p < tb) fetch(p, ta + p);
+    for (int t0 = ta; t0 < tb; t0 += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const int t = t0 + p;
+            if (t >= tb) break;
+            float x[CH], be[CH], g[CH], cpv[CH][9];
+            xr[p].to_float(x);
+            bl[p].to_float(be);
+            if constexpr (SAME_GATE) {
+#pragma unroll
+                for (int c = 0; c < CH; ++c) g[c] = x[c];
+            } else {
+                gs[p].to_float(g);
+            }
+            cp[p].to_float(cpv);
+            // the slot's values unpacked into registers of their own before
+            // its refill is issued
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                asm volatile("" : "+v"(x[c]), "+v"(be[c]), "+v"(g[c]));
+#pragma unroll
+                for (int k = 0; k < 9; ++k) asm volatile("" : "+v"(cpv[c][k]));
+            }
+            if (t + PF < tb) fetch(p, t + PF);
+            float ao[CH], s0v[CH], cr[CH][9];
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const float s0 = phase_of(be[c] + bv[c]);
+                const float raw = fmaf(prevs[c], tw[c], s0);
+                const float sv = raw * frsq(fmaf(raw, raw, 1.0f));
+                float amp, gate;
+                softplus_gate<!std::is_same<T, bf16_t>::value>(g[c], a.m, amp, gate);
+                const float act = fmaf(amp, sv, x[c]) * gate;
+                ao[c] = act;
+                s0v[c] = s0;
+                prevs[c] = s0;
+                float mt[9], pr[9];
+                carrier9<AXIS>(x[c], round_to<T>(sv), round_to<T>(act), a.alpha, mt);
+                mm3(mt, cpv[c], pr);
+                const float inv = 1.0f / rms9(pr);
+#pragma unroll
+                for (int k = 0; k < 9; ++k) cr[c][k] = round_to<T>(pr[k] * inv);
+            }
+            const int64_t e = (row0 + t) * H + h;
+            if (live) {
+                RowIO<T, CH>::store(a.act + e, ao);
+                if (t == T_ - 1) RowIO<T, CH>::store(a.next_trace + b * H + h, s0v);
+            }
+            if (t == T_ - 1) {
+#pragma unroll
+                for (int c = 0; c < CH; ++c)
+#pragma unroll
+                    for (int k = 0; k < 9; ++k) last[c][k] = cr[c][k];
+            } else {
+                const bool rs = a.reset[row0 + t] != 0;
+                cut = cut || rs;
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    float pre[9];
+                    if (!have || rs) {
+#pragma unroll
+                        for (int k = 0; k < 9; ++k) pre[k] = cr[c][k];
+                    } else {
+                        mm3(cr[c], acc[c], pre);
+                    }
+                    const float inv = 1.0f / rms9(pre);
+#pragma unroll
+                    for (int k = 0; k < 9; ++k) acc[c][k] = pre[k] * inv;
+                }
+                have = true;
+            }
+        }
+    }
+    // quarters 1..3 (and the last token's records, from the wave that holds
+    // T-1) to wave 0 through LDS
+    const int qlast = (T_ - 1) / L;
+    if (q > 0) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int k = 0; k < 9; ++k) xch[q][c * 9 + k][lane] = acc[c][k];
+        xch[q][9 * CH][lane] = have ? 1.0f : 0.0f;
+        xch[q][9 * CH + 1][lane] = cut ? 1.0f : 0.0f;
+    }
+    if (q == qlast && q > 0) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int k = 0; k < 9; ++k) xch[0][c * 9 + k][lane] = last[c][k];
+    }
+    __syncthreads();
+    if (q != 0) return;
+    if (qlast > 0) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int k = 0; k < 9; ++k) last[c][k] = xch[0][c * 9 + k][lane];
+    }
+    float rr[CH][9];
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int k = 0; k < 9; ++k) rr[c][k] = acc[c][k];
+    bool have_r = have;
+#pragma unroll
+    for (int j = 1; j < 4; ++j) {
+        if (xch[j][9 * CH][lane] == 0.0f) continue;   // quarter j saw no step
+        have_r = true;
+        const bool qcut = xch[j][9 * CH + 1][lane] != 0.0f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            float qv[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) qv[k] = xch[j][c * 9 + k][lane];
+            if (qcut) {
+#pragma unroll
+                for (int k = 0; k < 9; ++k) rr[c][k] = qv[k];
+            } else {
+                float pre[9];
+                mm3(qv, rr[c], pre);
+                const float inv = 1.0f / rms9(pre);
+#pragma unroll
+                for (int k = 0; k < 9; ++k) rr[c][k] = pre[k] * inv;
+            }
+        }
+    }
+    // the last step
+    const bool rl = a.reset[row0 + T_ - 1] != 0;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        float pre[9];
+        if (!have_r || rl) {
+#pragma unroll
+            for (int k = 0; k < 9; ++k) pre[k] = last[c][k];
+        } else {
+            mm3(last[c], rr[c], pre);
+        }
+        const float inv = 1.0f / rms9(pre);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) rr[c][k] = pre[k] * inv;
+    }
+    if (live) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                st(a.endpoint + (b * H + h + c) * 9 + k, rr[c][k]);
+                if (a.end_f32 != nullptr) a.end_f32[(b * H + h + c) * 9 + k] = rr[c][k];
+            }
+    }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(kTriaThreads)
 polarm_kernel(const T* __restrict__ in, T* __restrict__ out, const uint8_t* __restrict__ mask,
@@ -1115,6 +1422,43 @@ static int px_tria_typed(const void* r, const void* gsrc, const void* beta, cons
     return px_tria_dispatch<T, false>(a, mode, w != nullptr, gsrc == r, axis, st);
 }
 
+template <typename T>
+static int px_tria_end_typed(const void* r, const void* gsrc, const void* beta, const float* bias,
+                             const void* trace, const float* trace_w, float m, const void* prev,
+                             const uint8_t* reset, const void* initial, const uint8_t* init_valid,
+                             void* act, void* next_trace, void* endpoint, float* end_f32, int64_t B,
+                             int64_t T_, int64_t H, float alpha, int axis, hipStream_t st) {
+    // element pairs and record pairs move as words
+    auto al = [](const void* p, size_t n) { return p == nullptr || (uintptr_t)p % n == 0; };
+    const size_t two = 2 * sizeof(T);
+    LOOM_CHECK(al(r, two) && al(gsrc, two) && al(beta, two) && al(trace, two) && al(act, two) &&
+                   al(next_trace, two) && al(prev, 4) && al(initial, 4) && al(endpoint, 4) &&
+                   al(bias, 8) && al(trace_w, 8),
+               "paraplex_tria_endpoint: element operands must be aligned to two elements "
+               "(bias and trace_w to two floats)");
+    PxTriaEndArgs<T> a{};
+    a.r = (const T*)r; a.gsrc = (const T*)gsrc; a.beta = (const T*)beta; a.bias = bias;
+    a.trace = (const T*)trace; a.trace_w = trace_w; a.prev = (const T*)prev; a.reset = reset;
+    a.initial = (const T*)initial; a.init_valid = init_valid; a.act = (T*)act;
+    a.next_trace = (T*)next_trace; a.endpoint = (T*)endpoint; a.end_f32 = end_f32;
+    a.T_ = (int)T_; a.H = (int)H; a.m = m; a.alpha = alpha;
+    constexpr int CH = kPxEndCols;
+    const dim3 grid((unsigned)ceil_div(H, 64 * CH), (unsigned)B), blk(kTriaThreads);
+    const bool same = gsrc == r;
+#define LOOM_PE(A)                                                                                  \
+    if (same)                                                                                       \
+        hipLaunchKernelGGL((paraplex_tria_endpoint_kernel<T, A, true, CH>), grid, blk, 0, st, a);   \
+    else                                                                                            \
+        hipLaunchKernelGGL((paraplex_tria_endpoint_kernel<T, A, false, CH>), grid, blk, 0, st, a);
+    switch (axis) {
+        case 0: LOOM_PE(0) break;
+        case 1: LOOM_PE(1) break;
+        default: LOOM_PE(2) break;
+    }
+#undef LOOM_PE
+    return launch_status("loom_paraplex_tria_endpoint_forward");
+}
+
 #define LOOM_DTYPE_SWITCH(dtype, FN, ...)                            \
     switch (dtype) {                                                 \
         case LOOM_F32: return FN<float>(__VA_ARGS__);                \
@@ -1255,6 +1599,33 @@ extern "C" int loom_paraplex_tria_forward(int dtype, const void* p_real, const v
     LOOM_DTYPE_SWITCH(dtype, px_tria_typed, p_real, gate_src, beta_linear, bias, trace, trace_w, m,
                       carry_prev, seed, seed_valid, w, act, next_trace, carry_out, p_out, B, T, H,
                       alpha, axis, (hipStream_t)stream)
+}
+
+extern "C" int loom_paraplex_tria_endpoint_forward(int dtype, const void* p_real,
+                                                   const void* gate_src, const void* beta_linear,
+                                                   const float* bias, const void* trace,
+                                                   const float* trace_w, float m,
+                                                   const void* carry_prev, const uint8_t* reset,
+                                                   const void* initial,
+                                                   const uint8_t* initial_valid, void* act,
+                                                   void* next_trace, void* endpoint,
+                                                   float* endpoint_f32, int64_t B, int64_t T,
+                                                   int64_t H, float alpha, int axis, void* stream) {
+    clear_error();
+    LOOM_CHECK(p_real && gate_src && beta_linear && bias && trace && trace_w && carry_prev && reset &&
+                   act && next_trace && endpoint,
+               "paraplex_tria_endpoint: a required tensor is null");
+    LOOM_CHECK(axis >= 0 && axis <= 2, "paraplex_tria_endpoint: axis must be 0(z), 1(x), or 2(y), got %d",
+               axis);
+    LOOM_CHECK(B >= 0 && B < 65536 && T >= 1 && T < (1LL << 31) && H >= 0 && H < (1LL << 31) &&
+                   H % 2 == 0,
+               "paraplex_tria_endpoint: bad shape (B < 65536, T >= 1, H even)");
+    LOOM_CHECK(T <= 1 || trace != (const void*)next_trace,
+               "paraplex_tria_endpoint: trace and next_trace must be distinct buffers when T > 1");
+    if (B * H == 0) return LOOM_OK;
+    LOOM_DTYPE_SWITCH(dtype, px_tria_end_typed, p_real, gate_src, beta_linear, bias, trace, trace_w,
+                      m, carry_prev, reset, initial, initial_valid, act, next_trace, endpoint,
+                      endpoint_f32, B, T, H, alpha, axis, (hipStream_t)stream)
 }
 
 extern "C" int loom_gate_slot_mix_forward(int dtype, const void* carry, const void* w, void* p,

@@ -13,7 +13,7 @@ from ctypes import c_float, c_int, c_int64, c_void_p
 import torch
 
 # descriptor layouts and signatures below are those of loom_abi_version() == ABI_VERSION
-ABI_VERSION = 9
+ABI_VERSION = 10
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libloom_hip.so")
 
 _P = c_void_p
@@ -52,6 +52,9 @@ SIGNATURES = {
                                 c_int64, c_int64, c_float, c_int, _P],
     "loom_paraplex_tria_forward": [c_int, _P, _P, _P, _P, _P, _P, c_float, _P, _P, _P, _P, _P, _P,
                                    _P, _P, c_int64, c_int64, c_int64, c_float, c_int, _P],
+    "loom_paraplex_tria_endpoint_forward": [c_int, _P, _P, _P, _P, _P, _P, c_float, _P, _P, _P, _P,
+                                            _P, _P, _P, _P, c_int64, c_int64, c_int64, c_float,
+                                            c_int, _P],
     "loom_gate_slot_mix_forward": [c_int, _P, _P, _P, c_int64, _P],
     "loom_slot_attention_pool_forward": [c_int, _P, _P, _P, _P, c_int64, c_int64, _P],
     "loom_temporal_carry_forward": [c_int, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P],

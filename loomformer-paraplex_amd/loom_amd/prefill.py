@@ -286,16 +286,34 @@ def _prefill(eng, prompt: torch.Tensor) -> None:
             seeded = bi == 0 and have_state
             if seeded:
                 main.wait_stream(tail)      # the state after the previous chunk
-            call("loom_paraplex_tria_forward", code, _P(R), _P(gsrc), _P(beta), _P(blk["ib"]),
-                 _P(traces[tin, bi]), _P(blk["tw"]), float(c.powlu_m),
-                 None if (carry_i is None or seeded) else _P(carry[carry_i]),
-                 _P(state) if seeded else None, _P(seed_valid) if seeded else None,
-                 _P(blk["gate_w"]) if gate else None, _P(act), _P(traces[1 - tin, bi]),
-                 _P(carry[out_i]), _P(pbuf[new_p]) if gate else None, B, Tc, H,
-                 float(c.tria_alpha), bi % 3, st)
+            if last and carry_i is not None and H % 2 == 0:
+                # the last block and the chunk's temporal carry endpoint (loomformer.py:
+                # 3834-3850) in one pass: the carry restarts at position 0 and at a
+                # seeded first token, else continues from the state; the chunk's
+                # last carries are never stored
+                reset = z(B, Tc, dtype=torch.uint8)
+                if s == 0:
+                    reset[:, 0] = 1
+                else:
+                    reset[:, 0] = seed_valid
+                call("loom_paraplex_tria_endpoint_forward", code, _P(R), _P(gsrc), _P(beta),
+                     _P(blk["ib"]), _P(traces[tin, bi]), _P(blk["tw"]), float(c.powlu_m),
+                     _P(carry[carry_i]), _P(reset), _P(state) if have_state else None, None,
+                     _P(act), _P(traces[1 - tin, bi]), _P(state), _P(state32), B, Tc, H,
+                     float(c.tria_alpha), bi % 3, st)
+                endpoint_done = True
+            else:
+                call("loom_paraplex_tria_forward", code, _P(R), _P(gsrc), _P(beta), _P(blk["ib"]),
+                     _P(traces[tin, bi]), _P(blk["tw"]), float(c.powlu_m),
+                     None if (carry_i is None or seeded) else _P(carry[carry_i]),
+                     _P(state) if seeded else None, _P(seed_valid) if seeded else None,
+                     _P(blk["gate_w"]) if gate else None, _P(act), _P(traces[1 - tin, bi]),
+                     _P(carry[out_i]), _P(pbuf[new_p]) if gate else None, B, Tc, H,
+                     float(c.tria_alpha), bi % 3, st)
+                endpoint_done = False
             carry_i, p_i = out_i, new_p
             if last:
-                tail.wait_stream(main)      # the chunk's last carry is written
+                tail.wait_stream(main)      # the chunk's last carries (or its state) are written
             # ---- LN(w_o(d_h) + W2(act) + b2) (loomformer.py:4045)
             lin_ln(("ffn", bi), dh, eng.wo_for(sub), act, blk["w2"], blk["b2"], blk["ln2_w"],
                    blk["ln2_b"], rows)
@@ -312,13 +330,15 @@ def _prefill(eng, prompt: torch.Tensor) -> None:
         # temporal carry over the chunk, restarting at position 0 and at a
         # seeded first token, else continuing from the state (loomformer.py:3834-3850)
         with torch.cuda.stream(tail):
-            reset = z(B, Tc, dtype=torch.uint8)
-            if s == 0:
-                reset[:, 0] = 1
-            else:
-                reset[:, 0] = seed_valid
-            call("loom_temporal_carry_endpoint_forward", code, _P(carry[carry_i]), _P(reset),
-                 _P(state) if have_state else None, None, _P(state), _P(state32), B, Tc, H, tail_st)
+            if not endpoint_done:
+                reset = z(B, Tc, dtype=torch.uint8)
+                if s == 0:
+                    reset[:, 0] = 1
+                else:
+                    reset[:, 0] = seed_valid
+                call("loom_temporal_carry_endpoint_forward", code, _P(carry[carry_i]), _P(reset),
+                     _P(state) if have_state else None, None, _P(state), _P(state32), B, Tc, H,
+                     tail_st)
             have_state = True
             fire_e = fire_all_d[:, e]
             if bool(fire_all[:, e].any()):

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     assert "loom_paraplex_forward" in syms and len(syms) >= 15
     missing = [s for s in syms if not hasattr(lib, s)]
     assert not missing, missing
-    assert lib.loom_abi_version() == 9
+    assert lib.loom_abi_version() == 10
     # every declared compute entry point has a ctypes signature
     compute = [s for s in syms if s not in ("loom_last_error", "loom_abi_version")]
     bound = set(_lib.SIGNATURES) | set(_lib.QUERIES)

@@ -490,6 +490,116 @@ def test_paraplex_tria_fused(dtype, B, T, H, mode, gate, axis, same):
         check(p, ref.gate_slot_mix(wc, host(w)), dtype, **tol)
 
 
+@pytest.mark.parametrize("dtype", DTYPES3)
+@pytest.mark.parametrize("B,T,H,axis,same,initial", [
+    (2, 5, 24, 0, True, "none"), (3, 1, 6, 1, False, "valid"), (2, 7, 200, 2, True, "some"),
+    (1, 33, 130, 1, False, "some"), (2, 4, 128, 0, True, "valid"),
+    # the chunked prefill's last block: [32, 128] tokens of 3072
+    (32, 128, 3072, 0, True, "some"),
+])
+def test_paraplex_tria_endpoint_fused(dtype, B, T, H, axis, same, initial):
+    """loom_paraplex_tria_endpoint_forward against the two launches it
+    replaces (loom_paraplex_tria_forward with carried records, then
+    loom_temporal_carry_endpoint_forward on the stored carries): the same bits
+    for act, the next trace and the endpoint (both precisions), with resets
+    inside the chunk and at its first token, and an initial state valid for
+    none, some or all rows."""
+    from loom_amd._lib import call, dtype_code, ptr, stream_of
+    g = gen(B * 97 + T * 5 + H + axis)
+    r = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    gs = r if same else dev(rnd(g, B, T, H, scale=3.0), dtype)
+    beta = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    bias = dev(rnd(g, H, scale=0.5), torch.float32)
+    trace = dev(rnd(g, B, H, scale=0.5), dtype)
+    tw = dev(torch.rand(H, generator=g) - 0.5, torch.float32)
+    prev = dev(ref.local_normalize(rnd(g, B, T, H, 3, 3)), dtype)
+    reset = torch.rand(B, T, generator=g) > 0.9
+    reset[:, 0] = torch.rand(B, generator=g) > 0.5
+    reset = dev(reset, torch.bool)
+    init = dev(ref.local_normalize(rnd(g, B, H, 3, 3)), dtype) if initial != "none" else None
+    valid = None
+    if initial == "some":
+        valid = torch.rand(B, generator=g) > 0.5
+        valid[0] = True
+        valid = dev(valid, torch.bool)
+    a, m = 0.0375, 3.0
+
+    # the two launches
+    act2 = torch.empty_like(r)
+    nt2 = torch.empty_like(trace)
+    carry2 = torch.empty(B, T, H, 3, 3, dtype=dtype, device=DEV)
+    call("loom_paraplex_tria_forward", dtype_code(r), ptr(r), ptr(gs), ptr(beta), ptr(bias), ptr(trace),
+         ptr(tw), m, ptr(prev), None, None, None, ptr(act2), ptr(nt2), ptr(carry2), None, B, T, H, a,
+         axis, stream_of(r))
+    end2 = torch.empty(B, H, 3, 3, dtype=dtype, device=DEV)
+    end2_32 = torch.empty(B, H, 3, 3, dtype=torch.float32, device=DEV)
+    call("loom_temporal_carry_endpoint_forward", dtype_code(r), ptr(carry2), ptr(reset), ptr(init),
+         ptr(valid), ptr(end2), ptr(end2_32), B, T, H, stream_of(r))
+
+    for _ in range(2):  # a second call writes the same bits
+        act = torch.full_like(r, float("nan"))
+        nt = torch.full_like(trace, float("nan"))
+        end = torch.full((B, H, 3, 3), float("nan"), dtype=dtype, device=DEV)
+        end32 = torch.full((B, H, 3, 3), float("nan"), dtype=torch.float32, device=DEV)
+        call("loom_paraplex_tria_endpoint_forward", dtype_code(r), ptr(r), ptr(gs), ptr(beta),
+             ptr(bias), ptr(trace), ptr(tw), m, ptr(prev), ptr(reset), ptr(init), ptr(valid),
+             ptr(act), ptr(nt), ptr(end), ptr(end32), B, T, H, a, axis, stream_of(r))
+        torch.cuda.synchronize()
+        assert torch.equal(act, act2)
+        assert torch.equal(nt, nt2)
+        assert torch.equal(end, end2)
+        assert torch.equal(end32, end2_32)
+
+
+def test_paraplex_tria_endpoint_in_place_initial():
+    """The endpoint may overwrite the initial state (the chunked prefill's
+    use): the same bits as with separate buffers."""
+    from loom_amd._lib import call, dtype_code, ptr, stream_of
+    B, T, H, dtype = 4, 9, 256, torch.bfloat16
+    g = gen(5)
+    r = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    beta = dev(rnd(g, B, T, H, scale=2.0), dtype)
+    bias = dev(rnd(g, H, scale=0.5), torch.float32)
+    trace = dev(rnd(g, B, H, scale=0.5), dtype)
+    tw = dev(torch.rand(H, generator=g) - 0.5, torch.float32)
+    prev = dev(ref.local_normalize(rnd(g, B, T, H, 3, 3)), dtype)
+    reset = dev(torch.zeros(B, T, dtype=torch.bool), torch.bool)
+    init = dev(ref.local_normalize(rnd(g, B, H, 3, 3)), dtype)
+    outs = []
+    for in_place in (False, True):
+        state = init.clone()
+        end = state if in_place else torch.empty_like(init)
+        act, nt = torch.empty_like(r), torch.empty_like(trace)
+        call("loom_paraplex_tria_endpoint_forward", dtype_code(r), ptr(r), ptr(r), ptr(beta),
+             ptr(bias), ptr(trace), ptr(tw), 3.0, ptr(prev), ptr(reset), ptr(state), None,
+             ptr(act), ptr(nt), ptr(end), None, B, T, H, 0.0375, 1, stream_of(r))
+        torch.cuda.synchronize()
+        outs.append(end.clone())
+    assert torch.equal(outs[0], outs[1])
+
+
+def test_paraplex_tria_endpoint_argument_errors():
+    from loom_amd._lib import call, ptr
+    x = torch.zeros(2, 3, 4, device=DEV)
+    t = torch.zeros(2, 4, device=DEV)
+    h = torch.zeros(4, device=DEV)
+    c = torch.zeros(2, 3, 4, 9, device=DEV)
+    rs = torch.zeros(2, 3, dtype=torch.bool, device=DEV)
+    e = torch.zeros(2, 4, 9, device=DEV)
+    base = [0, ptr(x), ptr(x), ptr(x), ptr(h), ptr(t), ptr(h), 3.0, ptr(c), ptr(rs), None, None,
+            ptr(x), ptr(t), ptr(e), None, 2, 3, 4, 0.0375, 0, None]
+    # bad axis, no carried records, no reset, odd H, trace aliasing next_trace
+    cases = [[(20, 3)], [(8, None)], [(9, None)], [(18, 3)], [(13, ptr(t))]]
+    for edits in cases:
+        args = list(base)
+        for k, v in edits:
+            args[k] = v
+        with pytest.raises(RuntimeError, match="paraplex_tria_endpoint"):
+            call("loom_paraplex_tria_endpoint_forward", *args)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(e) == 0  # nothing was launched
+
+
 def test_paraplex_tria_argument_errors():
     from loom_amd._lib import call, ptr
     x = torch.zeros(2, 3, 4, device=DEV)
