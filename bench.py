@@ -23,7 +23,7 @@ bf16) per launch over its mean launch time, against 8 TB/s.
 ``cpu_baseline`` is the CPU oracle (fp32 PyTorch restatement of the
 reference's unfused path) running the e2e decode step on all host cores on a
 bounded sample (B=32 from position 2048 on a synthetic state of that size);
-``cpu_reference_config`` times BASELINE's CPU-reference config (nano.yaml,
+``cpu_reference_config`` times BASELINE.json's CPU-reference config (nano.yaml,
 B=1, 128 + 64 tokens, fp32) on the host cores and on the fp32 GPU engine;
 ``cpu_micro`` times the oracle on PX and DA at full size and on a slice of TR
 scaled to its full size.  CPU figures are 1 warm-up plus the median of 3.
@@ -434,7 +434,7 @@ def cpu_baseline(args):
 
 
 def cpu_reference_config(args):
-    """BASELINE's CPU-reference config: cfg/nano.yaml weights from seed 0,
+    """BASELINE.json's CPU-reference config: cfg/nano.yaml weights from seed 0,
     fp32, B = 1, a 128-token prompt (ids from a generator seeded 0), 128
     prefill steps and 64 greedy steps (Model.step each, as infer runs them).
     Timed with the fp32 oracle on the host cores (1 warm-up, median of 3)
