@@ -48,6 +48,11 @@ def test_error_channel_reports_argument_errors():
     with pytest.raises(RuntimeError, match="K=0"):
         _lib.call("loom_final_ca_sparse_forward", 0, *([ctypes.c_void_p(16)] * 5), None,
                   1, 1, 0, 8, 1.0, None)
+    p = ctypes.c_void_p(16)
+    with pytest.raises(RuntimeError, match="paraplex_tria_endpoint: bad shape"):
+        # H odd: the column pairs need H even
+        _lib.call("loom_paraplex_tria_endpoint_forward", 1, p, p, p, p, p, p, 3.0, p, p, None,
+                  None, p, p, p, None, 1, 1, 3, 0.0375, 0, None)
 
 
 def test_drop_in_modules_expose_reference_names():
