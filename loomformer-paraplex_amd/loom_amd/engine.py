@@ -209,6 +209,10 @@ class LoomDecoder:
         # call would in time share the main stream's queue and serialise
         self.aux_stream = torch.cuda.Stream(device=dev)
         self.tail_stream = torch.cuda.Stream(device=dev)
+        # the chunked prefill's chunk buffers, kept from one prompt to the next
+        # (≈1 GB at B = 32, 128-token chunks, H = 3072); free_prefill_buffers()
+        # drops them
+        self._prefill_buffers: Dict[str, torch.Tensor] = {}
 
     # ------------------------------------------------------------------ helpers
 
@@ -293,6 +297,11 @@ class LoomDecoder:
         self._call("loom_linear_ln", self.code, _lib.ctypes.byref(d), _P(gamma), _P(beta), 1e-5,
                    _P(self.h), self.cfg.N, _P(self.ln_ws), self.ln_ws.numel() * 4, _P(self.h_frag),
                    self._stream())
+
+    def free_prefill_buffers(self) -> None:
+        """Release the chunk buffers the chunked prefill keeps between prompts
+        (the next prefill allocates them again)."""
+        self._prefill_buffers.clear()
 
     def reset(self) -> None:
         """Forget all sequence state (Model.step at pos 0 starts afresh)."""

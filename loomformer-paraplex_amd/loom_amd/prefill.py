@@ -90,7 +90,7 @@ def _prefill(eng, prompt: torch.Tensor) -> None:
     # is written before it is read; first allocated NaN-filled, so that a read
     # before the first write shows in the results): no allocation and no fill
     # launches ahead of the first chunk
-    kept = eng.__dict__.setdefault("_prefill_buffers", {})
+    kept = eng._prefill_buffers
 
     def buf(name, *shape, dtype=dt):
         t = kept.get(name)

@@ -172,6 +172,31 @@ def test_tiny_chunked_prefill_matches_reference(carry):
     assert torch.equal(ids.cpu(), torch.from_numpy(z["greedy" + sfx]))
 
 
+def test_chunked_prefill_with_kept_and_freed_buffers():
+    """The chunk buffers kept on the engine between prompts: a second prefill
+    (of another prompt, then the first again) on the same engine, and one after
+    free_prefill_buffers(), give the same bits as a fresh engine's."""
+    from loom_amd.engine import LoomDecoder
+    z = np.load(os.path.join(GOLD, "tiny_decode.npz"))
+    state = {k[3:]: torch.from_numpy(z[k]) for k in z.files if k.startswith("w::")}
+    prompt = torch.from_numpy(z["prompt_carry"])
+    # another prompt with the same <CARRY> positions, so the same chunks and
+    # buffer shapes: the second prefill runs on the first one's buffers
+    other = torch.where(prompt == 5, prompt, torch.where(prompt == 4, 6, 4))
+    mk = lambda: LoomDecoder(_cfg("tiny"), state, batch=prompt.shape[0], dtype=torch.float32,
+                             carry_token_id=5)
+    fresh = mk().generate(prompt, 6, return_logits=True, chunked_prefill=True)[1]
+    eng = mk()
+    eng.generate(other, 6, chunked_prefill=True)
+    assert eng._prefill_buffers
+    again = eng.generate(prompt, 6, return_logits=True, chunked_prefill=True)[1]
+    assert torch.equal(again, fresh)
+    eng.free_prefill_buffers()
+    assert not eng._prefill_buffers
+    freed = eng.generate(prompt, 6, return_logits=True, chunked_prefill=True)[1]
+    assert torch.equal(freed, fresh)
+
+
 def test_nano_chunked_prefill_greedy_ids_bit_exact_fp32():
     """nano.yaml (W = 128): the 128-token prompt is one chunk ending in a fire;
     the 64 greedy ids after the chunked prefill are the reference's."""
